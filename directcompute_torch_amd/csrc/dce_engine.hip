@@ -1,0 +1,850 @@
+// libdcengine: device, buffer pool, dispatch registry and the fused C entry
+// points of the engine.dll ABI (include/dcengine.h), on one HIP stream.
+//
+// Design notes
+//  * One in-order stream replaces the D3D11 immediate context: a buffer that
+//    the host releases to the pool and hands out again is only touched by
+//    work queued after every earlier user, so pooled reuse needs no fences.
+//  * Device memory is freed only after the stream has drained.
+//  * Host->device copies never block on queued work: payloads of up to 256
+//    floats travel as kernel arguments, larger ones through a ring of pinned
+//    staging slots guarded by events.
+#include "dce_internal.h"
+#include "../../include/dcengine.h"
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+namespace dce {
+
+// ---------------------------------------------------------------------------
+// Global state
+// ---------------------------------------------------------------------------
+static bool g_init = false;
+static int g_device = 0;
+static hipStream_t g_stream = nullptr;
+static int g_cus = 256;
+static GPUInfo g_info;
+static char g_err[1024] = "";
+
+static std::unordered_map<uint32_t, std::vector<Buffer*>> g_pool;
+static std::vector<Buffer*> g_recycled;  // dead records, reused for new handles
+static uint64_t g_poolHits = 0, g_poolMisses = 0, g_poolBytes = 0;
+static uint64_t g_poolCapBytes = 0;
+
+static float* g_ws = nullptr;
+static size_t g_wsFloats = 0;
+static float* g_misc = nullptr;  // 1024 floats of device scratch for scalars
+
+// Pinned staging ring for host->device uploads.
+constexpr int kSlots = 4;
+constexpr size_t kSlotBytes = size_t(16) << 20;
+static char* g_stage = nullptr;
+static hipEvent_t g_slotEv[kSlots];
+static bool g_slotBusy[kSlots];
+static int g_nextSlot = 0;
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+hipStream_t stream() { return g_stream; }
+int num_cus() { return g_cus; }
+
+bool ensure_init() {
+  if (g_init) return true;
+  set_error("engine not initialised (InitEngine failed or was not called)");
+  return false;
+}
+
+bool check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: launch failed: %s", what, hipGetErrorString(e));
+    return false;
+  }
+  return true;
+}
+
+FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f;
+  f.d = d ? d : 1;
+  uint32_t l = 0;
+  while ((uint64_t(1) << l) < f.d) ++l;
+  uint64_t m = ((uint64_t(1) << 32) * ((uint64_t(1) << l) - f.d)) / f.d + 1;
+  f.mul = uint32_t(m);
+  f.shr = l;
+  return f;
+}
+
+// ---------------------------------------------------------------------------
+// Profiling: per-family event timing on the engine stream.
+// ---------------------------------------------------------------------------
+struct ProfStat {
+  uint64_t launches = 0;
+  double ms = 0, flops = 0, bytes = 0;
+};
+struct ProfPending {
+  const char* family;
+  hipEvent_t e0, e1;
+  double flops, bytes;
+};
+static bool g_prof = false;
+static std::unordered_map<std::string, ProfStat> g_profStats;
+static std::vector<ProfPending> g_profPending;
+static std::vector<hipEvent_t> g_eventFree;
+
+static hipEvent_t take_event() {
+  if (!g_eventFree.empty()) {
+    hipEvent_t e = g_eventFree.back();
+    g_eventFree.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+ProfScope::ProfScope(const char* fam, double fl, double by)
+    : family(fam), flops(fl), bytes(by), ev0(nullptr) {
+  if (!g_prof) return;
+  hipEvent_t e = take_event();
+  if (!e) return;
+  hipEventRecord(e, g_stream);
+  ev0 = e;
+}
+
+ProfScope::~ProfScope() {
+  if (!ev0) return;
+  hipEvent_t e1 = take_event();
+  if (!e1) return;
+  hipEventRecord(e1, g_stream);
+  g_profPending.push_back({family, (hipEvent_t)ev0, e1, flops, bytes});
+}
+
+static void resolve_profile() {
+  if (g_profPending.empty()) return;
+  hipStreamSynchronize(g_stream);
+  for (auto& p : g_profPending) {
+    float ms = 0;
+    hipEventElapsedTime(&ms, p.e0, p.e1);
+    ProfStat& s = g_profStats[p.family];
+    s.launches++;
+    s.ms += ms;
+    s.flops += p.flops;
+    s.bytes += p.bytes;
+    g_eventFree.push_back(p.e0);
+    g_eventFree.push_back(p.e1);
+  }
+  g_profPending.clear();
+}
+
+// ---------------------------------------------------------------------------
+// Buffers and pool
+// ---------------------------------------------------------------------------
+static size_t max_pool_for_size(uint32_t count) {
+  size_t bytes = size_t(count) * 4;
+  if (bytes >= (size_t(1) << 30)) return 4;
+  if (bytes >= (size_t(4) << 20)) return 8;
+  if (bytes >= (size_t(256) << 10)) return 16;
+  return 32;
+}
+
+static void free_record(Buffer* b) {
+  // The stream may still reference the memory: drain it first.
+  hipStreamSynchronize(g_stream);
+  hipFree(b->ptr);
+  b->ptr = nullptr;
+  b->magic = kMagicDead;
+  b->refCount = 0;
+  g_recycled.push_back(b);
+}
+
+static void drain_pool_locked() {
+  bool any = false;
+  for (auto& kv : g_pool) any |= !kv.second.empty();
+  if (!any) return;
+  hipStreamSynchronize(g_stream);
+  for (auto& kv : g_pool) {
+    for (Buffer* b : kv.second) {
+      hipFree(b->ptr);
+      b->ptr = nullptr;
+      b->magic = kMagicDead;
+      g_recycled.push_back(b);
+    }
+    kv.second.clear();
+  }
+  g_pool.clear();
+  g_poolBytes = 0;
+}
+
+Buffer* as_buffer(void* h, const char* what) {
+  if (!h) {
+    set_error("%s: NULL buffer handle", what);
+    return nullptr;
+  }
+  Buffer* b = static_cast<Buffer*>(h);
+  if (b->magic != kMagicLive) {
+    set_error("%s: handle %p is not a live buffer (released or foreign)", what, h);
+    return nullptr;
+  }
+  return b;
+}
+
+// Small uploads travel as kernel arguments: the launch copies them, so the
+// host memory is free on return and nothing waits for queued work.
+struct SmallPayload {
+  float v[256];
+};
+__global__ void k_upload_small(float* __restrict__ dst, SmallPayload pl, uint32_t n) {
+  uint32_t i = threadIdx.x;
+  if (i < n) dst[i] = pl.v[i];
+}
+
+static bool upload(float* dst, const float* src, size_t n) {
+  if (n == 0) return true;
+  if (n <= 256) {
+    SmallPayload pl;
+    memcpy(pl.v, src, n * 4);
+    hipLaunchKernelGGL(k_upload_small, dim3(1), dim3(256), 0, g_stream, dst, pl, uint32_t(n));
+    return check_launch("upload");
+  }
+  if (!g_stage) {
+    if (hipHostMalloc((void**)&g_stage, kSlots * kSlotBytes, hipHostMallocDefault) != hipSuccess) {
+      g_stage = nullptr;
+      set_error("upload: pinned staging allocation failed");
+      return false;
+    }
+    for (int i = 0; i < kSlots; ++i) {
+      hipEventCreateWithFlags(&g_slotEv[i], hipEventDisableTiming);
+      g_slotBusy[i] = false;
+    }
+  }
+  const char* s = reinterpret_cast<const char*>(src);
+  char* d = reinterpret_cast<char*>(dst);
+  size_t bytes = n * 4;
+  while (bytes) {
+    size_t chunk = std::min(bytes, kSlotBytes);
+    int slot = g_nextSlot;
+    g_nextSlot = (g_nextSlot + 1) % kSlots;
+    if (g_slotBusy[slot]) hipEventSynchronize(g_slotEv[slot]);
+    char* st = g_stage + size_t(slot) * kSlotBytes;
+    memcpy(st, s, chunk);
+    if (hipMemcpyAsync(d, st, chunk, hipMemcpyHostToDevice, g_stream) != hipSuccess) {
+      set_error("upload: hipMemcpyAsync failed");
+      return false;
+    }
+    hipEventRecord(g_slotEv[slot], g_stream);
+    g_slotBusy[slot] = true;
+    s += chunk;
+    d += chunk;
+    bytes -= chunk;
+  }
+  return true;
+}
+
+void* create_buffer(const float* data, uint32_t count) {
+  if (!ensure_init()) return nullptr;
+  if (count == 0) {
+    set_error("CreateBuffer: zero-size buffer");
+    return nullptr;
+  }
+  Buffer* b = nullptr;
+  auto it = g_pool.find(count);
+  if (it != g_pool.end() && !it->second.empty()) {
+    b = it->second.back();
+    it->second.pop_back();
+    g_poolBytes -= uint64_t(count) * 4;
+    g_poolHits++;
+  } else {
+    g_poolMisses++;
+    float* p = nullptr;
+    size_t bytes = size_t(count) * 4;
+    if (hipMalloc((void**)&p, bytes) != hipSuccess) {
+      hipGetLastError();
+      drain_pool_locked();
+      if (hipMalloc((void**)&p, bytes) != hipSuccess) {
+        hipGetLastError();
+        set_error("CreateBuffer: out of device memory for %u floats", count);
+        return nullptr;
+      }
+    }
+    if (!g_recycled.empty()) {
+      b = g_recycled.back();
+      g_recycled.pop_back();
+    } else {
+      b = new Buffer();
+    }
+    b->ptr = p;
+    b->count = count;
+  }
+  b->refCount = 1;
+  b->magic = kMagicLive;
+  b->poolTag = 0;
+  if (data && !upload(b->ptr, data, count)) {
+    b->magic = kMagicPooled;
+    g_pool[count].push_back(b);
+    g_poolBytes += uint64_t(count) * 4;
+    return nullptr;
+  }
+  return b;
+}
+
+static void release_internal(Buffer* b) {
+  auto& pool = g_pool[b->count];
+  uint64_t bytes = uint64_t(b->count) * 4;
+  if (pool.size() < max_pool_for_size(b->count) && g_poolBytes + bytes <= g_poolCapBytes) {
+    b->magic = kMagicPooled;
+    b->poolTag = 0;
+    pool.push_back(b);
+    g_poolBytes += bytes;
+  } else {
+    free_record(b);
+  }
+}
+
+void release_buffer(void* h) {
+  if (!h) return;
+  Buffer* b = static_cast<Buffer*>(h);
+  if (b->magic != kMagicLive) {
+    set_error("ReleaseBuffer: handle %p is not live (double release?)", h);
+    return;
+  }
+  if (--b->refCount <= 0) release_internal(b);
+}
+
+float* workspace(size_t floats) {
+  if (floats <= g_wsFloats) return g_ws;
+  size_t want = std::max(floats, g_wsFloats * 3 / 2);
+  want = (want + 65535) & ~size_t(65535);
+  if (g_ws) {
+    hipStreamSynchronize(g_stream);
+    hipFree(g_ws);
+    g_ws = nullptr;
+    g_wsFloats = 0;
+  }
+  if (hipMalloc((void**)&g_ws, want * 4) != hipSuccess) {
+    hipGetLastError();
+    drain_pool_locked();
+    if (hipMalloc((void**)&g_ws, want * 4) != hipSuccess) {
+      hipGetLastError();
+      g_ws = nullptr;
+      set_error("workspace: cannot allocate %zu floats", want);
+      return nullptr;
+    }
+  }
+  g_wsFloats = want;
+  return g_ws;
+}
+
+static void read_pci_device_id(int dev, uint32_t* out) {
+  char bus[64] = {0};
+  *out = 0;
+  if (hipDeviceGetPCIBusId(bus, sizeof(bus), dev) != hipSuccess) return;
+  for (char* c = bus; *c; ++c) *c = (char)tolower(*c);
+  char path[160];
+  snprintf(path, sizeof(path), "/sys/bus/pci/devices/%s/device", bus);
+  FILE* f = fopen(path, "r");
+  if (!f) return;
+  unsigned v = 0;
+  if (fscanf(f, "%x", &v) == 1) *out = v;
+  fclose(f);
+}
+
+}  // namespace dce
+
+using namespace dce;
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+extern "C" {
+
+bool InitEngine(void) {
+  if (g_init) return true;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+    hipGetLastError();
+    set_error("InitEngine: no HIP device visible");
+    return false;
+  }
+  const char* env = getenv("DCE_DEVICE");
+  g_device = env ? atoi(env) : 0;
+  if (g_device < 0 || g_device >= n) g_device = 0;
+  if (hipSetDevice(g_device) != hipSuccess) {
+    set_error("InitEngine: hipSetDevice(%d) failed", g_device);
+    return false;
+  }
+  // Default priority, non-blocking with respect to the legacy null stream.
+  if (hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking) != hipSuccess) {
+    set_error("InitEngine: stream creation failed");
+    return false;
+  }
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, g_device) != hipSuccess) {
+    set_error("InitEngine: hipGetDeviceProperties failed");
+    return false;
+  }
+  g_cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+  memset(&g_info, 0, sizeof(g_info));
+  g_info.vendorId = 0x1002;
+  read_pci_device_id(g_device, &g_info.deviceId);
+  g_info.dedicatedVRAM = prop.totalGlobalMem;
+  g_info.sharedMemory = 0;
+  g_info.isIntegrated = prop.integrated ? 1u : 0u;
+  snprintf(g_info.description, sizeof(g_info.description), "%s (%s)",
+           prop.name[0] ? prop.name : "AMD Instinct GPU", prop.gcnArchName);
+  g_poolCapBytes = uint64_t(prop.totalGlobalMem) / 2;
+  if (hipMalloc((void**)&g_misc, 1024 * 4) != hipSuccess) {
+    set_error("InitEngine: scratch allocation failed");
+    return false;
+  }
+  g_init = true;
+  g_err[0] = 0;
+  return true;
+}
+
+void GetGPUInfo(GPUInfo* info) {
+  if (!info) return;
+  if (!g_init) {
+    memset(info, 0, sizeof(*info));
+    return;
+  }
+  *info = g_info;
+}
+
+const char* GetLastErrorString(void) { return g_err; }
+void ClearLastError(void) { g_err[0] = 0; }
+
+void* CreateBuffer(float* data, uint32_t count) { return create_buffer(data, count); }
+
+void AddRefBuffer(void* handle) {
+  if (!handle) return;
+  Buffer* b = as_buffer(handle, "AddRefBuffer");
+  if (b) b->refCount++;
+}
+
+void ReleaseBuffer(void* handle) { release_buffer(handle); }
+
+void ReleaseBufferBatch(void** handles, uint32_t count) {
+  if (!handles) return;
+  for (uint32_t i = 0; i < count; ++i) release_buffer(handles[i]);
+}
+
+void UpdateBuffer(void* handle, float* data) {
+  if (!handle || !data || !g_init) return;
+  Buffer* b = as_buffer(handle, "UpdateBuffer");
+  if (b) upload(b->ptr, data, b->count);
+}
+
+void ReadBuffer(void* handle, float* dst) {
+  if (!handle || !dst || !g_init) return;
+  Buffer* b = as_buffer(handle, "ReadBuffer");
+  if (!b) return;
+  if (hipMemcpyAsync(dst, b->ptr, size_t(b->count) * 4, hipMemcpyDeviceToHost, g_stream) !=
+      hipSuccess) {
+    set_error("ReadBuffer: copy failed");
+  }
+  if (hipStreamSynchronize(g_stream) != hipSuccess) set_error("ReadBuffer: stream error");
+}
+
+void ClearBuffer(void* handle) {
+  if (!handle || !g_init) return;
+  Buffer* b = as_buffer(handle, "ClearBuffer");
+  if (b) fill_zero(b->ptr, b->count);
+}
+
+void FlushGPU(void) {}
+
+void SyncGPU(void) {
+  if (g_init) hipStreamSynchronize(g_stream);
+}
+
+void WarmPool(uint32_t* sizes, uint32_t numSizes, uint32_t copies) {
+  if (!g_init || !sizes) return;
+  for (uint32_t i = 0; i < numSizes; ++i) {
+    uint32_t count = sizes[i];
+    if (!count) continue;
+    size_t target = std::min<size_t>(copies, max_pool_for_size(count));
+    auto& pool = g_pool[count];
+    while (pool.size() < target) {
+      uint64_t misses = g_poolMisses;
+      Buffer* b = static_cast<Buffer*>(create_buffer(nullptr, count));
+      g_poolMisses = misses;  // warm-up allocations are not misses
+      if (!b) break;
+      size_t before = pool.size();
+      release_internal(b);
+      if (pool.size() == before) break;  // pool byte cap reached
+    }
+  }
+}
+
+void GetPoolStats(uint64_t* hits, uint64_t* misses) {
+  if (hits) *hits = g_poolHits;
+  if (misses) *misses = g_poolMisses;
+}
+
+void ResetPoolStats(void) {
+  g_poolHits = 0;
+  g_poolMisses = 0;
+}
+
+uint64_t GetPoolMemory(void) { return g_poolBytes; }
+
+void DrainPool(void) {
+  if (g_init) drain_pool_locked();
+}
+
+// ------------------------------------------------------------------ dispatch
+bool CompileShader(const char* name, const wchar_t* path) {
+  (void)path;
+  return name && find_shader(name) != nullptr;
+}
+
+bool CompileShaderEx(const char* name, const wchar_t* path, const char* entry) {
+  (void)path;
+  (void)entry;
+  set_error("CompileShaderEx(%s): custom HLSL shaders are not supported", name ? name : "?");
+  return false;
+}
+
+void RunShader(const char* name, void** srvs, uint32_t srvCount, void** uavs,
+               uint32_t uavCount, uint32_t* threads, void* cb, uint32_t cbSize) {
+  if (!g_init || !name) return;
+  const ShaderEntry* e = find_shader(name);
+  if (!e) {
+    set_error("RunShader: unknown kernel '%s'", name);
+    return;
+  }
+  Dispatch d{srvs, srvCount, uavs, uavCount, threads, static_cast<const uint8_t*>(cb),
+             cb ? cbSize : 0u};
+  e->fn(d);
+}
+
+void RunShaderRaw(const char* name, void** srvs, uint32_t srvCount, void** uavs,
+                  uint32_t uavCount, uint32_t* threads, void* cb, uint32_t cbSize) {
+  RunShader(name, srvs, srvCount, uavs, uavCount, threads, cb, cbSize);
+}
+
+void* RunShaderAlloc(const char* name, void** srvs, uint32_t srvCount, uint32_t outCount,
+                     uint32_t* threads, void* cb, uint32_t cbSize) {
+  void* out = CreateBuffer(nullptr, outCount);
+  if (!out) return nullptr;
+  void* uavs[1] = {out};
+  RunShader(name, srvs, srvCount, uavs, 1, threads, cb, cbSize);
+  return out;
+}
+
+void* RunShaderAlloc2(const char* name, void** srvs, uint32_t srvCount, uint32_t outCount,
+                      void* extraUav, uint32_t* threads, void* cb, uint32_t cbSize) {
+  void* out = CreateBuffer(nullptr, outCount);
+  if (!out) return nullptr;
+  void* uavs[2] = {out, extraUav};
+  RunShader(name, srvs, srvCount, uavs, 2, threads, cb, cbSize);
+  return out;
+}
+
+void* ResolveShader(const char* name) {
+  if (!name) return nullptr;
+  return const_cast<ShaderEntry*>(find_shader(name));
+}
+
+void RunSequence(SeqCmd* cmds, uint32_t count) {
+  if (!g_init || !cmds) return;
+  for (uint32_t i = 0; i < count; ++i) {
+    SeqCmd& c = cmds[i];
+    if (!c.shader) continue;
+    const ShaderEntry* e = static_cast<const ShaderEntry*>(c.shader);
+    if (find_shader(e->name) != e) {
+      set_error("RunSequence: command %u has an unresolved shader pointer", i);
+      continue;
+    }
+    Dispatch d{c.srvs, std::min<uint32_t>(c.srvCount, 8), c.uavs,
+               std::min<uint32_t>(c.uavCount, 4), c.threads, c.cbData,
+               std::min<uint32_t>(c.cbSize, 64)};
+    e->fn(d);
+  }
+}
+
+void RunSequenceWithSGD(SeqCmd* cmds, uint32_t cmdCount, void** params, void** grads,
+                        uint32_t* sizes, uint32_t numParams, float lr, float clip) {
+  RunSequence(cmds, cmdCount);
+  SGDBatch(params, grads, sizes, numParams, lr, clip);
+}
+
+// -------------------------------------------------------------- fused: GEMM
+void* MatMulAlloc(void* a, void* b, uint32_t M, uint32_t K, uint32_t N, uint32_t flags) {
+  if (!g_init) return nullptr;
+  Buffer* A = as_buffer(a, "MatMulAlloc(A)");
+  Buffer* B = as_buffer(b, "MatMulAlloc(B)");
+  if (!A || !B) return nullptr;
+  if (uint64_t(M) * N == 0 || uint64_t(M) * N > 0xFFFFFFFFull) {
+    set_error("MatMulAlloc: bad output size %ux%u", M, N);
+    return nullptr;
+  }
+  if (uint64_t(A->count) < uint64_t(M) * K || uint64_t(B->count) < uint64_t(K) * N) {
+    set_error("MatMulAlloc: operand smaller than M=%u K=%u N=%u implies", M, K, N);
+    return nullptr;
+  }
+  void* out = create_buffer(nullptr, M * N);
+  if (!out) return nullptr;
+  if (!gemm(A->ptr, B->ptr, static_cast<Buffer*>(out)->ptr, M, K, N, flags & 3u)) {
+    release_buffer(out);
+    return nullptr;
+  }
+  return out;
+}
+
+// -------------------------------------------------------------- fused: conv
+static bool conv_geom(const char* what, uint32_t B, uint32_t C, uint32_t H, uint32_t W,
+                      uint32_t OC, uint32_t kH, uint32_t kW, uint32_t s, uint32_t p,
+                      ConvGeom* g) {
+  if (kH != kW) {
+    set_error("%s: only square kernels are supported (kH=%u kW=%u)", what, kH, kW);
+    return false;
+  }
+  if (!B || !C || !H || !W || !OC || !kH || !s || H + 2 * p < kH || W + 2 * p < kW) {
+    set_error("%s: invalid geometry", what);
+    return false;
+  }
+  g->B = B; g->C = C; g->H = H; g->W = W; g->OC = OC; g->k = kH; g->s = s; g->p = p;
+  g->OH = (H + 2 * p - kH) / s + 1;
+  g->OW = (W + 2 * p - kW) / s + 1;
+  uint64_t xs = uint64_t(B) * C * H * W, ys = uint64_t(B) * OC * g->OH * g->OW;
+  if (xs >= (1ull << 31) || ys >= (1ull << 31)) {
+    set_error("%s: tensor too large for 31-bit indexing", what);
+    return false;
+  }
+  return true;
+}
+
+void* ConvForwardFused(void* x, void* filters, void* bias, uint32_t batch, uint32_t inC,
+                       uint32_t inH, uint32_t inW, uint32_t outC, uint32_t kH, uint32_t kW,
+                       uint32_t stride, uint32_t padding, uint32_t actType, void** pIm2col) {
+  if (pIm2col) *pIm2col = nullptr;
+  if (!g_init) return nullptr;
+  ConvGeom g;
+  if (!conv_geom("ConvForwardFused", batch, inC, inH, inW, outC, kH, kW, stride, padding, &g))
+    return nullptr;
+  Buffer* X = as_buffer(x, "ConvForwardFused(x)");
+  Buffer* Wt = as_buffer(filters, "ConvForwardFused(filters)");
+  Buffer* Bi = as_buffer(bias, "ConvForwardFused(bias)");
+  if (!X || !Wt || !Bi) return nullptr;
+  if (X->count < batch * inC * inH * inW || Wt->count < outC * inC * kH * kW ||
+      Bi->count < outC) {
+    set_error("ConvForwardFused: buffer smaller than geometry");
+    return nullptr;
+  }
+  void* out = create_buffer(nullptr, batch * outC * g.OH * g.OW);
+  if (!out) return nullptr;
+  if (!conv_forward(X->ptr, Wt->ptr, Bi->ptr, static_cast<Buffer*>(out)->ptr, g, actType)) {
+    release_buffer(out);
+    return nullptr;
+  }
+  return out;
+}
+
+void ConvBackwardFused(void* gradOut, void* fwdOut, void* x, void* filters, void* im2col,
+                       uint32_t batch, uint32_t inC, uint32_t inH, uint32_t inW,
+                       uint32_t outC, uint32_t kH, uint32_t kW, uint32_t stride,
+                       uint32_t padding, uint32_t actType, uint32_t xReq, uint32_t wReq,
+                       uint32_t bReq, void** pDFilters, void** pDBias, void** pDInput) {
+  if (pDFilters) *pDFilters = nullptr;
+  if (pDBias) *pDBias = nullptr;
+  if (pDInput) *pDInput = nullptr;
+  if (!g_init) return;
+  ConvGeom g;
+  bool ok = conv_geom("ConvBackwardFused", batch, inC, inH, inW, outC, kH, kW, stride,
+                      padding, &g);
+  Buffer* DY = ok ? as_buffer(gradOut, "ConvBackwardFused(grad)") : nullptr;
+  Buffer* X = DY ? as_buffer(x, "ConvBackwardFused(x)") : nullptr;
+  Buffer* Wt = X ? as_buffer(filters, "ConvBackwardFused(filters)") : nullptr;
+  Buffer* Y = nullptr;
+  if (Wt && actType == 1 && fwdOut) Y = as_buffer(fwdOut, "ConvBackwardFused(fwd_output)");
+  uint32_t ysz = batch * outC * g.OH * g.OW;
+  if (Wt && (actType != 1 || !fwdOut || Y)) {
+    if (DY->count < ysz || (Y && Y->count < ysz) || X->count < batch * inC * inH * inW ||
+        Wt->count < outC * inC * kH * kW) {
+      set_error("ConvBackwardFused: buffer smaller than geometry");
+    } else {
+      const float* yp = Y ? Y->ptr : nullptr;
+      bool wantW = wReq && pDFilters, wantB = bReq && pDBias, wantX = xReq && pDInput;
+      void* dW = wantW ? create_buffer(nullptr, outC * inC * kH * kW) : nullptr;
+      void* dB = wantB ? create_buffer(nullptr, outC) : nullptr;
+      if ((wantW && !dW) || (wantB && !dB)) {
+        release_buffer(dW);
+        release_buffer(dB);
+      } else {
+        bool good = true;
+        if (wantW || wantB)
+          good = conv_backward_filter(DY->ptr, yp, X->ptr,
+                                      dW ? static_cast<Buffer*>(dW)->ptr : nullptr,
+                                      dB ? static_cast<Buffer*>(dB)->ptr : nullptr, g);
+        void* dX = nullptr;
+        if (good && wantX) {
+          dX = create_buffer(nullptr, batch * inC * inH * inW);
+          good = dX && conv_backward_input(DY->ptr, yp, Wt->ptr,
+                                           static_cast<Buffer*>(dX)->ptr, g);
+        }
+        if (good) {
+          if (pDFilters) *pDFilters = dW;
+          if (pDBias) *pDBias = dB;
+          if (pDInput) *pDInput = dX;
+        } else {
+          release_buffer(dW);
+          release_buffer(dB);
+          release_buffer(dX);
+        }
+      }
+    }
+  }
+  // The reference releases the im2col handle it is given (engine.cpp:877).
+  if (im2col) release_buffer(im2col);
+}
+
+// ----------------------------------------------------------- fused: maxpool
+void* MaxPoolForwardFused(void* x, uint32_t batch, uint32_t inC, uint32_t inH, uint32_t inW,
+                          uint32_t poolSize, uint32_t stride, void** pIndices) {
+  if (pIndices) *pIndices = nullptr;
+  if (!g_init) return nullptr;
+  Buffer* X = as_buffer(x, "MaxPoolForwardFused(x)");
+  if (!X) return nullptr;
+  if (!poolSize || !stride || inH < poolSize || inW < poolSize || !batch || !inC) {
+    set_error("MaxPoolForwardFused: invalid geometry");
+    return nullptr;
+  }
+  if (uint64_t(batch) * inC * inH * inW >= (1ull << 31) ||
+      X->count < batch * inC * inH * inW) {
+    set_error("MaxPoolForwardFused: input buffer does not match geometry");
+    return nullptr;
+  }
+  uint32_t OH = (inH - poolSize) / stride + 1, OW = (inW - poolSize) / stride + 1;
+  uint32_t n = batch * inC * OH * OW;
+  void* out = create_buffer(nullptr, n);
+  void* idx = create_buffer(nullptr, n);
+  if (!out || !idx) {
+    release_buffer(out);
+    release_buffer(idx);
+    return nullptr;
+  }
+  Buffer* I = static_cast<Buffer*>(idx);
+  if (!maxpool_forward(X->ptr, static_cast<Buffer*>(out)->ptr, I->ptr, batch, inC, inH, inW,
+                       poolSize, stride, OH, OW)) {
+    release_buffer(out);
+    release_buffer(idx);
+    return nullptr;
+  }
+  I->poolTag = kPoolTag;
+  I->poolH = inH;
+  I->poolW = inW;
+  I->poolK = poolSize;
+  I->poolS = stride;
+  if (pIndices)
+    *pIndices = idx;
+  else
+    release_buffer(idx);
+  return out;
+}
+
+void* MaxPoolBackwardFused(void* gradOut, void* indices, uint32_t batch, uint32_t inC,
+                           uint32_t outH, uint32_t outW, uint32_t xSize) {
+  if (!g_init) return nullptr;
+  Buffer* DZ = as_buffer(gradOut, "MaxPoolBackwardFused(grad)");
+  Buffer* I = DZ ? as_buffer(indices, "MaxPoolBackwardFused(indices)") : nullptr;
+  void* dx = nullptr;
+  uint32_t n = batch * inC * outH * outW;
+  if (I && (DZ->count < n || I->count < n)) {
+    set_error("MaxPoolBackwardFused: buffer smaller than geometry");
+  } else if (I) {
+    dx = create_buffer(nullptr, xSize);
+    if (dx) {
+      uint32_t H = 0, W = 0, k = 0, s = 0;
+      if (I->poolTag == kPoolTag && uint64_t(batch) * inC * I->poolH * I->poolW == xSize &&
+          (I->poolH - I->poolK) / I->poolS + 1 == outH &&
+          (I->poolW - I->poolK) / I->poolS + 1 == outW) {
+        H = I->poolH; W = I->poolW; k = I->poolK; s = I->poolS;
+      }
+      if (!maxpool_backward(DZ->ptr, I->ptr, static_cast<Buffer*>(dx)->ptr, batch, inC, outH,
+                            outW, xSize, H, W, k, s)) {
+        release_buffer(dx);
+        dx = nullptr;
+      }
+    }
+  }
+  // The reference releases the indices after routing (engine.cpp:928).
+  if (indices) release_buffer(indices);
+  return dx;
+}
+
+// ---------------------------------------------------------------- optimisers
+void SGDBatch(void** params, void** grads, uint32_t* sizes, uint32_t numParams, float lr,
+              float clip) {
+  if (!g_init || !params || !grads || !sizes || !numParams) return;
+  sgd_multi(params, grads, sizes, numParams, lr, clip);
+}
+
+float SGDBatchClipped(void** params, void** grads, uint32_t* sizes, uint32_t numParams,
+                      float lr, float maxNorm) {
+  if (!g_init || !params || !grads || !sizes || !numParams) return 0.0f;
+  float* d_ns = g_misc;  // [norm, scale]
+  if (!grad_norm_multi(grads, sizes, numParams, maxNorm, d_ns)) return 0.0f;
+  if (!sgd_scaled_multi(params, grads, sizes, numParams, lr, d_ns)) return 0.0f;
+  float h[2] = {0, 0};
+  hipMemcpyAsync(h, d_ns, 8, hipMemcpyDeviceToHost, g_stream);
+  hipStreamSynchronize(g_stream);
+  return h[0];
+}
+
+void AdamBatch(void** params, void** grads, void** m, void** v, uint32_t* sizes,
+               uint32_t numParams, float stepSize, float beta1, float beta2, float eps,
+               float weightDecay, float clip) {
+  if (!g_init || !params || !grads || !m || !v || !sizes || !numParams) return;
+  adam_multi(params, grads, m, v, sizes, numParams, stepSize, beta1, beta2, eps, weightDecay,
+             clip);
+}
+
+float ClipGradNorm(void** grads, uint32_t* sizes, uint32_t numGrads, float maxNorm) {
+  if (!g_init || !grads || !sizes || !numGrads) return 0.0f;
+  float* ns = g_misc;  // [norm, scale]
+  if (!grad_norm_multi(grads, sizes, numGrads, maxNorm, ns)) return 0.0f;
+  if (!scale_grads_multi(grads, sizes, numGrads, ns)) return 0.0f;
+  float h[2] = {0, 0};
+  hipMemcpyAsync(h, ns, 8, hipMemcpyDeviceToHost, g_stream);
+  hipStreamSynchronize(g_stream);
+  return h[0];
+}
+
+// ----------------------------------------------------------------- profiling
+void SetProfiling(int enabled) {
+  if (!enabled) resolve_profile();
+  g_prof = enabled != 0;
+}
+
+bool GetProfile(const char* family, uint64_t* launches, double* ms, double* flops,
+                double* bytes) {
+  resolve_profile();
+  if (!family) return false;
+  auto it = g_profStats.find(family);
+  if (it == g_profStats.end()) return false;
+  if (launches) *launches = it->second.launches;
+  if (ms) *ms = it->second.ms;
+  if (flops) *flops = it->second.flops;
+  if (bytes) *bytes = it->second.bytes;
+  return true;
+}
+
+void ResetProfile(void) {
+  resolve_profile();
+  g_profStats.clear();
+}
+
+}  // extern "C"

@@ -1,0 +1,139 @@
+// Internal interfaces shared by the libdcengine translation units.
+// Nothing here is part of the C ABI (that is include/dcengine.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <cstddef>
+
+namespace dce {
+
+// ---------------------------------------------------------------------------
+// Buffer record behind every opaque handle of the C ABI.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kMagicLive = 0xDCB0F1A7u;
+constexpr uint32_t kMagicPooled = 0xDCB0900Du;
+constexpr uint32_t kMagicDead = 0xDEADB0F5u;
+
+struct Buffer {
+  float* ptr;         // device pointer (256-byte aligned, hipMalloc)
+  uint32_t count;     // element count in floats (the reference's u32 size)
+  int refCount;
+  uint32_t magic;
+  // Pooling geometry recorded by MaxPoolForwardFused on the indices buffer it
+  // returns, so the backward can run as a deterministic gather.  tag == 0
+  // means "no geometry known".
+  uint32_t poolTag, poolH, poolW, poolK, poolS;
+};
+constexpr uint32_t kPoolTag = 0x9001u;
+
+// A bounds-carrying view used by the RunShader-compatible kernels: reads past
+// `n` return 0 and writes past `n` are dropped, like D3D11 structured buffers.
+struct Buf {
+  float* p;
+  uint32_t n;
+};
+
+// Engine state accessors (dce_engine.hip).
+hipStream_t stream();
+int num_cus();
+bool ensure_init();
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+bool check_launch(const char* what);
+
+// Persistent scratch space in device memory, reused by consecutive launches on
+// the single in-order stream.  Grows on demand (the old block is freed only
+// after the stream drains).  Returns nullptr (error set) on failure.
+float* workspace(size_t floats);
+
+// Handle validation: returns the Buffer or nullptr (error set) for NULL,
+// released or foreign handles.
+Buffer* as_buffer(void* h, const char* what);
+void* create_buffer(const float* host, uint32_t count);
+void release_buffer(void* h);
+
+// ---------------------------------------------------------------------------
+// Fast unsigned division by a run-time constant (numerators < 2^31).
+// q = (umulhi(n, mul) + n) >> shr, with mul/shr computed on the host.
+// ---------------------------------------------------------------------------
+struct FastDiv {
+  uint32_t d, mul, shr;
+};
+FastDiv make_fastdiv(uint32_t d);
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, FastDiv f) {
+  return (__umulhi(n, f.mul) + n) >> f.shr;
+}
+
+// ---------------------------------------------------------------------------
+// Convolution geometry (NCHW, square kernels, zero padding, floor mode).
+// ---------------------------------------------------------------------------
+struct ConvGeom {
+  uint32_t B, C, H, W, OC, k, s, p, OH, OW;
+};
+
+// Implicit-GEMM MFMA launchers (dce_igemm.hip).  All pointers are device
+// pointers with at least the extents implied by the geometry.
+bool conv_forward(const float* x, const float* w, const float* bias, float* y,
+                  const ConvGeom& g, uint32_t act);
+// dW[OC, C*k*k] and (optionally) db[OC] from G = mask(dy, y).  `y` may be
+// null (no mask).  dw or db may be null when not requested.
+bool conv_backward_filter(const float* dy, const float* y, const float* x,
+                          float* dw, float* db, const ConvGeom& g);
+bool conv_backward_input(const float* dy, const float* y, const float* w,
+                         float* dx, const ConvGeom& g);
+// C[M,N] = op(A)·op(B); flags bit0: A stored K×M, bit1: B stored N×K.
+bool gemm(const float* a, const float* b, float* c, uint32_t M, uint32_t K,
+          uint32_t N, uint32_t flags);
+
+// Profiling hooks (dce_engine.hip): kernel-family timing with HIP events on
+// the engine stream.  `family` is a short static string.
+struct ProfScope {
+  const char* family;
+  double flops;
+  double bytes;
+  void* ev0;
+  ProfScope(const char* fam, double fl, double by);
+  ~ProfScope();
+};
+
+// Elementwise / reduction launchers used by the fused C entry points
+// (dce_kernels.hip).
+bool fill_zero(float* p, size_t n);
+bool maxpool_forward(const float* x, float* out, float* idx, uint32_t B, uint32_t C,
+                     uint32_t H, uint32_t W, uint32_t k, uint32_t s, uint32_t OH,
+                     uint32_t OW);
+bool maxpool_backward(const float* dz, const float* idx, float* dx, uint32_t B,
+                      uint32_t C, uint32_t OH, uint32_t OW, uint32_t xcount,
+                      uint32_t H, uint32_t W, uint32_t k, uint32_t s);
+
+// Shader registry (dce_kernels.hip).
+struct Dispatch {
+  void** srvs;
+  uint32_t nS;
+  void** uavs;
+  uint32_t nU;
+  const uint32_t* groups;
+  const uint8_t* cb;
+  uint32_t cbBytes;
+};
+typedef bool (*ShaderFn)(const Dispatch&);
+struct ShaderEntry {
+  const char* name;
+  ShaderFn fn;
+};
+const ShaderEntry* find_shader(const char* name);
+
+// Multi-tensor optimiser launchers (dce_optim.hip).
+bool sgd_multi(void** params, void** grads, const uint32_t* sizes, uint32_t n,
+               float lr, float clip);
+bool grad_norm_multi(void** grads, const uint32_t* sizes, uint32_t n, float max_norm,
+                     float* d_norm_scale /* device [2] */);
+bool sgd_scaled_multi(void** params, void** grads, const uint32_t* sizes, uint32_t n,
+                      float lr, const float* d_norm_scale);
+bool scale_grads_multi(void** grads, const uint32_t* sizes, uint32_t n,
+                       const float* d_norm_scale);
+bool adam_multi(void** params, void** grads, void** m, void** v, const uint32_t* sizes,
+                uint32_t n, float step, float b1, float b2, float eps, float wd, float clip);
+
+}  // namespace dce

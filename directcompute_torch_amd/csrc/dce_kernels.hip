@@ -1,0 +1,1282 @@
+// Memory-bound kernels and the RunShader registry.
+//
+// Each registry entry takes the reference shader's inputs (t-registers),
+// outputs (u-registers) and packed constant buffer, validates them on the
+// host, and launches a HIP kernel whose grid is derived from the constants.
+// Two flavours per hot op:
+//   * fast path: every buffer is at least as large as the constants imply ->
+//     unchecked, float4-vectorised where the layout allows;
+//   * checked path: D3D11 structured-buffer semantics (reads past a buffer
+//     return 0, writes past it are dropped), element by element.
+// Reductions are deterministic: per-thread partial sums, a fixed-shape
+// wave/LDS tree, and (for long rows) per-piece partials summed in a fixed
+// order by a second pass.
+#include "dce_internal.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+namespace dce {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+static inline uint32_t cdiv(uint64_t a, uint64_t b) { return uint32_t((a + b - 1) / b); }
+
+__device__ __forceinline__ float ld(const Buf& b, uint32_t i) { return i < b.n ? b.p[i] : 0.f; }
+__device__ __forceinline__ void st(const Buf& b, uint32_t i, float v) {
+  if (i < b.n) b.p[i] = v;
+}
+__device__ __forceinline__ uint32_t gtid() { return blockIdx.x * blockDim.x + threadIdx.x; }
+
+// Block-wide sum (256 threads) in double; result valid in thread 0.
+__device__ __forceinline__ double block_sum256(double v, double* sh) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_down(v, o, 64);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) sh[w] = v;
+  __syncthreads();
+  double s = 0;
+  if (threadIdx.x == 0) s = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+  return s;
+}
+
+// ===========================================================================
+// Generic elementwise kernels: out[i] = F(in0[i], in1[i]).
+// ===========================================================================
+template <class F>
+__global__ void k_ew_checked(F f, Buf out, Buf a, Buf b, uint32_t n) {
+  const uint32_t i = gtid();
+  if (i < n) st(out, i, f(ld(a, i), ld(b, i)));
+}
+
+template <class F>
+__global__ void k_ew_fast(F f, float* __restrict__ out, const float* __restrict__ a,
+                          const float* __restrict__ b, uint32_t n) {
+  const uint32_t i4 = gtid() * 4;
+  if (i4 + 3 < n) {
+    const f4 va = *reinterpret_cast<const f4*>(a + i4);
+    const f4 vb = b ? *reinterpret_cast<const f4*>(b + i4) : f4{0.f, 0.f, 0.f, 0.f};
+    f4 r;
+    r[0] = f(va[0], vb[0]);
+    r[1] = f(va[1], vb[1]);
+    r[2] = f(va[2], vb[2]);
+    r[3] = f(va[3], vb[3]);
+    *reinterpret_cast<f4*>(out + i4) = r;
+  } else {
+    for (uint32_t i = i4; i < n; ++i) out[i] = f(a[i], b ? b[i] : 0.f);
+  }
+}
+
+// Launch an elementwise op over n elements; fast path when every buffer
+// covers n.  `b` may be unbound (n == 0) for unary ops.
+template <class F>
+static bool run_ew(const char* what, F f, Buf out, Buf a, Buf b, uint32_t n, bool unary) {
+  if (n == 0) return true;
+  const bool fast = out.n >= n && a.n >= n && (unary || b.n >= n) && out.p && a.p &&
+                    (unary || b.p);
+  if (fast) {
+    hipLaunchKernelGGL(k_ew_fast<F>, dim3(cdiv(cdiv(n, 4), 256)), dim3(256), 0, stream(), f,
+                       out.p, a.p, unary ? nullptr : b.p, n);
+  } else {
+    hipLaunchKernelGGL(k_ew_checked<F>, dim3(cdiv(n, 256)), dim3(256), 0, stream(), f, out, a,
+                       b, n);
+  }
+  return check_launch(what);
+}
+
+struct OpRelu {
+  __device__ float operator()(float a, float) const { return fmaxf(0.f, a); }
+};
+struct OpReluGrad {  // nn_relu_grad.hlsl:8
+  __device__ float operator()(float g, float in) const { return in > 0.f ? g : 0.f; }
+};
+struct OpRelu6 {  // nn_relu6.hlsl:8-9
+  __device__ float operator()(float x, float) const { return fminf(fmaxf(x, 0.f), 6.f); }
+};
+struct OpRelu6Grad {  // nn_relu6_grad.hlsl:9-10
+  __device__ float operator()(float g, float x) const { return (x > 0.f && x < 6.f) ? g : 0.f; }
+};
+struct OpSigmoid {  // nn_sigmoid.hlsl:12
+  __device__ float operator()(float x, float) const { return 1.0f / (1.0f + expf(-x)); }
+};
+struct OpSigmoidGrad {  // nn_sigmoid_grad.hlsl:12-14
+  __device__ float operator()(float dy, float y) const { return dy * y * (1.0f - y); }
+};
+struct OpLeaky {  // nn_leaky_relu.hlsl:13-14
+  float alpha;
+  __device__ float operator()(float x, float) const { return x > 0.f ? x : x * alpha; }
+};
+struct OpLeakyGrad {  // nn_leaky_relu_grad.hlsl:13-16
+  float alpha;
+  __device__ float operator()(float dy, float x) const { return dy * (x > 0.f ? 1.0f : alpha); }
+};
+struct OpAdd {
+  __device__ float operator()(float a, float b) const { return a + b; }
+};
+struct OpScaleAdd {  // nn_scale_add.hlsl:9
+  float alpha, beta;
+  __device__ float operator()(float a, float b) const { return alpha * a + beta * b; }
+};
+struct OpCopy {
+  __device__ float operator()(float a, float) const { return a; }
+};
+
+__global__ void k_fill(float* __restrict__ p, float v, size_t n) {
+  size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const size_t stride = size_t(gridDim.x) * blockDim.x;
+  for (; i < n; i += stride) p[i] = v;
+}
+
+bool fill_zero(float* p, size_t n) {
+  if (n == 0) return true;
+  uint32_t blocks = uint32_t(std::min<size_t>(cdiv(n, 256), size_t(num_cus()) * 16));
+  hipLaunchKernelGGL(k_fill, dim3(blocks), dim3(256), 0, stream(), p, 0.f, n);
+  return check_launch("fill");
+}
+
+// ===========================================================================
+// Registry helpers
+// ===========================================================================
+static Buf bind(void** arr, uint32_t count, uint32_t i) {
+  if (!arr || i >= count || !arr[i]) return Buf{nullptr, 0};
+  Buffer* b = static_cast<Buffer*>(arr[i]);
+  if (b->magic != kMagicLive) {
+    set_error("RunShader: slot %u holds a handle that is not live", i);
+    return Buf{nullptr, 0};
+  }
+  return Buf{b->ptr, b->count};
+}
+static inline Buf S(const Dispatch& d, uint32_t i) { return bind(d.srvs, d.nS, i); }
+static inline Buf U(const Dispatch& d, uint32_t i) { return bind(d.uavs, d.nU, i); }
+static inline uint32_t CU(const Dispatch& d, uint32_t i) {
+  if (!d.cb || (i + 1) * 4 > d.cbBytes) return 0;
+  uint32_t v;
+  memcpy(&v, d.cb + 4 * i, 4);
+  return v;
+}
+static inline float CF(const Dispatch& d, uint32_t i) {
+  uint32_t u = CU(d, i);
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+static inline bool covers(const Buf& b, uint64_t n) { return b.p && uint64_t(b.n) >= n; }
+
+// ===========================================================================
+// Elementwise shaders
+// ===========================================================================
+static bool sh_relu(const Dispatch& d) {  // nn_relu.hlsl: no constants, bounded by the output
+  Buf o = U(d, 0);
+  return run_ew("relu", OpRelu{}, o, S(d, 0), Buf{nullptr, 0}, o.n, true);
+}
+static bool sh_relu_grad(const Dispatch& d) {
+  return run_ew("relu_grad", OpReluGrad{}, U(d, 0), S(d, 0), S(d, 1), CU(d, 0), false);
+}
+static bool sh_relu6(const Dispatch& d) {
+  return run_ew("relu6", OpRelu6{}, U(d, 0), S(d, 0), Buf{nullptr, 0}, CU(d, 0), true);
+}
+static bool sh_relu6_grad(const Dispatch& d) {
+  return run_ew("relu6_grad", OpRelu6Grad{}, U(d, 0), S(d, 0), S(d, 1), CU(d, 0), false);
+}
+static bool sh_sigmoid(const Dispatch& d) {
+  return run_ew("sigmoid", OpSigmoid{}, U(d, 0), S(d, 0), Buf{nullptr, 0}, CU(d, 0), true);
+}
+static bool sh_sigmoid_grad(const Dispatch& d) {
+  return run_ew("sigmoid_grad", OpSigmoidGrad{}, U(d, 0), S(d, 0), S(d, 1), CU(d, 0), false);
+}
+static bool sh_leaky(const Dispatch& d) {
+  return run_ew("leaky_relu", OpLeaky{CF(d, 1)}, U(d, 0), S(d, 0), Buf{nullptr, 0}, CU(d, 0),
+                true);
+}
+static bool sh_leaky_grad(const Dispatch& d) {
+  return run_ew("leaky_relu_grad", OpLeakyGrad{CF(d, 1)}, U(d, 0), S(d, 0), S(d, 1), CU(d, 0),
+                false);
+}
+static bool sh_add(const Dispatch& d) {  // nn_add.hlsl: count = M*N
+  uint64_t n = uint64_t(CU(d, 0)) * CU(d, 1);
+  return run_ew("add", OpAdd{}, U(d, 0), S(d, 0), S(d, 1), uint32_t(std::min<uint64_t>(n, 0xFFFFFFFFu)), false);
+}
+static bool sh_scale_add(const Dispatch& d) {
+  return run_ew("scale_add", OpScaleAdd{CF(d, 1), CF(d, 2)}, U(d, 0), S(d, 0), S(d, 1), CU(d, 0),
+                false);
+}
+static bool sh_grad_accum(const Dispatch& d) {  // acc[i] += g[i]
+  Buf acc = U(d, 0);
+  return run_ew("grad_accum", OpAdd{}, acc, acc, S(d, 0), CU(d, 0), false);
+}
+
+// add_bias / bias_relu: C[i] = A[i] + B[i % N] (+ ReLU), i < M*N.
+template <bool RELU>
+__global__ void k_add_bias(Buf C, Buf A, Buf B, uint32_t n, uint32_t N) {
+  const uint32_t i = gtid();
+  if (i >= n) return;
+  float v = ld(A, i) + ld(B, i % N);
+  st(C, i, RELU ? fmaxf(0.f, v) : v);
+}
+template <bool RELU>
+static bool sh_add_bias_t(const Dispatch& d) {
+  uint64_t n = uint64_t(CU(d, 0)) * CU(d, 1);
+  uint32_t N = CU(d, 1);
+  if (!n || !N) return true;
+  hipLaunchKernelGGL(k_add_bias<RELU>, dim3(cdiv(n, 256)), dim3(256), 0, stream(), U(d, 0),
+                     S(d, 0), S(d, 1), uint32_t(n), N);
+  return check_launch("add_bias");
+}
+
+// ===========================================================================
+// bias_grad: g[c] = sum_{i<rows} G[i*stride_i + c*stride_id]
+// (nn_bias_grad.hlsl).  Two layouts matter: stride_id == 1 (columns of a
+// row-major matrix: one thread per column, coalesced over columns) and
+// stride_i == 1 (contiguous rows: one block per class).
+// ===========================================================================
+__global__ void k_bias_grad_cols(Buf G, Buf g, uint32_t rows, uint32_t classes, uint32_t si,
+                                 uint32_t sid) {
+  const uint32_t c = gtid();
+  if (c >= classes) return;
+  float s = 0.f;
+  for (uint32_t i = 0; i < rows; ++i) s += ld(G, i * si + c * sid);
+  st(g, c, s);
+}
+__global__ void k_bias_grad_rows(Buf G, Buf g, uint32_t rows, uint32_t si, uint32_t sid) {
+  __shared__ double sh[4];
+  const uint32_t c = blockIdx.x;
+  float s = 0.f;
+  for (uint32_t i = threadIdx.x; i < rows; i += 256) s += ld(G, i * si + c * sid);
+  double t = block_sum256(double(s), sh);
+  if (threadIdx.x == 0) st(g, c, float(t));
+}
+static bool sh_bias_grad(const Dispatch& d) {
+  uint32_t rows = CU(d, 0), classes = CU(d, 1), si = CU(d, 2), sid = CU(d, 3);
+  if (!classes) return true;
+  if (rows >= 4096 && sid != 1) {
+    hipLaunchKernelGGL(k_bias_grad_rows, dim3(classes), dim3(256), 0, stream(), S(d, 0), U(d, 0),
+                       rows, si, sid);
+  } else {
+    hipLaunchKernelGGL(k_bias_grad_cols, dim3(cdiv(classes, 256)), dim3(256), 0, stream(),
+                       S(d, 0), U(d, 0), rows, classes, si, sid);
+  }
+  return check_launch("bias_grad");
+}
+
+// ===========================================================================
+// Softmax, cross-entropy, its gradient, metrics
+// ===========================================================================
+// One wave per row: softmax (nn_softmax.hlsl) and/or the row's CE term
+// (nn_loss.hlsl:20-32).  The row term goes to rowLoss when non-null.
+__global__ void k_softmax_rows(Buf in, Buf out, Buf labels, float* rowLoss, uint32_t B,
+                               uint32_t K, int writeSoftmax) {
+  const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= B) return;
+  const uint32_t base = row * K;
+  float mx = -1e30f;
+  for (uint32_t j = lane; j < K; j += 64) mx = fmaxf(mx, ld(in, base + j));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  float s = 0.f;
+  for (uint32_t j = lane; j < K; j += 64) s += expf(ld(in, base + j) - mx);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  if (writeSoftmax) {
+    for (uint32_t j = lane; j < K; j += 64) st(out, base + j, expf(ld(in, base + j) - mx) / s);
+  }
+  if (rowLoss && lane == 0) {
+    const uint32_t label = uint32_t(ld(labels, row));
+    rowLoss[row] = -(ld(in, base + label) - mx - logf(s));
+  }
+}
+__global__ void k_mean_rows(const float* rowLoss, Buf loss, uint32_t B) {
+  __shared__ double sh[4];
+  double s = 0;
+  for (uint32_t i = threadIdx.x; i < B; i += 256) s += rowLoss[i];
+  s = block_sum256(s, sh);
+  if (threadIdx.x == 0) st(loss, 0, float(s / double(B)));
+}
+static bool sh_softmax(const Dispatch& d) {
+  uint32_t B = CU(d, 0), K = CU(d, 1);
+  if (!B || !K) return true;
+  hipLaunchKernelGGL(k_softmax_rows, dim3(cdiv(B, 4)), dim3(256), 0, stream(), S(d, 0), U(d, 0),
+                     Buf{nullptr, 0}, nullptr, B, K, 1);
+  return check_launch("softmax");
+}
+static bool sh_loss(const Dispatch& d) {
+  uint32_t B = CU(d, 0), K = CU(d, 1);
+  if (!B || !K) return true;
+  float* rl = workspace(B);
+  if (!rl) return false;
+  hipLaunchKernelGGL(k_softmax_rows, dim3(cdiv(B, 4)), dim3(256), 0, stream(), S(d, 0),
+                     Buf{nullptr, 0}, S(d, 1), rl, B, K, 0);
+  hipLaunchKernelGGL(k_mean_rows, dim3(1), dim3(256), 0, stream(), rl, U(d, 0), B);
+  return check_launch("loss");
+}
+// (p - onehot(label))/B with the one-hot test labels[b] == (float)j.
+__global__ void k_softmax_ce_grad(Buf p, Buf labels, Buf g, uint32_t B, uint32_t K) {
+  const uint32_t i = gtid();
+  if (i >= B * K) return;
+  const uint32_t b = i / K, j = i - b * K;
+  const float lab = (ld(labels, b) == float(j)) ? 1.0f : 0.0f;
+  st(g, i, (ld(p, i) - lab) / float(B));
+}
+static bool sh_softmax_ce_grad(const Dispatch& d) {
+  uint32_t B = CU(d, 0), K = CU(d, 1);
+  if (!B || !K) return true;
+  hipLaunchKernelGGL(k_softmax_ce_grad, dim3(cdiv(uint64_t(B) * K, 256)), dim3(256), 0, stream(),
+                     S(d, 0), S(d, 1), U(d, 0), B, K);
+  return check_launch("softmax_ce_grad");
+}
+// First-max-wins argmax (strict >, from column 0), count matches on a u32 view.
+__global__ void k_argmax_correct(Buf logits, Buf labels, Buf cnt, uint32_t B, uint32_t K) {
+  const uint32_t i = gtid();
+  if (i >= B) return;
+  const uint32_t label = uint32_t(ld(labels, i));
+  float mx = ld(logits, i * K);
+  uint32_t mi = 0;
+  for (uint32_t j = 1; j < K; ++j) {
+    const float v = ld(logits, i * K + j);
+    if (v > mx) {
+      mx = v;
+      mi = j;
+    }
+  }
+  if (mi == label && cnt.n > 0) atomicAdd(reinterpret_cast<unsigned int*>(cnt.p), 1u);
+}
+static bool sh_argmax_correct(const Dispatch& d) {
+  uint32_t B = CU(d, 0), K = CU(d, 1);
+  if (!B || !K) return true;
+  hipLaunchKernelGGL(k_argmax_correct, dim3(cdiv(B, 256)), dim3(256), 0, stream(), S(d, 0),
+                     S(d, 1), U(d, 0), B, K);
+  return check_launch("argmax_correct");
+}
+__global__ void k_accumulate_scalar(Buf src, Buf dst) {
+  if (threadIdx.x == 0 && dst.n > 0) dst.p[0] = dst.p[0] + ld(src, 0);
+}
+static bool sh_accumulate_scalar(const Dispatch& d) {
+  hipLaunchKernelGGL(k_accumulate_scalar, dim3(1), dim3(64), 0, stream(), S(d, 0), U(d, 0));
+  return check_launch("accumulate_scalar");
+}
+
+// ===========================================================================
+// Dice loss (per-sample sums over `size` elements)
+// ===========================================================================
+// mode 0: Out[b] = 1 - 2I/(P+T+1e-6); mode 1: Sums[b*3 + {0,1,2}] = {I, P, T}
+__global__ void k_dice_sums(Buf pred, Buf tgt, Buf out, uint32_t B, uint32_t size, int mode) {
+  __shared__ double sh[4];
+  const uint32_t b = blockIdx.x;
+  float si = 0.f, sp = 0.f, stt = 0.f;
+  const uint32_t off = b * size;
+  for (uint32_t i = threadIdx.x; i < size; i += 256) {
+    const float p = ld(pred, off + i), t = ld(tgt, off + i);
+    si += p * t;
+    sp += p;
+    stt += t;
+  }
+  const double I = block_sum256(si, sh);
+  const double P = block_sum256(sp, sh);
+  const double T = block_sum256(stt, sh);
+  if (threadIdx.x == 0) {
+    if (mode == 0) {
+      const float dice = (2.0f * float(I)) / (float(P) + float(T) + 1e-6f);
+      st(out, b, 1.0f - dice);
+    } else {
+      st(out, b * 3 + 0, float(I));
+      st(out, b * 3 + 1, float(P));
+      st(out, b * 3 + 2, float(T));
+    }
+  }
+}
+static bool sh_dice_t(const Dispatch& d, int mode) {
+  uint32_t B = CU(d, 0), size = CU(d, 1);
+  if (!B) return true;
+  hipLaunchKernelGGL(k_dice_sums, dim3(B), dim3(256), 0, stream(), S(d, 0), S(d, 1), U(d, 0), B,
+                     size, mode);
+  return check_launch("dice");
+}
+static bool sh_dice_loss(const Dispatch& d) { return sh_dice_t(d, 0); }
+static bool sh_dice_sums(const Dispatch& d) { return sh_dice_t(d, 1); }
+// nn_dice_loss_grad.hlsl:22-33
+__global__ void k_dice_grad(Buf pred, Buf tgt, Buf sums, Buf dx, uint32_t B, uint32_t size) {
+  const uint32_t i = gtid();
+  if (i >= B * size) return;
+  const uint32_t b = i / size;
+  const float I = ld(sums, b * 3), P = ld(sums, b * 3 + 1), T = ld(sums, b * 3 + 2);
+  const float D = P + T + 1e-6f;
+  const float t = ld(tgt, i);
+  (void)pred;
+  const float g = -2.0f * ((t * D) - I) / (D * D);
+  st(dx, i, g / float(B));
+}
+static bool sh_dice_grad(const Dispatch& d) {
+  uint32_t B = CU(d, 0), size = CU(d, 1);
+  if (!B || !size) return true;
+  hipLaunchKernelGGL(k_dice_grad, dim3(cdiv(uint64_t(B) * size, 256)), dim3(256), 0, stream(),
+                     S(d, 0), S(d, 1), S(d, 2), U(d, 0), B, size);
+  return check_launch("dice_grad");
+}
+
+// ===========================================================================
+// Batch normalisation.  Per-channel sums over N*S elements are split into
+// `pieces` contiguous slices of the (n, s) range; slice partials (double)
+// are combined in a fixed order by a per-channel finalize.
+// ===========================================================================
+struct BnPieces {
+  uint32_t pieces;
+  uint32_t len;  // elements per channel = N*S
+};
+static BnPieces bn_pieces(uint32_t N, uint32_t S) {
+  BnPieces p;
+  p.len = N * S;
+  p.pieces = std::max<uint32_t>(1, std::min<uint32_t>(cdiv(p.len, 8192), 128));
+  return p;
+}
+
+// MODE 0: (Σx, Σx²).  MODE 1: (Σdy·x̂, Σdy) with x̂ from mean/var/eps.
+template <int MODE, bool CHECK>
+__global__ void k_bn_partial(Buf x, Buf dy, Buf mean, Buf var, float eps, uint32_t C, uint32_t S,
+                             uint32_t len, uint32_t pieces, FastDiv dS, double* part) {
+  __shared__ double sh[4];
+  const uint32_t c = blockIdx.y, pc = blockIdx.x;
+  const uint32_t i0 = uint32_t((uint64_t(len) * pc) / pieces);
+  const uint32_t i1 = uint32_t((uint64_t(len) * (pc + 1)) / pieces);
+  float mu = 0.f, rstd = 0.f;
+  if (MODE == 1) {
+    mu = ld(mean, c);
+    rstd = 1.0f / sqrtf(ld(var, c) + eps);
+  }
+  float a0 = 0.f, a1 = 0.f;
+  for (uint32_t i = i0 + threadIdx.x; i < i1; i += 256) {
+    const uint32_t n = fdiv(i, dS);
+    const uint32_t idx = n * C * S + c * S + (i - n * S);
+    const float xv = CHECK ? ld(x, idx) : x.p[idx];
+    if (MODE == 0) {
+      a0 += xv;
+      a1 += xv * xv;
+    } else {
+      const float g = CHECK ? ld(dy, idx) : dy.p[idx];
+      const float xh = (xv - mu) * rstd;
+      a0 += g * xh;
+      a1 += g;
+    }
+  }
+  const double s0 = block_sum256(a0, sh);
+  const double s1 = block_sum256(a1, sh);
+  if (threadIdx.x == 0) {
+    part[(size_t(c) * pieces + pc) * 2 + 0] = s0;
+    part[(size_t(c) * pieces + pc) * 2 + 1] = s1;
+  }
+}
+
+// batchnorm_mean_var finalize (nn_batchnorm_mean_var.hlsl:46-59).
+__global__ void k_bn_stats_final(const double* part, uint32_t pieces, uint32_t C, uint32_t m,
+                                 Buf mean, Buf var, Buf rmean, Buf rvar, uint32_t training,
+                                 float momentum) {
+  const uint32_t c = gtid();
+  if (c >= C) return;
+  double s0 = 0, s1 = 0;
+  for (uint32_t p = 0; p < pieces; ++p) {
+    s0 += part[(size_t(c) * pieces + p) * 2];
+    s1 += part[(size_t(c) * pieces + p) * 2 + 1];
+  }
+  const float mu = float(s0 / m);
+  const float x2 = float(s1 / m);
+  const float v = fmaxf(0.f, x2 - mu * mu);
+  st(mean, c, mu);
+  st(var, c, v);
+  if (training == 1) {
+    const float unb = v * (float(m) / fmaxf(1.0f, float(m - 1)));
+    st(rmean, c, (1.0f - momentum) * ld(rmean, c) + momentum * mu);
+    st(rvar, c, (1.0f - momentum) * ld(rvar, c) + momentum * unb);
+  }
+}
+__global__ void k_bn_grad_final(const double* part, uint32_t pieces, uint32_t C, Buf dgamma,
+                                Buf dbeta) {
+  const uint32_t c = gtid();
+  if (c >= C) return;
+  double s0 = 0, s1 = 0;
+  for (uint32_t p = 0; p < pieces; ++p) {
+    s0 += part[(size_t(c) * pieces + p) * 2];
+    s1 += part[(size_t(c) * pieces + p) * 2 + 1];
+  }
+  st(dgamma, c, float(s0));
+  st(dbeta, c, float(s1));
+}
+
+static bool bn_reduce(const char* what, int mode, const Dispatch& d, Buf x, Buf dy, Buf mean,
+                      Buf var, float eps, uint32_t N, uint32_t C, uint32_t S, double** partOut,
+                      BnPieces* pcOut) {
+  BnPieces pc = bn_pieces(N, S);
+  const uint64_t total = uint64_t(N) * C * S;
+  if (!total || total >= (1ull << 31)) {
+    if (total) set_error("%s: tensor too large", what);
+    return false;
+  }
+  double* part = reinterpret_cast<double*>(workspace(size_t(C) * pc.pieces * 4));
+  if (!part) return false;
+  const bool fast = covers(x, total) && (mode == 0 || covers(dy, total));
+  dim3 grid(pc.pieces, C);
+  FastDiv dS = make_fastdiv(S);
+  if (mode == 0) {
+    if (fast)
+      hipLaunchKernelGGL((k_bn_partial<0, false>), grid, dim3(256), 0, stream(), x, dy, mean, var,
+                         eps, C, S, pc.len, pc.pieces, dS, part);
+    else
+      hipLaunchKernelGGL((k_bn_partial<0, true>), grid, dim3(256), 0, stream(), x, dy, mean, var,
+                         eps, C, S, pc.len, pc.pieces, dS, part);
+  } else {
+    if (fast)
+      hipLaunchKernelGGL((k_bn_partial<1, false>), grid, dim3(256), 0, stream(), x, dy, mean, var,
+                         eps, C, S, pc.len, pc.pieces, dS, part);
+    else
+      hipLaunchKernelGGL((k_bn_partial<1, true>), grid, dim3(256), 0, stream(), x, dy, mean, var,
+                         eps, C, S, pc.len, pc.pieces, dS, part);
+  }
+  (void)d;
+  *partOut = part;
+  *pcOut = pc;
+  return check_launch(what);
+}
+
+static bool sh_bn_mean_var(const Dispatch& d) {
+  uint32_t N = CU(d, 0), C = CU(d, 1), Sz = CU(d, 2), training = CU(d, 3);
+  float momentum = CF(d, 4);
+  if (!N || !C || !Sz) return true;
+  double* part;
+  BnPieces pc;
+  ProfScope prof("bn_stats", 0, 4.0 * double(N) * C * Sz);
+  if (!bn_reduce("batchnorm_mean_var", 0, d, S(d, 0), Buf{nullptr, 0}, Buf{nullptr, 0},
+                 Buf{nullptr, 0}, 0.f, N, C, Sz, &part, &pc))
+    return false;
+  hipLaunchKernelGGL(k_bn_stats_final, dim3(cdiv(C, 256)), dim3(256), 0, stream(), part,
+                     pc.pieces, C, N * Sz, U(d, 0), U(d, 1), U(d, 2), U(d, 3), training,
+                     momentum);
+  return check_launch("batchnorm_mean_var");
+}
+
+static bool sh_bn_backward_reduce(const Dispatch& d) {
+  uint32_t N = CU(d, 0), C = CU(d, 1), Sz = CU(d, 2);
+  float eps = CF(d, 3);
+  if (!N || !C || !Sz) return true;
+  double* part;
+  BnPieces pc;
+  ProfScope prof("bn_bwd_reduce", 0, 8.0 * double(N) * C * Sz);
+  if (!bn_reduce("batchnorm_backward_reduce", 1, d, S(d, 0), S(d, 1), S(d, 2), S(d, 3), eps, N, C,
+                 Sz, &part, &pc))
+    return false;
+  hipLaunchKernelGGL(k_bn_grad_final, dim3(cdiv(C, 256)), dim3(256), 0, stream(), part,
+                     pc.pieces, C, U(d, 0), U(d, 1));
+  return check_launch("batchnorm_backward_reduce");
+}
+
+// y = (x - mu) * rstd * gamma + beta   (nn_batchnorm_forward.hlsl:24-34)
+// dx = (gamma*rstd) * (dy - (dbeta + xhat*dgamma)/m)   (nn_batchnorm_backward_dx.hlsl:26-38)
+template <int MODE, bool CHECK>
+__global__ void k_bn_elem(Buf x, Buf dy, Buf mean, Buf var, Buf gamma, Buf beta_or_dg, Buf dbeta,
+                          Buf out, float eps, uint32_t C, uint32_t total, FastDiv dS,
+                          FastDiv dC, float m) {
+  const uint32_t i = gtid();
+  if (i >= total) return;
+  const uint32_t q = fdiv(i, dS);
+  const uint32_t c = q - fdiv(q, dC) * C;
+  const float mu = ld(mean, c);
+  const float rstd = 1.0f / sqrtf(ld(var, c) + eps);
+  const float xv = CHECK ? ld(x, i) : x.p[i];
+  const float xh = (xv - mu) * rstd;
+  if (MODE == 0) {
+    const float v = xh * ld(gamma, c) + ld(beta_or_dg, c);
+    if (CHECK) st(out, i, v); else out.p[i] = v;
+  } else {
+    const float g = ld(gamma, c), dg = ld(beta_or_dg, c), db = ld(dbeta, c);
+    const float dyv = CHECK ? ld(dy, i) : dy.p[i];
+    const float v = (g * rstd) * (dyv - (db + xh * dg) / m);
+    if (CHECK) st(out, i, v); else out.p[i] = v;
+  }
+}
+template <int MODE>
+static bool bn_elem(const char* what, const Dispatch& d) {
+  uint32_t N = CU(d, 0), C = CU(d, 1), Sz = CU(d, 2);
+  float eps = CF(d, 3);
+  uint64_t total = uint64_t(N) * C * Sz;
+  if (!total) return true;
+  if (total >= (1ull << 31)) {
+    set_error("%s: tensor too large", what);
+    return false;
+  }
+  Buf x = S(d, 0);
+  Buf dy = MODE == 1 ? S(d, 1) : Buf{nullptr, 0};
+  Buf mean = MODE == 1 ? S(d, 2) : S(d, 1);
+  Buf var = MODE == 1 ? S(d, 3) : S(d, 2);
+  Buf gamma = MODE == 1 ? S(d, 4) : S(d, 3);
+  Buf b2 = MODE == 1 ? S(d, 5) : S(d, 4);
+  Buf db = MODE == 1 ? S(d, 6) : Buf{nullptr, 0};
+  Buf out = U(d, 0);
+  const bool fast = covers(x, total) && covers(out, total) && (MODE == 0 || covers(dy, total));
+  ProfScope prof(MODE == 0 ? "bn_fwd" : "bn_bwd_dx", 0, (MODE == 0 ? 8.0 : 12.0) * double(total));
+  dim3 grid(cdiv(total, 256));
+  if (fast)
+    hipLaunchKernelGGL((k_bn_elem<MODE, false>), grid, dim3(256), 0, stream(), x, dy, mean, var,
+                       gamma, b2, db, out, eps, C, uint32_t(total), make_fastdiv(Sz),
+                       make_fastdiv(C), float(uint64_t(N) * Sz));
+  else
+    hipLaunchKernelGGL((k_bn_elem<MODE, true>), grid, dim3(256), 0, stream(), x, dy, mean, var,
+                       gamma, b2, db, out, eps, C, uint32_t(total), make_fastdiv(Sz),
+                       make_fastdiv(C), float(uint64_t(N) * Sz));
+  return check_launch(what);
+}
+static bool sh_bn_forward(const Dispatch& d) { return bn_elem<0>("batchnorm_forward", d); }
+static bool sh_bn_backward_dx(const Dispatch& d) { return bn_elem<1>("batchnorm_backward_dx", d); }
+
+// ===========================================================================
+// Max pooling
+// ===========================================================================
+__global__ void k_maxpool_fwd(Buf x, Buf out, Buf idx, uint32_t BC, uint32_t H, uint32_t W,
+                              uint32_t k, uint32_t s, uint32_t OH, uint32_t OW) {
+  const uint32_t o = gtid();
+  if (o >= BC * OH * OW) return;
+  const uint32_t ow = o % OW, t = o / OW, oh = t % OH, bc = t / OH;
+  const uint32_t base = bc * H * W;
+  float mx = -1e30f;
+  uint32_t mi = 0xFFFFFFFFu;
+  for (uint32_t ph = 0; ph < k; ++ph) {
+    const uint32_t ih = oh * s + ph;
+    for (uint32_t pw = 0; pw < k; ++pw) {
+      const uint32_t iw = ow * s + pw;
+      if (ih < H && iw < W) {
+        const uint32_t ii = base + ih * W + iw;
+        const float v = ld(x, ii);
+        if (v > mx) {
+          mx = v;
+          mi = ii;
+        }
+      }
+    }
+  }
+  st(out, o, mx);
+  st(idx, o, __uint_as_float(mi));
+}
+
+bool maxpool_forward(const float* x, float* out, float* idx, uint32_t B, uint32_t C, uint32_t H,
+                     uint32_t W, uint32_t k, uint32_t s, uint32_t OH, uint32_t OW) {
+  const uint32_t n = B * C * OH * OW;
+  ProfScope prof("maxpool_fwd", 0, 4.0 * double(B) * C * H * W + 8.0 * n);
+  hipLaunchKernelGGL(k_maxpool_fwd, dim3(cdiv(n, 256)), dim3(256), 0, stream(),
+                     Buf{const_cast<float*>(x), B * C * H * W}, Buf{out, n}, Buf{idx, n}, B * C,
+                     H, W, k, s, OH, OW);
+  return check_launch("maxpool_forward");
+}
+
+// Deterministic gather: every input element sums dZ over the windows that
+// contain it and whose recorded argmax is this element, in (oh, ow) order.
+__global__ void k_maxpool_bwd_gather(const float* __restrict__ dz, const uint32_t* __restrict__ idx,
+                                     float* __restrict__ dx, uint32_t total, uint32_t H, uint32_t W,
+                                     uint32_t k, uint32_t s, uint32_t OH, uint32_t OW,
+                                     FastDiv dW, FastDiv dH) {
+  const uint32_t i = gtid();
+  if (i >= total) return;
+  const uint32_t t = fdiv(i, dW);
+  const uint32_t iw = i - t * W;
+  const uint32_t bc = fdiv(t, dH);
+  const uint32_t ih = t - bc * H;
+  const uint32_t ohlo = (ih + 1 >= k) ? (ih + 1 - k + s - 1) / s : 0;
+  const uint32_t ohhi = min(ih / s, OH - 1);
+  const uint32_t owlo = (iw + 1 >= k) ? (iw + 1 - k + s - 1) / s : 0;
+  const uint32_t owhi = min(iw / s, OW - 1);
+  float acc = 0.f;
+  const uint32_t ob = bc * OH * OW;
+  for (uint32_t oh = ohlo; oh <= ohhi; ++oh)
+    for (uint32_t ow = owlo; ow <= owhi; ++ow) {
+      const uint32_t o = ob + oh * OW + ow;
+      if (idx[o] == i) acc += dz[o];
+    }
+  dx[i] = acc;
+}
+// Fallback when the pooling geometry is unknown: zero + scatter-add.
+__global__ void k_maxpool_bwd_scatter(Buf dz, const uint32_t* idx, Buf dx, uint32_t n) {
+  const uint32_t o = gtid();
+  if (o >= n) return;
+  const uint32_t t = idx[o];
+  if (t != 0xFFFFFFFFu && t < dx.n) atomicAdd(dx.p + t, ld(dz, o));
+}
+
+bool maxpool_backward(const float* dz, const float* idx, float* dx, uint32_t B, uint32_t C,
+                      uint32_t OH, uint32_t OW, uint32_t xcount, uint32_t H, uint32_t W,
+                      uint32_t k, uint32_t s) {
+  const uint32_t n = B * C * OH * OW;
+  ProfScope prof("maxpool_bwd", 0, 8.0 * n + 4.0 * xcount);
+  const uint32_t* ip = reinterpret_cast<const uint32_t*>(idx);
+  if (k && s && H && W) {
+    hipLaunchKernelGGL(k_maxpool_bwd_gather, dim3(cdiv(xcount, 256)), dim3(256), 0, stream(), dz,
+                       ip, dx, xcount, H, W, k, s, OH, OW, make_fastdiv(W), make_fastdiv(H));
+    return check_launch("maxpool_backward");
+  }
+  if (!fill_zero(dx, xcount)) return false;
+  hipLaunchKernelGGL(k_maxpool_bwd_scatter, dim3(cdiv(n, 256)), dim3(256), 0, stream(),
+                     Buf{const_cast<float*>(dz), n}, ip, Buf{dx, xcount}, n);
+  return check_launch("maxpool_backward");
+}
+
+static bool sh_maxpool_forward(const Dispatch& d) {
+  uint32_t B = CU(d, 0), C = CU(d, 1), H = CU(d, 2), W = CU(d, 3), k = CU(d, 4), s = CU(d, 5),
+           OH = CU(d, 6), OW = CU(d, 7);
+  uint64_t n = uint64_t(B) * C * OH * OW;
+  if (!n) return true;
+  hipLaunchKernelGGL(k_maxpool_fwd, dim3(cdiv(n, 256)), dim3(256), 0, stream(), S(d, 0), U(d, 0),
+                     U(d, 1), B * C, H, W, k, s, OH, OW);
+  return check_launch("maxpool_forward");
+}
+// RunShader("maxpool_backward") keeps the reference's store semantics
+// (nn_maxpool_backward.hlsl:21-24): dX[idx] = dZ, the caller clears dX.
+__global__ void k_maxpool_bwd_store(Buf dz, Buf idx, Buf dx, uint32_t n) {
+  const uint32_t o = gtid();
+  if (o >= n) return;
+  const uint32_t t = __float_as_uint(ld(idx, o));
+  if (t != 0xFFFFFFFFu) st(dx, t, ld(dz, o));
+}
+static bool sh_maxpool_backward(const Dispatch& d) {
+  uint64_t n = uint64_t(CU(d, 0)) * CU(d, 1) * CU(d, 2) * CU(d, 3);
+  if (!n) return true;
+  hipLaunchKernelGGL(k_maxpool_bwd_store, dim3(cdiv(n, 256)), dim3(256), 0, stream(), S(d, 0),
+                     S(d, 1), U(d, 0), uint32_t(n));
+  return check_launch("maxpool_backward");
+}
+
+// ===========================================================================
+// Global average pooling, nearest upsampling, channel concat / slice
+// ===========================================================================
+__global__ void k_gap(Buf in, Buf out, uint32_t S) {
+  __shared__ double sh[4];
+  const uint32_t nc = blockIdx.x;
+  float s = 0.f;
+  for (uint32_t i = threadIdx.x; i < S; i += 256) s += ld(in, nc * S + i);
+  const double t = block_sum256(s, sh);
+  if (threadIdx.x == 0) st(out, nc, float(t) / float(S));
+}
+static bool sh_gap(const Dispatch& d) {
+  uint32_t BC = CU(d, 0) * CU(d, 1), Sz = CU(d, 2);
+  if (!BC || !Sz) return true;
+  hipLaunchKernelGGL(k_gap, dim3(BC), dim3(256), 0, stream(), S(d, 0), U(d, 0), Sz);
+  return check_launch("global_avg_pool");
+}
+__global__ void k_gap_bwd(Buf g, Buf dx, uint32_t total, uint32_t S) {
+  const uint32_t i = gtid();
+  if (i < total) st(dx, i, ld(g, i / S) / float(S));
+}
+static bool sh_gap_bwd(const Dispatch& d) {
+  uint32_t Sz = CU(d, 2);
+  uint64_t total = uint64_t(CU(d, 0)) * CU(d, 1) * Sz;
+  if (!total) return true;
+  ProfScope prof("gap_bwd", 0, 4.0 * double(total));
+  hipLaunchKernelGGL(k_gap_bwd, dim3(cdiv(total, 256)), dim3(256), 0, stream(), S(d, 0), U(d, 0),
+                     uint32_t(total), Sz);
+  return check_launch("global_avg_pool_backward");
+}
+
+__global__ void k_upsample(Buf X, Buf O, uint32_t total, uint32_t C, uint32_t H, uint32_t W,
+                           uint32_t OH, uint32_t OW, uint32_t sH, uint32_t sW) {
+  const uint32_t i = gtid();
+  if (i >= total) return;
+  const uint32_t wo = i % OW, t = i / OW, ho = t % OH, bc = t / OH;
+  st(O, i, ld(X, (bc * H + ho / sH) * W + wo / sW));
+}
+__global__ void k_upsample_bwd(Buf DY, Buf DX, uint32_t total, uint32_t H, uint32_t W,
+                               uint32_t OH, uint32_t OW, uint32_t sH, uint32_t sW) {
+  const uint32_t i = gtid();
+  if (i >= total) return;
+  const uint32_t wi = i % W, t = i / W, hi = t % H, bc = t / H;
+  float s = 0.f;
+  for (uint32_t a = 0; a < sH; ++a) {
+    const uint32_t ho = hi * sH + a;
+    for (uint32_t b = 0; b < sW; ++b) {
+      const uint32_t wo = wi * sW + b;
+      if (ho < OH && wo < OW) s += ld(DY, (bc * OH + ho) * OW + wo);
+    }
+  }
+  st(DX, i, s);
+}
+static bool sh_upsample(const Dispatch& d) {
+  uint32_t B = CU(d, 0), C = CU(d, 1), H = CU(d, 2), W = CU(d, 3), OH = CU(d, 4), OW = CU(d, 5),
+           sH = CU(d, 6), sW = CU(d, 7);
+  uint64_t total = uint64_t(B) * C * OH * OW;
+  if (!total || !sH || !sW) return true;
+  hipLaunchKernelGGL(k_upsample, dim3(cdiv(total, 256)), dim3(256), 0, stream(), S(d, 0),
+                     U(d, 0), uint32_t(total), C, H, W, OH, OW, sH, sW);
+  return check_launch("upsample");
+}
+static bool sh_upsample_bwd(const Dispatch& d) {
+  uint32_t B = CU(d, 0), C = CU(d, 1), H = CU(d, 2), W = CU(d, 3), OH = CU(d, 4), OW = CU(d, 5),
+           sH = CU(d, 6), sW = CU(d, 7);
+  uint64_t total = uint64_t(B) * C * H * W;
+  if (!total) return true;
+  ProfScope prof("upsample_bwd", 0, 4.0 * double(total) + 4.0 * double(B) * C * OH * OW);
+  hipLaunchKernelGGL(k_upsample_bwd, dim3(cdiv(total, 256)), dim3(256), 0, stream(), S(d, 0),
+                     U(d, 0), uint32_t(total), H, W, OH, OW, sH, sW);
+  return check_launch("upsample_backward");
+}
+
+// MODE 0: concat_insert (Out[b, c+off, s] = X[b, c, s]); MODE 1: slice (DX[b, c, s] = DY[b, c+off, s])
+template <int MODE>
+__global__ void k_chan_copy(Buf src, Buf dst, uint32_t total, uint32_t cin, uint32_t S,
+                            uint32_t cout, uint32_t coff) {
+  const uint32_t i = gtid();
+  if (i >= total) return;
+  const uint32_t s = i % S, t = i / S, c = t % cin, b = t / cin;
+  const uint32_t o = (b * cout + c + coff) * S + s;
+  if (MODE == 0)
+    st(dst, o, ld(src, i));
+  else
+    st(dst, i, ld(src, o));
+}
+template <int MODE>
+static bool sh_chan_copy(const Dispatch& d) {
+  uint32_t B = CU(d, 0), cin = CU(d, 1), Sz = CU(d, 2), cout = CU(d, 3), coff = CU(d, 4);
+  uint64_t total = uint64_t(B) * cin * Sz;
+  if (!total) return true;
+  hipLaunchKernelGGL(k_chan_copy<MODE>, dim3(cdiv(total, 256)), dim3(256), 0, stream(), S(d, 0),
+                     U(d, 0), uint32_t(total), cin, Sz, cout, coff);
+  return check_launch(MODE == 0 ? "concat_insert" : "slice");
+}
+
+// ===========================================================================
+// Depthwise convolution (filters (C,1,kH,kW), bias (C))
+// ===========================================================================
+struct DwGeom {
+  uint32_t B, C, H, W, kH, kW, s, p, OH, OW;
+};
+static DwGeom dw_geom(const Dispatch& d) {
+  DwGeom g{CU(d, 0), CU(d, 1), CU(d, 2), CU(d, 3), CU(d, 4), CU(d, 5), CU(d, 6), CU(d, 7), CU(d, 8), 0};
+  // nn_depthwise_conv_*.hlsl recompute OW from the other constants.
+  g.OW = (g.s && g.W + 2 * g.p >= g.kW) ? (g.W + 2 * g.p - g.kW) / g.s + 1 : 0;
+  return g;
+}
+__global__ void k_dw_fwd(Buf x, Buf f, Buf bias, Buf y, DwGeom g, uint32_t total) {
+  const uint32_t i = gtid();
+  if (i >= total) return;
+  const uint32_t ow = i % g.OW, t = i / g.OW, oh = t % g.OH, t2 = t / g.OH, c = t2 % g.C;
+  const uint32_t n = t2 / g.C;
+  const uint32_t xb = (n * g.C + c) * g.H * g.W, fb = c * g.kH * g.kW;
+  float s = 0.f;
+  for (uint32_t fh = 0; fh < g.kH; ++fh) {
+    const int ih = int(oh * g.s + fh) - int(g.p);
+    if (ih < 0 || ih >= int(g.H)) continue;
+    for (uint32_t fw = 0; fw < g.kW; ++fw) {
+      const int iw = int(ow * g.s + fw) - int(g.p);
+      if (iw < 0 || iw >= int(g.W)) continue;
+      s += ld(x, xb + uint32_t(ih) * g.W + uint32_t(iw)) * ld(f, fb + fh * g.kW + fw);
+    }
+  }
+  st(y, i, s + ld(bias, c));
+}
+__global__ void k_dw_bwd_input(Buf dy, Buf f, Buf dx, DwGeom g, uint32_t total) {
+  const uint32_t i = gtid();
+  if (i >= total) return;
+  const uint32_t iw = i % g.W, t = i / g.W, ih = t % g.H, t2 = t / g.H, c = t2 % g.C;
+  const uint32_t n = t2 / g.C;
+  const uint32_t gb = (n * g.C + c) * g.OH * g.OW, fb = c * g.kH * g.kW;
+  float s = 0.f;
+  for (uint32_t fh = 0; fh < g.kH; ++fh) {
+    const int ohs = int(ih) - int(fh) + int(g.p);
+    if (ohs < 0 || ohs % int(g.s) != 0) continue;
+    const uint32_t oh = uint32_t(ohs) / g.s;
+    if (oh >= g.OH) continue;
+    for (uint32_t fw = 0; fw < g.kW; ++fw) {
+      const int ows = int(iw) - int(fw) + int(g.p);
+      if (ows < 0 || ows % int(g.s) != 0) continue;
+      const uint32_t ow = uint32_t(ows) / g.s;
+      if (ow >= g.OW) continue;
+      s += ld(dy, gb + oh * g.OW + ow) * ld(f, fb + fh * g.kW + fw);
+    }
+  }
+  st(dx, i, s);
+}
+// One pass over dy per (channel, piece): every thread keeps all kH*kW+1
+// running sums (df taps and db) for the outputs it visits.
+constexpr int kDwMaxTaps = 25;
+__global__ void k_dw_bwd_filter_part(Buf dy, Buf x, DwGeom g, uint32_t pieces, double* part) {
+  __shared__ double sh[4];
+  const uint32_t c = blockIdx.y, pc = blockIdx.x;
+  const uint32_t taps = g.kH * g.kW;
+  const uint32_t len = g.B * g.OH * g.OW;
+  const uint32_t i0 = uint32_t((uint64_t(len) * pc) / pieces);
+  const uint32_t i1 = uint32_t((uint64_t(len) * (pc + 1)) / pieces);
+  float acc[kDwMaxTaps + 1];
+#pragma unroll
+  for (int t = 0; t <= kDwMaxTaps; ++t) acc[t] = 0.f;
+  const uint32_t ohw = g.OH * g.OW;
+  for (uint32_t i = i0 + threadIdx.x; i < i1; i += 256) {
+    const uint32_t n = i / ohw, r = i - n * ohw, oh = r / g.OW, ow = r - oh * g.OW;
+    const float gv = ld(dy, (n * g.C + c) * ohw + r);
+    acc[kDwMaxTaps] += gv;
+    const uint32_t xb = (n * g.C + c) * g.H * g.W;
+#pragma unroll
+    for (int t = 0; t < kDwMaxTaps; ++t) {
+      if (uint32_t(t) < taps) {
+        const uint32_t fh = uint32_t(t) / g.kW, fw = uint32_t(t) - fh * g.kW;
+        const int ih = int(oh * g.s + fh) - int(g.p);
+        const int iw = int(ow * g.s + fw) - int(g.p);
+        float xv = 0.f;
+        if (ih >= 0 && ih < int(g.H) && iw >= 0 && iw < int(g.W))
+          xv = ld(x, xb + uint32_t(ih) * g.W + uint32_t(iw));
+        acc[t] += gv * xv;
+      }
+    }
+  }
+  // Static indices keep acc[] in registers; the condition is block-uniform.
+#pragma unroll
+  for (int t = 0; t <= kDwMaxTaps; ++t) {
+    if (uint32_t(t) < taps || t == kDwMaxTaps) {
+      const double s = block_sum256(acc[t], sh);
+      const uint32_t slot = (t == kDwMaxTaps) ? taps : uint32_t(t);
+      if (threadIdx.x == 0) part[(size_t(c) * pieces + pc) * (taps + 1) + slot] = s;
+    }
+  }
+}
+__global__ void k_dw_bwd_filter_final(const double* part, uint32_t pieces, uint32_t C,
+                                      uint32_t taps, Buf df, Buf db) {
+  const uint32_t i = gtid();
+  if (i >= C * (taps + 1)) return;
+  const uint32_t c = i / (taps + 1), t = i - c * (taps + 1);
+  double s = 0;
+  for (uint32_t p = 0; p < pieces; ++p) s += part[(size_t(c) * pieces + p) * (taps + 1) + t];
+  if (t == taps)
+    st(db, c, float(s));
+  else
+    st(df, c * taps + t, float(s));
+}
+static bool dw_ok(const DwGeom& g, const char* what) {
+  if (!g.B || !g.C || !g.H || !g.W || !g.kH || !g.kW || !g.s || !g.OH || !g.OW) return false;
+  if (uint64_t(g.B) * g.C * std::max(g.H * g.W, g.OH * g.OW) >= (1ull << 31)) {
+    set_error("%s: tensor too large", what);
+    return false;
+  }
+  return true;
+}
+static bool sh_dw_fwd(const Dispatch& d) {
+  DwGeom g = dw_geom(d);
+  if (!dw_ok(g, "depthwise_conv_forward")) return true;
+  uint32_t total = g.B * g.C * g.OH * g.OW;
+  hipLaunchKernelGGL(k_dw_fwd, dim3(cdiv(total, 256)), dim3(256), 0, stream(), S(d, 0), S(d, 1),
+                     S(d, 2), U(d, 0), g, total);
+  return check_launch("depthwise_conv_forward");
+}
+static bool sh_dw_bwd_input(const Dispatch& d) {
+  DwGeom g = dw_geom(d);
+  if (!dw_ok(g, "depthwise_conv_backward_input")) return true;
+  uint32_t total = g.B * g.C * g.H * g.W;
+  ProfScope prof("dw_bwd_input", 2.0 * g.kH * g.kW * double(g.B) * g.C * g.OH * g.OW,
+                 4.0 * double(total) + 4.0 * double(g.B) * g.C * g.OH * g.OW);
+  hipLaunchKernelGGL(k_dw_bwd_input, dim3(cdiv(total, 256)), dim3(256), 0, stream(), S(d, 0),
+                     S(d, 1), U(d, 0), g, total);
+  return check_launch("depthwise_conv_backward_input");
+}
+static bool sh_dw_bwd_filter(const Dispatch& d) {
+  DwGeom g = dw_geom(d);
+  if (!dw_ok(g, "depthwise_conv_backward_filter")) return true;
+  const uint32_t taps = g.kH * g.kW;
+  if (taps > uint32_t(kDwMaxTaps)) {
+    set_error("depthwise_conv_backward_filter: kernels above 5x5 are not supported");
+    return false;
+  }
+  const uint32_t len = g.B * g.OH * g.OW;
+  const uint32_t pieces = std::max<uint32_t>(1, std::min<uint32_t>(cdiv(len, 8192), 128));
+  double* part = reinterpret_cast<double*>(workspace(size_t(g.C) * pieces * (taps + 1) * 2));
+  if (!part) return false;
+  ProfScope prof("dw_bwd_filter", 2.0 * taps * double(len) * g.C,
+                 4.0 * double(len) * g.C + 4.0 * double(g.B) * g.C * g.H * g.W);
+  hipLaunchKernelGGL(k_dw_bwd_filter_part, dim3(pieces, g.C), dim3(256), 0, stream(), S(d, 0),
+                     S(d, 1), g, pieces, part);
+  hipLaunchKernelGGL(k_dw_bwd_filter_final, dim3(cdiv(g.C * (taps + 1), 256)), dim3(256), 0,
+                     stream(), part, pieces, g.C, taps, U(d, 0), U(d, 1));
+  return check_launch("depthwise_conv_backward_filter");
+}
+
+// ===========================================================================
+// im2col / col2im / conv reshapes (RunShader compatibility; the fused conv
+// path never materialises these).
+// ===========================================================================
+struct ColGeom {
+  uint32_t B, C, H, W, k, s, p, OH, OW;
+};
+static ColGeom col_geom(const Dispatch& d) {
+  return ColGeom{CU(d, 0), CU(d, 1), CU(d, 2), CU(d, 3), CU(d, 4), CU(d, 5), CU(d, 6), CU(d, 7), CU(d, 8)};
+}
+__global__ void k_im2col(Buf x, Buf col, ColGeom g, uint32_t total) {
+  const uint32_t i = gtid();
+  if (i >= total) return;
+  const uint32_t tc = g.B * g.OH * g.OW;
+  const uint32_t row = i / tc, cl = i - row * tc;
+  const uint32_t b = cl / (g.OH * g.OW), pix = cl - b * g.OH * g.OW, oh = pix / g.OW,
+                 ow = pix - oh * g.OW;
+  const uint32_t ic = row / (g.k * g.k), kk = row - ic * g.k * g.k, kh = kk / g.k, kw = kk - kh * g.k;
+  const int ih = int(oh * g.s + kh) - int(g.p), iw = int(ow * g.s + kw) - int(g.p);
+  float v = 0.f;
+  if (ih >= 0 && ih < int(g.H) && iw >= 0 && iw < int(g.W))
+    v = ld(x, ((b * g.C + ic) * g.H + uint32_t(ih)) * g.W + uint32_t(iw));
+  st(col, i, v);
+}
+__global__ void k_col2im(Buf col, Buf dx, ColGeom g, uint32_t total) {
+  const uint32_t i = gtid();
+  if (i >= total) return;
+  const uint32_t iw = i % g.W, t = i / g.W, ih = t % g.H, t2 = t / g.H, ic = t2 % g.C, b = t2 / g.C;
+  const uint32_t tc = g.B * g.OH * g.OW;
+  float s = 0.f;
+  for (uint32_t kh = 0; kh < g.k; ++kh)
+    for (uint32_t kw = 0; kw < g.k; ++kw) {
+      const int ohs = int(ih) - int(kh) + int(g.p), ows = int(iw) - int(kw) + int(g.p);
+      if (ohs % int(g.s) == 0 && ows % int(g.s) == 0) {
+        const uint32_t oh = uint32_t(ohs / int(g.s)), ow = uint32_t(ows / int(g.s));
+        if (oh < g.OH && ow < g.OW)
+          s += ld(col, (ic * g.k * g.k + kh * g.k + kw) * tc + b * g.OH * g.OW + oh * g.OW + ow);
+      }
+    }
+  st(dx, i, s);
+}
+static bool sh_im2col(const Dispatch& d) {
+  ColGeom g = col_geom(d);
+  uint64_t total = uint64_t(g.C) * g.k * g.k * g.B * g.OH * g.OW;
+  if (!total || !g.s || total >= (1ull << 32)) return true;
+  hipLaunchKernelGGL(k_im2col, dim3(cdiv(total, 256)), dim3(256), 0, stream(), S(d, 0), U(d, 0), g,
+                     uint32_t(total));
+  return check_launch("im2col");
+}
+static bool sh_col2im(const Dispatch& d) {
+  ColGeom g = col_geom(d);
+  uint64_t total = uint64_t(g.B) * g.C * g.H * g.W;
+  if (!total || !g.s || total >= (1ull << 32)) return true;
+  hipLaunchKernelGGL(k_col2im, dim3(cdiv(total, 256)), dim3(256), 0, stream(), S(d, 0), U(d, 0), g,
+                     uint32_t(total));
+  return check_launch("col2im");
+}
+// conv_reshape: y[b, oc, pix] = act(mm[oc, b*OHW + pix] + bias[oc])
+__global__ void k_conv_reshape(Buf mm, Buf bias, Buf y, uint32_t B, uint32_t OC, uint32_t OHW,
+                               uint32_t act) {
+  const uint32_t i = gtid();
+  if (i >= B * OC * OHW) return;
+  const uint32_t pix = i % OHW, t = i / OHW, oc = t % OC, b = t / OC;
+  float z = ld(mm, oc * B * OHW + b * OHW + pix) + ld(bias, oc);
+  if (act == 1) z = fmaxf(0.f, z);
+  else if (act == 2) z = tanhf(z);
+  st(y, i, z);
+}
+static bool sh_conv_reshape(const Dispatch& d) {
+  uint32_t B = CU(d, 0), OC = CU(d, 1), OHW = CU(d, 2) * CU(d, 3);
+  uint64_t n = uint64_t(B) * OC * OHW;
+  if (!n) return true;
+  hipLaunchKernelGGL(k_conv_reshape, dim3(cdiv(n, 256)), dim3(256), 0, stream(), S(d, 0), S(d, 1),
+                     U(d, 0), B, OC, OHW, CU(d, 4));
+  return check_launch("conv_reshape");
+}
+// conv_grad_reshape(_relu): G[oc, b*OHW + pix] = dZ[b, oc, pix] (masked where y <= 0)
+template <bool RELU>
+__global__ void k_conv_grad_reshape(Buf dz, Buf y, Buf g, uint32_t B, uint32_t OC, uint32_t OHW) {
+  const uint32_t i = gtid();
+  if (i >= B * OC * OHW) return;
+  const uint32_t pix = i % OHW, t = i / OHW, oc = t % OC, b = t / OC;
+  float v = ld(dz, i);
+  if (RELU && ld(y, i) <= 0.f) v = 0.f;
+  st(g, oc * B * OHW + b * OHW + pix, v);
+}
+template <bool RELU>
+static bool sh_conv_grad_reshape(const Dispatch& d) {
+  uint32_t B = CU(d, 0), OC = CU(d, 4), OHW = CU(d, 7) * CU(d, 8);
+  uint64_t n = uint64_t(B) * OC * OHW;
+  if (!n) return true;
+  hipLaunchKernelGGL(k_conv_grad_reshape<RELU>, dim3(cdiv(n, 256)), dim3(256), 0, stream(),
+                     S(d, 0), RELU ? S(d, 1) : Buf{nullptr, 0}, U(d, 0), B, OC, OHW);
+  return check_launch("conv_grad_reshape");
+}
+
+// ===========================================================================
+// Flagged GEMM shaders (matmul_universal / heavy / dgpu / coarsened / reduce):
+// C = op(A)·op(B), constants {M, K, N, flags}.  Routed to the MFMA GEMM when
+// every buffer covers the shape; otherwise a bounds-checked reference loop.
+// ===========================================================================
+__global__ void k_gemm_checked(Buf A, Buf B, Buf C, uint32_t M, uint32_t K, uint32_t N,
+                               uint32_t flags) {
+  const uint32_t i = gtid();
+  if (i >= M * N) return;
+  const uint32_t m = i / N, n = i - m * N;
+  float s = 0.f;
+  for (uint32_t k = 0; k < K; ++k) {
+    const float a = ld(A, (flags & 1) ? k * M + m : m * K + k);
+    const float b = ld(B, (flags & 2) ? n * K + k : k * N + n);
+    s += a * b;
+  }
+  st(C, i, s);
+}
+static bool sh_matmul(const Dispatch& d) {
+  uint32_t M = CU(d, 0), K = CU(d, 1), N = CU(d, 2), flags = CU(d, 3) & 3u;
+  uint64_t mn = uint64_t(M) * N;
+  if (!mn) return true;
+  Buf A = S(d, 0), B = S(d, 1), C = U(d, 0);
+  if (covers(A, uint64_t(M) * K) && covers(B, uint64_t(K) * N) && covers(C, mn))
+    return gemm(A.p, B.p, C.p, M, K, N, flags);
+  if (mn >= (1ull << 32)) return false;
+  hipLaunchKernelGGL(k_gemm_checked, dim3(cdiv(mn, 256)), dim3(256), 0, stream(), A, B, C, M, K, N,
+                     flags);
+  return check_launch("matmul");
+}
+
+// ===========================================================================
+// Optimiser shaders (single tensor, RunShader form)
+// ===========================================================================
+__global__ void k_sgd(Buf w, Buf g, uint32_t n, float lr, float clip) {
+  const uint32_t i = gtid();
+  if (i >= n) return;
+  float gv = ld(g, i);
+  if (gv > clip) gv = clip;
+  if (gv < -clip) gv = -clip;
+  st(w, i, ld(w, i) - lr * gv);
+}
+static bool sh_sgd(const Dispatch& d) {  // cb {count, lr, clip, pad}; u0 = weight, t0 = grad
+  uint32_t n = CU(d, 0);
+  if (!n) return true;
+  hipLaunchKernelGGL(k_sgd, dim3(cdiv(n, 256)), dim3(256), 0, stream(), U(d, 0), S(d, 0), n,
+                     CF(d, 1), CF(d, 2));
+  return check_launch("sgd");
+}
+__global__ void k_sgd_clipped(Buf w, Buf g, Buf ns, uint32_t n, float lr) {
+  const uint32_t i = gtid();
+  if (i < n) st(w, i, ld(w, i) - lr * ld(g, i) * ld(ns, 1));
+}
+static bool sh_sgd_clipped(const Dispatch& d) {
+  uint32_t n = CU(d, 0);
+  if (!n) return true;
+  hipLaunchKernelGGL(k_sgd_clipped, dim3(cdiv(n, 256)), dim3(256), 0, stream(), U(d, 0), S(d, 0),
+                     S(d, 1), n, CF(d, 1));
+  return check_launch("sgd_clipped");
+}
+// One partial Σg² per 256-element group at globalOffset + group.
+__global__ void k_grad_sq_reduce(Buf g, Buf part, uint32_t n, uint32_t off) {
+  __shared__ double sh[4];
+  const uint32_t i = gtid();
+  const float v = i < n ? ld(g, i) : 0.f;
+  const double s = block_sum256(double(v * v), sh);
+  if (threadIdx.x == 0) st(part, off + blockIdx.x, float(s));
+}
+static bool sh_grad_sq_reduce(const Dispatch& d) {
+  uint32_t n = CU(d, 0);
+  if (!n) return true;
+  hipLaunchKernelGGL(k_grad_sq_reduce, dim3(cdiv(n, 256)), dim3(256), 0, stream(), S(d, 0), U(d, 0),
+                     n, CU(d, 1));
+  return check_launch("grad_sq_reduce");
+}
+__global__ void k_grad_norm_final(Buf part, Buf ns, uint32_t total, float maxNorm) {
+  __shared__ double sh[4];
+  double s = 0;
+  for (uint32_t i = threadIdx.x; i < total; i += 256) s += ld(part, i);
+  s = block_sum256(s, sh);
+  if (threadIdx.x == 0) {
+    const float norm = sqrtf(float(s));
+    st(ns, 0, norm);
+    st(ns, 1, (norm > maxNorm) ? (maxNorm / (norm + 1e-6f)) : 1.0f);
+  }
+}
+static bool sh_grad_norm_final(const Dispatch& d) {
+  hipLaunchKernelGGL(k_grad_norm_final, dim3(1), dim3(256), 0, stream(), S(d, 0), U(d, 0),
+                     CU(d, 0), CF(d, 1));
+  return check_launch("grad_norm_final");
+}
+__global__ void k_adam(Buf w, Buf m, Buf v, Buf g, uint32_t n, float step, float b1, float b2,
+                       float eps, float wd, float clip) {
+  const uint32_t i = gtid();
+  if (i >= n) return;
+  float gv = ld(g, i);
+  if (gv > clip) gv = clip;
+  if (gv < -clip) gv = -clip;
+  const float cw = ld(w, i);
+  const float mt = b1 * ld(m, i) + (1.0f - b1) * gv;
+  const float vt = b2 * ld(v, i) + (1.0f - b2) * gv * gv;
+  st(m, i, mt);
+  st(v, i, vt);
+  st(w, i, cw - wd * cw - step * mt / (sqrtf(vt) + eps));
+}
+static bool sh_adam(const Dispatch& d) {  // u0 weight, u1 m, u2 v, t0 grad
+  uint32_t n = CU(d, 0);
+  if (!n) return true;
+  hipLaunchKernelGGL(k_adam, dim3(cdiv(n, 256)), dim3(256), 0, stream(), U(d, 0), U(d, 1), U(d, 2),
+                     S(d, 0), n, CF(d, 1), CF(d, 2), CF(d, 3), CF(d, 4), CF(d, 5), CF(d, 6));
+  return check_launch("adam");
+}
+// rms: out[0] = sqrt(Σ A² / count) (nn_rms.hlsl)
+__global__ void k_rms(Buf A, Buf out, uint32_t n) {
+  __shared__ double sh[4];
+  double s = 0;
+  for (uint32_t i = threadIdx.x; i < n; i += 256) {
+    const float v = ld(A, i);
+    s += double(v * v);
+  }
+  s = block_sum256(s, sh);
+  if (threadIdx.x == 0) st(out, 0, sqrtf(float(s) / float(n)));
+}
+static bool sh_rms(const Dispatch& d) {
+  uint32_t n = CU(d, 0);
+  if (!n) return true;
+  hipLaunchKernelGGL(k_rms, dim3(1), dim3(256), 0, stream(), S(d, 0), U(d, 0), n);
+  return check_launch("rms");
+}
+
+// ===========================================================================
+// Registry (names of nn_engine.py:147-173 that have kernel sources)
+// ===========================================================================
+static const ShaderEntry kShaders[] = {
+    {"matmul_universal", sh_matmul},
+    {"matmul_coarsened", sh_matmul},
+    {"matmul_heavy", sh_matmul},
+    {"matmul_dgpu", sh_matmul},
+    {"matmul_reduce", sh_matmul},
+    {"add_bias", sh_add_bias_t<false>},
+    {"bias_relu", sh_add_bias_t<true>},
+    {"relu", sh_relu},
+    {"relu_grad", sh_relu_grad},
+    {"relu6", sh_relu6},
+    {"relu6_grad", sh_relu6_grad},
+    {"sigmoid", sh_sigmoid},
+    {"sigmoid_grad", sh_sigmoid_grad},
+    {"leaky_relu", sh_leaky},
+    {"leaky_relu_grad", sh_leaky_grad},
+    {"add", sh_add},
+    {"scale_add", sh_scale_add},
+    {"rms", sh_rms},
+    {"grad_accum", sh_grad_accum},
+    {"bias_grad", sh_bias_grad},
+    {"softmax", sh_softmax},
+    {"loss", sh_loss},
+    {"softmax_ce_grad", sh_softmax_ce_grad},
+    {"argmax_correct", sh_argmax_correct},
+    {"accumulate_scalar", sh_accumulate_scalar},
+    {"dice_loss", sh_dice_loss},
+    {"dice_loss_sums", sh_dice_sums},
+    {"dice_loss_grad", sh_dice_grad},
+    {"batchnorm_mean_var", sh_bn_mean_var},
+    {"batchnorm_forward", sh_bn_forward},
+    {"batchnorm_backward_reduce", sh_bn_backward_reduce},
+    {"batchnorm_backward_dx", sh_bn_backward_dx},
+    {"maxpool_forward", sh_maxpool_forward},
+    {"maxpool_backward", sh_maxpool_backward},
+    {"global_avg_pool", sh_gap},
+    {"global_avg_pool_backward", sh_gap_bwd},
+    {"upsample", sh_upsample},
+    {"upsample_backward", sh_upsample_bwd},
+    {"concat_insert", sh_chan_copy<0>},
+    {"slice", sh_chan_copy<1>},
+    {"depthwise_conv_forward", sh_dw_fwd},
+    {"depthwise_conv_backward_input", sh_dw_bwd_input},
+    {"depthwise_conv_backward_filter", sh_dw_bwd_filter},
+    {"im2col", sh_im2col},
+    {"col2im", sh_col2im},
+    {"conv_reshape", sh_conv_reshape},
+    {"conv_grad_reshape", sh_conv_grad_reshape<false>},
+    {"conv_grad_reshape_relu", sh_conv_grad_reshape<true>},
+    {"sgd", sh_sgd},
+    {"sgd_clipped", sh_sgd_clipped},
+    {"grad_sq_reduce", sh_grad_sq_reduce},
+    {"grad_norm_final", sh_grad_norm_final},
+    {"adam", sh_adam},
+};
+
+const ShaderEntry* find_shader(const char* name) {
+  for (const ShaderEntry& e : kShaders)
+    if (strcmp(e.name, name) == 0) return &e;
+  return nullptr;
+}
+
+}  // namespace dce

@@ -1,0 +1,301 @@
+// Multi-tensor optimiser kernels: one launch updates up to kMaxT tensors.
+//
+// The reference dispatches one shader per parameter tensor (SGDBatch loops
+// over `sgd` dispatches, engine.cpp:436-485; AdamW.step loops over `adam`
+// dispatches from Python, nn_engine.py:2217-2238; SGDBatchClipped runs
+// grad_sq_reduce per tensor, grad_norm_final, then sgd_clipped per tensor,
+// engine.cpp:494-614).  Here a table of tensor pointers travels as a kernel
+// argument and each 256-thread block owns a 4096-element chunk of one tensor;
+// float4 traffic, per-element arithmetic identical to the HLSL.
+#include "dce_internal.h"
+
+#include <algorithm>
+#include <vector>
+
+namespace dce {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+constexpr int kMaxT = 48;
+constexpr uint32_t kChunk = 4096;  // elements per block (256 threads x 16)
+
+struct Table {
+  float* w[kMaxT];
+  float* g[kMaxT];
+  float* m[kMaxT];
+  float* v[kMaxT];
+  uint32_t n[kMaxT];
+  uint32_t start[kMaxT + 1];  // first block of each tensor
+  uint32_t count;
+};
+
+static inline uint32_t cdiv(uint64_t a, uint64_t b) { return uint32_t((a + b - 1) / b); }
+
+__device__ __forceinline__ int find_tensor(const Table& t, uint32_t blk) {
+  int lo = 0, hi = int(t.count) - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (t.start[mid] <= blk) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+struct SgdOp {  // nn_sgd.hlsl:7-10
+  float lr, clip;
+  __device__ void operator()(float& w, float& g, float&, float&) const {
+    float gv = g;
+    if (gv > clip) gv = clip;
+    if (gv < -clip) gv = -clip;
+    w = w - lr * gv;
+  }
+};
+struct SgdScaledOp {  // nn_sgd_clipped.hlsl:18-19
+  float lr, scale;
+  __device__ void operator()(float& w, float& g, float&, float&) const { w -= lr * g * scale; }
+};
+struct ScaleOp {
+  float scale;
+  __device__ void operator()(float&, float& g, float&, float&) const { g = g * scale; }
+};
+struct AdamOp {  // nn_adam.hlsl:20-33
+  float step, b1, b2, eps, wd, clip;
+  __device__ void operator()(float& w, float& g, float& m, float& v) const {
+    float gv = g;
+    if (gv > clip) gv = clip;
+    if (gv < -clip) gv = -clip;
+    const float cw = w;
+    const float mt = b1 * m + (1.0f - b1) * gv;
+    const float vt = b2 * v + (1.0f - b2) * gv * gv;
+    m = mt;
+    v = vt;
+    w = cw - wd * cw - step * mt / (sqrtf(vt) + eps);
+  }
+};
+
+// WRITE: bit0 w, bit1 g, bit2 m, bit3 v.  READ likewise.
+template <class Op, int READ, int WRITE>
+__device__ __forceinline__ void apply_chunk(const Table& t, const Op& op, int ti, uint32_t c0) {
+  const uint32_t n = t.n[ti];
+  float* w = t.w[ti];
+  float* g = t.g[ti];
+  float* m = t.m[ti];
+  float* v = t.v[ti];
+  const uint32_t end = min(n, c0 + kChunk);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t i = c0 + (j * 256 + threadIdx.x) * 4;
+    if (i + 3 < end) {
+      f4 W = {0, 0, 0, 0}, G = W, M = W, V = W;
+      if (READ & 1) W = *reinterpret_cast<const f4*>(w + i);
+      if (READ & 2) G = *reinterpret_cast<const f4*>(g + i);
+      if (READ & 4) M = *reinterpret_cast<const f4*>(m + i);
+      if (READ & 8) V = *reinterpret_cast<const f4*>(v + i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float a = W[e], b = G[e], c = M[e], d = V[e];
+        op(a, b, c, d);
+        W[e] = a; G[e] = b; M[e] = c; V[e] = d;
+      }
+      if (WRITE & 1) *reinterpret_cast<f4*>(w + i) = W;
+      if (WRITE & 2) *reinterpret_cast<f4*>(g + i) = G;
+      if (WRITE & 4) *reinterpret_cast<f4*>(m + i) = M;
+      if (WRITE & 8) *reinterpret_cast<f4*>(v + i) = V;
+    } else {
+      for (uint32_t k = i; k < end && k < i + 4; ++k) {
+        float a = (READ & 1) ? w[k] : 0.f, b = (READ & 2) ? g[k] : 0.f;
+        float c = (READ & 4) ? m[k] : 0.f, d = (READ & 8) ? v[k] : 0.f;
+        op(a, b, c, d);
+        if (WRITE & 1) w[k] = a;
+        if (WRITE & 2) g[k] = b;
+        if (WRITE & 4) m[k] = c;
+        if (WRITE & 8) v[k] = d;
+      }
+    }
+  }
+}
+
+template <class Op, int READ, int WRITE>
+__global__ void __launch_bounds__(256) k_multi(const Table t, const Op op) {
+  const int ti = find_tensor(t, blockIdx.x);
+  apply_chunk<Op, READ, WRITE>(t, op, ti, (blockIdx.x - t.start[ti]) * kChunk);
+}
+
+// Scale read from device memory (norm clip): skipped entirely when 1.
+template <class Op, int READ, int WRITE>
+__global__ void __launch_bounds__(256) k_multi_devscale(const Table t, Op op, const float* ns) {
+  const float scale = ns[1];
+  if (Op::kSkipUnit && scale == 1.0f) return;
+  op.scale = scale;
+  const int ti = find_tensor(t, blockIdx.x);
+  apply_chunk<Op, READ, WRITE>(t, op, ti, (blockIdx.x - t.start[ti]) * kChunk);
+}
+struct SgdScaledDev : SgdScaledOp {
+  static constexpr bool kSkipUnit = false;
+};
+struct ScaleDev : ScaleOp {
+  static constexpr bool kSkipUnit = true;
+};
+
+// Σ g² per block (double), written at part[base + block].
+__global__ void __launch_bounds__(256) k_multi_sumsq(const Table t, double* part, uint32_t base) {
+  __shared__ double sh[4];
+  const int ti = find_tensor(t, blockIdx.x);
+  const uint32_t c0 = (blockIdx.x - t.start[ti]) * kChunk;
+  const uint32_t n = t.n[ti];
+  const float* g = t.g[ti];
+  const uint32_t end = min(n, c0 + kChunk);
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t i = c0 + (j * 256 + threadIdx.x) * 4;
+    if (i + 3 < end) {
+      const f4 G = *reinterpret_cast<const f4*>(g + i);
+      acc += G[0] * G[0] + G[1] * G[1] + G[2] * G[2] + G[3] * G[3];
+    } else {
+      for (uint32_t k = i; k < end && k < i + 4; ++k) acc += g[k] * g[k];
+    }
+  }
+  double s = acc;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_down(s, o, 64);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) part[base + blockIdx.x] = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+}
+
+// norm = sqrt(Σ partials); scale = norm > max ? max/(norm + 1e-6) : 1
+// (nn_grad_norm_final.hlsl:31-34).
+__global__ void k_norm_final(const double* part, uint32_t total, float maxNorm, float* ns) {
+  __shared__ double sh[4];
+  double s = 0;
+  for (uint32_t i = threadIdx.x; i < total; i += 256) s += part[i];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_down(s, o, 64);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const double tot = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+    const float norm = float(sqrt(tot));
+    ns[0] = norm;
+    ns[1] = (norm > maxNorm) ? (maxNorm / (norm + 1e-6f)) : 1.0f;
+  }
+}
+
+// Build tables of at most kMaxT tensors from handle arrays; entries whose
+// param/grad (or m/v) handle is NULL or not live are skipped.
+static bool build_tables(void** params, void** grads, void** m, void** v, const uint32_t* sizes,
+                         uint32_t n, bool needW, std::vector<Table>& out, uint32_t* totalBlocks) {
+  out.clear();
+  Table cur{};
+  uint32_t blocks = 0, all = 0;
+  for (uint32_t i = 0; i < n; ++i) {
+    if (!grads[i] || (needW && !params[i])) continue;
+    Buffer* G = as_buffer(grads[i], "optimizer(grad)");
+    Buffer* W = needW ? as_buffer(params[i], "optimizer(param)") : nullptr;
+    Buffer* M = m ? as_buffer(m[i], "optimizer(m)") : nullptr;
+    Buffer* V = v ? as_buffer(v[i], "optimizer(v)") : nullptr;
+    if (!G || (needW && !W) || (m && !M) || (v && !V)) return false;
+    uint32_t cnt = std::min(sizes[i], G->count);
+    if (W) cnt = std::min(cnt, W->count);
+    if (M) cnt = std::min(cnt, M->count);
+    if (V) cnt = std::min(cnt, V->count);
+    if (!cnt) continue;
+    if (cur.count == kMaxT) {
+      cur.start[cur.count] = blocks;
+      out.push_back(cur);
+      cur = Table{};
+      blocks = 0;
+    }
+    const uint32_t k = cur.count++;
+    cur.w[k] = W ? W->ptr : nullptr;
+    cur.g[k] = G->ptr;
+    cur.m[k] = M ? M->ptr : nullptr;
+    cur.v[k] = V ? V->ptr : nullptr;
+    cur.n[k] = cnt;
+    cur.start[k] = blocks;
+    blocks += cdiv(cnt, kChunk);
+    all += cdiv(cnt, kChunk);
+  }
+  if (cur.count) {
+    cur.start[cur.count] = blocks;
+    out.push_back(cur);
+  }
+  if (totalBlocks) *totalBlocks = all;
+  return true;
+}
+
+static inline uint32_t table_blocks(const Table& t) { return t.start[t.count]; }
+
+bool sgd_multi(void** params, void** grads, const uint32_t* sizes, uint32_t n, float lr,
+               float clip) {
+  std::vector<Table> tabs;
+  if (!build_tables(params, grads, nullptr, nullptr, sizes, n, true, tabs, nullptr)) return false;
+  for (const Table& t : tabs) {
+    hipLaunchKernelGGL((k_multi<SgdOp, 3, 1>), dim3(table_blocks(t)), dim3(256), 0, stream(), t,
+                       SgdOp{lr, clip});
+    if (!check_launch("SGDBatch")) return false;
+  }
+  return true;
+}
+
+bool grad_norm_multi(void** grads, const uint32_t* sizes, uint32_t n, float max_norm,
+                     float* d_ns) {
+  std::vector<Table> tabs;
+  uint32_t total = 0;
+  if (!build_tables(nullptr, grads, nullptr, nullptr, sizes, n, false, tabs, &total)) return false;
+  double* part = reinterpret_cast<double*>(workspace(size_t(std::max<uint32_t>(total, 1)) * 2));
+  if (!part) return false;
+  uint32_t base = 0;
+  for (const Table& t : tabs) {
+    hipLaunchKernelGGL(k_multi_sumsq, dim3(table_blocks(t)), dim3(256), 0, stream(), t, part, base);
+    base += table_blocks(t);
+  }
+  hipLaunchKernelGGL(k_norm_final, dim3(1), dim3(256), 0, stream(), part, total, max_norm, d_ns);
+  return check_launch("grad_norm");
+}
+
+bool sgd_scaled_multi(void** params, void** grads, const uint32_t* sizes, uint32_t n, float lr,
+                      const float* d_ns) {
+  std::vector<Table> tabs;
+  if (!build_tables(params, grads, nullptr, nullptr, sizes, n, true, tabs, nullptr)) return false;
+  SgdScaledDev op;
+  op.lr = lr;
+  op.scale = 1.f;
+  for (const Table& t : tabs) {
+    hipLaunchKernelGGL((k_multi_devscale<SgdScaledDev, 3, 1>), dim3(table_blocks(t)), dim3(256), 0,
+                       stream(), t, op, d_ns);
+    if (!check_launch("SGDBatchClipped")) return false;
+  }
+  return true;
+}
+
+bool scale_grads_multi(void** grads, const uint32_t* sizes, uint32_t n, const float* d_ns) {
+  std::vector<Table> tabs;
+  if (!build_tables(nullptr, grads, nullptr, nullptr, sizes, n, false, tabs, nullptr)) return false;
+  ScaleDev op;
+  op.scale = 1.f;
+  for (const Table& t : tabs) {
+    hipLaunchKernelGGL((k_multi_devscale<ScaleDev, 2, 2>), dim3(table_blocks(t)), dim3(256), 0,
+                       stream(), t, op, d_ns);
+    if (!check_launch("ClipGradNorm")) return false;
+  }
+  return true;
+}
+
+bool adam_multi(void** params, void** grads, void** m, void** v, const uint32_t* sizes, uint32_t n,
+                float step, float b1, float b2, float eps, float wd, float clip) {
+  std::vector<Table> tabs;
+  uint32_t total = 0;
+  if (!build_tables(params, grads, m, v, sizes, n, true, tabs, &total)) return false;
+  double elems = 0;
+  for (const Table& t : tabs)
+    for (uint32_t i = 0; i < t.count; ++i) elems += t.n[i];
+  ProfScope prof("adam", 0, 28.0 * elems);
+  for (const Table& t : tabs) {
+    hipLaunchKernelGGL((k_multi<AdamOp, 15, 13>), dim3(table_blocks(t)), dim3(256), 0, stream(), t,
+                       AdamOp{step, b1, b2, eps, wd, clip});
+    if (!check_launch("AdamBatch")) return false;
+  }
+  return true;
+}
+
+}  // namespace dce

@@ -1,0 +1,1144 @@
+"""MI355X backend with the ``nn_engine`` API of raviadi12/directcompute_torch.
+
+Same public surface as the reference module (Tensor / Function autograd,
+functional ops, layers, Model, SGD / AdamW / Adam, Metrics, end_batch, pool
+helpers), driving ``libdcengine.so`` through ctypes instead of engine.dll.
+The buffer-handle protocol is the reference's: every op asks the library for
+new handles, ``Tensor.from_gpu`` wraps them, ``_accumulate_grad`` aliases the
+first gradient and adds later ones in place (nn_engine.py:575-610).
+
+Importing this module initialises the HIP device (as the reference
+initialises D3D11 at import, nn_engine.py:121) and raises if that fails --
+there is no CPU fallback.
+
+Not provided (out of scope): custom HLSL shaders, the
+GELU / LayerNorm / attention family (their kernels do not exist in the
+reference tree), ONNX export/import, ComputeGraph record/replay, Muon, and the
+Python-side profilers.
+"""
+from __future__ import annotations
+
+import ctypes
+import struct
+
+import numpy as np
+
+from . import _lib
+
+lib = _lib.load()
+GPUInfo = _lib.GPUInfo
+
+
+def float_to_uint(f):
+    """Bit pattern of a float32 as u32 (nn_engine.py:10-11)."""
+    return struct.unpack("I", struct.pack("f", f))[0]
+
+
+_gpu_info = GPUInfo()
+lib.GetGPUInfo(ctypes.byref(_gpu_info))
+_IS_IGPU = bool(_gpu_info.isIntegrated)
+_GPU_VENDOR = {0x8086: "Intel", 0x10DE: "NVIDIA", 0x1002: "AMD"}.get(
+    _gpu_info.vendorId, f"0x{_gpu_info.vendorId:04X}")
+_GPU_NAME = _gpu_info.description.decode("ascii", errors="replace").strip("\x00")
+_VRAM_MB = _gpu_info.dedicatedVRAM // (1024 * 1024)
+_SHARED_MB = _gpu_info.sharedMemory // (1024 * 1024)
+
+# Kernel names the reference compiles at import (nn_engine.py:147-173).  No
+# shader source is compiled here; CompileShader only reports whether the
+# library implements the name, and (as in the reference) the result is not
+# required for names that are never dispatched.
+shaders = [
+    "matmul_universal", "matmul_coarsened", "matmul_heavy", "add_bias", "relu", "relu_grad",
+    "softmax", "softmax_ce_grad", "bias_grad", "sgd", "loss", "maxpool_forward",
+    "maxpool_backward", "grad_accum", "im2col", "conv_reshape", "conv_grad_reshape", "col2im",
+    "argmax_correct", "accumulate_scalar", "bias_relu", "conv_grad_reshape_relu",
+    "batchnorm_mean_var", "batchnorm_forward", "batchnorm_backward_reduce",
+    "batchnorm_backward_dx", "adam", "scale_add", "rms", "depthwise_conv_forward",
+    "depthwise_conv_backward_input", "depthwise_conv_backward_filter", "global_avg_pool",
+    "global_avg_pool_backward", "add", "relu6", "relu6_grad", "leaky_relu", "leaky_relu_grad",
+    "upsample", "upsample_backward", "concat_insert", "slice", "dice_loss", "dice_loss_grad",
+    "sigmoid", "sigmoid_grad", "matmul_reduce", "dice_loss_sums", "grad_sq_reduce",
+    "grad_norm_final", "sgd_clipped", "matmul_dgpu",
+]
+_MISSING_KERNELS = [s for s in shaders if not lib.CompileShader(s.encode(), None)]
+if _MISSING_KERNELS:
+    raise RuntimeError(f"libdcengine lacks kernels: {_MISSING_KERNELS}")
+
+
+def last_error():
+    """Reason for the library's last failure ('' if none)."""
+    return _lib.last_error(lib)
+
+
+def _check(handle, what):
+    if not handle:
+        raise RuntimeError(f"{what} failed: {last_error()}")
+    return handle
+
+
+# --------------------------------------------------------------------------
+# Dispatch helpers (same packing as nn_engine.py:421-448)
+# --------------------------------------------------------------------------
+class ParamsCB(ctypes.Structure):
+    _fields_ = [(f"u{i}", ctypes.c_uint) for i in range(1, 10)]
+
+
+_srv_arr = (ctypes.c_void_p * 8)()
+_uav_arr = (ctypes.c_void_p * 8)()
+_threads = (ctypes.c_uint * 3)()
+_cb = ParamsCB()
+
+
+def _fill(srvs, uavs, tx, ty, tz, vals):
+    for i, h in enumerate(srvs):
+        _srv_arr[i] = h
+    for i, h in enumerate(uavs):
+        _uav_arr[i] = h
+    _threads[0], _threads[1], _threads[2] = tx, ty, tz
+    (_cb.u1, _cb.u2, _cb.u3, _cb.u4, _cb.u5, _cb.u6, _cb.u7, _cb.u8, _cb.u9) = vals
+
+
+def _dispatch(name, srvs, uavs, tx, ty, tz, u1=0, u2=0, u3=0, u4=0, u5=0, u6=0, u7=0, u8=0, u9=0,
+              cbSize=16):
+    """RunShader with pre-allocated ctypes arrays."""
+    _fill(srvs, uavs, tx, ty, tz, (u1, u2, u3, u4, u5, u6, u7, u8, u9))
+    if cbSize > 0:
+        lib.RunShader(name, _srv_arr, len(srvs), _uav_arr, len(uavs), _threads, ctypes.byref(_cb), cbSize)
+    else:
+        lib.RunShader(name, _srv_arr, len(srvs), _uav_arr, len(uavs), _threads, None, 0)
+
+
+def _dispatch_raw(name, srvs, uavs, tx, ty, tz, u1=0, u2=0, u3=0, u4=0, u5=0, u6=0, u7=0, u8=0,
+                  u9=0, cbSize=16):
+    """RunShaderRaw with pre-allocated ctypes arrays."""
+    _fill(srvs, uavs, tx, ty, tz, (u1, u2, u3, u4, u5, u6, u7, u8, u9))
+    if cbSize > 0:
+        lib.RunShaderRaw(name, _srv_arr, len(srvs), _uav_arr, len(uavs), _threads, ctypes.byref(_cb), cbSize)
+    else:
+        lib.RunShaderRaw(name, _srv_arr, len(srvs), _uav_arr, len(uavs), _threads, None, 0)
+
+
+_all_tensors = []
+
+
+def release_all_buffers():
+    """Detach graph state of every tracked tensor and release their buffers
+    with one ReleaseBufferBatch call (nn_engine.py:486-505)."""
+    global _all_tensors
+    handles = []
+    for t in _all_tensors:
+        if t._ctx:
+            t._ctx.inputs = ()
+            t._ctx = None
+        t.grad = None
+        if t.gpu_buf:
+            handles.append(t.gpu_buf)
+            t.gpu_buf = None
+    _all_tensors = []
+    if handles:
+        arr = (ctypes.c_void_p * len(handles))(*handles)
+        lib.ReleaseBufferBatch(arr, len(handles))
+
+
+def _shape_size(shape):
+    s = 1
+    for d in shape:
+        s *= d
+    return s
+
+
+# --------------------------------------------------------------------------
+# Tensor / Function
+# --------------------------------------------------------------------------
+class Tensor:
+    __slots__ = ["data", "shape", "size", "requires_grad", "grad", "gpu_buf", "_ctx", "_cached_topo"]
+
+    def __init__(self, data, requires_grad=False, track=True):
+        if isinstance(data, np.ndarray):
+            arr = data if data.dtype == np.float32 else data.astype(np.float32)
+        else:
+            arr = np.array(data, dtype=np.float32)
+        arr = np.ascontiguousarray(arr)
+        self.data = arr
+        self.shape = arr.shape
+        self.size = arr.size
+        self.requires_grad = requires_grad
+        self.grad = None
+        self.gpu_buf = lib.CreateBuffer(arr.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), self.size)
+        self._ctx = None
+        if track:
+            _all_tensors.append(self)
+
+    def __del__(self):
+        try:
+            if self.gpu_buf:
+                lib.ReleaseBuffer(self.gpu_buf)
+                self.gpu_buf = None
+        except Exception:
+            pass
+
+    @classmethod
+    def from_gpu(cls, handle, shape, requires_grad=False, track=True):
+        t = object.__new__(cls)
+        t.data = None
+        t.shape = shape
+        t.size = _shape_size(shape)
+        t.requires_grad = requires_grad
+        t.grad = None
+        t.gpu_buf = handle
+        t._ctx = None
+        if track:
+            _all_tensors.append(t)
+        return t
+
+    @classmethod
+    def empty(cls, shape, requires_grad=False, track=True):
+        t = cls.from_gpu(_check(lib.CreateBuffer(None, _shape_size(shape)), "CreateBuffer"),
+                         tuple(shape), requires_grad=requires_grad, track=track)
+        return t
+
+    @classmethod
+    def empty_like(cls, other, requires_grad=None, track=True):
+        req = other.requires_grad if requires_grad is None else bool(requires_grad)
+        return cls.empty(other.shape, requires_grad=req, track=track)
+
+    def sync(self):
+        if self.gpu_buf:
+            if self.data is None or self.data.shape != tuple(self.shape):
+                self.data = np.empty(self.shape, dtype=np.float32)
+            lib.ReadBuffer(self.gpu_buf, self.data.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+        return self.data
+
+    def upload(self, data):
+        """Overwrite the device buffer with `data` (no new buffer)."""
+        if data.dtype != np.float32:
+            data = data.astype(np.float32)
+        data = np.ascontiguousarray(data)
+        self.data = data
+        self.shape = data.shape
+        self.size = data.size
+        lib.UpdateBuffer(self.gpu_buf, data.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+
+    def backward(self, grad=None):
+        """Reverse-topological traversal (nn_engine.py:575-603)."""
+        if grad is None:
+            grad = Tensor(np.ones(self.shape, dtype=np.float32), track=False)
+        self.grad = grad
+        try:
+            topo = self._cached_topo
+        except AttributeError:
+            topo = []
+            visited = set()
+            stack = [self]
+            while stack:
+                v = stack[-1]
+                if v in visited:
+                    stack.pop()
+                    continue
+                done = True
+                if v._ctx:
+                    for i in v._ctx.inputs:
+                        if isinstance(i, Tensor) and i.requires_grad and i not in visited:
+                            stack.append(i)
+                            done = False
+                if done:
+                    visited.add(v)
+                    stack.pop()
+                    topo.append(v)
+            self._cached_topo = topo
+        for v in reversed(topo):
+            if v._ctx and v.grad is not None:
+                v._ctx.backward(v.grad)
+
+    def _accumulate_grad(self, grad):
+        """First gradient is aliased; later ones are added in place with
+        grad_accum (nn_engine.py:605-610)."""
+        if self.grad is None or self.grad.gpu_buf is None:
+            self.grad = grad
+        else:
+            _dispatch(b"grad_accum", (grad.gpu_buf,), (self.grad.gpu_buf,),
+                      (self.size + 255) // 256, 1, 1, u1=self.size)
+
+
+class Function:
+    def __init__(self, *inputs):
+        self.inputs = inputs
+
+    def backward(self, grad_output):
+        raise NotImplementedError
+
+
+def _new(count, what):
+    return _check(lib.CreateBuffer(None, count), what)
+
+
+# --------------------------------------------------------------------------
+# Ops
+# --------------------------------------------------------------------------
+class MatMul(Function):
+    """Y = op(A)·op(B) via MatMulAlloc; backward computes dA/dB straight into
+    the raw layouts of A/B for the four transpose combinations
+    (nn_engine.py:913-952)."""
+
+    def forward(self, A, B, transA=False, transB=False):
+        self.inputs = (A, B)
+        self.transA, self.transB = transA, transB
+        self.A_shape, self.B_shape = A.shape, B.shape
+        flags = (1 if transA else 0) | (2 if transB else 0)
+        M = A.shape[1] if transA else A.shape[0]
+        K = A.shape[0] if transA else A.shape[1]
+        N = B.shape[0] if transB else B.shape[1]
+        h = _check(lib.MatMulAlloc(A.gpu_buf, B.gpu_buf, M, K, N, flags), "MatMulAlloc")
+        res = Tensor.from_gpu(h, (M, N), requires_grad=A.requires_grad or B.requires_grad)
+        res._ctx = self
+        return res
+
+    def backward(self, grad_output):
+        A, B = self.inputs
+        a0, a1 = self.A_shape
+        b0, b1 = self.B_shape
+        M, N = grad_output.shape
+        g = grad_output.gpu_buf
+        tA, tB = self.transA, self.transB
+        if A.requires_grad:
+            if not tA and not tB:
+                h = lib.MatMulAlloc(g, B.gpu_buf, M, N, a1, 2)      # dY·Bᵀ
+            elif not tA and tB:
+                h = lib.MatMulAlloc(g, B.gpu_buf, M, N, b1, 0)      # dY·B
+            elif tA and not tB:
+                h = lib.MatMulAlloc(B.gpu_buf, g, a0, N, a1, 2)     # B·dYᵀ
+            else:
+                h = lib.MatMulAlloc(B.gpu_buf, g, a0, N, a1, 3)     # Bᵀ·dYᵀ
+            A._accumulate_grad(Tensor.from_gpu(_check(h, "MatMul.backward(dA)"), A.shape, track=True))
+        if B.requires_grad:
+            if not tA and not tB:
+                h = lib.MatMulAlloc(A.gpu_buf, g, a1, a0, N, 1)     # Aᵀ·dY
+            elif not tA and tB:
+                h = lib.MatMulAlloc(g, A.gpu_buf, b0, a0, a1, 1)    # dYᵀ·A
+            elif tA and not tB:
+                h = lib.MatMulAlloc(A.gpu_buf, g, a0, a1, b1, 0)    # A·dY
+            else:
+                h = lib.MatMulAlloc(g, A.gpu_buf, b0, a1, b1, 3)    # dYᵀ·Aᵀ
+            B._accumulate_grad(Tensor.from_gpu(_check(h, "MatMul.backward(dB)"), B.shape, track=True))
+
+
+class Conv2D(Function):
+    """ConvForwardFused / ConvBackwardFused (nn_engine.py:954-1016).  The
+    implicit-GEMM library keeps no im2col buffer, so `im2col_handle` is None."""
+
+    def __del__(self):
+        h = getattr(self, "im2col_handle", None)
+        if h:
+            try:
+                lib.ReleaseBuffer(h)
+            except Exception:
+                pass
+            self.im2col_handle = None
+
+    def forward(self, x, filters, bias, stride=1, padding=0, actType=0):
+        self.inputs = (x, filters, bias)
+        self.stride, self.padding, self.actType = stride, padding, actType
+        batch, inC, inH, inW = x.shape
+        outC, _, kH, kW = filters.shape
+        outH = (inH + 2 * padding - kH) // stride + 1
+        outW = (inW + 2 * padding - kW) // stride + 1
+        needs_backward = x.requires_grad or filters.requires_grad or bias.requires_grad
+        p_im2col = ctypes.c_void_p()
+        h = lib.ConvForwardFused(x.gpu_buf, filters.gpu_buf, bias.gpu_buf, batch, inC, inH, inW,
+                                 outC, kH, kW, stride, padding, actType,
+                                 ctypes.byref(p_im2col) if needs_backward else None)
+        _check(h, "ConvForwardFused")
+        self.im2col_handle = p_im2col.value if needs_backward else None
+        res = Tensor.from_gpu(h, (batch, outC, outH, outW), requires_grad=needs_backward)
+        self.fwd_output = res if actType != 0 and needs_backward else None
+        res._ctx = self
+        return res
+
+    def backward(self, grad_output):
+        x, filters, bias = self.inputs
+        batch, inC, inH, inW = x.shape
+        outC, _, kH, kW = filters.shape
+        pdf, pdb, pdx = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+        fwd = self.fwd_output.gpu_buf if self.fwd_output else None
+        lib.ConvBackwardFused(grad_output.gpu_buf, fwd, x.gpu_buf, filters.gpu_buf,
+                              self.im2col_handle, batch, inC, inH, inW, outC, kH, kW,
+                              self.stride, self.padding, self.actType,
+                              1 if x.requires_grad else 0, 1 if filters.requires_grad else 0,
+                              1 if bias.requires_grad else 0,
+                              ctypes.byref(pdf), ctypes.byref(pdb), ctypes.byref(pdx))
+        self.fwd_output = None
+        self.im2col_handle = None  # consumed by ConvBackwardFused
+        if (filters.requires_grad and not pdf.value) or (x.requires_grad and not pdx.value):
+            raise RuntimeError(f"ConvBackwardFused failed: {last_error()}")
+        if pdf.value:
+            filters._accumulate_grad(Tensor.from_gpu(pdf.value, filters.shape, track=True))
+        if pdb.value:
+            bias._accumulate_grad(Tensor.from_gpu(pdb.value, bias.shape, track=True))
+        if pdx.value:
+            x._accumulate_grad(Tensor.from_gpu(pdx.value, x.shape, track=True))
+
+
+class MaxPool2D(Function):
+    def __del__(self):
+        h = getattr(self, "indices_handle", None)
+        if h:
+            try:
+                lib.ReleaseBuffer(h)
+            except Exception:
+                pass
+            self.indices_handle = None
+
+    def forward(self, x, pool_size=2, stride=2):
+        self.inputs = (x,)
+        batch, inC, inH, inW = x.shape
+        outH = (inH - pool_size) // stride + 1
+        outW = (inW - pool_size) // stride + 1
+        p_idx = ctypes.c_void_p()
+        h = _check(lib.MaxPoolForwardFused(x.gpu_buf, batch, inC, inH, inW, pool_size, stride,
+                                           ctypes.byref(p_idx)), "MaxPoolForwardFused")
+        self.indices_handle = p_idx.value
+        res = Tensor.from_gpu(h, (batch, inC, outH, outW), requires_grad=x.requires_grad)
+        res._ctx = self
+        return res
+
+    def backward(self, grad_output):
+        x = self.inputs[0]
+        batch, inC, outH, outW = grad_output.shape
+        h = lib.MaxPoolBackwardFused(grad_output.gpu_buf, self.indices_handle, batch, inC, outH,
+                                     outW, x.size)
+        self.indices_handle = None  # consumed by MaxPoolBackwardFused
+        x._accumulate_grad(Tensor.from_gpu(_check(h, "MaxPoolBackwardFused"), x.shape, track=True))
+
+
+class Flatten(Function):
+    def forward(self, x):
+        self.inputs = (x,)
+        lib.AddRefBuffer(x.gpu_buf)
+        res = Tensor.from_gpu(x.gpu_buf, (x.shape[0], x.size // x.shape[0]),
+                              requires_grad=x.requires_grad, track=False)
+        res._ctx = self
+        return res
+
+    def backward(self, grad_output):
+        lib.AddRefBuffer(grad_output.gpu_buf)
+        self.inputs[0]._accumulate_grad(
+            Tensor.from_gpu(grad_output.gpu_buf, self.inputs[0].shape, track=False))
+
+
+def _bias_grad(g_tensor, rows, n):
+    h = _new(n, "bias_grad")
+    _dispatch(b"bias_grad", (g_tensor.gpu_buf,), (h,), n, 1, 1, u1=rows, u2=n, u3=n, u4=1)
+    return h
+
+
+class AddBias(Function):
+    def forward(self, A, B):
+        self.inputs = (A, B)
+        h = _new(A.size, "add_bias")
+        _dispatch(b"add_bias", (A.gpu_buf, B.gpu_buf), (h,), (A.size + 255) // 256, 1, 1,
+                  u1=A.shape[0], u2=A.shape[1])
+        res = Tensor.from_gpu(h, A.shape, requires_grad=A.requires_grad or B.requires_grad)
+        res._ctx = self
+        return res
+
+    def backward(self, grad_output):
+        A, B = self.inputs
+        if A.requires_grad:
+            A._accumulate_grad(grad_output)
+        if B.requires_grad:
+            B._accumulate_grad(Tensor.from_gpu(_bias_grad(grad_output, grad_output.shape[0], B.size),
+                                               B.shape, track=True))
+
+
+class BiasReLUFunc(Function):
+    """add_bias + ReLU; backward masks on the *output* (nn_engine.py:1091-1106)."""
+
+    def forward(self, A, B):
+        self.inputs = (A, B)
+        h = _new(A.size, "bias_relu")
+        _dispatch(b"bias_relu", (A.gpu_buf, B.gpu_buf), (h,), (A.size + 255) // 256, 1, 1,
+                  u1=A.shape[0], u2=A.shape[1])
+        res = Tensor.from_gpu(h, A.shape, requires_grad=A.requires_grad or B.requires_grad)
+        self.output = res
+        res._ctx = self
+        return res
+
+    def backward(self, grad_output):
+        A, B = self.inputs
+        out = self.output
+        h = _new(grad_output.size, "relu_grad")
+        _dispatch(b"relu_grad", (grad_output.gpu_buf, out.gpu_buf), (h,),
+                  (grad_output.size + 255) // 256, 1, 1, u1=grad_output.size)
+        eff = Tensor.from_gpu(h, grad_output.shape, track=True)
+        self.output = None
+        if A.requires_grad:
+            A._accumulate_grad(eff)
+        if B.requires_grad:
+            B._accumulate_grad(Tensor.from_gpu(_bias_grad(eff, eff.shape[0], B.size), B.shape, track=True))
+
+
+class _Unary(Function):
+    """Elementwise op y = f(x) whose backward shader reads (grad, saved)."""
+    fwd_name = None
+    bwd_name = None
+    save_output = False
+
+    def _cb(self, x):
+        return dict(u1=x.size)
+
+    def forward(self, x):
+        self.inputs = (x,)
+        h = _new(x.size, self.fwd_name.decode())
+        if self.fwd_name == b"relu":
+            _dispatch(b"relu", (x.gpu_buf,), (h,), (x.size + 255) // 256, 1, 1, cbSize=0)
+        else:
+            _dispatch(self.fwd_name, (x.gpu_buf,), (h,), (x.size + 255) // 256, 1, 1, **self._cb(x))
+        res = Tensor.from_gpu(h, x.shape, requires_grad=x.requires_grad)
+        res._ctx = self
+        if self.save_output:
+            self.out_tensor = res
+        return res
+
+    def backward(self, grad_output):
+        x = self.inputs[0]
+        if x.requires_grad:
+            saved = self.out_tensor if self.save_output else x
+            h = _new(x.size, self.bwd_name.decode())
+            _dispatch(self.bwd_name, (grad_output.gpu_buf, saved.gpu_buf), (h,),
+                      (x.size + 255) // 256, 1, 1, **self._cb(x))
+            x._accumulate_grad(Tensor.from_gpu(h, x.shape, track=True))
+
+
+class ReLUFunc(_Unary):
+    fwd_name, bwd_name = b"relu", b"relu_grad"
+
+
+class ReLU6Func(_Unary):
+    fwd_name, bwd_name = b"relu6", b"relu6_grad"
+
+
+class SigmoidFunc(_Unary):
+    fwd_name, bwd_name, save_output = b"sigmoid", b"sigmoid_grad", True
+
+
+class LeakyReLUFunc(_Unary):
+    fwd_name, bwd_name = b"leaky_relu", b"leaky_relu_grad"
+
+    def forward(self, x, alpha=0.1):
+        self.alpha = alpha
+        return super().forward(x)
+
+    def _cb(self, x):
+        return dict(u1=x.size, u2=float_to_uint(self.alpha))
+
+
+class UpSample2D(Function):
+    def forward(self, x, scaleH=2, scaleW=2):
+        self.inputs = (x,)
+        self.scaleH, self.scaleW = scaleH, scaleW
+        batch, C, inH, inW = x.shape
+        outH, outW = inH * scaleH, inW * scaleW
+        n = batch * C * outH * outW
+        h = _new(n, "upsample")
+        _dispatch(b"upsample", (x.gpu_buf,), (h,), (n + 255) // 256, 1, 1, u1=batch, u2=C, u3=inH,
+                  u4=inW, u5=outH, u6=outW, u7=scaleH, u8=scaleW, cbSize=32)
+        res = Tensor.from_gpu(h, (batch, C, outH, outW), requires_grad=x.requires_grad)
+        res._ctx = self
+        return res
+
+    def backward(self, grad_output):
+        x = self.inputs[0]
+        if x.requires_grad:
+            batch, C, inH, inW = x.shape
+            h = _new(x.size, "upsample_backward")
+            _dispatch(b"upsample_backward", (grad_output.gpu_buf,), (h,), (x.size + 255) // 256, 1, 1,
+                      u1=batch, u2=C, u3=inH, u4=inW, u5=inH * self.scaleH, u6=inW * self.scaleW,
+                      u7=self.scaleH, u8=self.scaleW, cbSize=32)
+            x._accumulate_grad(Tensor.from_gpu(h, x.shape, track=True))
+
+
+class Concat(Function):
+    def forward(self, tensors, axis=1):
+        if axis != 1:
+            raise NotImplementedError("Concat currently only supported along channel dimension (axis 1)")
+        self.inputs = tuple(tensors)
+        batch, H, W = tensors[0].shape[0], tensors[0].shape[2], tensors[0].shape[3]
+        S = H * W
+        total_C = sum(t.shape[1] for t in tensors)
+        h = _new(batch * total_C * S, "concat")
+        off = 0
+        self.c_offsets = []
+        for t in tensors:
+            self.c_offsets.append(off)
+            c_in = t.shape[1]
+            n = batch * c_in * S
+            _dispatch(b"concat_insert", (t.gpu_buf,), (h,), (n + 255) // 256, 1, 1, u1=batch, u2=c_in,
+                      u3=S, u4=total_C, u5=off, cbSize=20)
+            off += c_in
+        res = Tensor.from_gpu(h, (batch, total_C, H, W), requires_grad=any(t.requires_grad for t in tensors))
+        res._ctx = self
+        return res
+
+    def backward(self, grad_output):
+        batch, total_C, H, W = grad_output.shape
+        S = H * W
+        for t, off in zip(self.inputs, self.c_offsets):
+            if t.requires_grad:
+                c_in = t.shape[1]
+                n = batch * c_in * S
+                h = _new(n, "slice")
+                _dispatch(b"slice", (grad_output.gpu_buf,), (h,), (n + 255) // 256, 1, 1, u1=batch,
+                          u2=c_in, u3=S, u4=total_C, u5=off, cbSize=20)
+                t._accumulate_grad(Tensor.from_gpu(h, t.shape, track=True))
+
+
+class SoftmaxCEFunc(Function):
+    """softmax + mean CE loss; backward (p - onehot)/B ignoring the incoming
+    gradient (nn_engine.py:1268-1288)."""
+
+    def forward(self, x, labels):
+        self.inputs = (x, labels)
+        B, K = x.shape
+        hs = _new(x.size, "softmax")
+        _dispatch(b"softmax", (x.gpu_buf,), (hs,), (B + 15) // 16, 1, 1, u1=B, u2=K)
+        self.softmax_out = Tensor.from_gpu(hs, x.shape)
+        hl = _new(1, "loss")
+        _dispatch(b"loss", (x.gpu_buf, labels.gpu_buf), (hl,), 1, 1, 1, u1=B, u2=K)
+        res = Tensor.from_gpu(hl, (1,), requires_grad=True)
+        res._ctx = self
+        return res
+
+    def backward(self, grad_output):
+        x, labels = self.inputs
+        B, K = x.shape
+        h = _new(x.size, "softmax_ce_grad")
+        _dispatch(b"softmax_ce_grad", (self.softmax_out.gpu_buf, labels.gpu_buf), (h,),
+                  (K + 15) // 16, (B + 15) // 16, 1, u1=B, u2=K)
+        x._accumulate_grad(Tensor.from_gpu(h, x.shape, track=True))
+
+
+class DiceLossFunc(Function):
+    def forward(self, pred, target):
+        self.inputs = (pred, target)
+        batch = pred.shape[0]
+        size = pred.size // batch
+        h = _new(batch, "dice_loss")
+        _dispatch(b"dice_loss", (pred.gpu_buf, target.gpu_buf), (h,), batch, 1, 1, u1=batch, u2=size)
+        res = Tensor.from_gpu(h, (batch,), requires_grad=True)
+        res._ctx = self
+        return res
+
+    def backward(self, grad_output):
+        pred, target = self.inputs
+        batch = pred.shape[0]
+        size = pred.size // batch
+        hs = _new(batch * 3, "dice_loss_sums")
+        _dispatch(b"dice_loss_sums", (pred.gpu_buf, target.gpu_buf), (hs,), batch, 1, 1, u1=batch, u2=size)
+        h = _new(pred.size, "dice_loss_grad")
+        _dispatch(b"dice_loss_grad", (pred.gpu_buf, target.gpu_buf, hs), (h,), (pred.size + 255) // 256,
+                  1, 1, u1=batch, u2=size)
+        lib.ReleaseBuffer(hs)
+        pred._accumulate_grad(Tensor.from_gpu(h, pred.shape, track=True))
+
+
+class AddFunc(Function):
+    """Residual add; backward passes the same buffer to both inputs via
+    AddRef (nn_engine.py:1379-1397)."""
+
+    def forward(self, A, B):
+        self.inputs = (A, B)
+        h = _new(A.size, "add")
+        _dispatch(b"add", (A.gpu_buf, B.gpu_buf), (h,), (A.size + 255) // 256, 1, 1, u1=A.size, u2=1)
+        res = Tensor.from_gpu(h, A.shape, requires_grad=A.requires_grad or B.requires_grad)
+        res._ctx = self
+        return res
+
+    def backward(self, grad_output):
+        A, B = self.inputs
+        for t in (A, B):
+            if t.requires_grad:
+                lib.AddRefBuffer(grad_output.gpu_buf)
+                t._accumulate_grad(Tensor.from_gpu(grad_output.gpu_buf, t.shape, track=False))
+
+
+class DepthwiseConv2DFunc(Function):
+    def forward(self, x, filters, bias, stride=1, padding=0):
+        self.inputs = (x, filters, bias)
+        self.stride, self.padding = stride, padding
+        batch, C, inH, inW = x.shape
+        kH, kW = filters.shape[2], filters.shape[3]
+        outH = (inH + 2 * padding - kH) // stride + 1
+        outW = (inW + 2 * padding - kW) // stride + 1
+        n = batch * C * outH * outW
+        h = _new(n, "depthwise_conv_forward")
+        _dispatch(b"depthwise_conv_forward", (x.gpu_buf, filters.gpu_buf, bias.gpu_buf), (h,),
+                  (n + 255) // 256, 1, 1, u1=batch, u2=C, u3=inH, u4=inW, u5=kH, u6=kW, u7=stride,
+                  u8=padding, u9=outH, cbSize=36)
+        res = Tensor.from_gpu(h, (batch, C, outH, outW),
+                              requires_grad=x.requires_grad or filters.requires_grad or bias.requires_grad)
+        res._ctx = self
+        return res
+
+    def backward(self, grad_output):
+        x, filters, bias = self.inputs
+        batch, C, inH, inW = x.shape
+        kH, kW = filters.shape[2], filters.shape[3]
+        outH = grad_output.shape[2]
+        cb = dict(u1=batch, u2=C, u3=inH, u4=inW, u5=kH, u6=kW, u7=self.stride, u8=self.padding,
+                  u9=outH, cbSize=36)
+        if x.requires_grad:
+            h = _new(x.size, "depthwise_conv_backward_input")
+            _dispatch(b"depthwise_conv_backward_input", (grad_output.gpu_buf, filters.gpu_buf), (h,),
+                      (x.size + 255) // 256, 1, 1, **cb)
+            x._accumulate_grad(Tensor.from_gpu(h, x.shape, track=True))
+        if filters.requires_grad or bias.requires_grad:
+            hf = _new(filters.size, "depthwise dW")
+            hb = _new(bias.size, "depthwise db")
+            _dispatch(b"depthwise_conv_backward_filter", (grad_output.gpu_buf, x.gpu_buf), (hf, hb),
+                      C, 1, 1, **cb)
+            if filters.requires_grad:
+                filters._accumulate_grad(Tensor.from_gpu(hf, filters.shape, track=True))
+            else:
+                lib.ReleaseBuffer(hf)
+            if bias.requires_grad:
+                bias._accumulate_grad(Tensor.from_gpu(hb, bias.shape, track=True))
+            else:
+                lib.ReleaseBuffer(hb)
+
+
+class GlobalAvgPool2DFunc(Function):
+    def forward(self, x):
+        self.inputs = (x,)
+        batch, C, H, W = x.shape
+        self.S = H * W
+        h = _new(batch * C, "global_avg_pool")
+        _dispatch(b"global_avg_pool", (x.gpu_buf,), (h,), batch * C, 1, 1, u1=batch, u2=C, u3=self.S)
+        res = Tensor.from_gpu(h, (batch, C), requires_grad=x.requires_grad)
+        res._ctx = self
+        return res
+
+    def backward(self, grad_output):
+        x = self.inputs[0]
+        if x.requires_grad:
+            batch, C = grad_output.shape
+            h = _new(x.size, "global_avg_pool_backward")
+            _dispatch(b"global_avg_pool_backward", (grad_output.gpu_buf,), (h,), (x.size + 255) // 256,
+                      1, 1, u1=batch, u2=C, u3=self.S)
+            x._accumulate_grad(Tensor.from_gpu(h, x.shape, track=True))
+
+
+class BatchNorm2dFunc(Function):
+    """Training-mode BN: batchnorm_mean_var + batchnorm_forward; backward
+    batchnorm_backward_reduce then batchnorm_backward_dx (nn_engine.py:1794-1868)."""
+
+    def forward(self, x, gamma, beta, running_mean, running_var, eps=1e-5, momentum=0.1, training=True):
+        self.inputs = (x, gamma, beta)
+        self.batch, self.channels, self.h, self.w = x.shape
+        self.S = self.h * self.w
+        self.eps = eps
+        if training:
+            self.batch_mean_handle = _new(self.channels, "bn mean")
+            self.batch_var_handle = _new(self.channels, "bn var")
+            _dispatch(b"batchnorm_mean_var", (x.gpu_buf,),
+                      (self.batch_mean_handle, self.batch_var_handle, running_mean.gpu_buf, running_var.gpu_buf),
+                      self.channels, 1, 1, u1=self.batch, u2=self.channels, u3=self.S, u4=1,
+                      u5=float_to_uint(momentum), cbSize=20)
+            mean_buf, var_buf = self.batch_mean_handle, self.batch_var_handle
+        else:
+            mean_buf, var_buf = running_mean.gpu_buf, running_var.gpu_buf
+            self.batch_mean_handle = self.batch_var_handle = None
+        h = _new(x.size, "batchnorm_forward")
+        _dispatch(b"batchnorm_forward", (x.gpu_buf, mean_buf, var_buf, gamma.gpu_buf, beta.gpu_buf), (h,),
+                  (x.size + 255) // 256, 1, 1, u1=self.batch, u2=self.channels, u3=self.S,
+                  u4=float_to_uint(eps), cbSize=16)
+        res = Tensor.from_gpu(h, x.shape, requires_grad=x.requires_grad or gamma.requires_grad or beta.requires_grad)
+        res._ctx = self
+        return res
+
+    def backward(self, grad_output):
+        x, gamma, beta = self.inputs
+        if self.batch_mean_handle is None:
+            raise RuntimeError("BatchNorm backward requires training=True during forward")
+        hg = _new(self.channels, "bn dgamma")
+        hb = _new(self.channels, "bn dbeta")
+        cb = dict(u1=self.batch, u2=self.channels, u3=self.S, u4=float_to_uint(self.eps))
+        _dispatch(b"batchnorm_backward_reduce",
+                  (x.gpu_buf, grad_output.gpu_buf, self.batch_mean_handle, self.batch_var_handle),
+                  (hg, hb), self.channels, 1, 1, **cb)
+        hx = _new(x.size, "bn dx")
+        _dispatch(b"batchnorm_backward_dx",
+                  (x.gpu_buf, grad_output.gpu_buf, self.batch_mean_handle, self.batch_var_handle,
+                   gamma.gpu_buf, hg, hb), (hx,), (x.size + 255) // 256, 1, 1, **cb)
+        for t, h in ((gamma, hg), (beta, hb), (x, hx)):
+            if t.requires_grad:
+                t._accumulate_grad(Tensor.from_gpu(h, t.shape, track=True))
+            else:
+                lib.ReleaseBuffer(h)
+        lib.ReleaseBuffer(self.batch_mean_handle)
+        lib.ReleaseBuffer(self.batch_var_handle)
+        self.batch_mean_handle = self.batch_var_handle = None
+
+
+def _absent(name):
+    def f(*args, **kwargs):
+        raise NotImplementedError(f"{name}: its kernels do not exist in the reference tree "
+                                  "(nn_engine.py:156-163 names shaders with no source)")
+    return f
+
+
+gelu = _absent("gelu")
+layernorm = _absent("layernorm")
+attention = _absent("attention")
+
+
+def matmul(A, B, transA=False, transB=False): return MatMul().forward(A, B, transA, transB)
+def add_bias(A, B): return AddBias().forward(A, B)
+def bias_relu(A, B): return BiasReLUFunc().forward(A, B)
+def relu(x): return ReLUFunc().forward(x)
+def relu6(x): return ReLU6Func().forward(x)
+def sigmoid(x): return SigmoidFunc().forward(x)
+def softmax_ce(x, labels): return SoftmaxCEFunc().forward(x, labels)
+def conv2d(x, f, b, stride=1, padding=0, actType=0): return Conv2D().forward(x, f, b, stride, padding, actType)
+def maxpool2d(x, pool_size=2, stride=2): return MaxPool2D().forward(x, pool_size, stride)
+def flatten(x): return Flatten().forward(x)
+def leaky_relu(x, alpha=0.1): return LeakyReLUFunc().forward(x, alpha)
+def upsample2d(x, scaleH=2, scaleW=2): return UpSample2D().forward(x, scaleH, scaleW)
+def concat(tensors, axis=1): return Concat().forward(tensors, axis)
+def dice_loss(pred, target): return DiceLossFunc().forward(pred, target)
+def add(A, B): return AddFunc().forward(A, B)
+def depthwise_conv2d(x, f, b, stride=1, padding=0): return DepthwiseConv2DFunc().forward(x, f, b, stride, padding)
+def global_avg_pool2d(x): return GlobalAvgPool2DFunc().forward(x)
+
+
+def batchnorm2d(x, gamma, beta, rm, rv, eps=1e-5, momentum=0.1, training=True):
+    return BatchNorm2dFunc().forward(x, gamma, beta, rm, rv, eps, momentum, training)
+
+
+def _handle_arrays(params):
+    n = len(params)
+    pa = (ctypes.c_void_p * n)(*[p.gpu_buf for p in params])
+    ga = (ctypes.c_void_p * n)(*[(p.grad.gpu_buf if p.grad is not None else None) for p in params])
+    sa = (ctypes.c_uint * n)(*[p.size for p in params])
+    return pa, ga, sa
+
+
+def clip_grad_norm(params, max_norm=1.0):
+    """Global L2 norm of all gradients; when it exceeds max_norm every gradient
+    is scaled by max_norm/(norm+1e-6).  Returns the norm (nn_engine.py:1335-1355).
+    Computed on the GPU (one multi-tensor reduction + one scale pass); only the
+    norm is read back."""
+    live = [p for p in params if p.grad is not None and p.grad.gpu_buf is not None]
+    if not live:
+        return 0.0
+    n = len(live)
+    ga = (ctypes.c_void_p * n)(*[p.grad.gpu_buf for p in live])
+    sa = (ctypes.c_uint * n)(*[p.size for p in live])
+    return float(lib.ClipGradNorm(ga, sa, n, max_norm))
+
+
+def sgd_step_clipped(params, lr, max_norm=1.0):
+    """Fused norm clip + SGD on the GPU; returns the norm (nn_engine.py:1357-1367)."""
+    pa, ga, sa = _handle_arrays(params)
+    return float(lib.SGDBatchClipped(pa, ga, sa, len(params), lr, max_norm))
+
+
+def scale_add(A, B, alpha=1.0, beta=1.0):
+    h = _new(A.size, "scale_add")
+    _dispatch(b"scale_add", (A.gpu_buf, B.gpu_buf), (h,), (A.size + 255) // 256, 1, 1, u1=A.size,
+              u2=float_to_uint(alpha), u3=float_to_uint(beta), cbSize=16)
+    return Tensor.from_gpu(h, A.shape, track=True)
+
+
+# --------------------------------------------------------------------------
+# Layers and Model (initialisers as nn_engine.py:1873-1927)
+# --------------------------------------------------------------------------
+class Linear:
+    def __init__(self, in_features, out_features):
+        limit = np.sqrt(6 / (in_features + out_features))
+        self.w = Tensor(np.random.uniform(-limit, limit, (in_features, out_features)), requires_grad=True, track=False)
+        self.b = Tensor(np.zeros(out_features), requires_grad=True, track=False)
+
+    def __call__(self, x, relu=False):
+        m = matmul(x, self.w)
+        return bias_relu(m, self.b) if relu else add_bias(m, self.b)
+
+
+class ConvLayer:
+    def __init__(self, inC, outC, ks, stride=1, padding=0):
+        fan_in, fan_out = inC * ks * ks, outC * ks * ks
+        limit = np.sqrt(6 / (fan_in + fan_out))
+        self.filters = Tensor(np.random.uniform(-limit, limit, (outC, inC, ks, ks)), requires_grad=True, track=False)
+        self.bias = Tensor(np.zeros(outC), requires_grad=True, track=False)
+        self.stride, self.padding = stride, padding
+
+    def __call__(self, x, actType=0, relu=False):
+        return conv2d(x, self.filters, self.bias, self.stride, self.padding, 1 if relu else actType)
+
+
+class DepthwiseConvLayer:
+    def __init__(self, channels, ks, stride=1, padding=0):
+        limit = np.sqrt(6 / (ks * ks * 2))
+        self.filters = Tensor(np.random.uniform(-limit, limit, (channels, 1, ks, ks)), requires_grad=True, track=False)
+        self.bias = Tensor(np.zeros(channels), requires_grad=True, track=False)
+        self.stride, self.padding = stride, padding
+
+    def __call__(self, x):
+        return depthwise_conv2d(x, self.filters, self.bias, self.stride, self.padding)
+
+
+class BatchNorm2d:
+    def __init__(self, num_features, eps=1e-5, momentum=0.1):
+        self.num_features = num_features
+        self.eps, self.momentum = eps, momentum
+        self.gamma = Tensor(np.ones(num_features, dtype=np.float32), requires_grad=True, track=False)
+        self.beta = Tensor(np.zeros(num_features, dtype=np.float32), requires_grad=True, track=False)
+        self.running_mean = Tensor(np.zeros(num_features, dtype=np.float32), requires_grad=False, track=False)
+        self.running_var = Tensor(np.ones(num_features, dtype=np.float32), requires_grad=False, track=False)
+        self.training = True
+
+    def __call__(self, x):
+        return batchnorm2d(x, self.gamma, self.beta, self.running_mean, self.running_var, self.eps,
+                           self.momentum, self.training)
+
+
+class Model:
+    """Parameter discovery / train / eval as nn_engine.py:1930-1987."""
+
+    def __init__(self):
+        self._forward_trace = []
+
+    def __call__(self, x):
+        return self.forward(x)
+
+    def forward(self, x):
+        raise NotImplementedError
+
+    def parameters(self):
+        params = []
+        for name in dir(self):
+            attr = getattr(self, name)
+            if isinstance(attr, (ConvLayer, DepthwiseConvLayer)):
+                params.extend([attr.filters, attr.bias])
+            elif isinstance(attr, Linear):
+                params.extend([attr.w, attr.b])
+            elif attr.__class__.__name__ in ("BatchNorm2d", "LayerNorm"):
+                params.extend([attr.gamma, attr.beta])
+        return params
+
+    def train(self, mode=True):
+        for name in dir(self):
+            attr = getattr(self, name)
+            if hasattr(attr, "training"):
+                attr.training = mode
+
+    def eval(self):
+        self.train(False)
+
+    def _get_layers(self):
+        return [(n, getattr(self, n)) for n in sorted(dir(self))
+                if isinstance(getattr(self, n), (ConvLayer, DepthwiseConvLayer, Linear))]
+
+
+# --------------------------------------------------------------------------
+# Optimisers (nn_engine.py:2172-2242)
+# --------------------------------------------------------------------------
+class SGD:
+    def __init__(self, params, lr):
+        self.params = params
+        self.lr = lr
+        n = len(params)
+        self._param_arr = (ctypes.c_void_p * n)()
+        self._grad_arr = (ctypes.c_void_p * n)()
+        self._size_arr = (ctypes.c_uint * n)()
+
+    def zero_grad(self):
+        for p in self.params:
+            if p.grad:
+                p.grad = None
+
+    def step(self, clip=1.0):
+        """w -= lr*clamp(g, -clip, clip) for every parameter with a gradient."""
+        n = 0
+        for p in self.params:
+            if p.grad:
+                self._param_arr[n] = p.gpu_buf
+                self._grad_arr[n] = p.grad.gpu_buf
+                self._size_arr[n] = p.size
+                n += 1
+        if n > 0:
+            lib.SGDBatch(self._param_arr, self._grad_arr, self._size_arr, n, self.lr, clip)
+
+
+class AdamW:
+    """AdamW with the reference's update rule: host-side bias-corrected step
+    size lr*sqrt(1-b2^t)/(1-b1^t), decay lr*wd*w on the old weight, element
+    clip of the gradient; one multi-tensor launch per step."""
+
+    def __init__(self, params, lr=0.001, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01):
+        self.params = params
+        self.lr = lr
+        self.beta1, self.beta2 = betas
+        self.eps = eps
+        self.weight_decay = weight_decay
+        self.t = 0
+        self.m = [Tensor(np.zeros(p.shape), track=False) for p in params]
+        self.v = [Tensor(np.zeros(p.shape), track=False) for p in params]
+        self._m_bufs = [x.gpu_buf for x in self.m]
+        self._v_bufs = [x.gpu_buf for x in self.v]
+        n = len(params)
+        self._pa = (ctypes.c_void_p * n)()
+        self._ga = (ctypes.c_void_p * n)()
+        self._ma = (ctypes.c_void_p * n)()
+        self._va = (ctypes.c_void_p * n)()
+        self._sa = (ctypes.c_uint * n)()
+
+    def zero_grad(self):
+        for p in self.params:
+            if p.grad:
+                p.grad = None
+
+    def step(self, clip=1.0):
+        self.t += 1
+        step_size = self.lr * (1 - self.beta2 ** self.t) ** 0.5 / (1 - self.beta1 ** self.t)
+        n = 0
+        for i, p in enumerate(self.params):
+            if not p.grad:
+                continue
+            self._pa[n] = p.gpu_buf
+            self._ga[n] = p.grad.gpu_buf
+            self._ma[n] = self._m_bufs[i]
+            self._va[n] = self._v_bufs[i]
+            self._sa[n] = p.size
+            n += 1
+        if n:
+            lib.AdamBatch(self._pa, self._ga, self._ma, self._va, self._sa, n, step_size,
+                          self.beta1, self.beta2, self.eps, self.lr * self.weight_decay, clip)
+
+
+class Adam(AdamW):
+    def __init__(self, params, lr=0.001, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0):
+        super().__init__(params, lr, betas, eps, weight_decay=weight_decay)
+
+
+# --------------------------------------------------------------------------
+# Metrics, batch end, pool helpers (nn_engine.py:2322-2485)
+# --------------------------------------------------------------------------
+def gpu_argmax_correct(logits, labels, correct_buf):
+    batch_size, num_classes = logits.shape
+    _dispatch_raw(b"argmax_correct", (logits.gpu_buf, labels.gpu_buf), (correct_buf,),
+                  (batch_size + 255) // 256, 1, 1, u1=batch_size, u2=num_classes)
+
+
+def gpu_accumulate_loss(loss_tensor, accum_buf):
+    _dispatch(b"accumulate_scalar", (loss_tensor.gpu_buf,), (accum_buf,), 1, 1, 1, cbSize=0)
+
+
+class Metrics:
+    """GPU-resident loss / accuracy accumulators, read back in collect()."""
+
+    def __init__(self):
+        self._correct_buf = _new(1, "Metrics")
+        self._loss_buf = _new(1, "Metrics")
+        self._f1 = np.empty(1, dtype=np.float32)
+        self._f1_ptr = self._f1.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+        self._n_batches = 0
+        self.reset()
+
+    def reset(self):
+        lib.ClearBuffer(self._correct_buf)
+        lib.ClearBuffer(self._loss_buf)
+        self._n_batches = 0
+
+    def update(self, loss, logits, labels):
+        gpu_accumulate_loss(loss, self._loss_buf)
+        gpu_argmax_correct(logits, labels, self._correct_buf)
+        self._n_batches += 1
+
+    def collect(self, num_samples):
+        lib.ReadBuffer(self._loss_buf, self._f1_ptr)
+        avg_loss = float(self._f1[0]) / self._n_batches if self._n_batches else 0.0
+        lib.ReadBuffer(self._correct_buf, self._f1_ptr)
+        correct = int(np.frombuffer(self._f1.tobytes(), dtype=np.uint32)[0])
+        return avg_loss, (correct / num_samples if num_samples else 0.0)
+
+    def __del__(self):
+        try:
+            if self._correct_buf:
+                lib.ReleaseBuffer(self._correct_buf)
+            if self._loss_buf:
+                lib.ReleaseBuffer(self._loss_buf)
+        except Exception:
+            pass
+
+
+def end_batch():
+    """Release the batch's intermediates; FlushGPU every flush_interval batches."""
+    release_all_buffers()
+    end_batch._count += 1
+    if end_batch._count % end_batch.flush_interval == 0:
+        lib.FlushGPU()
+
+
+end_batch._count = 0
+end_batch.flush_interval = 10
+
+
+def warm_pool(sizes, copies=2):
+    sizes = list(sizes)
+    arr = (ctypes.c_uint * len(sizes))(*sizes)
+    lib.WarmPool(arr, len(sizes), copies)
+
+
+def discover_buffer_sizes(forward_fn, params, X_batch, Y_batch, optimizer):
+    """Run one batch while recording every CreateBuffer size."""
+    sizes = set()
+    global lib
+    real = lib
+
+    class _Spy:
+        def __getattr__(self, name):
+            return getattr(real, name)
+
+        def CreateBuffer(self, data, count):
+            sizes.add(int(count))
+            return real.CreateBuffer(data, count)
+
+    lib = _Spy()
+    try:
+        optimizer.zero_grad()
+        xb = Tensor(X_batch, track=True)
+        yb = Tensor(Y_batch, track=True)
+        logits = forward_fn(xb)
+        loss = softmax_ce(logits, yb)
+        loss.backward()
+        optimizer.step(clip=1.0)
+        end_batch()
+    finally:
+        lib = real
+    return sizes
+
+
+def auto_warm(forward_fn, params, X_sample, Y_sample, optimizer, copies=2):
+    sizes = discover_buffer_sizes(forward_fn, params, X_sample, Y_sample, optimizer)
+    warm_pool(sizes, copies)
+    lib.ResetPoolStats()
+    return sizes
+
+
+def get_pool_stats():
+    hits, misses = ctypes.c_uint64(0), ctypes.c_uint64(0)
+    lib.GetPoolStats(ctypes.byref(hits), ctypes.byref(misses))
+    return hits.value, misses.value
+
+
+def get_pool_memory():
+    return lib.GetPoolMemory()
+
+
+def drain_pool():
+    lib.DrainPool()
+
+
+def sync_gpu():
+    """Block until all queued GPU work is done."""
+    lib.SyncGPU()

@@ -1,0 +1,197 @@
+"""GPU parity of the MFMA implicit-GEMM path against the float64 oracle:
+MatMulAlloc (all flag combinations, split-K and ragged shapes), ConvForwardFused
+and ConvBackwardFused (dW, fused db, dX; ReLU mask; strides, padding, kernel
+sizes, channel counts that take the chunked and the flat K layouts)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import kernels as K
+from tests.helpers import TOL, download, he, rel_err, release, rng, upload
+
+pytestmark = pytest.mark.gpu
+
+
+GEMM_SHAPES = [
+    (1, 1, 1), (5, 7, 3), (16, 16, 16), (17, 33, 65), (63, 64, 65), (64, 128, 64),
+    (127, 129, 130), (128, 1000, 10), (6, 18432, 25), (16, 32768, 27), (200, 300, 100),
+    (128, 9216, 256), (300, 40, 500),
+]
+
+
+@pytest.mark.parametrize("M,Kd,N", GEMM_SHAPES)
+@pytest.mark.parametrize("flags", [0, 1, 2, 3])
+def test_matmul_alloc(eng, M, Kd, N, flags):
+    r = rng(1000 + M * 7 + Kd * 3 + N + flags)
+    a = r.standard_normal((M, Kd)).astype(np.float32)
+    b = r.standard_normal((Kd, N)).astype(np.float32)
+    a_raw = a.T.copy() if flags & 1 else a
+    b_raw = b.T.copy() if flags & 2 else b
+    ha, hb = upload(eng, a_raw), upload(eng, b_raw)
+    hc = eng.lib.MatMulAlloc(ha, hb, M, Kd, N, flags)
+    assert hc, eng.last_error()
+    c = download(eng, hc, (M, N))
+    ref = K.matmul(a_raw, b_raw, M, Kd, N, flags)
+    release(eng, ha, hb, hc)
+    assert rel_err(c, ref) <= TOL
+
+
+CONV_CASES = [
+    # B, C, H, W, OC, k, s, p, act
+    (2, 3, 9, 8, 4, 3, 1, 1, 1),
+    (2, 1, 28, 28, 6, 5, 1, 0, 0),        # LeNet c1
+    (3, 6, 12, 12, 16, 5, 1, 0, 1),       # LeNet c2
+    (2, 16, 13, 11, 32, 3, 1, 1, 1),      # chunked K (C % 16 == 0)
+    (2, 48, 10, 10, 16, 3, 1, 1, 1),      # UNet-style concat channels
+    (2, 3, 35, 35, 64, 11, 4, 2, 1),      # AlexNet c1 geometry (small)
+    (2, 64, 13, 13, 192, 5, 1, 2, 1),     # AlexNet c2 geometry
+    (1, 32, 16, 16, 24, 1, 1, 0, 0),      # 1x1 (MobileNet project)
+    (2, 24, 15, 15, 144, 1, 1, 0, 0),     # 1x1 expand, OC % 16 == 0
+    (2, 16, 14, 14, 20, 3, 2, 1, 1),      # stride 2, OC not multiple of 16
+    (2, 17, 9, 9, 33, 3, 2, 0, 2),        # tanh act: no derivative applied (reference quirk)
+    (1, 8, 7, 7, 8, 3, 3, 1, 0),          # stride 3
+    (2, 192, 6, 6, 256, 3, 1, 1, 1),      # deep channels
+]
+
+
+def _conv_case(eng, B, C, H, W, OC, k, s, p, act, want=(1, 1, 1), seed=0):
+    r = rng(2000 + seed + B + C * 3 + H * 5 + OC * 7 + k + s + p)
+    x = r.standard_normal((B, C, H, W)).astype(np.float32)
+    w = he(r, (OC, C, k, k), C * k * k)
+    b = (0.1 * r.standard_normal(OC)).astype(np.float32)
+    hx, hw, hb = upload(eng, x), upload(eng, w), upload(eng, b)
+    pim = ctypes.c_void_p()
+    hy = eng.lib.ConvForwardFused(hx, hw, hb, B, C, H, W, OC, k, k, s, p, act, ctypes.byref(pim))
+    assert hy, eng.last_error()
+    OH, OW = K.conv_out_hw(H, W, k, s, p)
+    y = download(eng, hy, (B, OC, OH, OW))
+    y_ref = K.conv_forward(x, w, b, s, p, act)
+    assert rel_err(y, y_ref) <= TOL, "forward"
+    dy = r.standard_normal(y.shape).astype(np.float32)
+    hdy = upload(eng, dy)
+    pdf, pdb, pdx = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+    eng.lib.ConvBackwardFused(hdy, hy if act == 1 else None, hx, hw, pim.value, B, C, H, W, OC, k, k,
+                              s, p, act, want[0], want[1], want[2],
+                              ctypes.byref(pdf), ctypes.byref(pdb), ctypes.byref(pdx))
+    # Mask from the device's own forward output (exact same y the kernel saw).
+    dW_ref, db_ref, dX_ref = K.conv_backward(dy, y, x, w, s, p, act, need_x=want[0],
+                                             need_w=want[1], need_b=want[2])
+    out = {}
+    if want[1]:
+        assert pdf.value, eng.last_error()
+        out["dW"] = (download(eng, pdf.value, w.shape), dW_ref)
+    else:
+        assert not pdf.value
+    if want[2]:
+        assert pdb.value, eng.last_error()
+        out["db"] = (download(eng, pdb.value, (OC,)), db_ref)
+    else:
+        assert not pdb.value
+    if want[0]:
+        assert pdx.value, eng.last_error()
+        out["dX"] = (download(eng, pdx.value, x.shape), dX_ref)
+    else:
+        assert not pdx.value
+    release(eng, hx, hw, hb, hy, hdy, pdf.value, pdb.value, pdx.value)
+    for name, (got, ref) in out.items():
+        assert rel_err(got, ref) <= TOL, f"{name}: {rel_err(got, ref):.3e}"
+
+
+@pytest.mark.parametrize("case", CONV_CASES, ids=[str(c) for c in CONV_CASES])
+def test_conv_forward_backward(eng, case):
+    _conv_case(eng, *case)
+
+
+@pytest.mark.parametrize("want", [(0, 1, 1), (1, 0, 0), (0, 0, 1), (1, 1, 0)])
+def test_conv_backward_subsets(eng, want):
+    _conv_case(eng, 2, 16, 10, 10, 32, 3, 1, 1, 1, want=want, seed=11)
+
+
+def test_conv_backward_relu_mask_nan_keeps_grad(eng):
+    """y <= 0 zeroes the gradient; NaN in y keeps it (nn_conv_grad_reshape_relu.hlsl:36)."""
+    B, C, H, W, OC, k = 1, 16, 6, 6, 16, 3
+    r = rng(77)
+    x = r.standard_normal((B, C, H, W)).astype(np.float32)
+    w = he(r, (OC, C, k, k), C * k * k)
+    y = r.standard_normal((B, OC, H, W)).astype(np.float32)
+    y[0, 0, 0, 0] = np.nan
+    y[0, 1, 1, 1] = 0.0
+    dy = r.standard_normal(y.shape).astype(np.float32)
+    hs = [upload(eng, a) for a in (x, w, y, dy)]
+    pdf, pdb, pdx = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+    eng.lib.ConvBackwardFused(hs[3], hs[2], hs[0], hs[1], None, B, C, H, W, OC, k, k, 1, 1, 1, 1, 1, 1,
+                              ctypes.byref(pdf), ctypes.byref(pdb), ctypes.byref(pdx))
+    dW_ref, db_ref, dX_ref = K.conv_backward(dy, y, x, w, 1, 1, 1)
+    got = (download(eng, pdf.value, w.shape), download(eng, pdb.value, (OC,)), download(eng, pdx.value, x.shape))
+    release(eng, *hs, pdf.value, pdb.value, pdx.value)
+    for g, ref in zip(got, (dW_ref, db_ref, dX_ref)):
+        assert rel_err(g, ref) <= TOL
+
+
+def test_conv_backward_consumes_im2col_handle(eng):
+    """ConvBackwardFused releases the im2col handle it is given (engine.cpp:877)."""
+    h = upload(eng, np.zeros(16, np.float32))
+    x = upload(eng, np.ones((1, 1, 4, 4), np.float32))
+    w = upload(eng, np.ones((1, 1, 3, 3), np.float32))
+    dy = upload(eng, np.ones((1, 1, 2, 2), np.float32))
+    pdf, pdb, pdx = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+    eng.lib.ClearLastError()
+    eng.lib.ConvBackwardFused(dy, None, x, w, h, 1, 1, 4, 4, 1, 3, 3, 1, 0, 0, 1, 1, 1,
+                              ctypes.byref(pdf), ctypes.byref(pdb), ctypes.byref(pdx))
+    assert eng.last_error() == ""
+    eng.lib.ReleaseBuffer(h)  # second release of a consumed handle is rejected, not a crash
+    assert "not live" in eng.last_error()
+    release(eng, x, w, dy, pdf.value, pdb.value, pdx.value)
+
+
+def test_single_conv_full_size_sampled(eng):
+    """The single-conv workload at full size (x[128,64,56,56], W[128,64,3,3],
+    s1 p1, ReLU mask): every dW/db entry and a sample of dX pixels are checked
+    against float64 sums computed directly over the full batch."""
+    B, C, H, W, OC, k = 128, 64, 56, 56, 128, 3
+    r = rng(2 * 1000)
+    x = r.standard_normal((B, C, H, W)).astype(np.float32)
+    w = he(r, (OC, C, k, k), C * k * k)
+    b = np.zeros(OC, np.float32)
+    hx, hw, hb = upload(eng, x), upload(eng, w), upload(eng, b)
+    hy = eng.lib.ConvForwardFused(hx, hw, hb, B, C, H, W, OC, k, k, 1, 1, 1, None)
+    assert hy, eng.last_error()
+    y = download(eng, hy, (B, OC, H, W))
+    dy = r.standard_normal(y.shape).astype(np.float32)
+    hdy = upload(eng, dy)
+    pdf, pdb, pdx = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+    eng.lib.ConvBackwardFused(hdy, hy, hx, hw, None, B, C, H, W, OC, k, k, 1, 1, 1, 1, 1, 1,
+                              ctypes.byref(pdf), ctypes.byref(pdb), ctypes.byref(pdx))
+    dW = download(eng, pdf.value, w.shape)
+    db = download(eng, pdb.value, (OC,))
+    dX = download(eng, pdx.value, x.shape)
+    release(eng, hx, hw, hb, hy, hdy, pdf.value, pdb.value, pdx.value)
+    G = np.where(y <= 0, 0.0, dy.astype(np.float64))
+    # db: full check
+    assert rel_err(db, G.sum(axis=(0, 2, 3))) <= TOL
+    # dW: all (oc, c, kh, kw) via per-tap batched contractions over the full batch
+    xp = np.zeros((B, C, H + 2, W + 2), np.float32)
+    xp[:, :, 1:-1, 1:-1] = x
+    dW_ref = np.empty(w.shape, np.float64)
+    Gf = G.transpose(1, 0, 2, 3).reshape(OC, -1)
+    for kh in range(k):
+        for kw in range(k):
+            xs = xp[:, :, kh:kh + H, kw:kw + W].transpose(1, 0, 2, 3).reshape(C, -1).astype(np.float64)
+            dW_ref[:, :, kh, kw] = Gf @ xs.T
+    assert rel_err(dW, dW_ref) <= TOL
+    # dX: 64 sampled (b, ih, iw) pixels, all channels:
+    # dX[b, c, ih, iw] = sum_{oc,kh,kw} W[oc, c, kh, kw] * G[b, oc, ih + 1 - kh, iw + 1 - kw]
+    Gp = np.zeros((B, OC, H + 2, W + 2))
+    Gp[:, :, 1:-1, 1:-1] = G
+    w64 = w.astype(np.float64)
+    ref_s, got_s = [], []
+    for _ in range(64):
+        bb, ih, iw = int(r.integers(B)), int(r.integers(H)), int(r.integers(W))
+        acc = np.zeros(C)
+        for kh in range(k):
+            for kw in range(k):
+                acc += w64[:, :, kh, kw].T @ Gp[bb, :, ih + 2 - kh, iw + 2 - kw]
+        ref_s.append(acc)
+        got_s.append(dX[bb, :, ih, iw])
+    assert rel_err(np.array(got_s), np.array(ref_s)) <= TOL
