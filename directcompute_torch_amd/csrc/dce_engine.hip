@@ -289,7 +289,7 @@ void* create_buffer(const float* data, uint32_t count) {
   }
   b->refCount = 1;
   b->magic = kMagicLive;
-  b->poolTag = 0;
+  b->tag = 0;
   if (data && !upload(b->ptr, data, count)) {
     b->magic = kMagicPooled;
     g_pool[count].push_back(b);
@@ -304,7 +304,7 @@ static void release_internal(Buffer* b) {
   uint64_t bytes = uint64_t(b->count) * 4;
   if (pool.size() < max_pool_for_size(b->count) && g_poolBytes + bytes <= g_poolCapBytes) {
     b->magic = kMagicPooled;
-    b->poolTag = 0;
+    b->tag = 0;
     pool.push_back(b);
     g_poolBytes += bytes;
   } else {
@@ -646,9 +646,31 @@ void* ConvForwardFused(void* x, void* filters, void* bias, uint32_t batch, uint3
   }
   void* out = create_buffer(nullptr, batch * outC * g.OH * g.OW);
   if (!out) return nullptr;
-  if (!conv_forward(X->ptr, Wt->ptr, Bi->ptr, static_cast<Buffer*>(out)->ptr, g, actType)) {
+  // The "im2col" handle of this backend is the channel-innermost copy of x
+  // that the forward builds anyway; ConvBackwardFused reuses and releases it.
+  void* keep = nullptr;
+  if (pIm2col) {
+    keep = create_buffer(nullptr, uint32_t(nhwc_floats(batch, inC, inH, inW)));
+    if (!keep) {
+      release_buffer(out);
+      return nullptr;
+    }
+  }
+  Buffer* K = static_cast<Buffer*>(keep);
+  if (!conv_forward(X->ptr, K ? K->ptr : nullptr, Wt->ptr, Bi->ptr,
+                    static_cast<Buffer*>(out)->ptr, g, actType)) {
     release_buffer(out);
+    release_buffer(keep);
     return nullptr;
+  }
+  if (K) {
+    K->tag = kNhwcTag;
+    K->meta[0] = batch;
+    K->meta[1] = inC;
+    K->meta[2] = inH;
+    K->meta[3] = inW;
+    K->meta[4] = pad4(inC);
+    *pIm2col = keep;
   }
   return out;
 }
@@ -677,33 +699,32 @@ void ConvBackwardFused(void* gradOut, void* fwdOut, void* x, void* filters, void
       set_error("ConvBackwardFused: buffer smaller than geometry");
     } else {
       const float* yp = Y ? Y->ptr : nullptr;
+      const float* xn = nullptr;
+      if (im2col) {
+        Buffer* Kb = static_cast<Buffer*>(im2col);
+        if (Kb->magic == kMagicLive && Kb->tag == kNhwcTag && Kb->meta[0] == batch &&
+            Kb->meta[1] == inC && Kb->meta[2] == inH && Kb->meta[3] == inW &&
+            Kb->meta[4] == pad4(inC) && Kb->count >= nhwc_floats(batch, inC, inH, inW))
+          xn = Kb->ptr;
+      }
       bool wantW = wReq && pDFilters, wantB = bReq && pDBias, wantX = xReq && pDInput;
       void* dW = wantW ? create_buffer(nullptr, outC * inC * kH * kW) : nullptr;
       void* dB = wantB ? create_buffer(nullptr, outC) : nullptr;
-      if ((wantW && !dW) || (wantB && !dB)) {
+      void* dX = wantX ? create_buffer(nullptr, batch * inC * inH * inW) : nullptr;
+      bool good = (!wantW || dW) && (!wantB || dB) && (!wantX || dX);
+      if (good && (wantW || wantB || wantX))
+        good = conv_backward(DY->ptr, yp, X->ptr, xn, Wt->ptr,
+                             dW ? static_cast<Buffer*>(dW)->ptr : nullptr,
+                             dB ? static_cast<Buffer*>(dB)->ptr : nullptr,
+                             dX ? static_cast<Buffer*>(dX)->ptr : nullptr, g);
+      if (good) {
+        if (pDFilters) *pDFilters = dW;
+        if (pDBias) *pDBias = dB;
+        if (pDInput) *pDInput = dX;
+      } else {
         release_buffer(dW);
         release_buffer(dB);
-      } else {
-        bool good = true;
-        if (wantW || wantB)
-          good = conv_backward_filter(DY->ptr, yp, X->ptr,
-                                      dW ? static_cast<Buffer*>(dW)->ptr : nullptr,
-                                      dB ? static_cast<Buffer*>(dB)->ptr : nullptr, g);
-        void* dX = nullptr;
-        if (good && wantX) {
-          dX = create_buffer(nullptr, batch * inC * inH * inW);
-          good = dX && conv_backward_input(DY->ptr, yp, Wt->ptr,
-                                           static_cast<Buffer*>(dX)->ptr, g);
-        }
-        if (good) {
-          if (pDFilters) *pDFilters = dW;
-          if (pDBias) *pDBias = dB;
-          if (pDInput) *pDInput = dX;
-        } else {
-          release_buffer(dW);
-          release_buffer(dB);
-          release_buffer(dX);
-        }
+        release_buffer(dX);
       }
     }
   }
@@ -743,11 +764,11 @@ void* MaxPoolForwardFused(void* x, uint32_t batch, uint32_t inC, uint32_t inH, u
     release_buffer(idx);
     return nullptr;
   }
-  I->poolTag = kPoolTag;
-  I->poolH = inH;
-  I->poolW = inW;
-  I->poolK = poolSize;
-  I->poolS = stride;
+  I->tag = kPoolTag;
+  I->meta[0] = inH;
+  I->meta[1] = inW;
+  I->meta[2] = poolSize;
+  I->meta[3] = stride;
   if (pIndices)
     *pIndices = idx;
   else
@@ -768,10 +789,10 @@ void* MaxPoolBackwardFused(void* gradOut, void* indices, uint32_t batch, uint32_
     dx = create_buffer(nullptr, xSize);
     if (dx) {
       uint32_t H = 0, W = 0, k = 0, s = 0;
-      if (I->poolTag == kPoolTag && uint64_t(batch) * inC * I->poolH * I->poolW == xSize &&
-          (I->poolH - I->poolK) / I->poolS + 1 == outH &&
-          (I->poolW - I->poolK) / I->poolS + 1 == outW) {
-        H = I->poolH; W = I->poolW; k = I->poolK; s = I->poolS;
+      const uint32_t* m = I->meta;
+      if (I->tag == kPoolTag && uint64_t(batch) * inC * m[0] * m[1] == xSize &&
+          (m[0] - m[2]) / m[3] + 1 == outH && (m[1] - m[2]) / m[3] + 1 == outW) {
+        H = m[0]; W = m[1]; k = m[2]; s = m[3];
       }
       if (!maxpool_backward(DZ->ptr, I->ptr, static_cast<Buffer*>(dx)->ptr, batch, inC, outH,
                             outW, xSize, H, W, k, s)) {

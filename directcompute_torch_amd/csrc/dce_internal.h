@@ -20,12 +20,16 @@ struct Buffer {
   uint32_t count;     // element count in floats (the reference's u32 size)
   int refCount;
   uint32_t magic;
-  // Pooling geometry recorded by MaxPoolForwardFused on the indices buffer it
-  // returns, so the backward can run as a deterministic gather.  tag == 0
-  // means "no geometry known".
-  uint32_t poolTag, poolH, poolW, poolK, poolS;
+  // Producer metadata, reset whenever the buffer is handed out again:
+  //  kPoolTag: indices of MaxPoolForwardFused, meta = {H, W, k, s}, so the
+  //            backward can run as a deterministic gather;
+  //  kNhwcTag: channel-innermost copy of a conv input kept by
+  //            ConvForwardFused as its "im2col" handle, meta = {B, C, H, W, Cp}.
+  uint32_t tag;
+  uint32_t meta[5];
 };
 constexpr uint32_t kPoolTag = 0x9001u;
+constexpr uint32_t kNhwcTag = 0x9002u;
 
 // A bounds-carrying view used by the RunShader-compatible kernels: reads past
 // `n` return 0 and writes past `n` are dropped, like D3D11 structured buffers.
@@ -72,16 +76,24 @@ struct ConvGeom {
   uint32_t B, C, H, W, OC, k, s, p, OH, OW;
 };
 
+inline uint32_t pad4(uint32_t c) { return (c + 3u) & ~3u; }
+
 // Implicit-GEMM MFMA launchers (dce_igemm.hip).  All pointers are device
 // pointers with at least the extents implied by the geometry.
-bool conv_forward(const float* x, const float* w, const float* bias, float* y,
-                  const ConvGeom& g, uint32_t act);
-// dW[OC, C*k*k] and (optionally) db[OC] from G = mask(dy, y).  `y` may be
-// null (no mask).  dw or db may be null when not requested.
-bool conv_backward_filter(const float* dy, const float* y, const float* x,
-                          float* dw, float* db, const ConvGeom& g);
-bool conv_backward_input(const float* dy, const float* y, const float* w,
-                         float* dx, const ConvGeom& g);
+//
+// Channel-innermost ("NHWC") copy of an NCHW activation with the channel
+// count padded to pad4(C) (zeros): out[((b*H + h)*W + w)*Cp + c].
+size_t nhwc_floats(uint32_t B, uint32_t C, uint32_t H, uint32_t W);
+bool to_nhwc(const float* x, float* out, uint32_t B, uint32_t C, uint32_t H, uint32_t W);
+// y = act(conv(x, w) + bias) in NCHW.  x_nhwc_keep, when not null, receives
+// the NHWC copy of x (nhwc_floats(B, C, H, W)) for a later backward.
+bool conv_forward(const float* x, float* x_nhwc_keep, const float* w, const float* bias,
+                  float* y, const ConvGeom& g, uint32_t act);
+// dW[OC, C, k, k], db[OC], dX (NCHW) from G = dy masked by y (> 0 kept; y may
+// be null: no mask).  Any of dw, db, dx may be null (not requested).
+// x_nhwc, when not null, is the NHWC copy produced by conv_forward.
+bool conv_backward(const float* dy, const float* y, const float* x, const float* x_nhwc,
+                   const float* w, float* dw, float* db, float* dx, const ConvGeom& g);
 // C[M,N] = op(A)·op(B); flags bit0: A stored K×M, bit1: B stored N×K.
 bool gemm(const float* a, const float* b, float* c, uint32_t M, uint32_t K,
           uint32_t N, uint32_t flags);
