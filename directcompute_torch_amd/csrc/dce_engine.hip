@@ -252,6 +252,34 @@ static bool upload(float* dst, const float* src, size_t n) {
   return true;
 }
 
+// A fresh device allocation (never from the pool), refcount 1.
+static Buffer* alloc_record(uint32_t count) {
+  float* p = nullptr;
+  const size_t bytes = size_t(count) * 4;
+  if (hipMalloc((void**)&p, bytes) != hipSuccess) {
+    hipGetLastError();
+    drain_pool_locked();
+    if (hipMalloc((void**)&p, bytes) != hipSuccess) {
+      hipGetLastError();
+      set_error("CreateBuffer: out of device memory for %u floats", count);
+      return nullptr;
+    }
+  }
+  Buffer* b = nullptr;
+  if (!g_recycled.empty()) {
+    b = g_recycled.back();
+    g_recycled.pop_back();
+  } else {
+    b = new Buffer();
+  }
+  b->ptr = p;
+  b->count = count;
+  b->refCount = 1;
+  b->magic = kMagicLive;
+  b->tag = 0;
+  return b;
+}
+
 void* create_buffer(const float* data, uint32_t count) {
   if (!ensure_init()) return nullptr;
   if (count == 0) {
@@ -265,31 +293,14 @@ void* create_buffer(const float* data, uint32_t count) {
     it->second.pop_back();
     g_poolBytes -= uint64_t(count) * 4;
     g_poolHits++;
+    b->refCount = 1;
+    b->magic = kMagicLive;
+    b->tag = 0;
   } else {
     g_poolMisses++;
-    float* p = nullptr;
-    size_t bytes = size_t(count) * 4;
-    if (hipMalloc((void**)&p, bytes) != hipSuccess) {
-      hipGetLastError();
-      drain_pool_locked();
-      if (hipMalloc((void**)&p, bytes) != hipSuccess) {
-        hipGetLastError();
-        set_error("CreateBuffer: out of device memory for %u floats", count);
-        return nullptr;
-      }
-    }
-    if (!g_recycled.empty()) {
-      b = g_recycled.back();
-      g_recycled.pop_back();
-    } else {
-      b = new Buffer();
-    }
-    b->ptr = p;
-    b->count = count;
+    b = alloc_record(count);
+    if (!b) return nullptr;
   }
-  b->refCount = 1;
-  b->magic = kMagicLive;
-  b->tag = 0;
   if (data && !upload(b->ptr, data, count)) {
     b->magic = kMagicPooled;
     g_pool[count].push_back(b);
@@ -472,18 +483,15 @@ void SyncGPU(void) {
 void WarmPool(uint32_t* sizes, uint32_t numSizes, uint32_t copies) {
   if (!g_init || !sizes) return;
   for (uint32_t i = 0; i < numSizes; ++i) {
-    uint32_t count = sizes[i];
+    const uint32_t count = sizes[i];
     if (!count) continue;
-    size_t target = std::min<size_t>(copies, max_pool_for_size(count));
-    auto& pool = g_pool[count];
-    while (pool.size() < target) {
-      uint64_t misses = g_poolMisses;
-      Buffer* b = static_cast<Buffer*>(create_buffer(nullptr, count));
-      g_poolMisses = misses;  // warm-up allocations are not misses
+    const size_t target = std::min<size_t>(copies, max_pool_for_size(count));
+    size_t have = g_pool[count].size();
+    for (; have < target; ++have) {
+      Buffer* b = alloc_record(count);  // fresh allocations: not pool hits or misses
       if (!b) break;
-      size_t before = pool.size();
       release_internal(b);
-      if (pool.size() == before) break;  // pool byte cap reached
+      if (g_pool[count].size() <= have) break;  // pool byte cap reached (b was freed)
     }
   }
 }

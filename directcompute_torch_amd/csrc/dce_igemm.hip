@@ -508,8 +508,8 @@ __global__ void __launch_bounds__(kThreads)
 // filter re-layouts, split-K sums.
 // ---------------------------------------------------------------------------
 // out[((b*HW) + p)*Cp + c] = (c < C) ? in[(b*C + c)*HW + p] masked : 0.
-// Block: 32 channels x 64 pixels through LDS.  dbPart (per block of 64
-// pixels): the masked values summed over the block's pixels per channel.
+// Block: 32 channels x 64 pixels through LDS.  dbPart[c][b*npb + block]: the
+// masked values of channel c summed over the block's 64 pixels.
 __global__ void __launch_bounds__(256)
     k_to_nhwc(const float* __restrict__ in, const float* __restrict__ y, float* __restrict__ out,
               float* __restrict__ dbPart, uint32_t C, uint32_t HW, uint32_t Cp, uint32_t npb) {
@@ -539,7 +539,8 @@ __global__ void __launch_bounds__(256)
     s += __shfl_xor(s, 1, 64);
     s += __shfl_xor(s, 2, 64);
     s += __shfl_xor(s, 4, 64);
-    if (part == 0 && c0 + cl < C) dbPart[(size_t(b) * npb + blockIdx.x) * C + c0 + cl] = s;
+    if (part == 0 && c0 + cl < C)
+      dbPart[size_t(c0 + cl) * gridDim.z * npb + size_t(b) * npb + blockIdx.x] = s;
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -560,14 +561,20 @@ __global__ void k_to_nhwc_small(const float* __restrict__ in, float* __restrict_
   out[i] = c < C ? in[(size_t(b) * C + c) * HW + p] : 0.f;
 }
 
-// db[c] = sum over partial rows, in row order.
-__global__ void k_colsum(const float* __restrict__ part, float* __restrict__ out, uint32_t rows,
-                         uint32_t C) {
-  const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= C) return;
+// out[c] = sum of the `rows` partials of channel c (stored contiguously,
+// part[c*rows + r]): 256 strided per-thread sums, then a fixed tree.
+__global__ void __launch_bounds__(256)
+    k_rowsum(const float* __restrict__ part, float* __restrict__ out, uint32_t rows) {
+  __shared__ float sh[4];
+  const uint32_t c = blockIdx.x;
+  const float* p = part + size_t(c) * rows;
   float s = 0.f;
-  for (uint32_t r = 0; r < rows; ++r) s += part[size_t(r) * C + c];
-  out[c] = s;
+  for (uint32_t r = threadIdx.x; r < rows; r += 256) s += p[r];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_down(s, o, 64);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) out[c] = (sh[0] + sh[1]) + (sh[2] + sh[3]);
 }
 
 // mode 0 (forward A): out[oc][khw*Cp + c]  = c < C  ? w[oc][c][khw] : 0   (size OC*KK*Cp)
@@ -864,8 +871,7 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
   uint32_t npbGot = npb;
   if (!to_nhwc_masked(dy, y, gn, dbPart, g.B, g.OC, OHW, &npbGot)) return false;
   if (db) {
-    hipLaunchKernelGGL(k_colsum, dim3(cdiv(g.OC, 256)), dim3(256), 0, stream(), dbPart, db,
-                       g.B * npb, g.OC);
+    hipLaunchKernelGGL(k_rowsum, dim3(g.OC), dim3(256), 0, stream(), dbPart, db, g.B * npb);
     if (!check_launch("bias_grad")) return false;
   }
   if (dw) {

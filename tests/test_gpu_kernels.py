@@ -1,0 +1,536 @@
+"""GPU parity of the memory-bound kernels (RunShader registry and fused entry
+points) against the float64 oracle, plus the buffer API and the D3D11
+out-of-bounds rules the reference relies on."""
+import ctypes
+import struct
+
+import numpy as np
+import pytest
+
+from oracle import kernels as K
+from tests.helpers import TOL, download, rel_err, release, rng, upload
+
+pytestmark = pytest.mark.gpu
+
+
+def fbits(f):
+    return struct.unpack("I", struct.pack("f", f))[0]
+
+
+def run(eng, name, srvs, uavs, *cb):
+    """RunShader with the constant-buffer words given as ints."""
+    ns, nu = len(srvs), len(uavs)
+    sa = (ctypes.c_void_p * max(ns, 1))(*srvs)
+    ua = (ctypes.c_void_p * max(nu, 1))(*uavs)
+    th = (ctypes.c_uint * 3)(1, 1, 1)
+    if cb:
+        cba = (ctypes.c_uint * len(cb))(*cb)
+        eng.lib.RunShader(name.encode(), sa, ns, ua, nu, th, ctypes.cast(cba, ctypes.c_void_p), 4 * len(cb))
+    else:
+        eng.lib.RunShader(name.encode(), sa, ns, ua, nu, th, None, 0)
+
+
+def new(eng, n):
+    h = eng.lib.CreateBuffer(None, n)
+    assert h, eng.last_error()
+    return h
+
+
+# ----------------------------------------------------------------- buffers
+def test_buffer_roundtrip_update_clear(eng):
+    for n in (1, 7, 256, 257, 100003, 5_000_000):
+        a = rng(n).standard_normal(n).astype(np.float32)
+        h = upload(eng, a)
+        assert np.array_equal(download(eng, h, (n,)), a)
+        b = rng(n + 1).standard_normal(n).astype(np.float32)
+        eng.lib.UpdateBuffer(h, b.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+        assert np.array_equal(download(eng, h, (n,)), b)
+        eng.lib.ClearBuffer(h)
+        assert not download(eng, h, (n,)).any()
+        release(eng, h)
+
+
+def test_refcount_pool_and_errors(eng):
+    lib = eng.lib
+    assert lib.CreateBuffer(None, 0) is None          # zero-size: NULL + error
+    assert "zero-size" in eng.last_error()
+    h = new(eng, 1000)
+    lib.AddRefBuffer(h)
+    lib.ReleaseBuffer(h)                               # still referenced
+    lib.ClearBuffer(h)
+    lib.ReleaseBuffer(h)                               # back to the pool
+    lib.ClearLastError()
+    lib.ReleaseBuffer(h)                               # double release: rejected, no crash
+    assert "not live" in eng.last_error()
+    lib.ResetPoolStats()
+    h2 = new(eng, 1000)                                # pool hit (same size)
+    hits, misses = eng.get_pool_stats()
+    assert hits >= 1
+    arr = (ctypes.c_void_p * 2)(h2, None)
+    lib.ReleaseBufferBatch(arr, 2)                     # NULL entries skipped
+    sizes = (ctypes.c_uint * 2)(12345, 777)
+    lib.WarmPool(sizes, 2, 3)
+    assert lib.GetPoolMemory() >= (12345 + 777) * 4 * 3
+    lib.DrainPool()
+    assert lib.GetPoolMemory() == 0
+
+
+def test_gpu_info(eng):
+    info = eng.GPUInfo()
+    eng.lib.GetGPUInfo(ctypes.byref(info))
+    assert info.vendorId == 0x1002 and info.isIntegrated == 0
+    assert info.dedicatedVRAM > (64 << 30)
+    assert b"gfx950" in info.description
+
+
+def test_unknown_shader_is_noop_with_error(eng):
+    h = upload(eng, np.ones(4, np.float32))
+    eng.lib.ClearLastError()
+    run(eng, "gelu", [h], [h], 4)
+    assert "unknown kernel" in eng.last_error()
+    assert np.array_equal(download(eng, h, (4,)), np.ones(4, np.float32))
+    release(eng, h)
+
+
+# ------------------------------------------------------------ elementwise
+UNARY = [
+    ("relu", lambda x: K.relu(x), False),
+    ("relu6", lambda x: K.relu6(x), True),
+    ("sigmoid", lambda x: K.sigmoid(x), True),
+]
+BINARY = [
+    ("relu_grad", K.relu_grad),
+    ("relu6_grad", K.relu6_grad),
+    ("sigmoid_grad", K.sigmoid_grad),
+]
+
+
+@pytest.mark.parametrize("n", [1, 5, 1024, 1000003])
+def test_activations(eng, n):
+    r = rng(n)
+    x = (4 * r.standard_normal(n)).astype(np.float32)
+    x[: min(n, 3)] = [0.0, 6.0, -0.0][: min(n, 3)]
+    g = r.standard_normal(n).astype(np.float32)
+    hx, hg = upload(eng, x), upload(eng, g)
+    for name, fn, has_cb in UNARY:
+        ho = new(eng, n)
+        run(eng, name, [hx], [ho], *([n] if has_cb else []))
+        assert rel_err(download(eng, ho, (n,)), fn(x)) <= 1e-6, name
+        release(eng, ho)
+    for name, fn in BINARY:
+        ho = new(eng, n)
+        run(eng, name, [hg, hx], [ho], n)
+        assert rel_err(download(eng, ho, (n,)), fn(g, x)) <= 1e-6, name
+        release(eng, ho)
+    for alpha in (0.1, 0.01):
+        ho = new(eng, n)
+        run(eng, "leaky_relu", [hx], [ho], n, fbits(alpha))
+        assert rel_err(download(eng, ho, (n,)), K.leaky_relu(x, alpha)) <= 1e-6
+        run(eng, "leaky_relu_grad", [hg, hx], [ho], n, fbits(alpha))
+        assert rel_err(download(eng, ho, (n,)), K.leaky_relu_grad(g, x, alpha)) <= 1e-6
+        release(eng, ho)
+    ho = new(eng, n)
+    run(eng, "add", [hx, hg], [ho], n, 1)
+    assert rel_err(download(eng, ho, (n,)), x.astype(np.float64) + g) <= 1e-6
+    run(eng, "scale_add", [hx, hg], [ho], n, fbits(1.5), fbits(-0.5))
+    assert rel_err(download(eng, ho, (n,)), 1.5 * x.astype(np.float64) - 0.5 * g) <= 1e-6
+    acc = upload(eng, x)
+    run(eng, "grad_accum", [hg], [acc], n)
+    assert rel_err(download(eng, acc, (n,)), K.grad_accum(x, g)) <= 1e-6
+    release(eng, hx, hg, ho, acc)
+
+
+def test_out_of_bounds_reads_zero_writes_dropped(eng):
+    """D3D11 structured-buffer rules: count larger than the buffers reads 0 and
+    drops writes beyond the output (nn_relu.hlsl relies on it)."""
+    g = np.arange(1, 11, dtype=np.float32)
+    x = np.ones(6, np.float32)
+    hg, hx = upload(eng, g), upload(eng, x)
+    ho = upload(eng, np.full(8, 7.0, np.float32))
+    run(eng, "relu_grad", [hg, hx], [ho], 100)
+    out = download(eng, ho, (8,))
+    assert np.array_equal(out, np.array([1, 2, 3, 4, 5, 6, 0, 0], np.float32))
+    run(eng, "relu", [hg], [ho])            # no constants: bounded by the output
+    assert np.array_equal(download(eng, ho, (8,)), g[:8])
+    release(eng, hg, hx, ho)
+
+
+@pytest.mark.parametrize("M,N", [(1, 1), (128, 4096), (7, 13), (64, 10)])
+def test_bias_ops(eng, M, N):
+    r = rng(M * N)
+    A = r.standard_normal((M, N)).astype(np.float32)
+    b = r.standard_normal(N).astype(np.float32)
+    hA, hb, ho = upload(eng, A), upload(eng, b), new(eng, M * N)
+    run(eng, "add_bias", [hA, hb], [ho], M, N)
+    assert rel_err(download(eng, ho, (M, N)), K.add_bias(A, b)) <= 1e-6
+    run(eng, "bias_relu", [hA, hb], [ho], M, N)
+    assert rel_err(download(eng, ho, (M, N)), K.bias_relu(A, b)) <= 1e-6
+    hg = new(eng, N)
+    run(eng, "bias_grad", [hA], [hg], M, N, N, 1)          # linear layout
+    assert rel_err(download(eng, hg, (N,)), K.bias_grad(A, M, N, N, 1)) <= TOL
+    hg2 = new(eng, M)
+    run(eng, "bias_grad", [hA], [hg2], N, M, 1, N)         # conv layout (rows contiguous)
+    assert rel_err(download(eng, hg2, (M,)), K.bias_grad(A, N, M, 1, N)) <= TOL
+    release(eng, hA, hb, ho, hg, hg2)
+
+
+# ----------------------------------------------------------------- maxpool
+POOL_CASES = [(2, 3, 8, 8, 2, 2), (2, 4, 55, 55, 3, 2), (1, 2, 27, 27, 3, 2), (3, 5, 13, 11, 3, 2),
+              (2, 3, 9, 9, 3, 1), (1, 6, 24, 24, 2, 2), (2, 2, 7, 10, 2, 3)]
+
+
+@pytest.mark.parametrize("B,C,H,W,k,s", POOL_CASES)
+def test_maxpool_fused(eng, B, C, H, W, k, s):
+    r = rng(B * C * H * W + k)
+    x = r.standard_normal((B, C, H, W)).astype(np.float32)
+    x.flat[::17] = 0.5              # ties: first candidate in scan order wins
+    x.flat[5::97] = np.nan          # NaN is never selected (strict '>')
+    x.flat[0] = -np.inf
+    hx = upload(eng, x)
+    pidx = ctypes.c_void_p()
+    ho = eng.lib.MaxPoolForwardFused(hx, B, C, H, W, k, s, ctypes.byref(pidx))
+    assert ho, eng.last_error()
+    OH, OW = (H - k) // s + 1, (W - k) // s + 1
+    out = download(eng, ho, (B, C, OH, OW))
+    idx = download(eng, pidx.value, (B, C, OH, OW)).view(np.uint32)
+    ref_out, ref_idx = K.maxpool_forward(x, k, s)
+    assert np.array_equal(idx, ref_idx)                      # bit-exact routing
+    assert np.array_equal(out, ref_out.astype(np.float32))
+    dz = r.standard_normal((B, C, OH, OW)).astype(np.float32)
+    hdz = upload(eng, dz)
+    hdx = eng.lib.MaxPoolBackwardFused(hdz, pidx.value, B, C, OH, OW, x.size)
+    assert hdx, eng.last_error()
+    dx = download(eng, hdx, x.shape)
+    ref_dx = K.maxpool_backward(dz, ref_idx, x.size).reshape(x.shape)
+    if k <= s:
+        assert np.array_equal(dx, ref_dx.astype(np.float32))  # disjoint windows: exact
+    else:
+        assert rel_err(dx, ref_dx) <= 1e-6
+    release(eng, hx, ho, hdz, hdx)
+
+
+def test_maxpool_raw_shaders(eng):
+    B, C, H, W, k, s = 2, 3, 8, 8, 2, 2
+    x = rng(3).standard_normal((B, C, H, W)).astype(np.float32)
+    OH = OW = 4
+    hx, ho, hi = upload(eng, x), new(eng, B * C * 16), new(eng, B * C * 16)
+    run(eng, "maxpool_forward", [hx], [ho, hi], B, C, H, W, k, s, OH, OW)
+    ref_out, ref_idx = K.maxpool_forward(x, k, s)
+    assert np.array_equal(download(eng, hi, (B, C, OH, OW)).view(np.uint32), ref_idx)
+    dz = rng(4).standard_normal((B, C, OH, OW)).astype(np.float32)
+    hdz, hdx = upload(eng, dz), new(eng, x.size)
+    eng.lib.ClearBuffer(hdx)
+    run(eng, "maxpool_backward", [hdz, hi], [hdx], B, C, OH, OW)
+    assert np.array_equal(download(eng, hdx, x.shape), K.maxpool_backward(dz, ref_idx, x.size).reshape(x.shape).astype(np.float32))
+    release(eng, hx, ho, hi, hdz, hdx)
+
+
+# ---------------------------------------------------------------- batchnorm
+@pytest.mark.parametrize("N,C,H,W", [(2, 3, 5, 5), (8, 16, 32, 32), (4, 96, 28, 28), (64, 6, 12, 12), (1, 1, 1, 7)])
+def test_batchnorm(eng, N, C, H, W):
+    r = rng(N * C * H * W)
+    x = (r.standard_normal((N, C, H, W)) * 2 + 0.5).astype(np.float32)
+    gamma = (1 + 0.1 * r.standard_normal(C)).astype(np.float32)
+    beta = (0.1 * r.standard_normal(C)).astype(np.float32)
+    rm = (0.1 * r.standard_normal(C)).astype(np.float32)
+    rv = (1 + 0.1 * r.random(C)).astype(np.float32)
+    dy = r.standard_normal(x.shape).astype(np.float32)
+    eps, mom = 1e-5, 0.1
+    S = H * W
+    hx, hg, hb, hrm, hrv, hdy = (upload(eng, a) for a in (x, gamma, beta, rm, rv, dy))
+    hmu, hvar = new(eng, C), new(eng, C)
+    run(eng, "batchnorm_mean_var", [hx], [hmu, hvar, hrm, hrv], N, C, S, 1, fbits(mom))
+    mu_r, var_r, rm_r, rv_r = K.batchnorm_mean_var(x, rm, rv, mom, True)
+    mu, var = download(eng, hmu, (C,)), download(eng, hvar, (C,))
+    assert rel_err(mu, mu_r) <= 1e-5 and rel_err(var, var_r) <= 1e-5
+    assert rel_err(download(eng, hrm, (C,)), rm_r) <= 1e-5
+    assert rel_err(download(eng, hrv, (C,)), rv_r) <= 1e-5
+    hy = new(eng, x.size)
+    run(eng, "batchnorm_forward", [hx, hmu, hvar, hg, hb], [hy], N, C, S, fbits(eps))
+    assert rel_err(download(eng, hy, x.shape), K.batchnorm_forward(x, mu, var, gamma, beta, eps)) <= 1e-5
+    hdg, hdb = new(eng, C), new(eng, C)
+    run(eng, "batchnorm_backward_reduce", [hx, hdy, hmu, hvar], [hdg, hdb], N, C, S, fbits(eps))
+    dg_r, db_r = K.batchnorm_backward_reduce(x, dy, mu, var, eps)
+    dg, db = download(eng, hdg, (C,)), download(eng, hdb, (C,))
+    assert rel_err(dg, dg_r) <= TOL and rel_err(db, db_r) <= TOL
+    hdx = new(eng, x.size)
+    run(eng, "batchnorm_backward_dx", [hx, hdy, hmu, hvar, hg, hdg, hdb], [hdx], N, C, S, fbits(eps))
+    dx_r = K.batchnorm_backward_dx(x, dy, mu, var, gamma, dg, db, eps)
+    assert rel_err(download(eng, hdx, x.shape), dx_r) <= TOL
+    release(eng, hx, hg, hb, hrm, hrv, hdy, hmu, hvar, hy, hdg, hdb, hdx)
+
+
+# --------------------------------------------------- pooling / resampling
+@pytest.mark.parametrize("B,C,H,W", [(2, 3, 7, 7), (8, 64, 8, 8), (1, 1, 1, 1)])
+def test_global_avg_pool(eng, B, C, H, W):
+    x = rng(B + C).standard_normal((B, C, H, W)).astype(np.float32)
+    g = rng(7).standard_normal((B, C)).astype(np.float32)
+    hx, ho, hg, hdx = upload(eng, x), new(eng, B * C), upload(eng, g), new(eng, x.size)
+    run(eng, "global_avg_pool", [hx], [ho], B, C, H * W)
+    assert rel_err(download(eng, ho, (B, C)), K.global_avg_pool(x)) <= 1e-6
+    run(eng, "global_avg_pool_backward", [hg], [hdx], B, C, H * W)
+    assert rel_err(download(eng, hdx, x.shape), K.global_avg_pool_backward(g, x.shape)) <= 1e-6
+    release(eng, hx, ho, hg, hdx)
+
+
+@pytest.mark.parametrize("B,C,H,W,sH,sW", [(2, 3, 4, 5, 2, 2), (1, 16, 32, 32, 2, 2), (2, 2, 3, 3, 3, 2)])
+def test_upsample(eng, B, C, H, W, sH, sW):
+    x = rng(H * W).standard_normal((B, C, H, W)).astype(np.float32)
+    OH, OW = H * sH, W * sW
+    dy = rng(5).standard_normal((B, C, OH, OW)).astype(np.float32)
+    hx, hy, hdy, hdx = upload(eng, x), new(eng, B * C * OH * OW), upload(eng, dy), new(eng, x.size)
+    run(eng, "upsample", [hx], [hy], B, C, H, W, OH, OW, sH, sW)
+    assert np.array_equal(download(eng, hy, dy.shape), K.upsample(x, sH, sW).astype(np.float32))
+    run(eng, "upsample_backward", [hdy], [hdx], B, C, H, W, OH, OW, sH, sW)
+    assert rel_err(download(eng, hdx, x.shape), K.upsample_backward(dy, x.shape, sH, sW)) <= 1e-6
+    release(eng, hx, hy, hdy, hdx)
+
+
+def test_concat_slice(eng):
+    B, S = 2, 20
+    a = rng(1).standard_normal((B, 3, 4, 5)).astype(np.float32)
+    b = rng(2).standard_normal((B, 5, 4, 5)).astype(np.float32)
+    ha, hb, ho = upload(eng, a), upload(eng, b), new(eng, B * 8 * S)
+    run(eng, "concat_insert", [ha], [ho], B, 3, S, 8, 0)
+    run(eng, "concat_insert", [hb], [ho], B, 5, S, 8, 3)
+    cat = download(eng, ho, (B, 8, 4, 5))
+    assert np.array_equal(cat, K.concat([a, b]).astype(np.float32))
+    hs = new(eng, B * 5 * S)
+    run(eng, "slice", [ho], [hs], B, 5, S, 8, 3)
+    assert np.array_equal(download(eng, hs, b.shape), b)
+    release(eng, ha, hb, ho, hs)
+
+
+# ---------------------------------------------------------------- depthwise
+@pytest.mark.parametrize("B,C,H,W,k,s,p", [(2, 8, 9, 9, 3, 1, 1), (2, 6, 10, 12, 3, 2, 1), (1, 4, 7, 7, 5, 1, 2), (4, 96, 28, 28, 3, 2, 1)])
+def test_depthwise(eng, B, C, H, W, k, s, p):
+    r = rng(B * C * H + k + s)
+    x = r.standard_normal((B, C, H, W)).astype(np.float32)
+    f = r.standard_normal((C, 1, k, k)).astype(np.float32)
+    b = r.standard_normal(C).astype(np.float32)
+    OH, OW = (H + 2 * p - k) // s + 1, (W + 2 * p - k) // s + 1
+    dy = r.standard_normal((B, C, OH, OW)).astype(np.float32)
+    hx, hf, hb, hdy = upload(eng, x), upload(eng, f), upload(eng, b), upload(eng, dy)
+    hy, hdx, hdf, hdb = new(eng, dy.size), new(eng, x.size), new(eng, f.size), new(eng, C)
+    cb = (B, C, H, W, k, k, s, p, OH)
+    run(eng, "depthwise_conv_forward", [hx, hf, hb], [hy], *cb)
+    assert rel_err(download(eng, hy, dy.shape), K.depthwise_forward(x, f, b, s, p)) <= 1e-5
+    run(eng, "depthwise_conv_backward_input", [hdy, hf], [hdx], *cb)
+    assert rel_err(download(eng, hdx, x.shape), K.depthwise_backward_input(dy, f, x.shape, s, p)) <= TOL
+    run(eng, "depthwise_conv_backward_filter", [hdy, hx], [hdf, hdb], *cb)
+    df_r, db_r = K.depthwise_backward_filter(dy, x, k, k, s, p)
+    assert rel_err(download(eng, hdf, f.shape), df_r) <= TOL
+    assert rel_err(download(eng, hdb, (C,)), db_r) <= TOL
+    release(eng, hx, hf, hb, hdy, hy, hdx, hdf, hdb)
+
+
+# ------------------------------------------------------------ loss / metrics
+@pytest.mark.parametrize("B,Kc", [(1, 2), (64, 10), (128, 1000), (300, 7)])
+def test_softmax_ce(eng, B, Kc):
+    r = rng(B * Kc)
+    z = (3 * r.standard_normal((B, Kc))).astype(np.float32)
+    lab = r.integers(0, Kc, B).astype(np.float32)
+    hz, hl = upload(eng, z), upload(eng, lab)
+    hp, hloss, hg = new(eng, B * Kc), new(eng, 1), new(eng, B * Kc)
+    run(eng, "softmax", [hz], [hp], B, Kc)
+    p = download(eng, hp, (B, Kc))
+    assert rel_err(p, K.softmax(z)) <= 1e-5
+    run(eng, "loss", [hz, hl], [hloss], B, Kc)
+    assert abs(download(eng, hloss, (1,))[0] - K.ce_loss(z, lab)) <= 1e-5 * max(1, K.ce_loss(z, lab))
+    run(eng, "softmax_ce_grad", [hp, hl], [hg], B, Kc)
+    assert rel_err(download(eng, hg, (B, Kc)), K.softmax_ce_grad(p, lab)) <= 1e-5
+    hc = new(eng, 1)
+    eng.lib.ClearBuffer(hc)
+    z[0, :] = 1.0  # all-equal row: first column wins
+    hz2 = upload(eng, z)
+    run(eng, "argmax_correct", [hz2, hl], [hc], B, Kc)
+    run(eng, "argmax_correct", [hz2, hl], [hc], B, Kc)
+    cnt = download(eng, hc, (1,)).view(np.uint32)[0]
+    assert cnt == 2 * K.argmax_correct(z, lab)                 # bit-exact count
+    acc = upload(eng, np.array([1.5], np.float32))
+    run(eng, "accumulate_scalar", [hloss], [acc])
+    assert abs(download(eng, acc, (1,))[0] - (1.5 + download(eng, hloss, (1,))[0])) < 1e-6
+    release(eng, hz, hl, hp, hloss, hg, hc, hz2, acc)
+
+
+@pytest.mark.parametrize("B,C,H,W", [(2, 1, 16, 16), (8, 1, 64, 64), (3, 2, 5, 7)])
+def test_dice(eng, B, C, H, W):
+    r = rng(B * H)
+    p = r.random((B, C, H, W)).astype(np.float32)
+    t = (r.random((B, C, H, W)) < 0.3).astype(np.float32)
+    size = C * H * W
+    hp, ht = upload(eng, p), upload(eng, t)
+    hl, hs, hg = new(eng, B), new(eng, 3 * B), new(eng, p.size)
+    run(eng, "dice_loss", [hp, ht], [hl], B, size)
+    assert rel_err(download(eng, hl, (B,)), K.dice_loss(p, t)) <= 1e-5
+    run(eng, "dice_loss_sums", [hp, ht], [hs], B, size)
+    assert rel_err(download(eng, hs, (B, 3)), K.dice_sums(p, t)) <= 1e-5
+    run(eng, "dice_loss_grad", [hp, ht, hs], [hg], B, size)
+    assert rel_err(download(eng, hg, p.shape), K.dice_loss_grad(p, t)) <= TOL
+    release(eng, hp, ht, hl, hs, hg)
+
+
+# ---------------------------------------------------------------- optimisers
+def _param_set(seed, sizes):
+    r = rng(seed)
+    return ([r.standard_normal(n).astype(np.float32) for n in sizes],
+            [(2 * r.standard_normal(n)).astype(np.float32) for n in sizes])
+
+
+SIZES = [1, 3, 4, 5, 4095, 4096, 4097, 100000, 9216 * 40]
+
+
+def _arrays(hs):
+    return (ctypes.c_void_p * len(hs))(*hs)
+
+
+def test_sgd_batch(eng):
+    ws, gs = _param_set(1, SIZES)
+    hw, hg = [upload(eng, w) for w in ws], [upload(eng, g) for g in gs]
+    pa, ga = _arrays(hw + [None]), _arrays(hg + [hg[0]])     # trailing NULL param is skipped
+    sa = (ctypes.c_uint * (len(SIZES) + 1))(*SIZES, SIZES[0])
+    eng.lib.SGDBatch(pa, ga, sa, len(SIZES) + 1, 0.05, 1.0)
+    for h, w, g in zip(hw, ws, gs):
+        assert rel_err(download(eng, h, w.shape), K.sgd(w, g, 0.05, 1.0)) <= 1e-6
+    release(eng, *hw, *hg)
+
+
+@pytest.mark.parametrize("max_norm", [1.0, 1e6])
+def test_sgd_batch_clipped(eng, max_norm):
+    ws, gs = _param_set(2, SIZES)
+    hw, hg = [upload(eng, w) for w in ws], [upload(eng, g) for g in gs]
+    sa = (ctypes.c_uint * len(SIZES))(*SIZES)
+    norm = eng.lib.SGDBatchClipped(_arrays(hw), _arrays(hg), sa, len(SIZES), 0.1, max_norm)
+    n_ref, scale = K.grad_norm_scale(gs, max_norm)
+    assert abs(norm - n_ref) <= 1e-5 * n_ref
+    for h, w, g in zip(hw, ws, gs):
+        assert rel_err(download(eng, h, w.shape), K.sgd_clipped(w, g, 0.1, scale)) <= 1e-6
+    release(eng, *hw, *hg)
+
+
+def test_clip_grad_norm(eng):
+    _, gs = _param_set(3, SIZES)
+    hg = [upload(eng, g) for g in gs]
+    sa = (ctypes.c_uint * len(SIZES))(*SIZES)
+    norm = eng.lib.ClipGradNorm(_arrays(hg), sa, len(SIZES), 1.0)
+    n_ref, scale = K.grad_norm_scale(gs, 1.0)
+    assert abs(norm - n_ref) <= 1e-5 * n_ref
+    for h, g in zip(hg, gs):
+        assert rel_err(download(eng, h, g.shape), g.astype(np.float64) * scale) <= 1e-6
+    release(eng, *hg)
+
+
+@pytest.mark.parametrize("wd,clip", [(0.01, 1.0), (0.0, 1e30)])
+def test_adam_batch_and_shader(eng, wd, clip):
+    ws, gs = _param_set(4, SIZES)
+    r = rng(5)
+    ms = [(0.1 * r.standard_normal(n)).astype(np.float32) for n in SIZES]
+    vs = [(0.1 * r.random(n)).astype(np.float32) for n in SIZES]
+    lr, b1, b2, eps, t = 1e-3, 0.9, 0.999, 1e-8, 3
+    step = K.adam_step_size(lr, b1, b2, t)
+    # The kernel receives every hyper-parameter as a float32 (the shader's
+    # constant buffer); the oracle is fed the same float32 values, so e.g.
+    # 1 - beta2 carries the same rounding as in nn_adam.hlsl.
+    f32 = lambda v: float(np.float32(v))
+    o_step, o_b1, o_b2, o_eps, o_wd = f32(step), f32(b1), f32(b2), f32(eps), f32(lr * wd)
+    hw, hg, hm, hv = ([upload(eng, a) for a in arrs] for arrs in (ws, gs, ms, vs))
+    sa = (ctypes.c_uint * len(SIZES))(*SIZES)
+    eng.lib.AdamBatch(_arrays(hw), _arrays(hg), _arrays(hm), _arrays(hv), sa, len(SIZES), step, b1, b2,
+                      eps, lr * wd, clip)
+    for i in range(len(SIZES)):
+        w_r, m_r, v_r = K.adam(ws[i], gs[i], ms[i], vs[i], o_step, o_b1, o_b2, o_eps, o_wd, clip)
+        assert rel_err(download(eng, hw[i], ws[i].shape), w_r) <= 1e-6
+        assert rel_err(download(eng, hm[i], ms[i].shape), m_r) <= 1e-6
+        assert rel_err(download(eng, hv[i], vs[i].shape), v_r) <= 1e-6
+    # the single-tensor RunShader("adam") path (nn_adam.hlsl CB layout)
+    w2, m2, v2 = upload(eng, ws[5]), upload(eng, ms[5]), upload(eng, vs[5])
+    run(eng, "adam", [hg[5]], [w2, m2, v2], SIZES[5], fbits(step), fbits(b1), fbits(b2), fbits(eps),
+        fbits(lr * wd), fbits(clip), 0)
+    w_r, m_r, v_r = K.adam(ws[5], gs[5], ms[5], vs[5], o_step, o_b1, o_b2, o_eps, o_wd, clip)
+    assert rel_err(download(eng, w2, ws[5].shape), w_r) <= 1e-6
+    release(eng, *hw, *hg, *hm, *hv, w2, m2, v2)
+
+
+def test_norm_clip_shaders(eng):
+    """grad_sq_reduce per tensor + grad_norm_final + sgd_clipped (the
+    dispatches SGDBatchClipped makes in the reference, engine.cpp:514-598)."""
+    ws, gs = _param_set(6, [1000, 4097])
+    hw, hg = [upload(eng, w) for w in ws], [upload(eng, g) for g in gs]
+    parts = (1000 + 255) // 256 + (4097 + 255) // 256
+    hp, hns = new(eng, parts), new(eng, 2)
+    run(eng, "grad_sq_reduce", [hg[0]], [hp], 1000, 0)
+    run(eng, "grad_sq_reduce", [hg[1]], [hp], 4097, (1000 + 255) // 256)
+    run(eng, "grad_norm_final", [hp], [hns], parts, fbits(1.0))
+    n_ref, scale = K.grad_norm_scale(gs, 1.0)
+    ns = download(eng, hns, (2,))
+    assert abs(ns[0] - n_ref) <= 1e-5 * n_ref and abs(ns[1] - scale) <= 1e-5 * scale
+    for i in range(2):
+        run(eng, "sgd_clipped", [hg[i], hns], [hw[i]], ws[i].size, fbits(0.1))
+        assert rel_err(download(eng, hw[i], ws[i].shape), K.sgd_clipped(ws[i], gs[i], 0.1, scale)) <= 1e-5
+    hs = upload(eng, ws[0])
+    run(eng, "sgd", [hg[0]], [hs], 1000, fbits(0.05), fbits(0.5), 0)
+    assert rel_err(download(eng, hs, (1000,)), K.sgd(ws[0], gs[0], 0.05, 0.5)) <= 1e-6
+    release(eng, *hw, *hg, hp, hns, hs)
+
+
+# ------------------------------------------------- im2col path (RunShader)
+def test_im2col_col2im_reshapes(eng):
+    B, C, H, W, k, s, p, OC = 2, 3, 7, 6, 3, 2, 1, 4
+    OH, OW = K.conv_out_hw(H, W, k, s, p)
+    r = rng(9)
+    x = r.standard_normal((B, C, H, W)).astype(np.float32)
+    hx, hcol = upload(eng, x), new(eng, C * k * k * B * OH * OW)
+    cb = (B, C, H, W, k, s, p, OH, OW)
+    run(eng, "im2col", [hx], [hcol], *cb)
+    col = download(eng, hcol, (C * k * k, B * OH * OW))
+    assert np.array_equal(col, K.im2col(x, k, s, p).astype(np.float32))
+    hdx = new(eng, x.size)
+    run(eng, "col2im", [hcol], [hdx], *cb)
+    assert rel_err(download(eng, hdx, x.shape), K.col2im(col, x.shape, k, s, p)) <= 1e-6
+    mm = r.standard_normal((OC, B * OH * OW)).astype(np.float32)
+    bias = r.standard_normal(OC).astype(np.float32)
+    hmm, hb, hy = upload(eng, mm), upload(eng, bias), new(eng, B * OC * OH * OW)
+    for act in (0, 1, 2):
+        run(eng, "conv_reshape", [hmm, hb], [hy], B, OC, OH, OW, act)
+        z = mm.astype(np.float64) + bias[:, None]
+        z = np.maximum(z, 0) if act == 1 else (np.tanh(z) if act == 2 else z)
+        assert rel_err(download(eng, hy, (B, OC, OH, OW)), z.reshape(OC, B, OH, OW).transpose(1, 0, 2, 3)) <= 1e-6
+    dz = r.standard_normal((B, OC, OH, OW)).astype(np.float32)
+    y = r.standard_normal((B, OC, OH, OW)).astype(np.float32)
+    hdz, hyy, hG = upload(eng, dz), upload(eng, y), new(eng, dz.size)
+    run(eng, "conv_grad_reshape", [hdz], [hG], B, 0, 0, 0, OC, 0, 0, OH, OW)
+    assert np.array_equal(download(eng, hG, (OC, B * OH * OW)), K.conv_grad_reshape(dz).astype(np.float32))
+    run(eng, "conv_grad_reshape_relu", [hdz, hyy], [hG], B, 0, 0, 0, OC, 0, 0, OH, OW)
+    assert np.array_equal(download(eng, hG, (OC, B * OH * OW)), K.conv_grad_reshape(dz, y, 1).astype(np.float32))
+    for flags in range(4):
+        Mm, Kk, Nn = 5, 9, 7
+        a = r.standard_normal(Mm * Kk).astype(np.float32)
+        b = r.standard_normal(Kk * Nn).astype(np.float32)
+        ha, hb2, hc = upload(eng, a), upload(eng, b), new(eng, Mm * Nn)
+        for name in ("matmul_universal", "matmul_heavy", "matmul_reduce"):
+            run(eng, name, [ha, hb2], [hc], Mm, Kk, Nn, flags)
+            assert rel_err(download(eng, hc, (Mm, Nn)), K.matmul(a, b, Mm, Kk, Nn, flags)) <= 1e-5
+        release(eng, ha, hb2, hc)
+    release(eng, hx, hcol, hdx, hmm, hb, hy, hdz, hyy, hG)
+
+
+def test_run_sequence(eng):
+    """RunSequence replays SeqCmd records (engine.cpp:952-966) built with ResolveShader."""
+    from directcompute_torch_amd._lib import SeqCmd
+    n = 1000
+    g = rng(10).standard_normal(n).astype(np.float32)
+    x = rng(11).standard_normal(n).astype(np.float32)
+    hg, hx, ho, hw = upload(eng, g), upload(eng, x), new(eng, n), upload(eng, x)
+    cmds = (SeqCmd * 2)()
+    cmds[0].shader = eng.lib.ResolveShader(b"relu_grad")
+    cmds[0].srvs[0], cmds[0].srvs[1], cmds[0].srvCount = hg, hx, 2
+    cmds[0].uavs[0], cmds[0].uavCount = ho, 1
+    struct.pack_into("I", cmds[0].cbData, 0, n)
+    cmds[0].cbSize = 16
+    cmds[1].shader = None  # skipped
+    eng.lib.RunSequence(ctypes.byref(cmds), 2)
+    assert rel_err(download(eng, ho, (n,)), K.relu_grad(g, x)) <= 1e-6
+    sa = (ctypes.c_uint * 1)(n)
+    eng.lib.RunSequenceWithSGD(ctypes.byref(cmds), 1, _arrays([hw]), _arrays([ho]), sa, 1, 0.1, 1.0)
+    assert rel_err(download(eng, hw, (n,)), K.sgd(x, K.relu_grad(g, x), 0.1, 1.0)) <= 1e-6
+    release(eng, hg, hx, ho, hw)
