@@ -443,14 +443,16 @@ __global__ void k_bn_partial(Buf x, Buf dy, Buf mean, Buf var, float eps, uint32
     mu = ld(mean, c);
     rstd = 1.0f / sqrtf(ld(var, c) + eps);
   }
-  float a0 = 0.f, a1 = 0.f;
+  // Moments accumulate in double: the one-pass variance E[x^2] - E[x]^2
+  // cancels catastrophically in float when |mean| >> std.
+  double a0 = 0.0, a1 = 0.0;
   for (uint32_t i = i0 + threadIdx.x; i < i1; i += 256) {
     const uint32_t n = fdiv(i, dS);
     const uint32_t idx = n * C * S + c * S + (i - n * S);
     const float xv = CHECK ? ld(x, idx) : x.p[idx];
     if (MODE == 0) {
-      a0 += xv;
-      a1 += xv * xv;
+      a0 += double(xv);
+      a1 += double(xv) * double(xv);
     } else {
       const float g = CHECK ? ld(dy, idx) : dy.p[idx];
       const float xh = (xv - mu) * rstd;
@@ -466,7 +468,9 @@ __global__ void k_bn_partial(Buf x, Buf dy, Buf mean, Buf var, float eps, uint32
   }
 }
 
-// batchnorm_mean_var finalize (nn_batchnorm_mean_var.hlsl:46-59).
+// batchnorm_mean_var finalize: the formulas of nn_batchnorm_mean_var.hlsl:46-59
+// (one-pass var = max(0, E[x^2] - E[x]^2), unbiased running var
+// var*m/max(1, m-1), momentum update), evaluated in double.
 __global__ void k_bn_stats_final(const double* part, uint32_t pieces, uint32_t C, uint32_t m,
                                  Buf mean, Buf var, Buf rmean, Buf rvar, uint32_t training,
                                  float momentum) {
@@ -477,15 +481,15 @@ __global__ void k_bn_stats_final(const double* part, uint32_t pieces, uint32_t C
     s0 += part[(size_t(c) * pieces + p) * 2];
     s1 += part[(size_t(c) * pieces + p) * 2 + 1];
   }
-  const float mu = float(s0 / m);
-  const float x2 = float(s1 / m);
-  const float v = fmaxf(0.f, x2 - mu * mu);
-  st(mean, c, mu);
-  st(var, c, v);
+  const double mu = s0 / m;
+  const double v = fmax(0.0, s1 / m - mu * mu);
+  st(mean, c, float(mu));
+  st(var, c, float(v));
   if (training == 1) {
-    const float unb = v * (float(m) / fmaxf(1.0f, float(m - 1)));
-    st(rmean, c, (1.0f - momentum) * ld(rmean, c) + momentum * mu);
-    st(rvar, c, (1.0f - momentum) * ld(rvar, c) + momentum * unb);
+    const double unb = v * (double(m) / fmax(1.0, double(m) - 1.0));
+    const double mo = momentum;
+    st(rmean, c, float((1.0 - mo) * ld(rmean, c) + mo * mu));
+    st(rvar, c, float((1.0 - mo) * ld(rvar, c) + mo * unb));
   }
 }
 __global__ void k_bn_grad_final(const double* part, uint32_t pieces, uint32_t C, Buf dgamma,

@@ -71,11 +71,22 @@ def _node(data, parents, backward):
     return out
 
 
-def conv2d(x, w, b, stride=1, padding=0, act=0):
-    y = K.conv_forward(x.data, w.data, b.data, stride, padding, act)
+def conv2d(x, w, b, stride=1, padding=0, act=0, mask=None):
+    """``mask`` (bool, output shape; act == 1 only) pins the ReLU decision
+    (y > 0) to a given pattern, e.g. the device's own, so that a value
+    within round-off of 0 cannot route the gradient differently."""
+    if act == 1 and mask is not None:
+        z = K.conv_forward(x.data, w.data, b.data, stride, padding, 0)
+        y = np.where(mask, z, 0.0)
+    else:
+        y = K.conv_forward(x.data, w.data, b.data, stride, padding, act)
 
     def bw(g):
-        dW, db, dX = K.conv_backward(g, y, x.data, w.data, stride, padding, act,
+        if act == 1 and mask is not None:
+            g, y_mask, a = np.where(mask, g, 0.0), None, 0
+        else:
+            y_mask, a = y, act
+        dW, db, dX = K.conv_backward(g, y_mask, x.data, w.data, stride, padding, a,
                                      need_x=x.requires_grad, need_w=w.requires_grad,
                                      need_b=b.requires_grad)
         if w.requires_grad:
@@ -134,11 +145,13 @@ def add_bias(A, b):
     return _node(K.add_bias(A.data, b.data), (A, b), bw)
 
 
-def bias_relu(A, b):
+def bias_relu(A, b, mask=None):
     out = K.bias_relu(A.data, b.data)
+    if mask is not None:
+        out = np.where(mask, K.add_bias(A.data, b.data), 0.0)
 
     def bw(g):
-        eff = K.relu_grad(g, out)
+        eff = K.relu_grad(g, out) if mask is None else np.where(mask, g, 0.0)
         if A.requires_grad:
             A._acc(eff)
         if b.requires_grad:
@@ -146,16 +159,28 @@ def bias_relu(A, b):
     return _node(out, (A, b), bw)
 
 
-def relu(x):
-    def bw(g):
-        x._acc(K.relu_grad(g, x.data))
-    return _node(K.relu(x.data), (x,), bw)
+def relu(x, mask=None):
+    """``mask`` (bool) pins the decision x > 0 (see conv2d)."""
+    if mask is None:
+        def bw(g):
+            x._acc(K.relu_grad(g, x.data))
+        return _node(K.relu(x.data), (x,), bw)
+
+    def bwm(g):
+        x._acc(np.where(mask, g, 0.0))
+    return _node(np.where(mask, x.data, 0.0), (x,), bwm)
 
 
-def relu6(x):
-    def bw(g):
-        x._acc(K.relu6_grad(g, x.data))
-    return _node(K.relu6(x.data), (x,), bw)
+def relu6(x, mask=None):
+    """``mask`` (bool) pins the decision 0 < x < 6."""
+    if mask is None:
+        def bw(g):
+            x._acc(K.relu6_grad(g, x.data))
+        return _node(K.relu6(x.data), (x,), bw)
+
+    def bwm(g):
+        x._acc(np.where(mask, g, 0.0))
+    return _node(np.where(mask, x.data, np.where(x.data >= 6.0, 6.0, 0.0)), (x,), bwm)
 
 
 def sigmoid(x):
