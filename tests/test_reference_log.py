@@ -1,0 +1,116 @@
+"""The reference's own recorded outputs: compare_result.log, 20 lock-step
+training steps of the 3-level UNet-base16 of compare_unet_20batch.py on
+`segment/` images (batch 2, 128x128, Dice loss, clip_grad_norm 1.0, SGD lr
+1e-3 without element clip).  The fixture tests/golden/unet_segment_20steps.npz
+(made by tests/golden/make_unet_segment_fixture.py) holds the 40 input images,
+their masks and the logged DirectCompute loss / gradient norm of every step.
+
+* CPU: the float64 oracle replays the 20 steps and must reproduce the log.
+* GPU: the drop-in nn_engine API replays them on the device, with the same
+  calls as the reference script (conv2d + relu, maxpool2d, upsample2d, concat,
+  sigmoid, dice_loss, clip_grad_norm, SGDBatch with clip 1e30).
+
+Tolerances.  The logged run computed in float32.  Its losses match exact
+(float64) arithmetic to 1.6e-6, but its gradient norms drift from the
+float64 trajectory by up to 9.6e-4 relative over the 20 steps: replaying the
+same script in torch float64 gives the float64 oracle's norms to 1e-6 (e.g.
+step 19: 1.15464 vs logged 1.1556), replaying it in torch float32 gives the
+logged ones.  So |loss - log| <= 2e-6 and |norm - log| <= 1.2e-3 * norm; the
+float64 oracle is additionally held to torch float64 autograd at 1e-6
+(test_oracle_matches_float64_autograd_on_log_run).
+"""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+from oracle import kernels as K
+from tests import workloads as WL
+
+FIXTURE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "unet_segment_20steps.npz")
+LR = 1e-3
+
+
+def _check(step, loss, norm, dc_loss, dc_norm):
+    assert abs(loss - dc_loss[step]) <= 2e-6, (step + 1, loss, dc_loss[step])
+    assert abs(norm - dc_norm[step]) <= 1.2e-3 * dc_norm[step], (step + 1, norm, dc_norm[step])
+
+
+def test_oracle_reproduces_reference_log():
+    batches, dc_loss, dc_norm = WL.segment_batches(FIXTURE)
+    P = WL.unet3_rename(WL.unet3_ref_params())
+    for step, (x, y) in enumerate(batches):
+        ob = WL.Oracle(P)
+        loss = ob.dice(WL.unet3_ref(ob, x), y)
+        loss.backward()
+        g = ob.grads()
+        norm, scale = K.grad_norm_scale([g[k] for k in sorted(g)], 1.0)
+        _check(step, float(np.mean(loss.data)), norm, dc_loss, dc_norm)
+        # the reference keeps float32 weights on the device
+        P = {k: (P[k].astype(np.float64) - LR * g[k] * scale).astype(np.float32) for k in P}
+
+
+@pytest.mark.gpu
+def test_device_reproduces_reference_log(eng):
+    batches, dc_loss, dc_norm = WL.segment_batches(FIXTURE)
+    be = WL.Device(eng, WL.unet3_rename(WL.unet3_ref_params()))
+    params = list(be.P.values())
+    n = len(params)
+    for step, (x, y) in enumerate(batches):
+        be.pool_nodes, be.mask_nodes = [], []
+        loss = be.dice(WL.unet3_ref(be, x), y)
+        lv = float(np.mean(loss.sync()))
+        loss.backward()
+        norm = eng.clip_grad_norm(params, max_norm=1.0)
+        pa = (ctypes.c_void_p * n)(*[p.gpu_buf for p in params])
+        ga = (ctypes.c_void_p * n)(*[p.grad.gpu_buf for p in params])
+        sa = (ctypes.c_uint * n)(*[p.size for p in params])
+        eng.lib.SGDBatch(pa, ga, sa, n, LR, 1e30)
+        eng.release_all_buffers()
+        _check(step, lv, norm, dc_loss, dc_norm)
+
+
+def test_oracle_matches_float64_autograd_on_log_run():
+    """Independent pin of the oracle's UNet path (conv, ReLU, max-pool,
+    nearest upsample, concat, sigmoid, Dice, norm clip, SGD): torch float64
+    autograd on the same 20-step run agrees to 1e-6 in loss and norm."""
+    torch = pytest.importorskip("torch")
+    F = torch.nn.functional
+    batches, _, _ = WL.segment_batches(FIXTURE)
+    P = WL.unet3_rename(WL.unet3_ref_params())
+    T = {k: torch.tensor(v.astype(np.float64), requires_grad=True) for k, v in P.items()}
+
+    def blk(h, n):
+        h = F.relu(F.conv2d(h, T[n + "@1.w"], T[n + "@1.b"], padding=1))
+        return F.relu(F.conv2d(h, T[n + "@2.w"], T[n + "@2.b"], padding=1))
+
+    for step, (x, y) in enumerate(batches):
+        # oracle step
+        ob = WL.Oracle(P)
+        loss = ob.dice(WL.unet3_ref(ob, x), y)
+        loss.backward()
+        g = ob.grads()
+        norm, scale = K.grad_norm_scale([g[k] for k in sorted(g)], 1.0)
+        P = {k: (P[k].astype(np.float64) - LR * g[k] * scale).astype(np.float32) for k in P}
+        # torch float64 step from the same weights
+        xt, yt = torch.tensor(x, dtype=torch.float64), torch.tensor(y, dtype=torch.float64)
+        e1 = blk(xt, "enc1")
+        e2 = blk(F.max_pool2d(e1, 2), "enc2")
+        e3 = blk(F.max_pool2d(e2, 2), "enc3")
+        b = blk(F.max_pool2d(e3, 2), "bot")
+        d3 = blk(torch.cat([F.interpolate(b, scale_factor=2), e3], 1), "up3")
+        d2 = blk(torch.cat([F.interpolate(d3, scale_factor=2), e2], 1), "up2")
+        d1 = blk(torch.cat([F.interpolate(d2, scale_factor=2), e1], 1), "up1")
+        pred = torch.sigmoid(F.conv2d(d1, T["final@.w"], T["final@.b"]))
+        inter = (pred * yt).sum([1, 2, 3])
+        tl = (1 - 2 * inter / (pred.sum([1, 2, 3]) + yt.sum([1, 2, 3]) + 1e-6)).mean()
+        for v in T.values():
+            v.grad = None
+        tl.backward()
+        tn = float(torch.nn.utils.clip_grad_norm_(list(T.values()), 1.0))
+        assert abs(tl.item() - float(np.mean(loss.data))) <= 1e-9, step
+        assert abs(tn - norm) <= 1e-6 * norm, (step, tn, norm)
+        with torch.no_grad():
+            for k, v in T.items():
+                v.copy_(torch.from_numpy(P[k].astype(np.float64)))

@@ -336,3 +336,59 @@ def mobilenet(be, x):
         t = be.bn(be.conv(t, f"b{i}.proj"), f"b{i}.bn3")
         h = be.add(t, h) if (s == 1 and ci == co) else t
     return be.linear(be.gap(h), "fc", False)
+
+
+# ------------------------------------------------------------------ reference UNet run
+# The 3-level UNet-base16 of compare_unet_20batch.py (conv3x3 + ReLU x2 per
+# block, no BN), with the weights that script draws from RandomState(42).
+UNET3_BLOCKS = [("enc1", 3, 16), ("enc2", 16, 32), ("enc3", 32, 64), ("bot", 64, 128),
+                ("up3", 192, 64), ("up2", 96, 32), ("up1", 48, 16)]
+
+
+def unet3_ref_params():
+    rng = np.random.RandomState(42)
+    P = {}
+    for name, cin, cout in UNET3_BLOCKS:
+        P[name + ".w1"] = rng.randn(cout, cin, 3, 3).astype(np.float32) * np.sqrt(2.0 / (cin * 9))
+        P[name + ".b1"] = np.zeros(cout, np.float32)
+        P[name + ".w2"] = rng.randn(cout, cout, 3, 3).astype(np.float32) * np.sqrt(2.0 / (cout * 9))
+        P[name + ".b2"] = np.zeros(cout, np.float32)
+    P["final.w"] = rng.randn(1, 16, 1, 1).astype(np.float32) * np.sqrt(2.0 / 16)
+    P["final.b"] = np.zeros(1, np.float32)
+    return P
+
+
+def _block(be, h, name):
+    h = be.relu(be.conv(h, name + "@1", 1, 1))
+    return be.relu(be.conv(h, name + "@2", 1, 1))
+
+
+def unet3_ref(be, x):
+    e1 = _block(be, be.input(x), "enc1")
+    e2 = _block(be, be.maxpool(e1, 2, 2), "enc2")
+    e3 = _block(be, be.maxpool(e2, 2, 2), "enc3")
+    b = _block(be, be.maxpool(e3, 2, 2), "bot")
+    d3 = _block(be, be.concat([be.upsample(b), e3]), "up3")
+    d2 = _block(be, be.concat([be.upsample(d3), e2]), "up2")
+    d1 = _block(be, be.concat([be.upsample(d2), e1]), "up1")
+    return be.sigmoid(be.conv(d1, "final@", 1, 0))
+
+
+def unet3_rename(P):
+    """Parameter names as the backends look them up: '<block>@1.w' etc."""
+    out = {}
+    for k, v in P.items():
+        blk, kind = k.split(".")
+        if blk == "final":
+            out["final@." + kind] = v
+        else:
+            out[f"{blk}@{kind[1]}.{kind[0]}"] = v
+    return out
+
+
+def segment_batches(path):
+    """(x, y) float32 batches of the golden segment fixture, in step order."""
+    d = np.load(path)
+    X = d["images_u8"].astype(np.float32).transpose(0, 3, 1, 2) / 255.0
+    Y = np.unpackbits(d["masks"], axis=-1)[:, None, :, :].astype(np.float32)
+    return [(X[2 * i:2 * i + 2], Y[2 * i:2 * i + 2]) for i in range(len(X) // 2)], d["dc_loss"], d["dc_norm"]
