@@ -1,0 +1,444 @@
+"""CPU pins of the float64 oracle (oracle/kernels.py, oracle/engine64.py).
+
+Every oracle function is checked against something that does not restate its
+own formula: torch CPU library routines and autograd (float64), brute-force
+scalar loops written from the HLSL text, adjoint identities and central finite
+differences (the reference's own protocol, nn_verify.py:63-141).  The golden
+end-to-end pin (the reference's logged UNet run) is test_reference_log.py.
+"""
+import numpy as np
+import pytest
+
+from oracle import engine64 as E
+from oracle import kernels as K
+
+torch = pytest.importorskip("torch")
+F = torch.nn.functional
+
+
+def t64(a, grad=False):
+    return torch.tensor(np.asarray(a, dtype=np.float64), requires_grad=grad)
+
+
+def close(a, b, tol=1e-10):
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    assert a.shape == b.shape, (a.shape, b.shape)
+    scale = max(1.0, float(np.max(np.abs(b))) if b.size else 1.0)
+    assert float(np.max(np.abs(a - b))) <= tol * scale if a.size else True
+
+
+rng = np.random.default_rng
+
+CONV = [(2, 3, 9, 8, 4, 3, 1, 1), (1, 2, 11, 11, 3, 5, 2, 2), (2, 4, 7, 7, 5, 3, 3, 0), (1, 3, 30, 30, 2, 11, 4, 2),
+        (2, 5, 6, 6, 3, 1, 1, 0)]
+
+
+# ------------------------------------------------------------------ conv
+@pytest.mark.parametrize("B,C,H,W,OC,k,s,p", CONV)
+def test_conv_forward_vs_torch(B, C, H, W, OC, k, s, p):
+    r = rng(B + C + k + s)
+    x, w, b = r.standard_normal((B, C, H, W)), r.standard_normal((OC, C, k, k)), r.standard_normal(OC)
+    z = F.conv2d(t64(x), t64(w), t64(b), stride=s, padding=p).numpy()
+    close(K.conv_forward(x, w, b, s, p, 0), z)
+    close(K.conv_forward(x, w, b, s, p, 1), np.maximum(z, 0))
+    close(K.conv_forward(x, w, b, s, p, 2), np.tanh(z))
+
+
+@pytest.mark.parametrize("B,C,H,W,OC,k,s,p", CONV)
+def test_conv_backward_vs_torch_library(B, C, H, W, OC, k, s, p):
+    r = rng(7 * (B + C + k + s))
+    x, w = r.standard_normal((B, C, H, W)), r.standard_normal((OC, C, k, k))
+    OH, OW = K.conv_out_hw(H, W, k, s, p)
+    dy = r.standard_normal((B, OC, OH, OW))
+    dW, db, dX = K.conv_backward(dy, None, x, w, s, p, 0)
+    close(dW, torch.nn.grad.conv2d_weight(t64(x), w.shape, t64(dy), stride=s, padding=p).numpy())
+    close(dX, torch.nn.grad.conv2d_input(x.shape, t64(w), t64(dy), stride=s, padding=p).numpy())
+    close(db, dy.sum(axis=(0, 2, 3)))
+
+
+def test_conv_backward_relu_mask_matches_autograd():
+    """act == 1: the gradient of relu(conv(x)) (mask from the post-ReLU
+    output, nn_conv_grad_reshape_relu.hlsl:36)."""
+    r = rng(3)
+    x, w, b = r.standard_normal((2, 3, 8, 8)), r.standard_normal((5, 3, 3, 3)), r.standard_normal(5)
+    xt, wt, bt = t64(x, True), t64(w, True), t64(b, True)
+    y = F.relu(F.conv2d(xt, wt, bt, padding=1))
+    dy = r.standard_normal(y.shape)
+    y.backward(t64(dy))
+    dW, db, dX = K.conv_backward(dy, y.detach().numpy(), x, w, 1, 1, 1)
+    close(dW, wt.grad.numpy())
+    close(db, bt.grad.numpy())
+    close(dX, xt.grad.numpy())
+
+
+def test_conv_backward_tanh_applies_no_derivative():
+    """act == 2 backward uses dy unmasked and without tanh' (engine.cpp:816-835
+    only special-cases actType == 1)."""
+    r = rng(4)
+    x, w = r.standard_normal((1, 2, 6, 6)), r.standard_normal((3, 2, 3, 3))
+    dy = r.standard_normal((1, 3, 4, 4))
+    y = np.tanh(K.conv_forward(x, w, np.zeros(3), 1, 0, 0))
+    for a, c in zip(K.conv_backward(dy, y, x, w, 1, 0, 2), K.conv_backward(dy, None, x, w, 1, 0, 0)):
+        close(a, c)
+
+
+def test_conv_backward_finite_differences():
+    """Central differences of L = sum(conv(x, w, b) * dy), eps 1e-6."""
+    r = rng(5)
+    x, w, b = r.standard_normal((1, 2, 5, 6)), r.standard_normal((3, 2, 3, 3)), r.standard_normal(3)
+    dy = r.standard_normal((1, 3, 3, 3))
+
+    def L(x_, w_, b_):
+        return float((K.conv_forward(x_, w_, b_, 2, 1, 0) * dy).sum())
+
+    dW, db, dX = K.conv_backward(dy, None, x, w, 2, 1, 0)
+    eps = 1e-6
+    for arr, grad in ((w, dW), (x, dX), (b, db)):
+        num = np.zeros_like(arr)
+        for i in range(arr.size):
+            a1, a2 = arr.copy(), arr.copy()
+            a1.flat[i] += eps
+            a2.flat[i] -= eps
+            args1 = [a1 if arr is t else t for t in (x, w, b)]
+            args2 = [a2 if arr is t else t for t in (x, w, b)]
+            num.flat[i] = (L(*args1) - L(*args2)) / (2 * eps)
+        close(grad, num, 1e-7)
+
+
+def test_im2col_col2im_adjoint_and_brute_force():
+    r = rng(6)
+    B, C, H, W, k, s, p = 2, 3, 7, 6, 3, 2, 1
+    x = r.standard_normal((B, C, H, W))
+    col = K.im2col(x, k, s, p)
+    OH, OW = K.conv_out_hw(H, W, k, s, p)
+    # brute force from the shader's index formulas (nn_im2col.hlsl:23-41)
+    bf = np.zeros_like(col)
+    for row in range(C * k * k):
+        ic, kk = divmod(row, k * k)
+        kh, kw = divmod(kk, k)
+        for c in range(B * OH * OW):
+            b, pix = divmod(c, OH * OW)
+            oh, ow = divmod(pix, OW)
+            ih, iw = oh * s + kh - p, ow * s + kw - p
+            if 0 <= ih < H and 0 <= iw < W:
+                bf[row, c] = x[b, ic, ih, iw]
+    close(col, bf, 0)
+    c2 = r.standard_normal(col.shape)
+    # <im2col(x), c> == <x, col2im(c)>
+    assert abs(float((col * c2).sum()) - float((x * K.col2im(c2, x.shape, k, s, p)).sum())) < 1e-10
+
+
+@pytest.mark.parametrize("flags", range(4))
+def test_flagged_matmul_vs_torch(flags):
+    r = rng(flags)
+    M, Kd, N = 5, 7, 4
+    a = r.standard_normal((M, Kd))
+    b = r.standard_normal((Kd, N))
+    a_raw = a.T.copy() if flags & 1 else a
+    b_raw = b.T.copy() if flags & 2 else b
+    close(K.matmul(a_raw.ravel(), b_raw.ravel(), M, Kd, N, flags), torch.matmul(t64(a), t64(b)).numpy())
+
+
+@pytest.mark.parametrize("tA,tB", [(False, False), (True, False), (False, True), (True, True)])
+def test_matmul_backward_vs_autograd(tA, tB):
+    """engine64.matmul backward covers the four transpose combinations of
+    MatMul.backward (nn_engine.py:913-952)."""
+    r = rng(10 + 2 * tA + tB)
+    A = r.standard_normal((6, 4) if tA else (4, 6))
+    Bm = r.standard_normal((5, 6) if tB else (6, 5))
+    At, Bt = t64(A, True), t64(Bm, True)
+    out = (At.T if tA else At) @ (Bt.T if tB else Bt)
+    g = r.standard_normal(out.shape)
+    out.backward(t64(g))
+    a, b = E.T(A, True), E.T(Bm, True)
+    o = E.matmul(a, b, tA, tB)
+    o._backward(g)
+    close(a.grad, At.grad.numpy())
+    close(b.grad, Bt.grad.numpy())
+
+
+# --------------------------------------------------------------- maxpool
+def _maxpool_brute(x, k, s):
+    """Scalar loop of nn_maxpool_forward.hlsl:27-51."""
+    B, C, H, W = x.shape
+    OH, OW = (H - k) // s + 1, (W - k) // s + 1
+    out = np.zeros((B, C, OH, OW))
+    idx = np.zeros((B, C, OH, OW), np.uint32)
+    for b in range(B):
+        for c in range(C):
+            for oh in range(OH):
+                for ow in range(OW):
+                    m, mi = -1e30, 0xFFFFFFFF
+                    for ph in range(k):
+                        for pw in range(k):
+                            ih, iw = oh * s + ph, ow * s + pw
+                            if ih < H and iw < W:
+                                v = float(x[b, c, ih, iw])
+                                if v > m:
+                                    m, mi = v, ((b * C + c) * H + ih) * W + iw
+                    out[b, c, oh, ow], idx[b, c, oh, ow] = m, mi
+    return out, idx
+
+
+@pytest.mark.parametrize("k,s", [(2, 2), (3, 2), (3, 1), (2, 3)])
+def test_maxpool_forward_brute_force_with_ties_and_nan(k, s):
+    r = rng(k * 10 + s)
+    x = r.integers(-3, 3, (2, 3, 9, 8)).astype(np.float32)   # many ties
+    x[0, 0, 0, 0] = np.nan
+    x[1, 2, 4, 4] = np.nan
+    o, i = K.maxpool_forward(x, k, s)
+    bo, bi = _maxpool_brute(x, k, s)
+    assert np.array_equal(i, bi)
+    close(o, bo, 0)
+
+
+@pytest.mark.parametrize("k,s", [(2, 2), (3, 2)])
+def test_maxpool_vs_torch_tie_free(k, s):
+    r = rng(20 + k)
+    x = r.permutation(2 * 3 * 13 * 13).reshape(2, 3, 13, 13).astype(np.float64)  # distinct values
+    o, i = K.maxpool_forward(x, k, s)
+    xt = t64(x, True)
+    to, ti = F.max_pool2d(xt, k, s, return_indices=True)
+    plane = (np.arange(6).reshape(2, 3, 1, 1) * 13 * 13)
+    assert np.array_equal(i.astype(np.int64), ti.numpy() + plane)
+    close(o, to.detach().numpy(), 0)
+    g = r.standard_normal(o.shape)
+    to.backward(t64(g))
+    close(K.maxpool_backward(g, i, x.size).reshape(x.shape), xt.grad.numpy())
+
+
+# ------------------------------------------------------------- batchnorm
+def test_batchnorm_vs_torch_training_mode():
+    r = rng(30)
+    x = r.standard_normal((4, 5, 6, 7)) * 3 + 1
+    g, b = r.standard_normal(5), r.standard_normal(5)
+    rm, rv = r.standard_normal(5), r.random(5) + 0.5
+    xt, gt, bt = t64(x, True), t64(g, True), t64(b, True)
+    rmt, rvt = t64(rm), t64(rv)
+    y = F.batch_norm(xt, rmt, rvt, gt, bt, training=True, momentum=0.1, eps=1e-5)
+    mu, var, nrm, nrv = K.batchnorm_mean_var(x, rm, rv, 0.1, True)
+    close(K.batchnorm_forward(x, mu, var, g, b, 1e-5), y.detach().numpy())
+    close(nrm, rmt.numpy())
+    close(nrv, rvt.numpy())
+    dy = r.standard_normal(x.shape)
+    y.backward(t64(dy))
+    dg, db = K.batchnorm_backward_reduce(x, dy, mu, var, 1e-5)
+    close(dg, gt.grad.numpy())
+    close(db, bt.grad.numpy())
+    close(K.batchnorm_backward_dx(x, dy, mu, var, g, dg, db, 1e-5), xt.grad.numpy(), 1e-9)
+
+
+# ----------------------------------------------------------- elementwise
+def test_activation_grads_vs_autograd():
+    r = rng(40)
+    x = r.standard_normal(200) * 4
+    x[:4] = [0.0, 6.0, -0.0, 3.0]
+    g = r.standard_normal(200)
+    for fo, fg, tf in [(K.relu, K.relu_grad, F.relu), (K.relu6, K.relu6_grad, lambda v: F.hardtanh(v, 0.0, 6.0)),
+                       (lambda v: K.leaky_relu(v, 0.1), lambda gg, v: K.leaky_relu_grad(gg, v, 0.1),
+                        lambda v: F.leaky_relu(v, 0.1))]:
+        xt = t64(x, True)
+        y = tf(xt)
+        y.backward(t64(g))
+        close(fo(x), y.detach().numpy())
+        close(fg(g, x), xt.grad.numpy())
+    xt = t64(x, True)
+    y = torch.sigmoid(xt)
+    y.backward(t64(g))
+    close(K.sigmoid(x), y.detach().numpy())
+    close(K.sigmoid_grad(g, K.sigmoid(x)), xt.grad.numpy())
+
+
+def test_bias_ops_vs_autograd():
+    r = rng(41)
+    A, b, g = r.standard_normal((6, 9)), r.standard_normal(9), r.standard_normal((6, 9))
+    At, bt = t64(A, True), t64(b, True)
+    y = F.relu(At + bt)
+    y.backward(t64(g))
+    close(K.bias_relu(A, b), y.detach().numpy())
+    a, bb = E.T(A, True), E.T(b, True)
+    E.bias_relu(a, bb)._backward(g)
+    close(a.grad, At.grad.numpy())
+    close(bb.grad, bt.grad.numpy())
+    # bias_grad in both layouts it is dispatched with
+    close(K.bias_grad(A, 6, 9, 9, 1), A.sum(axis=0))
+    close(K.bias_grad(A.T.copy(), 6, 9, 1, 6), A.sum(axis=0))
+
+
+def test_pool_resample_plumbing_vs_autograd():
+    r = rng(42)
+    x = r.standard_normal((2, 3, 4, 5))
+    xt = t64(x, True)
+    y = F.adaptive_avg_pool2d(xt, 1).reshape(2, 3)
+    g = r.standard_normal((2, 3))
+    y.backward(t64(g))
+    close(K.global_avg_pool(x), y.detach().numpy())
+    close(K.global_avg_pool_backward(g, x.shape), xt.grad.numpy())
+    for sH, sW in [(2, 2), (3, 2)]:
+        xt = t64(x, True)
+        y = F.interpolate(xt, scale_factor=(sH, sW), mode="nearest")
+        g = r.standard_normal(y.shape)
+        y.backward(t64(g))
+        close(K.upsample(x, sH, sW), y.detach().numpy())
+        close(K.upsample_backward(g, x.shape, sH, sW), xt.grad.numpy())
+    a, b = r.standard_normal((2, 3, 4, 4)), r.standard_normal((2, 5, 4, 4))
+    close(K.concat([a, b]), torch.cat([t64(a), t64(b)], 1).numpy())
+    close(K.slice_channels(K.concat([a, b]), 3, 5), b)
+
+
+@pytest.mark.parametrize("s,p,k", [(1, 1, 3), (2, 1, 3), (1, 2, 5)])
+def test_depthwise_vs_torch_grouped_conv(s, p, k):
+    r = rng(50 + s + k)
+    x, f, b = r.standard_normal((2, 4, 9, 8)), r.standard_normal((4, 1, k, k)), r.standard_normal(4)
+    xt, ft, bt = t64(x, True), t64(f, True), t64(b, True)
+    y = F.conv2d(xt, ft, bt, stride=s, padding=p, groups=4)
+    close(K.depthwise_forward(x, f, b, s, p), y.detach().numpy())
+    dy = r.standard_normal(y.shape)
+    y.backward(t64(dy))
+    close(K.depthwise_backward_input(dy, f, x.shape, s, p), xt.grad.numpy())
+    df, db = K.depthwise_backward_filter(dy, x, k, k, s, p)
+    close(df, ft.grad.numpy())
+    close(db, bt.grad.numpy())
+
+
+# ------------------------------------------------------------ losses
+def test_softmax_ce_vs_torch():
+    r = rng(60)
+    z, lab = r.standard_normal((7, 10)) * 3, r.integers(0, 10, 7).astype(np.float32)
+    zt = t64(z, True)
+    loss = F.cross_entropy(zt, torch.tensor(lab.astype(np.int64)))
+    loss.backward()
+    close(K.softmax(z), torch.softmax(t64(z), 1).numpy())
+    assert abs(K.ce_loss(z, lab) - loss.item()) < 1e-12
+    close(K.softmax_ce_grad(K.softmax(z), lab), zt.grad.numpy())
+
+
+def test_argmax_correct_first_max_wins():
+    z = np.array([[1, 3, 3, 0], [2, 2, 2, 2], [0, 0, 5, 5], [1, 0, 0, 0]], np.float32)
+    lab = np.array([1, 0, 3, 0], np.float32)
+    assert K.argmax_correct(z, lab) == int((np.argmax(z, 1) == lab).sum()) == 3
+
+
+def test_dice_vs_autograd_mean_loss():
+    """Dice grad = d mean_b(1 - 2I/(P+T+1e-6)) / dp (nn_dice_loss_grad.hlsl:22-33)."""
+    r = rng(61)
+    p, t = r.random((3, 1, 5, 6)), (r.random((3, 1, 5, 6)) < 0.3).astype(np.float64)
+    pt = t64(p, True)
+    tt = t64(t)
+    inter = (pt * tt).sum([1, 2, 3])
+    loss = 1 - 2 * inter / (pt.sum([1, 2, 3]) + tt.sum([1, 2, 3]) + 1e-6)
+    loss.mean().backward()
+    close(K.dice_loss(p, t), loss.detach().numpy())
+    close(K.dice_loss_grad(p, t), pt.grad.numpy())
+
+
+# ------------------------------------------------------------ optimisers
+def test_sgd_and_norm_clip_vs_torch():
+    r = rng(70)
+    ws = [r.standard_normal(n) for n in (5, 17)]
+    gs = [r.standard_normal(n) * 3 for n in (5, 17)]
+    pts = [t64(w, True) for w in ws]
+    for p, g in zip(pts, gs):
+        p.grad = t64(g)
+    tn = float(torch.nn.utils.clip_grad_norm_(pts, 1.0))
+    n, scale = K.grad_norm_scale(gs, 1.0)
+    assert abs(n - tn) < 1e-12
+    for p, g in zip(pts, gs):
+        close(np.asarray(g) * scale, p.grad.numpy())
+    # element clip then SGD == torch SGD on clamped gradients
+    for w, g in zip(ws, gs):
+        pt = t64(w, True)
+        pt.grad = torch.clamp(t64(g), -1.0, 1.0)
+        torch.optim.SGD([pt], lr=0.05).step()
+        close(K.sgd(w, g, 0.05, 1.0), pt.detach().numpy())
+        close(K.sgd_clipped(w, g, 0.05, scale), w - 0.05 * g * scale)
+
+
+def test_adamw_vs_torch_three_steps():
+    """The reference's AdamW (host step size lr*sqrt(1-b2^t)/(1-b1^t), decay
+    lr*wd*w on the old weight, element clip) equals torch AdamW on clamped
+    gradients with eps_t = eps / sqrt(1 - b2^t)."""
+    r = rng(71)
+    w0 = r.standard_normal(50)
+    lr, b1, b2, eps, wd, clip = 1e-2, 0.9, 0.999, 1e-8, 0.01, 1.0
+    pt = t64(w0, True)
+    opt = torch.optim.AdamW([pt], lr=lr, betas=(b1, b2), eps=eps, weight_decay=wd)
+    w, m, v = w0.copy(), np.zeros(50), np.zeros(50)
+    for t in (1, 2, 3):
+        g = r.standard_normal(50) * 2
+        w, m, v = K.adam(w, g, m, v, K.adam_step_size(lr, b1, b2, t), b1, b2, eps, lr * wd, clip)
+        pt.grad = torch.clamp(t64(g), -clip, clip)
+        opt.param_groups[0]["eps"] = eps / np.sqrt(1 - b2 ** t)
+        opt.step()
+        close(w, pt.detach().numpy(), 1e-12)
+
+
+# --------------------------------------------------------- composition
+def test_engine64_lenet_vs_autograd():
+    """The float64 autograd (topological order, accumulation, fused conv+ReLU,
+    max-pool routing, flatten, (in, out) linear weights, bias+ReLU, softmax-CE)
+    against torch autograd on the same network."""
+    r = rng(80)
+    x, lab = r.standard_normal((4, 1, 28, 28)), r.integers(0, 10, 4).astype(np.float32)
+    W = {"c1": r.standard_normal((6, 1, 5, 5)) * 0.3, "c1b": r.standard_normal(6) * 0.1,
+         "c2": r.standard_normal((16, 6, 5, 5)) * 0.1, "c2b": r.standard_normal(16) * 0.1,
+         "l1": r.standard_normal((256, 10)) * 0.1, "l1b": r.standard_normal(10) * 0.1}
+    T = {k: t64(v, True) for k, v in W.items()}
+    h = F.max_pool2d(F.relu(F.conv2d(t64(x), T["c1"], T["c1b"])), 2)
+    h = F.max_pool2d(F.relu(F.conv2d(h, T["c2"], T["c2b"])), 2)
+    h = F.relu(h.reshape(4, -1) @ T["l1"] + T["l1b"])
+    F.cross_entropy(h, torch.tensor(lab.astype(np.int64))).backward()
+    O = {k: E.T(v, True) for k, v in W.items()}
+    g = E.maxpool2d(E.conv2d(E.T(x), O["c1"], O["c1b"], 1, 0, 1), 2, 2)
+    g = E.maxpool2d(E.conv2d(g, O["c2"], O["c2b"], 1, 0, 1), 2, 2)
+    g = E.bias_relu(E.matmul(E.flatten(g), O["l1"]), O["l1b"])
+    E.softmax_ce(g, lab).backward()
+    for k in W:
+        close(O[k].grad, T[k].grad.numpy(), 1e-9)
+
+
+def test_engine64_mobilenet_block_vs_autograd():
+    """BN (training), ReLU6, depthwise, 1x1 convs and a residual add (fan-out
+    accumulation) against torch autograd."""
+    r = rng(81)
+    x = r.standard_normal((2, 8, 6, 6))
+    W = {"e": r.standard_normal((24, 8, 1, 1)) * 0.3, "eb": np.zeros(24), "g1": r.random(24) + 0.5,
+         "b1": r.standard_normal(24) * 0.1, "d": r.standard_normal((24, 1, 3, 3)) * 0.3, "db": np.zeros(24),
+         "g2": r.random(24) + 0.5, "b2": r.standard_normal(24) * 0.1, "p": r.standard_normal((8, 24, 1, 1)) * 0.3,
+         "pb": np.zeros(8), "g3": r.random(8) + 0.5, "b3": r.standard_normal(8) * 0.1}
+    T = {k: t64(v, True) for k, v in W.items()}
+    xt = t64(x, True)
+
+    def bn_t(h, g, b):
+        return F.batch_norm(h, None, None, g, b, training=True, eps=1e-5)
+
+    h = F.hardtanh(bn_t(F.conv2d(xt, T["e"], T["eb"]), T["g1"], T["b1"]), 0, 6)
+    h = F.hardtanh(bn_t(F.conv2d(h, T["d"], T["db"], padding=1, groups=24), T["g2"], T["b2"]), 0, 6)
+    h = bn_t(F.conv2d(h, T["p"], T["pb"]), T["g3"], T["b3"]) + xt
+    dy = r.standard_normal(h.shape)
+    h.backward(t64(dy))
+    O = {k: E.T(v, True) for k, v in W.items()}
+    xo = E.T(x, True)
+    g = E.relu6(E.batchnorm2d(E.conv2d(xo, O["e"], O["eb"]), O["g1"], O["b1"])[0])
+    g = E.relu6(E.batchnorm2d(E.depthwise_conv2d(g, O["d"], O["db"], 1, 1), O["g2"], O["b2"])[0])
+    out = E.add(E.batchnorm2d(E.conv2d(g, O["p"], O["pb"]), O["g3"], O["b3"])[0], xo)
+    out.grad = dy
+    # run the traversal from `out` with the given upstream gradient
+    topo, seen, stack = [], set(), [(out, False)]
+    while stack:
+        v, done = stack.pop()
+        if done:
+            topo.append(v)
+            continue
+        if id(v) in seen:
+            continue
+        seen.add(id(v))
+        stack.append((v, True))
+        stack.extend((p, False) for p in v._parents if p.requires_grad and id(p) not in seen)
+    for v in reversed(topo):
+        if v._backward is not None and v.grad is not None:
+            v._backward(v.grad)
+    close(xo.grad, xt.grad.numpy(), 1e-9)
+    for k in ("e", "g1", "b1", "d", "g2", "b2", "p", "g3", "b3"):
+        close(O[k].grad, T[k].grad.numpy(), 1e-9)
