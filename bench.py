@@ -15,7 +15,7 @@ region; achieved = algorithmic FLOPs (2*OC*C*k*k*B*OH*OW per dW and per dX;
 c1 has no dX since the input needs no gradient) / summed kernel time.
 
 cpu_baseline: the float64 NumPy oracle running the same train step on a
-4-image sample on the host, timed on this machine.
+64-image sample on the host, timed on this machine.
 """
 from __future__ import annotations
 
@@ -106,7 +106,7 @@ def build_alexnet(nn, params):
     return AlexNet()
 
 
-def cpu_baseline(sample=4):
+def cpu_baseline(sample=64):
     """Time the float64 oracle on the same train step for `sample` images."""
     from oracle import models as OM
     threads = os.cpu_count() or 1

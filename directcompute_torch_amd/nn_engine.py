@@ -11,7 +11,7 @@ Importing this module initialises the HIP device (as the reference
 initialises D3D11 at import, nn_engine.py:121) and raises if that fails --
 there is no CPU fallback.
 
-Not provided (out of scope): custom HLSL shaders, the
+Not provided (outside the backward path): custom HLSL shaders, the
 GELU / LayerNorm / attention family (their kernels do not exist in the
 reference tree), ONNX export/import, ComputeGraph record/replay, Muon, and the
 Python-side profilers.

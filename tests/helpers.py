@@ -17,7 +17,7 @@ def rel_err(got, ref):
     return float(num / den)
 
 
-TOL = 1e-4  # max|g - g_ref| / max|g_ref| for every gradient
+TOL = 1e-4  # max|g - g_ref| / max|g_ref| bound for every gradient tensor
 
 
 def rng(seed):

@@ -2,7 +2,7 @@
 the device (drop-in ``nn_engine`` API) and on the float64 oracle
 (``oracle.engine64``), so whole training steps can be compared.
 
-Networks (BASELINE configurations):
+Networks (the benchmark configurations):
   lenet     LeNet-5: conv 1->6 k5 +ReLU, maxpool 2, conv 6->16 k5 +ReLU, maxpool 2,
             Linear 256->120->84->10 (train_lenet.py:22-45 without BN)
   alexnet   AlexNet-224 with Linear 9216->4096->4096->1000 (train_alexnet.py:28-52)
