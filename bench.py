@@ -221,7 +221,7 @@ def main():
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "conv-backward implicit GEMM (dW k_igemm<GLoader,XColLoader> + dX k_igemm<DenseLoader,GPixLoader>), all layers",
+            "kernel": "conv-backward implicit GEMM, all layers: dW k_igemm<LdGradKR,LdXTapKR> + k_dw_final, dX k_igemm<LdDenseRK,LdPixRK> (+ k_splitk_nchw when split)",
             "achieved": round(achieved, 3),
             "peak": MFMA_FP32_PEAK_TFLOPS,
             "unit": "TFLOP/s",

@@ -35,7 +35,10 @@
 #include "dce_internal.h"
 
 #include <algorithm>
+#include <cmath>
+#include <cstdio>
 #include <cstdlib>
+#include <map>
 #include <type_traits>
 
 namespace dce {
@@ -93,12 +96,32 @@ struct LoaderBase {
 };
 
 __device__ __forceinline__ f4 zero4() { return f4{0.f, 0.f, 0.f, 0.f}; }
-__device__ __forceinline__ f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
+
+// Operand view through a buffer resource.  The descriptor's range check makes
+// a load at or past num_records return zeros, so a padding or out-of-image
+// element is read by moving its offset to kOob instead of branching around the
+// load: every quad load of a K tile is issued back to back, with no exec-mask
+// juggling between them.  Offsets are in floats; the host admits operands of
+// fewer than kMaxOperandFloats floats, so kOob (+ any tile offset) is always
+// past num_records.
+constexpr uint32_t kOob = 0x20000000u;
+struct BRes {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ __forceinline__ void init(const float* p, uint32_t nfloats) {
+    // Word 3 = 0x00020000: 32-bit data format, no swizzle, raw (stride 0).
+    r = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), 0, int(nfloats * 4u), 0x00020000);
+  }
+  __device__ __forceinline__ f4 ld4(uint32_t off) const {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off * 4u, 0, 0);
+  }
+};
 
 // ---------------------------------------------------------------------------
-// Dense operands.
+// Dense operands.  Preconditions (the host pads copies to meet them): 16-byte
+// aligned base, ld % 4 == 0, and kdim (ROWK) / rows (KROW) a multiple of 4, so
+// a quad is either wholly inside the matrix or wholly padding.
 // ---------------------------------------------------------------------------
-// [rows][kdim] row-major (ROWK).  vec: ld % 4 == 0, kdim % 4 == 0, aligned.
+// [rows][kdim] row-major (ROWK).
 template <int R, int KT>
 struct LdDenseRK : LoaderBase<Stage<R, KT, false>> {
   using St = Stage<R, KT, false>;
@@ -106,42 +129,32 @@ struct LdDenseRK : LoaderBase<Stage<R, KT, false>> {
   using LoaderBase<St>::Q;
   struct Params {
     const float* p;
-    uint32_t ld, rows, kdim, vec;
+    uint32_t ld, rows, kdim, n;  // n: floats in the buffer
   };
-  const float* p;
-  uint32_t ld, kdim;
-  bool vec;
-  uint32_t row[Q], kq[Q];
-  bool rok[Q];
+  BRes b;
+  uint32_t kdim;
+  uint32_t base[Q], kq[Q];
   __device__ __forceinline__ void init(const Params& P, uint32_t row0, int tid) {
     this->base_init(tid);
-    p = P.p;
-    ld = P.ld;
+    b.init(P.p, P.n);
     kdim = P.kdim;
-    vec = P.vec != 0;
 #pragma unroll
     for (int i = 0; i < Q; ++i) {
-      row[i] = row0 + St::qrow(tid, i);
+      const uint32_t row = row0 + St::qrow(tid, i);
       kq[i] = St::qk(tid, i);
-      rok[i] = row[i] < P.rows;
+      base[i] = row < P.rows ? row * P.ld + kq[i] : kOob;
     }
   }
   __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
 #pragma unroll
     for (int i = 0; i < Q; ++i) {
-      const uint32_t k0 = kt * KT + kq[i];
-      if (vec) {
-        r[i] = (rok[i] && k0 < kdim) ? ld4(p + row[i] * ld + k0) : zero4();
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          r[i][e] = (rok[i] && k0 + e < kdim) ? p[row[i] * ld + k0 + e] : 0.f;
-      }
+      const uint32_t k0 = kt * KT;
+      r[i] = b.ld4(k0 + kq[i] < kdim ? base[i] + k0 : kOob);
     }
   }
 };
 
-// [kdim][rows] k-major (KROW).  vec: rows % 4 == 0, ld % 4 == 0, aligned.
+// [kdim][rows] k-major (KROW).
 template <int R, int KT>
 struct LdDenseKR : LoaderBase<Stage<R, KT, true>> {
   using St = Stage<R, KT, true>;
@@ -149,36 +162,28 @@ struct LdDenseKR : LoaderBase<Stage<R, KT, true>> {
   using LoaderBase<St>::Q;
   struct Params {
     const float* p;
-    uint32_t ld, rows, kdim, vec;
+    uint32_t ld, rows, kdim, n;
   };
-  const float* p;
-  uint32_t ld, kdim, rows;
-  bool vec;
-  uint32_t row[Q], kk[Q];
+  BRes b;
+  uint32_t kdim, ld;
+  uint32_t base[Q], kk[Q];
   __device__ __forceinline__ void init(const Params& P, uint32_t row0, int tid) {
     this->base_init(tid);
-    p = P.p;
-    ld = P.ld;
+    b.init(P.p, P.n);
     kdim = P.kdim;
-    rows = P.rows;
-    vec = P.vec != 0;
+    ld = P.ld;
 #pragma unroll
     for (int i = 0; i < Q; ++i) {
-      row[i] = row0 + St::qrow(tid, i);
+      const uint32_t row = row0 + St::qrow(tid, i);
       kk[i] = St::qk(tid, i);
+      base[i] = row < P.rows ? kk[i] * P.ld + row : kOob;
     }
   }
   __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
 #pragma unroll
     for (int i = 0; i < Q; ++i) {
-      const uint32_t k = kt * KT + kk[i];
-      if (vec) {
-        r[i] = (k < kdim && row[i] < rows) ? ld4(p + k * ld + row[i]) : zero4();
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          r[i][e] = (k < kdim && row[i] + e < rows) ? p[k * ld + row[i] + e] : 0.f;
-      }
+      const uint32_t k0 = kt * KT;
+      r[i] = b.ld4(k0 + kk[i] < kdim ? base[i] + k0 * ld : kOob);
     }
   }
 };
@@ -198,18 +203,17 @@ struct LdPixRK : LoaderBase<Stage<R, KT, false>> {
   struct Params {
     const float* src;
     uint32_t srcH, srcW, Cp, k, s, p;
-    uint32_t gridW, gridHW, N, kdim;
+    uint32_t gridW, gridHW, N, kdim, n;
     FastDiv dGridHW, dGridW, dCp, dK;
   };
-  const float* src;
+  BRes b;
   uint32_t srcH, srcW, Cp, k, s, kdim;
   FastDiv dCp, dK;
   uint32_t pbase[Q], kq[Q];
   int r0[Q], c0[Q];
-  bool rok[Q];
   __device__ __forceinline__ void init(const Params& P, uint32_t row0, int tid) {
     this->base_init(tid);
-    src = P.src;
+    b.init(P.src, P.n);
     srcH = P.srcH;
     srcW = P.srcW;
     Cp = P.Cp;
@@ -222,12 +226,11 @@ struct LdPixRK : LoaderBase<Stage<R, KT, false>> {
     for (int i = 0; i < Q; ++i) {
       const uint32_t n = row0 + St::qrow(tid, i);
       kq[i] = St::qk(tid, i);
-      rok[i] = n < P.N;
-      const uint32_t b = fdiv(n, P.dGridHW);
-      const uint32_t rem = n - b * P.gridHW;
+      const uint32_t bb = fdiv(n, P.dGridHW);
+      const uint32_t rem = n - bb * P.gridHW;
       const uint32_t a = fdiv(rem, P.dGridW);
       const uint32_t c = rem - a * P.gridW;
-      pbase[i] = b * P.srcH * P.srcW;
+      pbase[i] = bb * P.srcH * P.srcW;
       if (FWD) {
         r0[i] = int(a * P.s) - int(P.p);
         c0[i] = int(c * P.s) - int(P.p);
@@ -235,6 +238,8 @@ struct LdPixRK : LoaderBase<Stage<R, KT, false>> {
         r0[i] = int(a + P.p);
         c0[i] = int(c + P.p);
       }
+      // A row past the grid gets an origin no tap can bring into the image.
+      if (n >= P.N) r0[i] = FWD ? -(1 << 20) : (1 << 20);
     }
   }
   __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
@@ -246,7 +251,7 @@ struct LdPixRK : LoaderBase<Stage<R, KT, false>> {
       const uint32_t kh = fdiv(khw, dK);
       const uint32_t kw = khw - kh * k;
       int h, w;
-      bool ok = rok[i] && kk0 < kdim;
+      bool ok = kk0 < kdim;
       if (FWD) {
         h = r0[i] + int(kh);
         w = c0[i] + int(kw);
@@ -261,7 +266,7 @@ struct LdPixRK : LoaderBase<Stage<R, KT, false>> {
         ok = ok && uint32_t(h) * s == uint32_t(hs) && uint32_t(w) * s == uint32_t(ws);
       }
       ok = ok && uint32_t(h) < srcH && uint32_t(w) < srcW;
-      r[i] = ok ? ld4(src + (pbase[i] + uint32_t(h) * srcW + uint32_t(w)) * Cp + ch) : zero4();
+      r[i] = b.ld4(ok ? (pbase[i] + uint32_t(h) * srcW + uint32_t(w)) * Cp + ch : kOob);
     }
   }
 };
@@ -277,27 +282,28 @@ struct LdGradKR : LoaderBase<Stage<R, KT, true>> {
   using LoaderBase<St>::Q;
   struct Params {
     const float* g;
-    uint32_t OCp, npix;
+    uint32_t OCp, npix, n;
   };
-  const float* g;
+  BRes b;
   uint32_t OCp, npix;
-  uint32_t oc[Q], kk[Q];
+  uint32_t base[Q], kk[Q];
   __device__ __forceinline__ void init(const Params& P, uint32_t row0, int tid) {
     this->base_init(tid);
-    g = P.g;
+    b.init(P.g, P.n);
     OCp = P.OCp;
     npix = P.npix;
 #pragma unroll
     for (int i = 0; i < Q; ++i) {
-      oc[i] = row0 + St::qrow(tid, i);
+      const uint32_t oc = row0 + St::qrow(tid, i);
       kk[i] = St::qk(tid, i);
+      base[i] = oc < P.OCp ? kk[i] * P.OCp + oc : kOob;
     }
   }
   __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
 #pragma unroll
     for (int i = 0; i < Q; ++i) {
-      const uint32_t pix = kt * KT + kk[i];
-      r[i] = (oc[i] < OCp && pix < npix) ? ld4(g + pix * OCp + oc[i]) : zero4();
+      const uint32_t p0 = kt * KT;
+      r[i] = b.ld4(p0 + kk[i] < npix ? base[i] + p0 * OCp : kOob);
     }
   }
 };
@@ -311,18 +317,17 @@ struct LdXTapKR : LoaderBase<Stage<R, KT, true>> {
   using LoaderBase<St>::Q;
   struct Params {
     const float* x;
-    uint32_t H, W, Cp, k, s, p, OW, OHW, npix, N;
+    uint32_t H, W, Cp, k, s, p, OW, OHW, npix, N, n;
     FastDiv dOHW, dOW, dCp, dK;
   };
-  const float* x;
+  BRes b;
   uint32_t H, W, Cp, s, OW, OHW, npix;
   FastDiv dOHW, dOW;
   uint32_t off[Q], kk[Q];
   int kh[Q], kw[Q];
-  bool rok[Q];
   __device__ __forceinline__ void init(const Params& P, uint32_t row0, int tid) {
     this->base_init(tid);
-    x = P.x;
+    b.init(P.x, P.n);
     H = P.H;
     W = P.W;
     Cp = P.Cp;
@@ -336,26 +341,27 @@ struct LdXTapKR : LoaderBase<Stage<R, KT, true>> {
     for (int i = 0; i < Q; ++i) {
       const uint32_t n = row0 + St::qrow(tid, i);
       kk[i] = St::qk(tid, i);
-      rok[i] = n < P.N;
       const uint32_t khw = fdiv(n, P.dCp);
       off[i] = n - khw * P.Cp;
       const uint32_t a = fdiv(khw, P.dK);
       kh[i] = int(a) - int(P.p);
       kw[i] = int(khw - a * P.k) - int(P.p);
+      // A row past the taps gets an offset no pixel can bring into the image.
+      if (n >= P.N) kh[i] = -(1 << 20);
     }
   }
   __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
 #pragma unroll
     for (int i = 0; i < Q; ++i) {
       const uint32_t pix = kt * KT + kk[i];
-      const uint32_t b = fdiv(pix, dOHW);
-      const uint32_t rem = pix - b * OHW;
+      const uint32_t bb = fdiv(pix, dOHW);
+      const uint32_t rem = pix - bb * OHW;
       const uint32_t oh = fdiv(rem, dOW);
       const uint32_t ow = rem - oh * OW;
       const int ih = int(oh * s) + kh[i];
       const int iw = int(ow * s) + kw[i];
-      const bool ok = rok[i] && pix < npix && uint32_t(ih) < H && uint32_t(iw) < W;
-      r[i] = ok ? ld4(x + ((b * H + uint32_t(ih)) * W + uint32_t(iw)) * Cp + off[i]) : zero4();
+      const bool ok = pix < npix && uint32_t(ih) < H && uint32_t(iw) < W;
+      r[i] = b.ld4(ok ? ((bb * H + uint32_t(ih)) * W + uint32_t(iw)) * Cp + off[i] : kOob);
     }
   }
 };
@@ -432,10 +438,33 @@ struct EpiNCHW {
 // ---------------------------------------------------------------------------
 // The kernel.
 // ---------------------------------------------------------------------------
+// Tile order.  The dispatcher hands consecutive workgroup ids to the eight
+// XCDs in turn, and each XCD has its own L2.  With `xcd` set, the ids are
+// renumbered so that each XCD receives a contiguous run of logical tiles; the
+// logical order is m-tile fastest, then n-tile, then split, so the tiles that
+// read the same operand rows (the same n-tile, or the same split's K range)
+// run on one XCD at about the same time.
+struct TileGrid {
+  uint32_t gm, gn, xcd;
+};
+__device__ __forceinline__ void tile_coords(const TileGrid& tg, uint32_t& mt, uint32_t& nt,
+                                            uint32_t& z) {
+  const uint32_t nwg = gridDim.x, L = blockIdx.x;
+  uint32_t id = L;
+  if (tg.xcd) {
+    const uint32_t q = nwg >> 3, r = nwg & 7, x = L & 7;
+    id = x * q + min(x, r) + (L >> 3);
+  }
+  mt = id % tg.gm;
+  const uint32_t t = id / tg.gm;
+  nt = t % tg.gn;
+  z = t / tg.gn;
+}
+
 template <int MT, int NT, int KT, class LA, class LB, class EPI>
 __global__ void __launch_bounds__(kThreads)
     k_igemm(const typename LA::Params pa, const typename LB::Params pb,
-            const typename EPI::Params pe, uint32_t ktiles, uint32_t splits) {
+            const typename EPI::Params pe, TileGrid tg, uint32_t ktiles, uint32_t splits) {
   using SA = typename LA::St;
   using SB = typename LB::St;
   constexpr int WM = MT / 2, WN = NT / 2, FM = WM / 16, FN = WN / 16;
@@ -445,7 +474,9 @@ __global__ void __launch_bounds__(kThreads)
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const uint32_t m0 = blockIdx.y * MT, n0 = blockIdx.x * NT, z = blockIdx.z;
+  uint32_t mt, nt, z;
+  tile_coords(tg, mt, nt, z);
+  const uint32_t m0 = mt * MT, n0 = nt * NT;
   const uint32_t kb = uint32_t((uint64_t(ktiles) * z) / splits);
   const uint32_t ke = uint32_t((uint64_t(ktiles) * (z + 1)) / splits);
 
@@ -605,29 +636,85 @@ __global__ void k_splitk_sum(const float* __restrict__ part, float* __restrict__
   out[i] = s;
 }
 
-// dW finalize: dw[oc][c][khw] = sum_z part[z][oc][khw*Cp + c].
+// dW finalize: dw[oc][c][khw] = sum_z part[z][oc][khw*Cp + c], z in order.
+// One thread per partial column in storage order, so the splits x OC x KK*Cp
+// partial reads (the bulk of the traffic) are coalesced; padding channels
+// (c >= C) are skipped.
 __global__ void k_dw_final(const float* __restrict__ part, float* __restrict__ dw, uint32_t OC,
                            uint32_t C, uint32_t KK, uint32_t Cp, uint32_t splits) {
+  const uint32_t N = KK * Cp;
   const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= OC * C * KK) return;
-  const uint32_t oc = i / (C * KK), rr = i - oc * C * KK;
-  const uint32_t c = rr / KK, khw = rr - c * KK;
-  const size_t N = size_t(KK) * Cp, src = size_t(oc) * N + khw * Cp + c, zs = size_t(OC) * N;
+  if (i >= OC * N) return;
+  const uint32_t oc = i / N, n = i - oc * N;
+  const uint32_t khw = n / Cp, c = n - khw * Cp;
+  if (c >= C) return;
+  const size_t zs = size_t(OC) * N;
   float s = 0.f;
-  for (uint32_t z = 0; z < splits; ++z) s += part[z * zs + src];
-  dw[i] = s;
+  for (uint32_t z = 0; z < splits; ++z) s += part[z * zs + i];
+  dw[(size_t(oc) * C + c) * KK + khw] = s;
+}
+
+// Split-K finish for an NCHW output: out[b][m][pix] = act(sum_z part[z][m][n]
+// + bias[m]) for n = b*HW + pix, z summed in order (deterministic).
+__global__ void k_splitk_nchw(const float* __restrict__ part, const float* __restrict__ bias,
+                              float* __restrict__ out, uint32_t M, uint32_t N, uint32_t HW,
+                              uint32_t splits, uint32_t act) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= M * N) return;
+  const uint32_t m = i / N, n = i - m * N;
+  float z = 0.f;
+  for (uint32_t k = 0; k < splits; ++k) z += part[size_t(k) * M * N + i];
+  if (bias) z += bias[m];
+  if (act == 1)
+    z = fmaxf(z, 0.f);
+  else if (act == 2)
+    z = tanhf(z);
+  const uint32_t b = n / HW, pix = n - b * HW;
+  out[(size_t(b) * M + m) * HW + pix] = z;
+}
+
+// Zero-padded copy of a row-major [rows][cols] matrix to row stride ldp.
+__global__ void k_pad_cols(const float* __restrict__ in, float* __restrict__ out, uint32_t rows,
+                           uint32_t cols, uint32_t ldp) {
+  const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= size_t(rows) * ldp) return;
+  const uint32_t r = uint32_t(i / ldp), c = uint32_t(i - size_t(r) * ldp);
+  out[i] = c < cols ? in[size_t(r) * cols + c] : 0.f;
 }
 
 // ---------------------------------------------------------------------------
 // Host side.
 // ---------------------------------------------------------------------------
-static int g_kt = 0;  // K-tile depth 16 (measured best); DCE_KT=32 selects 32 (tuning)
-static int kt_choice() {
-  if (!g_kt) {
-    const char* e = getenv("DCE_KT");
-    g_kt = (e && atoi(e) == 32) ? 32 : 16;
-  }
-  return g_kt;
+// Operands are read through buffer resources addressed by 32-bit float
+// offsets below kOob.
+static bool operand_fits(size_t floats, const char* what) {
+  if (floats < kOob) return true;
+  set_error("%s: operand of %zu floats exceeds the implicit-GEMM limit of %u floats (2 GiB)", what,
+            floats, kOob);
+  return false;
+}
+
+struct TileCfg {
+  int MT, NT, KT;
+  uint32_t splits;
+};
+
+// Tuning overrides: DCE_TUNE_<FWD|DW|DX|GEMM>="MT,NT,KT,splits" replaces the
+// heuristic choice for that GEMM family (read on every call).
+static bool tune_override(const char* var, TileCfg& c) {
+  const char* e = getenv(var);
+  if (!e || !*e) return false;
+  int a, b, k;
+  unsigned sp;
+  if (sscanf(e, "%d,%d,%d,%u", &a, &b, &k, &sp) != 4) return false;
+  c = TileCfg{a, b, k, sp ? sp : 1u};
+  return true;
+}
+
+// XCD-contiguous tile order (on unless DCE_XCD=0; read on every call).
+static bool xcd_order() {
+  const char* e = getenv("DCE_XCD");
+  return !(e && *e && atoi(e) == 0);
 }
 
 // 128 unless 64 wastes clearly less padding.
@@ -636,37 +723,120 @@ static int pick_tile(uint32_t extent) {
   return (w128 * 100 > w64 * 112) ? 64 : 128;
 }
 
-static uint32_t pick_splits(uint32_t tiles, uint32_t ktiles, uint32_t min_kt) {
-  const uint32_t target = uint32_t(num_cus()) * 2;
-  if (tiles >= target) return 1;
-  const uint32_t s = cdiv(target, tiles);
-  const uint32_t cap = std::max<uint32_t>(1, ktiles / std::max<uint32_t>(1, min_kt));
-  return std::max<uint32_t>(1, std::min(s, cap));
+// Workgroups of one kernel instantiation that fit on a CU at once.
+template <class Kern>
+static int occupancy(Kern kernel) {
+  static std::map<const void*, int> cache;
+  const void* key = reinterpret_cast<const void*>(kernel);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, kThreads, 0) != hipSuccess || n < 1)
+    n = 1;
+  cache[key] = n;
+  return n;
+}
+
+// Estimated microseconds of one launch plus its split-K finish, used to pick
+// the split count.  The W = tiles * splits workgroups run in rounds of
+// cap = CUs * occupancy; in a round with r workgroups per CU, one K tile
+// takes max(kLatencyUs, r * tm), where tm is the K tile's MFMA time for a
+// lone workgroup (MT*NT*KT*2 flops at the CU's 614 GFLOP/s fp32 matrix peak)
+// and kLatencyUs the latency-bound floor.  Split partials cost
+// 2 * splits * M * N * 4 bytes at kFinishBytesPerUs.  The constants were
+// fitted to a tile/split sweep of the AlexNet convolutions on MI355X; they
+// pick within a few percent of the best measured configuration.
+constexpr double kCuFlopsPerUs = 614.4e3;
+constexpr double kLatencyUs = 3.0;
+constexpr double kFinishBytesPerUs = 1.0e6;
+static double est_us(uint32_t M, uint32_t N, uint32_t kdim, const TileCfg& c, int occ,
+                     bool partials) {
+  const double cus = num_cus();
+  const double tiles = double(cdiv(M, c.MT)) * cdiv(N, c.NT);
+  const double cap = cus * occ;
+  const double kps = double(cdiv(kdim, c.KT)) / c.splits;
+  const double tm = double(c.MT) * c.NT * c.KT * 2.0 / kCuFlopsPerUs;
+  const double W = tiles * c.splits;
+  const double full = std::floor(W / cap), rest = W - full * cap;
+  double T = kps * full * std::max(kLatencyUs, cap / cus * tm);
+  if (rest > 0) T += kps * std::max(kLatencyUs, rest / cus * tm);
+  if (partials) T += 2.0 * c.splits * double(M) * N * 4.0 / kFinishBytesPerUs;
+  return T;
+}
+
+// Tile / split choice for an M x N output with kdim-long dot products.  The
+// tile is 128 or 64 per axis (pick_tile); the split count minimises est_us
+// over 1..max_splits with at least 8 K tiles per split.  `occ(cfg)` gives the
+// occupancy of the kernel that cfg launches; `dense_out` says the unsplit
+// launch writes the final output (no partial buffer).
+template <class OccFn>
+static TileCfg choose(const char* var, uint32_t M, uint32_t N, uint32_t kdim, uint32_t max_splits,
+                      bool dense_out, OccFn&& occ) {
+  TileCfg c{pick_tile(M), pick_tile(N), 16, 1};
+  const uint32_t ktiles = cdiv(kdim, uint32_t(c.KT));
+  if (tune_override(var, c)) {
+    c.splits = std::max<uint32_t>(1, std::min<uint32_t>(c.splits, cdiv(kdim, uint32_t(c.KT))));
+    return c;
+  }
+  const uint32_t smax = std::max<uint32_t>(1, std::min(max_splits, ktiles / 8));
+  double best = 0;
+  uint32_t bestS = 1;
+  for (uint32_t sp = 1; sp <= smax; ++sp) {
+    TileCfg t = c;
+    t.splits = sp;
+    const double e = est_us(M, N, kdim, t, occ(t), sp > 1 || !dense_out);
+    if (sp == 1 || e < best) {
+      best = e;
+      bestS = sp;
+    }
+  }
+  c.splits = bestS;
+  return c;
 }
 
 template <int MT, int NT, int KT, class LA, class LB, class EPI>
 static bool launch(const typename LA::Params& pa, const typename LB::Params& pb,
                    const typename EPI::Params& pe, uint32_t M, uint32_t N, uint32_t ktiles,
                    uint32_t splits, const char* what) {
-  const dim3 grid(cdiv(N, NT), cdiv(M, MT), splits);
-  hipLaunchKernelGGL((k_igemm<MT, NT, KT, LA, LB, EPI>), grid, dim3(kThreads), 0, stream(), pa,
-                     pb, pe, ktiles, splits);
+  const TileGrid tg{cdiv(M, MT), cdiv(N, NT), xcd_order() ? 1u : 0u};
+  const uint32_t nwg = tg.gm * tg.gn * splits;
+  hipLaunchKernelGGL((k_igemm<MT, NT, KT, LA, LB, EPI>), dim3(nwg), dim3(kThreads), 0, stream(),
+                     pa, pb, pe, tg, ktiles, splits);
   return check_launch(what);
 }
 
 // Dispatch a functor over the four (MT, NT) tile shapes and two KT depths.
 template <class F>
-static bool tiles_dispatch(int MT, int NT, int KT, F&& f) {
-#define DCE_T(a, b, c) \
-  if (MT == a && NT == b && KT == c) return f.template run<a, b, c>();
+static bool tiles_dispatch(const TileCfg& c, F&& f) {
+#define DCE_T(a, b, k) \
+  if (c.MT == a && c.NT == b && c.KT == k) return f.template run<a, b, k>();
   DCE_T(128, 128, 32) DCE_T(128, 64, 32) DCE_T(64, 128, 32) DCE_T(64, 64, 32)
   DCE_T(128, 128, 16) DCE_T(128, 64, 16) DCE_T(64, 128, 16) DCE_T(64, 64, 16)
 #undef DCE_T
-  set_error("igemm: unsupported tile %dx%dx%d", MT, NT, KT);
+  set_error("igemm: unsupported tile %dx%dx%d", c.MT, c.NT, c.KT);
   return false;
 }
 
+// Occupancy of the kernel a functor would launch for cfg.
+template <class F>
+static int tiles_occ(const TileCfg& c, const F& f) {
+#define DCE_T(a, b, k) \
+  if (c.MT == a && c.NT == b && c.KT == k) return f.template occ<a, b, k>(c.splits > 1);
+  DCE_T(128, 128, 32) DCE_T(128, 64, 32) DCE_T(64, 128, 32) DCE_T(64, 64, 32)
+  DCE_T(128, 128, 16) DCE_T(128, 64, 16) DCE_T(64, 128, 16) DCE_T(64, 64, 16)
+#undef DCE_T
+  return 1;
+}
+
 static inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+static inline size_t al64(size_t n) { return (n + 63) & ~size_t(63); }
+
+static bool split_nchw(const float* part, const float* bias, float* out, uint32_t M, uint32_t N,
+                       uint32_t HW, uint32_t splits, uint32_t act) {
+  hipLaunchKernelGGL(k_splitk_nchw, dim3(cdiv(size_t(M) * N, 256)), dim3(256), 0, stream(), part,
+                     bias, out, M, N, HW, splits, act);
+  return check_launch("splitk_nchw");
+}
 
 // ----------------------------------------------------------------- GEMM
 template <bool AT, bool BT>
@@ -674,51 +844,88 @@ struct GemmRun {
   const float *a, *b;
   float* c;
   uint32_t M, K, N, splits;
+  uint32_t lda, ldb, kdA, kdB;  // row strides and K extents as stored (padded)
+  // A[m][k]: stored M x K (ROWK) or K x M (KROW); B[n][k]: stored N x K (ROWK) or K x N (KROW).
+  template <int MT, int KT>
+  using LAt = typename std::conditional<AT, LdDenseKR<MT, KT>, LdDenseRK<MT, KT>>::type;
+  template <int NT, int KT>
+  using LBt = typename std::conditional<BT, LdDenseRK<NT, KT>, LdDenseKR<NT, KT>>::type;
+  template <int MT, int NT, int KT>
+  int occ(bool) const {
+    return occupancy(k_igemm<MT, NT, KT, LAt<MT, KT>, LBt<NT, KT>, EpiRowMajor>);
+  }
   template <int MT, int NT, int KT>
   bool run() {
-    // A[m][k]: stored M×K (ROWK) or K×M (KROW); B[n][k]: stored N×K (ROWK) or K×N (KROW).
-    using LA = typename std::conditional<AT, LdDenseKR<MT, KT>, LdDenseRK<MT, KT>>::type;
-    using LB = typename std::conditional<BT, LdDenseRK<NT, KT>, LdDenseKR<NT, KT>>::type;
-    typename LA::Params pa{a, AT ? M : K, M, K, 0};
-    pa.vec = AT ? (M % 4 == 0 && aligned16(a)) : (K % 4 == 0 && aligned16(a));
-    typename LB::Params pb{b, BT ? K : N, N, K, 0};
-    pb.vec = BT ? (K % 4 == 0 && aligned16(b)) : (N % 4 == 0 && aligned16(b));
-    EpiRowMajor::Params pe{c, M, N, N, M * N};
-    return launch<MT, NT, KT, LA, LB, EpiRowMajor>(pa, pb, pe, M, N, cdiv(K, KT), splits, "gemm");
+    using LA = LAt<MT, KT>;
+    using LB = LBt<NT, KT>;
+    const typename LA::Params pa{a, lda, AT ? lda : M, kdA, (AT ? K : M) * lda};
+    const typename LB::Params pb{b, ldb, BT ? N : ldb, kdB, (BT ? N : K) * ldb};
+    const EpiRowMajor::Params pe{c, M, N, N, M * N};
+    return launch<MT, NT, KT, LA, LB, EpiRowMajor>(pa, pb, pe, M, N, cdiv(std::max(kdA, kdB), KT),
+                                                  splits, "gemm");
   }
 };
 
 bool gemm(const float* a, const float* b, float* c, uint32_t M, uint32_t K, uint32_t N,
           uint32_t flags) {
   if (K == 0) return fill_zero(c, size_t(M) * N);
-  const int KT = kt_choice();
-  const int MT = pick_tile(M), NT = pick_tile(N);
-  const uint32_t tiles = cdiv(M, MT) * cdiv(N, NT);
-  const uint32_t ktiles = cdiv(K, KT);
-  const uint32_t splits = pick_splits(tiles, ktiles, 8);
-  float* out = c;
-  if (splits > 1) {
-    out = workspace(size_t(splits) * M * N);
-    if (!out) return false;
+  const bool aT = flags & 1, bT = flags & 2;
+  if (!operand_fits(size_t(M) * pad4(K), "gemm") || !operand_fits(size_t(K) * pad4(N), "gemm") ||
+      !operand_fits(size_t(pad4(M)) * K, "gemm") || !operand_fits(size_t(N) * pad4(K), "gemm"))
+    return false;
+  // The dense loaders read whole quads along each operand's contiguous axis:
+  // a stride that is not a multiple of 4 (or an unaligned base) gets a
+  // zero-padded copy.
+  const uint32_t aRows = aT ? K : M, aCols = aT ? M : K;
+  const uint32_t bRows = bT ? N : K, bCols = bT ? K : N;
+  const bool padA = (aCols % 4) || !aligned16(a), padB = (bCols % 4) || !aligned16(b);
+  const TileCfg cfg = choose("DCE_TUNE_GEMM", M, N, pad4(K), 16, true, [&](const TileCfg& t) {
+    if (!aT && !bT) return tiles_occ(t, GemmRun<false, false>{});
+    if (!aT && bT) return tiles_occ(t, GemmRun<false, true>{});
+    if (aT && !bT) return tiles_occ(t, GemmRun<true, false>{});
+    return tiles_occ(t, GemmRun<true, true>{});
+  });
+  const size_t nA = padA ? al64(size_t(aRows) * pad4(aCols)) : 0;
+  const size_t nB = padB ? al64(size_t(bRows) * pad4(bCols)) : 0;
+  const size_t nP = cfg.splits > 1 ? size_t(cfg.splits) * M * N : 0;
+  float* ws = (nA + nB + nP) ? workspace(nA + nB + nP) : nullptr;
+  if ((nA + nB + nP) && !ws) return false;
+  const float* ap = a;
+  const float* bp = b;
+  if (padA) {
+    hipLaunchKernelGGL(k_pad_cols, dim3(cdiv(nA, 256)), dim3(256), 0, stream(), a, ws, aRows,
+                       aCols, pad4(aCols));
+    if (!check_launch("gemm_pad")) return false;
+    ap = ws;
   }
+  if (padB) {
+    hipLaunchKernelGGL(k_pad_cols, dim3(cdiv(nB, 256)), dim3(256), 0, stream(), b, ws + nA,
+                       bRows, bCols, pad4(bCols));
+    if (!check_launch("gemm_pad")) return false;
+    bp = ws + nA;
+  }
+  float* out = cfg.splits > 1 ? ws + nA + nB : c;
+  const uint32_t lda = pad4(aCols), ldb = pad4(bCols);
+  // K extents: a ROWK operand's k axis is its padded row (zeros past K); a
+  // KROW operand's k axis is its row count K.
+  const uint32_t kdA = aT ? K : lda, kdB = bT ? ldb : K;
   bool ok;
   {
     ProfScope prof("gemm", 2.0 * M * N * double(K),
                    4.0 * (double(M) * K + double(K) * N + double(M) * N));
-    const bool aT = flags & 1, bT = flags & 2;
     if (!aT && !bT)
-      ok = tiles_dispatch(MT, NT, KT, GemmRun<false, false>{a, b, out, M, K, N, splits});
+      ok = tiles_dispatch(cfg, GemmRun<false, false>{ap, bp, out, M, K, N, cfg.splits, lda, ldb, kdA, kdB});
     else if (!aT && bT)
-      ok = tiles_dispatch(MT, NT, KT, GemmRun<false, true>{a, b, out, M, K, N, splits});
+      ok = tiles_dispatch(cfg, GemmRun<false, true>{ap, bp, out, M, K, N, cfg.splits, lda, ldb, kdA, kdB});
     else if (aT && !bT)
-      ok = tiles_dispatch(MT, NT, KT, GemmRun<true, false>{a, b, out, M, K, N, splits});
+      ok = tiles_dispatch(cfg, GemmRun<true, false>{ap, bp, out, M, K, N, cfg.splits, lda, ldb, kdA, kdB});
     else
-      ok = tiles_dispatch(MT, NT, KT, GemmRun<true, true>{a, b, out, M, K, N, splits});
-  }
-  if (ok && splits > 1) {
-    hipLaunchKernelGGL(k_splitk_sum, dim3(cdiv(size_t(M) * N, 256)), dim3(256), 0, stream(), out,
-                       c, M * N, splits);
-    ok = check_launch("splitk_sum");
+      ok = tiles_dispatch(cfg, GemmRun<true, true>{ap, bp, out, M, K, N, cfg.splits, lda, ldb, kdA, kdB});
+    if (ok && cfg.splits > 1) {
+      hipLaunchKernelGGL(k_splitk_sum, dim3(cdiv(size_t(M) * N, 256)), dim3(256), 0, stream(),
+                         out, c, M * N, cfg.splits);
+      ok = check_launch("splitk_sum");
+    }
   }
   return ok;
 }
@@ -749,26 +956,42 @@ bool to_nhwc(const float* x, float* out, uint32_t B, uint32_t C, uint32_t H, uin
 }
 
 // ----------------------------------------------------------- conv forward
+// Output pixels as GEMM columns: split-K partials go to a row-major [M][N]
+// workspace and k_splitk_nchw finishes (bias, activation, NCHW scatter).
 template <bool S1>
 struct FwdRun {
   const float* wp;
   const float* xn;
   const float* bias;
   float* y;
+  float* part;
   ConvGeom g;
-  uint32_t act;
+  uint32_t act, splits;
+  template <int MT, int NT, int KT>
+  int occ(bool split) const {
+    using LA = LdDenseRK<MT, KT>;
+    using LB = LdPixRK<NT, KT, true, S1>;
+    return split ? occupancy(k_igemm<MT, NT, KT, LA, LB, EpiRowMajor>)
+                 : occupancy(k_igemm<MT, NT, KT, LA, LB, EpiNCHW>);
+  }
   template <int MT, int NT, int KT>
   bool run() {
     const uint32_t Cp = pad4(g.C), KK = g.k * g.k, kdim = KK * Cp;
     const uint32_t OHW = g.OH * g.OW, N = g.B * OHW;
     using LA = LdDenseRK<MT, KT>;
     using LB = LdPixRK<NT, KT, true, S1>;
-    typename LA::Params pa{wp, kdim, g.OC, kdim, 1};
-    typename LB::Params pb{xn, g.H, g.W, Cp, g.k, g.s, g.p, g.OW, OHW, N, kdim,
-                           make_fastdiv(OHW), make_fastdiv(g.OW), make_fastdiv(Cp), make_fastdiv(g.k)};
-    EpiNCHW::Params pe{y, bias, g.OC, OHW, N, act, make_fastdiv(OHW)};
-    return launch<MT, NT, KT, LA, LB, EpiNCHW>(pa, pb, pe, g.OC, N, cdiv(kdim, KT), 1,
-                                              "conv_forward");
+    const typename LA::Params pa{wp, kdim, g.OC, kdim, g.OC * kdim};
+    const typename LB::Params pb{xn, g.H, g.W, Cp, g.k, g.s, g.p, g.OW, OHW, N, kdim,
+                                 g.B * g.H * g.W * Cp, make_fastdiv(OHW), make_fastdiv(g.OW),
+                                 make_fastdiv(Cp), make_fastdiv(g.k)};
+    const uint32_t kt = cdiv(kdim, KT);
+    if (splits > 1) {
+      const EpiRowMajor::Params pe{part, g.OC, N, N, g.OC * N};
+      return launch<MT, NT, KT, LA, LB, EpiRowMajor>(pa, pb, pe, g.OC, N, kt, splits,
+                                                    "conv_forward");
+    }
+    const EpiNCHW::Params pe{y, bias, g.OC, OHW, N, act, make_fastdiv(OHW)};
+    return launch<MT, NT, KT, LA, LB, EpiNCHW>(pa, pb, pe, g.OC, N, kt, 1, "conv_forward");
   }
 };
 
@@ -776,21 +999,35 @@ bool conv_forward(const float* x, float* x_nhwc_keep, const float* w, const floa
                   float* y, const ConvGeom& g, uint32_t act) {
   const uint32_t Cp = pad4(g.C), KK = g.k * g.k;
   const size_t nx = nhwc_floats(g.B, g.C, g.H, g.W);
-  const size_t nw = (size_t(g.OC) * KK * Cp + 63) & ~size_t(63);
-  float* ws = workspace(nw + (x_nhwc_keep ? 0 : nx));
+  const uint32_t N = g.B * g.OH * g.OW;
+  if (!operand_fits(nx, "conv_forward") || !operand_fits(size_t(g.OC) * KK * Cp, "conv_forward"))
+    return false;
+  const TileCfg cfg = choose("DCE_TUNE_FWD", g.OC, N, KK * Cp, 8, true, [&](const TileCfg& t) {
+    return g.s == 1 ? tiles_occ(t, FwdRun<true>{}) : tiles_occ(t, FwdRun<false>{});
+  });
+  const size_t nw = al64(size_t(g.OC) * KK * Cp);
+  const size_t nxs = x_nhwc_keep ? 0 : al64(nx);
+  const size_t nP = cfg.splits > 1 ? size_t(cfg.splits) * g.OC * N : 0;
+  float* ws = workspace(nw + nxs + nP);
   if (!ws) return false;
   float* wp = ws;
   float* xn = x_nhwc_keep ? x_nhwc_keep : ws + nw;
+  float* part = ws + nw + nxs;
   if (!to_nhwc(x, xn, g.B, g.C, g.H, g.W)) return false;
   hipLaunchKernelGGL(k_permute_w, dim3(cdiv(size_t(g.OC) * KK * Cp, 256)), dim3(256), 0, stream(),
                      w, wp, g.OC, g.C, KK, Cp, 0);
   if (!check_launch("permute_w")) return false;
   const double fl = 2.0 * g.OC * g.C * KK * double(g.B) * g.OH * g.OW;
-  ProfScope prof("conv_fwd", fl,
-                 4.0 * (double(g.B) * g.C * g.H * g.W + double(g.B) * g.OC * g.OH * g.OW));
-  const int MT = pick_tile(g.OC), NT = 128, KT = kt_choice();
-  if (g.s == 1) return tiles_dispatch(MT, NT, KT, FwdRun<true>{wp, xn, bias, y, g, act});
-  return tiles_dispatch(MT, NT, KT, FwdRun<false>{wp, xn, bias, y, g, act});
+  {
+    ProfScope prof("conv_fwd", fl,
+                   4.0 * (double(g.B) * g.C * g.H * g.W + double(g.B) * g.OC * g.OH * g.OW));
+    const bool ok = g.s == 1
+        ? tiles_dispatch(cfg, FwdRun<true>{wp, xn, bias, y, part, g, act, cfg.splits})
+        : tiles_dispatch(cfg, FwdRun<false>{wp, xn, bias, y, part, g, act, cfg.splits});
+    if (!ok) return false;
+    if (cfg.splits > 1) return split_nchw(part, bias, y, g.OC, N, g.OH * g.OW, cfg.splits, act);
+  }
+  return true;
 }
 
 // ----------------------------------------------------------- conv backward
@@ -801,15 +1038,20 @@ struct DwRun {
   ConvGeom g;
   uint32_t splits;
   template <int MT, int NT, int KT>
+  int occ(bool) const {
+    return occupancy(k_igemm<MT, NT, KT, LdGradKR<MT, KT>, LdXTapKR<NT, KT>, EpiRowMajor>);
+  }
+  template <int MT, int NT, int KT>
   bool run() {
     const uint32_t Cp = pad4(g.C), OCp = pad4(g.OC), KK = g.k * g.k, N = KK * Cp;
     const uint32_t OHW = g.OH * g.OW, npix = g.B * OHW;
     using LA = LdGradKR<MT, KT>;
     using LB = LdXTapKR<NT, KT>;
-    typename LA::Params pa{gn, OCp, npix};
-    typename LB::Params pb{xn, g.H, g.W, Cp, g.k, g.s, g.p, g.OW, OHW, npix, N,
-                           make_fastdiv(OHW), make_fastdiv(g.OW), make_fastdiv(Cp), make_fastdiv(g.k)};
-    EpiRowMajor::Params pe{part, g.OC, N, N, g.OC * N};
+    const typename LA::Params pa{gn, OCp, npix, npix * OCp};
+    const typename LB::Params pb{xn, g.H, g.W, Cp, g.k, g.s, g.p, g.OW, OHW, npix, N,
+                                 g.B * g.H * g.W * Cp, make_fastdiv(OHW), make_fastdiv(g.OW),
+                                 make_fastdiv(Cp), make_fastdiv(g.k)};
+    const EpiRowMajor::Params pe{part, g.OC, N, N, g.OC * N};
     return launch<MT, NT, KT, LA, LB, EpiRowMajor>(pa, pb, pe, g.OC, N, cdiv(npix, KT), splits,
                                                   "conv_backward_filter");
   }
@@ -820,53 +1062,73 @@ struct DxRun {
   const float* wt;
   const float* gn;
   float* dx;
+  float* part;
   ConvGeom g;
+  uint32_t splits;
+  template <int MT, int NT, int KT>
+  int occ(bool split) const {
+    using LA = LdDenseRK<MT, KT>;
+    using LB = LdPixRK<NT, KT, false, S1>;
+    return split ? occupancy(k_igemm<MT, NT, KT, LA, LB, EpiRowMajor>)
+                 : occupancy(k_igemm<MT, NT, KT, LA, LB, EpiNCHW>);
+  }
   template <int MT, int NT, int KT>
   bool run() {
     const uint32_t OCp = pad4(g.OC), KK = g.k * g.k, kdim = KK * OCp;
     const uint32_t HW = g.H * g.W, N = g.B * HW;
     using LA = LdDenseRK<MT, KT>;
     using LB = LdPixRK<NT, KT, false, S1>;
-    typename LA::Params pa{wt, kdim, g.C, kdim, 1};
-    typename LB::Params pb{gn, g.OH, g.OW, OCp, g.k, g.s, g.p, g.W, HW, N, kdim,
-                           make_fastdiv(HW), make_fastdiv(g.W), make_fastdiv(OCp), make_fastdiv(g.k)};
-    EpiNCHW::Params pe{dx, nullptr, g.C, HW, N, 0, make_fastdiv(HW)};
-    return launch<MT, NT, KT, LA, LB, EpiNCHW>(pa, pb, pe, g.C, N, cdiv(kdim, KT), 1,
-                                              "conv_backward_input");
+    const typename LA::Params pa{wt, kdim, g.C, kdim, g.C * kdim};
+    const typename LB::Params pb{gn, g.OH, g.OW, OCp, g.k, g.s, g.p, g.W, HW, N, kdim,
+                                 g.B * g.OH * g.OW * OCp, make_fastdiv(HW), make_fastdiv(g.W),
+                                 make_fastdiv(OCp), make_fastdiv(g.k)};
+    const uint32_t kt = cdiv(kdim, KT);
+    if (splits > 1) {
+      const EpiRowMajor::Params pe{part, g.C, N, N, g.C * N};
+      return launch<MT, NT, KT, LA, LB, EpiRowMajor>(pa, pb, pe, g.C, N, kt, splits,
+                                                    "conv_backward_input");
+    }
+    const EpiNCHW::Params pe{dx, nullptr, g.C, HW, N, 0, make_fastdiv(HW)};
+    return launch<MT, NT, KT, LA, LB, EpiNCHW>(pa, pb, pe, g.C, N, kt, 1, "conv_backward_input");
   }
 };
-
-static inline size_t al64(size_t n) { return (n + 63) & ~size_t(63); }
 
 bool conv_backward(const float* dy, const float* y, const float* x, const float* x_nhwc,
                    const float* w, float* dw, float* db, float* dx, const ConvGeom& g) {
   const uint32_t Cp = pad4(g.C), OCp = pad4(g.OC), KK = g.k * g.k;
-  const uint32_t OHW = g.OH * g.OW, npix = g.B * OHW;
-  const int KT = kt_choice();
+  const uint32_t OHW = g.OH * g.OW, npix = g.B * OHW, HW = g.H * g.W;
+  if (!operand_fits(size_t(npix) * OCp, "conv_backward") ||
+      !operand_fits(nhwc_floats(g.B, g.C, g.H, g.W), "conv_backward") ||
+      !operand_fits(size_t(g.C) * KK * OCp, "conv_backward"))
+    return false;
   // Workspace carve-up: G (NHWC), db partials, x (NHWC) if not kept by the
-  // forward, dW split-K partials, dX filters.
+  // forward, dW split-K partials, dX filters, dX split-K partials.
   const uint32_t npb = cdiv(OHW, 64);
   const size_t nG = al64(size_t(npix) * OCp);
   const size_t nDb = db ? al64(size_t(g.B) * npb * g.OC) : 0;
   const size_t nX = (dw && !x_nhwc) ? al64(nhwc_floats(g.B, g.C, g.H, g.W)) : 0;
-  int dMT = 128, dNT = 128;
-  uint32_t splits = 1;
-  size_t nP = 0;
+  TileCfg dwc{128, 128, 16, 1}, dxc{128, 128, 16, 1};
+  size_t nP = 0, nW = 0, nQ = 0;
   if (dw) {
-    dMT = pick_tile(g.OC);
-    dNT = pick_tile(KK * Cp);
-    const uint32_t tiles = cdiv(g.OC, dMT) * cdiv(KK * Cp, dNT);
-    splits = pick_splits(tiles, cdiv(npix, KT), 8);
-    nP = al64(size_t(splits) * g.OC * KK * Cp);
+    dwc = choose("DCE_TUNE_DW", g.OC, KK * Cp, npix, 256, false,
+                 [&](const TileCfg& t) { return tiles_occ(t, DwRun{}); });
+    nP = al64(size_t(dwc.splits) * g.OC * KK * Cp);
   }
-  const size_t nW = dx ? al64(size_t(g.C) * KK * OCp) : 0;
-  float* ws = workspace(nG + nDb + nX + nP + nW);
+  if (dx) {
+    dxc = choose("DCE_TUNE_DX", g.C, g.B * HW, KK * OCp, 8, true, [&](const TileCfg& t) {
+      return g.s == 1 ? tiles_occ(t, DxRun<true>{}) : tiles_occ(t, DxRun<false>{});
+    });
+    nW = al64(size_t(g.C) * KK * OCp);
+    nQ = dxc.splits > 1 ? size_t(dxc.splits) * g.C * g.B * HW : 0;
+  }
+  float* ws = workspace(nG + nDb + nX + nP + nW + nQ);
   if (!ws) return false;
   float* gn = ws;
   float* dbPart = db ? gn + nG : nullptr;
   float* xs = ws + nG + nDb;
   float* part = xs + nX;
   float* wt = part + nP;
+  float* qpart = wt + nW;
 
   uint32_t npbGot = npb;
   if (!to_nhwc_masked(dy, y, gn, dbPart, g.B, g.OC, OHW, &npbGot)) return false;
@@ -885,22 +1147,28 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
       const double fl = 2.0 * g.OC * g.C * KK * double(npix);
       ProfScope prof("conv_dw", fl,
                      4.0 * (double(npix) * OCp + double(g.B) * g.H * g.W * Cp + double(g.OC) * KK * Cp));
-      ok = tiles_dispatch(dMT, dNT, KT, DwRun{gn, xn, part, g, splits});
+      ok = tiles_dispatch(dwc, DwRun{gn, xn, part, g, dwc.splits});
+      if (ok) {
+        hipLaunchKernelGGL(k_dw_final, dim3(cdiv(size_t(g.OC) * KK * Cp, 256)), dim3(256), 0,
+                           stream(), part, dw, g.OC, g.C, KK, Cp, dwc.splits);
+        ok = check_launch("dw_final");
+      }
     }
     if (!ok) return false;
-    hipLaunchKernelGGL(k_dw_final, dim3(cdiv(size_t(g.OC) * g.C * KK, 256)), dim3(256), 0,
-                       stream(), part, dw, g.OC, g.C, KK, Cp, splits);
-    if (!check_launch("dw_final")) return false;
   }
   if (dx) {
     hipLaunchKernelGGL(k_permute_w, dim3(cdiv(size_t(g.C) * KK * OCp, 256)), dim3(256), 0,
                        stream(), w, wt, g.OC, g.C, KK, OCp, 1);
     if (!check_launch("permute_w")) return false;
     const double fl = 2.0 * g.OC * g.C * KK * double(npix);
-    ProfScope prof("conv_dx", fl, 4.0 * (double(npix) * OCp + double(g.B) * g.C * g.H * g.W));
-    const int MT = pick_tile(g.C), NT = 128;
-    if (g.s == 1) return tiles_dispatch(MT, NT, KT, DxRun<true>{wt, gn, dx, g});
-    return tiles_dispatch(MT, NT, KT, DxRun<false>{wt, gn, dx, g});
+    {
+      ProfScope prof("conv_dx", fl, 4.0 * (double(npix) * OCp + double(g.B) * g.C * g.H * g.W));
+      const bool ok = g.s == 1
+          ? tiles_dispatch(dxc, DxRun<true>{wt, gn, dx, qpart, g, dxc.splits})
+          : tiles_dispatch(dxc, DxRun<false>{wt, gn, dx, qpart, g, dxc.splits});
+      if (!ok) return false;
+      if (dxc.splits > 1) return split_nchw(qpart, nullptr, dx, g.C, g.B * HW, HW, dxc.splits, 0);
+    }
   }
   return true;
 }

@@ -195,3 +195,29 @@ def test_single_conv_full_size_sampled(eng):
         ref_s.append(acc)
         got_s.append(dX[bb, :, ih, iw])
     assert rel_err(np.array(got_s), np.array(ref_s)) <= TOL
+
+
+TILE_CFGS = [f"{mt},{nt},{kt},{sp}" for mt in (64, 128) for nt in (64, 128) for kt in (16, 32)
+             for sp in (1, 3)]
+
+
+@pytest.mark.parametrize("cfg", TILE_CFGS)
+def test_forced_tile_configs(eng, monkeypatch, cfg):
+    """Every tile shape, K depth and split-K count (forced through the
+    DCE_TUNE_* overrides, split-K included for the forward and dX GEMMs that
+    the heuristic never splits) gives the oracle's result."""
+    for var in ("DCE_TUNE_FWD", "DCE_TUNE_DW", "DCE_TUNE_DX", "DCE_TUNE_GEMM"):
+        monkeypatch.setenv(var, cfg)
+    _conv_case(eng, 2, 16, 14, 14, 20, 3, 2, 1, 1)   # stride 2, OC not a multiple of 16
+    _conv_case(eng, 2, 48, 10, 10, 16, 3, 1, 1, 1)   # stride 1
+    for flags in range(4):
+        test_matmul_alloc(eng, 127, 129, 130, flags)
+        test_matmul_alloc(eng, 5, 7, 3, flags)
+
+
+def test_linear_tile_order(eng, monkeypatch):
+    """DCE_XCD=0 (plain tile order) gives the same results as the default
+    XCD-contiguous order."""
+    monkeypatch.setenv("DCE_XCD", "0")
+    _conv_case(eng, 2, 64, 13, 13, 192, 5, 1, 2, 1)
+    test_matmul_alloc(eng, 200, 300, 100, 0)
