@@ -582,14 +582,21 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// Few channels (Cp <= 8): one thread per output element.
+// Few channels (Cp <= 8): one thread per pixel reads its C channel values
+// (coalesced across threads per channel) and stores Cp/4 quads.
 __global__ void k_to_nhwc_small(const float* __restrict__ in, float* __restrict__ out, uint32_t C,
-                                uint32_t HW, uint32_t Cp, uint32_t total) {
-  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= total) return;
-  const uint32_t bp = i / Cp, c = i - bp * Cp;
-  const uint32_t b = bp / HW, p = bp - b * HW;
-  out[i] = c < C ? in[(size_t(b) * C + c) * HW + p] : 0.f;
+                                uint32_t HW, uint32_t Cp, uint32_t npix, FastDiv dHW) {
+  const uint32_t n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= npix) return;
+  const uint32_t b = fdiv(n, dHW), p = n - b * HW;
+  const float* src = in + size_t(b) * C * HW + p;
+  f4* dst = reinterpret_cast<f4*>(out + size_t(n) * Cp);
+  for (uint32_t q = 0; q < Cp / 4; ++q) {
+    f4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = (4 * q + e < C) ? src[size_t(4 * q + e) * HW] : 0.f;
+    dst[q] = v;
+  }
 }
 
 // out[c] = sum of the `rows` partials of channel c (stored contiguously,
@@ -636,22 +643,34 @@ __global__ void k_splitk_sum(const float* __restrict__ part, float* __restrict__
   out[i] = s;
 }
 
-// dW finalize: dw[oc][c][khw] = sum_z part[z][oc][khw*Cp + c], z in order.
-// One thread per partial column in storage order, so the splits x OC x KK*Cp
-// partial reads (the bulk of the traffic) are coalesced; padding channels
-// (c >= C) are skipped.
-__global__ void k_dw_final(const float* __restrict__ part, float* __restrict__ dw, uint32_t OC,
-                           uint32_t C, uint32_t KK, uint32_t Cp, uint32_t splits) {
+// dW finalize: dw[oc][c][khw] = sum_z part[z][oc][khw*Cp + c].  Block of
+// 1024 = 64 consecutive partial columns (storage order, so the
+// splits x OC x KK*Cp partial reads are coalesced) x 16 split slices: slice w
+// sums z = w, w+16, ..., then the 16 slice sums are added in slice order.
+// Padding channels (c >= C) are dropped.
+__global__ void __launch_bounds__(1024)
+    k_dw_final(const float* __restrict__ part, float* __restrict__ dw, uint32_t OC, uint32_t C,
+               uint32_t KK, uint32_t Cp, uint32_t splits) {
+  __shared__ float sh[16][64];
   const uint32_t N = KK * Cp;
-  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= OC * N) return;
-  const uint32_t oc = i / N, n = i - oc * N;
-  const uint32_t khw = n / Cp, c = n - khw * Cp;
-  if (c >= C) return;
+  const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const uint32_t i = blockIdx.x * 64 + lane;
+  const bool ok = i < OC * N;
   const size_t zs = size_t(OC) * N;
   float s = 0.f;
-  for (uint32_t z = 0; z < splits; ++z) s += part[z * zs + i];
-  dw[(size_t(oc) * C + c) * KK + khw] = s;
+  if (ok) {
+#pragma unroll 4
+    for (uint32_t z = w; z < splits; z += 16) s += part[z * zs + i];
+  }
+  sh[w][lane] = s;
+  __syncthreads();
+  if (w != 0 || !ok) return;
+  float t = 0.f;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) t += sh[k][lane];
+  const uint32_t oc = i / N, n = i - oc * N;
+  const uint32_t khw = n / Cp, c = n - khw * Cp;
+  if (c < C) dw[(size_t(oc) * C + c) * KK + khw] = t;
 }
 
 // Split-K finish for an NCHW output: out[b][m][pix] = act(sum_z part[z][m][n]
@@ -939,9 +958,9 @@ static bool to_nhwc_masked(const float* in, const float* y, float* out, float* d
                            uint32_t B, uint32_t C, uint32_t HW, uint32_t* npbOut) {
   const uint32_t Cp = pad4(C);
   if (Cp <= 8 && !y && !dbPart) {
-    const size_t total = size_t(B) * HW * Cp;
-    hipLaunchKernelGGL(k_to_nhwc_small, dim3(cdiv(total, 256)), dim3(256), 0, stream(), in, out,
-                       C, HW, Cp, uint32_t(total));
+    const uint32_t npix = B * HW;
+    hipLaunchKernelGGL(k_to_nhwc_small, dim3(cdiv(npix, 256)), dim3(256), 0, stream(), in, out, C,
+                       HW, Cp, npix, make_fastdiv(HW));
     return check_launch("to_nhwc");
   }
   const uint32_t npb = cdiv(HW, 64);
@@ -1149,7 +1168,7 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
                      4.0 * (double(npix) * OCp + double(g.B) * g.H * g.W * Cp + double(g.OC) * KK * Cp));
       ok = tiles_dispatch(dwc, DwRun{gn, xn, part, g, dwc.splits});
       if (ok) {
-        hipLaunchKernelGGL(k_dw_final, dim3(cdiv(size_t(g.OC) * KK * Cp, 256)), dim3(256), 0,
+        hipLaunchKernelGGL(k_dw_final, dim3(cdiv(size_t(g.OC) * KK * Cp, 64)), dim3(1024), 0,
                            stream(), part, dw, g.OC, g.C, KK, Cp, dwc.splits);
         ok = check_launch("dw_final");
       }

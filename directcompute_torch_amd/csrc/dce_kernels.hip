@@ -230,13 +230,27 @@ static bool sh_add_bias_t(const Dispatch& d) {
 // row-major matrix: one thread per column, coalesced over columns) and
 // stride_i == 1 (contiguous rows: one block per class).
 // ===========================================================================
-__global__ void k_bias_grad_cols(Buf G, Buf g, uint32_t rows, uint32_t classes, uint32_t si,
-                                 uint32_t sid) {
-  const uint32_t c = gtid();
-  if (c >= classes) return;
+// Block of 1024 = 64 columns x 16 row slices: lane l takes column
+// 64*block + l, wave w rows w, w+16, ...; the 16 slice sums of a column are
+// then added in slice order.
+__global__ void __launch_bounds__(1024)
+    k_bias_grad_cols(Buf G, Buf g, uint32_t rows, uint32_t classes, uint32_t si, uint32_t sid) {
+  __shared__ float sh[16][64];
+  const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const uint32_t c = blockIdx.x * 64 + lane;
   float s = 0.f;
-  for (uint32_t i = 0; i < rows; ++i) s += ld(G, i * si + c * sid);
-  st(g, c, s);
+  if (c < classes) {
+#pragma unroll 8
+    for (uint32_t i = w; i < rows; i += 16) s += ld(G, i * si + c * sid);
+  }
+  sh[w][lane] = s;
+  __syncthreads();
+  if (w == 0 && c < classes) {
+    float t = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) t += sh[k][lane];
+    st(g, c, t);
+  }
 }
 __global__ void k_bias_grad_rows(Buf G, Buf g, uint32_t rows, uint32_t si, uint32_t sid) {
   __shared__ double sh[4];
@@ -253,7 +267,7 @@ static bool sh_bias_grad(const Dispatch& d) {
     hipLaunchKernelGGL(k_bias_grad_rows, dim3(classes), dim3(256), 0, stream(), S(d, 0), U(d, 0),
                        rows, si, sid);
   } else {
-    hipLaunchKernelGGL(k_bias_grad_cols, dim3(cdiv(classes, 256)), dim3(256), 0, stream(),
+    hipLaunchKernelGGL(k_bias_grad_cols, dim3(cdiv(classes, 64)), dim3(1024), 0, stream(),
                        S(d, 0), U(d, 0), rows, classes, si, sid);
   }
   return check_launch("bias_grad");
@@ -658,10 +672,54 @@ __global__ void k_maxpool_fwd(Buf x, Buf out, Buf idx, uint32_t BC, uint32_t H, 
   st(idx, o, __uint_as_float(mi));
 }
 
+// Fused-path forward for windows that lie inside the input (floor mode):
+// K x K window unrolled, every load unconditional, same first-max rule.
+template <int K>
+__global__ void k_maxpool_fwd_k(const float* __restrict__ x, float* __restrict__ out,
+                                uint32_t* __restrict__ idx, uint32_t total, uint32_t H, uint32_t W,
+                                uint32_t s, uint32_t OH, uint32_t OW, FastDiv dOW, FastDiv dOH) {
+  const uint32_t o = gtid();
+  if (o >= total) return;
+  const uint32_t t = fdiv(o, dOW);
+  const uint32_t ow = o - t * OW;
+  const uint32_t bc = fdiv(t, dOH);
+  const uint32_t oh = t - bc * OH;
+  const uint32_t base = bc * H * W + oh * s * W + ow * s;
+  float v[K][K];
+#pragma unroll
+  for (int a = 0; a < K; ++a)
+#pragma unroll
+    for (int b = 0; b < K; ++b) v[a][b] = x[base + a * W + b];
+  float mx = -1e30f;
+  uint32_t mi = 0xFFFFFFFFu;
+#pragma unroll
+  for (int a = 0; a < K; ++a)
+#pragma unroll
+    for (int b = 0; b < K; ++b)
+      if (v[a][b] > mx) {
+        mx = v[a][b];
+        mi = base + a * W + b;
+      }
+  out[o] = mx;
+  idx[o] = mi;
+}
+
 bool maxpool_forward(const float* x, float* out, float* idx, uint32_t B, uint32_t C, uint32_t H,
                      uint32_t W, uint32_t k, uint32_t s, uint32_t OH, uint32_t OW) {
   const uint32_t n = B * C * OH * OW;
   ProfScope prof("maxpool_fwd", 0, 4.0 * double(B) * C * H * W + 8.0 * n);
+  const bool inside = n && s && (OH - 1) * s + k <= H && (OW - 1) * s + k <= W;
+  if (inside && (k == 2 || k == 3)) {
+    uint32_t* ip = reinterpret_cast<uint32_t*>(idx);
+    const FastDiv fOW = make_fastdiv(OW), fOH = make_fastdiv(OH);
+    if (k == 2)
+      hipLaunchKernelGGL(k_maxpool_fwd_k<2>, dim3(cdiv(n, 256)), dim3(256), 0, stream(), x, out, ip,
+                         n, H, W, s, OH, OW, fOW, fOH);
+    else
+      hipLaunchKernelGGL(k_maxpool_fwd_k<3>, dim3(cdiv(n, 256)), dim3(256), 0, stream(), x, out, ip,
+                         n, H, W, s, OH, OW, fOW, fOH);
+    return check_launch("maxpool_forward");
+  }
   hipLaunchKernelGGL(k_maxpool_fwd, dim3(cdiv(n, 256)), dim3(256), 0, stream(),
                      Buf{const_cast<float*>(x), B * C * H * W}, Buf{out, n}, Buf{idx, n}, B * C,
                      H, W, k, s, OH, OW);
@@ -693,6 +751,47 @@ __global__ void k_maxpool_bwd_gather(const float* __restrict__ dz, const uint32_
     }
   dx[i] = acc;
 }
+// Same gather with at most NW windows per axis covering an input element
+// (NW = ceil(k / s)): all NW*NW (index, value) pairs are loaded up front from
+// clamped in-plane addresses, then the matching ones are added in (oh, ow)
+// order -- no load waits on a compare.
+template <int NW>
+__global__ void k_maxpool_bwd_gather_n(const float* __restrict__ dz,
+                                       const uint32_t* __restrict__ idx, float* __restrict__ dx,
+                                       uint32_t total, uint32_t H, uint32_t W, uint32_t k,
+                                       uint32_t OH, uint32_t OW, FastDiv dW, FastDiv dH,
+                                       FastDiv dS) {
+  const uint32_t i = gtid();
+  if (i >= total) return;
+  const uint32_t t = fdiv(i, dW);
+  const uint32_t iw = i - t * W;
+  const uint32_t bc = fdiv(t, dH);
+  const uint32_t ih = t - bc * H;
+  const uint32_t s = dS.d;
+  const uint32_t ohlo = (ih + 1 >= k) ? fdiv(ih + 1 - k + s - 1, dS) : 0;
+  const uint32_t ohhi = min(fdiv(ih, dS), OH - 1);
+  const uint32_t owlo = (iw + 1 >= k) ? fdiv(iw + 1 - k + s - 1, dS) : 0;
+  const uint32_t owhi = min(fdiv(iw, dS), OW - 1);
+  const uint32_t ob = bc * OH * OW;
+  uint32_t id[NW][NW];
+  float v[NW][NW];
+#pragma unroll
+  for (int a = 0; a < NW; ++a)
+#pragma unroll
+    for (int b = 0; b < NW; ++b) {
+      const uint32_t o = ob + min(ohlo + a, OH - 1) * OW + min(owlo + b, OW - 1);
+      id[a][b] = idx[o];
+      v[a][b] = dz[o];
+    }
+  float acc = 0.f;
+#pragma unroll
+  for (int a = 0; a < NW; ++a)
+#pragma unroll
+    for (int b = 0; b < NW; ++b)
+      if (ohlo + a <= ohhi && owlo + b <= owhi && id[a][b] == i) acc += v[a][b];
+  dx[i] = acc;
+}
+
 // Fallback when the pooling geometry is unknown: zero + scatter-add.
 __global__ void k_maxpool_bwd_scatter(Buf dz, const uint32_t* idx, Buf dx, uint32_t n) {
   const uint32_t o = gtid();
@@ -708,8 +807,22 @@ bool maxpool_backward(const float* dz, const float* idx, float* dx, uint32_t B, 
   ProfScope prof("maxpool_bwd", 0, 8.0 * n + 4.0 * xcount);
   const uint32_t* ip = reinterpret_cast<const uint32_t*>(idx);
   if (k && s && H && W) {
-    hipLaunchKernelGGL(k_maxpool_bwd_gather, dim3(cdiv(xcount, 256)), dim3(256), 0, stream(), dz,
-                       ip, dx, xcount, H, W, k, s, OH, OW, make_fastdiv(W), make_fastdiv(H));
+    if (n == 0) return fill_zero(dx, xcount);
+    const uint32_t nw = (k + s - 1) / s;
+    const dim3 grid(cdiv(xcount, 256));
+    const FastDiv fW = make_fastdiv(W), fH = make_fastdiv(H), fS = make_fastdiv(s);
+    if (nw == 1)
+      hipLaunchKernelGGL(k_maxpool_bwd_gather_n<1>, grid, dim3(256), 0, stream(), dz, ip, dx,
+                         xcount, H, W, k, OH, OW, fW, fH, fS);
+    else if (nw == 2)
+      hipLaunchKernelGGL(k_maxpool_bwd_gather_n<2>, grid, dim3(256), 0, stream(), dz, ip, dx,
+                         xcount, H, W, k, OH, OW, fW, fH, fS);
+    else if (nw == 3)
+      hipLaunchKernelGGL(k_maxpool_bwd_gather_n<3>, grid, dim3(256), 0, stream(), dz, ip, dx,
+                         xcount, H, W, k, OH, OW, fW, fH, fS);
+    else
+      hipLaunchKernelGGL(k_maxpool_bwd_gather, grid, dim3(256), 0, stream(), dz, ip, dx, xcount, H,
+                         W, k, s, OH, OW, fW, fH);
     return check_launch("maxpool_backward");
   }
   if (!fill_zero(dx, xcount)) return false;
