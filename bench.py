@@ -131,6 +131,21 @@ def cpu_baseline(sample=64):
                       f"float64 NumPy oracle, {blas}, {dt:.1f} s"}
 
 
+def copy_calibration(mib=256, reps=3):
+    """Plain elementwise copy (torch's mul-by-one kernel) of `mib` MiB: each
+    launch reads and writes exactly mib MiB, so its counter readings give the
+    scale between rocprofv3's FETCH_SIZE / WRITE_SIZE and bytes."""
+    import torch
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration": {"bytes_read": n * 4, "bytes_written": n * 4,
+                                           "launches": reps}}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -138,10 +153,16 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=64)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain device copy of 256 MiB three times (the reference "
+                         "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1"}))
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration()
+        return
 
     from directcompute_torch_amd import nn_engine as nn
     lib = nn.lib
