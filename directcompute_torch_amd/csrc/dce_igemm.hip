@@ -60,16 +60,19 @@ struct Stage {
   static constexpr int Q = R * KT / 4 / kThreads;
   // Quad i of thread t.  ROWK: consecutive lanes take consecutive k-quads of
   // one row; KROW: consecutive lanes take consecutive row-quads of one k.
+  // kThreads is a multiple of KQ and RQ, so quad i sits DROW rows (ROWK) or
+  // DK k-steps (KROW) past quad 0, and DLDS floats past it in LDS.
+  static constexpr int DROW = KROW ? 0 : kThreads / KQ;
+  static constexpr int DK = KROW ? kThreads / RQ : 0;
+  static constexpr int DLDS = KROW ? DK * LD : DROW * LD;
   __device__ static __forceinline__ int qrow(int t, int i) {
-    const int q = t + kThreads * i;
-    return KROW ? 4 * (q % RQ) : q / KQ;
+    return KROW ? 4 * (t % RQ) : t / KQ + DROW * i;
   }
   __device__ static __forceinline__ int qk(int t, int i) {
-    const int q = t + kThreads * i;
-    return KROW ? q / RQ : 4 * (q % KQ);
+    return KROW ? t / RQ + DK * i : 4 * (t % KQ);
   }
-  __device__ static __forceinline__ int lds_off(int t, int i) {
-    return KROW ? qk(t, i) * LD + qrow(t, i) : qrow(t, i) * LD + qk(t, i);
+  __device__ static __forceinline__ int lds_off(int t) {
+    return KROW ? qk(t, 0) * LD + qrow(t, 0) : qrow(t, 0) * LD + qk(t, 0);
   }
   // MFMA operand of 16 rows starting at rb, k slice kb: components s = 0..3.
   __device__ static __forceinline__ f4 frag(const float* S, int rb, int r, int g, int kb) {
@@ -84,14 +87,11 @@ struct Stage {
 template <class St>
 struct LoaderBase {
   static constexpr int Q = St::Q;
-  int lds[Q];
-  __device__ __forceinline__ void base_init(int tid) {
-#pragma unroll
-    for (int i = 0; i < Q; ++i) lds[i] = St::lds_off(tid, i);
-  }
+  int lds0;
+  __device__ __forceinline__ void base_init(int tid) { lds0 = St::lds_off(tid); }
   __device__ __forceinline__ void store(float* S, const f4 (&r)[Q]) const {
 #pragma unroll
-    for (int i = 0; i < Q; ++i) *reinterpret_cast<f4*>(S + lds[i]) = r[i];
+    for (int i = 0; i < Q; ++i) *reinterpret_cast<f4*>(S + lds0 + i * St::DLDS) = r[i];
   }
 };
 
@@ -132,25 +132,24 @@ struct LdDenseRK : LoaderBase<Stage<R, KT, false>> {
     uint32_t ld, rows, kdim, n;  // n: floats in the buffer
   };
   BRes b;
-  uint32_t kdim;
-  uint32_t base[Q], kq[Q];
+  uint32_t kdim, kq;
+  uint32_t base[Q];
   __device__ __forceinline__ void init(const Params& P, uint32_t row0, int tid) {
     this->base_init(tid);
     b.init(P.p, P.n);
     kdim = P.kdim;
+    kq = St::qk(tid, 0);
 #pragma unroll
     for (int i = 0; i < Q; ++i) {
       const uint32_t row = row0 + St::qrow(tid, i);
-      kq[i] = St::qk(tid, i);
-      base[i] = row < P.rows ? row * P.ld + kq[i] : kOob;
+      base[i] = row < P.rows ? row * P.ld + kq : kOob;
     }
   }
   __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
+    const uint32_t k0 = kt * KT;
+    const bool kok = k0 + kq < kdim;
 #pragma unroll
-    for (int i = 0; i < Q; ++i) {
-      const uint32_t k0 = kt * KT;
-      r[i] = b.ld4(k0 + kq[i] < kdim ? base[i] + k0 : kOob);
-    }
+    for (int i = 0; i < Q; ++i) r[i] = b.ld4(kok ? base[i] + k0 : kOob);
   }
 };
 
@@ -165,38 +164,47 @@ struct LdDenseKR : LoaderBase<Stage<R, KT, true>> {
     uint32_t ld, rows, kdim, n;
   };
   BRes b;
-  uint32_t kdim, ld;
-  uint32_t base[Q], kk[Q];
+  uint32_t kdim, ld, kk0, base;  // base: quad 0's offset, or kOob for rows past the matrix
   __device__ __forceinline__ void init(const Params& P, uint32_t row0, int tid) {
     this->base_init(tid);
     b.init(P.p, P.n);
     kdim = P.kdim;
     ld = P.ld;
-#pragma unroll
-    for (int i = 0; i < Q; ++i) {
-      const uint32_t row = row0 + St::qrow(tid, i);
-      kk[i] = St::qk(tid, i);
-      base[i] = row < P.rows ? kk[i] * P.ld + row : kOob;
-    }
+    kk0 = St::qk(tid, 0);
+    const uint32_t row = row0 + St::qrow(tid, 0);
+    base = row < P.rows ? kk0 * P.ld + row : kOob;
   }
   __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
+    const uint32_t k0 = kt * KT;
 #pragma unroll
     for (int i = 0; i < Q; ++i) {
-      const uint32_t k0 = kt * KT;
-      r[i] = b.ld4(k0 + kk[i] < kdim ? base[i] + k0 * ld : kOob);
+      const uint32_t k = k0 + kk0 + St::DK * i;
+      r[i] = b.ld4(k < kdim ? base + (k0 + St::DK * i) * ld : kOob);
     }
   }
 };
 
 // ---------------------------------------------------------------------------
 // Pixel-row gather over an NHWC source (ROWK): rows = pixels of a grid
-// (b, a, c), k = (kh, kw, ch) with ch fastest (ch padded to Cp % 4 == 0).
+// (b, a, c); k runs over the taps (kh, kw) and the Cp source channels (Cp the
+// padded channel count, Cp % 4 == 0) in one of two orders:
+//   flat    (BLK false): k = (kh * k + kw) * Cp + ch;
+//   blocked (BLK true, Cp % kCB == 0, KT == kCB):
+//           k = (cb * KK + kh * k + kw) * kCB + ci, ch = cb * kCB + ci.
+// The blocked order makes a K tile one tap of one channel block, so a block's
+// slice of the source stays in L1 while all KK taps walk over it (the flat
+// order re-fetches each source pixel once per tap when Cp is large).  Within
+// a thread, all quads share their k (ROWK), so the tap decomposition is done
+// once per K tile.
 //   FWD: source = x, rows = output pixels, tap reads x[b, a*s + kh - p, c*s + kw - p].
 //   !FWD (dX): source = G, rows = input pixels, tap reads G[b, oh, ow] with
 //        oh*s == a + p - kh exactly (S1: s == 1, no divisibility test).
 // ---------------------------------------------------------------------------
-template <int R, int KT, bool FWD, bool S1>
+constexpr int kCB = 16;
+
+template <int R, int KT, bool FWD, bool S1, bool BLK>
 struct LdPixRK : LoaderBase<Stage<R, KT, false>> {
+  static_assert(!BLK || KT == kCB, "blocked order: one K tile per (channel block, tap)");
   using St = Stage<R, KT, false>;
   static constexpr bool KROW = false;
   using LoaderBase<St>::Q;
@@ -204,12 +212,12 @@ struct LdPixRK : LoaderBase<Stage<R, KT, false>> {
     const float* src;
     uint32_t srcH, srcW, Cp, k, s, p;
     uint32_t gridW, gridHW, N, kdim, n;
-    FastDiv dGridHW, dGridW, dCp, dK;
+    FastDiv dGridHW, dGridW, dInner, dK;  // dInner: KK (blocked) or Cp (flat)
   };
   BRes b;
-  uint32_t srcH, srcW, Cp, k, s, kdim;
-  FastDiv dCp, dK;
-  uint32_t pbase[Q], kq[Q];
+  uint32_t srcH, srcW, Cp, k, s, kdim, kq;
+  FastDiv dInner, dK;
+  uint32_t pbase[Q];
   int r0[Q], c0[Q];
   __device__ __forceinline__ void init(const Params& P, uint32_t row0, int tid) {
     this->base_init(tid);
@@ -220,12 +228,12 @@ struct LdPixRK : LoaderBase<Stage<R, KT, false>> {
     k = P.k;
     s = P.s;
     kdim = P.kdim;
-    dCp = P.dCp;
+    dInner = P.dInner;
     dK = P.dK;
+    kq = St::qk(tid, 0);
 #pragma unroll
     for (int i = 0; i < Q; ++i) {
       const uint32_t n = row0 + St::qrow(tid, i);
-      kq[i] = St::qk(tid, i);
       const uint32_t bb = fdiv(n, P.dGridHW);
       const uint32_t rem = n - bb * P.gridHW;
       const uint32_t a = fdiv(rem, P.dGridW);
@@ -243,15 +251,25 @@ struct LdPixRK : LoaderBase<Stage<R, KT, false>> {
     }
   }
   __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
+    uint32_t khw, ch;
+    bool kok;
+    if (BLK) {
+      const uint32_t cb = fdiv(kt, dInner);
+      khw = kt - cb * dInner.d;
+      ch = cb * kCB + kq;
+      kok = ch < Cp;
+    } else {
+      const uint32_t kk0 = kt * KT + kq;
+      khw = fdiv(kk0, dInner);
+      ch = kk0 - khw * Cp;
+      kok = kk0 < kdim;
+    }
+    const uint32_t kh = fdiv(khw, dK);
+    const uint32_t kw = khw - kh * k;
 #pragma unroll
     for (int i = 0; i < Q; ++i) {
-      const uint32_t kk0 = kt * KT + kq[i];
-      const uint32_t khw = fdiv(kk0, dCp);
-      const uint32_t ch = kk0 - khw * Cp;
-      const uint32_t kh = fdiv(khw, dK);
-      const uint32_t kw = khw - kh * k;
       int h, w;
-      bool ok = kk0 < kdim;
+      bool ok = kok;
       if (FWD) {
         h = r0[i] + int(kh);
         w = c0[i] + int(kw);
@@ -285,25 +303,22 @@ struct LdGradKR : LoaderBase<Stage<R, KT, true>> {
     uint32_t OCp, npix, n;
   };
   BRes b;
-  uint32_t OCp, npix;
-  uint32_t base[Q], kk[Q];
+  uint32_t OCp, npix, kk0, base;  // base: quad 0's offset, or kOob for channels past OCp
   __device__ __forceinline__ void init(const Params& P, uint32_t row0, int tid) {
     this->base_init(tid);
     b.init(P.g, P.n);
     OCp = P.OCp;
     npix = P.npix;
-#pragma unroll
-    for (int i = 0; i < Q; ++i) {
-      const uint32_t oc = row0 + St::qrow(tid, i);
-      kk[i] = St::qk(tid, i);
-      base[i] = oc < P.OCp ? kk[i] * P.OCp + oc : kOob;
-    }
+    kk0 = St::qk(tid, 0);
+    const uint32_t oc = row0 + St::qrow(tid, 0);
+    base = oc < P.OCp ? kk0 * P.OCp + oc : kOob;
   }
   __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
+    const uint32_t p0 = kt * KT;
 #pragma unroll
     for (int i = 0; i < Q; ++i) {
-      const uint32_t p0 = kt * KT;
-      r[i] = b.ld4(p0 + kk[i] < npix ? base[i] + p0 * OCp : kOob);
+      const uint32_t pix = p0 + kk0 + St::DK * i;
+      r[i] = b.ld4(pix < npix ? base + (p0 + St::DK * i) * OCp : kOob);
     }
   }
 };
@@ -321,10 +336,9 @@ struct LdXTapKR : LoaderBase<Stage<R, KT, true>> {
     FastDiv dOHW, dOW, dCp, dK;
   };
   BRes b;
-  uint32_t H, W, Cp, s, OW, OHW, npix;
+  uint32_t H, W, Cp, s, OW, OHW, npix, kk0, off;
   FastDiv dOHW, dOW;
-  uint32_t off[Q], kk[Q];
-  int kh[Q], kw[Q];
+  int kh, kw;  // the thread's tap row (same for all its quads)
   __device__ __forceinline__ void init(const Params& P, uint32_t row0, int tid) {
     this->base_init(tid);
     b.init(P.x, P.n);
@@ -337,31 +351,28 @@ struct LdXTapKR : LoaderBase<Stage<R, KT, true>> {
     npix = P.npix;
     dOHW = P.dOHW;
     dOW = P.dOW;
-#pragma unroll
-    for (int i = 0; i < Q; ++i) {
-      const uint32_t n = row0 + St::qrow(tid, i);
-      kk[i] = St::qk(tid, i);
-      const uint32_t khw = fdiv(n, P.dCp);
-      off[i] = n - khw * P.Cp;
-      const uint32_t a = fdiv(khw, P.dK);
-      kh[i] = int(a) - int(P.p);
-      kw[i] = int(khw - a * P.k) - int(P.p);
-      // A row past the taps gets an offset no pixel can bring into the image.
-      if (n >= P.N) kh[i] = -(1 << 20);
-    }
+    kk0 = St::qk(tid, 0);
+    const uint32_t n = row0 + St::qrow(tid, 0);
+    const uint32_t khw = fdiv(n, P.dCp);
+    off = n - khw * P.Cp;
+    const uint32_t a = fdiv(khw, P.dK);
+    kh = int(a) - int(P.p);
+    kw = int(khw - a * P.k) - int(P.p);
+    // A row past the taps gets an offset no pixel can bring into the image.
+    if (n >= P.N) kh = -(1 << 20);
   }
   __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
 #pragma unroll
     for (int i = 0; i < Q; ++i) {
-      const uint32_t pix = kt * KT + kk[i];
+      const uint32_t pix = kt * KT + kk0 + St::DK * i;
       const uint32_t bb = fdiv(pix, dOHW);
       const uint32_t rem = pix - bb * OHW;
       const uint32_t oh = fdiv(rem, dOW);
       const uint32_t ow = rem - oh * OW;
-      const int ih = int(oh * s) + kh[i];
-      const int iw = int(ow * s) + kw[i];
+      const int ih = int(oh * s) + kh;
+      const int iw = int(ow * s) + kw;
       const bool ok = pix < npix && uint32_t(ih) < H && uint32_t(iw) < W;
-      r[i] = b.ld4(ok ? ((bb * H + uint32_t(ih)) * W + uint32_t(iw)) * Cp + off[i] : kOob);
+      r[i] = b.ld4(ok ? ((bb * H + uint32_t(ih)) * W + uint32_t(iw)) * Cp + off : kOob);
     }
   }
 };
@@ -461,8 +472,15 @@ __device__ __forceinline__ void tile_coords(const TileGrid& tg, uint32_t& mt, ui
   z = t / tg.gn;
 }
 
+// Occupancy floor: the 128 x 128 tile holds 64 accumulator registers per
+// lane, and four workgroups per CU (the LDS limit) need the rest of the
+// register file to fit in 64 more.
+template <int MT, int NT>
+constexpr int igemm_min_waves() { return MT * NT == 128 * 128 ? 4 : 1; }
+
 template <int MT, int NT, int KT, class LA, class LB, class EPI>
 __global__ void __launch_bounds__(kThreads)
+    __attribute__((amdgpu_waves_per_eu(igemm_min_waves<MT, NT>())))
     k_igemm(const typename LA::Params pa, const typename LB::Params pb,
             const typename EPI::Params pe, TileGrid tg, uint32_t ktiles, uint32_t splits) {
   using SA = typename LA::St;
@@ -615,22 +633,34 @@ __global__ void __launch_bounds__(256)
   if (threadIdx.x == 0) out[c] = (sh[0] + sh[1]) + (sh[2] + sh[3]);
 }
 
-// mode 0 (forward A): out[oc][khw*Cp + c]  = c < C  ? w[oc][c][khw] : 0   (size OC*KK*Cp)
-// mode 1 (dX A):      out[c][khw*OCp + oc] = oc < OC ? w[oc][c][khw] : 0  (size C*KK*OCp)
+// Filters in the K order of the pixel loaders (flat or blocked), zero for
+// padding channels; `inner` is the padded channel count the K axis runs over
+// (Cp for the forward, OCp for dX):
+// mode 0 (forward A): out[oc][kk] = w[oc][c][khw]   with c  = channel of kk
+// mode 1 (dX A):      out[c][kk]  = w[oc][c][khw]   with oc = channel of kk
+// where kk = khw*inner + ch (flat) or (cb*KK + khw)*kCB + ci, ch = cb*kCB + ci
+// (blocked).  Size rows * KK*inner, rows = OC (mode 0) or C (mode 1).
 __global__ void k_permute_w(const float* __restrict__ w, float* __restrict__ out, uint32_t OC,
-                            uint32_t C, uint32_t KK, uint32_t padded, int mode) {
+                            uint32_t C, uint32_t KK, uint32_t inner, int mode, int blocked) {
+  const uint32_t kdim = KK * inner;
+  const uint32_t rows = mode == 0 ? OC : C;
   const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (mode == 0) {
-    if (i >= OC * KK * padded) return;
-    const uint32_t oc = i / (KK * padded), rr = i - oc * KK * padded;
-    const uint32_t khw = rr / padded, c = rr - khw * padded;
-    out[i] = c < C ? w[(oc * C + c) * KK + khw] : 0.f;
+  if (i >= rows * kdim) return;
+  const uint32_t r = i / kdim, kk = i - r * kdim;
+  uint32_t khw, ch;
+  if (blocked) {
+    const uint32_t blk = kk / kCB, ci = kk - blk * kCB;
+    const uint32_t cb = blk / KK;
+    khw = blk - cb * KK;
+    ch = cb * kCB + ci;
   } else {
-    if (i >= C * KK * padded) return;
-    const uint32_t c = i / (KK * padded), rr = i - c * KK * padded;
-    const uint32_t khw = rr / padded, oc = rr - khw * padded;
-    out[i] = oc < OC ? w[(oc * C + c) * KK + khw] : 0.f;
+    khw = kk / inner;
+    ch = kk - khw * inner;
   }
+  if (mode == 0)
+    out[i] = ch < C ? w[(r * C + ch) * KK + khw] : 0.f;
+  else
+    out[i] = ch < OC ? w[(ch * C + r) * KK + khw] : 0.f;
 }
 
 // Deterministic split-K sum: out[i] = sum_z part[z*n + i] in z order.
@@ -790,10 +820,11 @@ static double est_us(uint32_t M, uint32_t N, uint32_t kdim, const TileCfg& c, in
 // launch writes the final output (no partial buffer).
 template <class OccFn>
 static TileCfg choose(const char* var, uint32_t M, uint32_t N, uint32_t kdim, uint32_t max_splits,
-                      bool dense_out, OccFn&& occ) {
+                      bool dense_out, OccFn&& occ, bool kt16_only = false) {
   TileCfg c{pick_tile(M), pick_tile(N), 16, 1};
   const uint32_t ktiles = cdiv(kdim, uint32_t(c.KT));
   if (tune_override(var, c)) {
+    if (kt16_only) c.KT = 16;
     c.splits = std::max<uint32_t>(1, std::min<uint32_t>(c.splits, cdiv(kdim, uint32_t(c.KT))));
     return c;
   }
@@ -810,6 +841,11 @@ static TileCfg choose(const char* var, uint32_t M, uint32_t N, uint32_t kdim, ui
     }
   }
   c.splits = bestS;
+  if (const char* e = getenv("DCE_TUNE_LOG")) {
+    if (*e && *e != '0')
+      fprintf(stderr, "[dcengine] %s M=%u N=%u K=%u -> %dx%dx%d splits %u (occupancy %d)\n", var, M,
+              N, kdim, c.MT, c.NT, c.KT, c.splits, occ(c));
+  }
   return c;
 }
 
@@ -834,6 +870,25 @@ static bool tiles_dispatch(const TileCfg& c, F&& f) {
 #undef DCE_T
   set_error("igemm: unsupported tile %dx%dx%d", c.MT, c.NT, c.KT);
   return false;
+}
+
+// The same over the KT = 16 shapes only (the blocked-K pixel loaders).
+template <class F>
+static bool tiles_dispatch16(const TileCfg& c, F&& f) {
+#define DCE_T(a, b) \
+  if (c.MT == a && c.NT == b && c.KT == 16) return f.template run<a, b, 16>();
+  DCE_T(128, 128) DCE_T(128, 64) DCE_T(64, 128) DCE_T(64, 64)
+#undef DCE_T
+  set_error("igemm: unsupported tile %dx%dx%d", c.MT, c.NT, c.KT);
+  return false;
+}
+template <class F>
+static int tiles_occ16(const TileCfg& c, const F& f) {
+#define DCE_T(a, b) \
+  if (c.MT == a && c.NT == b && c.KT == 16) return f.template occ<a, b, 16>(c.splits > 1);
+  DCE_T(128, 128) DCE_T(128, 64) DCE_T(64, 128) DCE_T(64, 64)
+#undef DCE_T
+  return 1;
 }
 
 // Occupancy of the kernel a functor would launch for cfg.
@@ -977,7 +1032,27 @@ bool to_nhwc(const float* x, float* out, uint32_t B, uint32_t C, uint32_t H, uin
 // ----------------------------------------------------------- conv forward
 // Output pixels as GEMM columns: split-K partials go to a row-major [M][N]
 // workspace and k_splitk_nchw finishes (bias, activation, NCHW scatter).
-template <bool S1>
+// K order: blocked when the padded channel count is a multiple of kCB (no
+// extra padding then), flat otherwise.
+static inline bool blocked_k(uint32_t Cp) { return Cp % kCB == 0; }
+
+// Run F<S1, BLK> for the runtime (stride == 1, blocked) pair.
+template <template <bool, bool> class F, class... A>
+static bool conv_variant(bool s1, bool blk, const TileCfg& c, A&&... a) {
+  if (s1 && blk) return tiles_dispatch16(c, F<true, true>{a...});
+  if (s1) return tiles_dispatch16(c, F<true, false>{a...});
+  if (blk) return tiles_dispatch16(c, F<false, true>{a...});
+  return tiles_dispatch16(c, F<false, false>{a...});
+}
+template <template <bool, bool> class F>
+static int conv_variant_occ(bool s1, bool blk, const TileCfg& c) {
+  if (s1 && blk) return tiles_occ16(c, F<true, true>{});
+  if (s1) return tiles_occ16(c, F<true, false>{});
+  if (blk) return tiles_occ16(c, F<false, true>{});
+  return tiles_occ16(c, F<false, false>{});
+}
+
+template <bool S1, bool BLK>
 struct FwdRun {
   const float* wp;
   const float* xn;
@@ -989,7 +1064,7 @@ struct FwdRun {
   template <int MT, int NT, int KT>
   int occ(bool split) const {
     using LA = LdDenseRK<MT, KT>;
-    using LB = LdPixRK<NT, KT, true, S1>;
+    using LB = LdPixRK<NT, KT, true, S1, BLK>;
     return split ? occupancy(k_igemm<MT, NT, KT, LA, LB, EpiRowMajor>)
                  : occupancy(k_igemm<MT, NT, KT, LA, LB, EpiNCHW>);
   }
@@ -998,11 +1073,11 @@ struct FwdRun {
     const uint32_t Cp = pad4(g.C), KK = g.k * g.k, kdim = KK * Cp;
     const uint32_t OHW = g.OH * g.OW, N = g.B * OHW;
     using LA = LdDenseRK<MT, KT>;
-    using LB = LdPixRK<NT, KT, true, S1>;
+    using LB = LdPixRK<NT, KT, true, S1, BLK>;
     const typename LA::Params pa{wp, kdim, g.OC, kdim, g.OC * kdim};
     const typename LB::Params pb{xn, g.H, g.W, Cp, g.k, g.s, g.p, g.OW, OHW, N, kdim,
                                  g.B * g.H * g.W * Cp, make_fastdiv(OHW), make_fastdiv(g.OW),
-                                 make_fastdiv(Cp), make_fastdiv(g.k)};
+                                 make_fastdiv(BLK ? KK : Cp), make_fastdiv(g.k)};
     const uint32_t kt = cdiv(kdim, KT);
     if (splits > 1) {
       const EpiRowMajor::Params pe{part, g.OC, N, N, g.OC * N};
@@ -1016,15 +1091,16 @@ struct FwdRun {
 
 bool conv_forward(const float* x, float* x_nhwc_keep, const float* w, const float* bias,
                   float* y, const ConvGeom& g, uint32_t act) {
-  const uint32_t Cp = pad4(g.C), KK = g.k * g.k;
+  const uint32_t Cp = pad4(g.C), KK = g.k * g.k, kdim = KK * Cp;
+  const bool blk = blocked_k(Cp), s1 = g.s == 1;
   const size_t nx = nhwc_floats(g.B, g.C, g.H, g.W);
   const uint32_t N = g.B * g.OH * g.OW;
-  if (!operand_fits(nx, "conv_forward") || !operand_fits(size_t(g.OC) * KK * Cp, "conv_forward"))
+  if (!operand_fits(nx, "conv_forward") || !operand_fits(size_t(g.OC) * kdim, "conv_forward"))
     return false;
-  const TileCfg cfg = choose("DCE_TUNE_FWD", g.OC, N, KK * Cp, 8, true, [&](const TileCfg& t) {
-    return g.s == 1 ? tiles_occ(t, FwdRun<true>{}) : tiles_occ(t, FwdRun<false>{});
-  });
-  const size_t nw = al64(size_t(g.OC) * KK * Cp);
+  const TileCfg cfg = choose(
+      "DCE_TUNE_FWD", g.OC, N, kdim, 8, true,
+      [&](const TileCfg& t) { return conv_variant_occ<FwdRun>(s1, blk, t); }, true);
+  const size_t nw = al64(size_t(g.OC) * kdim);
   const size_t nxs = x_nhwc_keep ? 0 : al64(nx);
   const size_t nP = cfg.splits > 1 ? size_t(cfg.splits) * g.OC * N : 0;
   float* ws = workspace(nw + nxs + nP);
@@ -1033,17 +1109,15 @@ bool conv_forward(const float* x, float* x_nhwc_keep, const float* w, const floa
   float* xn = x_nhwc_keep ? x_nhwc_keep : ws + nw;
   float* part = ws + nw + nxs;
   if (!to_nhwc(x, xn, g.B, g.C, g.H, g.W)) return false;
-  hipLaunchKernelGGL(k_permute_w, dim3(cdiv(size_t(g.OC) * KK * Cp, 256)), dim3(256), 0, stream(),
-                     w, wp, g.OC, g.C, KK, Cp, 0);
+  hipLaunchKernelGGL(k_permute_w, dim3(cdiv(size_t(g.OC) * kdim, 256)), dim3(256), 0, stream(), w,
+                     wp, g.OC, g.C, KK, Cp, 0, blk ? 1 : 0);
   if (!check_launch("permute_w")) return false;
   const double fl = 2.0 * g.OC * g.C * KK * double(g.B) * g.OH * g.OW;
   {
     ProfScope prof("conv_fwd", fl,
                    4.0 * (double(g.B) * g.C * g.H * g.W + double(g.B) * g.OC * g.OH * g.OW));
-    const bool ok = g.s == 1
-        ? tiles_dispatch(cfg, FwdRun<true>{wp, xn, bias, y, part, g, act, cfg.splits})
-        : tiles_dispatch(cfg, FwdRun<false>{wp, xn, bias, y, part, g, act, cfg.splits});
-    if (!ok) return false;
+    if (!conv_variant<FwdRun>(s1, blk, cfg, wp, xn, bias, y, part, g, act, cfg.splits))
+      return false;
     if (cfg.splits > 1) return split_nchw(part, bias, y, g.OC, N, g.OH * g.OW, cfg.splits, act);
   }
   return true;
@@ -1076,7 +1150,7 @@ struct DwRun {
   }
 };
 
-template <bool S1>
+template <bool S1, bool BLK>
 struct DxRun {
   const float* wt;
   const float* gn;
@@ -1087,7 +1161,7 @@ struct DxRun {
   template <int MT, int NT, int KT>
   int occ(bool split) const {
     using LA = LdDenseRK<MT, KT>;
-    using LB = LdPixRK<NT, KT, false, S1>;
+    using LB = LdPixRK<NT, KT, false, S1, BLK>;
     return split ? occupancy(k_igemm<MT, NT, KT, LA, LB, EpiRowMajor>)
                  : occupancy(k_igemm<MT, NT, KT, LA, LB, EpiNCHW>);
   }
@@ -1096,11 +1170,11 @@ struct DxRun {
     const uint32_t OCp = pad4(g.OC), KK = g.k * g.k, kdim = KK * OCp;
     const uint32_t HW = g.H * g.W, N = g.B * HW;
     using LA = LdDenseRK<MT, KT>;
-    using LB = LdPixRK<NT, KT, false, S1>;
+    using LB = LdPixRK<NT, KT, false, S1, BLK>;
     const typename LA::Params pa{wt, kdim, g.C, kdim, g.C * kdim};
     const typename LB::Params pb{gn, g.OH, g.OW, OCp, g.k, g.s, g.p, g.W, HW, N, kdim,
                                  g.B * g.OH * g.OW * OCp, make_fastdiv(HW), make_fastdiv(g.W),
-                                 make_fastdiv(OCp), make_fastdiv(g.k)};
+                                 make_fastdiv(BLK ? KK : OCp), make_fastdiv(g.k)};
     const uint32_t kt = cdiv(kdim, KT);
     if (splits > 1) {
       const EpiRowMajor::Params pe{part, g.C, N, N, g.C * N};
@@ -1134,9 +1208,10 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
     nP = al64(size_t(dwc.splits) * g.OC * KK * Cp);
   }
   if (dx) {
-    dxc = choose("DCE_TUNE_DX", g.C, g.B * HW, KK * OCp, 8, true, [&](const TileCfg& t) {
-      return g.s == 1 ? tiles_occ(t, DxRun<true>{}) : tiles_occ(t, DxRun<false>{});
-    });
+    const bool blk = blocked_k(OCp);
+    dxc = choose(
+        "DCE_TUNE_DX", g.C, g.B * HW, KK * OCp, 8, true,
+        [&](const TileCfg& t) { return conv_variant_occ<DxRun>(g.s == 1, blk, t); }, true);
     nW = al64(size_t(g.C) * KK * OCp);
     nQ = dxc.splits > 1 ? size_t(dxc.splits) * g.C * g.B * HW : 0;
   }
@@ -1176,16 +1251,15 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
     if (!ok) return false;
   }
   if (dx) {
+    const bool blk = blocked_k(OCp);
     hipLaunchKernelGGL(k_permute_w, dim3(cdiv(size_t(g.C) * KK * OCp, 256)), dim3(256), 0,
-                       stream(), w, wt, g.OC, g.C, KK, OCp, 1);
+                       stream(), w, wt, g.OC, g.C, KK, OCp, 1, blk ? 1 : 0);
     if (!check_launch("permute_w")) return false;
     const double fl = 2.0 * g.OC * g.C * KK * double(npix);
     {
       ProfScope prof("conv_dx", fl, 4.0 * (double(npix) * OCp + double(g.B) * g.C * g.H * g.W));
-      const bool ok = g.s == 1
-          ? tiles_dispatch(dxc, DxRun<true>{wt, gn, dx, qpart, g, dxc.splits})
-          : tiles_dispatch(dxc, DxRun<false>{wt, gn, dx, qpart, g, dxc.splits});
-      if (!ok) return false;
+      if (!conv_variant<DxRun>(g.s == 1, blk, dxc, wt, gn, dx, qpart, g, dxc.splits))
+        return false;
       if (dxc.splits > 1) return split_nchw(qpart, nullptr, dx, g.C, g.B * HW, HW, dxc.splits, 0);
     }
   }
