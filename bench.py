@@ -131,6 +131,199 @@ def cpu_baseline(sample=64):
                       f"float64 NumPy oracle, {blas}, {dt:.1f} s"}
 
 
+HBM_PEAK_BYTES_PER_S = HBM_PEAK_GBS * 1e9
+
+
+def memory_suite(reps=10):
+    """Backward memory-bound kernels at the shapes of the benchmark networks,
+    each driven through the same dispatch the API's backward makes.  One JSON
+    line per kernel: algorithmic bytes per launch (each required tensor read
+    or written once), mean HIP-event time, GB/s and fraction of 8 TB/s."""
+    from directcompute_torch_amd import nn_engine as nn
+    lib = nn.lib
+    rng = np.random.default_rng(SEED + 7)
+    f2u = nn.float_to_uint
+    held = []
+
+    def buf(shape, kind="normal"):
+        n = int(np.prod(shape))
+        if kind == "normal":
+            a = rng.standard_normal(n).astype(np.float32)
+        elif kind == "unit":
+            a = rng.random(n).astype(np.float32)
+        else:
+            a = np.zeros(n, np.float32)
+        h = lib.CreateBuffer(a.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), n)
+        held.append(h)
+        return h
+
+    def prof(fam):
+        n, ms, fl, by = ctypes.c_uint64(), ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+        if not lib.GetProfile(fam.encode(), ctypes.byref(n), ctypes.byref(ms), ctypes.byref(fl), ctypes.byref(by)):
+            return 0, 0.0
+        return n.value, ms.value
+
+    out = []
+
+    def run(kernel, family, shape, nbytes, fn):
+        fn()
+        lib.SyncGPU()
+        lib.ResetProfile()
+        lib.SetProfiling(1)
+        for _ in range(reps):
+            fn()
+        lib.SyncGPU()
+        lib.SetProfiling(0)
+        n, ms = prof(family)
+        us = ms / max(n, 1) * 1e3
+        gbps = nbytes / (us * 1e-6) / 1e9 if us > 0 else 0.0
+        rec = {"suite": "memory", "kernel": kernel, "family": family, "shape": list(shape),
+               "bytes_per_launch": int(nbytes), "us": round(us, 2), "GB/s": round(gbps, 1),
+               "frac_hbm": round(gbps * 1e9 / HBM_PEAK_BYTES_PER_S, 4)}
+        out.append(rec)
+        print(json.dumps(rec), flush=True)
+
+    def ew(name, shape, unary_saved="normal", extra=None):
+        n = int(np.prod(shape))
+        g, x, o = buf(shape), buf(shape, unary_saved), buf(shape, "zero")
+        cb = dict(u1=n)
+        if extra:
+            cb.update(extra)
+        run(name, name, shape, 12 * n,
+            lambda: nn._dispatch(name.encode(), (g, x), (o,), (n + 255) // 256, 1, 1, **cb))
+
+    mb = (64, 96, 112, 112)      # MobileNetV2 IR stack b64: 96-channel expand at 112^2
+    ew("relu6_grad", mb)
+    ew("relu_grad", mb)
+    ew("leaky_relu_grad", mb, extra=dict(u2=f2u(0.1)))
+    ew("sigmoid_grad", (8, 1, 256, 256), "unit")
+
+    un = (8, 16, 256, 256)       # UNet-base16 b8 level-1 activation
+    n = int(np.prod(un))
+    acc, g = buf(un), buf(un)
+    run("grad_accum", "grad_accum", un, 12 * n,
+        lambda: nn._dispatch(b"grad_accum", (g,), (acc,), (n + 255) // 256, 1, 1, u1=n))
+
+    # BatchNorm backward (reduce + dx)
+    B, C, H, W = mb
+    S = H * W
+    n = B * C * S
+    x, dy = buf(mb), buf(mb)
+    mean, var, gamma = buf((C,), "zero"), buf((C,), "unit"), buf((C,), "unit")
+    dg, db, dx = buf((C,), "zero"), buf((C,), "zero"), buf(mb, "zero")
+    nn._dispatch(b"batchnorm_mean_var", (x,), (mean, var, buf((C,), "zero"), buf((C,), "unit")),
+                 C, 1, 1, u1=B, u2=C, u3=S, u4=1, u5=f2u(0.1), cbSize=20)
+    cb = dict(u1=B, u2=C, u3=S, u4=f2u(1e-5))
+    run("batchnorm_backward_reduce", "bn_bwd_reduce", mb, 8 * n,
+        lambda: nn._dispatch(b"batchnorm_backward_reduce", (x, dy, mean, var), (dg, db), C, 1, 1, **cb))
+    run("batchnorm_backward_dx", "bn_bwd_dx", mb, 12 * n,
+        lambda: nn._dispatch(b"batchnorm_backward_dx", (x, dy, mean, var, gamma, dg, db), (dx,),
+                             (n + 255) // 256, 1, 1, **cb))
+    run("batchnorm_mean_var", "bn_stats", mb, 4 * n,
+        lambda: nn._dispatch(b"batchnorm_mean_var", (x,), (mean, var, buf((C,), "zero"), buf((C,), "unit")),
+                             C, 1, 1, u1=B, u2=C, u3=S, u4=1, u5=f2u(0.1), cbSize=20))
+
+    # Depthwise 3x3 backward: stride 1 (hidden 144 at 56^2) and stride 2 (96 at 112^2 -> 56^2)
+    for (B, C, H, W, s) in ((64, 144, 56, 56, 1), (64, 96, 112, 112, 2)):
+        OH = (H + 2 - 3) // s + 1
+        nx, ny = B * C * H * W, B * C * OH * OH
+        xs, dys, fs = buf((B, C, H, W)), buf((B, C, OH, OH)), buf((C, 1, 3, 3))
+        dxs, dfs, dbs = buf((B, C, H, W), "zero"), buf((C, 1, 3, 3), "zero"), buf((C,), "zero")
+        cb = dict(u1=B, u2=C, u3=H, u4=W, u5=3, u6=3, u7=s, u8=1, u9=OH, cbSize=36)
+        run(f"depthwise_conv_backward_input_s{s}", "dw_bwd_input", (B, C, H, W), 4 * (nx + ny),
+            lambda: nn._dispatch(b"depthwise_conv_backward_input", (dys, fs), (dxs,), (nx + 255) // 256, 1, 1, **cb))
+        run(f"depthwise_conv_backward_filter_s{s}", "dw_bwd_filter", (B, C, H, W), 4 * (nx + ny),
+            lambda: nn._dispatch(b"depthwise_conv_backward_filter", (dys, xs), (dfs, dbs), C, 1, 1, **cb))
+
+    # Max-pool backward: UNet 2x2 s2 and AlexNet c1 3x3 s2 (indices from the fused forward,
+    # which the backward consumes, so each launch is preceded by a forward)
+    for (shape, k, st) in (((8, 16, 256, 256), 2, 2), ((128, 64, 55, 55), 3, 2)):
+        B, C, H, W = shape
+        OH, OW = (H - k) // st + 1, (W - k) // st + 1
+        xin, dz = buf(shape), buf((B, C, OH, OW))
+        nx, no = B * C * H * W, B * C * OH * OW
+
+        def mp(xin=xin, dz=dz, B=B, C=C, H=H, W=W, OH=OH, OW=OW, nx=nx, k=k, st=st):
+            pidx = ctypes.c_void_p()
+            y = lib.MaxPoolForwardFused(xin, B, C, H, W, k, st, ctypes.byref(pidx))
+            d = lib.MaxPoolBackwardFused(dz, pidx.value, B, C, OH, OW, nx)
+            lib.ReleaseBuffer(y)
+            lib.ReleaseBuffer(d)
+        run(f"maxpool_backward_{k}x{k}s{st}", "maxpool_bwd", shape, 8 * no + 4 * nx, mp)
+
+    # UNet decoder: nearest upsample x2 backward, concat backward (slice)
+    B, C, H, W = 8, 32, 128, 128
+    dyu, dxu = buf((B, C, 2 * H, 2 * W)), buf((B, C, H, W), "zero")
+    run("upsample_backward", "upsample_bwd", (B, C, H, W), 4 * B * C * H * W * 5,
+        lambda: nn._dispatch(b"upsample_backward", (dyu,), (dxu,), (B * C * H * W + 255) // 256, 1, 1,
+                             u1=B, u2=C, u3=H, u4=W, u5=2 * H, u6=2 * W, u7=2, u8=2, cbSize=32))
+    B, Ct, S = 8, 32, 256 * 256
+    dyc, sl = buf((B, Ct, 256, 256)), buf((B, 16, 256, 256), "zero")
+    run("slice", "slice", (B, 16, 256, 256), 8 * B * 16 * S,
+        lambda: nn._dispatch(b"slice", (dyc,), (sl,), (B * 16 * S + 255) // 256, 1, 1,
+                             u1=B, u2=16, u3=S, u4=Ct, u5=16, cbSize=20))
+
+    # Global-average-pool backward: broadcast g/S over [64, 96, 112, 112]
+    B, C, H, W = mb
+    gg, dxg = buf((B, C)), buf(mb, "zero")
+    run("global_avg_pool_backward", "gap_bwd", mb, 4 * B * C * H * W,
+        lambda: nn._dispatch(b"global_avg_pool_backward", (gg,), (dxg,), (B * C * H * W + 255) // 256, 1, 1,
+                             u1=B, u2=C, u3=H * W))
+
+    # Dice loss gradient, UNet output [8, 1, 256, 256]
+    B, size = 8, 256 * 256
+    pred, tgt, sums, gd = buf((B, size), "unit"), buf((B, size), "unit"), buf((B * 3,), "zero"), buf((B, size), "zero")
+    nn._dispatch(b"dice_loss_sums", (pred, tgt), (sums,), B, 1, 1, u1=B, u2=size)
+    run("dice_loss_grad", "dice_loss_grad", (B, 1, 256, 256), 12 * B * size,
+        lambda: nn._dispatch(b"dice_loss_grad", (pred, tgt, sums), (gd,), (B * size + 255) // 256, 1, 1,
+                             u1=B, u2=size))
+
+    # Conv backward G pass (mask + NHWC transpose + bias partials) at AlexNet c1/c2 shapes,
+    # through ConvBackwardFused with only db requested.
+    for name, cin, cout, k, s, p, hw in CONVS[:2]:
+        o = (hw + 2 * p - k) // s + 1
+        xc, wc, bc = buf((BATCH, cin, hw, hw)), buf((cout, cin, k, k)), buf((cout,), "zero")
+        yc = lib.ConvForwardFused(xc, wc, bc, BATCH, cin, hw, hw, cout, k, k, s, p, 1, None)
+        held.append(yc)
+        dyc2 = buf((BATCH, cout, o, o))
+        cpad = (cout + 3) // 4 * 4
+
+        def gpass(xc=xc, wc=wc, yc=yc, dyc2=dyc2, cin=cin, hw=hw, cout=cout, k=k, s=s, p=p):
+            pdf, pdb, pdx = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+            lib.ConvBackwardFused(dyc2, yc, xc, wc, None, BATCH, cin, hw, hw, cout, k, k, s, p, 1,
+                                  0, 0, 1, ctypes.byref(pdf), ctypes.byref(pdb), ctypes.byref(pdx))
+            lib.ReleaseBuffer(pdb.value)
+        run(f"conv_grad_reshape_relu_{name}", "conv_grad_nhwc", (BATCH, cout, o, o),
+            4 * BATCH * o * o * (2 * cout + cpad), gpass)
+
+    # Optimisers over AlexNet's 61.1 M parameters (16 tensors)
+    shapes = [(c[2], c[1], c[3], c[3]) for c in CONVS] + [(c[2],) for c in CONVS] + \
+             [(f[1], f[2]) for f in FCS] + [(f[2],) for f in FCS]
+    ps = [buf(sh, "unit") for sh in shapes]
+    gs = [buf(sh) for sh in shapes]
+    ms = [buf(sh, "zero") for sh in shapes]
+    vs = [buf(sh, "zero") for sh in shapes]
+    sizes = [int(np.prod(sh)) for sh in shapes]
+    P = len(shapes)
+    arr = lambda hs: (ctypes.c_void_p * P)(*hs)
+    pa, ga, ma, va = arr(ps), arr(gs), arr(ms), arr(vs)
+    sa = (ctypes.c_uint * P)(*sizes)
+    tot = sum(sizes)
+    run("SGDBatch", "sgd", (tot,), 12 * tot, lambda: lib.SGDBatch(pa, ga, sa, P, 1e-9, 1.0))
+    run("AdamBatch", "adam", (tot,), 28 * tot,
+        lambda: lib.AdamBatch(pa, ga, ma, va, sa, P, 1e-9, 0.9, 0.999, 1e-8, 0.0, 1.0))
+    run("ClipGradNorm: sum of squares", "grad_norm", (tot,), 4 * tot,
+        lambda: lib.ClipGradNorm(ga, sa, P, 1e30))
+
+    for h in held:
+        lib.ReleaseBuffer(h)
+    fr = [r["frac_hbm"] for r in out if r["bytes_per_launch"] >= 64 << 20]
+    print(json.dumps({"suite": "memory", "summary": {
+        "kernels": len(out), "kernels_over_64MiB": len(fr),
+        "median_frac_hbm_over_64MiB": round(float(np.median(fr)), 4) if fr else None,
+        "min_frac_hbm_over_64MiB": round(float(min(fr)), 4) if fr else None}}), flush=True)
+
+
 def copy_calibration(mib=256, reps=3):
     """Plain elementwise copy (torch's mul-by-one kernel) of `mib` MiB: each
     launch reads and writes exactly mib MiB, so its counter readings give the
@@ -153,6 +346,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=64)
+    ap.add_argument("--suite", choices=["train", "memory"], default="train",
+                    help="train: the AlexNet-224 b128 train step (default, one JSON line); "
+                         "memory: the backward memory-bound kernels, one JSON line each")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of 256 MiB three times (the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -162,6 +358,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.suite == "memory":
+        memory_suite()
         return
 
     from directcompute_torch_amd import nn_engine as nn

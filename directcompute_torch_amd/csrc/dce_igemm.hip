@@ -1012,6 +1012,10 @@ size_t nhwc_floats(uint32_t B, uint32_t C, uint32_t H, uint32_t W) {
 static bool to_nhwc_masked(const float* in, const float* y, float* out, float* dbPart,
                            uint32_t B, uint32_t C, uint32_t HW, uint32_t* npbOut) {
   const uint32_t Cp = pad4(C);
+  // Family "conv_grad_nhwc": the masked dy -> G pass of the conv backward
+  // (reads dy and y, writes G); "nhwc": a plain copy of an activation.
+  ProfScope prof(y ? "conv_grad_nhwc" : "nhwc", 0,
+                 4.0 * double(B) * HW * ((y ? 2.0 : 1.0) * C + Cp));
   if (Cp <= 8 && !y && !dbPart) {
     const uint32_t npix = B * HW;
     hipLaunchKernelGGL(k_to_nhwc_small, dim3(cdiv(npix, 256)), dim3(256), 0, stream(), in, out, C,

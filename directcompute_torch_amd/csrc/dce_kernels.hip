@@ -73,6 +73,7 @@ __global__ void k_ew_fast(F f, float* __restrict__ out, const float* __restrict_
 template <class F>
 static bool run_ew(const char* what, F f, Buf out, Buf a, Buf b, uint32_t n, bool unary) {
   if (n == 0) return true;
+  ProfScope prof(what, 0, (unary ? 8.0 : 12.0) * double(n));
   const bool fast = out.n >= n && a.n >= n && (unary || b.n >= n) && out.p && a.p &&
                     (unary || b.p);
   if (fast) {
@@ -263,6 +264,7 @@ __global__ void k_bias_grad_rows(Buf G, Buf g, uint32_t rows, uint32_t si, uint3
 static bool sh_bias_grad(const Dispatch& d) {
   uint32_t rows = CU(d, 0), classes = CU(d, 1), si = CU(d, 2), sid = CU(d, 3);
   if (!classes) return true;
+  ProfScope prof("bias_grad", 0, 4.0 * double(rows) * classes);
   if (rows >= 4096 && sid != 1) {
     hipLaunchKernelGGL(k_bias_grad_rows, dim3(classes), dim3(256), 0, stream(), S(d, 0), U(d, 0),
                        rows, si, sid);
@@ -423,6 +425,7 @@ __global__ void k_dice_grad(Buf pred, Buf tgt, Buf sums, Buf dx, uint32_t B, uin
 static bool sh_dice_grad(const Dispatch& d) {
   uint32_t B = CU(d, 0), size = CU(d, 1);
   if (!B || !size) return true;
+  ProfScope prof("dice_loss_grad", 0, 12.0 * double(B) * size);
   hipLaunchKernelGGL(k_dice_grad, dim3(cdiv(uint64_t(B) * size, 256)), dim3(256), 0, stream(),
                      S(d, 0), S(d, 1), S(d, 2), U(d, 0), B, size);
   return check_launch("dice_grad");
@@ -947,6 +950,7 @@ static bool sh_chan_copy(const Dispatch& d) {
   uint32_t B = CU(d, 0), cin = CU(d, 1), Sz = CU(d, 2), cout = CU(d, 3), coff = CU(d, 4);
   uint64_t total = uint64_t(B) * cin * Sz;
   if (!total) return true;
+  ProfScope prof(MODE == 0 ? "concat_insert" : "slice", 0, 8.0 * double(total));
   hipLaunchKernelGGL(k_chan_copy<MODE>, dim3(cdiv(total, 256)), dim3(256), 0, stream(), S(d, 0),
                      U(d, 0), uint32_t(total), cin, Sz, cout, coff);
   return check_launch(MODE == 0 ? "concat_insert" : "slice");

@@ -225,10 +225,18 @@ static bool build_tables(void** params, void** grads, void** m, void** v, const 
 
 static inline uint32_t table_blocks(const Table& t) { return t.start[t.count]; }
 
+static double table_elems(const std::vector<Table>& tabs) {
+  double e = 0;
+  for (const Table& t : tabs)
+    for (uint32_t i = 0; i < t.count; ++i) e += t.n[i];
+  return e;
+}
+
 bool sgd_multi(void** params, void** grads, const uint32_t* sizes, uint32_t n, float lr,
                float clip) {
   std::vector<Table> tabs;
   if (!build_tables(params, grads, nullptr, nullptr, sizes, n, true, tabs, nullptr)) return false;
+  ProfScope prof("sgd", 0, 12.0 * table_elems(tabs));
   for (const Table& t : tabs) {
     hipLaunchKernelGGL((k_multi<SgdOp, 3, 1>), dim3(table_blocks(t)), dim3(256), 0, stream(), t,
                        SgdOp{lr, clip});
@@ -244,6 +252,7 @@ bool grad_norm_multi(void** grads, const uint32_t* sizes, uint32_t n, float max_
   if (!build_tables(nullptr, grads, nullptr, nullptr, sizes, n, false, tabs, &total)) return false;
   double* part = reinterpret_cast<double*>(workspace(size_t(std::max<uint32_t>(total, 1)) * 2));
   if (!part) return false;
+  ProfScope prof("grad_norm", 0, 4.0 * table_elems(tabs));
   uint32_t base = 0;
   for (const Table& t : tabs) {
     hipLaunchKernelGGL(k_multi_sumsq, dim3(table_blocks(t)), dim3(256), 0, stream(), t, part, base);
@@ -260,6 +269,7 @@ bool sgd_scaled_multi(void** params, void** grads, const uint32_t* sizes, uint32
   SgdScaledDev op;
   op.lr = lr;
   op.scale = 1.f;
+  ProfScope prof("sgd_clipped", 0, 12.0 * table_elems(tabs));
   for (const Table& t : tabs) {
     hipLaunchKernelGGL((k_multi_devscale<SgdScaledDev, 3, 1>), dim3(table_blocks(t)), dim3(256), 0,
                        stream(), t, op, d_ns);
@@ -273,6 +283,7 @@ bool scale_grads_multi(void** grads, const uint32_t* sizes, uint32_t n, const fl
   if (!build_tables(nullptr, grads, nullptr, nullptr, sizes, n, false, tabs, nullptr)) return false;
   ScaleDev op;
   op.scale = 1.f;
+  ProfScope prof("clip_scale", 0, 8.0 * table_elems(tabs));
   for (const Table& t : tabs) {
     hipLaunchKernelGGL((k_multi_devscale<ScaleDev, 2, 2>), dim3(table_blocks(t)), dim3(256), 0,
                        stream(), t, op, d_ns);
@@ -286,10 +297,7 @@ bool adam_multi(void** params, void** grads, void** m, void** v, const uint32_t*
   std::vector<Table> tabs;
   uint32_t total = 0;
   if (!build_tables(params, grads, m, v, sizes, n, true, tabs, &total)) return false;
-  double elems = 0;
-  for (const Table& t : tabs)
-    for (uint32_t i = 0; i < t.count; ++i) elems += t.n[i];
-  ProfScope prof("adam", 0, 28.0 * elems);
+  ProfScope prof("adam", 0, 28.0 * table_elems(tabs));
   for (const Table& t : tabs) {
     hipLaunchKernelGGL((k_multi<AdamOp, 15, 13>), dim3(table_blocks(t)), dim3(256), 0, stream(), t,
                        AdamOp{step, b1, b2, eps, wd, clip});
