@@ -43,7 +43,6 @@
 
 namespace dce {
 
-typedef float f4 __attribute__((ext_vector_type(4)));
 constexpr int kThreads = 256;
 static inline uint32_t cdiv(uint64_t a, uint64_t b) { return uint32_t((a + b - 1) / b); }
 
@@ -96,25 +95,6 @@ struct LoaderBase {
 };
 
 __device__ __forceinline__ f4 zero4() { return f4{0.f, 0.f, 0.f, 0.f}; }
-
-// Operand view through a buffer resource.  The descriptor's range check makes
-// a load at or past num_records return zeros, so a padding or out-of-image
-// element is read by moving its offset to kOob instead of branching around the
-// load: every quad load of a K tile is issued back to back, with no exec-mask
-// juggling between them.  Offsets are in floats; the host admits operands of
-// fewer than kMaxOperandFloats floats, so kOob (+ any tile offset) is always
-// past num_records.
-constexpr uint32_t kOob = 0x20000000u;
-struct BRes {
-  __amdgpu_buffer_rsrc_t r;
-  __device__ __forceinline__ void init(const float* p, uint32_t nfloats) {
-    // Word 3 = 0x00020000: 32-bit data format, no swizzle, raw (stride 0).
-    r = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), 0, int(nfloats * 4u), 0x00020000);
-  }
-  __device__ __forceinline__ f4 ld4(uint32_t off) const {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, off * 4u, 0, 0);
-  }
-};
 
 // ---------------------------------------------------------------------------
 // Dense operands.  Preconditions (the host pads copies to meet them): 16-byte

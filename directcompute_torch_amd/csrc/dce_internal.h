@@ -70,6 +70,32 @@ __device__ __forceinline__ uint32_t fdiv(uint32_t n, FastDiv f) {
 }
 
 // ---------------------------------------------------------------------------
+// Operand view through a buffer resource.  The descriptor's range check makes
+// a load at or past num_records return zeros, so a padding or out-of-image
+// element is read by moving its offset to kOob instead of branching around
+// the load: a thread's loads are issued back to back, with no exec-mask
+// juggling between them.  Offsets are in floats; callers admit operands of
+// fewer than kOob floats (2 GiB), so kOob (+ any tile offset) is always past
+// num_records.
+// ---------------------------------------------------------------------------
+typedef float f4 __attribute__((ext_vector_type(4)));
+constexpr uint32_t kOob = 0x20000000u;
+struct BRes {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ __forceinline__ void init(const float* p, uint32_t nfloats) {
+    // Word 3 = 0x00020000: 32-bit data format, no swizzle, raw (stride 0).
+    r = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), 0, int(nfloats * 4u), 0x00020000);
+  }
+  // The builtins return raw 32-bit words; the bit casts keep them bits.
+  __device__ __forceinline__ f4 ld4(uint32_t off) const {
+    return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, off * 4u, 0, 0));
+  }
+  __device__ __forceinline__ float ld1(uint32_t off) const {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off * 4u, 0, 0));
+  }
+};
+
+// ---------------------------------------------------------------------------
 // Convolution geometry (NCHW, square kernels, zero padding, floor mode).
 // ---------------------------------------------------------------------------
 struct ConvGeom {

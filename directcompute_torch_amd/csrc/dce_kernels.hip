@@ -19,7 +19,6 @@
 
 namespace dce {
 
-typedef float f4 __attribute__((ext_vector_type(4)));
 static inline uint32_t cdiv(uint64_t a, uint64_t b) { return uint32_t((a + b - 1) / b); }
 
 __device__ __forceinline__ float ld(const Buf& b, uint32_t i) { return i < b.n ? b.p[i] : 0.f; }
@@ -1062,6 +1061,278 @@ __global__ void k_dw_bwd_filter_final(const double* part, uint32_t pieces, uint3
   else
     st(df, c * taps + t, float(s));
 }
+// Pipelined band kernels for the common shapes (K x K taps with K in {3, 5},
+// stride S in {1, 2}, pad < K, natural output size).  A block walks a list of
+// bands (rows of one (image, channel) plane).  A band's input window (zero
+// outside the plane) is loaded into registers -- at most kDwRegs values per
+// thread, through a buffer resource so that out-of-plane reads return zero
+// with no branch -- then written to LDS; the next band's loads are issued
+// before the current band is computed, so global traffic overlaps the
+// stencil work.  Each thread computes a 2 x 2 block of outputs from one
+// register window read out of LDS.
+constexpr int kDwRegs = 16;
+constexpr uint32_t kDwBand = 256 * kDwRegs;  // LDS floats one band window may use
+
+// A window of R rows x LW columns of a rows x cols plane, anchored at plane
+// row rb / column cb (either may be negative); cells outside the plane are 0.
+struct DwWin {
+  int rb, cb;
+  uint32_t R, LW;
+};
+template <int N>
+__device__ __forceinline__ void dw_win_load(const BRes& b, uint32_t base, uint32_t rows,
+                                            uint32_t cols, const DwWin& w, FastDiv dLW,
+                                            float (&v)[N]) {
+#pragma unroll
+  for (int u = 0; u < N; ++u) {
+    const uint32_t e = u * 256 + threadIdx.x;
+    const uint32_t i = fdiv(e, dLW), j = e - i * w.LW;
+    const int r = w.rb + int(i), c = w.cb + int(j);
+    const bool ok = e < w.R * w.LW && r >= 0 && r < int(rows) && c >= 0 && c < int(cols);
+    v[u] = b.ld1(ok ? base + uint32_t(r) * cols + uint32_t(c) : kOob);
+  }
+}
+template <int N>
+__device__ __forceinline__ void dw_win_store(float* lds, const float (&v)[N], uint32_t n) {
+#pragma unroll
+  for (int u = 0; u < N; ++u)
+    if (u * 256 + threadIdx.x < n) lds[u * 256 + threadIdx.x] = v[u];
+}
+
+// Sub-pixel geometry of the stride-2 input gradient: with p = 2*ph + PODD,
+// output row 2A + r takes tap fh exactly when r + PODD - fh is even, from dy
+// row A + ph + (r + PODD - fh) / 2.  Window row j holds dy row A + ph + JMIN + j.
+template <int K, int PODD>
+struct DwS2 {
+  static constexpr int JMIN = -((K - 1 - PODD + 1) / 2);  // floor((PODD - K + 1) / 2)
+  static constexpr int JMAX = (1 + PODD) / 2;
+  static constexpr int WR = JMAX - JMIN + 1;
+};
+
+// dX band: input rows [r0, r0 + RB) (RB even) of plane (n, c).
+//   S = 1: LDS cell (i, j) = dy[r0 + p - (K-1) + i][p - (K-1) + j]; output
+//          block (2a, 2b) reads the (K+1) x (K+1) window at (2a, 2b).
+//   S = 2: LDS cell (i, j) = dy[r0/2 + ph + JMIN + i][ph + JMIN + j]; output
+//          block (2a, 2b) reads the WR x WR window at (a, b).
+// Taps are summed in (fh, fw) order for every output, as the generic kernel.
+template <int K, int S, int PODD>
+__global__ void __launch_bounds__(256)
+    k_dw_bwd_input_band(const float* __restrict__ dy, const float* __restrict__ f,
+                        float* __restrict__ dx, uint32_t C, uint32_t H, uint32_t W, uint32_t OH,
+                        uint32_t OW, uint32_t p, uint32_t RB, uint32_t nb, uint32_t nbands,
+                        uint32_t LR, uint32_t LW, uint32_t BW, uint32_t ndy, FastDiv dLW,
+                        FastDiv dNb, FastDiv dBW) {
+  constexpr int WR = S == 1 ? K + 1 : DwS2<K, PODD>::WR;
+  __shared__ float sd[kDwBand];
+  BRes bd;
+  bd.init(dy, ndy);
+  float v[kDwRegs];
+  const uint32_t ph = p / 2;
+  auto decode = [&](uint32_t band, uint32_t& plane, uint32_t& r0) {
+    plane = fdiv(band, dNb);
+    r0 = (band - plane * nb) * RB;
+  };
+  auto win = [&](uint32_t r0) {
+    DwWin w;
+    w.R = LR;
+    w.LW = LW;
+    if (S == 1) {
+      w.rb = int(r0) + int(p) - (K - 1);
+      w.cb = int(p) - (K - 1);
+    } else {
+      w.rb = int(r0 / 2 + ph) + DwS2<K, PODD>::JMIN;
+      w.cb = int(ph) + DwS2<K, PODD>::JMIN;
+    }
+    return w;
+  };
+  uint32_t band = blockIdx.x;
+  if (band < nbands) {
+    uint32_t plane, r0;
+    decode(band, plane, r0);
+    dw_win_load(bd, plane * OH * OW, OH, OW, win(r0), dLW, v);
+  }
+  for (; band < nbands; band += gridDim.x) {
+    uint32_t plane, r0;
+    decode(band, plane, r0);
+    const uint32_t c = plane % C;
+    __syncthreads();  // the previous band's LDS reads are done
+    dw_win_store(sd, v, LR * LW);
+    __syncthreads();
+    if (band + gridDim.x < nbands) {
+      uint32_t pn, rn;
+      decode(band + gridDim.x, pn, rn);
+      dw_win_load(bd, pn * OH * OW, OH, OW, win(rn), dLW, v);
+    }
+    float w[K * K];
+#pragma unroll
+    for (int t = 0; t < K * K; ++t) w[t] = f[c * K * K + t];
+    const uint32_t r1 = min(r0 + RB, H);
+    float* dxp = dx + size_t(plane) * H * W;
+    const uint32_t items = ((r1 - r0 + 1) / 2) * BW;
+    for (uint32_t e = threadIdx.x; e < items; e += 256) {
+      const uint32_t a = fdiv(e, dBW), b2 = e - a * BW;
+      const uint32_t i0 = S == 1 ? 2 * a : a, j0 = S == 1 ? 2 * b2 : b2;
+      float win_[WR][WR];
+#pragma unroll
+      for (int i = 0; i < WR; ++i)
+#pragma unroll
+        for (int j = 0; j < WR; ++j) win_[i][j] = sd[(i0 + i) * LW + j0 + j];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const uint32_t ih = r0 + 2 * a + r;
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+          const uint32_t iw = 2 * b2 + cc;
+          float acc = 0.f;
+#pragma unroll
+          for (int fh = 0; fh < K; ++fh) {
+#pragma unroll
+            for (int fw = 0; fw < K; ++fw) {
+              if (S == 1) {
+                acc += win_[r + K - 1 - fh][cc + K - 1 - fw] * w[fh * K + fw];
+              } else if (((r + PODD - fh) & 1) == 0 && ((cc + PODD - fw) & 1) == 0) {
+                constexpr int J = DwS2<K, PODD>::JMIN;
+                acc += win_[(r + PODD - fh) / 2 - J][(cc + PODD - fw) / 2 - J] * w[fh * K + fw];
+              }
+            }
+          }
+          if (ih < r1 && iw < W) dxp[size_t(ih) * W + iw] = acc;
+        }
+      }
+    }
+  }
+}
+
+// dW / db partials.  Block (y, c) walks the bands (image n, output rows
+// [o0, o0 + RB), RB even) of channel c for n = y, y + gridDim.x, ...:
+//   LDS x cell (i, j) = x[o0*S - p + i][j - p]      (LXR x LXW, zero outside)
+//   LDS g cell (i, j) = dy[o0 + i][j]               (LGR x LGW, zero outside)
+// A thread takes 2 x 2 blocks of dy and the (S + K) x (S + K) x window under
+// them.  The K*K + 1 running sums are reduced once per block (waves by
+// shuffle, then the 4 wave sums in order) and stored as part[c][y][t] (double).
+template <int K, int S>
+__global__ void __launch_bounds__(256)
+    k_dw_bwd_filter_band(const float* __restrict__ dy, const float* __restrict__ x,
+                         double* __restrict__ part, uint32_t B, uint32_t C, uint32_t H,
+                         uint32_t W, uint32_t OH, uint32_t OW, uint32_t p, uint32_t RB,
+                         uint32_t nb, uint32_t LXR, uint32_t LXW, uint32_t LGR, uint32_t LGW,
+                         FastDiv dLXW, FastDiv dLGW, FastDiv dNb, FastDiv dBW) {
+  constexpr int T = K * K + 1;
+  constexpr int XW = S + K;  // x window edge under a 2 x 2 dy block
+  __shared__ float sx[kDwBand];
+  __shared__ float sg[kDwBand / 2];
+  __shared__ float red[4][T];
+  const uint32_t c = blockIdx.y;
+  BRes bx, bg;
+  bx.init(x, B * C * H * W);
+  bg.init(dy, B * C * OH * OW);
+  float xv[kDwRegs], gv[kDwRegs / 2];
+  const uint32_t nimg = blockIdx.x < B ? (B - blockIdx.x + gridDim.x - 1) / gridDim.x : 0u;
+  const uint32_t total = nimg * nb;
+  auto issue = [&](uint32_t j) {
+    const uint32_t q = fdiv(j, dNb);
+    const uint32_t n = blockIdx.x + q * gridDim.x, o0 = (j - q * nb) * RB;
+    const uint32_t plane = n * C + c;
+    dw_win_load(bx, plane * H * W, H, W, DwWin{int(o0 * S) - int(p), -int(p), LXR, LXW}, dLXW, xv);
+    dw_win_load(bg, plane * OH * OW, OH, OW, DwWin{int(o0), 0, LGR, LGW}, dLGW, gv);
+  };
+  float acc[T];
+#pragma unroll
+  for (int q = 0; q < T; ++q) acc[q] = 0.f;
+  if (total) issue(0);
+  for (uint32_t jb = 0; jb < total; ++jb) {
+    __syncthreads();  // the previous band's LDS reads are done
+    dw_win_store(sx, xv, LXR * LXW);
+    dw_win_store(sg, gv, LGR * LGW);
+    __syncthreads();
+    if (jb + 1 < total) issue(jb + 1);
+    const uint32_t items = (LGR / 2) * (LGW / 2);
+    for (uint32_t e = threadIdx.x; e < items; e += 256) {
+      const uint32_t a = fdiv(e, dBW), b2 = e - a * (LGW / 2);
+      float g[2][2];
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) g[r][cc] = sg[(2 * a + r) * LGW + 2 * b2 + cc];
+      float xw[XW][XW];
+#pragma unroll
+      for (int i = 0; i < XW; ++i)
+#pragma unroll
+        for (int jj = 0; jj < XW; ++jj) xw[i][jj] = sx[(2 * a * S + i) * LXW + 2 * b2 * S + jj];
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+          acc[K * K] += g[r][cc];
+#pragma unroll
+          for (int fh = 0; fh < K; ++fh)
+#pragma unroll
+            for (int fw = 0; fw < K; ++fw) acc[fh * K + fw] += g[r][cc] * xw[r * S + fh][cc * S + fw];
+        }
+    }
+  }
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int q = 0; q < T; ++q) {
+    float t = acc[q];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
+    if (lane == 0) red[wv][q] = t;
+  }
+  __syncthreads();
+  if (threadIdx.x < T) {
+    const int q = threadIdx.x;
+    const double t = (double(red[0][q]) + double(red[1][q])) + (double(red[2][q]) + double(red[3][q]));
+    part[(size_t(c) * gridDim.x + blockIdx.x) * T + q] = t;
+  }
+}
+
+// Band-path geometry (0 rows: use the generic kernels).  Eligible shapes:
+// K in {3, 5}, S in {1, 2}, p < K, the natural output size, operands below
+// kOob floats, and windows that fit the LDS / register budget with bands of
+// at least 2 rows (RB is even).
+struct DwBand {
+  uint32_t RB, R, LW, R2, LW2;  // dX: window R x LW; filter: x R x LW, dy R2 x LW2
+};
+static bool dw_band_ok(const DwGeom& g) {
+  if (g.kH != g.kW || (g.kH != 3 && g.kH != 5) || (g.s != 1 && g.s != 2) || g.p >= g.kH)
+    return false;
+  if (g.H + 2 * g.p < g.kH || g.OH != (g.H + 2 * g.p - g.kH) / g.s + 1) return false;
+  return uint64_t(g.B) * g.C * g.H * g.W < kOob && uint64_t(g.B) * g.C * g.OH * g.OW < kOob;
+}
+static DwBand dw_band_input(const DwGeom& g) {
+  DwBand b{0, 0, 0, 0, 0};
+  if (!dw_band_ok(g)) return b;
+  const uint32_t K = g.kH, BW = (g.W + 1) / 2;
+  const uint32_t WR = g.s == 1 ? K + 1 : ((1 + (g.p & 1)) / 2 + (K - (g.p & 1)) / 2 + 1);
+  b.LW = g.s == 1 ? 2 * BW + K : BW + WR;
+  const uint32_t rows = kDwBand / b.LW;  // window rows that fit
+  uint32_t RB = g.s == 1 ? (rows > K ? rows - K : 0) : (rows > WR ? 2 * (rows - WR) : 0);
+  RB &= ~1u;
+  if (RB < 2) return DwBand{0, 0, 0, 0, 0};
+  RB = std::min(RB, (g.H + 1) & ~1u);
+  b.RB = RB;
+  b.R = g.s == 1 ? RB + K : RB / 2 + WR;
+  return b;
+}
+static DwBand dw_band_filter(const DwGeom& g) {
+  DwBand b{0, 0, 0, 0, 0};
+  if (!dw_band_ok(g)) return b;
+  const uint32_t K = g.kH, S = g.s;
+  b.LW2 = (g.OW + 1) & ~1u;
+  b.LW = (b.LW2 - 1) * S + K;
+  if (b.LW2 * 2 > kDwBand / 2 || uint64_t(b.LW) * (S + K) > kDwBand) return DwBand{0, 0, 0, 0, 0};
+  const uint32_t byg = (kDwBand / 2) / b.LW2;
+  const uint32_t byx = (kDwBand / b.LW - K) / S + 1;
+  uint32_t RB = std::min(byg, byx) & ~1u;
+  if (RB < 2) return DwBand{0, 0, 0, 0, 0};
+  RB = std::min(RB, (g.OH + 1) & ~1u);
+  b.RB = RB;
+  b.R2 = RB;
+  b.R = (RB - 1) * S + K;
+  return b;
+}
+
 static bool dw_ok(const DwGeom& g, const char* what) {
   if (!g.B || !g.C || !g.H || !g.W || !g.kH || !g.kW || !g.s || !g.OH || !g.OW) return false;
   if (uint64_t(g.B) * g.C * std::max(g.H * g.W, g.OH * g.OW) >= (1ull << 31)) {
@@ -1084,8 +1355,27 @@ static bool sh_dw_bwd_input(const Dispatch& d) {
   uint32_t total = g.B * g.C * g.H * g.W;
   ProfScope prof("dw_bwd_input", 2.0 * g.kH * g.kW * double(g.B) * g.C * g.OH * g.OW,
                  4.0 * double(total) + 4.0 * double(g.B) * g.C * g.OH * g.OW);
-  hipLaunchKernelGGL(k_dw_bwd_input, dim3(cdiv(total, 256)), dim3(256), 0, stream(), S(d, 0),
-                     S(d, 1), U(d, 0), g, total);
+  const Buf dy = S(d, 0), f = S(d, 1), dx = U(d, 0);
+  const DwBand bb = dw_band_input(g);
+  if (bb.RB && covers(dy, uint64_t(g.B) * g.C * g.OH * g.OW) &&
+      covers(f, uint64_t(g.C) * g.kH * g.kW) && covers(dx, total)) {
+    const uint32_t nb = cdiv(g.H, bb.RB), nbands = g.B * g.C * nb;
+    const uint32_t blocks = std::min<uint32_t>(nbands, uint32_t(num_cus()) * 8);
+    const uint32_t BW = (g.W + 1) / 2, ndy = g.B * g.C * g.OH * g.OW;
+    const FastDiv fLW = make_fastdiv(bb.LW), fNb = make_fastdiv(nb), fBW = make_fastdiv(BW);
+    const uint32_t podd = g.p & 1;
+#define DCE_DWI(K, SS, PO)                                                                        \
+  if (g.kH == K && g.s == SS && (SS == 1 || podd == PO))                                         \
+    hipLaunchKernelGGL((k_dw_bwd_input_band<K, SS, PO>), dim3(blocks), dim3(256), 0, stream(),     \
+                       dy.p, f.p, dx.p, g.C, g.H, g.W, g.OH, g.OW, g.p, bb.RB, nb, nbands, bb.R,   \
+                       bb.LW, BW, ndy, fLW, fNb, fBW);
+    DCE_DWI(3, 1, 0) DCE_DWI(3, 2, 0) DCE_DWI(3, 2, 1)
+    DCE_DWI(5, 1, 0) DCE_DWI(5, 2, 0) DCE_DWI(5, 2, 1)
+#undef DCE_DWI
+    return check_launch("depthwise_conv_backward_input");
+  }
+  hipLaunchKernelGGL(k_dw_bwd_input, dim3(cdiv(total, 256)), dim3(256), 0, stream(), dy, f, dx, g,
+                     total);
   return check_launch("depthwise_conv_backward_input");
 }
 static bool sh_dw_bwd_filter(const Dispatch& d) {
@@ -1097,6 +1387,32 @@ static bool sh_dw_bwd_filter(const Dispatch& d) {
     return false;
   }
   const uint32_t len = g.B * g.OH * g.OW;
+  const Buf dy = S(d, 0), x = S(d, 1);
+  const DwBand bb = dw_band_filter(g);
+  if (bb.RB && covers(dy, uint64_t(len) * g.C) && covers(x, uint64_t(g.B) * g.C * g.H * g.W)) {
+    // Image groups per channel: about 8 blocks per CU, each walking at least
+    // one whole plane.
+    const uint32_t want = std::max<uint32_t>(1, uint32_t(num_cus()) * 8 / std::max<uint32_t>(1, g.C));
+    const uint32_t pieces = std::min<uint32_t>(g.B, want);
+    double* part = reinterpret_cast<double*>(workspace(size_t(g.C) * pieces * (taps + 1) * 2));
+    if (!part) return false;
+    ProfScope prof("dw_bwd_filter", 2.0 * taps * double(len) * g.C,
+                   4.0 * double(len) * g.C + 4.0 * double(g.B) * g.C * g.H * g.W);
+    const dim3 grid(pieces, g.C);
+    const uint32_t nb = cdiv(g.OH, bb.RB);
+    const FastDiv fLX = make_fastdiv(bb.LW), fLG = make_fastdiv(bb.LW2), fNb = make_fastdiv(nb),
+                  fBW = make_fastdiv(bb.LW2 / 2);
+#define DCE_DWF(K, SS)                                                                          \
+  if (g.kH == K && g.s == SS)                                                                  \
+    hipLaunchKernelGGL((k_dw_bwd_filter_band<K, SS>), grid, dim3(256), 0, stream(), dy.p, x.p,   \
+                       part, g.B, g.C, g.H, g.W, g.OH, g.OW, g.p, bb.RB, nb, bb.R, bb.LW, bb.R2, \
+                       bb.LW2, fLX, fLG, fNb, fBW);
+    DCE_DWF(3, 1) DCE_DWF(3, 2) DCE_DWF(5, 1) DCE_DWF(5, 2)
+#undef DCE_DWF
+    hipLaunchKernelGGL(k_dw_bwd_filter_final, dim3(cdiv(g.C * (taps + 1), 256)), dim3(256), 0,
+                       stream(), part, pieces, g.C, taps, U(d, 0), U(d, 1));
+    return check_launch("depthwise_conv_backward_filter");
+  }
   const uint32_t pieces = std::max<uint32_t>(1, std::min<uint32_t>(cdiv(len, 8192), 128));
   double* part = reinterpret_cast<double*>(workspace(size_t(g.C) * pieces * (taps + 1) * 2));
   if (!part) return false;

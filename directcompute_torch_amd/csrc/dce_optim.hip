@@ -14,7 +14,6 @@
 
 namespace dce {
 
-typedef float f4 __attribute__((ext_vector_type(4)));
 constexpr int kMaxT = 48;
 constexpr uint32_t kChunk = 4096;  // elements per block (256 threads x 16)
 

@@ -302,7 +302,17 @@ def test_concat_slice(eng):
 
 
 # ---------------------------------------------------------------- depthwise
-@pytest.mark.parametrize("B,C,H,W,k,s,p", [(2, 8, 9, 9, 3, 1, 1), (2, 6, 10, 12, 3, 2, 1), (1, 4, 7, 7, 5, 1, 2), (4, 96, 28, 28, 3, 2, 1)])
+DW_CASES = [
+    (2, 8, 9, 9, 3, 1, 1), (2, 6, 10, 12, 3, 2, 1), (1, 4, 7, 7, 5, 1, 2), (4, 96, 28, 28, 3, 2, 1),
+    # band kernels: several bands per plane, K 5 stride 2, pad 0, one-row bands on a wide plane
+    (2, 16, 56, 56, 3, 1, 1), (2, 16, 112, 112, 3, 2, 1), (2, 5, 11, 13, 5, 2, 2), (2, 3, 8, 9, 3, 1, 0),
+    (1, 2, 3, 1100, 3, 1, 1),
+    # generic kernels: 2x2 taps, stride 3
+    (2, 4, 8, 8, 2, 2, 0), (1, 4, 10, 10, 3, 3, 1),
+]
+
+
+@pytest.mark.parametrize("B,C,H,W,k,s,p", DW_CASES)
 def test_depthwise(eng, B, C, H, W, k, s, p):
     r = rng(B * C * H + k + s)
     x = r.standard_normal((B, C, H, W)).astype(np.float32)
