@@ -439,10 +439,13 @@ struct BnPieces {
   uint32_t pieces;
   uint32_t len;  // elements per channel = N*S
 };
-static BnPieces bn_pieces(uint32_t N, uint32_t S) {
+// Pieces per channel: about 8 blocks per CU over all channels, each piece at
+// least 4096 elements long (and at most 128 pieces).
+static BnPieces bn_pieces(uint32_t N, uint32_t C, uint32_t S) {
   BnPieces p;
   p.len = N * S;
-  p.pieces = std::max<uint32_t>(1, std::min<uint32_t>(cdiv(p.len, 8192), 128));
+  const uint32_t want = cdiv(uint32_t(num_cus()) * 8, std::max<uint32_t>(1, C));
+  p.pieces = std::max<uint32_t>(1, std::min<uint32_t>({want, cdiv(p.len, 4096), 128u}));
   return p;
 }
 
@@ -474,6 +477,65 @@ __global__ void k_bn_partial(Buf x, Buf dy, Buf mean, Buf var, float eps, uint32
       const float xh = (xv - mu) * rstd;
       a0 += g * xh;
       a1 += g;
+    }
+  }
+  const double s0 = block_sum256(a0, sh);
+  const double s1 = block_sum256(a1, sh);
+  if (threadIdx.x == 0) {
+    part[(size_t(c) * pieces + pc) * 2 + 0] = s0;
+    part[(size_t(c) * pieces + pc) * 2 + 1] = s1;
+  }
+}
+
+// Same sums over quads when S % 4 == 0 (every quad lies in one plane): the
+// piece is a range of quad indices k (plane n = k / (S/4)), read kBnUnroll
+// quads at a time so that each thread keeps several loads in flight.
+constexpr int kBnUnroll = 4;
+template <int MODE>
+__global__ void __launch_bounds__(256)
+    k_bn_partial4(const float* __restrict__ x, const float* __restrict__ dy,
+                  const float* __restrict__ mean, const float* __restrict__ var, float eps,
+                  uint32_t C, uint32_t S4, uint32_t len4, uint32_t pieces, FastDiv dS4,
+                  double* __restrict__ part) {
+  __shared__ double sh[4];
+  const uint32_t c = blockIdx.y, pc = blockIdx.x;
+  const uint32_t k0 = uint32_t((uint64_t(len4) * pc) / pieces);
+  const uint32_t k1 = uint32_t((uint64_t(len4) * (pc + 1)) / pieces);
+  float mu = 0.f, rstd = 0.f;
+  if (MODE == 1) {
+    mu = mean[c];
+    rstd = 1.0f / sqrtf(var[c] + eps);
+  }
+  const f4* x4 = reinterpret_cast<const f4*>(x);
+  const f4* g4 = reinterpret_cast<const f4*>(dy);
+  double a0 = 0.0, a1 = 0.0;
+  for (uint32_t kb = k0 + threadIdx.x; kb < k1; kb += 256 * kBnUnroll) {
+    f4 xv[kBnUnroll], gv[kBnUnroll];
+    bool ok[kBnUnroll];
+#pragma unroll
+    for (int u = 0; u < kBnUnroll; ++u) {
+      const uint32_t k = kb + u * 256;
+      ok[u] = k < k1;
+      const uint32_t kk = ok[u] ? k : k0;
+      const uint32_t n = fdiv(kk, dS4);
+      const size_t q = (size_t(n) * C + c) * S4 + (kk - n * S4);
+      xv[u] = x4[q];
+      if (MODE == 1) gv[u] = g4[q];
+    }
+#pragma unroll
+    for (int u = 0; u < kBnUnroll; ++u) {
+      if (!ok[u]) continue;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (MODE == 0) {
+          a0 += double(xv[u][e]);
+          a1 += double(xv[u][e]) * double(xv[u][e]);
+        } else {
+          const float xh = (xv[u][e] - mu) * rstd;
+          a0 += gv[u][e] * xh;
+          a1 += gv[u][e];
+        }
+      }
     }
   }
   const double s0 = block_sum256(a0, sh);
@@ -524,7 +586,7 @@ __global__ void k_bn_grad_final(const double* part, uint32_t pieces, uint32_t C,
 static bool bn_reduce(const char* what, int mode, const Dispatch& d, Buf x, Buf dy, Buf mean,
                       Buf var, float eps, uint32_t N, uint32_t C, uint32_t S, double** partOut,
                       BnPieces* pcOut) {
-  BnPieces pc = bn_pieces(N, S);
+  BnPieces pc = bn_pieces(N, C, S);
   const uint64_t total = uint64_t(N) * C * S;
   if (!total || total >= (1ull << 31)) {
     if (total) set_error("%s: tensor too large", what);
@@ -535,6 +597,21 @@ static bool bn_reduce(const char* what, int mode, const Dispatch& d, Buf x, Buf 
   const bool fast = covers(x, total) && (mode == 0 || covers(dy, total));
   dim3 grid(pc.pieces, C);
   FastDiv dS = make_fastdiv(S);
+  if (fast && S % 4 == 0 && (reinterpret_cast<uintptr_t>(x.p) & 15) == 0 &&
+      (mode == 0 || (reinterpret_cast<uintptr_t>(dy.p) & 15) == 0) &&
+      (mode == 0 || (covers(mean, C) && covers(var, C)))) {
+    const uint32_t S4 = S / 4, len4 = N * S4;
+    const FastDiv dS4 = make_fastdiv(S4);
+    if (mode == 0)
+      hipLaunchKernelGGL(k_bn_partial4<0>, grid, dim3(256), 0, stream(), x.p, nullptr, nullptr,
+                         nullptr, eps, C, S4, len4, pc.pieces, dS4, part);
+    else
+      hipLaunchKernelGGL(k_bn_partial4<1>, grid, dim3(256), 0, stream(), x.p, dy.p, mean.p, var.p,
+                         eps, C, S4, len4, pc.pieces, dS4, part);
+    *partOut = part;
+    *pcOut = pc;
+    return check_launch(what);
+  }
   if (mode == 0) {
     if (fast)
       hipLaunchKernelGGL((k_bn_partial<0, false>), grid, dim3(256), 0, stream(), x, dy, mean, var,
@@ -611,6 +688,39 @@ __global__ void k_bn_elem(Buf x, Buf dy, Buf mean, Buf var, Buf gamma, Buf beta_
     if (CHECK) st(out, i, v); else out.p[i] = v;
   }
 }
+// Quad form (S % 4 == 0, every buffer covering its size): the four elements
+// of a quad share a channel, whose parameters are computed once.
+template <int MODE>
+__global__ void __launch_bounds__(256)
+    k_bn_elem4(const float* __restrict__ x, const float* __restrict__ dy,
+               const float* __restrict__ mean, const float* __restrict__ var,
+               const float* __restrict__ gamma, const float* __restrict__ beta_or_dg,
+               const float* __restrict__ dbeta, float* __restrict__ out, float eps, uint32_t C,
+               uint32_t total4, FastDiv dS4, FastDiv dC, float m) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= total4) return;
+  const uint32_t q = fdiv(i, dS4);
+  const uint32_t c = q - fdiv(q, dC) * C;
+  const float mu = mean[c];
+  const float rstd = 1.0f / sqrtf(var[c] + eps);
+  const f4 xv = reinterpret_cast<const f4*>(x)[i];
+  f4 r;
+  if (MODE == 0) {
+    const float g = gamma[c], b = beta_or_dg[c];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = (xv[e] - mu) * rstd * g + b;
+  } else {
+    const float g = gamma[c], dg = beta_or_dg[c], db = dbeta[c];
+    const f4 gv = reinterpret_cast<const f4*>(dy)[i];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float xh = (xv[e] - mu) * rstd;
+      r[e] = (g * rstd) * (gv[e] - (db + xh * dg) / m);
+    }
+  }
+  reinterpret_cast<f4*>(out)[i] = r;
+}
+
 template <int MODE>
 static bool bn_elem(const char* what, const Dispatch& d) {
   uint32_t N = CU(d, 0), C = CU(d, 1), Sz = CU(d, 2);
@@ -631,6 +741,16 @@ static bool bn_elem(const char* what, const Dispatch& d) {
   Buf out = U(d, 0);
   const bool fast = covers(x, total) && covers(out, total) && (MODE == 0 || covers(dy, total));
   ProfScope prof(MODE == 0 ? "bn_fwd" : "bn_bwd_dx", 0, (MODE == 0 ? 8.0 : 12.0) * double(total));
+  const auto al16 = [](const Buf& b) { return (reinterpret_cast<uintptr_t>(b.p) & 15) == 0; };
+  if (fast && Sz % 4 == 0 && al16(x) && al16(out) && (MODE == 0 || al16(dy)) &&
+      covers(mean, C) && covers(var, C) && covers(gamma, C) && covers(b2, C) &&
+      (MODE == 0 || covers(db, C))) {
+    const uint32_t total4 = uint32_t(total / 4);
+    hipLaunchKernelGGL(k_bn_elem4<MODE>, dim3(cdiv(total4, 256)), dim3(256), 0, stream(), x.p,
+                       dy.p, mean.p, var.p, gamma.p, b2.p, db.p, out.p, eps, C, total4,
+                       make_fastdiv(Sz / 4), make_fastdiv(C), float(uint64_t(N) * Sz));
+    return check_launch(what);
+  }
   dim3 grid(cdiv(total, 256));
   if (fast)
     hipLaunchKernelGGL((k_bn_elem<MODE, false>), grid, dim3(256), 0, stream(), x, dy, mean, var,
@@ -879,11 +999,27 @@ __global__ void k_gap_bwd(Buf g, Buf dx, uint32_t total, uint32_t S) {
   const uint32_t i = gtid();
   if (i < total) st(dx, i, ld(g, i / S) / float(S));
 }
+// Quad form (S % 4 == 0, buffers covering the shapes): one g value per quad.
+__global__ void k_gap_bwd4(const float* __restrict__ g, float* __restrict__ dx, uint32_t total4,
+                           FastDiv dS4, float S) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= total4) return;
+  const float v = g[fdiv(i, dS4)] / S;
+  reinterpret_cast<f4*>(dx)[i] = f4{v, v, v, v};
+}
 static bool sh_gap_bwd(const Dispatch& d) {
   uint32_t Sz = CU(d, 2);
   uint64_t total = uint64_t(CU(d, 0)) * CU(d, 1) * Sz;
   if (!total) return true;
   ProfScope prof("gap_bwd", 0, 4.0 * double(total));
+  const Buf g = S(d, 0), dx = U(d, 0);
+  if (Sz % 4 == 0 && total < (1ull << 31) && covers(g, total / Sz) && covers(dx, total) &&
+      (reinterpret_cast<uintptr_t>(dx.p) & 15) == 0) {
+    const uint32_t total4 = uint32_t(total / 4);
+    hipLaunchKernelGGL(k_gap_bwd4, dim3(cdiv(total4, 256)), dim3(256), 0, stream(), g.p, dx.p,
+                       total4, make_fastdiv(Sz / 4), float(Sz));
+    return check_launch("global_avg_pool_backward");
+  }
   hipLaunchKernelGGL(k_gap_bwd, dim3(cdiv(total, 256)), dim3(256), 0, stream(), S(d, 0), U(d, 0),
                      uint32_t(total), Sz);
   return check_launch("global_avg_pool_backward");
@@ -920,12 +1056,35 @@ static bool sh_upsample(const Dispatch& d) {
                      U(d, 0), uint32_t(total), C, H, W, OH, OW, sH, sW);
   return check_launch("upsample");
 }
+// Nearest x2 with even W and exact output size: a thread sums two 2 x 2
+// blocks (two quads of dy rows 2h and 2h+1) into a pair of dx values, in the
+// reference's (a, then b) order.
+__global__ void k_upsample2_bwd(const float* __restrict__ dy, float* __restrict__ dx,
+                                uint32_t pairs, uint32_t W2, FastDiv dW2) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= pairs) return;
+  const uint32_t row = fdiv(i, dW2), j = i - row * W2;  // row = bc*H + h
+  const f4* r0 = reinterpret_cast<const f4*>(dy + size_t(2 * row) * 4 * W2);
+  const f4* r1 = reinterpret_cast<const f4*>(dy + size_t(2 * row + 1) * 4 * W2);
+  const f4 a = r0[j], b = r1[j];
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  reinterpret_cast<f2*>(dx)[i] = f2{((a[0] + a[1]) + b[0]) + b[1], ((a[2] + a[3]) + b[2]) + b[3]};
+}
 static bool sh_upsample_bwd(const Dispatch& d) {
   uint32_t B = CU(d, 0), C = CU(d, 1), H = CU(d, 2), W = CU(d, 3), OH = CU(d, 4), OW = CU(d, 5),
            sH = CU(d, 6), sW = CU(d, 7);
   uint64_t total = uint64_t(B) * C * H * W;
   if (!total) return true;
   ProfScope prof("upsample_bwd", 0, 4.0 * double(total) + 4.0 * double(B) * C * OH * OW);
+  const Buf dyb = S(d, 0), dxb = U(d, 0);
+  if (sH == 2 && sW == 2 && OH == 2 * H && OW == 2 * W && W % 2 == 0 && 4 * total < (1ull << 31) &&
+      covers(dyb, 4 * total) && covers(dxb, total) &&
+      ((reinterpret_cast<uintptr_t>(dyb.p) | reinterpret_cast<uintptr_t>(dxb.p)) & 15) == 0) {
+    const uint32_t pairs = uint32_t(total / 2), W2 = W / 2;
+    hipLaunchKernelGGL(k_upsample2_bwd, dim3(cdiv(pairs, 256)), dim3(256), 0, stream(), dyb.p,
+                       dxb.p, pairs, W2, make_fastdiv(W2));
+    return check_launch("upsample_backward");
+  }
   hipLaunchKernelGGL(k_upsample_bwd, dim3(cdiv(total, 256)), dim3(256), 0, stream(), S(d, 0),
                      U(d, 0), uint32_t(total), H, W, OH, OW, sH, sW);
   return check_launch("upsample_backward");
@@ -944,12 +1103,40 @@ __global__ void k_chan_copy(Buf src, Buf dst, uint32_t total, uint32_t cin, uint
   else
     st(dst, i, ld(src, o));
 }
+// Quad form (S % 4 == 0, buffers covering the shapes, 16-byte aligned).
+template <int MODE>
+__global__ void k_chan_copy4(const float* __restrict__ src, float* __restrict__ dst,
+                             uint32_t total4, uint32_t cin, uint32_t S4, uint32_t cout,
+                             uint32_t coff, FastDiv dS4, FastDiv dCin) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= total4) return;
+  const uint32_t t = fdiv(i, dS4), s4 = i - t * S4;
+  const uint32_t b = fdiv(t, dCin), c = t - b * cin;
+  const uint32_t o = (b * cout + c + coff) * S4 + s4;
+  if (MODE == 0)
+    reinterpret_cast<f4*>(dst)[o] = reinterpret_cast<const f4*>(src)[i];
+  else
+    reinterpret_cast<f4*>(dst)[i] = reinterpret_cast<const f4*>(src)[o];
+}
 template <int MODE>
 static bool sh_chan_copy(const Dispatch& d) {
   uint32_t B = CU(d, 0), cin = CU(d, 1), Sz = CU(d, 2), cout = CU(d, 3), coff = CU(d, 4);
   uint64_t total = uint64_t(B) * cin * Sz;
   if (!total) return true;
   ProfScope prof(MODE == 0 ? "concat_insert" : "slice", 0, 8.0 * double(total));
+  {
+    const Buf src = S(d, 0), dst = U(d, 0);
+    const uint64_t big = uint64_t(B) * cout * Sz;  // the concatenated tensor
+    if (Sz % 4 == 0 && cin + coff <= cout && big < (1ull << 31) &&
+        covers(MODE == 0 ? src : dst, total) && covers(MODE == 0 ? dst : src, big) &&
+        ((reinterpret_cast<uintptr_t>(src.p) | reinterpret_cast<uintptr_t>(dst.p)) & 15) == 0) {
+      const uint32_t total4 = uint32_t(total / 4);
+      hipLaunchKernelGGL(k_chan_copy4<MODE>, dim3(cdiv(total4, 256)), dim3(256), 0, stream(),
+                         src.p, dst.p, total4, cin, Sz / 4, cout, coff, make_fastdiv(Sz / 4),
+                         make_fastdiv(cin));
+      return check_launch(MODE == 0 ? "concat_insert" : "slice");
+    }
+  }
   hipLaunchKernelGGL(k_chan_copy<MODE>, dim3(cdiv(total, 256)), dim3(256), 0, stream(), S(d, 0),
                      U(d, 0), uint32_t(total), cin, Sz, cout, coff);
   return check_launch(MODE == 0 ? "concat_insert" : "slice");

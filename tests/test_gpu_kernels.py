@@ -226,7 +226,8 @@ def test_maxpool_raw_shaders(eng):
 
 
 # ---------------------------------------------------------------- batchnorm
-@pytest.mark.parametrize("N,C,H,W", [(2, 3, 5, 5), (8, 16, 32, 32), (4, 96, 28, 28), (64, 6, 12, 12), (1, 1, 1, 7)])
+@pytest.mark.parametrize("N,C,H,W", [(2, 3, 5, 5), (8, 16, 32, 32), (4, 96, 28, 28), (64, 6, 12, 12), (1, 1, 1, 7),
+                                     (16, 4, 64, 64)])
 def test_batchnorm(eng, N, C, H, W):
     r = rng(N * C * H * W)
     x = (r.standard_normal((N, C, H, W)) * 2 + 0.5).astype(np.float32)
@@ -286,14 +287,15 @@ def test_upsample(eng, B, C, H, W, sH, sW):
     release(eng, hx, hy, hdy, hdx)
 
 
-def test_concat_slice(eng):
-    B, S = 2, 20
-    a = rng(1).standard_normal((B, 3, 4, 5)).astype(np.float32)
-    b = rng(2).standard_normal((B, 5, 4, 5)).astype(np.float32)
+@pytest.mark.parametrize("H,W", [(4, 5), (3, 5)])   # plane sizes 20 (quad path) and 15
+def test_concat_slice(eng, H, W):
+    B, S = 2, H * W
+    a = rng(1).standard_normal((B, 3, H, W)).astype(np.float32)
+    b = rng(2).standard_normal((B, 5, H, W)).astype(np.float32)
     ha, hb, ho = upload(eng, a), upload(eng, b), new(eng, B * 8 * S)
     run(eng, "concat_insert", [ha], [ho], B, 3, S, 8, 0)
     run(eng, "concat_insert", [hb], [ho], B, 5, S, 8, 3)
-    cat = download(eng, ho, (B, 8, 4, 5))
+    cat = download(eng, ho, (B, 8, H, W))
     assert np.array_equal(cat, K.concat([a, b]).astype(np.float32))
     hs = new(eng, B * 5 * S)
     run(eng, "slice", [ho], [hs], B, 5, S, 8, 3)
