@@ -914,6 +914,55 @@ __global__ void k_maxpool_bwd_gather_n(const float* __restrict__ dz,
   dx[i] = acc;
 }
 
+// Block form: a thread owns an S x S block of inputs (rows aS.., cols bS..),
+// which the windows o in [a - (K-1)/S, a] x [b - (K-1)/S, b] cover; it loads
+// each of those NW x NW (index, value) pairs once.  A window whose recorded
+// argmax is input i necessarily contains i, so every input of the block adds
+// the values of the matching windows, in (oh, ow) order as above.
+template <int K, int S>
+__global__ void k_maxpool_bwd_blk(const float* __restrict__ dz, const uint32_t* __restrict__ idx,
+                                  float* __restrict__ dx, uint32_t items, uint32_t H, uint32_t W,
+                                  uint32_t OH, uint32_t OW, uint32_t BH, uint32_t BW,
+                                  FastDiv dBW, FastDiv dBH) {
+  constexpr int NW = (K - 1) / S + 1;
+  const uint32_t item = blockIdx.x * 256 + threadIdx.x;
+  if (item >= items) return;
+  const uint32_t t = fdiv(item, dBW), b = item - t * BW;
+  const uint32_t plane = fdiv(t, dBH), a = t - plane * BH;
+  uint32_t id[NW][NW];
+  float v[NW][NW];
+#pragma unroll
+  for (int wa = 0; wa < NW; ++wa) {
+    const int oh = int(a) - (NW - 1) + wa;
+#pragma unroll
+    for (int wb = 0; wb < NW; ++wb) {
+      const int ow = int(b) - (NW - 1) + wb;
+      const bool ok = oh >= 0 && oh < int(OH) && ow >= 0 && ow < int(OW);
+      const uint32_t o = (plane * OH + uint32_t(ok ? oh : 0)) * OW + uint32_t(ok ? ow : 0);
+      const uint32_t iv = idx[o];
+      v[wa][wb] = dz[o];
+      id[wa][wb] = ok ? iv : 0xFFFFFFFFu;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < S; ++r) {
+    const uint32_t ih = a * S + r;
+#pragma unroll
+    for (int c = 0; c < S; ++c) {
+      const uint32_t iw = b * S + c;
+      if (ih >= H || iw >= W) continue;
+      const uint32_t i = (plane * H + ih) * W + iw;
+      float acc = 0.f;
+#pragma unroll
+      for (int wa = 0; wa < NW; ++wa)
+#pragma unroll
+        for (int wb = 0; wb < NW; ++wb)
+          if (id[wa][wb] == i) acc += v[wa][wb];
+      dx[i] = acc;
+    }
+  }
+}
+
 // Fallback when the pooling geometry is unknown: zero + scatter-add.
 __global__ void k_maxpool_bwd_scatter(Buf dz, const uint32_t* idx, Buf dx, uint32_t n) {
   const uint32_t o = gtid();
@@ -930,6 +979,18 @@ bool maxpool_backward(const float* dz, const float* idx, float* dx, uint32_t B, 
   const uint32_t* ip = reinterpret_cast<const uint32_t*>(idx);
   if (k && s && H && W) {
     if (n == 0) return fill_zero(dx, xcount);
+    if (s == 2 && (k == 2 || k == 3) && xcount == B * C * H * W) {
+      const uint32_t BH = cdiv(H, 2), BW = cdiv(W, 2), items = B * C * BH * BW;
+      const dim3 grid(cdiv(items, 256));
+      const FastDiv fBW = make_fastdiv(BW), fBH = make_fastdiv(BH);
+      if (k == 2)
+        hipLaunchKernelGGL((k_maxpool_bwd_blk<2, 2>), grid, dim3(256), 0, stream(), dz, ip, dx,
+                           items, H, W, OH, OW, BH, BW, fBW, fBH);
+      else
+        hipLaunchKernelGGL((k_maxpool_bwd_blk<3, 2>), grid, dim3(256), 0, stream(), dz, ip, dx,
+                           items, H, W, OH, OW, BH, BW, fBW, fBH);
+      return check_launch("maxpool_backward");
+    }
     const uint32_t nw = (k + s - 1) / s;
     const dim3 grid(cdiv(xcount, 256));
     const FastDiv fW = make_fastdiv(W), fH = make_fastdiv(H), fS = make_fastdiv(s);
