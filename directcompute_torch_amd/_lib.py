@@ -128,6 +128,8 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.SetProfiling.restype = None
     lib.GetProfile.argtypes = [ctypes.c_char_p, P(ctypes.c_uint64), P(ctypes.c_double), P(ctypes.c_double), P(ctypes.c_double)]
     lib.GetProfile.restype = ctypes.c_bool
+    lib.SetProfileFilter.argtypes = [ctypes.c_char_p]
+    lib.SetProfileFilter.restype = None
     lib.ResetProfile.argtypes = []
     lib.ResetProfile.restype = None
     return lib

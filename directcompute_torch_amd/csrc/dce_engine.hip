@@ -114,9 +114,18 @@ static hipEvent_t take_event() {
   return e;
 }
 
+// Families recorded while profiling is on (empty: all).
+static std::vector<std::string> g_profFilter;
+static bool prof_wanted(const char* fam) {
+  if (g_profFilter.empty()) return true;
+  for (const std::string& f : g_profFilter)
+    if (f == fam) return true;
+  return false;
+}
+
 ProfScope::ProfScope(const char* fam, double fl, double by)
     : family(fam), flops(fl), bytes(by), ev0(nullptr) {
-  if (!g_prof) return;
+  if (!g_prof || !prof_wanted(fam)) return;
   hipEvent_t e = take_event();
   if (!e) return;
   hipEventRecord(e, g_stream);
@@ -874,6 +883,22 @@ bool GetProfile(const char* family, uint64_t* launches, double* ms, double* flop
 void ResetProfile(void) {
   resolve_profile();
   g_profStats.clear();
+}
+
+void SetProfileFilter(const char* families) {
+  resolve_profile();
+  g_profFilter.clear();
+  if (!families) return;
+  std::string cur;
+  for (const char* c = families;; ++c) {
+    if (*c == ',' || *c == 0) {
+      if (!cur.empty()) g_profFilter.push_back(cur);
+      cur.clear();
+      if (*c == 0) break;
+    } else if (*c != ' ') {
+      cur.push_back(*c);
+    }
+  }
 }
 
 }  // extern "C"

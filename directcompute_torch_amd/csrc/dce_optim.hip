@@ -79,6 +79,42 @@ __device__ __forceinline__ void apply_chunk(const Table& t, const Op& op, int ti
   float* m = t.m[ti];
   float* v = t.v[ti];
   const uint32_t end = min(n, c0 + kChunk);
+  if (c0 + kChunk <= n && ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(g) |
+                            reinterpret_cast<uintptr_t>(m) | reinterpret_cast<uintptr_t>(v)) & 15) == 0) {
+    // Whole, aligned chunk: every quad of the thread is loaded before any is
+    // stored, so all of them are in flight together.
+    f4 W[4], G[4], M[4], V[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t i = c0 + (j * 256 + threadIdx.x) * 4;
+      W[j] = G[j] = M[j] = V[j] = f4{0.f, 0.f, 0.f, 0.f};
+      if (READ & 1) W[j] = *reinterpret_cast<const f4*>(w + i);
+      if (READ & 2) G[j] = *reinterpret_cast<const f4*>(g + i);
+      if (READ & 4) M[j] = *reinterpret_cast<const f4*>(m + i);
+      if (READ & 8) V[j] = *reinterpret_cast<const f4*>(v + i);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float a = W[j][e], b = G[j][e], c = M[j][e], d = V[j][e];
+        op(a, b, c, d);
+        W[j][e] = a;
+        G[j][e] = b;
+        M[j][e] = c;
+        V[j][e] = d;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t i = c0 + (j * 256 + threadIdx.x) * 4;
+      if (WRITE & 1) *reinterpret_cast<f4*>(w + i) = W[j];
+      if (WRITE & 2) *reinterpret_cast<f4*>(g + i) = G[j];
+      if (WRITE & 4) *reinterpret_cast<f4*>(m + i) = M[j];
+      if (WRITE & 8) *reinterpret_cast<f4*>(v + i) = V[j];
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const uint32_t i = c0 + (j * 256 + threadIdx.x) * 4;
@@ -143,14 +179,22 @@ __global__ void __launch_bounds__(256) k_multi_sumsq(const Table t, double* part
   const float* g = t.g[ti];
   const uint32_t end = min(n, c0 + kChunk);
   float acc = 0.f;
+  if (c0 + kChunk <= n && (reinterpret_cast<uintptr_t>(g) & 15) == 0) {
+    f4 G[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t i = c0 + (j * 256 + threadIdx.x) * 4;
-    if (i + 3 < end) {
-      const f4 G = *reinterpret_cast<const f4*>(g + i);
-      acc += G[0] * G[0] + G[1] * G[1] + G[2] * G[2] + G[3] * G[3];
-    } else {
-      for (uint32_t k = i; k < end && k < i + 4; ++k) acc += g[k] * g[k];
+    for (int j = 0; j < 4; ++j) G[j] = *reinterpret_cast<const f4*>(g + c0 + (j * 256 + threadIdx.x) * 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc += G[j][0] * G[j][0] + G[j][1] * G[j][1] + G[j][2] * G[j][2] + G[j][3] * G[j][3];
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t i = c0 + (j * 256 + threadIdx.x) * 4;
+      if (i + 3 < end) {
+        const f4 G = *reinterpret_cast<const f4*>(g + i);
+        acc += G[0] * G[0] + G[1] * G[1] + G[2] * G[2] + G[3] * G[3];
+      } else {
+        for (uint32_t k = i; k < end && k < i + 4; ++k) acc += g[k] * g[k];
+      }
     }
   }
   double s = acc;

@@ -198,6 +198,9 @@ void SetProfiling(int enabled);
 bool GetProfile(const char* family, uint64_t* launches, double* ms, double* flops,
                 double* bytes);
 void ResetProfile(void);
+/* Restrict recording to a comma-separated list of families (NULL or "": all),
+ * so that a timed run carries only the events it reports. */
+void SetProfileFilter(const char* families);
 
 #ifdef __cplusplus
 }
