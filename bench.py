@@ -23,6 +23,7 @@ import argparse
 import ctypes
 import json
 import os
+import re
 import sys
 import time
 
@@ -47,6 +48,28 @@ BATCH = 128
 SEED = 5 * 1000
 # Kernel families timed (HIP events) during the timed steps; no others record.
 BENCH_FAMILIES = ("conv_dw", "conv_dx", "conv_fwd", "gemm", "maxpool_fwd", "maxpool_bwd", "adam")
+
+
+TRAFFIC_PROFILE = os.path.join(REPO, "profiles", "alexnet224_b128_conv_bwd_hbm_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per conv-backward GEMM launch (its split-K finish included)
+    from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE measurement, and the
+    algorithmic bytes per launch; (None, None) when the summary is absent."""
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None, None
+    vals = {}
+    for key in ("conv_bwd_hbm_bytes_per_step", "conv_bwd_gemm_launches_per_step",
+                "conv_bwd_algorithmic_bytes_per_step"):
+        m = re.search(key + r": (\d+)", text)
+        if not m:
+            return None, None
+        vals[key] = int(m.group(1))
+    n = vals["conv_bwd_gemm_launches_per_step"]
+    return vals["conv_bwd_hbm_bytes_per_step"] / n, vals["conv_bwd_algorithmic_bytes_per_step"] / n
 
 
 def log(*a):
@@ -424,6 +447,9 @@ def main():
         f"({achieved / MFMA_FP32_PEAK_TFLOPS * 100:.1f}% of fp32 MFMA peak), "
         f"{ms_bwd / args.steps:.3f} ms/step in conv-bwd kernels")
 
+    traffic, alg_bytes = measured_traffic()
+    if traffic:
+        traffic, alg_bytes = round(traffic), round(alg_bytes)
     out = {
         "metric": "train-step img/s, AlexNet-224 fp32 b128; conv-bwd TFLOP/s & % roofline",
         "value": round(img_s, 2),
@@ -450,7 +476,11 @@ def main():
             "peak": MFMA_FP32_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / MFMA_FP32_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_unit": "HBM bytes per conv-backward GEMM launch incl. its split-K finish "
+                            "(rocprofv3 FETCH_SIZE/WRITE_SIZE scaled by a copy kernel; "
+                            "profiles/alexnet224_b128_conv_bwd_hbm_traffic.md)" if traffic else None,
+            "algorithmic_bytes_per_launch": alg_bytes,
             "launches_per_step": (n_dw + n_dx) / args.steps,
             "kernel_ms_per_step": round(ms_bwd / args.steps, 4),
         },
