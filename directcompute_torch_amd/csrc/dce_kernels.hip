@@ -400,11 +400,87 @@ __global__ void k_dice_sums(Buf pred, Buf tgt, Buf out, uint32_t B, uint32_t siz
     }
   }
 }
+// Split form for long rows: block (piece, b) sums a contiguous slice of row b
+// (float4 loads, several in flight per thread) into double partials
+// part[b][piece][3]; k_dice_final adds a row's pieces in order.
+__global__ void __launch_bounds__(256)
+    k_dice_part(const float* __restrict__ pred, const float* __restrict__ tgt,
+                double* __restrict__ part, uint32_t size4, uint32_t pieces) {
+  __shared__ double sh[4];
+  const uint32_t b = blockIdx.y, pc = blockIdx.x;
+  const uint32_t k0 = uint32_t((uint64_t(size4) * pc) / pieces);
+  const uint32_t k1 = uint32_t((uint64_t(size4) * (pc + 1)) / pieces);
+  const f4* p4 = reinterpret_cast<const f4*>(pred) + size_t(b) * size4;
+  const f4* t4 = reinterpret_cast<const f4*>(tgt) + size_t(b) * size4;
+  float si = 0.f, sp = 0.f, stt = 0.f;
+  for (uint32_t kb = k0 + threadIdx.x; kb < k1; kb += 1024) {
+    f4 pv[4], tv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t k = min(kb + u * 256, k1 - 1);
+      pv[u] = p4[k];
+      tv[u] = t4[k];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (kb + u * 256 >= k1) continue;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        si += pv[u][e] * tv[u][e];
+        sp += pv[u][e];
+        stt += tv[u][e];
+      }
+    }
+  }
+  const double I = block_sum256(si, sh);
+  const double P = block_sum256(sp, sh);
+  const double T = block_sum256(stt, sh);
+  if (threadIdx.x == 0) {
+    double* o = part + (size_t(b) * pieces + pc) * 3;
+    o[0] = I;
+    o[1] = P;
+    o[2] = T;
+  }
+}
+__global__ void k_dice_final(const double* part, uint32_t pieces, uint32_t B, Buf out, int mode) {
+  const uint32_t b = gtid();
+  if (b >= B) return;
+  double I = 0, P = 0, T = 0;
+  for (uint32_t q = 0; q < pieces; ++q) {
+    const double* o = part + (size_t(b) * pieces + q) * 3;
+    I += o[0];
+    P += o[1];
+    T += o[2];
+  }
+  if (mode == 0) {
+    const float dice = (2.0f * float(I)) / (float(P) + float(T) + 1e-6f);
+    st(out, b, 1.0f - dice);
+  } else {
+    st(out, b * 3 + 0, float(I));
+    st(out, b * 3 + 1, float(P));
+    st(out, b * 3 + 2, float(T));
+  }
+}
+
 static bool sh_dice_t(const Dispatch& d, int mode) {
   uint32_t B = CU(d, 0), size = CU(d, 1);
   if (!B) return true;
-  hipLaunchKernelGGL(k_dice_sums, dim3(B), dim3(256), 0, stream(), S(d, 0), S(d, 1), U(d, 0), B,
-                     size, mode);
+  const Buf pred = S(d, 0), tgt = S(d, 1);
+  const uint64_t total = uint64_t(B) * size;
+  if (size % 4 == 0 && size >= 4096 && covers(pred, total) && covers(tgt, total) &&
+      ((reinterpret_cast<uintptr_t>(pred.p) | reinterpret_cast<uintptr_t>(tgt.p)) & 15) == 0) {
+    const uint32_t want = cdiv(uint32_t(num_cus()) * 4, B);
+    const uint32_t pieces = std::max<uint32_t>(1, std::min<uint32_t>(want, size / 4096));
+    double* part = reinterpret_cast<double*>(workspace(size_t(B) * pieces * 6));
+    if (!part) return false;
+    hipLaunchKernelGGL(k_dice_part, dim3(pieces, B), dim3(256), 0, stream(), pred.p, tgt.p, part,
+                       size / 4, pieces);
+    hipLaunchKernelGGL(k_dice_final, dim3(cdiv(B, 256)), dim3(256), 0, stream(), part, pieces, B,
+                       U(d, 0), mode);
+    return check_launch("dice");
+  }
+  hipLaunchKernelGGL(k_dice_sums, dim3(B), dim3(256), 0, stream(), pred, tgt, U(d, 0), B, size,
+                     mode);
   return check_launch("dice");
 }
 static bool sh_dice_loss(const Dispatch& d) { return sh_dice_t(d, 0); }

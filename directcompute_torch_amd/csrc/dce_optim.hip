@@ -207,16 +207,27 @@ __global__ void __launch_bounds__(256) k_multi_sumsq(const Table t, double* part
 
 // norm = sqrt(Σ partials); scale = norm > max ? max/(norm + 1e-6) : 1
 // (nn_grad_norm_final.hlsl:31-34).
-__global__ void k_norm_final(const double* part, uint32_t total, float maxNorm, float* ns) {
-  __shared__ double sh[4];
+// One block of 1024 threads; thread t adds partials t, t + 1024, ... (four
+// loads in flight), then a fixed shuffle / LDS tree.
+__global__ void __launch_bounds__(1024)
+    k_norm_final(const double* part, uint32_t total, float maxNorm, float* ns) {
+  __shared__ double sh[16];
   double s = 0;
-  for (uint32_t i = threadIdx.x; i < total; i += 256) s += part[i];
+  for (uint32_t i = threadIdx.x; i < total; i += 4096) {
+    double v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = i + u * 1024 < total ? part[i + u * 1024] : 0.0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) s += v[u];
+  }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) s += __shfl_down(s, o, 64);
   if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = s;
   __syncthreads();
   if (threadIdx.x == 0) {
-    const double tot = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+    double tot = 0;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) tot += sh[w];
     const float norm = float(sqrt(tot));
     ns[0] = norm;
     ns[1] = (norm > maxNorm) ? (maxNorm / (norm + 1e-6f)) : 1.0f;
@@ -301,7 +312,7 @@ bool grad_norm_multi(void** grads, const uint32_t* sizes, uint32_t n, float max_
     hipLaunchKernelGGL(k_multi_sumsq, dim3(table_blocks(t)), dim3(256), 0, stream(), t, part, base);
     base += table_blocks(t);
   }
-  hipLaunchKernelGGL(k_norm_final, dim3(1), dim3(256), 0, stream(), part, total, max_norm, d_ns);
+  hipLaunchKernelGGL(k_norm_final, dim3(1), dim3(1024), 0, stream(), part, total, max_norm, d_ns);
   return check_launch("grad_norm");
 }
 

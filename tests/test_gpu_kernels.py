@@ -365,7 +365,7 @@ def test_softmax_ce(eng, B, Kc):
     release(eng, hz, hl, hp, hloss, hg, hc, hz2, acc)
 
 
-@pytest.mark.parametrize("B,C,H,W", [(2, 1, 16, 16), (8, 1, 64, 64), (3, 2, 5, 7)])
+@pytest.mark.parametrize("B,C,H,W", [(2, 1, 16, 16), (8, 1, 64, 64), (3, 2, 5, 7), (8, 1, 256, 256)])
 def test_dice(eng, B, C, H, W):
     r = rng(B * H)
     p = r.random((B, C, H, W)).astype(np.float32)
