@@ -132,8 +132,11 @@ void RunSequenceWithSGD(SeqCmd* cmds, uint32_t cmdCount, void** params, void** g
 void* MatMulAlloc(void* a, void* b, uint32_t M, uint32_t K, uint32_t N, uint32_t flags);
 
 /* engine.cpp:751 ConvForwardFused: y = act(conv(x, W) + b), NCHW, act 0 id,
- * 1 ReLU, 2 tanh.  Implicit GEMM: no im2col buffer exists, so *pIm2col (when
- * pIm2col != NULL) receives NULL; ConvBackwardFused recomputes from x. */
+ * 1 ReLU, 2 tanh.  Implicit GEMM: no im2col matrix exists.  When pIm2col !=
+ * NULL, *pIm2col receives the channel-innermost copy of x (padded to a
+ * multiple of 4 channels, the size of x) that the forward built; it is an
+ * opaque handle that ConvBackwardFused consumes, as the reference's im2col
+ * buffer.  Operands of 2 GiB or more are refused (NULL + error). */
 void* ConvForwardFused(void* x, void* filters, void* bias, uint32_t batch, uint32_t inC,
                        uint32_t inH, uint32_t inW, uint32_t outC, uint32_t kH, uint32_t kW,
                        uint32_t stride, uint32_t padding, uint32_t actType, void** pIm2col);
@@ -141,8 +144,10 @@ void* ConvForwardFused(void* x, void* filters, void* bias, uint32_t batch, uint3
 /* engine.cpp:802 ConvBackwardFused: G = dy masked by (y > 0) when actType == 1
  * and y != NULL (act 2 applies no derivative, as the reference); dW = G·colᵀ,
  * db = Σ G, dX = col2im(Wᵀ·G), each only when requested (NULL otherwise).
- * Consumes (releases) the im2col handle, as the reference.  dW/dX are
- * implicit-GEMM fp32 MFMA kernels; db is fused into the dW kernel. */
+ * Consumes (releases) the im2col handle, as the reference; with im2col ==
+ * NULL the channel-innermost copy of x is rebuilt from x.  dW/dX are
+ * implicit-GEMM fp32 MFMA kernels; db is reduced from partials written by the
+ * pass that masks and transposes dy into G. */
 void ConvBackwardFused(void* gradOut, void* fwdOut, void* x, void* filters, void* im2col,
                        uint32_t batch, uint32_t inC, uint32_t inH, uint32_t inW,
                        uint32_t outC, uint32_t kH, uint32_t kW, uint32_t stride,
