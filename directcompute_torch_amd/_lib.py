@@ -130,6 +130,14 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.GetProfile.restype = ctypes.c_bool
     lib.SetProfileFilter.argtypes = [ctypes.c_char_p]
     lib.SetProfileFilter.restype = None
+    lib.BeginCapture.argtypes = []
+    lib.BeginCapture.restype = ctypes.c_bool
+    lib.EndCapture.argtypes = []
+    lib.EndCapture.restype = c_void_p
+    lib.ReplayGraph.argtypes = [c_void_p]
+    lib.ReplayGraph.restype = ctypes.c_bool
+    lib.ReleaseGraph.argtypes = [c_void_p]
+    lib.ReleaseGraph.restype = None
     lib.ResetProfile.argtypes = []
     lib.ResetProfile.restype = None
     return lib

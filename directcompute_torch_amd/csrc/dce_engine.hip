@@ -13,6 +13,7 @@
 #include "../../include/dcengine.h"
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -40,6 +41,18 @@ static uint64_t g_poolCapBytes = 0;
 
 static float* g_ws = nullptr;
 static size_t g_wsFloats = 0;
+
+// HIP-graph capture of the engine stream (BeginCapture / EndCapture).  While a
+// capture is open every buffer handed out or released is held for the graph
+// (a recorded node may read it), nothing is freed, and calls that would wait
+// on the stream are refused.  Workspace
+// blocks a live graph may reference are retired, not freed.
+static bool g_capturing = false;
+static bool g_captureFailed = false;
+static std::vector<Buffer*> g_captureHeld;
+static std::vector<float*> g_wsRetired;
+static int g_liveGraphs = 0;
+static bool refuse_in_capture(const char* what);
 static float* g_misc = nullptr;  // 1024 floats of device scratch for scalars
 
 // Pinned staging ring for host->device uploads.
@@ -64,6 +77,16 @@ bool ensure_init() {
   if (g_init) return true;
   set_error("engine not initialised (InitEngine failed or was not called)");
   return false;
+}
+
+// Calls that wait on the stream (or stage host memory) cannot be recorded:
+// during a capture they fail, and the capture is marked failed so that
+// EndCapture returns NULL with this reason.
+static bool refuse_in_capture(const char* what) {
+  if (!g_capturing) return false;
+  set_error("%s is not allowed while a graph capture is open", what);
+  g_captureFailed = true;
+  return true;
 }
 
 bool check_launch(const char* what) {
@@ -125,7 +148,7 @@ static bool prof_wanted(const char* fam) {
 
 ProfScope::ProfScope(const char* fam, double fl, double by)
     : family(fam), flops(fl), bytes(by), ev0(nullptr) {
-  if (!g_prof || !prof_wanted(fam)) return;
+  if (!g_prof || g_capturing || !prof_wanted(fam)) return;
   hipEvent_t e = take_event();
   if (!e) return;
   hipEventRecord(e, g_stream);
@@ -141,7 +164,7 @@ ProfScope::~ProfScope() {
 }
 
 static void resolve_profile() {
-  if (g_profPending.empty()) return;
+  if (g_profPending.empty() || g_capturing) return;
   hipStreamSynchronize(g_stream);
   for (auto& p : g_profPending) {
     float ms = 0;
@@ -179,6 +202,7 @@ static void free_record(Buffer* b) {
 }
 
 static void drain_pool_locked() {
+  if (g_capturing) return;  // frees would wait on the stream
   bool any = false;
   for (auto& kv : g_pool) any |= !kv.second.empty();
   if (!any) return;
@@ -227,6 +251,8 @@ static bool upload(float* dst, const float* src, size_t n) {
     hipLaunchKernelGGL(k_upload_small, dim3(1), dim3(256), 0, g_stream, dst, pl, uint32_t(n));
     return check_launch("upload");
   }
+  // A staged copy would replay whatever the staging slot holds later.
+  if (refuse_in_capture("a host upload of more than 256 floats")) return false;
   if (!g_stage) {
     if (hipHostMalloc((void**)&g_stage, kSlots * kSlotBytes, hipHostMallocDefault) != hipSuccess) {
       g_stage = nullptr;
@@ -316,6 +342,10 @@ void* create_buffer(const float* data, uint32_t count) {
     g_poolBytes += uint64_t(count) * 4;
     return nullptr;
   }
+  if (g_capturing) {  // the graph keeps it until ReleaseGraph
+    b->refCount++;
+    g_captureHeld.push_back(b);
+  }
   return b;
 }
 
@@ -339,7 +369,13 @@ void release_buffer(void* h) {
     set_error("ReleaseBuffer: handle %p is not live (double release?)", h);
     return;
   }
-  if (--b->refCount <= 0) release_internal(b);
+  if (--b->refCount > 0) return;
+  if (g_capturing) {  // a recorded node may still read it: the graph keeps it
+    b->refCount = 1;
+    g_captureHeld.push_back(b);
+    return;
+  }
+  release_internal(b);
 }
 
 float* workspace(size_t floats) {
@@ -347,8 +383,12 @@ float* workspace(size_t floats) {
   size_t want = std::max(floats, g_wsFloats * 3 / 2);
   want = (want + 65535) & ~size_t(65535);
   if (g_ws) {
-    hipStreamSynchronize(g_stream);
-    hipFree(g_ws);
+    if (g_capturing || g_liveGraphs > 0) {
+      g_wsRetired.push_back(g_ws);  // a graph may reference it
+    } else {
+      hipStreamSynchronize(g_stream);
+      hipFree(g_ws);
+    }
     g_ws = nullptr;
     g_wsFloats = 0;
   }
@@ -468,6 +508,7 @@ void UpdateBuffer(void* handle, float* data) {
 
 void ReadBuffer(void* handle, float* dst) {
   if (!handle || !dst || !g_init) return;
+  if (refuse_in_capture("ReadBuffer")) return;
   Buffer* b = as_buffer(handle, "ReadBuffer");
   if (!b) return;
   if (hipMemcpyAsync(dst, b->ptr, size_t(b->count) * 4, hipMemcpyDeviceToHost, g_stream) !=
@@ -486,11 +527,11 @@ void ClearBuffer(void* handle) {
 void FlushGPU(void) {}
 
 void SyncGPU(void) {
-  if (g_init) hipStreamSynchronize(g_stream);
+  if (g_init && !refuse_in_capture("SyncGPU")) hipStreamSynchronize(g_stream);
 }
 
 void WarmPool(uint32_t* sizes, uint32_t numSizes, uint32_t copies) {
-  if (!g_init || !sizes) return;
+  if (!g_init || !sizes || refuse_in_capture("WarmPool")) return;
   for (uint32_t i = 0; i < numSizes; ++i) {
     const uint32_t count = sizes[i];
     if (!count) continue;
@@ -836,6 +877,7 @@ float SGDBatchClipped(void** params, void** grads, uint32_t* sizes, uint32_t num
   float* d_ns = g_misc;  // [norm, scale]
   if (!grad_norm_multi(grads, sizes, numParams, maxNorm, d_ns)) return 0.0f;
   if (!sgd_scaled_multi(params, grads, sizes, numParams, lr, d_ns)) return 0.0f;
+  if (g_capturing) return std::nanf("");  // the norm is known only when the graph runs
   float h[2] = {0, 0};
   hipMemcpyAsync(h, d_ns, 8, hipMemcpyDeviceToHost, g_stream);
   hipStreamSynchronize(g_stream);
@@ -855,6 +897,7 @@ float ClipGradNorm(void** grads, uint32_t* sizes, uint32_t numGrads, float maxNo
   float* ns = g_misc;  // [norm, scale]
   if (!grad_norm_multi(grads, sizes, numGrads, maxNorm, ns)) return 0.0f;
   if (!scale_grads_multi(grads, sizes, numGrads, ns)) return 0.0f;
+  if (g_capturing) return std::nanf("");  // the norm is known only when the graph runs
   float h[2] = {0, 0};
   hipMemcpyAsync(h, ns, 8, hipMemcpyDeviceToHost, g_stream);
   hipStreamSynchronize(g_stream);
@@ -883,6 +926,100 @@ bool GetProfile(const char* family, uint64_t* launches, double* ms, double* flop
 void ResetProfile(void) {
   resolve_profile();
   g_profStats.clear();
+}
+
+// ------------------------------------------------------------ graph capture
+struct GraphRec {
+  uint32_t magic;
+  hipGraphExec_t exec;
+  std::vector<Buffer*> held;
+};
+constexpr uint32_t kMagicGraph = 0xDC6A9A7Fu;
+
+static void abort_capture() {
+  g_capturing = false;
+  std::vector<Buffer*> held;
+  held.swap(g_captureHeld);
+  for (Buffer* b : held) release_buffer(b);
+}
+
+bool BeginCapture(void) {
+  if (!ensure_init()) return false;
+  if (g_capturing) {
+    set_error("BeginCapture: a capture is already open");
+    return false;
+  }
+  resolve_profile();
+  if (hipStreamBeginCapture(g_stream, hipStreamCaptureModeRelaxed) != hipSuccess) {
+    hipGetLastError();
+    set_error("BeginCapture: hipStreamBeginCapture failed");
+    return false;
+  }
+  g_capturing = true;
+  g_captureFailed = false;
+  g_captureHeld.clear();
+  return true;
+}
+
+void* EndCapture(void) {
+  if (!g_capturing) {
+    set_error("EndCapture: no capture is open");
+    return nullptr;
+  }
+  hipGraph_t graph = nullptr;
+  const hipError_t e = hipStreamEndCapture(g_stream, &graph);
+  if (e != hipSuccess || g_captureFailed || !graph) {
+    if (e != hipSuccess) hipGetLastError();
+    if (graph) hipGraphDestroy(graph);
+    const bool failed = g_captureFailed;
+    abort_capture();
+    if (!failed) set_error("EndCapture: hipStreamEndCapture failed");
+    return nullptr;
+  }
+  hipGraphExec_t exec = nullptr;
+  if (hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) != hipSuccess) {
+    hipGetLastError();
+    hipGraphDestroy(graph);
+    abort_capture();
+    set_error("EndCapture: hipGraphInstantiate failed");
+    return nullptr;
+  }
+  hipGraphDestroy(graph);
+  GraphRec* g = new GraphRec{kMagicGraph, exec, std::move(g_captureHeld)};
+  g_captureHeld.clear();
+  g_capturing = false;
+  g_liveGraphs++;
+  return g;
+}
+
+bool ReplayGraph(void* graph) {
+  GraphRec* g = static_cast<GraphRec*>(graph);
+  if (!g_init || !g || g->magic != kMagicGraph) {
+    set_error("ReplayGraph: not a live graph handle");
+    return false;
+  }
+  if (refuse_in_capture("ReplayGraph")) return false;
+  if (hipGraphLaunch(g->exec, g_stream) != hipSuccess) {
+    hipGetLastError();
+    set_error("ReplayGraph: hipGraphLaunch failed");
+    return false;
+  }
+  return true;
+}
+
+void ReleaseGraph(void* graph) {
+  GraphRec* g = static_cast<GraphRec*>(graph);
+  if (!g || g->magic != kMagicGraph) return;
+  if (refuse_in_capture("ReleaseGraph")) return;
+  hipStreamSynchronize(g_stream);
+  hipGraphExecDestroy(g->exec);
+  for (Buffer* b : g->held) release_buffer(b);
+  g->magic = 0;
+  delete g;
+  if (--g_liveGraphs == 0) {
+    for (float* p : g_wsRetired) hipFree(p);
+    g_wsRetired.clear();
+  }
 }
 
 void SetProfileFilter(const char* families) {

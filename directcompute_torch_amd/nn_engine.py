@@ -13,8 +13,7 @@ there is no CPU fallback.
 
 Not provided (outside the backward path): custom HLSL shaders, the
 GELU / LayerNorm / attention family (their kernels do not exist in the
-reference tree), ONNX export/import, ComputeGraph record/replay, Muon, and the
-Python-side profilers.
+reference tree), ONNX export/import, Muon, and the Python-side profilers.
 """
 from __future__ import annotations
 
@@ -1081,6 +1080,140 @@ def end_batch():
 
 end_batch._count = 0
 end_batch.flush_interval = 10
+
+
+class ComputeGraph:
+    """Record one training step -- forward, softmax-CE loss, backward and the
+    optimiser update -- once, then replay it with new data
+    (nn_engine.py:2505-2771).
+
+    The reference records the step's RunShader dispatches and replays them with
+    RunSequence plus an SGDBatch call, so the fused conv / pool / matmul calls
+    fall outside its record.  Here the library captures every launch of the
+    step on its stream as a HIP graph (BeginCapture / EndCapture): any model
+    replays, with one ReplayGraph call per batch, and the graph holds the
+    step's buffers until release().
+
+    trace() runs the traced batch eagerly (which also sizes the pool and the
+    workspace), then records the same step.  Host scalars are those of the
+    recorded step: the SGD learning rate and clip, and for Adam / AdamW the
+    bias-corrected step size of the traced step.  The model may not read
+    buffers back or upload more than 256 floats inside the step.
+    """
+
+    def __init__(self):
+        self._graph = None
+        self._input_handle = None
+        self._label_handle = None
+        self._loss_handle = None
+        self._logits_handle = None
+        self._loss_size = 0
+        self._logits_shape = None
+        self._input_shape = None
+        self._label_shape = None
+        self._compiled = False
+
+    def _step(self, forward_fn, optimizer, clip):
+        optimizer.zero_grad()
+        lib.AddRefBuffer(self._input_handle)
+        # The traced input's gradient is never readable after the step, so it
+        # is not requested (nn_engine.py:2631 asks for it and discards it).
+        xb = Tensor.from_gpu(self._input_handle, self._input_shape)
+        lib.AddRefBuffer(self._label_handle)
+        yb = Tensor.from_gpu(self._label_handle, self._label_shape)
+        logits = forward_fn(xb)
+        loss = softmax_ce(logits, yb)
+        loss.backward()
+        optimizer.step(clip=clip)
+        return loss, logits
+
+    def trace(self, forward_fn, optimizer, X_batch, Y_batch, params, clip=1.0):
+        """Run one batch eagerly, then record the same step as a graph.
+        Returns the eager step's (loss, logits) tensors, whose buffers are
+        released on return as in the reference."""
+        self.release()
+        X = np.ascontiguousarray(X_batch, dtype=np.float32)
+        Y = np.ascontiguousarray(Y_batch, dtype=np.float32)
+        self._input_shape, self._label_shape = X.shape, Y.shape
+        self._input_handle = _check(
+            lib.CreateBuffer(X.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), X.size), "CreateBuffer")
+        self._label_handle = _check(
+            lib.CreateBuffer(Y.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), Y.size), "CreateBuffer")
+        loss, logits = self._step(forward_fn, optimizer, clip)
+        loss_val = np.empty(loss.size, dtype=np.float32)
+        logits_val = np.empty(logits.shape, dtype=np.float32)
+        lib.ReadBuffer(loss.gpu_buf, loss_val.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+        lib.ReadBuffer(logits.gpu_buf, logits_val.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+        release_all_buffers()
+        if not lib.BeginCapture():
+            raise RuntimeError(f"BeginCapture failed: {last_error()}")
+        try:
+            loss2, logits2 = self._step(forward_fn, optimizer, clip)
+            self._loss_handle, self._loss_size = loss2.gpu_buf, loss2.size
+            self._logits_handle, self._logits_shape = logits2.gpu_buf, logits2.shape
+            lib.AddRefBuffer(self._loss_handle)
+            lib.AddRefBuffer(self._logits_handle)
+        except BaseException:
+            graph = lib.EndCapture()
+            release_all_buffers()
+            if graph:
+                lib.ReleaseGraph(graph)
+            self.release()
+            raise
+        graph = lib.EndCapture()
+        release_all_buffers()
+        if not graph:
+            self.release()
+            raise RuntimeError(f"ComputeGraph.trace: capture failed: {last_error()}")
+        self._graph = graph
+        self._params_ref = params
+        self._compiled = True
+        # read_loss / read_logits before the first replay give the traced step's values
+        lib.UpdateBuffer(self._loss_handle, loss_val.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+        lib.UpdateBuffer(self._logits_handle, logits_val.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+        return loss, logits
+
+    def replay(self, X_batch, Y_batch):
+        """Upload a new batch into the traced input/label buffers and enqueue
+        one replay of the step."""
+        if not self._compiled:
+            raise RuntimeError("Graph not compiled. Call trace() first.")
+        X = np.ascontiguousarray(X_batch, dtype=np.float32)
+        Y = np.ascontiguousarray(Y_batch, dtype=np.float32)
+        if X.shape != self._input_shape or Y.shape != self._label_shape:
+            raise ValueError("replay batch shapes differ from the traced ones")
+        lib.UpdateBuffer(self._input_handle, X.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+        lib.UpdateBuffer(self._label_handle, Y.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+        if not lib.ReplayGraph(self._graph):
+            raise RuntimeError(f"ReplayGraph failed: {last_error()}")
+
+    def read_loss(self):
+        out = np.empty(self._loss_size, dtype=np.float32)
+        lib.ReadBuffer(self._loss_handle, out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+        return float(out[0])
+
+    def read_logits(self):
+        out = np.empty(self._logits_shape, dtype=np.float32)
+        lib.ReadBuffer(self._logits_handle, out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+        return out
+
+    def release(self):
+        """Free the graph, the buffers it holds and the input/label buffers."""
+        if self._graph:
+            lib.ReleaseGraph(self._graph)
+            self._graph = None
+        for name in ("_input_handle", "_label_handle", "_loss_handle", "_logits_handle"):
+            h = getattr(self, name)
+            if h:
+                lib.ReleaseBuffer(h)
+                setattr(self, name, None)
+        self._compiled = False
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass
 
 
 def warm_pool(sizes, copies=2):

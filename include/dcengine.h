@@ -207,6 +207,23 @@ void ResetProfile(void);
  * so that a timed run carries only the events it reports. */
 void SetProfileFilter(const char* families);
 
+/* Record / replay of queued work as a HIP graph: the MI355X form of the
+ * reference's ComputeGraph (nn_engine.py:2505-2771), which records RunShader
+ * dispatches and replays them through RunSequence (engine.cpp:952).  Between
+ * BeginCapture and EndCapture every launch on the engine stream is captured
+ * instead of run -- the fused conv / pool / matmul calls included -- and every
+ * buffer handed out is held until ReleaseGraph.  Calls that wait on the
+ * stream (ReadBuffer, SyncGPU, ReplayGraph, ReleaseGraph) and host uploads of
+ * more than 256 floats are refused while capturing; EndCapture then returns
+ * NULL with the reason in GetLastErrorString.  ClipGradNorm and
+ * SGDBatchClipped return NaN while capturing (the norm exists only when the
+ * graph runs).  ReplayGraph enqueues one replay; kernel arguments (sizes,
+ * host scalars, small uploads) are those of the captured call. */
+bool BeginCapture(void);
+void* EndCapture(void);
+bool ReplayGraph(void* graph);
+void ReleaseGraph(void* graph);
+
 #ifdef __cplusplus
 }
 #endif
