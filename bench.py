@@ -349,6 +349,228 @@ def memory_suite(reps=10):
         "min_frac_hbm_over_64MiB": round(float(min(fr)), 4) if fr else None}}), flush=True)
 
 
+def _prof_all(lib):
+    """Every kernel family's (launches, ms, flops, bytes) recorded so far."""
+    fams = ("conv_fwd", "conv_dw", "conv_dx", "gemm", "maxpool_fwd", "maxpool_bwd", "bn_stats",
+            "bn_bwd_reduce", "dw_bwd_input", "dw_bwd_filter", "gap_bwd", "upsample_bwd",
+            "dice_loss_grad", "bias_grad", "sgd", "adam", "grad_norm", "clip_scale",
+            "relu_grad", "relu6_grad", "sigmoid_grad", "grad_accum", "batchnorm_backward_dx",
+            "slice", "conv_grad_nhwc", "nhwc")
+    out = {}
+    for f in fams:
+        n, ms, fl, by = ctypes.c_uint64(), ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+        if lib.GetProfile(f.encode(), ctypes.byref(n), ctypes.byref(ms), ctypes.byref(fl), ctypes.byref(by)):
+            if n.value:
+                out[f] = (n.value, ms.value, fl.value, by.value)
+    return out
+
+
+def configs_suite(steps=10, warmup=3):
+    """The other measured configurations of the backward path, each a full
+    training step through the nn_engine API (synthetic inputs, seeds
+    1000*config + {0: x, 1: weights, 2: labels}):
+      1 LeNet-5 b64 (SGD lr 0.01, element clip 1.0)
+      2 single conv backward x[128,64,56,56], W[128,64,3,3] p1, ReLU (dW + dX + db)
+      3 MobileNetV2 inverted-residual stack b64 @112^2 + GAP + Linear 10 (SGD lr 0.01)
+      4 UNet-base16 b8 @256^2, 4 levels, Dice on sigmoid, norm clip 1.0 + Adam lr 1e-3
+    One JSON line per configuration: wall ms/step and img/s (no profiling in
+    that timing), then per-family kernel ms/step with TFLOP/s or GB/s from a
+    second, profiled pass (HIP events on the engine stream)."""
+    from directcompute_torch_amd import nn_engine as nn
+    lib = nn.lib
+    T = lambda a, rg=False: nn.Tensor(np.ascontiguousarray(a, dtype=np.float32), requires_grad=rg, track=False)
+
+    def he_conv(r, cout, cin, k):
+        return T(r.standard_normal((cout, cin, k, k)) * np.sqrt(2.0 / (cin * k * k)), True)
+
+    def he_lin(r, fin, fout):
+        return T(r.standard_normal((fin, fout)) * np.sqrt(2.0 / fin), True)
+
+    def zeros(n, rg=True):
+        return T(np.zeros(n), rg)
+
+    def ones(n, rg=True):
+        return T(np.ones(n), rg)
+
+    def run_config(cid, name, batch, step, extra=None):
+        for _ in range(warmup):
+            step()
+        lib.SyncGPU()
+        h0, m0 = ctypes.c_uint64(), ctypes.c_uint64()
+        lib.GetPoolStats(ctypes.byref(h0), ctypes.byref(m0))
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        lib.SyncGPU()
+        dt = (time.perf_counter() - t0) / steps
+        h1, m1 = ctypes.c_uint64(), ctypes.c_uint64()
+        lib.GetPoolStats(ctypes.byref(h1), ctypes.byref(m1))
+        pool = {"hits_per_step": (h1.value - h0.value) / steps, "misses_per_step": (m1.value - m0.value) / steps}
+        lib.ResetProfile()
+        lib.SetProfiling(1)
+        for _ in range(steps):
+            step()
+        lib.SyncGPU()
+        lib.SetProfiling(0)
+        fams = {}
+        for f, (n, ms, fl, by) in _prof_all(lib).items():
+            rec = {"launches_per_step": round(n / steps, 2), "ms_per_step": round(ms / steps, 4)}
+            if fl:
+                tf = fl / (ms * 1e-3) / 1e12
+                rec.update({"TFLOP/s": round(tf, 2), "frac_mfma": round(tf / MFMA_FP32_PEAK_TFLOPS, 4)})
+            elif by:
+                gb = by / (ms * 1e-3) / 1e9
+                rec.update({"GB/s": round(gb, 1), "frac_hbm": round(gb / HBM_PEAK_GBS, 4)})
+            fams[f] = rec
+        dw, dx = fams.get("conv_dw"), fams.get("conv_dx")
+        bwd = None
+        if dw:
+            fl = sum(v[2] for k, v in _prof_all(lib).items() if k in ("conv_dw", "conv_dx"))
+            ms = sum(v[1] for k, v in _prof_all(lib).items() if k in ("conv_dw", "conv_dx"))
+            tf = fl / (ms * 1e-3) / 1e12
+            bwd = {"gflop_per_step": round(fl / steps / 1e9, 2), "ms_per_step": round(ms / steps, 4),
+                   "TFLOP/s": round(tf, 2), "frac_mfma": round(tf / MFMA_FP32_PEAK_TFLOPS, 4)}
+        rec = {"suite": "configs", "config": cid, "workload": name, "batch": batch,
+               "ms_per_step": round(dt * 1e3, 4), "img_s": round(batch / dt, 1),
+               "conv_bwd": bwd, "pool": pool, "families": fams}
+        if extra:
+            rec.update(extra)
+        print(json.dumps(rec), flush=True)
+        log(f"[configs] {cid} {name}: {dt * 1e3:.3f} ms/step, {batch / dt:.0f} img/s"
+            + (f"; conv-bwd {bwd['TFLOP/s']} TFLOP/s ({bwd['frac_mfma'] * 100:.1f}%)" if bwd else "")
+            + f"; pool misses/step {pool['misses_per_step']:.1f} of {pool['hits_per_step'] + pool['misses_per_step']:.1f}")
+        nn.end_batch()
+
+    # 1 LeNet-5 b64
+    r = np.random.default_rng(1001)
+    P = [he_conv(r, 6, 1, 5), zeros(6), he_conv(r, 16, 6, 5), zeros(16),
+         he_lin(r, 256, 120), zeros(120), he_lin(r, 120, 84), zeros(84), he_lin(r, 84, 10), zeros(10)]
+    x = T(np.random.default_rng(1000).standard_normal((64, 1, 28, 28)))
+    y = T(np.random.default_rng(1002).integers(0, 10, 64))
+    opt = nn.SGD(P, lr=0.01)
+
+    def lenet_step():
+        opt.zero_grad()
+        h = nn.maxpool2d(nn.conv2d(x, P[0], P[1], 1, 0, 1), 2, 2)
+        h = nn.flatten(nn.maxpool2d(nn.conv2d(h, P[2], P[3], 1, 0, 1), 2, 2))
+        h = nn.bias_relu(nn.matmul(h, P[4]), P[5])
+        h = nn.bias_relu(nn.matmul(h, P[6]), P[7])
+        loss = nn.softmax_ce(nn.add_bias(nn.matmul(h, P[8]), P[9]), y)
+        loss.backward()
+        opt.step(clip=1.0)
+        nn.end_batch()
+    run_config(1, "LeNet-5 b64 train step (SGD lr 0.01, clip 1.0)", 64, lenet_step)
+    del P, x, y, opt
+
+    # 2 single conv backward
+    r = np.random.default_rng(2001)
+    W, b = he_conv(r, 128, 64, 3), zeros(128)
+    x2 = T(np.random.default_rng(2000).standard_normal((128, 64, 56, 56)), True)
+    dy = np.random.default_rng(2002).standard_normal((128, 128, 56, 56)).astype(np.float32)
+    gy = T(dy)
+
+    def conv_step():
+        W.grad = b.grad = x2.grad = None
+        yv = nn.conv2d(x2, W, b, 1, 1, 1)
+        yv.backward(gy)  # ConvBackwardFused masks dy with [y > 0]
+        nn.end_batch()
+    run_config(2, "single conv backward x[128,64,56,56] W[128,64,3,3] p1 ReLU: dW + dX + db",
+               128, conv_step, {"conv_bwd_gflop_algorithmic": round(2 * 2 * 128 * 64 * 9 * 128 * 56 * 56 / 1e9, 2)})
+    del W, b, x2, gy, dy
+
+    # 3 MobileNetV2 inverted-residual stack b64 @112^2
+    r = np.random.default_rng(3001)
+    blocks = []
+    for ci, co, s in [(16, 24, 2), (24, 24, 1), (24, 32, 2), (32, 32, 1), (32, 32, 1)]:
+        h = ci * 6
+        blocks.append(dict(ci=ci, co=co, s=s,
+                           exp=(he_conv(r, h, ci, 1), zeros(h)),
+                           bn1=(ones(h), zeros(h), zeros(h, False), ones(h, False)),
+                           dw=(T(r.standard_normal((h, 1, 3, 3)) * np.sqrt(2.0 / 9), True), zeros(h)),
+                           bn2=(ones(h), zeros(h), zeros(h, False), ones(h, False)),
+                           proj=(he_conv(r, co, h, 1), zeros(co)),
+                           bn3=(ones(co), zeros(co), zeros(co, False), ones(co, False))))
+    fc = (he_lin(r, 32, 10), zeros(10))
+    Pm = [fc[0], fc[1]]
+    for bl in blocks:
+        for k in ("exp", "dw", "proj"):
+            Pm += list(bl[k])
+        for k in ("bn1", "bn2", "bn3"):
+            Pm += list(bl[k][:2])
+    x3 = T(np.random.default_rng(3000).standard_normal((64, 16, 112, 112)))
+    y3 = T(np.random.default_rng(3002).integers(0, 10, 64))
+    opt3 = nn.SGD(Pm, lr=0.01)
+
+    def mbv2_step():
+        opt3.zero_grad()
+        h = x3
+        for bl in blocks:
+            t = nn.relu6(nn.batchnorm2d(nn.conv2d(h, *bl["exp"], 1, 0, 0), *bl["bn1"]))
+            t = nn.relu6(nn.batchnorm2d(nn.depthwise_conv2d(t, *bl["dw"], bl["s"], 1), *bl["bn2"]))
+            t = nn.batchnorm2d(nn.conv2d(t, *bl["proj"], 1, 0, 0), *bl["bn3"])
+            h = nn.add(t, h) if (bl["s"] == 1 and bl["ci"] == bl["co"]) else t
+        loss = nn.softmax_ce(nn.add_bias(nn.matmul(nn.global_avg_pool2d(h), fc[0]), fc[1]), y3)
+        loss.backward()
+        opt3.step(clip=1e30)
+        nn.end_batch()
+    run_config(3, "MobileNetV2 IR stack b64 @112^2 (16-24 s2, 24-24, 24-32 s2, 32-32 x2; "
+                  "expand x6, BN train, ReLU6, dw3x3) + GAP + Linear 10, SGD lr 0.01", 64, mbv2_step)
+    del blocks, Pm, x3, y3, opt3
+
+    # 4 UNet-base16 b8 @256^2
+    r = np.random.default_rng(4001)
+    U = {}
+
+    def cbr_p(name, cin, cout):
+        U[name] = (he_conv(r, cout, cin, 3), zeros(cout), ones(cout), zeros(cout),
+                   zeros(cout, False), ones(cout, False))
+    ch = [16, 32, 64, 128]
+    prev = 3
+    for i, c in enumerate(ch):
+        cbr_p(f"e{i}a", prev, c)
+        cbr_p(f"e{i}b", c, c)
+        prev = c
+    cbr_p("ba", prev, 256)
+    cbr_p("bb", 256, 256)
+    prev = 256
+    for i in reversed(range(4)):
+        cbr_p(f"d{i}a", prev + ch[i], ch[i])
+        cbr_p(f"d{i}b", ch[i], ch[i])
+        prev = ch[i]
+    head = (he_conv(r, 1, 16, 1), zeros(1))
+    Pu = list(head)
+    for v in U.values():
+        Pu += list(v[:4])
+    x4 = T(np.random.default_rng(4000).random((8, 3, 256, 256)))
+    m = (np.random.default_rng(4002).random((8, 1, 32, 32)) < 0.3).astype(np.float32)
+    t4 = T(m.repeat(8, axis=2).repeat(8, axis=3))
+    opt4 = nn.Adam(Pu, lr=1e-3)
+
+    def cbr(h, name):
+        w, bb, g, be, rm, rv = U[name]
+        return nn.relu(nn.batchnorm2d(nn.conv2d(h, w, bb, 1, 1, 0), g, be, rm, rv))
+
+    def unet_step():
+        opt4.zero_grad()
+        h = x4
+        skips = []
+        for i in range(4):
+            h = cbr(cbr(h, f"e{i}a"), f"e{i}b")
+            skips.append(h)
+            h = nn.maxpool2d(h, 2, 2)
+        h = cbr(cbr(h, "ba"), "bb")
+        for i in reversed(range(4)):
+            h = nn.concat([nn.upsample2d(h, 2, 2), skips[i]])
+            h = cbr(cbr(h, f"d{i}a"), f"d{i}b")
+        loss = nn.dice_loss(nn.sigmoid(nn.conv2d(h, head[0], head[1], 1, 0, 0)), t4)
+        loss.backward()
+        nn.clip_grad_norm(Pu, 1.0)
+        opt4.step(clip=1e30)
+        nn.end_batch()
+    run_config(4, "UNet-base16 b8 @256^2 (4 levels, conv3x3-BN-ReLU x2, Dice on sigmoid; "
+                  "norm clip 1.0 + Adam lr 1e-3)", 8, unet_step)
+
+
 def copy_calibration(mib=256, reps=3):
     """Plain elementwise copy (torch's mul-by-one kernel) of `mib` MiB: each
     launch reads and writes exactly mib MiB, so its counter readings give the
@@ -371,9 +593,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=64)
-    ap.add_argument("--suite", choices=["train", "memory"], default="train",
+    ap.add_argument("--suite", choices=["train", "memory", "configs"], default="train",
                     help="train: the AlexNet-224 b128 train step (default, one JSON line); "
-                         "memory: the backward memory-bound kernels, one JSON line each")
+                         "memory: the backward memory-bound kernels, one JSON line each; "
+                         "configs: LeNet, single conv, MobileNetV2 stack, UNet steps, one line each")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of 256 MiB three times (the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -386,6 +609,9 @@ def main():
         return
     if args.suite == "memory":
         memory_suite()
+        return
+    if args.suite == "configs":
+        configs_suite(steps=min(args.steps, 10), warmup=args.warmup)
         return
 
     from directcompute_torch_amd import nn_engine as nn
@@ -413,11 +639,17 @@ def main():
     lib.ResetProfile()
     lib.SetProfileFilter(b",".join(f.encode() for f in BENCH_FAMILIES))
     lib.SetProfiling(1)
+    h0, m0 = ctypes.c_uint64(), ctypes.c_uint64()
+    lib.GetPoolStats(ctypes.byref(h0), ctypes.byref(m0))
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
     lib.SyncGPU()
     t1 = time.perf_counter()
+    h1, m1 = ctypes.c_uint64(), ctypes.c_uint64()
+    lib.GetPoolStats(ctypes.byref(h1), ctypes.byref(m1))
+    log(f"[bench] pool: {(m1.value - m0.value) / args.steps:.1f} misses of "
+        f"{(h1.value + m1.value - h0.value - m0.value) / args.steps:.1f} buffer requests per step")
     lib.SetProfiling(0)
     lib.SetProfileFilter(None)
 

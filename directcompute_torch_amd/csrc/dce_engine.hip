@@ -183,13 +183,11 @@ static void resolve_profile() {
 // ---------------------------------------------------------------------------
 // Buffers and pool
 // ---------------------------------------------------------------------------
-static size_t max_pool_for_size(uint32_t count) {
-  size_t bytes = size_t(count) * 4;
-  if (bytes >= (size_t(1) << 30)) return 4;
-  if (bytes >= (size_t(4) << 20)) return 8;
-  if (bytes >= (size_t(256) << 10)) return 16;
-  return 32;
-}
+// Copies of one size the pool keeps.  The real bound is the byte cap (half of
+// device memory): a step that holds dozens of same-size activations at once
+// (UNet or MobileNet at full resolution) gets all of them back next step,
+// instead of freeing the excess (a stream drain each) and allocating again.
+static size_t max_pool_for_size(uint32_t) { return 4096; }
 
 static void free_record(Buffer* b) {
   // The stream may still reference the memory: drain it first.
