@@ -365,7 +365,7 @@ def _prof_all(lib):
     return out
 
 
-def configs_suite(steps=10, warmup=3):
+def configs_suite(steps=10, warmup=3, ids=None):
     """The other measured configurations of the backward path, each a full
     training step through the nn_engine API (synthetic inputs, seeds
     1000*config + {0: x, 1: weights, 2: labels}):
@@ -442,133 +442,138 @@ def configs_suite(steps=10, warmup=3):
         nn.end_batch()
 
     # 1 LeNet-5 b64
-    r = np.random.default_rng(1001)
-    P = [he_conv(r, 6, 1, 5), zeros(6), he_conv(r, 16, 6, 5), zeros(16),
-         he_lin(r, 256, 120), zeros(120), he_lin(r, 120, 84), zeros(84), he_lin(r, 84, 10), zeros(10)]
-    x = T(np.random.default_rng(1000).standard_normal((64, 1, 28, 28)))
-    y = T(np.random.default_rng(1002).integers(0, 10, 64))
-    opt = nn.SGD(P, lr=0.01)
+    def config1():
+        r = np.random.default_rng(1001)
+        P = [he_conv(r, 6, 1, 5), zeros(6), he_conv(r, 16, 6, 5), zeros(16),
+             he_lin(r, 256, 120), zeros(120), he_lin(r, 120, 84), zeros(84), he_lin(r, 84, 10), zeros(10)]
+        x = T(np.random.default_rng(1000).standard_normal((64, 1, 28, 28)))
+        y = T(np.random.default_rng(1002).integers(0, 10, 64))
+        opt = nn.SGD(P, lr=0.01)
 
-    def lenet_step():
-        opt.zero_grad()
-        h = nn.maxpool2d(nn.conv2d(x, P[0], P[1], 1, 0, 1), 2, 2)
-        h = nn.flatten(nn.maxpool2d(nn.conv2d(h, P[2], P[3], 1, 0, 1), 2, 2))
-        h = nn.bias_relu(nn.matmul(h, P[4]), P[5])
-        h = nn.bias_relu(nn.matmul(h, P[6]), P[7])
-        loss = nn.softmax_ce(nn.add_bias(nn.matmul(h, P[8]), P[9]), y)
-        loss.backward()
-        opt.step(clip=1.0)
-        nn.end_batch()
-    run_config(1, "LeNet-5 b64 train step (SGD lr 0.01, clip 1.0)", 64, lenet_step)
-    del P, x, y, opt
+        def lenet_step():
+            opt.zero_grad()
+            h = nn.maxpool2d(nn.conv2d(x, P[0], P[1], 1, 0, 1), 2, 2)
+            h = nn.flatten(nn.maxpool2d(nn.conv2d(h, P[2], P[3], 1, 0, 1), 2, 2))
+            h = nn.bias_relu(nn.matmul(h, P[4]), P[5])
+            h = nn.bias_relu(nn.matmul(h, P[6]), P[7])
+            loss = nn.softmax_ce(nn.add_bias(nn.matmul(h, P[8]), P[9]), y)
+            loss.backward()
+            opt.step(clip=1.0)
+            nn.end_batch()
+        run_config(1, "LeNet-5 b64 train step (SGD lr 0.01, clip 1.0)", 64, lenet_step)
 
     # 2 single conv backward
-    r = np.random.default_rng(2001)
-    W, b = he_conv(r, 128, 64, 3), zeros(128)
-    x2 = T(np.random.default_rng(2000).standard_normal((128, 64, 56, 56)), True)
-    dy = np.random.default_rng(2002).standard_normal((128, 128, 56, 56)).astype(np.float32)
-    gy = T(dy)
+    def config2():
+        r = np.random.default_rng(2001)
+        W, b = he_conv(r, 128, 64, 3), zeros(128)
+        x2 = T(np.random.default_rng(2000).standard_normal((128, 64, 56, 56)), True)
+        dy = np.random.default_rng(2002).standard_normal((128, 128, 56, 56)).astype(np.float32)
+        gy = T(dy)
 
-    def conv_step():
-        W.grad = b.grad = x2.grad = None
-        yv = nn.conv2d(x2, W, b, 1, 1, 1)
-        yv.backward(gy)  # ConvBackwardFused masks dy with [y > 0]
-        nn.end_batch()
-    run_config(2, "single conv backward x[128,64,56,56] W[128,64,3,3] p1 ReLU: dW + dX + db",
-               128, conv_step, {"conv_bwd_gflop_algorithmic": round(2 * 2 * 128 * 64 * 9 * 128 * 56 * 56 / 1e9, 2)})
-    del W, b, x2, gy, dy
+        def conv_step():
+            W.grad = b.grad = x2.grad = None
+            yv = nn.conv2d(x2, W, b, 1, 1, 1)
+            yv.backward(gy)  # ConvBackwardFused masks dy with [y > 0]
+            nn.end_batch()
+        run_config(2, "single conv backward x[128,64,56,56] W[128,64,3,3] p1 ReLU: dW + dX + db",
+                   128, conv_step, {"conv_bwd_gflop_algorithmic": round(2 * 2 * 128 * 64 * 9 * 128 * 56 * 56 / 1e9, 2)})
 
     # 3 MobileNetV2 inverted-residual stack b64 @112^2
-    r = np.random.default_rng(3001)
-    blocks = []
-    for ci, co, s in [(16, 24, 2), (24, 24, 1), (24, 32, 2), (32, 32, 1), (32, 32, 1)]:
-        h = ci * 6
-        blocks.append(dict(ci=ci, co=co, s=s,
-                           exp=(he_conv(r, h, ci, 1), zeros(h)),
-                           bn1=(ones(h), zeros(h), zeros(h, False), ones(h, False)),
-                           dw=(T(r.standard_normal((h, 1, 3, 3)) * np.sqrt(2.0 / 9), True), zeros(h)),
-                           bn2=(ones(h), zeros(h), zeros(h, False), ones(h, False)),
-                           proj=(he_conv(r, co, h, 1), zeros(co)),
-                           bn3=(ones(co), zeros(co), zeros(co, False), ones(co, False))))
-    fc = (he_lin(r, 32, 10), zeros(10))
-    Pm = [fc[0], fc[1]]
-    for bl in blocks:
-        for k in ("exp", "dw", "proj"):
-            Pm += list(bl[k])
-        for k in ("bn1", "bn2", "bn3"):
-            Pm += list(bl[k][:2])
-    x3 = T(np.random.default_rng(3000).standard_normal((64, 16, 112, 112)))
-    y3 = T(np.random.default_rng(3002).integers(0, 10, 64))
-    opt3 = nn.SGD(Pm, lr=0.01)
-
-    def mbv2_step():
-        opt3.zero_grad()
-        h = x3
+    def config3():
+        r = np.random.default_rng(3001)
+        blocks = []
+        for ci, co, s in [(16, 24, 2), (24, 24, 1), (24, 32, 2), (32, 32, 1), (32, 32, 1)]:
+            h = ci * 6
+            blocks.append(dict(ci=ci, co=co, s=s,
+                               exp=(he_conv(r, h, ci, 1), zeros(h)),
+                               bn1=(ones(h), zeros(h), zeros(h, False), ones(h, False)),
+                               dw=(T(r.standard_normal((h, 1, 3, 3)) * np.sqrt(2.0 / 9), True), zeros(h)),
+                               bn2=(ones(h), zeros(h), zeros(h, False), ones(h, False)),
+                               proj=(he_conv(r, co, h, 1), zeros(co)),
+                               bn3=(ones(co), zeros(co), zeros(co, False), ones(co, False))))
+        fc = (he_lin(r, 32, 10), zeros(10))
+        Pm = [fc[0], fc[1]]
         for bl in blocks:
-            t = nn.relu6(nn.batchnorm2d(nn.conv2d(h, *bl["exp"], 1, 0, 0), *bl["bn1"]))
-            t = nn.relu6(nn.batchnorm2d(nn.depthwise_conv2d(t, *bl["dw"], bl["s"], 1), *bl["bn2"]))
-            t = nn.batchnorm2d(nn.conv2d(t, *bl["proj"], 1, 0, 0), *bl["bn3"])
-            h = nn.add(t, h) if (bl["s"] == 1 and bl["ci"] == bl["co"]) else t
-        loss = nn.softmax_ce(nn.add_bias(nn.matmul(nn.global_avg_pool2d(h), fc[0]), fc[1]), y3)
-        loss.backward()
-        opt3.step(clip=1e30)
-        nn.end_batch()
-    run_config(3, "MobileNetV2 IR stack b64 @112^2 (16-24 s2, 24-24, 24-32 s2, 32-32 x2; "
-                  "expand x6, BN train, ReLU6, dw3x3) + GAP + Linear 10, SGD lr 0.01", 64, mbv2_step)
-    del blocks, Pm, x3, y3, opt3
+            for k in ("exp", "dw", "proj"):
+                Pm += list(bl[k])
+            for k in ("bn1", "bn2", "bn3"):
+                Pm += list(bl[k][:2])
+        x3 = T(np.random.default_rng(3000).standard_normal((64, 16, 112, 112)))
+        y3 = T(np.random.default_rng(3002).integers(0, 10, 64))
+        opt3 = nn.SGD(Pm, lr=0.01)
+
+        def mbv2_step():
+            opt3.zero_grad()
+            h = x3
+            for bl in blocks:
+                t = nn.relu6(nn.batchnorm2d(nn.conv2d(h, *bl["exp"], 1, 0, 0), *bl["bn1"]))
+                t = nn.relu6(nn.batchnorm2d(nn.depthwise_conv2d(t, *bl["dw"], bl["s"], 1), *bl["bn2"]))
+                t = nn.batchnorm2d(nn.conv2d(t, *bl["proj"], 1, 0, 0), *bl["bn3"])
+                h = nn.add(t, h) if (bl["s"] == 1 and bl["ci"] == bl["co"]) else t
+            loss = nn.softmax_ce(nn.add_bias(nn.matmul(nn.global_avg_pool2d(h), fc[0]), fc[1]), y3)
+            loss.backward()
+            opt3.step(clip=1e30)
+            nn.end_batch()
+        run_config(3, "MobileNetV2 IR stack b64 @112^2 (16-24 s2, 24-24, 24-32 s2, 32-32 x2; "
+                      "expand x6, BN train, ReLU6, dw3x3) + GAP + Linear 10, SGD lr 0.01", 64, mbv2_step)
 
     # 4 UNet-base16 b8 @256^2
-    r = np.random.default_rng(4001)
-    U = {}
+    def config4():
+        r = np.random.default_rng(4001)
+        U = {}
 
-    def cbr_p(name, cin, cout):
-        U[name] = (he_conv(r, cout, cin, 3), zeros(cout), ones(cout), zeros(cout),
-                   zeros(cout, False), ones(cout, False))
-    ch = [16, 32, 64, 128]
-    prev = 3
-    for i, c in enumerate(ch):
-        cbr_p(f"e{i}a", prev, c)
-        cbr_p(f"e{i}b", c, c)
-        prev = c
-    cbr_p("ba", prev, 256)
-    cbr_p("bb", 256, 256)
-    prev = 256
-    for i in reversed(range(4)):
-        cbr_p(f"d{i}a", prev + ch[i], ch[i])
-        cbr_p(f"d{i}b", ch[i], ch[i])
-        prev = ch[i]
-    head = (he_conv(r, 1, 16, 1), zeros(1))
-    Pu = list(head)
-    for v in U.values():
-        Pu += list(v[:4])
-    x4 = T(np.random.default_rng(4000).random((8, 3, 256, 256)))
-    m = (np.random.default_rng(4002).random((8, 1, 32, 32)) < 0.3).astype(np.float32)
-    t4 = T(m.repeat(8, axis=2).repeat(8, axis=3))
-    opt4 = nn.Adam(Pu, lr=1e-3)
-
-    def cbr(h, name):
-        w, bb, g, be, rm, rv = U[name]
-        return nn.relu(nn.batchnorm2d(nn.conv2d(h, w, bb, 1, 1, 0), g, be, rm, rv))
-
-    def unet_step():
-        opt4.zero_grad()
-        h = x4
-        skips = []
-        for i in range(4):
-            h = cbr(cbr(h, f"e{i}a"), f"e{i}b")
-            skips.append(h)
-            h = nn.maxpool2d(h, 2, 2)
-        h = cbr(cbr(h, "ba"), "bb")
+        def cbr_p(name, cin, cout):
+            U[name] = (he_conv(r, cout, cin, 3), zeros(cout), ones(cout), zeros(cout),
+                       zeros(cout, False), ones(cout, False))
+        ch = [16, 32, 64, 128]
+        prev = 3
+        for i, c in enumerate(ch):
+            cbr_p(f"e{i}a", prev, c)
+            cbr_p(f"e{i}b", c, c)
+            prev = c
+        cbr_p("ba", prev, 256)
+        cbr_p("bb", 256, 256)
+        prev = 256
         for i in reversed(range(4)):
-            h = nn.concat([nn.upsample2d(h, 2, 2), skips[i]])
-            h = cbr(cbr(h, f"d{i}a"), f"d{i}b")
-        loss = nn.dice_loss(nn.sigmoid(nn.conv2d(h, head[0], head[1], 1, 0, 0)), t4)
-        loss.backward()
-        nn.clip_grad_norm(Pu, 1.0)
-        opt4.step(clip=1e30)
-        nn.end_batch()
-    run_config(4, "UNet-base16 b8 @256^2 (4 levels, conv3x3-BN-ReLU x2, Dice on sigmoid; "
-                  "norm clip 1.0 + Adam lr 1e-3)", 8, unet_step)
+            cbr_p(f"d{i}a", prev + ch[i], ch[i])
+            cbr_p(f"d{i}b", ch[i], ch[i])
+            prev = ch[i]
+        head = (he_conv(r, 1, 16, 1), zeros(1))
+        Pu = list(head)
+        for v in U.values():
+            Pu += list(v[:4])
+        x4 = T(np.random.default_rng(4000).random((8, 3, 256, 256)))
+        m = (np.random.default_rng(4002).random((8, 1, 32, 32)) < 0.3).astype(np.float32)
+        t4 = T(m.repeat(8, axis=2).repeat(8, axis=3))
+        opt4 = nn.Adam(Pu, lr=1e-3)
+
+        def cbr(h, name):
+            w, bb, g, be, rm, rv = U[name]
+            return nn.relu(nn.batchnorm2d(nn.conv2d(h, w, bb, 1, 1, 0), g, be, rm, rv))
+
+        def unet_step():
+            opt4.zero_grad()
+            h = x4
+            skips = []
+            for i in range(4):
+                h = cbr(cbr(h, f"e{i}a"), f"e{i}b")
+                skips.append(h)
+                h = nn.maxpool2d(h, 2, 2)
+            h = cbr(cbr(h, "ba"), "bb")
+            for i in reversed(range(4)):
+                h = nn.concat([nn.upsample2d(h, 2, 2), skips[i]])
+                h = cbr(cbr(h, f"d{i}a"), f"d{i}b")
+            loss = nn.dice_loss(nn.sigmoid(nn.conv2d(h, head[0], head[1], 1, 0, 0)), t4)
+            loss.backward()
+            nn.clip_grad_norm(Pu, 1.0)
+            opt4.step(clip=1e30)
+            nn.end_batch()
+        run_config(4, "UNet-base16 b8 @256^2 (4 levels, conv3x3-BN-ReLU x2, Dice on sigmoid; "
+                      "norm clip 1.0 + Adam lr 1e-3)", 8, unet_step)
+
+    for cid, fn in ((1, config1), (2, config2), (3, config3), (4, config4)):
+        if not ids or cid in ids:
+            fn()
 
 
 def copy_calibration(mib=256, reps=3):
@@ -597,6 +602,8 @@ def main():
                     help="train: the AlexNet-224 b128 train step (default, one JSON line); "
                          "memory: the backward memory-bound kernels, one JSON line each; "
                          "configs: LeNet, single conv, MobileNetV2 stack, UNet steps, one line each")
+    ap.add_argument("--configs", default="",
+                    help="with --suite configs: comma-separated configuration numbers (default all)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of 256 MiB three times (the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -611,7 +618,8 @@ def main():
         memory_suite()
         return
     if args.suite == "configs":
-        configs_suite(steps=min(args.steps, 10), warmup=args.warmup)
+        ids = {int(v) for v in args.configs.split(",")} if args.configs else None
+        configs_suite(steps=min(args.steps, 10), warmup=args.warmup, ids=ids)
         return
 
     from directcompute_torch_amd import nn_engine as nn

@@ -4,9 +4,10 @@
 //
 //   C[m, n] = sum_k A[m, k] * B[n, k]
 //
-// Workgroup: 256 threads = 4 wave64 in a 2x2 arrangement owning an MT x NT
-// output tile (MT, NT in {64, 128}); each wave an (MT/2) x (NT/2) block of
-// 16x16 accumulators.  K advances in tiles of KT (16 or 32) through a double
+// Workgroup: 256 threads = 4 wave64 owning an MT x NT output tile: for MT in
+// {64, 128} the waves sit 2x2, each with an (MT/2) x (NT/2) block of 16x16
+// accumulators; for the narrow tiles MT in {16, 32} (few output channels)
+// they sit 1x4, each with an MT x (NT/4) block.  K advances in tiles of KT (16 or 32) through a double
 // buffered LDS stage with one barrier per tile; the next tile's global loads
 // are in flight while the current one is multiplied.
 //
@@ -55,8 +56,13 @@ struct Stage {
   static constexpr int SIZE = KROW ? KT * LD : R * LD;
   static constexpr int KQ = KT / 4;
   static constexpr int RQ = R / 4;
-  static_assert((R * KT / 4) % kThreads == 0, "tile must split evenly over the workgroup");
-  static constexpr int Q = R * KT / 4 / kThreads;
+  // NQ quads per stage.  A narrow operand (NQ < kThreads) is staged by the
+  // first NQ threads, one quad each; the others load and store nothing.
+  static constexpr int NQ = R * KT / 4;
+  static_assert(NQ % kThreads == 0 || kThreads % NQ == 0, "tile must split evenly over the workgroup");
+  static constexpr bool PART = NQ < kThreads;
+  static constexpr int Q = PART ? 1 : NQ / kThreads;
+  __device__ static __forceinline__ bool active(int t) { return !PART || t < NQ; }
   // Quad i of thread t.  ROWK: consecutive lanes take consecutive k-quads of
   // one row; KROW: consecutive lanes take consecutive row-quads of one k.
   // kThreads is a multiple of KQ and RQ, so quad i sits DROW rows (ROWK) or
@@ -87,8 +93,13 @@ template <class St>
 struct LoaderBase {
   static constexpr int Q = St::Q;
   int lds0;
-  __device__ __forceinline__ void base_init(int tid) { lds0 = St::lds_off(tid); }
+  bool act;
+  __device__ __forceinline__ void base_init(int tid) {
+    lds0 = St::lds_off(tid);
+    act = St::active(tid);
+  }
   __device__ __forceinline__ void store(float* S, const f4 (&r)[Q]) const {
+    if (St::PART && !act) return;
 #pragma unroll
     for (int i = 0; i < Q; ++i) *reinterpret_cast<f4*>(S + lds0 + i * St::DLDS) = r[i];
   }
@@ -122,7 +133,7 @@ struct LdDenseRK : LoaderBase<Stage<R, KT, false>> {
 #pragma unroll
     for (int i = 0; i < Q; ++i) {
       const uint32_t row = row0 + St::qrow(tid, i);
-      base[i] = row < P.rows ? row * P.ld + kq : kOob;
+      base[i] = (this->act && row < P.rows) ? row * P.ld + kq : kOob;
     }
   }
   __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
@@ -152,7 +163,7 @@ struct LdDenseKR : LoaderBase<Stage<R, KT, true>> {
     ld = P.ld;
     kk0 = St::qk(tid, 0);
     const uint32_t row = row0 + St::qrow(tid, 0);
-    base = row < P.rows ? kk0 * P.ld + row : kOob;
+    base = (this->act && row < P.rows) ? kk0 * P.ld + row : kOob;
   }
   __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
     const uint32_t k0 = kt * KT;
@@ -185,6 +196,7 @@ constexpr int kCB = 16;
 template <int R, int KT, bool FWD, bool S1, bool BLK>
 struct LdPixRK : LoaderBase<Stage<R, KT, false>> {
   static_assert(!BLK || KT == kCB, "blocked order: one K tile per (channel block, tap)");
+  static_assert(!Stage<R, KT, false>::PART, "pixel operands fill the workgroup");
   using St = Stage<R, KT, false>;
   static constexpr bool KROW = false;
   using LoaderBase<St>::Q;
@@ -291,7 +303,7 @@ struct LdGradKR : LoaderBase<Stage<R, KT, true>> {
     npix = P.npix;
     kk0 = St::qk(tid, 0);
     const uint32_t oc = row0 + St::qrow(tid, 0);
-    base = oc < P.OCp ? kk0 * P.OCp + oc : kOob;
+    base = (this->act && oc < P.OCp) ? kk0 * P.OCp + oc : kOob;
   }
   __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
     const uint32_t p0 = kt * KT;
@@ -307,6 +319,7 @@ struct LdGradKR : LoaderBase<Stage<R, KT, true>> {
 // x_nhwc[b, oh*s + kh - p, ow*s + kw - p, c] or 0 outside the image.
 template <int R, int KT>
 struct LdXTapKR : LoaderBase<Stage<R, KT, true>> {
+  static_assert(!Stage<R, KT, true>::PART, "pixel operands fill the workgroup");
   using St = Stage<R, KT, true>;
   static constexpr bool KROW = true;
   using LoaderBase<St>::Q;
@@ -359,7 +372,7 @@ struct LdXTapKR : LoaderBase<Stage<R, KT, true>> {
 
 // ---------------------------------------------------------------------------
 // Epilogues.  Lane l of wave (wm, wn) holds, for MFMA block (i, j) and
-// register v, C[m0 + wm*MT/2 + 16i + 4(l/16) + v][n0 + wn*NT/2 + 16j + l%16].
+// register v, C[m0 + wm*16FM + 16i + 4(l/16) + v][n0 + wn*16FN + 16j + l%16].
 // ---------------------------------------------------------------------------
 struct EpiRowMajor {
   struct Params {
@@ -374,12 +387,12 @@ struct EpiRowMajor {
     const int r = lane & 15, g = lane >> 4;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-      const uint32_t n = n0 + wn * (NT / 2) + j * 16 + r;
+      const uint32_t n = n0 + wn * (FN * 16) + j * 16 + r;
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const uint32_t m = m0 + wm * (MT / 2) + i * 16 + 4 * g + v;
+          const uint32_t m = m0 + wm * (FM * 16) + i * 16 + 4 * g + v;
           if (m < p.M && n < p.N) c[m * p.ldc + n] = acc[i][j][v];
         }
       }
@@ -403,14 +416,14 @@ struct EpiNCHW {
     const int r = lane & 15, g = lane >> 4;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-      const uint32_t n = n0 + wn * (NT / 2) + j * 16 + r;
+      const uint32_t n = n0 + wn * (FN * 16) + j * 16 + r;
       const uint32_t b = fdiv(n, p.dHW);
       const uint32_t base = b * p.M * p.HW + (n - b * p.HW);
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const uint32_t m = m0 + wm * (MT / 2) + i * 16 + 4 * g + v;
+          const uint32_t m = m0 + wm * (FM * 16) + i * 16 + 4 * g + v;
           if (m < p.M && n < p.N) {
             float z = acc[i][j][v];
             if (p.bias) z += p.bias[m];
@@ -465,13 +478,15 @@ __global__ void __launch_bounds__(kThreads)
             const typename EPI::Params pe, TileGrid tg, uint32_t ktiles, uint32_t splits) {
   using SA = typename LA::St;
   using SB = typename LB::St;
-  constexpr int WM = MT / 2, WN = NT / 2, FM = WM / 16, FN = WN / 16;
+  constexpr int WGM = MT >= 64 ? 2 : 1, WGN = 4 / WGM;  // wave grid
+  constexpr int WM = MT / WGM, WN = NT / WGN, FM = WM / 16, FN = WN / 16;
+  static_assert(FM >= 1 && FN >= 1 && WM % 16 == 0 && WN % 16 == 0, "tile too small");
   __shared__ __attribute__((aligned(16))) float As[2 * SA::SIZE];
   __shared__ __attribute__((aligned(16))) float Bs[2 * SB::SIZE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WGN, wn = wave % WGN;
   uint32_t mt, nt, z;
   tile_coords(tg, mt, nt, z);
   const uint32_t m0 = mt * MT, n0 = nt * NT;
@@ -752,6 +767,15 @@ static int pick_tile(uint32_t extent) {
   return (w128 * 100 > w64 * 112) ? 64 : 128;
 }
 
+// Rows of the output tile (the channel axis): the narrow 16- and 32-row tiles
+// for up to 16 / 32 channels, where a 64-row tile would feed the matrix unit
+// mostly zero rows.
+static int pick_tile_m(uint32_t M) {
+  if (M <= 16) return 16;
+  if (M <= 32) return 32;
+  return pick_tile(M);
+}
+
 // Workgroups of one kernel instantiation that fit on a CU at once.
 template <class Kern>
 static int occupancy(Kern kernel) {
@@ -801,7 +825,8 @@ static double est_us(uint32_t M, uint32_t N, uint32_t kdim, const TileCfg& c, in
 template <class OccFn>
 static TileCfg choose(const char* var, uint32_t M, uint32_t N, uint32_t kdim, uint32_t max_splits,
                       bool dense_out, OccFn&& occ, bool kt16_only = false) {
-  TileCfg c{pick_tile(M), pick_tile(N), 16, 1};
+  TileCfg c{pick_tile_m(M), pick_tile(N), 16, 1};
+  if (kt16_only && c.MT < 64) c.NT = 128;  // the pixel GEMMs' narrow tiles are 128 or 256 wide
   const uint32_t ktiles = cdiv(kdim, uint32_t(c.KT));
   if (tune_override(var, c)) {
     if (kt16_only) c.KT = 16;
@@ -840,24 +865,28 @@ static bool launch(const typename LA::Params& pa, const typename LB::Params& pb,
   return check_launch(what);
 }
 
-// Dispatch a functor over the four (MT, NT) tile shapes and two KT depths.
+// Dispatch a functor over the (MT, NT) tile shapes: 64/128 square-ish tiles at
+// two KT depths and the narrow MT = 16/32 tiles at KT = 16.
 template <class F>
 static bool tiles_dispatch(const TileCfg& c, F&& f) {
 #define DCE_T(a, b, k) \
   if (c.MT == a && c.NT == b && c.KT == k) return f.template run<a, b, k>();
   DCE_T(128, 128, 32) DCE_T(128, 64, 32) DCE_T(64, 128, 32) DCE_T(64, 64, 32)
   DCE_T(128, 128, 16) DCE_T(128, 64, 16) DCE_T(64, 128, 16) DCE_T(64, 64, 16)
+  DCE_T(32, 128, 16) DCE_T(32, 64, 16) DCE_T(16, 128, 16) DCE_T(16, 64, 16)
 #undef DCE_T
   set_error("igemm: unsupported tile %dx%dx%d", c.MT, c.NT, c.KT);
   return false;
 }
 
-// The same over the KT = 16 shapes only (the blocked-K pixel loaders).
+// The KT = 16 shapes of the pixel-row GEMMs (forward, dX): the narrow tiles
+// come with 128 or 256 pixel columns.
 template <class F>
 static bool tiles_dispatch16(const TileCfg& c, F&& f) {
 #define DCE_T(a, b) \
   if (c.MT == a && c.NT == b && c.KT == 16) return f.template run<a, b, 16>();
   DCE_T(128, 128) DCE_T(128, 64) DCE_T(64, 128) DCE_T(64, 64)
+  DCE_T(32, 256) DCE_T(32, 128) DCE_T(16, 256) DCE_T(16, 128)
 #undef DCE_T
   set_error("igemm: unsupported tile %dx%dx%d", c.MT, c.NT, c.KT);
   return false;
@@ -867,6 +896,7 @@ static int tiles_occ16(const TileCfg& c, const F& f) {
 #define DCE_T(a, b) \
   if (c.MT == a && c.NT == b && c.KT == 16) return f.template occ<a, b, 16>(c.splits > 1);
   DCE_T(128, 128) DCE_T(128, 64) DCE_T(64, 128) DCE_T(64, 64)
+  DCE_T(32, 256) DCE_T(32, 128) DCE_T(16, 256) DCE_T(16, 128)
 #undef DCE_T
   return 1;
 }
@@ -878,6 +908,7 @@ static int tiles_occ(const TileCfg& c, const F& f) {
   if (c.MT == a && c.NT == b && c.KT == k) return f.template occ<a, b, k>(c.splits > 1);
   DCE_T(128, 128, 32) DCE_T(128, 64, 32) DCE_T(64, 128, 32) DCE_T(64, 64, 32)
   DCE_T(128, 128, 16) DCE_T(128, 64, 16) DCE_T(64, 128, 16) DCE_T(64, 64, 16)
+  DCE_T(32, 128, 16) DCE_T(32, 64, 16) DCE_T(16, 128, 16) DCE_T(16, 64, 16)
 #undef DCE_T
   return 1;
 }

@@ -215,6 +215,27 @@ def test_forced_tile_configs(eng, monkeypatch, cfg):
         test_matmul_alloc(eng, 5, 7, 3, flags)
 
 
+NARROW_CFGS = [(f"{mt},{nt},16,{sp}", f"{mt},{nd},16,{sp}") for mt in (16, 32)
+               for nt, nd in ((128, 64), (256, 128)) for sp in (1, 3)]
+
+
+@pytest.mark.parametrize("pix_cfg,dense_cfg", NARROW_CFGS, ids=[c[0] for c in NARROW_CFGS])
+def test_forced_narrow_tiles(eng, monkeypatch, pix_cfg, dense_cfg):
+    """The narrow 16- and 32-row tiles (1x4 wave grid, A operand staged by a
+    subset of the threads), forced on every GEMM family, including output
+    channel counts above the tile height (several M tiles) and split-K."""
+    for var in ("DCE_TUNE_FWD", "DCE_TUNE_DX"):
+        monkeypatch.setenv(var, pix_cfg)
+    for var in ("DCE_TUNE_DW", "DCE_TUNE_GEMM"):
+        monkeypatch.setenv(var, dense_cfg)
+    _conv_case(eng, 2, 16, 14, 14, 20, 3, 2, 1, 1)   # stride 2, OC 20 (two 16-row tiles)
+    _conv_case(eng, 2, 48, 10, 10, 16, 3, 1, 1, 1)   # stride 1, C 48 (dX: three 16-row tiles)
+    _conv_case(eng, 3, 3, 17, 19, 8, 5, 1, 2, 1)     # C = 3 padded to 4, OC 8
+    for flags in range(4):
+        test_matmul_alloc(eng, 37, 129, 70, flags)
+        test_matmul_alloc(eng, 5, 7, 3, flags)
+
+
 def test_linear_tile_order(eng, monkeypatch):
     """DCE_XCD=0 (plain tile order) gives the same results as the default
     XCD-contiguous order."""
