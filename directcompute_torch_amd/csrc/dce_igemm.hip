@@ -580,9 +580,7 @@ __global__ void __launch_bounds__(256)
     float s = 0.f;
 #pragma unroll
     for (int q = 0; q < 8; ++q) s += t[cl][part * 8 + q];
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
-    s += __shfl_xor(s, 4, 64);
+    s = group8_reduce(s);
     if (part == 0 && c0 + cl < C)
       dbPart[size_t(c0 + cl) * gridDim.z * npb + size_t(b) * npb + blockIdx.x] = s;
   }
@@ -621,8 +619,7 @@ __global__ void __launch_bounds__(256)
   const float* p = part + size_t(c) * rows;
   float s = 0.f;
   for (uint32_t r = threadIdx.x; r < rows; r += 256) s += p[r];
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) s += __shfl_down(s, o, 64);
+  s = wave_reduce(s);
   if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = s;
   __syncthreads();
   if (threadIdx.x == 0) out[c] = (sh[0] + sh[1]) + (sh[2] + sh[3]);

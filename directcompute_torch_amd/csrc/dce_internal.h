@@ -96,6 +96,90 @@ struct BRes {
 };
 
 // ---------------------------------------------------------------------------
+// Wave-wide reductions over the 64 lanes of a wavefront, without LDS.  Inside
+// each row of 16 lanes, DPP moves combine lanes: quad_perm [1,0,3,2] and
+// [2,3,0,1] (every lane holds its quad's total), row_half_mirror (its 8-lane
+// half-row's), row_mirror (its row's).  ds_swizzle with xor mask 16 then
+// combines neighbouring rows inside each 32-lane half, and readlane 0 / 32
+// joins the halves.  Every step pairs each lane with a partner holding the
+// mirror-image partial, so all lanes carry bit-identical values throughout and
+// the result (returned in every lane) does not depend on the lane.  All 64
+// lanes must be active.
+// ---------------------------------------------------------------------------
+namespace xl {
+constexpr int kQuadSwap1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int kQuadSwap2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int kHalfMirror = 0x141; // row_half_mirror
+constexpr int kRowMirror = 0x140;  // row_mirror
+constexpr int kSwzXor16 = 0x401F;  // ds_swizzle bit mode: and 0x1F, or 0, xor 0x10
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp32(uint32_t v) {
+  return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ uint32_t swz32(uint32_t v) {
+  return uint32_t(__builtin_amdgcn_ds_swizzle(int(v), kSwzXor16));
+}
+__device__ __forceinline__ uint32_t rdl32(uint32_t v, int lane) {
+  return uint32_t(__builtin_amdgcn_readlane(int(v), lane));
+}
+// A value moved lane to lane as 32-bit words.
+template <class T>
+struct Words;
+template <>
+struct Words<float> {
+  template <class F>
+  __device__ static __forceinline__ float map(float v, F f) {
+    return __builtin_bit_cast(float, f(__builtin_bit_cast(uint32_t, v)));
+  }
+};
+template <>
+struct Words<double> {
+  template <class F>
+  __device__ static __forceinline__ double map(double v, F f) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint64_t lo = f(uint32_t(u)), hi = f(uint32_t(u >> 32));
+    return __builtin_bit_cast(double, (hi << 32) | lo);
+  }
+};
+template <int CTRL, class T>
+__device__ __forceinline__ T dpp(T v) {
+  return Words<T>::map(v, [](uint32_t w) { return dpp32<CTRL>(w); });
+}
+template <class T>
+__device__ __forceinline__ T swz(T v) {
+  return Words<T>::map(v, [](uint32_t w) { return swz32(w); });
+}
+template <class T>
+__device__ __forceinline__ T readlane(T v, int lane) {
+  return Words<T>::map(v, [lane](uint32_t w) { return rdl32(w, lane); });
+}
+}  // namespace xl
+
+struct OpAddR {
+  template <class T>
+  __device__ __forceinline__ T operator()(T a, T b) const { return a + b; }
+};
+struct OpMaxR {
+  __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+
+// Combine of the 8 lanes 8j..8j+7 (every lane of the group gets it).
+template <class T, class Op = OpAddR>
+__device__ __forceinline__ T group8_reduce(T v, Op op = Op()) {
+  v = op(v, xl::dpp<xl::kQuadSwap1>(v));
+  v = op(v, xl::dpp<xl::kQuadSwap2>(v));
+  return op(v, xl::dpp<xl::kHalfMirror>(v));
+}
+template <class T, class Op = OpAddR>
+__device__ __forceinline__ T wave_reduce(T v, Op op = Op()) {
+  v = group8_reduce(v, op);
+  v = op(v, xl::dpp<xl::kRowMirror>(v));
+  v = op(v, xl::swz(v));
+  return op(xl::readlane(v, 0), xl::readlane(v, 32));
+}
+
+// ---------------------------------------------------------------------------
 // Convolution geometry (NCHW, square kernels, zero padding, floor mode).
 // ---------------------------------------------------------------------------
 struct ConvGeom {

@@ -29,8 +29,7 @@ __device__ __forceinline__ uint32_t gtid() { return blockIdx.x * blockDim.x + th
 
 // Block-wide sum (256 threads) in double; result valid in thread 0.
 __device__ __forceinline__ double block_sum256(double v, double* sh) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_down(v, o, 64);
+  v = wave_reduce(v);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   __syncthreads();
   if (lane == 0) sh[w] = v;
@@ -287,12 +286,10 @@ __global__ void k_softmax_rows(Buf in, Buf out, Buf labels, float* rowLoss, uint
   const uint32_t base = row * K;
   float mx = -1e30f;
   for (uint32_t j = lane; j < K; j += 64) mx = fmaxf(mx, ld(in, base + j));
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  mx = wave_reduce(mx, OpMaxR());
   float s = 0.f;
   for (uint32_t j = lane; j < K; j += 64) s += expf(ld(in, base + j) - mx);
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  s = wave_reduce(s);
   if (writeSoftmax) {
     for (uint32_t j = lane; j < K; j += 64) st(out, base + j, expf(ld(in, base + j) - mx) / s);
   }
@@ -622,19 +619,32 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// The pieces of channel c summed by one wave: lane l adds pieces l, l+64, ...
+// (two moments), then a DPP wave reduction.  Four channels per 256 threads.
+__device__ __forceinline__ bool bn_piece_sums(const double* part, uint32_t pieces, uint32_t C,
+                                              uint32_t& c, double& s0, double& s1) {
+  c = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (c >= C) return false;  // whole waves leave together
+  const uint32_t lane = threadIdx.x & 63;
+  double a0 = 0, a1 = 0;
+  for (uint32_t p = lane; p < pieces; p += 64) {
+    a0 += part[(size_t(c) * pieces + p) * 2];
+    a1 += part[(size_t(c) * pieces + p) * 2 + 1];
+  }
+  s0 = wave_reduce(a0);
+  s1 = wave_reduce(a1);
+  return lane == 0;
+}
+
 // batchnorm_mean_var finalize: the formulas of nn_batchnorm_mean_var.hlsl:46-59
 // (one-pass var = max(0, E[x^2] - E[x]^2), unbiased running var
 // var*m/max(1, m-1), momentum update), evaluated in double.
-__global__ void k_bn_stats_final(const double* part, uint32_t pieces, uint32_t C, uint32_t m,
-                                 Buf mean, Buf var, Buf rmean, Buf rvar, uint32_t training,
-                                 float momentum) {
-  const uint32_t c = gtid();
-  if (c >= C) return;
-  double s0 = 0, s1 = 0;
-  for (uint32_t p = 0; p < pieces; ++p) {
-    s0 += part[(size_t(c) * pieces + p) * 2];
-    s1 += part[(size_t(c) * pieces + p) * 2 + 1];
-  }
+__global__ void __launch_bounds__(256)
+    k_bn_stats_final(const double* part, uint32_t pieces, uint32_t C, uint32_t m, Buf mean,
+                     Buf var, Buf rmean, Buf rvar, uint32_t training, float momentum) {
+  uint32_t c;
+  double s0, s1;
+  if (!bn_piece_sums(part, pieces, C, c, s0, s1)) return;
   const double mu = s0 / m;
   const double v = fmax(0.0, s1 / m - mu * mu);
   st(mean, c, float(mu));
@@ -646,15 +656,11 @@ __global__ void k_bn_stats_final(const double* part, uint32_t pieces, uint32_t C
     st(rvar, c, float((1.0 - mo) * ld(rvar, c) + mo * unb));
   }
 }
-__global__ void k_bn_grad_final(const double* part, uint32_t pieces, uint32_t C, Buf dgamma,
-                                Buf dbeta) {
-  const uint32_t c = gtid();
-  if (c >= C) return;
-  double s0 = 0, s1 = 0;
-  for (uint32_t p = 0; p < pieces; ++p) {
-    s0 += part[(size_t(c) * pieces + p) * 2];
-    s1 += part[(size_t(c) * pieces + p) * 2 + 1];
-  }
+__global__ void __launch_bounds__(256)
+    k_bn_grad_final(const double* part, uint32_t pieces, uint32_t C, Buf dgamma, Buf dbeta) {
+  uint32_t c;
+  double s0, s1;
+  if (!bn_piece_sums(part, pieces, C, c, s0, s1)) return;
   st(dgamma, c, float(s0));
   st(dbeta, c, float(s1));
 }
@@ -719,7 +725,7 @@ static bool sh_bn_mean_var(const Dispatch& d) {
   if (!bn_reduce("batchnorm_mean_var", 0, d, S(d, 0), Buf{nullptr, 0}, Buf{nullptr, 0},
                  Buf{nullptr, 0}, 0.f, N, C, Sz, &part, &pc))
     return false;
-  hipLaunchKernelGGL(k_bn_stats_final, dim3(cdiv(C, 256)), dim3(256), 0, stream(), part,
+  hipLaunchKernelGGL(k_bn_stats_final, dim3(cdiv(C, 4)), dim3(256), 0, stream(), part,
                      pc.pieces, C, N * Sz, U(d, 0), U(d, 1), U(d, 2), U(d, 3), training,
                      momentum);
   return check_launch("batchnorm_mean_var");
@@ -735,7 +741,7 @@ static bool sh_bn_backward_reduce(const Dispatch& d) {
   if (!bn_reduce("batchnorm_backward_reduce", 1, d, S(d, 0), S(d, 1), S(d, 2), S(d, 3), eps, N, C,
                  Sz, &part, &pc))
     return false;
-  hipLaunchKernelGGL(k_bn_grad_final, dim3(cdiv(C, 256)), dim3(256), 0, stream(), part,
+  hipLaunchKernelGGL(k_bn_grad_final, dim3(cdiv(C, 4)), dim3(256), 0, stream(), part,
                      pc.pieces, C, U(d, 0), U(d, 1));
   return check_launch("batchnorm_backward_reduce");
 }
@@ -1598,9 +1604,7 @@ __global__ void __launch_bounds__(256)
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
 #pragma unroll
   for (int q = 0; q < T; ++q) {
-    float t = acc[q];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
+    const float t = wave_reduce(acc[q]);
     if (lane == 0) red[wv][q] = t;
   }
   __syncthreads();

@@ -197,9 +197,7 @@ __global__ void __launch_bounds__(256) k_multi_sumsq(const Table t, double* part
       }
     }
   }
-  double s = acc;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) s += __shfl_down(s, o, 64);
+  const double s = wave_reduce(double(acc));
   if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = s;
   __syncthreads();
   if (threadIdx.x == 0) part[base + blockIdx.x] = (sh[0] + sh[1]) + (sh[2] + sh[3]);
@@ -220,8 +218,7 @@ __global__ void __launch_bounds__(1024)
 #pragma unroll
     for (int u = 0; u < 4; ++u) s += v[u];
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) s += __shfl_down(s, o, 64);
+  s = wave_reduce(s);
   if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = s;
   __syncthreads();
   if (threadIdx.x == 0) {
