@@ -401,6 +401,7 @@ def configs_suite(steps=10, warmup=3, ids=None):
         t0 = time.perf_counter()
         for _ in range(steps):
             step()
+        th = (time.perf_counter() - t0) / steps  # host issue time (queue not yet drained)
         lib.SyncGPU()
         dt = (time.perf_counter() - t0) / steps
         h1, m1 = ctypes.c_uint64(), ctypes.c_uint64()
@@ -432,11 +433,12 @@ def configs_suite(steps=10, warmup=3, ids=None):
                    "TFLOP/s": round(tf, 2), "frac_mfma": round(tf / MFMA_FP32_PEAK_TFLOPS, 4)}
         rec = {"suite": "configs", "config": cid, "workload": name, "batch": batch,
                "ms_per_step": round(dt * 1e3, 4), "img_s": round(batch / dt, 1),
+               "host_issue_ms_per_step": round(th * 1e3, 4),
                "conv_bwd": bwd, "pool": pool, "families": fams}
         if extra:
             rec.update(extra)
         print(json.dumps(rec), flush=True)
-        log(f"[configs] {cid} {name}: {dt * 1e3:.3f} ms/step, {batch / dt:.0f} img/s"
+        log(f"[configs] {cid} {name}: {dt * 1e3:.3f} ms/step (host issue {th * 1e3:.3f}), {batch / dt:.0f} img/s"
             + (f"; conv-bwd {bwd['TFLOP/s']} TFLOP/s ({bwd['frac_mfma'] * 100:.1f}%)" if bwd else "")
             + f"; pool misses/step {pool['misses_per_step']:.1f} of {pool['hits_per_step'] + pool['misses_per_step']:.1f}")
         nn.end_batch()

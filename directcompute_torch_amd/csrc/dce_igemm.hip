@@ -285,15 +285,16 @@ struct LdPixRK : LoaderBase<Stage<R, KT, false>> {
 // dW operands (KROW, k = flat output pixel over the batch).
 // ---------------------------------------------------------------------------
 // A: G rows oc, element (oc, pix) = G_nhwc[pix*OCp + oc].
+struct GradKRParams {
+  const float* g;
+  uint32_t OCp, npix, n;
+};
 template <int R, int KT>
 struct LdGradKR : LoaderBase<Stage<R, KT, true>> {
   using St = Stage<R, KT, true>;
   static constexpr bool KROW = true;
   using LoaderBase<St>::Q;
-  struct Params {
-    const float* g;
-    uint32_t OCp, npix, n;
-  };
+  using Params = GradKRParams;
   BRes b;
   uint32_t OCp, npix, kk0, base;  // base: quad 0's offset, or kOob for channels past OCp
   __device__ __forceinline__ void init(const Params& P, uint32_t row0, int tid) {
@@ -317,17 +318,17 @@ struct LdGradKR : LoaderBase<Stage<R, KT, true>> {
 
 // B: x taps, rows n = (kh, kw, c) (c fastest, Cp), element (n, pix) =
 // x_nhwc[b, oh*s + kh - p, ow*s + kw - p, c] or 0 outside the image.
+struct XTapParams {
+  const float* x;
+  uint32_t H, W, Cp, k, s, p, OW, OHW, npix, N, n;
+  FastDiv dOHW, dOW, dCp, dK;
+};
 template <int R, int KT>
 struct LdXTapKR : LoaderBase<Stage<R, KT, true>> {
-  static_assert(!Stage<R, KT, true>::PART, "pixel operands fill the workgroup");
   using St = Stage<R, KT, true>;
   static constexpr bool KROW = true;
   using LoaderBase<St>::Q;
-  struct Params {
-    const float* x;
-    uint32_t H, W, Cp, k, s, p, OW, OHW, npix, N, n;
-    FastDiv dOHW, dOW, dCp, dK;
-  };
+  using Params = XTapParams;
   BRes b;
   uint32_t H, W, Cp, s, OW, OHW, npix, kk0, off;
   FastDiv dOHW, dOW;
@@ -351,8 +352,9 @@ struct LdXTapKR : LoaderBase<Stage<R, KT, true>> {
     const uint32_t a = fdiv(khw, P.dK);
     kh = int(a) - int(P.p);
     kw = int(khw - a * P.k) - int(P.p);
-    // A row past the taps gets an offset no pixel can bring into the image.
-    if (n >= P.N) kh = -(1 << 20);
+    // A row past the taps (or a thread that stages nothing) gets an offset no
+    // pixel can bring into the image.
+    if (n >= P.N || !this->act) kh = -(1 << 20);
   }
   __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
 #pragma unroll
@@ -665,14 +667,15 @@ __global__ void k_splitk_sum(const float* __restrict__ part, float* __restrict__
   out[i] = s;
 }
 
-// dW finalize: dw[oc][c][khw] = sum_z part[z][oc][khw*Cp + c].  Block of
-// 1024 = 64 consecutive partial columns (storage order, so the
-// splits x OC x KK*Cp partial reads are coalesced) x 16 split slices: slice w
-// sums z = w, w+16, ..., then the 16 slice sums are added in slice order.
-// Padding channels (c >= C) are dropped.
+// dW finalize: dw[oc][c][khw] = sum_z part[z][oc][khw*Cp + c], or with
+// `trans` (the GEMM ran with taps as rows) sum_z part[z][khw*Cp + c][oc].
+// Block of 1024 = 64 consecutive partial elements (storage order, so the
+// partial reads are coalesced) x 16 split slices: slice w sums z = w, w+16,
+// ..., then the 16 slice sums are added in slice order.  Padding channels
+// (c >= C) are dropped.
 __global__ void __launch_bounds__(1024)
     k_dw_final(const float* __restrict__ part, float* __restrict__ dw, uint32_t OC, uint32_t C,
-               uint32_t KK, uint32_t Cp, uint32_t splits) {
+               uint32_t KK, uint32_t Cp, uint32_t splits, uint32_t trans) {
   __shared__ float sh[16][64];
   const uint32_t N = KK * Cp;
   const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -690,7 +693,14 @@ __global__ void __launch_bounds__(1024)
   float t = 0.f;
 #pragma unroll
   for (int k = 0; k < 16; ++k) t += sh[k][lane];
-  const uint32_t oc = i / N, n = i - oc * N;
+  uint32_t oc, n;
+  if (trans) {
+    n = i / OC;
+    oc = i - n * OC;
+  } else {
+    oc = i / N;
+    n = i - oc * N;
+  }
   const uint32_t khw = n / Cp, c = n - khw * Cp;
   if (c < C) dw[(size_t(oc) * C + c) * KK + khw] = t;
 }
@@ -1136,31 +1146,45 @@ bool conv_forward(const float* x, float* x_nhwc_keep, const float* w, const floa
 }
 
 // ----------------------------------------------------------- conv backward
+// dW = G (rows oc) x x-taps (rows (kh, kw, c)), both with k = output pixel.
+// `trans` swaps the operands (taps as output rows) for layers with fewer taps
+// x channels than output channels, so the narrow tiles cover the short axis.
 struct DwRun {
   const float* gn;
   const float* xn;
   float* part;
   ConvGeom g;
   uint32_t splits;
+  bool trans;
   template <int MT, int NT, int KT>
   int occ(bool) const {
-    return occupancy(k_igemm<MT, NT, KT, LdGradKR<MT, KT>, LdXTapKR<NT, KT>, EpiRowMajor>);
+    return trans ? occupancy(k_igemm<MT, NT, KT, LdXTapKR<MT, KT>, LdGradKR<NT, KT>, EpiRowMajor>)
+                 : occupancy(k_igemm<MT, NT, KT, LdGradKR<MT, KT>, LdXTapKR<NT, KT>, EpiRowMajor>);
   }
   template <int MT, int NT, int KT>
   bool run() {
     const uint32_t Cp = pad4(g.C), OCp = pad4(g.OC), KK = g.k * g.k, N = KK * Cp;
     const uint32_t OHW = g.OH * g.OW, npix = g.B * OHW;
-    using LA = LdGradKR<MT, KT>;
-    using LB = LdXTapKR<NT, KT>;
-    const typename LA::Params pa{gn, OCp, npix, npix * OCp};
-    const typename LB::Params pb{xn, g.H, g.W, Cp, g.k, g.s, g.p, g.OW, OHW, npix, N,
-                                 g.B * g.H * g.W * Cp, make_fastdiv(OHW), make_fastdiv(g.OW),
-                                 make_fastdiv(Cp), make_fastdiv(g.k)};
+    const GradKRParams pg{gn, OCp, npix, npix * OCp};
+    const XTapParams px{xn, g.H, g.W, Cp, g.k, g.s, g.p, g.OW, OHW, npix, N,
+                        g.B * g.H * g.W * Cp, make_fastdiv(OHW), make_fastdiv(g.OW),
+                        make_fastdiv(Cp), make_fastdiv(g.k)};
+    if (trans) {
+      const EpiRowMajor::Params pe{part, N, g.OC, g.OC, g.OC * N};
+      return launch<MT, NT, KT, LdXTapKR<MT, KT>, LdGradKR<NT, KT>, EpiRowMajor>(
+          px, pg, pe, N, g.OC, cdiv(npix, KT), splits, "conv_backward_filter");
+    }
     const EpiRowMajor::Params pe{part, g.OC, N, N, g.OC * N};
-    return launch<MT, NT, KT, LA, LB, EpiRowMajor>(pa, pb, pe, g.OC, N, cdiv(npix, KT), splits,
-                                                  "conv_backward_filter");
+    return launch<MT, NT, KT, LdGradKR<MT, KT>, LdXTapKR<NT, KT>, EpiRowMajor>(
+        pg, px, pe, g.OC, N, cdiv(npix, KT), splits, "conv_backward_filter");
   }
 };
+
+// Fraction of an M x N tile grid's area that is real output.
+static double tile_fill(uint32_t M, uint32_t N) {
+  const double mt = pick_tile_m(M), nt = pick_tile(N);
+  return double(M) * N / (std::ceil(M / mt) * mt * std::ceil(N / nt) * nt);
+}
 
 template <bool S1, bool BLK>
 struct DxRun {
@@ -1214,9 +1238,20 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
   const size_t nX = (dw && !x_nhwc) ? al64(nhwc_floats(g.B, g.C, g.H, g.W)) : 0;
   TileCfg dwc{128, 128, 16, 1}, dxc{128, 128, 16, 1};
   size_t nP = 0, nW = 0, nQ = 0;
+  bool dwT = false;
   if (dw) {
-    dwc = choose("DCE_TUNE_DW", g.OC, KK * Cp, npix, 256, false,
-                 [&](const TileCfg& t) { return tiles_occ(t, DwRun{}); });
+    // Orientation with the fuller tile grid; a grid of a few tiles gets more
+    // split-K slices so that the whole chip works on it.
+    const uint32_t taps = KK * Cp;
+    dwT = tile_fill(taps, g.OC) > tile_fill(g.OC, taps) * 1.25;
+    const uint32_t dM = dwT ? taps : g.OC, dN = dwT ? g.OC : taps;
+    const uint32_t ntiles = cdiv(dM, pick_tile_m(dM)) * cdiv(dN, pick_tile(dN));
+    dwc = choose("DCE_TUNE_DW", dM, dN, npix, ntiles <= 4 ? 1024 : 256, false,
+                 [&](const TileCfg& t) {
+                   DwRun r{};
+                   r.trans = dwT;
+                   return tiles_occ(t, r);
+                 });
     nP = al64(size_t(dwc.splits) * g.OC * KK * Cp);
   }
   if (dx) {
@@ -1253,10 +1288,10 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
       const double fl = 2.0 * g.OC * g.C * KK * double(npix);
       ProfScope prof("conv_dw", fl,
                      4.0 * (double(npix) * OCp + double(g.B) * g.H * g.W * Cp + double(g.OC) * KK * Cp));
-      ok = tiles_dispatch(dwc, DwRun{gn, xn, part, g, dwc.splits});
+      ok = tiles_dispatch(dwc, DwRun{gn, xn, part, g, dwc.splits, dwT});
       if (ok) {
         hipLaunchKernelGGL(k_dw_final, dim3(cdiv(size_t(g.OC) * KK * Cp, 64)), dim3(1024), 0,
-                           stream(), part, dw, g.OC, g.C, KK, Cp, dwc.splits);
+                           stream(), part, dw, g.OC, g.C, KK, Cp, dwc.splits, dwT ? 1u : 0u);
         ok = check_launch("dw_final");
       }
     }

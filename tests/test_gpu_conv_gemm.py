@@ -47,7 +47,10 @@ CONV_CASES = [
     (2, 3, 35, 35, 64, 11, 4, 2, 1),      # AlexNet c1 geometry (small)
     (2, 64, 13, 13, 192, 5, 1, 2, 1),     # AlexNet c2 geometry
     (1, 32, 16, 16, 24, 1, 1, 0, 0),      # 1x1 (MobileNet project)
-    (2, 24, 15, 15, 144, 1, 1, 0, 0),     # 1x1 expand, OC % 16 == 0
+    (2, 24, 15, 15, 144, 1, 1, 0, 0),     # 1x1 expand, OC % 16 == 0 (dW with taps as rows)
+    (2, 16, 12, 12, 96, 1, 1, 0, 1),      # 1x1 expand x6 (dW with taps as rows)
+    (2, 3, 10, 11, 40, 1, 1, 0, 1),       # 1x1, C = 3 padded to 4 (dW with taps as rows)
+    (2, 3, 64, 64, 16, 3, 1, 1, 1),       # one dW tile: many split-K slices
     (2, 16, 14, 14, 20, 3, 2, 1, 1),      # stride 2, OC not multiple of 16
     (2, 17, 9, 9, 33, 3, 2, 0, 2),        # tanh act: no derivative applied (reference quirk)
     (1, 8, 7, 7, 8, 3, 3, 1, 0),          # stride 3
