@@ -455,12 +455,7 @@ struct TileGrid {
 };
 __device__ __forceinline__ void tile_coords(const TileGrid& tg, uint32_t& mt, uint32_t& nt,
                                             uint32_t& z) {
-  const uint32_t nwg = gridDim.x, L = blockIdx.x;
-  uint32_t id = L;
-  if (tg.xcd) {
-    const uint32_t q = nwg >> 3, r = nwg & 7, x = L & 7;
-    id = x * q + min(x, r) + (L >> 3);
-  }
+  const uint32_t id = tg.xcd ? xcd_block_id() : blockIdx.x;
   mt = id % tg.gm;
   const uint32_t t = id / tg.gm;
   nt = t % tg.gn;
@@ -558,9 +553,15 @@ __global__ void __launch_bounds__(kThreads)
 // masked values of channel c summed over the block's 64 pixels.
 __global__ void __launch_bounds__(256)
     k_to_nhwc(const float* __restrict__ in, const float* __restrict__ y, float* __restrict__ out,
-              float* __restrict__ dbPart, uint32_t C, uint32_t HW, uint32_t Cp, uint32_t npb) {
+              float* __restrict__ dbPart, uint32_t C, uint32_t HW, uint32_t Cp, uint32_t npb,
+              uint32_t ncb, uint32_t nB) {
   __shared__ float t[32][65];
-  const uint32_t c0 = blockIdx.y * 32, p0 = blockIdx.x * 64, b = blockIdx.z;
+  // 1-D grid over (pixel block, channel block, image), pixel block fastest,
+  // in XCD-contiguous order: a plane row's neighbouring blocks share its
+  // partial cache lines.
+  const uint32_t id = xcd_block_id();
+  const uint32_t pb = id % npb, rest = id / npb;
+  const uint32_t c0 = (rest % ncb) * 32, p0 = pb * 64, b = rest / ncb;
   const int tid = threadIdx.x;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -584,7 +585,7 @@ __global__ void __launch_bounds__(256)
     for (int q = 0; q < 8; ++q) s += t[cl][part * 8 + q];
     s = group8_reduce(s);
     if (part == 0 && c0 + cl < C)
-      dbPart[size_t(c0 + cl) * gridDim.z * npb + size_t(b) * npb + blockIdx.x] = s;
+      dbPart[size_t(c0 + cl) * nB * npb + size_t(b) * npb + pb] = s;
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -1042,8 +1043,9 @@ static bool to_nhwc_masked(const float* in, const float* y, float* out, float* d
   }
   const uint32_t npb = cdiv(HW, 64);
   if (npbOut) *npbOut = npb;
-  hipLaunchKernelGGL(k_to_nhwc, dim3(npb, cdiv(Cp, 32), B), dim3(256), 0, stream(), in, y, out,
-                     dbPart, C, HW, Cp, npb);
+  const uint32_t ncb = cdiv(Cp, 32);
+  hipLaunchKernelGGL(k_to_nhwc, dim3(npb * ncb * B), dim3(256), 0, stream(), in, y, out, dbPart,
+                     C, HW, Cp, npb, ncb, B);
   return check_launch("to_nhwc");
 }
 

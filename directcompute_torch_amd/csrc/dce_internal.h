@@ -96,6 +96,19 @@ struct BRes {
 };
 
 // ---------------------------------------------------------------------------
+// Workgroup order.  The dispatcher hands consecutive workgroup ids to the 8
+// XCDs in turn, and each XCD has its own L2.  xcd_block_id() renumbers a 1-D
+// grid so that each XCD runs a contiguous range of logical ids: neighbouring
+// logical blocks that share cache lines (rows of odd length, halos) then hit
+// the same L2 instead of fetching the line once per XCD.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t xcd_block_id() {
+  const uint32_t nwg = gridDim.x, L = blockIdx.x;
+  const uint32_t q = nwg >> 3, r = nwg & 7, x = L & 7;
+  return x * q + min(x, r) + (L >> 3);
+}
+
+// ---------------------------------------------------------------------------
 // Wave-wide reductions over the 64 lanes of a wavefront, without LDS.  Inside
 // each row of 16 lanes, DPP moves combine lanes: quad_perm [1,0,3,2] and
 // [2,3,0,1] (every lane holds its quad's total), row_half_mirror (its 8-lane

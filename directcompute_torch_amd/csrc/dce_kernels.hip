@@ -512,13 +512,14 @@ struct BnPieces {
   uint32_t pieces;
   uint32_t len;  // elements per channel = N*S
 };
-// Pieces per channel: about 8 blocks per CU over all channels, each piece at
-// least 4096 elements long (and at most 128 pieces).
+// Pieces per channel: about four rounds of resident blocks (8 per CU) over
+// all channels, so that the last, partly filled round is a small share of
+// the pass; each piece at least 2048 elements long, at most 512 pieces.
 static BnPieces bn_pieces(uint32_t N, uint32_t C, uint32_t S) {
   BnPieces p;
   p.len = N * S;
-  const uint32_t want = cdiv(uint32_t(num_cus()) * 8, std::max<uint32_t>(1, C));
-  p.pieces = std::max<uint32_t>(1, std::min<uint32_t>({want, cdiv(p.len, 4096), 128u}));
+  const uint32_t want = cdiv(uint32_t(num_cus()) * 32, std::max<uint32_t>(1, C));
+  p.pieces = std::max<uint32_t>(1, std::min<uint32_t>({want, cdiv(p.len, 2048), 512u}));
   return p;
 }
 
@@ -1379,13 +1380,18 @@ __global__ void k_dw_bwd_filter_part(Buf dy, Buf x, DwGeom g, uint32_t pieces, d
     }
   }
 }
-__global__ void k_dw_bwd_filter_final(const double* part, uint32_t pieces, uint32_t C,
-                                      uint32_t taps, Buf df, Buf db) {
-  const uint32_t i = gtid();
-  if (i >= C * (taps + 1)) return;
+// One wave per output (c, t): lane l adds pieces l, l+64, ..., then a DPP
+// wave reduction.  Four outputs per 256 threads.
+__global__ void __launch_bounds__(256)
+    k_dw_bwd_filter_final(const double* part, uint32_t pieces, uint32_t C, uint32_t taps, Buf df,
+                          Buf db) {
+  const uint32_t i = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (i >= C * (taps + 1)) return;  // whole waves leave together
   const uint32_t c = i / (taps + 1), t = i - c * (taps + 1);
-  double s = 0;
-  for (uint32_t p = 0; p < pieces; ++p) s += part[(size_t(c) * pieces + p) * (taps + 1) + t];
+  double a = 0;
+  for (uint32_t p = lane; p < pieces; p += 64) a += part[(size_t(c) * pieces + p) * (taps + 1) + t];
+  const double s = wave_reduce(a);
+  if (lane != 0) return;
   if (t == taps)
     st(db, c, float(s));
   else
@@ -1557,11 +1563,13 @@ __global__ void __launch_bounds__(256)
   bx.init(x, B * C * H * W);
   bg.init(dy, B * C * OH * OW);
   float xv[kDwRegs], gv[kDwRegs / 2];
-  const uint32_t nimg = blockIdx.x < B ? (B - blockIdx.x + gridDim.x - 1) / gridDim.x : 0u;
-  const uint32_t total = nimg * nb;
+  // The channel's B * nb (image, band) units, split evenly over the pieces.
+  const uint32_t units = B * nb;
+  const uint32_t u0 = uint32_t(uint64_t(units) * blockIdx.x / gridDim.x);
+  const uint32_t total = uint32_t(uint64_t(units) * (blockIdx.x + 1) / gridDim.x) - u0;
   auto issue = [&](uint32_t j) {
-    const uint32_t q = fdiv(j, dNb);
-    const uint32_t n = blockIdx.x + q * gridDim.x, o0 = (j - q * nb) * RB;
+    const uint32_t u = u0 + j;
+    const uint32_t n = fdiv(u, dNb), o0 = (u - n * nb) * RB;
     const uint32_t plane = n * C + c;
     dw_win_load(bx, plane * H * W, H, W, DwWin{int(o0 * S) - int(p), -int(p), LXR, LXW}, dLXW, xv);
     dw_win_load(bg, plane * OH * OW, OH, OW, DwWin{int(o0), 0, LGR, LGW}, dLGW, gv);
@@ -1718,8 +1726,9 @@ static bool sh_dw_bwd_filter(const Dispatch& d) {
   const Buf dy = S(d, 0), x = S(d, 1);
   const DwBand bb = dw_band_filter(g);
   if (bb.RB && covers(dy, uint64_t(len) * g.C) && covers(x, uint64_t(g.B) * g.C * g.H * g.W)) {
-    // Image groups per channel: about 8 blocks per CU, each walking at least
-    // one whole plane.
+    // Pieces per channel: about 8 blocks per CU over all channels; each piece
+    // an even share of the channel's (image, band) units, at least about one
+    // image's worth.
     const uint32_t want = std::max<uint32_t>(1, uint32_t(num_cus()) * 8 / std::max<uint32_t>(1, g.C));
     const uint32_t pieces = std::min<uint32_t>(g.B, want);
     double* part = reinterpret_cast<double*>(workspace(size_t(g.C) * pieces * (taps + 1) * 2));
@@ -1737,7 +1746,7 @@ static bool sh_dw_bwd_filter(const Dispatch& d) {
                        bb.LW2, fLX, fLG, fNb, fBW);
     DCE_DWF(3, 1) DCE_DWF(3, 2) DCE_DWF(5, 1) DCE_DWF(5, 2)
 #undef DCE_DWF
-    hipLaunchKernelGGL(k_dw_bwd_filter_final, dim3(cdiv(g.C * (taps + 1), 256)), dim3(256), 0,
+    hipLaunchKernelGGL(k_dw_bwd_filter_final, dim3(cdiv(g.C * (taps + 1), 4)), dim3(256), 0,
                        stream(), part, pieces, g.C, taps, U(d, 0), U(d, 1));
     return check_launch("depthwise_conv_backward_filter");
   }
@@ -1748,7 +1757,7 @@ static bool sh_dw_bwd_filter(const Dispatch& d) {
                  4.0 * double(len) * g.C + 4.0 * double(g.B) * g.C * g.H * g.W);
   hipLaunchKernelGGL(k_dw_bwd_filter_part, dim3(pieces, g.C), dim3(256), 0, stream(), S(d, 0),
                      S(d, 1), g, pieces, part);
-  hipLaunchKernelGGL(k_dw_bwd_filter_final, dim3(cdiv(g.C * (taps + 1), 256)), dim3(256), 0,
+  hipLaunchKernelGGL(k_dw_bwd_filter_final, dim3(cdiv(g.C * (taps + 1), 4)), dim3(256), 0,
                      stream(), part, pieces, g.C, taps, U(d, 0), U(d, 1));
   return check_launch("depthwise_conv_backward_filter");
 }
