@@ -96,6 +96,40 @@ struct BRes {
 };
 
 // ---------------------------------------------------------------------------
+// Streaming accesses: 16-byte loads and stores with the nontemporal cache
+// policy, for passes over more data than the 256 MB MALL (Infinity Cache)
+// holds.  On MI355X they sustain more HBM bandwidth than the default policy
+// (read streams 89% against 79% of 8 TB/s, a read-read-write update 77%
+// against 69%, measured on 1.2 GB buffers).  Below that size the default
+// policy wins: the producer's output is still in the MALL when the next
+// kernel reads it.
+// ---------------------------------------------------------------------------
+constexpr double kStreamBytes = 256.0 * 1024 * 1024;
+inline bool stream_nt(double bytes) { return bytes > kStreamBytes; }
+__device__ __forceinline__ f4 ldnt4(const float* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const f4*>(p));
+}
+__device__ __forceinline__ void stnt4(float* p, f4 v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<f4*>(p));
+}
+// The policy is a template parameter: a run-time choice between two loads of
+// one address lets the compiler merge them and drop the nontemporal hint.
+template <bool NT>
+__device__ __forceinline__ f4 ld4s(const float* p) {
+  if constexpr (NT)
+    return ldnt4(p);
+  else
+    return *reinterpret_cast<const f4*>(p);
+}
+template <bool NT>
+__device__ __forceinline__ void st4s(float* p, f4 v) {
+  if constexpr (NT)
+    stnt4(p, v);
+  else
+    *reinterpret_cast<f4*>(p) = v;
+}
+
+// ---------------------------------------------------------------------------
 // Workgroup order.  The dispatcher hands consecutive workgroup ids to the 8
 // XCDs in turn, and each XCD has its own L2.  xcd_block_id() renumbers a 1-D
 // grid so that each XCD runs a contiguous range of logical ids: neighbouring

@@ -48,19 +48,19 @@ __global__ void k_ew_checked(F f, Buf out, Buf a, Buf b, uint32_t n) {
   if (i < n) st(out, i, f(ld(a, i), ld(b, i)));
 }
 
-template <class F>
+template <class F, bool NT>
 __global__ void k_ew_fast(F f, float* __restrict__ out, const float* __restrict__ a,
                           const float* __restrict__ b, uint32_t n) {
   const uint32_t i4 = gtid() * 4;
   if (i4 + 3 < n) {
-    const f4 va = *reinterpret_cast<const f4*>(a + i4);
-    const f4 vb = b ? *reinterpret_cast<const f4*>(b + i4) : f4{0.f, 0.f, 0.f, 0.f};
+    const f4 va = ld4s<NT>(a + i4);
+    const f4 vb = b ? ld4s<NT>(b + i4) : f4{0.f, 0.f, 0.f, 0.f};
     f4 r;
     r[0] = f(va[0], vb[0]);
     r[1] = f(va[1], vb[1]);
     r[2] = f(va[2], vb[2]);
     r[3] = f(va[3], vb[3]);
-    *reinterpret_cast<f4*>(out + i4) = r;
+    st4s<NT>(out + i4, r);
   } else {
     for (uint32_t i = i4; i < n; ++i) out[i] = f(a[i], b ? b[i] : 0.f);
   }
@@ -71,12 +71,17 @@ __global__ void k_ew_fast(F f, float* __restrict__ out, const float* __restrict_
 template <class F>
 static bool run_ew(const char* what, F f, Buf out, Buf a, Buf b, uint32_t n, bool unary) {
   if (n == 0) return true;
-  ProfScope prof(what, 0, (unary ? 8.0 : 12.0) * double(n));
+  const double bytes = (unary ? 8.0 : 12.0) * double(n);
+  ProfScope prof(what, 0, bytes);
   const bool fast = out.n >= n && a.n >= n && (unary || b.n >= n) && out.p && a.p &&
                     (unary || b.p);
   if (fast) {
-    hipLaunchKernelGGL(k_ew_fast<F>, dim3(cdiv(cdiv(n, 4), 256)), dim3(256), 0, stream(), f,
-                       out.p, a.p, unary ? nullptr : b.p, n);
+    if (stream_nt(bytes))
+      hipLaunchKernelGGL((k_ew_fast<F, true>), dim3(cdiv(cdiv(n, 4), 256)), dim3(256), 0,
+                         stream(), f, out.p, a.p, unary ? nullptr : b.p, n);
+    else
+      hipLaunchKernelGGL((k_ew_fast<F, false>), dim3(cdiv(cdiv(n, 4), 256)), dim3(256), 0,
+                         stream(), f, out.p, a.p, unary ? nullptr : b.p, n);
   } else {
     hipLaunchKernelGGL(k_ew_checked<F>, dim3(cdiv(n, 256)), dim3(256), 0, stream(), f, out, a,
                        b, n);
@@ -565,7 +570,7 @@ __global__ void k_bn_partial(Buf x, Buf dy, Buf mean, Buf var, float eps, uint32
 // piece is a range of quad indices k (plane n = k / (S/4)), read kBnUnroll
 // quads at a time so that each thread keeps several loads in flight.
 constexpr int kBnUnroll = 4;
-template <int MODE>
+template <int MODE, bool NT>
 __global__ void __launch_bounds__(256)
     k_bn_partial4(const float* __restrict__ x, const float* __restrict__ dy,
                   const float* __restrict__ mean, const float* __restrict__ var, float eps,
@@ -580,8 +585,6 @@ __global__ void __launch_bounds__(256)
     mu = mean[c];
     rstd = 1.0f / sqrtf(var[c] + eps);
   }
-  const f4* x4 = reinterpret_cast<const f4*>(x);
-  const f4* g4 = reinterpret_cast<const f4*>(dy);
   double a0 = 0.0, a1 = 0.0;
   for (uint32_t kb = k0 + threadIdx.x; kb < k1; kb += 256 * kBnUnroll) {
     f4 xv[kBnUnroll], gv[kBnUnroll];
@@ -593,8 +596,8 @@ __global__ void __launch_bounds__(256)
       const uint32_t kk = ok[u] ? k : k0;
       const uint32_t n = fdiv(kk, dS4);
       const size_t q = (size_t(n) * C + c) * S4 + (kk - n * S4);
-      xv[u] = x4[q];
-      if (MODE == 1) gv[u] = g4[q];
+      xv[u] = ld4s<NT>(x + q * 4);
+      if (MODE == 1) gv[u] = ld4s<NT>(dy + q * 4);
     }
 #pragma unroll
     for (int u = 0; u < kBnUnroll; ++u) {
@@ -685,12 +688,16 @@ static bool bn_reduce(const char* what, int mode, const Dispatch& d, Buf x, Buf 
       (mode == 0 || (covers(mean, C) && covers(var, C)))) {
     const uint32_t S4 = S / 4, len4 = N * S4;
     const FastDiv dS4 = make_fastdiv(S4);
-    if (mode == 0)
-      hipLaunchKernelGGL(k_bn_partial4<0>, grid, dim3(256), 0, stream(), x.p, nullptr, nullptr,
-                         nullptr, eps, C, S4, len4, pc.pieces, dS4, part);
-    else
-      hipLaunchKernelGGL(k_bn_partial4<1>, grid, dim3(256), 0, stream(), x.p, dy.p, mean.p, var.p,
-                         eps, C, S4, len4, pc.pieces, dS4, part);
+    const bool nt = stream_nt((mode == 0 ? 4.0 : 8.0) * double(total));
+#define DCE_BNP(M, NT)                                                                         \
+  hipLaunchKernelGGL((k_bn_partial4<M, NT>), grid, dim3(256), 0, stream(), x.p,               \
+                     M ? dy.p : nullptr, M ? mean.p : nullptr, M ? var.p : nullptr, eps, C, S4, \
+                     len4, pc.pieces, dS4, part)
+    if (mode == 0 && nt) DCE_BNP(0, true);
+    else if (mode == 0) DCE_BNP(0, false);
+    else if (nt) DCE_BNP(1, true);
+    else DCE_BNP(1, false);
+#undef DCE_BNP
     *partOut = part;
     *pcOut = pc;
     return check_launch(what);
@@ -773,7 +780,7 @@ __global__ void k_bn_elem(Buf x, Buf dy, Buf mean, Buf var, Buf gamma, Buf beta_
 }
 // Quad form (S % 4 == 0, every buffer covering its size): the four elements
 // of a quad share a channel, whose parameters are computed once.
-template <int MODE>
+template <int MODE, bool NT>
 __global__ void __launch_bounds__(256)
     k_bn_elem4(const float* __restrict__ x, const float* __restrict__ dy,
                const float* __restrict__ mean, const float* __restrict__ var,
@@ -786,7 +793,7 @@ __global__ void __launch_bounds__(256)
   const uint32_t c = q - fdiv(q, dC) * C;
   const float mu = mean[c];
   const float rstd = 1.0f / sqrtf(var[c] + eps);
-  const f4 xv = reinterpret_cast<const f4*>(x)[i];
+  const f4 xv = ld4s<NT>(x + size_t(i) * 4);
   f4 r;
   if (MODE == 0) {
     const float g = gamma[c], b = beta_or_dg[c];
@@ -794,14 +801,14 @@ __global__ void __launch_bounds__(256)
     for (int e = 0; e < 4; ++e) r[e] = (xv[e] - mu) * rstd * g + b;
   } else {
     const float g = gamma[c], dg = beta_or_dg[c], db = dbeta[c];
-    const f4 gv = reinterpret_cast<const f4*>(dy)[i];
+    const f4 gv = ld4s<NT>(dy + size_t(i) * 4);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float xh = (xv[e] - mu) * rstd;
       r[e] = (g * rstd) * (gv[e] - (db + xh * dg) / m);
     }
   }
-  reinterpret_cast<f4*>(out)[i] = r;
+  st4s<NT>(out + size_t(i) * 4, r);
 }
 
 template <int MODE>
@@ -829,9 +836,14 @@ static bool bn_elem(const char* what, const Dispatch& d) {
       covers(mean, C) && covers(var, C) && covers(gamma, C) && covers(b2, C) &&
       (MODE == 0 || covers(db, C))) {
     const uint32_t total4 = uint32_t(total / 4);
-    hipLaunchKernelGGL(k_bn_elem4<MODE>, dim3(cdiv(total4, 256)), dim3(256), 0, stream(), x.p,
-                       dy.p, mean.p, var.p, gamma.p, b2.p, db.p, out.p, eps, C, total4,
-                       make_fastdiv(Sz / 4), make_fastdiv(C), float(uint64_t(N) * Sz));
+    if (stream_nt((MODE == 1 ? 12.0 : 8.0) * double(total)))
+      hipLaunchKernelGGL((k_bn_elem4<MODE, true>), dim3(cdiv(total4, 256)), dim3(256), 0,
+                         stream(), x.p, dy.p, mean.p, var.p, gamma.p, b2.p, db.p, out.p, eps, C,
+                         total4, make_fastdiv(Sz / 4), make_fastdiv(C), float(uint64_t(N) * Sz));
+    else
+      hipLaunchKernelGGL((k_bn_elem4<MODE, false>), dim3(cdiv(total4, 256)), dim3(256), 0,
+                         stream(), x.p, dy.p, mean.p, var.p, gamma.p, b2.p, db.p, out.p, eps, C,
+                         total4, make_fastdiv(Sz / 4), make_fastdiv(C), float(uint64_t(N) * Sz));
     return check_launch(what);
   }
   dim3 grid(cdiv(total, 256));
@@ -1144,12 +1156,13 @@ __global__ void k_gap_bwd(Buf g, Buf dx, uint32_t total, uint32_t S) {
   if (i < total) st(dx, i, ld(g, i / S) / float(S));
 }
 // Quad form (S % 4 == 0, buffers covering the shapes): one g value per quad.
+template <bool NT>
 __global__ void k_gap_bwd4(const float* __restrict__ g, float* __restrict__ dx, uint32_t total4,
                            FastDiv dS4, float S) {
   const uint32_t i = blockIdx.x * 256 + threadIdx.x;
   if (i >= total4) return;
   const float v = g[fdiv(i, dS4)] / S;
-  reinterpret_cast<f4*>(dx)[i] = f4{v, v, v, v};
+  st4s<NT>(dx + size_t(i) * 4, f4{v, v, v, v});
 }
 static bool sh_gap_bwd(const Dispatch& d) {
   uint32_t Sz = CU(d, 2);
@@ -1160,8 +1173,12 @@ static bool sh_gap_bwd(const Dispatch& d) {
   if (Sz % 4 == 0 && total < (1ull << 31) && covers(g, total / Sz) && covers(dx, total) &&
       (reinterpret_cast<uintptr_t>(dx.p) & 15) == 0) {
     const uint32_t total4 = uint32_t(total / 4);
-    hipLaunchKernelGGL(k_gap_bwd4, dim3(cdiv(total4, 256)), dim3(256), 0, stream(), g.p, dx.p,
-                       total4, make_fastdiv(Sz / 4), float(Sz));
+    if (stream_nt(4.0 * double(total)))
+      hipLaunchKernelGGL(k_gap_bwd4<true>, dim3(cdiv(total4, 256)), dim3(256), 0, stream(), g.p,
+                         dx.p, total4, make_fastdiv(Sz / 4), float(Sz));
+    else
+      hipLaunchKernelGGL(k_gap_bwd4<false>, dim3(cdiv(total4, 256)), dim3(256), 0, stream(), g.p,
+                         dx.p, total4, make_fastdiv(Sz / 4), float(Sz));
     return check_launch("global_avg_pool_backward");
   }
   hipLaunchKernelGGL(k_gap_bwd, dim3(cdiv(total, 256)), dim3(256), 0, stream(), S(d, 0), U(d, 0),
@@ -1203,14 +1220,14 @@ static bool sh_upsample(const Dispatch& d) {
 // Nearest x2 with even W and exact output size: a thread sums two 2 x 2
 // blocks (two quads of dy rows 2h and 2h+1) into a pair of dx values, in the
 // reference's (a, then b) order.
+template <bool NT>
 __global__ void k_upsample2_bwd(const float* __restrict__ dy, float* __restrict__ dx,
                                 uint32_t pairs, uint32_t W2, FastDiv dW2) {
   const uint32_t i = blockIdx.x * 256 + threadIdx.x;
   if (i >= pairs) return;
   const uint32_t row = fdiv(i, dW2), j = i - row * W2;  // row = bc*H + h
-  const f4* r0 = reinterpret_cast<const f4*>(dy + size_t(2 * row) * 4 * W2);
-  const f4* r1 = reinterpret_cast<const f4*>(dy + size_t(2 * row + 1) * 4 * W2);
-  const f4 a = r0[j], b = r1[j];
+  const f4 a = ld4s<NT>(dy + (size_t(2 * row) * W2 + j) * 4);
+  const f4 b = ld4s<NT>(dy + (size_t(2 * row + 1) * W2 + j) * 4);
   typedef float f2 __attribute__((ext_vector_type(2)));
   reinterpret_cast<f2*>(dx)[i] = f2{((a[0] + a[1]) + b[0]) + b[1], ((a[2] + a[3]) + b[2]) + b[3]};
 }
@@ -1225,8 +1242,12 @@ static bool sh_upsample_bwd(const Dispatch& d) {
       covers(dyb, 4 * total) && covers(dxb, total) &&
       ((reinterpret_cast<uintptr_t>(dyb.p) | reinterpret_cast<uintptr_t>(dxb.p)) & 15) == 0) {
     const uint32_t pairs = uint32_t(total / 2), W2 = W / 2;
-    hipLaunchKernelGGL(k_upsample2_bwd, dim3(cdiv(pairs, 256)), dim3(256), 0, stream(), dyb.p,
-                       dxb.p, pairs, W2, make_fastdiv(W2));
+    if (stream_nt(20.0 * double(total)))
+      hipLaunchKernelGGL(k_upsample2_bwd<true>, dim3(cdiv(pairs, 256)), dim3(256), 0, stream(),
+                         dyb.p, dxb.p, pairs, W2, make_fastdiv(W2));
+    else
+      hipLaunchKernelGGL(k_upsample2_bwd<false>, dim3(cdiv(pairs, 256)), dim3(256), 0, stream(),
+                         dyb.p, dxb.p, pairs, W2, make_fastdiv(W2));
     return check_launch("upsample_backward");
   }
   hipLaunchKernelGGL(k_upsample_bwd, dim3(cdiv(total, 256)), dim3(256), 0, stream(), S(d, 0),
@@ -1248,7 +1269,7 @@ __global__ void k_chan_copy(Buf src, Buf dst, uint32_t total, uint32_t cin, uint
     st(dst, i, ld(src, o));
 }
 // Quad form (S % 4 == 0, buffers covering the shapes, 16-byte aligned).
-template <int MODE>
+template <int MODE, bool NT>
 __global__ void k_chan_copy4(const float* __restrict__ src, float* __restrict__ dst,
                              uint32_t total4, uint32_t cin, uint32_t S4, uint32_t cout,
                              uint32_t coff, FastDiv dS4, FastDiv dCin) {
@@ -1258,9 +1279,9 @@ __global__ void k_chan_copy4(const float* __restrict__ src, float* __restrict__ 
   const uint32_t b = fdiv(t, dCin), c = t - b * cin;
   const uint32_t o = (b * cout + c + coff) * S4 + s4;
   if (MODE == 0)
-    reinterpret_cast<f4*>(dst)[o] = reinterpret_cast<const f4*>(src)[i];
+    st4s<NT>(dst + size_t(o) * 4, ld4s<NT>(src + size_t(i) * 4));
   else
-    reinterpret_cast<f4*>(dst)[i] = reinterpret_cast<const f4*>(src)[o];
+    st4s<NT>(dst + size_t(i) * 4, ld4s<NT>(src + size_t(o) * 4));
 }
 template <int MODE>
 static bool sh_chan_copy(const Dispatch& d) {
@@ -1275,9 +1296,14 @@ static bool sh_chan_copy(const Dispatch& d) {
         covers(MODE == 0 ? src : dst, total) && covers(MODE == 0 ? dst : src, big) &&
         ((reinterpret_cast<uintptr_t>(src.p) | reinterpret_cast<uintptr_t>(dst.p)) & 15) == 0) {
       const uint32_t total4 = uint32_t(total / 4);
-      hipLaunchKernelGGL(k_chan_copy4<MODE>, dim3(cdiv(total4, 256)), dim3(256), 0, stream(),
-                         src.p, dst.p, total4, cin, Sz / 4, cout, coff, make_fastdiv(Sz / 4),
-                         make_fastdiv(cin));
+      if (stream_nt(8.0 * double(total)))
+        hipLaunchKernelGGL((k_chan_copy4<MODE, true>), dim3(cdiv(total4, 256)), dim3(256), 0,
+                           stream(), src.p, dst.p, total4, cin, Sz / 4, cout, coff,
+                           make_fastdiv(Sz / 4), make_fastdiv(cin));
+      else
+        hipLaunchKernelGGL((k_chan_copy4<MODE, false>), dim3(cdiv(total4, 256)), dim3(256), 0,
+                           stream(), src.p, dst.p, total4, cin, Sz / 4, cout, coff,
+                           make_fastdiv(Sz / 4), make_fastdiv(cin));
       return check_launch(MODE == 0 ? "concat_insert" : "slice");
     }
   }

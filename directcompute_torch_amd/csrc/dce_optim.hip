@@ -71,7 +71,8 @@ struct AdamOp {  // nn_adam.hlsl:20-33
 };
 
 // WRITE: bit0 w, bit1 g, bit2 m, bit3 v.  READ likewise.
-template <class Op, int READ, int WRITE>
+// NT: streaming (nontemporal) accesses, for a pass larger than the MALL.
+template <class Op, int READ, int WRITE, bool NT>
 __device__ __forceinline__ void apply_chunk(const Table& t, const Op& op, int ti, uint32_t c0) {
   const uint32_t n = t.n[ti];
   float* w = t.w[ti];
@@ -88,10 +89,10 @@ __device__ __forceinline__ void apply_chunk(const Table& t, const Op& op, int ti
     for (int j = 0; j < 4; ++j) {
       const uint32_t i = c0 + (j * 256 + threadIdx.x) * 4;
       W[j] = G[j] = M[j] = V[j] = f4{0.f, 0.f, 0.f, 0.f};
-      if (READ & 1) W[j] = *reinterpret_cast<const f4*>(w + i);
-      if (READ & 2) G[j] = *reinterpret_cast<const f4*>(g + i);
-      if (READ & 4) M[j] = *reinterpret_cast<const f4*>(m + i);
-      if (READ & 8) V[j] = *reinterpret_cast<const f4*>(v + i);
+      if (READ & 1) W[j] = ld4s<NT>(w + i);
+      if (READ & 2) G[j] = ld4s<NT>(g + i);
+      if (READ & 4) M[j] = ld4s<NT>(m + i);
+      if (READ & 8) V[j] = ld4s<NT>(v + i);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -108,10 +109,10 @@ __device__ __forceinline__ void apply_chunk(const Table& t, const Op& op, int ti
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t i = c0 + (j * 256 + threadIdx.x) * 4;
-      if (WRITE & 1) *reinterpret_cast<f4*>(w + i) = W[j];
-      if (WRITE & 2) *reinterpret_cast<f4*>(g + i) = G[j];
-      if (WRITE & 4) *reinterpret_cast<f4*>(m + i) = M[j];
-      if (WRITE & 8) *reinterpret_cast<f4*>(v + i) = V[j];
+      if (WRITE & 1) st4s<NT>(w + i, W[j]);
+      if (WRITE & 2) st4s<NT>(g + i, G[j]);
+      if (WRITE & 4) st4s<NT>(m + i, M[j]);
+      if (WRITE & 8) st4s<NT>(v + i, V[j]);
     }
     return;
   }
@@ -148,20 +149,20 @@ __device__ __forceinline__ void apply_chunk(const Table& t, const Op& op, int ti
   }
 }
 
-template <class Op, int READ, int WRITE>
+template <class Op, int READ, int WRITE, bool NT>
 __global__ void __launch_bounds__(256) k_multi(const Table t, const Op op) {
   const int ti = find_tensor(t, blockIdx.x);
-  apply_chunk<Op, READ, WRITE>(t, op, ti, (blockIdx.x - t.start[ti]) * kChunk);
+  apply_chunk<Op, READ, WRITE, NT>(t, op, ti, (blockIdx.x - t.start[ti]) * kChunk);
 }
 
 // Scale read from device memory (norm clip): skipped entirely when 1.
-template <class Op, int READ, int WRITE>
+template <class Op, int READ, int WRITE, bool NT>
 __global__ void __launch_bounds__(256) k_multi_devscale(const Table t, Op op, const float* ns) {
   const float scale = ns[1];
   if (Op::kSkipUnit && scale == 1.0f) return;
   op.scale = scale;
   const int ti = find_tensor(t, blockIdx.x);
-  apply_chunk<Op, READ, WRITE>(t, op, ti, (blockIdx.x - t.start[ti]) * kChunk);
+  apply_chunk<Op, READ, WRITE, NT>(t, op, ti, (blockIdx.x - t.start[ti]) * kChunk);
 }
 struct SgdScaledDev : SgdScaledOp {
   static constexpr bool kSkipUnit = false;
@@ -171,6 +172,7 @@ struct ScaleDev : ScaleOp {
 };
 
 // Σ g² per block (double), written at part[base + block].
+template <bool NT>
 __global__ void __launch_bounds__(256) k_multi_sumsq(const Table t, double* part, uint32_t base) {
   __shared__ double sh[4];
   const int ti = find_tensor(t, blockIdx.x);
@@ -182,7 +184,7 @@ __global__ void __launch_bounds__(256) k_multi_sumsq(const Table t, double* part
   if (c0 + kChunk <= n && (reinterpret_cast<uintptr_t>(g) & 15) == 0) {
     f4 G[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) G[j] = *reinterpret_cast<const f4*>(g + c0 + (j * 256 + threadIdx.x) * 4);
+    for (int j = 0; j < 4; ++j) G[j] = ld4s<NT>(g + c0 + (j * 256 + threadIdx.x) * 4);
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc += G[j][0] * G[j][0] + G[j][1] * G[j][1] + G[j][2] * G[j][2] + G[j][3] * G[j][3];
   } else {
@@ -283,14 +285,22 @@ static double table_elems(const std::vector<Table>& tabs) {
   return e;
 }
 
+
+
 bool sgd_multi(void** params, void** grads, const uint32_t* sizes, uint32_t n, float lr,
                float clip) {
   std::vector<Table> tabs;
   if (!build_tables(params, grads, nullptr, nullptr, sizes, n, true, tabs, nullptr)) return false;
-  ProfScope prof("sgd", 0, 12.0 * table_elems(tabs));
+  const double bytes = 12.0 * table_elems(tabs);
+  const bool nt = stream_nt(bytes);
+  ProfScope prof("sgd", 0, bytes);
   for (const Table& t : tabs) {
-    hipLaunchKernelGGL((k_multi<SgdOp, 3, 1>), dim3(table_blocks(t)), dim3(256), 0, stream(), t,
-                       SgdOp{lr, clip});
+    if (nt)
+      hipLaunchKernelGGL((k_multi<SgdOp, 3, 1, true>), dim3(table_blocks(t)), dim3(256), 0,
+                         stream(), t, SgdOp{lr, clip});
+    else
+      hipLaunchKernelGGL((k_multi<SgdOp, 3, 1, false>), dim3(table_blocks(t)), dim3(256), 0,
+                         stream(), t, SgdOp{lr, clip});
     if (!check_launch("SGDBatch")) return false;
   }
   return true;
@@ -303,10 +313,17 @@ bool grad_norm_multi(void** grads, const uint32_t* sizes, uint32_t n, float max_
   if (!build_tables(nullptr, grads, nullptr, nullptr, sizes, n, false, tabs, &total)) return false;
   double* part = reinterpret_cast<double*>(workspace(size_t(std::max<uint32_t>(total, 1)) * 2));
   if (!part) return false;
-  ProfScope prof("grad_norm", 0, 4.0 * table_elems(tabs));
+  const double bytes = 4.0 * table_elems(tabs);
+  const bool nt = stream_nt(bytes);
+  ProfScope prof("grad_norm", 0, bytes);
   uint32_t base = 0;
   for (const Table& t : tabs) {
-    hipLaunchKernelGGL(k_multi_sumsq, dim3(table_blocks(t)), dim3(256), 0, stream(), t, part, base);
+    if (nt)
+      hipLaunchKernelGGL(k_multi_sumsq<true>, dim3(table_blocks(t)), dim3(256), 0, stream(), t,
+                         part, base);
+    else
+      hipLaunchKernelGGL(k_multi_sumsq<false>, dim3(table_blocks(t)), dim3(256), 0, stream(), t,
+                         part, base);
     base += table_blocks(t);
   }
   hipLaunchKernelGGL(k_norm_final, dim3(1), dim3(1024), 0, stream(), part, total, max_norm, d_ns);
@@ -320,10 +337,16 @@ bool sgd_scaled_multi(void** params, void** grads, const uint32_t* sizes, uint32
   SgdScaledDev op;
   op.lr = lr;
   op.scale = 1.f;
-  ProfScope prof("sgd_clipped", 0, 12.0 * table_elems(tabs));
+  const double bytes = 12.0 * table_elems(tabs);
+  const bool nt = stream_nt(bytes);
+  ProfScope prof("sgd_clipped", 0, bytes);
   for (const Table& t : tabs) {
-    hipLaunchKernelGGL((k_multi_devscale<SgdScaledDev, 3, 1>), dim3(table_blocks(t)), dim3(256), 0,
-                       stream(), t, op, d_ns);
+    if (nt)
+      hipLaunchKernelGGL((k_multi_devscale<SgdScaledDev, 3, 1, true>), dim3(table_blocks(t)),
+                         dim3(256), 0, stream(), t, op, d_ns);
+    else
+      hipLaunchKernelGGL((k_multi_devscale<SgdScaledDev, 3, 1, false>), dim3(table_blocks(t)),
+                         dim3(256), 0, stream(), t, op, d_ns);
     if (!check_launch("SGDBatchClipped")) return false;
   }
   return true;
@@ -334,10 +357,16 @@ bool scale_grads_multi(void** grads, const uint32_t* sizes, uint32_t n, const fl
   if (!build_tables(nullptr, grads, nullptr, nullptr, sizes, n, false, tabs, nullptr)) return false;
   ScaleDev op;
   op.scale = 1.f;
-  ProfScope prof("clip_scale", 0, 8.0 * table_elems(tabs));
+  const double bytes = 8.0 * table_elems(tabs);
+  const bool nt = stream_nt(bytes);
+  ProfScope prof("clip_scale", 0, bytes);
   for (const Table& t : tabs) {
-    hipLaunchKernelGGL((k_multi_devscale<ScaleDev, 2, 2>), dim3(table_blocks(t)), dim3(256), 0,
-                       stream(), t, op, d_ns);
+    if (nt)
+      hipLaunchKernelGGL((k_multi_devscale<ScaleDev, 2, 2, true>), dim3(table_blocks(t)),
+                         dim3(256), 0, stream(), t, op, d_ns);
+    else
+      hipLaunchKernelGGL((k_multi_devscale<ScaleDev, 2, 2, false>), dim3(table_blocks(t)),
+                         dim3(256), 0, stream(), t, op, d_ns);
     if (!check_launch("ClipGradNorm")) return false;
   }
   return true;
@@ -348,10 +377,16 @@ bool adam_multi(void** params, void** grads, void** m, void** v, const uint32_t*
   std::vector<Table> tabs;
   uint32_t total = 0;
   if (!build_tables(params, grads, m, v, sizes, n, true, tabs, &total)) return false;
-  ProfScope prof("adam", 0, 28.0 * table_elems(tabs));
+  const double bytes = 28.0 * table_elems(tabs);
+  const bool nt = stream_nt(bytes);
+  ProfScope prof("adam", 0, bytes);
   for (const Table& t : tabs) {
-    hipLaunchKernelGGL((k_multi<AdamOp, 15, 13>), dim3(table_blocks(t)), dim3(256), 0, stream(), t,
-                       AdamOp{step, b1, b2, eps, wd, clip});
+    if (nt)
+      hipLaunchKernelGGL((k_multi<AdamOp, 15, 13, true>), dim3(table_blocks(t)), dim3(256), 0,
+                         stream(), t, AdamOp{step, b1, b2, eps, wd, clip});
+    else
+      hipLaunchKernelGGL((k_multi<AdamOp, 15, 13, false>), dim3(table_blocks(t)), dim3(256), 0,
+                         stream(), t, AdamOp{step, b1, b2, eps, wd, clip});
     if (!check_launch("AdamBatch")) return false;
   }
   return true;
