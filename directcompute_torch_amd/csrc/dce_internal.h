@@ -79,6 +79,7 @@ __device__ __forceinline__ uint32_t fdiv(uint32_t n, FastDiv f) {
 // num_records.
 // ---------------------------------------------------------------------------
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f2 __attribute__((ext_vector_type(2)));
 constexpr uint32_t kOob = 0x20000000u;
 struct BRes {
   __amdgpu_buffer_rsrc_t r;

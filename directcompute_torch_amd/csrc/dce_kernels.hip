@@ -1042,18 +1042,28 @@ __global__ void k_maxpool_bwd_blk(const float* __restrict__ dz, const uint32_t* 
 #pragma unroll
   for (int r = 0; r < S; ++r) {
     const uint32_t ih = a * S + r;
+    if (ih >= H) continue;
+    float o[S];
 #pragma unroll
     for (int c = 0; c < S; ++c) {
-      const uint32_t iw = b * S + c;
-      if (ih >= H || iw >= W) continue;
-      const uint32_t i = (plane * H + ih) * W + iw;
+      const uint32_t i = (plane * H + ih) * W + b * S + c;
       float acc = 0.f;
 #pragma unroll
       for (int wa = 0; wa < NW; ++wa)
 #pragma unroll
         for (int wb = 0; wb < NW; ++wb)
           if (id[wa][wb] == i) acc += v[wa][wb];
-      dx[i] = acc;
+      o[c] = acc;
+    }
+    // Rows of even length: the S = 2 pair is aligned and inside the row, and
+    // goes out as one 8-byte store (one contiguous run per wave).
+    float* row = dx + (plane * H + ih) * W + b * S;
+    if (S == 2 && (W & 1) == 0) {
+      *reinterpret_cast<f2*>(row) = f2{o[0], o[S - 1]};
+    } else {
+#pragma unroll
+      for (int c = 0; c < S; ++c)
+        if (b * S + c < W) row[c] = o[c];
     }
   }
 }
@@ -1228,7 +1238,6 @@ __global__ void k_upsample2_bwd(const float* __restrict__ dy, float* __restrict_
   const uint32_t row = fdiv(i, dW2), j = i - row * W2;  // row = bc*H + h
   const f4 a = ld4s<NT>(dy + (size_t(2 * row) * W2 + j) * 4);
   const f4 b = ld4s<NT>(dy + (size_t(2 * row + 1) * W2 + j) * 4);
-  typedef float f2 __attribute__((ext_vector_type(2)));
   reinterpret_cast<f2*>(dx)[i] = f2{((a[0] + a[1]) + b[0]) + b[1], ((a[2] + a[3]) + b[2]) + b[3]};
 }
 static bool sh_upsample_bwd(const Dispatch& d) {
@@ -1530,6 +1539,7 @@ __global__ void __launch_bounds__(256)
     for (int t = 0; t < K * K; ++t) w[t] = f[c * K * K + t];
     const uint32_t r1 = min(r0 + RB, H);
     float* dxp = dx + size_t(plane) * H * W;
+    const bool evenW = (W & 1) == 0;
     const uint32_t items = ((r1 - r0 + 1) / 2) * BW;
     for (uint32_t e = threadIdx.x; e < items; e += 256) {
       const uint32_t a = fdiv(e, dBW), b2 = e - a * BW;
@@ -1542,9 +1552,9 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
         const uint32_t ih = r0 + 2 * a + r;
+        float o[2];
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
-          const uint32_t iw = 2 * b2 + cc;
           float acc = 0.f;
 #pragma unroll
           for (int fh = 0; fh < K; ++fh) {
@@ -1558,7 +1568,19 @@ __global__ void __launch_bounds__(256)
               }
             }
           }
-          if (ih < r1 && iw < W) dxp[size_t(ih) * W + iw] = acc;
+          o[cc] = acc;
+        }
+        // The pair goes out as one 8-byte store when rows have even length
+        // (the pair is then aligned and inside the row): a wave writes one
+        // contiguous run instead of two interleaved half-density ones.
+        if (ih < r1) {
+          float* row = dxp + size_t(ih) * W + 2 * b2;
+          if (evenW) {
+            *reinterpret_cast<f2*>(row) = f2{o[0], o[1]};
+          } else {
+            row[0] = o[0];
+            if (2 * b2 + 1 < W) row[1] = o[1];
+          }
         }
       }
     }
