@@ -17,6 +17,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -96,6 +97,20 @@ bool check_launch(const char* what) {
     return false;
   }
   return true;
+}
+
+int blocks_per_cu_raw(const void* kernel, int threads) {
+  static std::map<std::pair<const void*, int>, int> cache;
+  const auto key = std::make_pair(kernel, threads);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0) != hipSuccess || n < 1) {
+    hipGetLastError();
+    n = 1;
+  }
+  cache[key] = n;
+  return n;
 }
 
 FastDiv make_fastdiv(uint32_t d) {

@@ -143,6 +143,15 @@ __device__ __forceinline__ uint32_t xcd_block_id() {
   return x * q + min(x, r) + (L >> 3);
 }
 
+// Workgroups of `threads` threads of one kernel that a CU holds at once (from
+// the runtime, cached per kernel address: kernels of one signature share the
+// template instance).
+int blocks_per_cu_raw(const void* kernel, int threads);
+template <class Kern>
+int blocks_per_cu(Kern kernel, int threads) {
+  return blocks_per_cu_raw(reinterpret_cast<const void*>(kernel), threads);
+}
+
 // ---------------------------------------------------------------------------
 // Wave-wide reductions over the 64 lanes of a wavefront, without LDS.  Inside
 // each row of 16 lanes, DPP moves combine lanes: quad_perm [1,0,3,2] and

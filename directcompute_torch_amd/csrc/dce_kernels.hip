@@ -1744,15 +1744,19 @@ static bool sh_dw_bwd_input(const Dispatch& d) {
   if (bb.RB && covers(dy, uint64_t(g.B) * g.C * g.OH * g.OW) &&
       covers(f, uint64_t(g.C) * g.kH * g.kW) && covers(dx, total)) {
     const uint32_t nb = cdiv(g.H, bb.RB), nbands = g.B * g.C * nb;
-    const uint32_t blocks = std::min<uint32_t>(nbands, uint32_t(num_cus()) * 8);
     const uint32_t BW = (g.W + 1) / 2, ndy = g.B * g.C * g.OH * g.OW;
     const FastDiv fLW = make_fastdiv(bb.LW), fNb = make_fastdiv(nb), fBW = make_fastdiv(BW);
     const uint32_t podd = g.p & 1;
+    // One resident round of blocks (the runtime's occupancy), each walking
+    // bands with a grid stride: no partly filled second round.
 #define DCE_DWI(K, SS, PO)                                                                        \
-  if (g.kH == K && g.s == SS && (SS == 1 || podd == PO))                                         \
+  if (g.kH == K && g.s == SS && (SS == 1 || podd == PO)) {                                       \
+    const uint32_t blocks = std::min<uint32_t>(                                                  \
+        nbands, uint32_t(num_cus()) * blocks_per_cu(k_dw_bwd_input_band<K, SS, PO>, 256));      \
     hipLaunchKernelGGL((k_dw_bwd_input_band<K, SS, PO>), dim3(blocks), dim3(256), 0, stream(),     \
                        dy.p, f.p, dx.p, g.C, g.H, g.W, g.OH, g.OW, g.p, bb.RB, nb, nbands, bb.R,   \
-                       bb.LW, BW, ndy, fLW, fNb, fBW);
+                       bb.LW, BW, ndy, fLW, fNb, fBW);                                             \
+  }
     DCE_DWI(3, 1, 0) DCE_DWI(3, 2, 0) DCE_DWI(3, 2, 1)
     DCE_DWI(5, 1, 0) DCE_DWI(5, 2, 0) DCE_DWI(5, 2, 1)
 #undef DCE_DWI
@@ -1774,10 +1778,17 @@ static bool sh_dw_bwd_filter(const Dispatch& d) {
   const Buf dy = S(d, 0), x = S(d, 1);
   const DwBand bb = dw_band_filter(g);
   if (bb.RB && covers(dy, uint64_t(len) * g.C) && covers(x, uint64_t(g.B) * g.C * g.H * g.W)) {
-    // Pieces per channel: about 8 blocks per CU over all channels; each piece
-    // an even share of the channel's (image, band) units, at least about one
-    // image's worth.
-    const uint32_t want = std::max<uint32_t>(1, uint32_t(num_cus()) * 8 / std::max<uint32_t>(1, g.C));
+    // Pieces per channel: one resident round of blocks over all channels (the
+    // runtime's occupancy; a partly filled second round would run at a
+    // fraction of the machine), each piece an even share of the channel's
+    // (image, band) units, at least about one image's worth.
+    int occ = 1;
+#define DCE_DWO(K, SS) \
+  if (g.kH == K && g.s == SS) occ = blocks_per_cu(k_dw_bwd_filter_band<K, SS>, 256);
+    DCE_DWO(3, 1) DCE_DWO(3, 2) DCE_DWO(5, 1) DCE_DWO(5, 2)
+#undef DCE_DWO
+    const uint32_t want =
+        std::max<uint32_t>(1, uint32_t(num_cus()) * uint32_t(occ) / std::max<uint32_t>(1, g.C));
     const uint32_t pieces = std::min<uint32_t>(g.B, want);
     double* part = reinterpret_cast<double*>(workspace(size_t(g.C) * pieces * (taps + 1) * 2));
     if (!part) return false;
