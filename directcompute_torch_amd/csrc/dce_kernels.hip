@@ -1469,6 +1469,53 @@ __device__ __forceinline__ void dw_win_store(float* lds, const float (&v)[N], ui
   for (int u = 0; u < N; ++u)
     if (u * 256 + threadIdx.x < n) lds[u * 256 + threadIdx.x] = v[u];
 }
+// Quad form, for planes whose width is a multiple of 4: the stored window
+// starts lo = cb & 3 columns left of the logical one, at a 4-aligned plane
+// column, and its width w.LW (the stored width) is a multiple of 4.  Each
+// quad then lies wholly inside or wholly outside the plane and is one 16-byte
+// buffer load (a quarter of the loads and index divisions of the dword form).
+template <int N>
+__device__ __forceinline__ void dw_win_load4(const BRes& b, uint32_t base, uint32_t rows,
+                                             uint32_t cols, const DwWin& w, FastDiv dQW,
+                                             f4 (&v)[N]) {
+  const int cs = w.cb - (w.cb & 3);
+  const uint32_t qw = w.LW / 4;
+#pragma unroll
+  for (int u = 0; u < N; ++u) {
+    const uint32_t q = u * 256 + threadIdx.x;
+    const uint32_t i = fdiv(q, dQW), jq = q - i * qw;
+    const int r = w.rb + int(i), c = cs + 4 * int(jq);
+    const bool ok = q < w.R * qw && r >= 0 && r < int(rows) && c >= 0 && c < int(cols);
+    v[u] = b.ld4(ok ? base + uint32_t(r) * cols + uint32_t(c) : kOob);
+  }
+}
+template <int N>
+__device__ __forceinline__ void dw_win_store4(float* lds, const f4 (&v)[N], uint32_t nq) {
+#pragma unroll
+  for (int u = 0; u < N; ++u)
+    if (u * 256 + threadIdx.x < nq) *reinterpret_cast<f4*>(lds + 4 * (u * 256 + threadIdx.x)) = v[u];
+}
+// A band window in dword or quad form (V4), with the quad form's column shift.
+template <bool V4, int N>
+struct DwRegs {
+  float v[V4 ? 1 : N];
+  f4 q[V4 ? N / 4 : 1];
+  __device__ __forceinline__ void load(const BRes& b, uint32_t base, uint32_t rows, uint32_t cols,
+                                       const DwWin& w, FastDiv d) {
+    if constexpr (V4)
+      dw_win_load4(b, base, rows, cols, w, d, q);
+    else
+      dw_win_load(b, base, rows, cols, w, d, v);
+  }
+  __device__ __forceinline__ void store(float* lds, uint32_t R, uint32_t LW) const {
+    if constexpr (V4)
+      dw_win_store4(lds, q, R * LW / 4);
+    else
+      dw_win_store(lds, v, R * LW);
+  }
+  // Stored column of logical window column 0.
+  __device__ static __forceinline__ int shift(int cb) { return V4 ? (cb & 3) : 0; }
+};
 
 // Sub-pixel geometry of the stride-2 input gradient: with p = 2*ph + PODD,
 // output row 2A + r takes tap fh exactly when r + PODD - fh is even, from dy
@@ -1486,7 +1533,7 @@ struct DwS2 {
 //   S = 2: LDS cell (i, j) = dy[r0/2 + ph + JMIN + i][ph + JMIN + j]; output
 //          block (2a, 2b) reads the WR x WR window at (a, b).
 // Taps are summed in (fh, fw) order for every output, as the generic kernel.
-template <int K, int S, int PODD>
+template <int K, int S, int PODD, bool V4>
 __global__ void __launch_bounds__(256)
     k_dw_bwd_input_band(const float* __restrict__ dy, const float* __restrict__ f,
                         float* __restrict__ dx, uint32_t C, uint32_t H, uint32_t W, uint32_t OH,
@@ -1494,10 +1541,10 @@ __global__ void __launch_bounds__(256)
                         uint32_t LR, uint32_t LW, uint32_t BW, uint32_t ndy, FastDiv dLW,
                         FastDiv dNb, FastDiv dBW) {
   constexpr int WR = S == 1 ? K + 1 : DwS2<K, PODD>::WR;
-  __shared__ float sd[kDwBand];
+  __shared__ __attribute__((aligned(16))) float sd[kDwBand];
   BRes bd;
   bd.init(dy, ndy);
-  float v[kDwRegs];
+  DwRegs<V4, kDwRegs> v;
   const uint32_t ph = p / 2;
   auto decode = [&](uint32_t band, uint32_t& plane, uint32_t& r0) {
     plane = fdiv(band, dNb);
@@ -1516,23 +1563,24 @@ __global__ void __launch_bounds__(256)
     }
     return w;
   };
+  const int lo = DwRegs<V4, kDwRegs>::shift(win(0).cb);
   uint32_t band = blockIdx.x;
   if (band < nbands) {
     uint32_t plane, r0;
     decode(band, plane, r0);
-    dw_win_load(bd, plane * OH * OW, OH, OW, win(r0), dLW, v);
+    v.load(bd, plane * OH * OW, OH, OW, win(r0), dLW);
   }
   for (; band < nbands; band += gridDim.x) {
     uint32_t plane, r0;
     decode(band, plane, r0);
     const uint32_t c = plane % C;
     __syncthreads();  // the previous band's LDS reads are done
-    dw_win_store(sd, v, LR * LW);
+    v.store(sd, LR, LW);
     __syncthreads();
     if (band + gridDim.x < nbands) {
       uint32_t pn, rn;
       decode(band + gridDim.x, pn, rn);
-      dw_win_load(bd, pn * OH * OW, OH, OW, win(rn), dLW, v);
+      v.load(bd, pn * OH * OW, OH, OW, win(rn), dLW);
     }
     float w[K * K];
 #pragma unroll
@@ -1548,7 +1596,7 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
       for (int i = 0; i < WR; ++i)
 #pragma unroll
-        for (int j = 0; j < WR; ++j) win_[i][j] = sd[(i0 + i) * LW + j0 + j];
+        for (int j = 0; j < WR; ++j) win_[i][j] = sd[(i0 + i) * LW + j0 + j + lo];
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
         const uint32_t ih = r0 + 2 * a + r;
@@ -1594,7 +1642,7 @@ __global__ void __launch_bounds__(256)
 // A thread takes 2 x 2 blocks of dy and the (S + K) x (S + K) x window under
 // them.  The K*K + 1 running sums are reduced once per block (waves by
 // shuffle, then the 4 wave sums in order) and stored as part[c][y][t] (double).
-template <int K, int S>
+template <int K, int S, bool V4>
 __global__ void __launch_bounds__(256)
     k_dw_bwd_filter_band(const float* __restrict__ dy, const float* __restrict__ x,
                          double* __restrict__ part, uint32_t B, uint32_t C, uint32_t H,
@@ -1603,14 +1651,16 @@ __global__ void __launch_bounds__(256)
                          FastDiv dLXW, FastDiv dLGW, FastDiv dNb, FastDiv dBW) {
   constexpr int T = K * K + 1;
   constexpr int XW = S + K;  // x window edge under a 2 x 2 dy block
-  __shared__ float sx[kDwBand];
-  __shared__ float sg[kDwBand / 2];
+  __shared__ __attribute__((aligned(16))) float sx[kDwBand];
+  __shared__ __attribute__((aligned(16))) float sg[kDwBand / 2];
   __shared__ float red[4][T];
   const uint32_t c = blockIdx.y;
   BRes bx, bg;
   bx.init(x, B * C * H * W);
   bg.init(dy, B * C * OH * OW);
-  float xv[kDwRegs], gv[kDwRegs / 2];
+  DwRegs<V4, kDwRegs> xv;
+  DwRegs<V4, kDwRegs / 2> gv;
+  const int lox = DwRegs<V4, kDwRegs>::shift(-int(p));
   // The channel's B * nb (image, band) units, split evenly over the pieces.
   const uint32_t units = B * nb;
   const uint32_t u0 = uint32_t(uint64_t(units) * blockIdx.x / gridDim.x);
@@ -1619,8 +1669,8 @@ __global__ void __launch_bounds__(256)
     const uint32_t u = u0 + j;
     const uint32_t n = fdiv(u, dNb), o0 = (u - n * nb) * RB;
     const uint32_t plane = n * C + c;
-    dw_win_load(bx, plane * H * W, H, W, DwWin{int(o0 * S) - int(p), -int(p), LXR, LXW}, dLXW, xv);
-    dw_win_load(bg, plane * OH * OW, OH, OW, DwWin{int(o0), 0, LGR, LGW}, dLGW, gv);
+    xv.load(bx, plane * H * W, H, W, DwWin{int(o0 * S) - int(p), -int(p), LXR, LXW}, dLXW);
+    gv.load(bg, plane * OH * OW, OH, OW, DwWin{int(o0), 0, LGR, LGW}, dLGW);
   };
   float acc[T];
 #pragma unroll
@@ -1628,8 +1678,8 @@ __global__ void __launch_bounds__(256)
   if (total) issue(0);
   for (uint32_t jb = 0; jb < total; ++jb) {
     __syncthreads();  // the previous band's LDS reads are done
-    dw_win_store(sx, xv, LXR * LXW);
-    dw_win_store(sg, gv, LGR * LGW);
+    xv.store(sx, LXR, LXW);
+    gv.store(sg, LGR, LGW);
     __syncthreads();
     if (jb + 1 < total) issue(jb + 1);
     const uint32_t items = (LGR / 2) * (LGW / 2);
@@ -1644,7 +1694,7 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
       for (int i = 0; i < XW; ++i)
 #pragma unroll
-        for (int jj = 0; jj < XW; ++jj) xw[i][jj] = sx[(2 * a * S + i) * LXW + 2 * b2 * S + jj];
+        for (int jj = 0; jj < XW; ++jj) xw[i][jj] = sx[(2 * a * S + i) * LXW + 2 * b2 * S + jj + lox];
 #pragma unroll
       for (int r = 0; r < 2; ++r)
 #pragma unroll
@@ -1677,7 +1727,9 @@ __global__ void __launch_bounds__(256)
 // at least 2 rows (RB is even).
 struct DwBand {
   uint32_t RB, R, LW, R2, LW2;  // dX: window R x LW; filter: x R x LW, dy R2 x LW2
+  bool v4;                      // quad windows: LW, LW2 are the stored widths
 };
+static uint32_t round4(uint32_t v) { return (v + 3) & ~3u; }
 static bool dw_band_ok(const DwGeom& g) {
   if (g.kH != g.kW || (g.kH != 3 && g.kH != 5) || (g.s != 1 && g.s != 2) || g.p >= g.kH)
     return false;
@@ -1685,31 +1737,42 @@ static bool dw_band_ok(const DwGeom& g) {
   return uint64_t(g.B) * g.C * g.H * g.W < kOob && uint64_t(g.B) * g.C * g.OH * g.OW < kOob;
 }
 static DwBand dw_band_input(const DwGeom& g) {
-  DwBand b{0, 0, 0, 0, 0};
+  DwBand b{0, 0, 0, 0, 0, false};
   if (!dw_band_ok(g)) return b;
   const uint32_t K = g.kH, BW = (g.W + 1) / 2;
   const uint32_t WR = g.s == 1 ? K + 1 : ((1 + (g.p & 1)) / 2 + (K - (g.p & 1)) / 2 + 1);
   b.LW = g.s == 1 ? 2 * BW + K : BW + WR;
+  // Quad windows when dy rows are 4-aligned: the stored window starts at the
+  // 4-aligned column left of the logical start cb.
+  b.v4 = g.OW % 4 == 0;
+  if (b.v4) {
+    const int cb = g.s == 1 ? int(g.p) - int(K - 1) : int(g.p / 2) - int((K - (g.p & 1)) / 2);
+    b.LW = round4(b.LW + uint32_t(cb & 3));
+  }
   const uint32_t rows = kDwBand / b.LW;  // window rows that fit
   uint32_t RB = g.s == 1 ? (rows > K ? rows - K : 0) : (rows > WR ? 2 * (rows - WR) : 0);
   RB &= ~1u;
-  if (RB < 2) return DwBand{0, 0, 0, 0, 0};
+  if (RB < 2) return DwBand{0, 0, 0, 0, 0, false};
   RB = std::min(RB, (g.H + 1) & ~1u);
   b.RB = RB;
   b.R = g.s == 1 ? RB + K : RB / 2 + WR;
   return b;
 }
 static DwBand dw_band_filter(const DwGeom& g) {
-  DwBand b{0, 0, 0, 0, 0};
+  DwBand b{0, 0, 0, 0, 0, false};
   if (!dw_band_ok(g)) return b;
   const uint32_t K = g.kH, S = g.s;
   b.LW2 = (g.OW + 1) & ~1u;
   b.LW = (b.LW2 - 1) * S + K;
-  if (b.LW2 * 2 > kDwBand / 2 || uint64_t(b.LW) * (S + K) > kDwBand) return DwBand{0, 0, 0, 0, 0};
+  // Quad windows when x and dy rows are 4-aligned (LW2 = OW is then a
+  // multiple of 4; the x window starts at the 4-aligned column left of -p).
+  b.v4 = g.W % 4 == 0 && g.OW % 4 == 0;
+  if (b.v4) b.LW = round4(b.LW + uint32_t(-int(g.p) & 3));
+  if (b.LW2 * 2 > kDwBand / 2 || uint64_t(b.LW) * (S + K) > kDwBand) return DwBand{0, 0, 0, 0, 0, false};
   const uint32_t byg = (kDwBand / 2) / b.LW2;
   const uint32_t byx = (kDwBand / b.LW - K) / S + 1;
   uint32_t RB = std::min(byg, byx) & ~1u;
-  if (RB < 2) return DwBand{0, 0, 0, 0, 0};
+  if (RB < 2) return DwBand{0, 0, 0, 0, 0, false};
   RB = std::min(RB, (g.OH + 1) & ~1u);
   b.RB = RB;
   b.R2 = RB;
@@ -1745,21 +1808,30 @@ static bool sh_dw_bwd_input(const Dispatch& d) {
       covers(f, uint64_t(g.C) * g.kH * g.kW) && covers(dx, total)) {
     const uint32_t nb = cdiv(g.H, bb.RB), nbands = g.B * g.C * nb;
     const uint32_t BW = (g.W + 1) / 2, ndy = g.B * g.C * g.OH * g.OW;
-    const FastDiv fLW = make_fastdiv(bb.LW), fNb = make_fastdiv(nb), fBW = make_fastdiv(BW);
+    const FastDiv fLW = make_fastdiv(bb.v4 ? bb.LW / 4 : bb.LW), fNb = make_fastdiv(nb),
+                  fBW = make_fastdiv(BW);
     const uint32_t podd = g.p & 1;
     // One resident round of blocks (the runtime's occupancy), each walking
     // bands with a grid stride: no partly filled second round.
+#define DCE_DWI_V(K, SS, PO, V)                                                                   \
+  {                                                                                              \
+    const uint32_t blocks = std::min<uint32_t>(                                                  \
+        nbands, uint32_t(num_cus()) * blocks_per_cu(k_dw_bwd_input_band<K, SS, PO, V>, 256));   \
+    hipLaunchKernelGGL((k_dw_bwd_input_band<K, SS, PO, V>), dim3(blocks), dim3(256), 0,          \
+                       stream(), dy.p, f.p, dx.p, g.C, g.H, g.W, g.OH, g.OW, g.p, bb.RB, nb,     \
+                       nbands, bb.R, bb.LW, BW, ndy, fLW, fNb, fBW);                             \
+  }
 #define DCE_DWI(K, SS, PO)                                                                        \
   if (g.kH == K && g.s == SS && (SS == 1 || podd == PO)) {                                       \
-    const uint32_t blocks = std::min<uint32_t>(                                                  \
-        nbands, uint32_t(num_cus()) * blocks_per_cu(k_dw_bwd_input_band<K, SS, PO>, 256));      \
-    hipLaunchKernelGGL((k_dw_bwd_input_band<K, SS, PO>), dim3(blocks), dim3(256), 0, stream(),     \
-                       dy.p, f.p, dx.p, g.C, g.H, g.W, g.OH, g.OW, g.p, bb.RB, nb, nbands, bb.R,   \
-                       bb.LW, BW, ndy, fLW, fNb, fBW);                                             \
+    if (bb.v4)                                                                                   \
+      DCE_DWI_V(K, SS, PO, true)                                                                 \
+    else                                                                                         \
+      DCE_DWI_V(K, SS, PO, false)                                                                \
   }
     DCE_DWI(3, 1, 0) DCE_DWI(3, 2, 0) DCE_DWI(3, 2, 1)
     DCE_DWI(5, 1, 0) DCE_DWI(5, 2, 0) DCE_DWI(5, 2, 1)
 #undef DCE_DWI
+#undef DCE_DWI_V
     return check_launch("depthwise_conv_backward_input");
   }
   hipLaunchKernelGGL(k_dw_bwd_input, dim3(cdiv(total, 256)), dim3(256), 0, stream(), dy, f, dx, g,
@@ -1783,8 +1855,10 @@ static bool sh_dw_bwd_filter(const Dispatch& d) {
     // fraction of the machine), each piece an even share of the channel's
     // (image, band) units, at least about one image's worth.
     int occ = 1;
-#define DCE_DWO(K, SS) \
-  if (g.kH == K && g.s == SS) occ = blocks_per_cu(k_dw_bwd_filter_band<K, SS>, 256);
+#define DCE_DWO(K, SS)                                                                      \
+  if (g.kH == K && g.s == SS)                                                              \
+    occ = bb.v4 ? blocks_per_cu(k_dw_bwd_filter_band<K, SS, true>, 256)                    \
+                : blocks_per_cu(k_dw_bwd_filter_band<K, SS, false>, 256);
     DCE_DWO(3, 1) DCE_DWO(3, 2) DCE_DWO(5, 1) DCE_DWO(5, 2)
 #undef DCE_DWO
     const uint32_t want =
@@ -1796,15 +1870,23 @@ static bool sh_dw_bwd_filter(const Dispatch& d) {
                    4.0 * double(len) * g.C + 4.0 * double(g.B) * g.C * g.H * g.W);
     const dim3 grid(pieces, g.C);
     const uint32_t nb = cdiv(g.OH, bb.RB);
-    const FastDiv fLX = make_fastdiv(bb.LW), fLG = make_fastdiv(bb.LW2), fNb = make_fastdiv(nb),
+    const FastDiv fLX = make_fastdiv(bb.v4 ? bb.LW / 4 : bb.LW),
+                  fLG = make_fastdiv(bb.v4 ? bb.LW2 / 4 : bb.LW2), fNb = make_fastdiv(nb),
                   fBW = make_fastdiv(bb.LW2 / 2);
+#define DCE_DWF_V(K, SS, V)                                                                      \
+  hipLaunchKernelGGL((k_dw_bwd_filter_band<K, SS, V>), grid, dim3(256), 0, stream(), dy.p, x.p,   \
+                     part, g.B, g.C, g.H, g.W, g.OH, g.OW, g.p, bb.RB, nb, bb.R, bb.LW, bb.R2,    \
+                     bb.LW2, fLX, fLG, fNb, fBW);
 #define DCE_DWF(K, SS)                                                                          \
-  if (g.kH == K && g.s == SS)                                                                  \
-    hipLaunchKernelGGL((k_dw_bwd_filter_band<K, SS>), grid, dim3(256), 0, stream(), dy.p, x.p,   \
-                       part, g.B, g.C, g.H, g.W, g.OH, g.OW, g.p, bb.RB, nb, bb.R, bb.LW, bb.R2, \
-                       bb.LW2, fLX, fLG, fNb, fBW);
+  if (g.kH == K && g.s == SS) {                                                                \
+    if (bb.v4)                                                                                 \
+      DCE_DWF_V(K, SS, true)                                                                   \
+    else                                                                                       \
+      DCE_DWF_V(K, SS, false)                                                                  \
+  }
     DCE_DWF(3, 1) DCE_DWF(3, 2) DCE_DWF(5, 1) DCE_DWF(5, 2)
 #undef DCE_DWF
+#undef DCE_DWF_V
     hipLaunchKernelGGL(k_dw_bwd_filter_final, dim3(cdiv(g.C * (taps + 1), 4)), dim3(256), 0,
                        stream(), part, pieces, g.C, taps, U(d, 0), U(d, 1));
     return check_launch("depthwise_conv_backward_filter");

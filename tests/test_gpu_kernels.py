@@ -310,6 +310,9 @@ DW_CASES = [
     # band kernels: several bands per plane, K 5 stride 2, pad 0, one-row bands on a wide plane
     (2, 16, 56, 56, 3, 1, 1), (2, 16, 112, 112, 3, 2, 1), (2, 5, 11, 13, 5, 2, 2), (2, 3, 8, 9, 3, 1, 0),
     (1, 2, 3, 1100, 3, 1, 1),
+    # quad windows (row widths multiples of 4), shifted window origins, mixed dword / quad
+    (2, 4, 32, 32, 5, 1, 2), (2, 4, 40, 40, 5, 2, 2), (2, 4, 31, 33, 3, 2, 0), (2, 4, 18, 18, 3, 1, 0),
+    (2, 3, 25, 25, 5, 2, 1), (1, 2, 200, 64, 3, 1, 1),
     # generic kernels: 2x2 taps, stride 3
     (2, 4, 8, 8, 2, 2, 0), (1, 4, 10, 10, 3, 3, 1),
 ]
