@@ -568,18 +568,28 @@ __global__ void __launch_bounds__(256)
   const uint32_t pb = id % npb, rest = id / npb;
   const uint32_t c0 = (rest % ncb) * 32, p0 = pb * 64, b = rest / ncb;
   const int tid = threadIdx.x;
+  // Branch-free loads through buffer resources (elements outside the tile's
+  // channels / pixels read at kOob, i.e. zero): all sixteen of a thread's
+  // loads are in flight together.  Callers admit tensors below kOob floats.
+  BRes bi, by;
+  const uint32_t n = nB * C * HW;
+  bi.init(in, n);
+  by.init(y ? y : in, n);
+  float v[8], m[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int e = tid + 256 * j;
     const int cl = e >> 6, pl = e & 63;
     const uint32_t c = c0 + cl, p = p0 + pl;
-    float v = 0.f;
-    if (c < C && p < HW) {
-      const size_t idx = (size_t(b) * C + c) * HW + p;
-      v = in[idx];
-      if (y != nullptr && y[idx] <= 0.f) v = 0.f;
-    }
-    t[cl][pl] = v;
+    const uint32_t off = (c < C && p < HW) ? (b * C + c) * HW + p : kOob;
+    v[j] = bi.ld1(off);
+    m[j] = y ? by.ld1(off) : 1.f;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int e = tid + 256 * j;
+    // ReLU mask: y <= 0 zeroes the gradient (a NaN y keeps it).
+    t[e >> 6][e & 63] = m[j] <= 0.f ? 0.f : v[j];
   }
   __syncthreads();
   if (dbPart != nullptr) {
