@@ -182,3 +182,35 @@ def test_mobilenet_ir_stack_step(eng):
     _compare_grads(g, og)
     for k in P:
         assert rel_err(new[k], K.sgd(P[k], g[k], f32(0.01), 1e30)) <= 1e-6, k
+
+
+def test_metrics_epoch(eng):
+    """Metrics (nn_engine.py:2336-2385): loss and accuracy accumulated on the
+    GPU over several batches of a LeNet forward, read back once by collect().
+    The correct count is bit-exact (first-max-wins argmax, ties included);
+    the average loss matches the oracle's per-batch CE within float32."""
+    P = WL.lenet_params(rng(6001))
+    be = WL.Device(eng, P)
+    m = eng.Metrics()
+    losses, correct, n = [], 0, 0
+    for i in range(4):
+        B = 16 + 8 * i
+        x = rng(6100 + i).standard_normal((B, 1, 28, 28)).astype(np.float32)
+        y = rng(6200 + i).integers(0, 10, B).astype(np.float32)
+        z = WL.lenet(be, x)
+        if i == 2:  # a tied row: the first maximum wins
+            zz = z.sync().copy()
+            zz[0, :] = 0.0
+            z.upload(zz)
+        loss = eng.softmax_ce(z, eng.Tensor(y, track=True))
+        m.update(loss, z, eng.Tensor(y, track=True))
+        zv = z.sync().copy()
+        losses.append(K.ce_loss(zv, y))
+        correct += K.argmax_correct(zv, y)
+        n += B
+        eng.end_batch()
+    avg, acc = m.collect(n)
+    assert acc == correct / n
+    assert abs(avg - np.mean(losses)) <= 1e-5 * abs(np.mean(losses))
+    m.reset()
+    assert m.collect(n) == (0.0, 0.0)
