@@ -97,10 +97,15 @@ struct Stage {
 template <class St>
 struct LoaderBase {
   static constexpr int Q = St::Q;
-  int lds0;
+  // LDSD: the operand goes global -> LDS directly (buffer_load ... lds).  Only
+  // the unpadded [row][k] stages qualify: there a wave's 64 quads of one load
+  // are 64 consecutive 16-byte LDS slots in lane order (lds_off(t) = 4 t).
+  static constexpr bool LDSD = false;
+  int lds0, wbase;
   bool act;
   __device__ __forceinline__ void base_init(int tid) {
     lds0 = St::lds_off(tid);
+    wbase = St::lds_off(tid & ~63);
     act = St::active(tid);
   }
   __device__ __forceinline__ void store(float* S, const f4 (&r)[Q]) const {
@@ -146,6 +151,14 @@ struct LdDenseRK : LoaderBase<Stage<R, KT, false>> {
     const bool kok = k0 + kq < kdim;
 #pragma unroll
     for (int i = 0; i < Q; ++i) r[i] = b.ld4(kok ? base[i] + k0 : kOob);
+  }
+  static constexpr bool LDSD = true;
+  __device__ __forceinline__ void issue_lds(uint32_t kt, float* S) const {
+    if (St::PART && !this->act) return;  // whole waves (NQ is a multiple of 64)
+    const uint32_t k0 = kt * KT;
+    const bool kok = k0 + kq < kdim;
+#pragma unroll
+    for (int i = 0; i < Q; ++i) b.ld4_lds(kok ? base[i] + k0 : kOob, S + this->wbase + i * St::DLDS);
   }
 };
 
@@ -248,6 +261,19 @@ struct LdPixRK : LoaderBase<Stage<R, KT, false>> {
     }
   }
   __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
+    uint32_t off[Q];
+    offsets(kt, off);
+#pragma unroll
+    for (int i = 0; i < Q; ++i) r[i] = b.ld4(off[i]);
+  }
+  static constexpr bool LDSD = true;
+  __device__ __forceinline__ void issue_lds(uint32_t kt, float* S) const {
+    uint32_t off[Q];
+    offsets(kt, off);
+#pragma unroll
+    for (int i = 0; i < Q; ++i) b.ld4_lds(off[i], S + this->wbase + i * St::DLDS);
+  }
+  __device__ __forceinline__ void offsets(uint32_t kt, uint32_t (&o)[Q]) const {
     uint32_t khw, ch;
     bool kok;
     if (BLK) {
@@ -281,7 +307,7 @@ struct LdPixRK : LoaderBase<Stage<R, KT, false>> {
         ok = ok && uint32_t(h) * s == uint32_t(hs) && uint32_t(w) * s == uint32_t(ws);
       }
       ok = ok && uint32_t(h) < srcH && uint32_t(w) < srcW;
-      r[i] = b.ld4(ok ? (pbase[i] + uint32_t(h) * srcW + uint32_t(w)) * Cp + ch : kOob);
+      o[i] = ok ? (pbase[i] + uint32_t(h) * srcW + uint32_t(w)) * Cp + ch : kOob;
     }
   }
 };
@@ -507,21 +533,25 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = zero4();
 
+  constexpr bool DA = LA::LDSD, DB = LB::LDSD;
   if (kb < ke) {
-    la.load(kb, ra);
-    lb.load(kb, rb);
-    la.store(As, ra);
-    lb.store(Bs, rb);
+    if constexpr (DA) la.issue_lds(kb, As); else la.load(kb, ra);
+    if constexpr (DB) lb.issue_lds(kb, Bs); else lb.load(kb, rb);
+    if constexpr (!DA) la.store(As, ra);
+    if constexpr (!DB) lb.store(Bs, rb);
   }
+  if constexpr (DA || DB) __builtin_amdgcn_s_waitcnt(0);  // the direct loads have landed
   __syncthreads();
 
   const int r = lane & 15, g = lane >> 4;
   for (uint32_t kt = kb; kt < ke; ++kt) {
     const int cur = int(kt - kb) & 1;
     const bool more = kt + 1 < ke;
+    // Next tile: register staging, or straight into the other LDS stage (its
+    // readers finished before the previous barrier).
     if (more) {
-      la.load(kt + 1, ra);
-      lb.load(kt + 1, rb);
+      if constexpr (DA) la.issue_lds(kt + 1, As + (cur ^ 1) * SA::SIZE); else la.load(kt + 1, ra);
+      if constexpr (DB) lb.issue_lds(kt + 1, Bs + (cur ^ 1) * SB::SIZE); else lb.load(kt + 1, rb);
     }
     const float* Ac = As + cur * SA::SIZE;
     const float* Bc = Bs + cur * SB::SIZE;
@@ -541,9 +571,10 @@ __global__ void __launch_bounds__(kThreads)
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][s], bf[j][s], acc[i][j], 0, 0, 0);
     }
     if (more) {
-      la.store(As + (cur ^ 1) * SA::SIZE, ra);
-      lb.store(Bs + (cur ^ 1) * SB::SIZE, rb);
+      if constexpr (!DA) la.store(As + (cur ^ 1) * SA::SIZE, ra);
+      if constexpr (!DB) lb.store(Bs + (cur ^ 1) * SB::SIZE, rb);
     }
+    if constexpr (DA || DB) __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
   EPI::template store<MT, NT, FM, FN>(pe, acc, m0, n0, z, wm, wn, lane);

@@ -94,6 +94,13 @@ struct BRes {
   __device__ __forceinline__ float ld1(uint32_t off) const {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off * 4u, 0, 0));
   }
+  // 16 bytes per lane straight into LDS: the wave's lanes fill 64 consecutive
+  // 16-byte slots from `lds` (wave-uniform) in lane order; an offset past
+  // num_records writes zeros.  Completion is tracked by vmcnt.
+  __device__ __forceinline__ void ld4_lds(uint32_t off, float* lds) const {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        r, (__attribute__((address_space(3))) void*)lds, 16, off * 4u, 0, 0, 0);
+  }
 };
 
 // ---------------------------------------------------------------------------
