@@ -49,15 +49,21 @@ static inline uint32_t cdiv(uint64_t a, uint64_t b) { return uint32_t((a + b - 1
 // ---------------------------------------------------------------------------
 // LDS stage geometry of one operand.
 // ---------------------------------------------------------------------------
-template <int R, int KT, bool KROW>
+template <int R, int KT, bool KROW, bool SWZOK = true>
 struct Stage {
-  // KROW rows are padded by 4 floats; ROWK rows are KT floats, unpadded.
-  // Measured with an LDS probe on gfx950 (64 banks): 16-byte stores of the
-  // loaders' ROWK pattern (KQ quads of consecutive rows) run 15% slower with
-  // a +4 pad than without, while the fragment reads (one quad of 16
-  // consecutive rows) cost the same either way; the 16-byte KROW stores are
-  // contiguous runs of a k row.
-  static constexpr int LD = KROW ? (R + 4) : KT;
+  // ROWK rows are KT floats, unpadded.  Measured with an LDS probe on gfx950
+  // (64 banks): 16-byte stores of the loaders' ROWK pattern (KQ quads of
+  // consecutive rows) run 15% slower with a +4 pad than without, while the
+  // fragment reads (one quad of 16 consecutive rows) cost the same either way.
+  // KROW rows of at least 64 floats (SWZ, when the loader opts in) are
+  // unpadded too, with the row-quad index XOR-swizzled by k (fk): a fragment
+  // read takes one float of 16 consecutive rows at 4 k's 4 apart, which the
+  // swizzle spreads over all 64 banks (unswizzled, k rows R floats apart
+  // would share banks).  Other KROW rows keep a +4 pad.  Unpadded stages take
+  // direct global-to-LDS loads.  The conv dW loaders stay padded: with direct
+  // loads their per-quad tap rows cost more than the staging they save.
+  static constexpr bool SWZ = KROW && SWZOK && R >= 64;
+  static constexpr int LD = KROW ? (SWZ ? R : R + 4) : KT;
   static constexpr int SIZE = KROW ? KT * LD : R * LD;
   static constexpr int KQ = KT / 4;
   static constexpr int RQ = R / 4;
@@ -84,12 +90,24 @@ struct Stage {
   __device__ static __forceinline__ int lds_off(int t) {
     return KROW ? qk(t, 0) * LD + qrow(t, 0) : qrow(t, 0) * LD + qk(t, 0);
   }
+  // SWZ: logical row quad rq of k row k sits at physical quad rq ^ fk(k).
+  __device__ static __forceinline__ int fk(int k) { return 4 * ((k >> 2) & 3); }
+  // The logical first row of quad i of thread t (its physical slot is
+  // lds_off(t) + i * DLDS): KROW rows are swizzled back from the slot.
+  __device__ static __forceinline__ int qrow_data(int t, int i) {
+    if (!SWZ) return qrow(t, i);
+    return 4 * ((t % RQ) ^ fk(qk(t, i)));
+  }
   // MFMA operand of 16 rows starting at rb, k slice kb: components s = 0..3.
   __device__ static __forceinline__ f4 frag(const float* S, int rb, int r, int g, int kb) {
     if (!KROW) return *reinterpret_cast<const f4*>(S + (rb + r) * LD + kb + 4 * g);
     f4 v;
+    const int row = rb + r;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) v[s] = S[(kb + 4 * g + s) * LD + rb + r];
+    for (int s = 0; s < 4; ++s) {
+      const int k = kb + 4 * g + s;
+      v[s] = SWZ ? S[k * LD + 4 * ((row >> 2) ^ fk(k)) + (row & 3)] : S[k * LD + row];
+    }
     return v;
   }
 };
@@ -173,23 +191,40 @@ struct LdDenseKR : LoaderBase<Stage<R, KT, true>> {
     uint32_t ld, rows, kdim, n;
   };
   BRes b;
-  uint32_t kdim, ld, kk0, base;  // base: quad 0's offset, or kOob for rows past the matrix
+  uint32_t kdim, ld, kk0;
+  uint32_t base[Q];  // quad i's offset at k tile 0, or kOob for rows past the matrix
   __device__ __forceinline__ void init(const Params& P, uint32_t row0, int tid) {
     this->base_init(tid);
     b.init(P.p, P.n);
     kdim = P.kdim;
     ld = P.ld;
     kk0 = St::qk(tid, 0);
-    const uint32_t row = row0 + St::qrow(tid, 0);
-    base = (this->act && row < P.rows) ? kk0 * P.ld + row : kOob;
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+      const uint32_t row = row0 + St::qrow_data(tid, i);
+      base[i] = (this->act && row < P.rows) ? (kk0 + St::DK * i) * P.ld + row : kOob;
+    }
   }
-  __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
+  __device__ __forceinline__ void offsets(uint32_t kt, uint32_t (&o)[Q]) const {
     const uint32_t k0 = kt * KT;
 #pragma unroll
     for (int i = 0; i < Q; ++i) {
       const uint32_t k = k0 + kk0 + St::DK * i;
-      r[i] = b.ld4(k < kdim ? base + (k0 + St::DK * i) * ld : kOob);
+      o[i] = k < kdim ? base[i] + k0 * ld : kOob;
     }
+  }
+  __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
+    uint32_t o[Q];
+    offsets(kt, o);
+#pragma unroll
+    for (int i = 0; i < Q; ++i) r[i] = b.ld4(o[i]);
+  }
+  static constexpr bool LDSD = St::SWZ;
+  __device__ __forceinline__ void issue_lds(uint32_t kt, float* S) const {
+    uint32_t o[Q];
+    offsets(kt, o);
+#pragma unroll
+    for (int i = 0; i < Q; ++i) b.ld4_lds(o[i], S + this->wbase + i * St::DLDS);
   }
 };
 
@@ -321,29 +356,46 @@ struct GradKRParams {
   uint32_t OCp, npix, n;
 };
 template <int R, int KT>
-struct LdGradKR : LoaderBase<Stage<R, KT, true>> {
-  using St = Stage<R, KT, true>;
+struct LdGradKR : LoaderBase<Stage<R, KT, true, false>> {
+  using St = Stage<R, KT, true, false>;
   static constexpr bool KROW = true;
   using LoaderBase<St>::Q;
   using Params = GradKRParams;
   BRes b;
-  uint32_t OCp, npix, kk0, base;  // base: quad 0's offset, or kOob for channels past OCp
+  uint32_t OCp, npix, kk0;
+  uint32_t base[Q];  // quad i's offset at k tile 0, or kOob for channels past OCp
   __device__ __forceinline__ void init(const Params& P, uint32_t row0, int tid) {
     this->base_init(tid);
     b.init(P.g, P.n);
     OCp = P.OCp;
     npix = P.npix;
     kk0 = St::qk(tid, 0);
-    const uint32_t oc = row0 + St::qrow(tid, 0);
-    base = (this->act && oc < P.OCp) ? kk0 * P.OCp + oc : kOob;
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+      const uint32_t oc = row0 + St::qrow_data(tid, i);
+      base[i] = (this->act && oc < P.OCp) ? (kk0 + St::DK * i) * P.OCp + oc : kOob;
+    }
   }
-  __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
+  __device__ __forceinline__ void offsets(uint32_t kt, uint32_t (&o)[Q]) const {
     const uint32_t p0 = kt * KT;
 #pragma unroll
     for (int i = 0; i < Q; ++i) {
       const uint32_t pix = p0 + kk0 + St::DK * i;
-      r[i] = b.ld4(pix < npix ? base + (p0 + St::DK * i) * OCp : kOob);
+      o[i] = pix < npix ? base[i] + p0 * OCp : kOob;
     }
+  }
+  __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
+    uint32_t o[Q];
+    offsets(kt, o);
+#pragma unroll
+    for (int i = 0; i < Q; ++i) r[i] = b.ld4(o[i]);
+  }
+  static constexpr bool LDSD = St::SWZ;
+  __device__ __forceinline__ void issue_lds(uint32_t kt, float* S) const {
+    uint32_t o[Q];
+    offsets(kt, o);
+#pragma unroll
+    for (int i = 0; i < Q; ++i) b.ld4_lds(o[i], S + this->wbase + i * St::DLDS);
   }
 };
 
@@ -355,15 +407,18 @@ struct XTapParams {
   FastDiv dOHW, dOW, dCp, dK;
 };
 template <int R, int KT>
-struct LdXTapKR : LoaderBase<Stage<R, KT, true>> {
-  using St = Stage<R, KT, true>;
+struct LdXTapKR : LoaderBase<Stage<R, KT, true, false>> {
+  using St = Stage<R, KT, true, false>;
   static constexpr bool KROW = true;
   using LoaderBase<St>::Q;
   using Params = XTapParams;
   BRes b;
-  uint32_t H, W, Cp, s, OW, OHW, npix, kk0, off;
+  uint32_t H, W, Cp, s, OW, OHW, npix, kk0;
   FastDiv dOHW, dOW;
-  int kh, kw;  // the thread's tap row (same for all its quads)
+  // Quad i's tap row: channel offset and tap origin (kh, kw); with the
+  // swizzled stage the quads of one thread sit on different tap rows.
+  uint32_t off[Q];
+  int kh[Q], kw[Q];
   __device__ __forceinline__ void init(const Params& P, uint32_t row0, int tid) {
     this->base_init(tid);
     b.init(P.x, P.n);
@@ -377,17 +432,20 @@ struct LdXTapKR : LoaderBase<Stage<R, KT, true>> {
     dOHW = P.dOHW;
     dOW = P.dOW;
     kk0 = St::qk(tid, 0);
-    const uint32_t n = row0 + St::qrow(tid, 0);
-    const uint32_t khw = fdiv(n, P.dCp);
-    off = n - khw * P.Cp;
-    const uint32_t a = fdiv(khw, P.dK);
-    kh = int(a) - int(P.p);
-    kw = int(khw - a * P.k) - int(P.p);
-    // A row past the taps (or a thread that stages nothing) gets an offset no
-    // pixel can bring into the image.
-    if (n >= P.N || !this->act) kh = -(1 << 20);
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+      const uint32_t n = row0 + St::qrow_data(tid, i);
+      const uint32_t khw = fdiv(n, P.dCp);
+      off[i] = n - khw * P.Cp;
+      const uint32_t a = fdiv(khw, P.dK);
+      kh[i] = int(a) - int(P.p);
+      kw[i] = int(khw - a * P.k) - int(P.p);
+      // A row past the taps (or a thread that stages nothing) gets an offset
+      // no pixel can bring into the image.
+      if (n >= P.N || !this->act) kh[i] = -(1 << 20);
+    }
   }
-  __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
+  __device__ __forceinline__ void offsets(uint32_t kt, uint32_t (&o)[Q]) const {
 #pragma unroll
     for (int i = 0; i < Q; ++i) {
       const uint32_t pix = kt * KT + kk0 + St::DK * i;
@@ -395,11 +453,24 @@ struct LdXTapKR : LoaderBase<Stage<R, KT, true>> {
       const uint32_t rem = pix - bb * OHW;
       const uint32_t oh = fdiv(rem, dOW);
       const uint32_t ow = rem - oh * OW;
-      const int ih = int(oh * s) + kh;
-      const int iw = int(ow * s) + kw;
+      const int ih = int(oh * s) + kh[i];
+      const int iw = int(ow * s) + kw[i];
       const bool ok = pix < npix && uint32_t(ih) < H && uint32_t(iw) < W;
-      r[i] = b.ld4(ok ? ((bb * H + uint32_t(ih)) * W + uint32_t(iw)) * Cp + off : kOob);
+      o[i] = ok ? ((bb * H + uint32_t(ih)) * W + uint32_t(iw)) * Cp + off[i] : kOob;
     }
+  }
+  __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
+    uint32_t o[Q];
+    offsets(kt, o);
+#pragma unroll
+    for (int i = 0; i < Q; ++i) r[i] = b.ld4(o[i]);
+  }
+  static constexpr bool LDSD = St::SWZ;
+  __device__ __forceinline__ void issue_lds(uint32_t kt, float* S) const {
+    uint32_t o[Q];
+    offsets(kt, o);
+#pragma unroll
+    for (int i = 0; i < Q; ++i) b.ld4_lds(o[i], S + this->wbase + i * St::DLDS);
   }
 };
 
