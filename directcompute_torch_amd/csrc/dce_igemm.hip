@@ -785,42 +785,106 @@ __global__ void k_splitk_sum(const float* __restrict__ part, float* __restrict__
   out[i] = s;
 }
 
+// Quad form of k_splitk_sum for n % 4 == 0 (same summation order).
+__global__ void __launch_bounds__(256)
+    k_splitk_sum4(const f4* __restrict__ part, f4* __restrict__ out, uint32_t nq,
+                  uint32_t splits) {
+  const uint32_t q = blockIdx.x * 256 + threadIdx.x;
+  if (q >= nq) return;
+  f4 s = {0.f, 0.f, 0.f, 0.f};
+  uint32_t z = 0;
+  for (; z + 3 < splits; z += 4) {
+    const f4 a = part[size_t(z) * nq + q], b = part[size_t(z + 1) * nq + q];
+    const f4 c = part[size_t(z + 2) * nq + q], d = part[size_t(z + 3) * nq + q];
+    s += a;
+    s += b;
+    s += c;
+    s += d;
+  }
+  for (; z < splits; ++z) s += part[size_t(z) * nq + q];
+  out[q] = s;
+}
+
 // dW finalize: dw[oc][c][khw] = sum_z part[z][oc][khw*Cp + c], or with
 // `trans` (the GEMM ran with taps as rows) sum_z part[z][khw*Cp + c][oc].
-// Block of 1024 = 64 consecutive partial elements (storage order, so the
-// partial reads are coalesced) x 16 split slices: slice w sums z = w, w+16,
-// ..., then the 16 slice sums are added in slice order.  Padding channels
-// (c >= C) are dropped.
-__global__ void __launch_bounds__(1024)
-    k_dw_final(const float* __restrict__ part, float* __restrict__ dw, uint32_t OC, uint32_t C,
+// Quad form: thread (quad q, slice w) sums the 16-byte quads part[z][4q..]
+// over z = w, w + SL, w + 2 SL, ... (four loads in flight); with SL > 1 the
+// SL slice sums are then added in slice order through LDS, so the result is
+// deterministic.  SL (1, 4 or 16) is chosen from the quad count alone, which
+// keeps enough loads in flight when few quads take many splits.  Elements
+// i = 4q + j are stored in storage order of the partials; OC*KK*Cp is a
+// multiple of 4 because Cp is.  Padding channels (c >= C) are dropped.
+template <int SL>
+__global__ void __launch_bounds__(256)
+    k_dw_final(const f4* __restrict__ part, float* __restrict__ dw, uint32_t OC, uint32_t C,
                uint32_t KK, uint32_t Cp, uint32_t splits, uint32_t trans) {
-  __shared__ float sh[16][64];
-  const uint32_t N = KK * Cp;
-  const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const uint32_t i = blockIdx.x * 64 + lane;
-  const bool ok = i < OC * N;
-  const size_t zs = size_t(OC) * N;
-  float s = 0.f;
-  if (ok) {
-#pragma unroll 4
-    for (uint32_t z = w; z < splits; z += 16) s += part[z * zs + i];
+  constexpr uint32_t QB = 256 / SL;
+  __shared__ f4 sh[SL][QB];
+  const uint32_t N = KK * Cp, nq = OC * (N / 4);
+  const uint32_t lq = threadIdx.x % QB, w = threadIdx.x / QB;
+  const uint32_t q = blockIdx.x * QB + lq;
+  f4 s = {0.f, 0.f, 0.f, 0.f};
+  if (q < nq) {
+    const size_t zs = nq;
+    uint32_t z = w;
+    for (; z + 3 * SL < splits; z += 4 * SL) {
+      const f4 a = part[z * zs + q], b = part[(z + SL) * zs + q];
+      const f4 c = part[(z + 2 * SL) * zs + q], d = part[(z + 3 * SL) * zs + q];
+      s += a;
+      s += b;
+      s += c;
+      s += d;
+    }
+    for (; z < splits; z += SL) s += part[z * zs + q];
   }
-  sh[w][lane] = s;
-  __syncthreads();
-  if (w != 0 || !ok) return;
-  float t = 0.f;
+  if constexpr (SL > 1) {
+    sh[w][lq] = s;
+    __syncthreads();
+    if (w != 0) return;
+    s = sh[0][lq];
 #pragma unroll
-  for (int k = 0; k < 16; ++k) t += sh[k][lane];
-  uint32_t oc, n;
-  if (trans) {
-    n = i / OC;
-    oc = i - n * OC;
-  } else {
-    oc = i / N;
-    n = i - oc * N;
+    for (int k = 1; k < SL; ++k) s += sh[k][lq];
   }
-  const uint32_t khw = n / Cp, c = n - khw * Cp;
-  if (c < C) dw[(size_t(oc) * C + c) * KK + khw] = t;
+  if (q >= nq) return;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t i = 4 * q + j;
+    uint32_t oc, n;
+    if (trans) {
+      n = i / OC;
+      oc = i - n * OC;
+    } else {
+      oc = i / N;
+      n = i - oc * N;
+    }
+    const uint32_t khw = n / Cp, c = n - khw * Cp;
+    if (c < C) dw[(size_t(oc) * C + c) * KK + khw] = s[j];
+  }
+}
+
+// Slices per quad for k_dw_final: the fewest (1, 4, 16) that give about
+// 128 K threads, never more than the splits.
+static uint32_t dw_final_slices(uint32_t nq, uint32_t splits) {
+  uint32_t sl = 1;
+  while (sl < 16 && size_t(nq) * sl < 131072 && sl * 4 <= splits) sl *= 4;
+  return sl;
+}
+
+static bool dw_final(const float* part, float* dw, uint32_t OC, uint32_t C, uint32_t KK,
+                     uint32_t Cp, uint32_t splits, bool trans) {
+  const uint32_t nq = OC * (KK * Cp / 4), sl = dw_final_slices(nq, splits);
+  const f4* p4 = reinterpret_cast<const f4*>(part);
+  const uint32_t tr = trans ? 1u : 0u;
+  if (sl == 1)
+    hipLaunchKernelGGL(k_dw_final<1>, dim3(cdiv(nq, 256u)), dim3(256), 0, stream(), p4, dw, OC, C,
+                       KK, Cp, splits, tr);
+  else if (sl == 4)
+    hipLaunchKernelGGL(k_dw_final<4>, dim3(cdiv(nq, 64u)), dim3(256), 0, stream(), p4, dw, OC, C,
+                       KK, Cp, splits, tr);
+  else
+    hipLaunchKernelGGL(k_dw_final<16>, dim3(cdiv(nq, 16u)), dim3(256), 0, stream(), p4, dw, OC,
+                       C, KK, Cp, splits, tr);
+  return check_launch("dw_final");
 }
 
 // Split-K finish for an NCHW output: out[b][m][pix] = act(sum_z part[z][m][n]
@@ -840,6 +904,46 @@ __global__ void k_splitk_nchw(const float* __restrict__ part, const float* __res
     z = tanhf(z);
   const uint32_t b = n / HW, pix = n - b * HW;
   out[(size_t(b) * M + m) * HW + pix] = z;
+}
+
+// Quad form of k_splitk_nchw for N % 4 == 0: 16-byte partial loads, four in
+// flight, z still summed in order (same bits as the scalar form).  The four
+// elements of a quad lie in one row m and may straddle an image boundary.
+__global__ void __launch_bounds__(256)
+    k_splitk_nchw4(const f4* __restrict__ part, const float* __restrict__ bias,
+                   float* __restrict__ out, uint32_t M, uint32_t N, uint32_t HW, uint32_t splits,
+                   uint32_t act) {
+  const uint32_t q = blockIdx.x * 256 + threadIdx.x;
+  const uint32_t nq = M * (N / 4);
+  if (q >= nq) return;
+  const size_t zs = nq;
+  f4 s = {0.f, 0.f, 0.f, 0.f};
+  uint32_t z = 0;
+  for (; z + 3 < splits; z += 4) {
+    const f4 a = part[z * zs + q], b = part[(z + 1) * zs + q];
+    const f4 c = part[(z + 2) * zs + q], d = part[(z + 3) * zs + q];
+    s += a;
+    s += b;
+    s += c;
+    s += d;
+  }
+  for (; z < splits; ++z) s += part[z * zs + q];
+  const uint32_t m = (4 * q) / N, n0 = 4 * q - m * N;
+  uint32_t b = n0 / HW, pix = n0 - b * HW;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float v = s[j];
+    if (bias) v += bias[m];
+    if (act == 1)
+      v = fmaxf(v, 0.f);
+    else if (act == 2)
+      v = tanhf(v);
+    out[(size_t(b) * M + m) * HW + pix] = v;
+    if (++pix == HW) {
+      pix = 0;
+      ++b;
+    }
+  }
 }
 
 // Zero-padded copy of a row-major [rows][cols] matrix to row stride ldp.
@@ -916,28 +1020,29 @@ static int occupancy(Kern kernel) {
 }
 
 // Estimated microseconds of one launch plus its split-K finish, used to pick
-// the split count.  The W = tiles * splits workgroups run in rounds of
-// cap = CUs * occupancy; in a round with r workgroups per CU, one K tile
-// takes max(kLatencyUs, r * tm), where tm is the K tile's MFMA time for a
-// lone workgroup (MT*NT*KT*2 flops at the CU's 614 GFLOP/s fp32 matrix peak)
-// and kLatencyUs the latency-bound floor.  Split partials cost
+// the split count.  The W = tiles * splits workgroups are spread evenly over
+// the CUs; the busiest CU gets n = ceil(W / CUs) of them and runs them in
+// batches of at most `occ` (the kernel's workgroups per CU).  In a batch of r
+// workgroups one K tile takes max(kLatencyUs, r * tm), where tm is the K
+// tile's MFMA time for a lone workgroup (MT*NT*KT*2 flops at the CU's
+// 614 GFLOP/s fp32 matrix peak) and kLatencyUs the latency-bound floor, so a
+// short last batch costs less than a full one.  Split partials cost
 // 2 * splits * M * N * 4 bytes at kFinishBytesPerUs.  The constants were
-// fitted to a tile/split sweep of the AlexNet convolutions on MI355X; they
-// pick within a few percent of the best measured configuration.
+// fitted to a sweep of every split count of the AlexNet convolutions on
+// MI355X: the choices are within 1 % of the best measured configurations.
 constexpr double kCuFlopsPerUs = 614.4e3;
-constexpr double kLatencyUs = 3.0;
-constexpr double kFinishBytesPerUs = 1.0e6;
+constexpr double kLatencyUs = 2.0;
+constexpr double kFinishBytesPerUs = 3.0e6;
 static double est_us(uint32_t M, uint32_t N, uint32_t kdim, const TileCfg& c, int occ,
                      bool partials) {
-  const double cus = num_cus();
-  const double tiles = double(cdiv(M, c.MT)) * cdiv(N, c.NT);
-  const double cap = cus * occ;
-  const double kps = double(cdiv(kdim, c.KT)) / c.splits;
+  const uint32_t cus = uint32_t(num_cus());
+  const uint32_t tiles = cdiv(M, uint32_t(c.MT)) * cdiv(N, uint32_t(c.NT));
+  const uint32_t n = cdiv(tiles * c.splits, cus);
+  const uint32_t full = n / uint32_t(occ), rem = n - full * uint32_t(occ);
+  const double kps = double(cdiv(kdim, uint32_t(c.KT))) / c.splits;
   const double tm = double(c.MT) * c.NT * c.KT * 2.0 / kCuFlopsPerUs;
-  const double W = tiles * c.splits;
-  const double full = std::floor(W / cap), rest = W - full * cap;
-  double T = kps * full * std::max(kLatencyUs, cap / cus * tm);
-  if (rest > 0) T += kps * std::max(kLatencyUs, rest / cus * tm);
+  double T = kps * full * std::max(kLatencyUs, occ * tm);
+  if (rem > 0) T += kps * std::max(kLatencyUs, rem * tm);
   if (partials) T += 2.0 * c.splits * double(M) * N * 4.0 / kFinishBytesPerUs;
   return T;
 }
@@ -1043,8 +1148,13 @@ static inline size_t al64(size_t n) { return (n + 63) & ~size_t(63); }
 
 static bool split_nchw(const float* part, const float* bias, float* out, uint32_t M, uint32_t N,
                        uint32_t HW, uint32_t splits, uint32_t act) {
-  hipLaunchKernelGGL(k_splitk_nchw, dim3(cdiv(size_t(M) * N, 256)), dim3(256), 0, stream(), part,
-                     bias, out, M, N, HW, splits, act);
+  if (N % 4 == 0 && aligned16(part))
+    hipLaunchKernelGGL(k_splitk_nchw4, dim3(cdiv(size_t(M) * (N / 4), 256)), dim3(256), 0,
+                       stream(), reinterpret_cast<const f4*>(part), bias, out, M, N, HW, splits,
+                       act);
+  else
+    hipLaunchKernelGGL(k_splitk_nchw, dim3(cdiv(size_t(M) * N, 256)), dim3(256), 0, stream(),
+                       part, bias, out, M, N, HW, splits, act);
   return check_launch("splitk_nchw");
 }
 
@@ -1132,8 +1242,14 @@ bool gemm(const float* a, const float* b, float* c, uint32_t M, uint32_t K, uint
     else
       ok = tiles_dispatch(cfg, GemmRun<true, true>{ap, bp, out, M, K, N, cfg.splits, lda, ldb, kdA, kdB});
     if (ok && cfg.splits > 1) {
-      hipLaunchKernelGGL(k_splitk_sum, dim3(cdiv(size_t(M) * N, 256)), dim3(256), 0, stream(),
-                         out, c, M * N, cfg.splits);
+      const uint32_t n = M * N;
+      if (n % 4 == 0 && aligned16(out) && aligned16(c))
+        hipLaunchKernelGGL(k_splitk_sum4, dim3(cdiv(n / 4, 256u)), dim3(256), 0, stream(),
+                           reinterpret_cast<const f4*>(out), reinterpret_cast<f4*>(c), n / 4,
+                           cfg.splits);
+      else
+        hipLaunchKernelGGL(k_splitk_sum, dim3(cdiv(n, 256u)), dim3(256), 0, stream(), out, c, n,
+                           cfg.splits);
       ok = check_launch("splitk_sum");
     }
   }
@@ -1409,9 +1525,7 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
                      4.0 * (double(npix) * OCp + double(g.B) * g.H * g.W * Cp + double(g.OC) * KK * Cp));
       ok = tiles_dispatch(dwc, DwRun{gn, xn, part, g, dwc.splits, dwT});
       if (ok) {
-        hipLaunchKernelGGL(k_dw_final, dim3(cdiv(size_t(g.OC) * KK * Cp, 64)), dim3(1024), 0,
-                           stream(), part, dw, g.OC, g.C, KK, Cp, dwc.splits, dwT ? 1u : 0u);
-        ok = check_launch("dw_final");
+        ok = dw_final(part, dw, g.OC, g.C, KK, Cp, dwc.splits, dwT);
       }
     }
     if (!ok) return false;
