@@ -123,7 +123,8 @@ struct LoaderBase {
   bool act;
   __device__ __forceinline__ void base_init(int tid) {
     lds0 = St::lds_off(tid);
-    wbase = St::lds_off(tid & ~63);
+    // Wave-uniform, so M0 of the direct loads is set with scalar arithmetic.
+    wbase = __builtin_amdgcn_readfirstlane(St::lds_off(tid & ~63));
     act = St::active(tid);
   }
   __device__ __forceinline__ void store(float* S, const f4 (&r)[Q]) const {
@@ -259,10 +260,14 @@ struct LdPixRK : LoaderBase<Stage<R, KT, false>> {
     uint32_t gridW, gridHW, N, kdim, n;
     FastDiv dGridHW, dGridW, dInner, dK;  // dInner: KK (blocked) or Cp (flat)
   };
+  // FAST (blocked order, forward or stride-1 dX): the K tile's tap and
+  // channel block are wave-uniform, so a quad's source offset is a per-quad
+  // constant qbase plus a uniform tap term -- no per-tile multiplies.
+  static constexpr bool FAST = BLK && (FWD || S1);
   BRes b;
   uint32_t srcH, srcW, Cp, k, s, kdim, kq;
   FastDiv dInner, dK;
-  uint32_t pbase[Q];
+  uint32_t pbase[Q], qbase[Q];
   int r0[Q], c0[Q];
   __device__ __forceinline__ void init(const Params& P, uint32_t row0, int tid) {
     this->base_init(tid);
@@ -293,6 +298,9 @@ struct LdPixRK : LoaderBase<Stage<R, KT, false>> {
       }
       // A row past the grid gets an origin no tap can bring into the image.
       if (n >= P.N) r0[i] = FWD ? -(1 << 20) : (1 << 20);
+      // Offset of tap (0, 0), channel kq, modulo 2^32 (the origin may lie
+      // in the padding); only in-image taps are ever used.
+      qbase[i] = (pbase[i] + uint32_t(r0[i]) * P.srcW + uint32_t(c0[i])) * P.Cp + kq;
     }
   }
   __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
@@ -309,6 +317,23 @@ struct LdPixRK : LoaderBase<Stage<R, KT, false>> {
     for (int i = 0; i < Q; ++i) b.ld4_lds(off[i], S + this->wbase + i * St::DLDS);
   }
   __device__ __forceinline__ void offsets(uint32_t kt, uint32_t (&o)[Q]) const {
+    if constexpr (FAST) {
+      const uint32_t cb = fdiv(kt, dInner);
+      const uint32_t khw = kt - cb * dInner.d;
+      const uint32_t kh = fdiv(khw, dK);
+      const uint32_t kw = khw - kh * k;
+      const bool kok = cb * kCB < Cp;  // Cp % kCB == 0: the whole tile or none
+      const uint32_t tap = (kh * srcW + kw) * Cp;
+      const uint32_t toff = FWD ? cb * kCB + tap : cb * kCB - tap;
+#pragma unroll
+      for (int i = 0; i < Q; ++i) {
+        const int h = FWD ? r0[i] + int(kh) : r0[i] - int(kh);
+        const int w = FWD ? c0[i] + int(kw) : c0[i] - int(kw);
+        const bool ok = kok && uint32_t(h) < srcH && uint32_t(w) < srcW;
+        o[i] = ok ? qbase[i] + toff : kOob;
+      }
+      return;
+    }
     uint32_t khw, ch;
     bool kok;
     if (BLK) {
@@ -738,6 +763,7 @@ __global__ void __launch_bounds__(256)
   const uint32_t c = blockIdx.x;
   const float* p = part + size_t(c) * rows;
   float s = 0.f;
+#pragma unroll 8
   for (uint32_t r = threadIdx.x; r < rows; r += 256) s += p[r];
   s = wave_reduce(s);
   if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = s;
