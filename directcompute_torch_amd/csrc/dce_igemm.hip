@@ -683,6 +683,11 @@ __global__ void __launch_bounds__(kThreads)
 // out[((b*HW) + p)*Cp + c] = (c < C) ? in[(b*C + c)*HW + p] masked : 0.
 // Block: 32 channels x 64 pixels through LDS.  dbPart[c][b*npb + block]: the
 // masked values of channel c summed over the block's 64 pixels.
+// Loads are 16-byte quads of 4 pixels of one channel row and stores 16-byte
+// quads of 4 channels of one pixel (Cp % 4 == 0 keeps those aligned).  Plane
+// rows of odd length leave the load quads only 4-byte aligned; the GPU runs
+// with unaligned access enabled.  A quad that would cross the end of its row
+// is read dword by dword.
 __global__ void __launch_bounds__(256)
     k_to_nhwc(const float* __restrict__ in, const float* __restrict__ y, float* __restrict__ out,
               float* __restrict__ dbPart, uint32_t C, uint32_t HW, uint32_t Cp, uint32_t npb,
@@ -696,28 +701,36 @@ __global__ void __launch_bounds__(256)
   const uint32_t c0 = (rest % ncb) * 32, p0 = pb * 64, b = rest / ncb;
   const int tid = threadIdx.x;
   // Branch-free loads through buffer resources (elements outside the tile's
-  // channels / pixels read at kOob, i.e. zero): all sixteen of a thread's
-  // loads are in flight together.  Callers admit tensors below kOob floats.
+  // channels / pixels read at kOob, i.e. zero): all of a thread's loads are
+  // in flight together.  Callers admit tensors below kOob floats.
   BRes bi, by;
   const uint32_t n = nB * C * HW;
   bi.init(in, n);
   by.init(y ? y : in, n);
-  float v[8], m[8];
+  const int pq = tid & 15;  // pixel quad of the load phase
+  f4 v[2], m[2];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int e = tid + 256 * j;
-    const int cl = e >> 6, pl = e & 63;
-    const uint32_t c = c0 + cl, p = p0 + pl;
-    const uint32_t off = (c < C && p < HW) ? (b * C + c) * HW + p : kOob;
-    v[j] = bi.ld1(off);
-    m[j] = y ? by.ld1(off) : 1.f;
+  for (int j = 0; j < 2; ++j) {
+    const uint32_t c = c0 + (tid >> 4) + 16 * j, p = p0 + 4 * pq;
+    const uint32_t row = (b * C + c) * HW;
+    if (c < C && p + 3 < HW) {
+      v[j] = bi.ld4(row + p);
+      m[j] = y ? by.ld4(row + p) : f4{1.f, 1.f, 1.f, 1.f};
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t off = (c < C && p + e < HW) ? row + p + e : kOob;
+        v[j][e] = bi.ld1(off);
+        m[j][e] = y ? by.ld1(off) : 1.f;
+      }
+    }
   }
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int e = tid + 256 * j;
-    // ReLU mask: y <= 0 zeroes the gradient (a NaN y keeps it).
-    t[e >> 6][e & 63] = m[j] <= 0.f ? 0.f : v[j];
-  }
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      // ReLU mask: y <= 0 zeroes the gradient (a NaN y keeps it).
+      t[(tid >> 4) + 16 * j][4 * pq + e] = m[j][e] <= 0.f ? 0.f : v[j][e];
   __syncthreads();
   if (dbPart != nullptr) {
     // 8 lanes per channel, 8 pixels each, then a fixed butterfly.
@@ -729,12 +742,13 @@ __global__ void __launch_bounds__(256)
     if (part == 0 && c0 + cl < C)
       dbPart[size_t(c0 + cl) * nB * npb + size_t(b) * npb + pb] = s;
   }
+  const int cq = tid & 7;  // channel quad of the store phase
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int e = tid + 256 * j;
-    const int pl = e >> 5, cl = e & 31;
-    const uint32_t c = c0 + cl, p = p0 + pl;
-    if (p < HW && c < Cp) out[(size_t(b) * HW + p) * Cp + c] = t[cl][pl];
+  for (int j = 0; j < 2; ++j) {
+    const int pl = (tid >> 3) + 32 * j;
+    const uint32_t c = c0 + 4 * cq, p = p0 + pl;
+    const f4 q = {t[4 * cq][pl], t[4 * cq + 1][pl], t[4 * cq + 2][pl], t[4 * cq + 3][pl]};
+    if (p < HW && c < Cp) *reinterpret_cast<f4*>(out + (size_t(b) * HW + p) * Cp + c) = q;
   }
 }
 
