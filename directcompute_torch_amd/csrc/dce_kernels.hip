@@ -1686,6 +1686,95 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// Forward band: output rows [o0, o0 + RB) (RB even) of plane (n, c).  LDS
+// cell (i, j) = x[o0*S - p + i][j - p] (window R x LW, zero outside the
+// plane); output block (2a, 2b) reads the (S + K) x (S + K) window at
+// (2a*S, 2b*S).  Taps are summed in (fh, fw) order and the bias added last,
+// as in the generic kernel.  An output pair inside its row is one 8-byte
+// store (4-byte aligned for rows of odd length: unaligned access is on).
+template <int K, int S, bool V4>
+__global__ void __launch_bounds__(256)
+    k_dw_fwd_band(const float* __restrict__ x, const float* __restrict__ f,
+                  const float* __restrict__ bias, float* __restrict__ y, uint32_t C, uint32_t H,
+                  uint32_t W, uint32_t OH, uint32_t OW, uint32_t p, uint32_t RB, uint32_t nb,
+                  uint32_t nbands, uint32_t LR, uint32_t LW, uint32_t BW, uint32_t nx,
+                  FastDiv dLW, FastDiv dNb, FastDiv dBW) {
+  constexpr int XW = S + K;
+  __shared__ __attribute__((aligned(16))) float sd[kDwBand];
+  BRes bx;
+  bx.init(x, nx);
+  DwRegs<V4, kDwRegs> v;
+  auto decode = [&](uint32_t band, uint32_t& plane, uint32_t& o0) {
+    plane = fdiv(band, dNb);
+    o0 = (band - plane * nb) * RB;
+  };
+  auto win = [&](uint32_t o0) {
+    DwWin w;
+    w.R = LR;
+    w.LW = LW;
+    w.rb = int(o0 * S) - int(p);
+    w.cb = -int(p);
+    return w;
+  };
+  const int lo = DwRegs<V4, kDwRegs>::shift(win(0).cb);
+  uint32_t band = blockIdx.x;
+  if (band < nbands) {
+    uint32_t plane, o0;
+    decode(band, plane, o0);
+    v.load(bx, plane * H * W, H, W, win(o0), dLW);
+  }
+  for (; band < nbands; band += gridDim.x) {
+    uint32_t plane, o0;
+    decode(band, plane, o0);
+    const uint32_t c = plane % C;
+    __syncthreads();  // the previous band's LDS reads are done
+    v.store(sd, LR, LW);
+    __syncthreads();
+    if (band + gridDim.x < nbands) {
+      uint32_t pn, on;
+      decode(band + gridDim.x, pn, on);
+      v.load(bx, pn * H * W, H, W, win(on), dLW);
+    }
+    float w[K * K];
+#pragma unroll
+    for (int t = 0; t < K * K; ++t) w[t] = f[c * K * K + t];
+    const float bc = bias[c];
+    const uint32_t o1 = min(o0 + RB, OH);
+    float* yp = y + size_t(plane) * OH * OW;
+    const uint32_t items = ((o1 - o0 + 1) / 2) * BW;
+    for (uint32_t e = threadIdx.x; e < items; e += 256) {
+      const uint32_t a = fdiv(e, dBW), b2 = e - a * BW;
+      float win_[XW][XW];
+#pragma unroll
+      for (int i = 0; i < XW; ++i)
+#pragma unroll
+        for (int j = 0; j < XW; ++j) win_[i][j] = sd[(2 * a * S + i) * LW + 2 * b2 * S + j + lo];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const uint32_t oh = o0 + 2 * a + r;
+        float o[2];
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+          float acc = 0.f;
+#pragma unroll
+          for (int fh = 0; fh < K; ++fh)
+#pragma unroll
+            for (int fw = 0; fw < K; ++fw) acc += win_[r * S + fh][cc * S + fw] * w[fh * K + fw];
+          o[cc] = acc + bc;
+        }
+        if (oh < o1) {
+          float* row = yp + size_t(oh) * OW + 2 * b2;
+          if (2 * b2 + 1 < OW) {
+            *reinterpret_cast<f2*>(row) = f2{o[0], o[1]};
+          } else {
+            row[0] = o[0];
+          }
+        }
+      }
+    }
+  }
+}
+
 // dW / db partials.  Block (y, c) walks the bands (image n, output rows
 // [o0, o0 + RB), RB even) of channel c for n = y, y + gridDim.x, ...:
 //   LDS x cell (i, j) = x[o0*S - p + i][j - p]      (LXR x LXW, zero outside)
@@ -1809,6 +1898,23 @@ static DwBand dw_band_input(const DwGeom& g) {
   b.R = g.s == 1 ? RB + K : RB / 2 + WR;
   return b;
 }
+static DwBand dw_band_fwd(const DwGeom& g) {
+  DwBand b{0, 0, 0, 0, 0, false};
+  if (!dw_band_ok(g)) return b;
+  const uint32_t K = g.kH, S = g.s, BW = (g.OW + 1) / 2;
+  b.LW = (2 * BW - 1) * S + K;
+  // Quad windows when x rows are 4-aligned: the stored window starts at the
+  // 4-aligned column left of -p.
+  b.v4 = g.W % 4 == 0;
+  if (b.v4) b.LW = round4(b.LW + uint32_t(-int(g.p) & 3));
+  const uint32_t rows = kDwBand / b.LW;  // window rows that fit
+  uint32_t RB = rows >= K ? ((rows - K) / S + 1) & ~1u : 0;
+  if (RB < 2) return DwBand{0, 0, 0, 0, 0, false};
+  RB = std::min(RB, (g.OH + 1) & ~1u);
+  b.RB = RB;
+  b.R = (RB - 1) * S + K;
+  return b;
+}
 static DwBand dw_band_filter(const DwGeom& g) {
   DwBand b{0, 0, 0, 0, 0, false};
   if (!dw_band_ok(g)) return b;
@@ -1843,6 +1949,36 @@ static bool sh_dw_fwd(const Dispatch& d) {
   DwGeom g = dw_geom(d);
   if (!dw_ok(g, "depthwise_conv_forward")) return true;
   uint32_t total = g.B * g.C * g.OH * g.OW;
+  const Buf x = S(d, 0), f = S(d, 1), bias = S(d, 2), y = U(d, 0);
+  const DwBand bb = dw_band_fwd(g);
+  const uint32_t nx = g.B * g.C * g.H * g.W;
+  if (bb.RB && covers(x, nx) && covers(f, uint64_t(g.C) * g.kH * g.kW) && covers(bias, g.C) &&
+      covers(y, total)) {
+    const uint32_t nb = cdiv(g.OH, bb.RB), nbands = g.B * g.C * nb;
+    const uint32_t BW = (g.OW + 1) / 2;
+    const FastDiv fLW = make_fastdiv(bb.v4 ? bb.LW / 4 : bb.LW), fNb = make_fastdiv(nb),
+                  fBW = make_fastdiv(BW);
+    // One resident round of blocks, each walking bands with a grid stride.
+#define DCE_DWF_V(K, SS, V)                                                                      \
+  {                                                                                             \
+    const uint32_t blocks = std::min<uint32_t>(                                                 \
+        nbands, uint32_t(num_cus()) * blocks_per_cu(k_dw_fwd_band<K, SS, V>, 256));             \
+    hipLaunchKernelGGL((k_dw_fwd_band<K, SS, V>), dim3(blocks), dim3(256), 0, stream(), x.p,     \
+                       f.p, bias.p, y.p, g.C, g.H, g.W, g.OH, g.OW, g.p, bb.RB, nb, nbands,      \
+                       bb.R, bb.LW, BW, nx, fLW, fNb, fBW);                                      \
+  }
+#define DCE_DWF(K, SS)                                                                           \
+  if (g.kH == K && g.s == SS) {                                                                 \
+    if (bb.v4)                                                                                  \
+      DCE_DWF_V(K, SS, true)                                                                    \
+    else                                                                                        \
+      DCE_DWF_V(K, SS, false)                                                                   \
+  }
+    DCE_DWF(3, 1) DCE_DWF(3, 2) DCE_DWF(5, 1) DCE_DWF(5, 2)
+#undef DCE_DWF
+#undef DCE_DWF_V
+    return check_launch("depthwise_conv_forward");
+  }
   hipLaunchKernelGGL(k_dw_fwd, dim3(cdiv(total, 256)), dim3(256), 0, stream(), S(d, 0), S(d, 1),
                      S(d, 2), U(d, 0), g, total);
   return check_launch("depthwise_conv_forward");
