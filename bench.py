@@ -131,7 +131,7 @@ def build_alexnet(nn, params):
     return AlexNet()
 
 
-def cpu_baseline(sample=64):
+def cpu_baseline(sample=256):
     """Time the float64 oracle on the same train step for `sample` images."""
     from oracle import models as OM
     threads = os.cpu_count() or 1
@@ -599,7 +599,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample", type=int, default=64)
+    ap.add_argument("--cpu-sample", type=int, default=256)
     ap.add_argument("--suite", choices=["train", "memory", "configs"], default="train",
                     help="train: the AlexNet-224 b128 train step (default, one JSON line); "
                          "memory: the backward memory-bound kernels, one JSON line each; "
