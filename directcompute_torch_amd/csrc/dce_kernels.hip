@@ -1583,15 +1583,21 @@ struct DwS2 {
 //          block (2a, 2b) reads the (K+1) x (K+1) window at (2a, 2b).
 //   S = 2: LDS cell (i, j) = dy[r0/2 + ph + JMIN + i][ph + JMIN + j]; output
 //          block (2a, 2b) reads the WR x WR window at (a, b).
-// Taps are summed in (fh, fw) order for every output, as the generic kernel.
-template <int K, int S, int PODD, bool V4>
+// A thread takes 2 rows x CW columns (CW / 2 such blocks side by side, one
+// register window of WR x WC) and stores each row's CW outputs as one
+// vector store when they lie in the row (unaligned for rows whose length is
+// not a multiple of CW: unaligned access is on).  Taps are summed in
+// (fh, fw) order for every output, as the generic kernel.
+template <int K, int S, int PODD, bool V4, int CW>
 __global__ void __launch_bounds__(256)
     k_dw_bwd_input_band(const float* __restrict__ dy, const float* __restrict__ f,
                         float* __restrict__ dx, uint32_t C, uint32_t H, uint32_t W, uint32_t OH,
                         uint32_t OW, uint32_t p, uint32_t RB, uint32_t nb, uint32_t nbands,
                         uint32_t LR, uint32_t LW, uint32_t BW, uint32_t ndy, FastDiv dLW,
                         FastDiv dNb, FastDiv dBW) {
+  static_assert(CW == 2 || CW == 4, "2 or 4 columns per thread");
   constexpr int WR = S == 1 ? K + 1 : DwS2<K, PODD>::WR;
+  constexpr int WC = S == 1 ? WR + CW - 2 : WR + CW / 2 - 1;
   __shared__ __attribute__((aligned(16))) float sd[kDwBand];
   BRes bd;
   bd.init(dy, ndy);
@@ -1638,47 +1644,50 @@ __global__ void __launch_bounds__(256)
     for (int t = 0; t < K * K; ++t) w[t] = f[c * K * K + t];
     const uint32_t r1 = min(r0 + RB, H);
     float* dxp = dx + size_t(plane) * H * W;
-    const bool evenW = (W & 1) == 0;
     const uint32_t items = ((r1 - r0 + 1) / 2) * BW;
     for (uint32_t e = threadIdx.x; e < items; e += 256) {
-      const uint32_t a = fdiv(e, dBW), b2 = e - a * BW;
-      const uint32_t i0 = S == 1 ? 2 * a : a, j0 = S == 1 ? 2 * b2 : b2;
-      float win_[WR][WR];
+      const uint32_t a = fdiv(e, dBW), q = e - a * BW;
+      const uint32_t i0 = S == 1 ? 2 * a : a, j0 = S == 1 ? CW * q : (CW / 2) * q;
+      float win_[WR][WC];
 #pragma unroll
       for (int i = 0; i < WR; ++i)
 #pragma unroll
-        for (int j = 0; j < WR; ++j) win_[i][j] = sd[(i0 + i) * LW + j0 + j + lo];
+        for (int j = 0; j < WC; ++j) win_[i][j] = sd[(i0 + i) * LW + j0 + j + lo];
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
         const uint32_t ih = r0 + 2 * a + r;
-        float o[2];
+        float o[CW];
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
+        for (int cc = 0; cc < CW; ++cc) {
+          // Column c2 of 2x2 block sb, whose window starts co columns in.
+          const int sb = cc / 2, c2 = cc % 2, co = S == 1 ? 2 * sb : sb;
           float acc = 0.f;
 #pragma unroll
           for (int fh = 0; fh < K; ++fh) {
 #pragma unroll
             for (int fw = 0; fw < K; ++fw) {
               if (S == 1) {
-                acc += win_[r + K - 1 - fh][cc + K - 1 - fw] * w[fh * K + fw];
-              } else if (((r + PODD - fh) & 1) == 0 && ((cc + PODD - fw) & 1) == 0) {
+                acc += win_[r + K - 1 - fh][co + c2 + K - 1 - fw] * w[fh * K + fw];
+              } else if (((r + PODD - fh) & 1) == 0 && ((c2 + PODD - fw) & 1) == 0) {
                 constexpr int J = DwS2<K, PODD>::JMIN;
-                acc += win_[(r + PODD - fh) / 2 - J][(cc + PODD - fw) / 2 - J] * w[fh * K + fw];
+                acc += win_[(r + PODD - fh) / 2 - J][co + (c2 + PODD - fw) / 2 - J] * w[fh * K + fw];
               }
             }
           }
           o[cc] = acc;
         }
-        // The pair goes out as one 8-byte store when rows have even length
-        // (the pair is then aligned and inside the row): a wave writes one
-        // contiguous run instead of two interleaved half-density ones.
         if (ih < r1) {
-          float* row = dxp + size_t(ih) * W + 2 * b2;
-          if (evenW) {
-            *reinterpret_cast<f2*>(row) = f2{o[0], o[1]};
+          const uint32_t col = CW * q;
+          float* row = dxp + size_t(ih) * W + col;
+          if (col + CW - 1 < W) {
+            if constexpr (CW == 4)
+              *reinterpret_cast<f4*>(row) = f4{o[0], o[1], o[2], o[3]};
+            else
+              *reinterpret_cast<f2*>(row) = f2{o[0], o[1]};
           } else {
-            row[0] = o[0];
-            if (2 * b2 + 1 < W) row[1] = o[1];
+#pragma unroll
+            for (int cc = 0; cc < CW; ++cc)
+              if (col + cc < W) row[cc] = o[cc];
           }
         }
       }
@@ -1876,12 +1885,15 @@ static bool dw_band_ok(const DwGeom& g) {
   if (g.H + 2 * g.p < g.kH || g.OH != (g.H + 2 * g.p - g.kH) / g.s + 1) return false;
   return uint64_t(g.B) * g.C * g.H * g.W < kOob && uint64_t(g.B) * g.C * g.OH * g.OW < kOob;
 }
+// The dX band kernels take kDwCW output columns per thread.
+constexpr uint32_t kDwCW = 4;
 static DwBand dw_band_input(const DwGeom& g) {
   DwBand b{0, 0, 0, 0, 0, false};
   if (!dw_band_ok(g)) return b;
-  const uint32_t K = g.kH, BW = (g.W + 1) / 2;
+  const uint32_t K = g.kH, BW = (g.W + kDwCW - 1) / kDwCW;
   const uint32_t WR = g.s == 1 ? K + 1 : ((1 + (g.p & 1)) / 2 + (K - (g.p & 1)) / 2 + 1);
-  b.LW = g.s == 1 ? 2 * BW + K : BW + WR;
+  // Columns the last thread's window reaches (plus one).
+  b.LW = g.s == 1 ? kDwCW * BW + K : (kDwCW / 2) * BW + WR;
   // Quad windows when dy rows are 4-aligned: the stored window starts at the
   // 4-aligned column left of the logical start cb.
   b.v4 = g.OW % 4 == 0;
@@ -1994,7 +2006,7 @@ static bool sh_dw_bwd_input(const Dispatch& d) {
   if (bb.RB && covers(dy, uint64_t(g.B) * g.C * g.OH * g.OW) &&
       covers(f, uint64_t(g.C) * g.kH * g.kW) && covers(dx, total)) {
     const uint32_t nb = cdiv(g.H, bb.RB), nbands = g.B * g.C * nb;
-    const uint32_t BW = (g.W + 1) / 2, ndy = g.B * g.C * g.OH * g.OW;
+    const uint32_t BW = (g.W + kDwCW - 1) / kDwCW, ndy = g.B * g.C * g.OH * g.OW;
     const FastDiv fLW = make_fastdiv(bb.v4 ? bb.LW / 4 : bb.LW), fNb = make_fastdiv(nb),
                   fBW = make_fastdiv(BW);
     const uint32_t podd = g.p & 1;
@@ -2003,8 +2015,8 @@ static bool sh_dw_bwd_input(const Dispatch& d) {
 #define DCE_DWI_V(K, SS, PO, V)                                                                   \
   {                                                                                              \
     const uint32_t blocks = std::min<uint32_t>(                                                  \
-        nbands, uint32_t(num_cus()) * blocks_per_cu(k_dw_bwd_input_band<K, SS, PO, V>, 256));   \
-    hipLaunchKernelGGL((k_dw_bwd_input_band<K, SS, PO, V>), dim3(blocks), dim3(256), 0,          \
+        nbands, uint32_t(num_cus()) * blocks_per_cu(k_dw_bwd_input_band<K, SS, PO, V, kDwCW>, 256));   \
+    hipLaunchKernelGGL((k_dw_bwd_input_band<K, SS, PO, V, kDwCW>), dim3(blocks), dim3(256), 0,          \
                        stream(), dy.p, f.p, dx.p, g.C, g.H, g.W, g.OH, g.OW, g.p, bb.RB, nb,     \
                        nbands, bb.R, bb.LW, BW, ndy, fLW, fNb, fBW);                             \
   }
