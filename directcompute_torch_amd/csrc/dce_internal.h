@@ -104,6 +104,23 @@ struct BRes {
 };
 
 // ---------------------------------------------------------------------------
+// 8- and 16-byte accesses at 4-byte alignment (rows of odd length).  The GPU
+// runs with unaligned memory access enabled, so these stay single
+// global_load/store_dwordx2/x4 instructions; memcpy states the alignment
+// without the undefined behaviour of a misaligned vector-pointer cast.
+// ---------------------------------------------------------------------------
+template <class V>
+__device__ __forceinline__ V ldu(const void* p) {
+  V v;
+  __builtin_memcpy(&v, p, sizeof(V));
+  return v;
+}
+template <class V>
+__device__ __forceinline__ void stu(void* p, const V& v) {
+  __builtin_memcpy(p, &v, sizeof(V));
+}
+
+// ---------------------------------------------------------------------------
 // Streaming accesses: 16-byte loads and stores with the nontemporal cache
 // policy, for passes over more data than the 256 MB MALL (Infinity Cache)
 // holds.  On MI355X they sustain more HBM bandwidth than the default policy

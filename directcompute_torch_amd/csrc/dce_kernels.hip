@@ -913,11 +913,11 @@ __global__ void k_maxpool_fwd_k(const float* __restrict__ x, float* __restrict__
     for (int a = 0; a < K; ++a) {
       const float* r = x + base + a * W;
       if constexpr (K == 2) {
-        const f2 q = *reinterpret_cast<const f2*>(r);
+        const f2 q = ldu<f2>(r);
         v[a][0] = q[0];
         v[a][1] = q[1];
       } else {
-        const f4 q = *reinterpret_cast<const f4*>(r);
+        const f4 q = ldu<f4>(r);
 #pragma unroll
         for (int b = 0; b < K; ++b) v[a][b] = q[b];
       }
@@ -1065,8 +1065,8 @@ __global__ void k_maxpool_bwd_blk(const float* __restrict__ dz, const uint32_t* 
       const int oh = int(a) - (NW - 1) + wa;
       const bool hok = oh >= 0 && oh < int(OH);
       const uint32_t o = (plane * OH + uint32_t(hok ? oh : 0)) * OW + ps;
-      const u2 iv = *reinterpret_cast<const u2*>(idx + o);
-      const f2 dv = *reinterpret_cast<const f2*>(dz + o);
+      const u2 iv = ldu<u2>(idx + o);
+      const f2 dv = ldu<f2>(dz + o);
       id[wa][0] = (hok && lok) ? (li ? iv[1] : iv[0]) : 0xFFFFFFFFu;
       id[wa][1] = (hok && rok) ? (ri ? iv[1] : iv[0]) : 0xFFFFFFFFu;
       v[wa][0] = li ? dv[1] : dv[0];
@@ -1107,7 +1107,7 @@ __global__ void k_maxpool_bwd_blk(const float* __restrict__ dz, const uint32_t* 
     // (aligned for rows of even length; PAIR also takes odd ones).
     float* row = dx + (plane * H + ih) * W + b * S;
     if (S == 2 && b * S + 1 < W && (PAIR || (W & 1) == 0)) {
-      *reinterpret_cast<f2*>(row) = f2{o[0], o[S - 1]};
+      stu(row, f2{o[0], o[S - 1]});
     } else {
 #pragma unroll
       for (int c = 0; c < S; ++c)
@@ -1681,9 +1681,9 @@ __global__ void __launch_bounds__(256)
           float* row = dxp + size_t(ih) * W + col;
           if (col + CW - 1 < W) {
             if constexpr (CW == 4)
-              *reinterpret_cast<f4*>(row) = f4{o[0], o[1], o[2], o[3]};
+              stu(row, f4{o[0], o[1], o[2], o[3]});
             else
-              *reinterpret_cast<f2*>(row) = f2{o[0], o[1]};
+              stu(row, f2{o[0], o[1]});
           } else {
 #pragma unroll
             for (int cc = 0; cc < CW; ++cc)
@@ -1774,7 +1774,7 @@ __global__ void __launch_bounds__(256)
         if (oh < o1) {
           float* row = yp + size_t(oh) * OW + 2 * b2;
           if (2 * b2 + 1 < OW) {
-            *reinterpret_cast<f2*>(row) = f2{o[0], o[1]};
+            stu(row, f2{o[0], o[1]});
           } else {
             row[0] = o[0];
           }
