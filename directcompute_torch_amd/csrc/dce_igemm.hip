@@ -681,24 +681,31 @@ __global__ void __launch_bounds__(kThreads)
 // filter re-layouts, split-K sums.
 // ---------------------------------------------------------------------------
 // out[((b*HW) + p)*Cp + c] = (c < C) ? in[(b*C + c)*HW + p] masked : 0.
-// Block: 32 channels x 64 pixels through LDS.  dbPart[c][b*npb + block]: the
-// masked values of channel c summed over the block's 64 pixels.
+// Block: CB channels x PB = 2048 / CB pixels through LDS (CB = 16 for tensors
+// of at most 16 channels, 32 otherwise, so few-channel tensors do not leave
+// half the block idle).  dbPart[c][b*npb + block]: the masked values of
+// channel c summed over the block's pixels.
 // Loads are 16-byte quads of 4 pixels of one channel row and stores 16-byte
 // quads of 4 channels of one pixel (Cp % 4 == 0 keeps those aligned).  Plane
 // rows of odd length leave the load quads only 4-byte aligned; the GPU runs
 // with unaligned access enabled.  A quad that would cross the end of its row
 // is read dword by dword.
+template <int CB>
 __global__ void __launch_bounds__(256)
     k_to_nhwc(const float* __restrict__ in, const float* __restrict__ y, float* __restrict__ out,
               float* __restrict__ dbPart, uint32_t C, uint32_t HW, uint32_t Cp, uint32_t npb,
               uint32_t ncb, uint32_t nB) {
-  __shared__ float t[32][65];
+  constexpr int PB = 2048 / CB, PQ = PB / 4;  // pixels per block, pixel quads per row
+  constexpr int CR = 256 / PQ;                // channel rows per load pass
+  constexpr int PR = 256 / (CB / 4);          // pixels per store pass
+  static_assert(CR * 2 == CB && PR * 2 == PB, "two load and two store passes");
+  __shared__ float t[CB][PB + 1];
   // 1-D grid over (pixel block, channel block, image), pixel block fastest,
   // in XCD-contiguous order: a plane row's neighbouring blocks share its
   // partial cache lines.
   const uint32_t id = xcd_block_id();
   const uint32_t pb = id % npb, rest = id / npb;
-  const uint32_t c0 = (rest % ncb) * 32, p0 = pb * 64, b = rest / ncb;
+  const uint32_t c0 = (rest % ncb) * CB, p0 = pb * PB, b = rest / ncb;
   const int tid = threadIdx.x;
   // Branch-free loads through buffer resources (elements outside the tile's
   // channels / pixels read at kOob, i.e. zero): all of a thread's loads are
@@ -707,11 +714,11 @@ __global__ void __launch_bounds__(256)
   const uint32_t n = nB * C * HW;
   bi.init(in, n);
   by.init(y ? y : in, n);
-  const int pq = tid & 15;  // pixel quad of the load phase
+  const int pq = tid % PQ;  // pixel quad of the load phase
   f4 v[2], m[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const uint32_t c = c0 + (tid >> 4) + 16 * j, p = p0 + 4 * pq;
+    const uint32_t c = c0 + tid / PQ + CR * j, p = p0 + 4 * pq;
     const uint32_t row = (b * C + c) * HW;
     if (c < C && p + 3 < HW) {
       v[j] = bi.ld4(row + p);
@@ -730,22 +737,22 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int e = 0; e < 4; ++e)
       // ReLU mask: y <= 0 zeroes the gradient (a NaN y keeps it).
-      t[(tid >> 4) + 16 * j][4 * pq + e] = m[j][e] <= 0.f ? 0.f : v[j][e];
+      t[tid / PQ + CR * j][4 * pq + e] = m[j][e] <= 0.f ? 0.f : v[j][e];
   __syncthreads();
-  if (dbPart != nullptr) {
-    // 8 lanes per channel, 8 pixels each, then a fixed butterfly.
+  if (dbPart != nullptr && tid < 8 * CB) {
+    // 8 lanes per channel, PB / 8 pixels each, then a fixed butterfly.
     const int cl = tid >> 3, part = tid & 7;
     float s = 0.f;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) s += t[cl][part * 8 + q];
+    for (int q = 0; q < PB / 8; ++q) s += t[cl][part * (PB / 8) + q];
     s = group8_reduce(s);
     if (part == 0 && c0 + cl < C)
       dbPart[size_t(c0 + cl) * nB * npb + size_t(b) * npb + pb] = s;
   }
-  const int cq = tid & 7;  // channel quad of the store phase
+  const int cq = tid % (CB / 4);  // channel quad of the store phase
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int pl = (tid >> 3) + 32 * j;
+    const int pl = tid / (CB / 4) + PR * j;
     const uint32_t c = c0 + 4 * cq, p = p0 + pl;
     const f4 q = {t[4 * cq][pl], t[4 * cq + 1][pl], t[4 * cq + 2][pl], t[4 * cq + 3][pl]};
     if (p < HW && c < Cp) *reinterpret_cast<f4*>(out + (size_t(b) * HW + p) * Cp + c) = q;
@@ -1314,11 +1321,18 @@ static bool to_nhwc_masked(const float* in, const float* y, float* out, float* d
                        HW, Cp, npix, make_fastdiv(HW));
     return check_launch("to_nhwc");
   }
-  const uint32_t npb = cdiv(HW, 64);
-  if (npbOut) *npbOut = npb;
-  const uint32_t ncb = cdiv(Cp, 32);
-  hipLaunchKernelGGL(k_to_nhwc, dim3(npb * ncb * B), dim3(256), 0, stream(), in, y, out, dbPart,
-                     C, HW, Cp, npb, ncb, B);
+  if (Cp <= 16) {
+    const uint32_t npb = cdiv(HW, 128);
+    if (npbOut) *npbOut = npb;
+    hipLaunchKernelGGL(k_to_nhwc<16>, dim3(npb * B), dim3(256), 0, stream(), in, y, out, dbPart,
+                       C, HW, Cp, npb, 1u, B);
+  } else {
+    const uint32_t npb = cdiv(HW, 64);
+    if (npbOut) *npbOut = npb;
+    const uint32_t ncb = cdiv(Cp, 32);
+    hipLaunchKernelGGL(k_to_nhwc<32>, dim3(npb * ncb * B), dim3(256), 0, stream(), in, y, out,
+                       dbPart, C, HW, Cp, npb, ncb, B);
+  }
   return check_launch("to_nhwc");
 }
 
@@ -1549,7 +1563,7 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
   uint32_t npbGot = npb;
   if (!to_nhwc_masked(dy, y, gn, dbPart, g.B, g.OC, OHW, &npbGot)) return false;
   if (db) {
-    hipLaunchKernelGGL(k_rowsum, dim3(g.OC), dim3(256), 0, stream(), dbPart, db, g.B * npb);
+    hipLaunchKernelGGL(k_rowsum, dim3(g.OC), dim3(256), 0, stream(), dbPart, db, g.B * npbGot);
     if (!check_launch("bias_grad")) return false;
   }
   if (dw) {
