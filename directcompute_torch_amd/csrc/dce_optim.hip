@@ -106,13 +106,18 @@ __device__ __forceinline__ void apply_chunk(const Table& t, const Op& op, int ti
         V[j][e] = d;
       }
     }
+    // Nontemporal stores only when several streams are written: with one
+    // written stream (SGD: 115 -> 110 us over AlexNet's 61 M parameters) the
+    // default policy stores faster, with three (Adam: 293 vs 330 us) the
+    // streaming one does.
+    constexpr bool NTS = NT && (WRITE & (WRITE - 1)) != 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t i = c0 + (j * 256 + threadIdx.x) * 4;
-      if (WRITE & 1) st4s<NT>(w + i, W[j]);
-      if (WRITE & 2) st4s<NT>(g + i, G[j]);
-      if (WRITE & 4) st4s<NT>(m + i, M[j]);
-      if (WRITE & 8) st4s<NT>(v + i, V[j]);
+      if (WRITE & 1) st4s<NTS>(w + i, W[j]);
+      if (WRITE & 2) st4s<NTS>(g + i, G[j]);
+      if (WRITE & 4) st4s<NTS>(m + i, M[j]);
+      if (WRITE & 8) st4s<NTS>(v + i, V[j]);
     }
     return;
   }
