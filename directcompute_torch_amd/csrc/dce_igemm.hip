@@ -602,15 +602,21 @@ __global__ void __launch_bounds__(kThreads)
             const typename EPI::Params pe, TileGrid tg, uint32_t ktiles, uint32_t splits) {
   using SA = typename LA::St;
   using SB = typename LB::St;
-  constexpr int WGM = MT >= 64 ? 2 : 1, WGN = 4 / WGM;  // wave grid
+  // WKS (narrow tiles, MT <= 32 with KT = 64): the four waves split every K
+  // tile, each computing the whole MT x NT tile over its own 16-k slice, and
+  // the four partial tiles are added in wave order at the end.  A barrier
+  // then covers four times the MFMA work of the 1 x 4 wave grid at KT = 16.
+  constexpr bool WKS = MT <= 32 && KT == 64;
+  constexpr int WGM = WKS ? 1 : (MT >= 64 ? 2 : 1), WGN = WKS ? 1 : 4 / WGM;  // wave grid
   constexpr int WM = MT / WGM, WN = NT / WGN, FM = WM / 16, FN = WN / 16;
   static_assert(FM >= 1 && FN >= 1 && WM % 16 == 0 && WN % 16 == 0, "tile too small");
   __shared__ __attribute__((aligned(16))) float As[2 * SA::SIZE];
   __shared__ __attribute__((aligned(16))) float Bs[2 * SB::SIZE];
+  static_assert(!WKS || 3 * FM * FN * 256 <= 2 * SB::SIZE, "wave partials fit the B stages");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WGN, wn = wave % WGN;
+  const int wm = WKS ? 0 : wave / WGN, wn = WKS ? 0 : wave % WGN;  // WKS: every wave the whole tile
   uint32_t mt, nt, z;
   tile_coords(tg, mt, nt, z);
   const uint32_t m0 = mt * MT, n0 = nt * NT;
@@ -651,8 +657,7 @@ __global__ void __launch_bounds__(kThreads)
     }
     const float* Ac = As + cur * SA::SIZE;
     const float* Bc = Bs + cur * SB::SIZE;
-#pragma unroll
-    for (int ks = 0; ks < KT; ks += 16) {
+    auto slice = [&](int ks) {
       f4 af[FM], bf[FN];
 #pragma unroll
       for (int i = 0; i < FM; ++i) af[i] = SA::frag(Ac, wm * WM + i * 16, r, g, ks);
@@ -665,6 +670,12 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
           for (int j = 0; j < FN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][s], bf[j][s], acc[i][j], 0, 0, 0);
+    };
+    if constexpr (WKS) {
+      slice(16 * wave);
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < KT; ks += 16) slice(ks);
     }
     if (more) {
       if constexpr (!DA) la.store(As + (cur ^ 1) * SA::SIZE, ra);
@@ -672,6 +683,25 @@ __global__ void __launch_bounds__(kThreads)
     }
     if constexpr (DA || DB) __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+  }
+  if constexpr (WKS) {
+    // Waves 1-3 park their partial tiles in the (now idle) B stages; wave 0
+    // adds them in wave order and stores the tile.
+    f4* red = reinterpret_cast<f4*>(Bs);
+    if (wave != 0) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) red[((wave - 1) * FM * FN + i * FN + j) * 64 + lane] = acc[i][j];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int w = 0; w < 3; ++w)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] += red[(w * FM * FN + i * FN + j) * 64 + lane];
   }
   EPI::template store<MT, NT, FM, FN>(pe, acc, m0, n0, z, wm, wn, lane);
 }
@@ -1101,9 +1131,16 @@ static double est_us(uint32_t M, uint32_t N, uint32_t kdim, const TileCfg& c, in
 // launch writes the final output (no partial buffer).
 template <class OccFn>
 static TileCfg choose(const char* var, uint32_t M, uint32_t N, uint32_t kdim, uint32_t max_splits,
-                      bool dense_out, OccFn&& occ, bool kt16_only = false) {
+                      bool dense_out, OccFn&& occ, bool kt16_only = false,
+                      bool narrow_ksplit = false) {
   TileCfg c{pick_tile_m(M), pick_tile(N), 16, 1};
   if (kt16_only && c.MT < 64) c.NT = 128;  // the pixel GEMMs' narrow tiles are 128 or 256 wide
+  if (narrow_ksplit && c.MT < 64) {
+    // Narrow tiles with the waves splitting K: 64 columns (a wave then holds
+    // the whole tile's accumulators; 128 would cost registers and occupancy).
+    c.NT = 64;
+    c.KT = 64;
+  }
   const uint32_t ktiles = cdiv(kdim, uint32_t(c.KT));
   if (tune_override(var, c)) {
     if (kt16_only) c.KT = 16;
@@ -1143,7 +1180,8 @@ static bool launch(const typename LA::Params& pa, const typename LB::Params& pb,
 }
 
 // Dispatch a functor over the (MT, NT) tile shapes: 64/128 square-ish tiles at
-// two KT depths and the narrow MT = 16/32 tiles at KT = 16.
+// two KT depths and the narrow MT = 16/32 tiles at KT = 16 (1 x 4 wave grid)
+// or KT = 64 (waves split the K tile).
 template <class F>
 static bool tiles_dispatch(const TileCfg& c, F&& f) {
 #define DCE_T(a, b, k) \
@@ -1151,6 +1189,7 @@ static bool tiles_dispatch(const TileCfg& c, F&& f) {
   DCE_T(128, 128, 32) DCE_T(128, 64, 32) DCE_T(64, 128, 32) DCE_T(64, 64, 32)
   DCE_T(128, 128, 16) DCE_T(128, 64, 16) DCE_T(64, 128, 16) DCE_T(64, 64, 16)
   DCE_T(32, 128, 16) DCE_T(32, 64, 16) DCE_T(16, 128, 16) DCE_T(16, 64, 16)
+  DCE_T(32, 128, 64) DCE_T(32, 64, 64) DCE_T(16, 128, 64) DCE_T(16, 64, 64)
 #undef DCE_T
   set_error("igemm: unsupported tile %dx%dx%d", c.MT, c.NT, c.KT);
   return false;
@@ -1186,6 +1225,7 @@ static int tiles_occ(const TileCfg& c, const F& f) {
   DCE_T(128, 128, 32) DCE_T(128, 64, 32) DCE_T(64, 128, 32) DCE_T(64, 64, 32)
   DCE_T(128, 128, 16) DCE_T(128, 64, 16) DCE_T(64, 128, 16) DCE_T(64, 64, 16)
   DCE_T(32, 128, 16) DCE_T(32, 64, 16) DCE_T(16, 128, 16) DCE_T(16, 64, 16)
+  DCE_T(32, 128, 64) DCE_T(32, 64, 64) DCE_T(16, 128, 64) DCE_T(16, 64, 64)
 #undef DCE_T
   return 1;
 }
@@ -1535,12 +1575,14 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
     dwT = tile_fill(taps, g.OC) > tile_fill(g.OC, taps) * 1.25;
     const uint32_t dM = dwT ? taps : g.OC, dN = dwT ? g.OC : taps;
     const uint32_t ntiles = cdiv(dM, pick_tile_m(dM)) * cdiv(dN, pick_tile(dN));
-    dwc = choose("DCE_TUNE_DW", dM, dN, npix, ntiles <= 4 ? 1024 : 256, false,
-                 [&](const TileCfg& t) {
-                   DwRun r{};
-                   r.trans = dwT;
-                   return tiles_occ(t, r);
-                 });
+    dwc = choose(
+        "DCE_TUNE_DW", dM, dN, npix, ntiles <= 4 ? 1024 : 256, false,
+        [&](const TileCfg& t) {
+          DwRun r{};
+          r.trans = dwT;
+          return tiles_occ(t, r);
+        },
+        false, true);
     nP = al64(size_t(dwc.splits) * g.OC * KK * Cp);
   }
   if (dx) {

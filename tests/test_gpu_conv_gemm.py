@@ -239,6 +239,24 @@ def test_forced_narrow_tiles(eng, monkeypatch, pix_cfg, dense_cfg):
         test_matmul_alloc(eng, 5, 7, 3, flags)
 
 
+KSPLIT_CFGS = [f"{mt},{nt},64,{sp}" for mt in (16, 32) for nt in (64, 128) for sp in (1, 3)]
+
+
+@pytest.mark.parametrize("cfg", KSPLIT_CFGS)
+def test_forced_narrow_ksplit_tiles(eng, monkeypatch, cfg):
+    """The narrow tiles whose four waves split each 64-deep K tile and add
+    their partial tiles at the end, forced on the dW and dense GEMMs (the
+    pixel GEMMs take K tiles of 16 only), with several M tiles and split-K."""
+    for var in ("DCE_TUNE_DW", "DCE_TUNE_GEMM"):
+        monkeypatch.setenv(var, cfg)
+    _conv_case(eng, 2, 16, 14, 14, 20, 3, 2, 1, 1)   # OC 20: two 16-row tiles
+    _conv_case(eng, 2, 48, 10, 10, 40, 3, 1, 1, 1)   # OC 40: two 32-row tiles
+    _conv_case(eng, 3, 3, 17, 19, 8, 5, 1, 2, 1)     # C = 3 padded to 4, OC 8
+    for flags in range(4):
+        test_matmul_alloc(eng, 37, 129, 70, flags)
+        test_matmul_alloc(eng, 5, 7, 3, flags)
+
+
 def test_linear_tile_order(eng, monkeypatch):
     """DCE_XCD=0 (plain tile order) gives the same results as the default
     XCD-contiguous order."""
