@@ -303,6 +303,58 @@ __global__ void k_softmax_rows(Buf in, Buf out, Buf labels, float* rowLoss, uint
     rowLoss[row] = -(ld(in, base + label) - mx - logf(s));
   }
 }
+// Rows of at most 64 * NV elements: each lane loads its NV values once (all
+// loads in flight together), then the same max, sum (in the same order) and
+// outputs as k_softmax_rows, so the results are identical.
+template <int NV>
+__global__ void k_softmax_rows_reg(Buf in, Buf out, Buf labels, float* rowLoss, uint32_t B,
+                                   uint32_t K, int writeSoftmax) {
+  const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= B) return;
+  const uint32_t base = row * K;
+  float v[NV];
+#pragma unroll
+  for (int u = 0; u < NV; ++u) {
+    const uint32_t j = lane + 64 * u;
+    v[u] = j < K ? ld(in, base + j) : -1e30f;
+  }
+  float mx = -1e30f;
+#pragma unroll
+  for (int u = 0; u < NV; ++u)
+    if (lane + 64 * u < K) mx = fmaxf(mx, v[u]);
+  mx = wave_reduce(mx, OpMaxR());
+  float s = 0.f;
+#pragma unroll
+  for (int u = 0; u < NV; ++u)
+    if (lane + 64 * u < K) s += expf(v[u] - mx);
+  s = wave_reduce(s);
+  if (writeSoftmax) {
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+      const uint32_t j = lane + 64 * u;
+      if (j < K) st(out, base + j, expf(v[u] - mx) / s);
+    }
+  }
+  if (rowLoss && lane == 0) {
+    const uint32_t label = uint32_t(ld(labels, row));
+    rowLoss[row] = -(ld(in, base + label) - mx - logf(s));
+  }
+}
+// Launch the register form for rows of up to 1024 elements.
+static void softmax_rows(Buf in, Buf out, Buf labels, float* rowLoss, uint32_t B, uint32_t K,
+                         int writeSoftmax) {
+  const dim3 grid(cdiv(B, 4)), blk(256);
+  if (K <= 256)
+    hipLaunchKernelGGL(k_softmax_rows_reg<4>, grid, blk, 0, stream(), in, out, labels, rowLoss,
+                       B, K, writeSoftmax);
+  else if (K <= 1024)
+    hipLaunchKernelGGL(k_softmax_rows_reg<16>, grid, blk, 0, stream(), in, out, labels, rowLoss,
+                       B, K, writeSoftmax);
+  else
+    hipLaunchKernelGGL(k_softmax_rows, grid, blk, 0, stream(), in, out, labels, rowLoss, B, K,
+                       writeSoftmax);
+}
 __global__ void k_mean_rows(const float* rowLoss, Buf loss, uint32_t B) {
   __shared__ double sh[4];
   double s = 0;
@@ -313,8 +365,7 @@ __global__ void k_mean_rows(const float* rowLoss, Buf loss, uint32_t B) {
 static bool sh_softmax(const Dispatch& d) {
   uint32_t B = CU(d, 0), K = CU(d, 1);
   if (!B || !K) return true;
-  hipLaunchKernelGGL(k_softmax_rows, dim3(cdiv(B, 4)), dim3(256), 0, stream(), S(d, 0), U(d, 0),
-                     Buf{nullptr, 0}, nullptr, B, K, 1);
+  softmax_rows(S(d, 0), U(d, 0), Buf{nullptr, 0}, nullptr, B, K, 1);
   return check_launch("softmax");
 }
 static bool sh_loss(const Dispatch& d) {
@@ -322,8 +373,7 @@ static bool sh_loss(const Dispatch& d) {
   if (!B || !K) return true;
   float* rl = workspace(B);
   if (!rl) return false;
-  hipLaunchKernelGGL(k_softmax_rows, dim3(cdiv(B, 4)), dim3(256), 0, stream(), S(d, 0),
-                     Buf{nullptr, 0}, S(d, 1), rl, B, K, 0);
+  softmax_rows(S(d, 0), Buf{nullptr, 0}, S(d, 1), rl, B, K, 0);
   hipLaunchKernelGGL(k_mean_rows, dim3(1), dim3(256), 0, stream(), rl, U(d, 0), B);
   return check_launch("loss");
 }
