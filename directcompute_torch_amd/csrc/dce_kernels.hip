@@ -1864,6 +1864,12 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// LDS floats of the filter kernels' dy band window: a full band for stride 1
+// (bands of up to 73 rows at 56 wide: one band per 56x56 image, 52 -> 47 us
+// at MobileNetV2's s1 shape), half of one for stride 2 (the larger x window
+// is the limit there, and more LDS per block cost occupancy: 73 -> 77 us).
+__host__ __device__ constexpr uint32_t dw_gband(uint32_t S) { return S == 1 ? kDwBand : kDwBand / 2; }
+
 // dW / db partials.  Block (y, c) walks the bands (image n, output rows
 // [o0, o0 + RB), RB even) of channel c for n = y, y + gridDim.x, ...:
 //   LDS x cell (i, j) = x[o0*S - p + i][j - p]      (LXR x LXW, zero outside)
@@ -1881,14 +1887,14 @@ __global__ void __launch_bounds__(256)
   constexpr int T = K * K + 1;
   constexpr int XW = S + K;  // x window edge under a 2 x 2 dy block
   __shared__ __attribute__((aligned(16))) float sx[kDwBand];
-  __shared__ __attribute__((aligned(16))) float sg[kDwBand / 2];
+  __shared__ __attribute__((aligned(16))) float sg[dw_gband(S)];
   __shared__ float red[4][T];
   const uint32_t c = blockIdx.y;
   BRes bx, bg;
   bx.init(x, B * C * H * W);
   bg.init(dy, B * C * OH * OW);
   DwRegs<V4, kDwRegs> xv;
-  DwRegs<V4, kDwRegs / 2> gv;
+  DwRegs<V4, dw_gband(S) / 256> gv;
   const int lox = DwRegs<V4, kDwRegs>::shift(-int(p));
   // The channel's B * nb (image, band) units, split evenly over the pieces.
   const uint32_t units = B * nb;
@@ -2036,8 +2042,8 @@ static DwBand dw_band_filter(const DwGeom& g) {
     b.LW = round4(b.LW + uint32_t(-int(g.p) & 3));
   else
     b.LW = S == 2 ? round4(b.LW) : b.LW;  // stride-2 phase-split rows need LW % 4 == 0
-  if (b.LW2 * 2 > kDwBand / 2 || uint64_t(b.LW) * (S + K) > kDwBand) return DwBand{0, 0, 0, 0, 0, false};
-  const uint32_t byg = (kDwBand / 2) / b.LW2;
+  if (b.LW2 * 2 > dw_gband(S) || uint64_t(b.LW) * (S + K) > kDwBand) return DwBand{0, 0, 0, 0, 0, false};
+  const uint32_t byg = dw_gband(S) / b.LW2;
   const uint32_t byx = (kDwBand / b.LW - K) / S + 1;
   uint32_t RB = std::min(byg, byx) & ~1u;
   if (RB < 2) return DwBand{0, 0, 0, 0, 0, false};
