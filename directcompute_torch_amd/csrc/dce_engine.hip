@@ -721,7 +721,7 @@ void* ConvForwardFused(void* x, void* filters, void* bias, uint32_t batch, uint3
   // that the forward builds anyway; ConvBackwardFused reuses and releases it.
   void* keep = nullptr;
   if (pIm2col) {
-    keep = create_buffer(nullptr, uint32_t(nhwc_floats(batch, inC, inH, inW)));
+    keep = create_buffer(nullptr, uint32_t(xcopy_floats(g)));
     if (!keep) {
       release_buffer(out);
       return nullptr;
@@ -740,7 +740,7 @@ void* ConvForwardFused(void* x, void* filters, void* bias, uint32_t batch, uint3
     K->meta[1] = inC;
     K->meta[2] = inH;
     K->meta[3] = inW;
-    K->meta[4] = pad4(inC);
+    K->meta[4] = xcopy_tag(g);
     *pIm2col = keep;
   }
   return out;
@@ -775,7 +775,7 @@ void ConvBackwardFused(void* gradOut, void* fwdOut, void* x, void* filters, void
         Buffer* Kb = static_cast<Buffer*>(im2col);
         if (Kb->magic == kMagicLive && Kb->tag == kNhwcTag && Kb->meta[0] == batch &&
             Kb->meta[1] == inC && Kb->meta[2] == inH && Kb->meta[3] == inW &&
-            Kb->meta[4] == pad4(inC) && Kb->count >= nhwc_floats(batch, inC, inH, inW))
+            Kb->meta[4] == xcopy_tag(g) && Kb->count >= xcopy_floats(g))
           xn = Kb->ptr;
       }
       bool wantW = wReq && pDFilters, wantB = bReq && pDBias, wantX = xReq && pDInput;

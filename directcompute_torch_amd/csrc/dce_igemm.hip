@@ -500,6 +500,128 @@ struct LdXTapKR : LoaderBase<Stage<R, KT, true, false>> {
 };
 
 // ---------------------------------------------------------------------------
+// Channel-packed source for convolutions over C < 4 channels: x copied by
+// k_to_pk to [B][Hp][Wp][C] (Hp = H + 2p, Wp = W + 2p, zero border), and the
+// unpadded tap order t = kh * kC + j with kC = k * C, j = kw * C + c (kdim =
+// k * kC; the NHWC layout would pad C to 4 and waste up to 3/4 of the
+// tap axis).  For every output pixel a kernel row's kC values are contiguous,
+// so a quad of 4 consecutive t is one 16-byte load (4-byte aligned) unless it
+// runs past the end of its kernel row (j + 3 >= kC): its tail then comes from
+// a second load at the next kernel row, shifted so that element e lines up
+// (from t's row origin + rowp - (kC - j)).  Tail elements past the last
+// kernel row read as zeros.
+// ---------------------------------------------------------------------------
+struct PkParams {
+  const float* src;
+  uint32_t rowp, imgp, C, k, s, kC, kdim;  // rowp = Wp * C, imgp = Hp * Wp * C
+  uint32_t OW, OHW, npix, n;               // n: floats in the copy
+  FastDiv dOHW, dOW, dKC;
+};
+
+// Offset of output pixel pix's window origin in the packed copy.
+__device__ __forceinline__ uint32_t pk_origin(const PkParams& P, uint32_t pix) {
+  const uint32_t bb = fdiv(pix, P.dOHW);
+  const uint32_t rem = pix - bb * P.OHW;
+  const uint32_t oh = fdiv(rem, P.dOW);
+  const uint32_t ow = rem - oh * P.OW;
+  return bb * P.imgp + oh * P.s * P.rowp + ow * P.s * P.C;
+}
+
+// Quad of taps t..t+3 at a window origin: o1 = t's offset from the origin,
+// o2 = the shifted next-row offset (kOob: none), m = elements left in t's row.
+__device__ __forceinline__ f4 pk_quad(const BRes& b, bool ok, uint32_t org, uint32_t o1,
+                                      uint32_t o2, uint32_t m) {
+  f4 v = b.ld4(ok && o1 != kOob ? org + o1 : kOob);
+  if (m < 4) {
+    const f4 w = b.ld4(ok && o2 != kOob ? org + o2 : kOob);
+#pragma unroll
+    for (int e = 1; e < 4; ++e)
+      if (uint32_t(e) >= m) v[e] = w[e];
+  }
+  return v;
+}
+
+// Row-origin offsets of tap t (shared by the two loaders below).
+__device__ __forceinline__ void pk_tap(const PkParams& P, uint32_t t, uint32_t& o1, uint32_t& o2,
+                                       uint32_t& m) {
+  if (t >= P.kdim) {
+    o1 = o2 = kOob;
+    m = 4;
+    return;
+  }
+  const uint32_t kh = fdiv(t, P.dKC), j = t - kh * P.kC;
+  m = P.kC - j;
+  o1 = kh * P.rowp + j;
+  o2 = (m < 4 && kh + 1 < P.k) ? (kh + 1) * P.rowp - m : kOob;
+}
+
+// Forward B operand (ROWK): rows = output pixels, k = packed taps.  All quads
+// of a thread share their taps, so the tap split is done once per K tile.
+template <int R, int KT>
+struct LdPkRK : LoaderBase<Stage<R, KT, false>> {
+  static_assert(!Stage<R, KT, false>::PART, "pixel operands fill the workgroup");
+  using St = Stage<R, KT, false>;
+  static constexpr bool KROW = false;
+  using LoaderBase<St>::Q;
+  using Params = PkParams;
+  BRes b;
+  PkParams P;
+  uint32_t kq;
+  uint32_t org[Q];
+  bool ok[Q];
+  __device__ __forceinline__ void init(const Params& p, uint32_t row0, int tid) {
+    this->base_init(tid);
+    P = p;
+    b.init(p.src, p.n);
+    kq = St::qk(tid, 0);
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+      const uint32_t pix = row0 + St::qrow(tid, i);
+      ok[i] = pix < p.npix;
+      org[i] = ok[i] ? pk_origin(p, pix) : 0u;
+    }
+  }
+  __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
+    uint32_t o1, o2, m;
+    pk_tap(P, kt * KT + kq, o1, o2, m);
+#pragma unroll
+    for (int i = 0; i < Q; ++i) r[i] = pk_quad(b, ok[i], org[i], o1, o2, m);
+  }
+};
+
+// dW operand (KROW): rows = packed taps, k = output pixels.  A thread's quads
+// keep their taps for the whole K loop; the pixel walks.
+template <int R, int KT>
+struct LdPkKR : LoaderBase<Stage<R, KT, true, false>> {
+  using St = Stage<R, KT, true, false>;
+  static constexpr bool KROW = true;
+  using LoaderBase<St>::Q;
+  using Params = PkParams;
+  BRes b;
+  PkParams P;
+  uint32_t kk0;
+  uint32_t o1[Q], o2[Q], m[Q];
+  __device__ __forceinline__ void init(const Params& p, uint32_t row0, int tid) {
+    this->base_init(tid);
+    P = p;
+    b.init(p.src, p.n);
+    kk0 = St::qk(tid, 0);
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+      pk_tap(p, this->act ? row0 + St::qrow_data(tid, i) : p.kdim, o1[i], o2[i], m[i]);
+    }
+  }
+  __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+      const uint32_t pix = kt * KT + kk0 + St::DK * i;
+      const bool ok = pix < P.npix;
+      r[i] = pk_quad(b, ok, ok ? pk_origin(P, pix) : 0u, o1[i], o2[i], m[i]);
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
 // Epilogues.  Lane l of wave (wm, wn) holds, for MFMA block (i, j) and
 // register v, C[m0 + wm*16FM + 16i + 4(l/16) + v][n0 + wn*16FN + 16j + l%16].
 // ---------------------------------------------------------------------------
@@ -636,25 +758,9 @@ __global__ void __launch_bounds__(kThreads)
     for (int j = 0; j < FN; ++j) acc[i][j] = zero4();
 
   constexpr bool DA = LA::LDSD, DB = LB::LDSD;
-  if (kb < ke) {
-    if constexpr (DA) la.issue_lds(kb, As); else la.load(kb, ra);
-    if constexpr (DB) lb.issue_lds(kb, Bs); else lb.load(kb, rb);
-    if constexpr (!DA) la.store(As, ra);
-    if constexpr (!DB) lb.store(Bs, rb);
-  }
-  if constexpr (DA || DB) __builtin_amdgcn_s_waitcnt(0);  // the direct loads have landed
-  __syncthreads();
-
   const int r = lane & 15, g = lane >> 4;
-  for (uint32_t kt = kb; kt < ke; ++kt) {
-    const int cur = int(kt - kb) & 1;
-    const bool more = kt + 1 < ke;
-    // Next tile: register staging, or straight into the other LDS stage (its
-    // readers finished before the previous barrier).
-    if (more) {
-      if constexpr (DA) la.issue_lds(kt + 1, As + (cur ^ 1) * SA::SIZE); else la.load(kt + 1, ra);
-      if constexpr (DB) lb.issue_lds(kt + 1, Bs + (cur ^ 1) * SB::SIZE); else lb.load(kt + 1, rb);
-    }
+  // MFMAs of the K tile in LDS stage `cur`.
+  auto compute = [&](int cur) {
     const float* Ac = As + cur * SA::SIZE;
     const float* Bc = Bs + cur * SB::SIZE;
     auto slice = [&](int ks) {
@@ -677,6 +783,26 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
       for (int ks = 0; ks < KT; ks += 16) slice(ks);
     }
+  };
+  if (kb < ke) {
+    if constexpr (DA) la.issue_lds(kb, As); else la.load(kb, ra);
+    if constexpr (DB) lb.issue_lds(kb, Bs); else lb.load(kb, rb);
+    if constexpr (!DA) la.store(As, ra);
+    if constexpr (!DB) lb.store(Bs, rb);
+  }
+  if constexpr (DA || DB) __builtin_amdgcn_s_waitcnt(0);  // the direct loads have landed
+  __syncthreads();
+
+  for (uint32_t kt = kb; kt < ke; ++kt) {
+    const int cur = int(kt - kb) & 1;
+    const bool more = kt + 1 < ke;
+    // Next tile: register staging, or straight into the other LDS stage (its
+    // readers finished before the previous barrier).
+    if (more) {
+      if constexpr (DA) la.issue_lds(kt + 1, As + (cur ^ 1) * SA::SIZE); else la.load(kt + 1, ra);
+      if constexpr (DB) lb.issue_lds(kt + 1, Bs + (cur ^ 1) * SB::SIZE); else lb.load(kt + 1, rb);
+    }
+    compute(cur);
     if (more) {
       if constexpr (!DA) la.store(As + (cur ^ 1) * SA::SIZE, ra);
       if constexpr (!DB) lb.store(Bs + (cur ^ 1) * SB::SIZE, rb);
@@ -828,14 +954,21 @@ __global__ void __launch_bounds__(256)
 // mode 0 (forward A): out[oc][kk] = w[oc][c][khw]   with c  = channel of kk
 // mode 1 (dX A):      out[c][kk]  = w[oc][c][khw]   with oc = channel of kk
 // where kk = khw*inner + ch (flat) or (cb*KK + khw)*kCB + ci, ch = cb*kCB + ci
-// (blocked).  Size rows * KK*inner, rows = OC (mode 0) or C (mode 1).
+// (blocked).  Rows are ld >= KK*inner floats apart, zero past KK*inner; size
+// rows * ld, rows = OC (mode 0) or C (mode 1).  The packed forward (C < 4
+// channels) uses the flat order with inner = C and ld = pad4(KK*C).
 __global__ void k_permute_w(const float* __restrict__ w, float* __restrict__ out, uint32_t OC,
-                            uint32_t C, uint32_t KK, uint32_t inner, int mode, int blocked) {
+                            uint32_t C, uint32_t KK, uint32_t inner, uint32_t ld, int mode,
+                            int blocked) {
   const uint32_t kdim = KK * inner;
   const uint32_t rows = mode == 0 ? OC : C;
   const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= rows * kdim) return;
-  const uint32_t r = i / kdim, kk = i - r * kdim;
+  if (i >= rows * ld) return;
+  const uint32_t r = i / ld, kk = i - r * ld;
+  if (kk >= kdim) {  // row pitch padding
+    out[i] = 0.f;
+    return;
+  }
   uint32_t khw, ch;
   if (blocked) {
     const uint32_t blk = kk / kCB, ci = kk - blk * kCB;
@@ -889,15 +1022,17 @@ __global__ void __launch_bounds__(256)
 // SL slice sums are then added in slice order through LDS, so the result is
 // deterministic.  SL (1, 4 or 16) is chosen from the quad count alone, which
 // keeps enough loads in flight when few quads take many splits.  Elements
-// i = 4q + j are stored in storage order of the partials; OC*KK*Cp is a
-// multiple of 4 because Cp is.  Padding channels (c >= C) are dropped.
+// i = 4q + j are stored in storage order of the partials; Cp is the channel
+// stride of the tap axis (pad4(C), or C for the packed layout), and each
+// split's partials start 4 * ceil(OC*KK*Cp / 4) floats apart.  Padding
+// channels (c >= C) and the tail past OC*KK*Cp are dropped.
 template <int SL>
 __global__ void __launch_bounds__(256)
     k_dw_final(const f4* __restrict__ part, float* __restrict__ dw, uint32_t OC, uint32_t C,
                uint32_t KK, uint32_t Cp, uint32_t splits, uint32_t trans) {
   constexpr uint32_t QB = 256 / SL;
   __shared__ f4 sh[SL][QB];
-  const uint32_t N = KK * Cp, nq = OC * (N / 4);
+  const uint32_t N = KK * Cp, total = OC * N, nq = (total + 3) / 4;
   const uint32_t lq = threadIdx.x % QB, w = threadIdx.x / QB;
   const uint32_t q = blockIdx.x * QB + lq;
   f4 s = {0.f, 0.f, 0.f, 0.f};
@@ -926,6 +1061,7 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const uint32_t i = 4 * q + j;
+    if (i >= total) break;
     uint32_t oc, n;
     if (trans) {
       n = i / OC;
@@ -949,7 +1085,7 @@ static uint32_t dw_final_slices(uint32_t nq, uint32_t splits) {
 
 static bool dw_final(const float* part, float* dw, uint32_t OC, uint32_t C, uint32_t KK,
                      uint32_t Cp, uint32_t splits, bool trans) {
-  const uint32_t nq = OC * (KK * Cp / 4), sl = dw_final_slices(nq, splits);
+  const uint32_t nq = cdiv(size_t(OC) * KK * Cp, 4), sl = dw_final_slices(nq, splits);
   const f4* p4 = reinterpret_cast<const f4*>(part);
   const uint32_t tr = trans ? 1u : 0u;
   if (sl == 1)
@@ -1380,6 +1516,48 @@ bool to_nhwc(const float* x, float* out, uint32_t B, uint32_t C, uint32_t H, uin
   return to_nhwc_masked(x, nullptr, out, nullptr, B, C, H * W, nullptr);
 }
 
+// Channel-packed, zero-padded copy (fewer than four channels): one thread per
+// padded pixel, out[((b*Hp + h)*Wp + w)*C + c] = x[b][c][h - p][w - p], zero
+// in the border.
+__global__ void k_to_pk(const float* __restrict__ x, float* __restrict__ out, uint32_t C,
+                        uint32_t H, uint32_t W, uint32_t p, uint32_t Hp, uint32_t Wp,
+                        uint32_t npix, FastDiv dWp, FastDiv dHp) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= npix) return;
+  const uint32_t t = fdiv(i, dWp), w = i - t * Wp;
+  const uint32_t b = fdiv(t, dHp), h = t - b * Hp;
+  const uint32_t ih = h - p, iw = w - p;  // wraps when in the border
+  const bool in = ih < H && iw < W;
+  const size_t plane = size_t(H) * W;
+  const size_t src = in ? (size_t(b) * C * H + ih) * W + iw : 0;
+  float* dst = out + size_t(i) * C;
+  for (uint32_t c = 0; c < C; ++c) dst[c] = in ? x[src + c * plane] : 0.f;
+}
+
+bool packed_x(const ConvGeom& g) { return g.C < 4; }
+
+size_t xcopy_floats(const ConvGeom& g) {
+  if (!packed_x(g)) return nhwc_floats(g.B, g.C, g.H, g.W);
+  return size_t(g.B) * (g.H + 2 * g.p) * (g.W + 2 * g.p) * g.C;
+}
+
+uint32_t xcopy_tag(const ConvGeom& g) { return packed_x(g) ? 0x10000u + g.p : pad4(g.C); }
+
+static bool to_pk(const float* x, float* out, const ConvGeom& g) {
+  const uint32_t Hp = g.H + 2 * g.p, Wp = g.W + 2 * g.p, npix = g.B * Hp * Wp;
+  ProfScope prof("nhwc", 0, 4.0 * (double(g.B) * g.C * g.H * g.W + double(npix) * g.C));
+  hipLaunchKernelGGL(k_to_pk, dim3(cdiv(npix, 256)), dim3(256), 0, stream(), x, out, g.C, g.H,
+                     g.W, g.p, Hp, Wp, npix, make_fastdiv(Wp), make_fastdiv(Hp));
+  return check_launch("to_pk");
+}
+
+static PkParams pk_params(const float* src, const ConvGeom& g) {
+  const uint32_t Hp = g.H + 2 * g.p, Wp = g.W + 2 * g.p, OHW = g.OH * g.OW, kC = g.k * g.C;
+  return PkParams{src, Wp * g.C, Hp * Wp * g.C, g.C, g.k, g.s, kC, g.k * kC, g.OW, OHW,
+                  g.B * OHW, uint32_t(xcopy_floats(g)), make_fastdiv(OHW), make_fastdiv(g.OW),
+                  make_fastdiv(kC)};
+}
+
 // ----------------------------------------------------------- conv forward
 // Output pixels as GEMM columns: split-K partials go to a row-major [M][N]
 // workspace and k_splitk_nchw finishes (bias, activation, NCHW scatter).
@@ -1440,17 +1618,57 @@ struct FwdRun {
   }
 };
 
+// Forward over the channel-packed copy (C < 4): K runs over the unpadded
+// taps (kh, kw, c), filters padded to pad4(KK * C) per row.
+struct FwdPkRun {
+  const float* wp;
+  const float* xp;
+  const float* bias;
+  float* y;
+  float* part;
+  ConvGeom g;
+  uint32_t act, splits;
+  template <int MT, int NT, int KT>
+  int occ(bool split) const {
+    using LA = LdDenseRK<MT, KT>;
+    using LB = LdPkRK<NT, KT>;
+    return split ? occupancy(k_igemm<MT, NT, KT, LA, LB, EpiRowMajor>)
+                 : occupancy(k_igemm<MT, NT, KT, LA, LB, EpiNCHW>);
+  }
+  template <int MT, int NT, int KT>
+  bool run() {
+    const uint32_t kdim = pad4(g.k * g.k * g.C);
+    const uint32_t OHW = g.OH * g.OW, N = g.B * OHW;
+    using LA = LdDenseRK<MT, KT>;
+    using LB = LdPkRK<NT, KT>;
+    const typename LA::Params pa{wp, kdim, g.OC, kdim, g.OC * kdim};
+    const PkParams pb = pk_params(xp, g);
+    const uint32_t kt = cdiv(kdim, KT);
+    if (splits > 1) {
+      const EpiRowMajor::Params pe{part, g.OC, N, N, g.OC * N};
+      return launch<MT, NT, KT, LA, LB, EpiRowMajor>(pa, pb, pe, g.OC, N, kt, splits,
+                                                    "conv_forward");
+    }
+    const EpiNCHW::Params pe{y, bias, g.OC, OHW, N, act, make_fastdiv(OHW)};
+    return launch<MT, NT, KT, LA, LB, EpiNCHW>(pa, pb, pe, g.OC, N, kt, 1, "conv_forward");
+  }
+};
+
 bool conv_forward(const float* x, float* x_nhwc_keep, const float* w, const float* bias,
                   float* y, const ConvGeom& g, uint32_t act) {
-  const uint32_t Cp = pad4(g.C), KK = g.k * g.k, kdim = KK * Cp;
-  const bool blk = blocked_k(Cp), s1 = g.s == 1;
-  const size_t nx = nhwc_floats(g.B, g.C, g.H, g.W);
+  const bool pk = packed_x(g);
+  const uint32_t Cp = pad4(g.C), KK = g.k * g.k, kdim = pk ? pad4(KK * g.C) : KK * Cp;
+  const bool blk = !pk && blocked_k(Cp), s1 = g.s == 1;
+  const size_t nx = xcopy_floats(g);
   const uint32_t N = g.B * g.OH * g.OW;
   if (!operand_fits(nx, "conv_forward") || !operand_fits(size_t(g.OC) * kdim, "conv_forward"))
     return false;
   const TileCfg cfg = choose(
       "DCE_TUNE_FWD", g.OC, N, kdim, 8, true,
-      [&](const TileCfg& t) { return conv_variant_occ<FwdRun>(s1, blk, t); }, true);
+      [&](const TileCfg& t) {
+        return pk ? tiles_occ16(t, FwdPkRun{}) : conv_variant_occ<FwdRun>(s1, blk, t);
+      },
+      true);
   const size_t nw = al64(size_t(g.OC) * kdim);
   const size_t nxs = x_nhwc_keep ? 0 : al64(nx);
   const size_t nP = cfg.splits > 1 ? size_t(cfg.splits) * g.OC * N : 0;
@@ -1459,16 +1677,18 @@ bool conv_forward(const float* x, float* x_nhwc_keep, const float* w, const floa
   float* wp = ws;
   float* xn = x_nhwc_keep ? x_nhwc_keep : ws + nw;
   float* part = ws + nw + nxs;
-  if (!to_nhwc(x, xn, g.B, g.C, g.H, g.W)) return false;
+  if (!(pk ? to_pk(x, xn, g) : to_nhwc(x, xn, g.B, g.C, g.H, g.W))) return false;
   hipLaunchKernelGGL(k_permute_w, dim3(cdiv(size_t(g.OC) * kdim, 256)), dim3(256), 0, stream(), w,
-                     wp, g.OC, g.C, KK, Cp, 0, blk ? 1 : 0);
+                     wp, g.OC, g.C, KK, pk ? g.C : Cp, kdim, 0, blk ? 1 : 0);
   if (!check_launch("permute_w")) return false;
   const double fl = 2.0 * g.OC * g.C * KK * double(g.B) * g.OH * g.OW;
   {
     ProfScope prof("conv_fwd", fl,
                    4.0 * (double(g.B) * g.C * g.H * g.W + double(g.B) * g.OC * g.OH * g.OW));
-    if (!conv_variant<FwdRun>(s1, blk, cfg, wp, xn, bias, y, part, g, act, cfg.splits))
-      return false;
+    const bool ok =
+        pk ? tiles_dispatch16(cfg, FwdPkRun{wp, xn, bias, y, part, g, act, cfg.splits})
+           : conv_variant<FwdRun>(s1, blk, cfg, wp, xn, bias, y, part, g, act, cfg.splits);
+    if (!ok) return false;
     if (cfg.splits > 1) return split_nchw(part, bias, y, g.OC, N, g.OH * g.OW, cfg.splits, act);
   }
   return true;
@@ -1485,27 +1705,40 @@ struct DwRun {
   ConvGeom g;
   uint32_t splits;
   bool trans;
+  bool pk;  // xn is the channel-packed copy: taps (kh, kw, c) with C unpadded
   template <int MT, int NT, int KT>
   int occ(bool) const {
+    if (pk)
+      return trans ? occupancy(k_igemm<MT, NT, KT, LdPkKR<MT, KT>, LdGradKR<NT, KT>, EpiRowMajor>)
+                   : occupancy(k_igemm<MT, NT, KT, LdGradKR<MT, KT>, LdPkKR<NT, KT>, EpiRowMajor>);
     return trans ? occupancy(k_igemm<MT, NT, KT, LdXTapKR<MT, KT>, LdGradKR<NT, KT>, EpiRowMajor>)
                  : occupancy(k_igemm<MT, NT, KT, LdGradKR<MT, KT>, LdXTapKR<NT, KT>, EpiRowMajor>);
   }
+  template <int MT, int NT, int KT, class LX>
+  bool go(const typename LX::Params& px, uint32_t N) {
+    const uint32_t OCp = pad4(g.OC), npix = g.B * g.OH * g.OW;
+    const GradKRParams pg{gn, OCp, npix, npix * OCp};
+    const uint32_t zs = 4 * cdiv(size_t(g.OC) * N, 4);  // split stride of the partials
+    if (trans) {
+      const EpiRowMajor::Params pe{part, N, g.OC, g.OC, zs};
+      return launch<MT, NT, KT, LX, LdGradKR<NT, KT>, EpiRowMajor>(
+          px, pg, pe, N, g.OC, cdiv(npix, KT), splits, "conv_backward_filter");
+    }
+    using LB = typename std::conditional<std::is_same<LX, LdPkKR<MT, KT>>::value, LdPkKR<NT, KT>,
+                                         LdXTapKR<NT, KT>>::type;
+    const EpiRowMajor::Params pe{part, g.OC, N, N, zs};
+    return launch<MT, NT, KT, LdGradKR<MT, KT>, LB, EpiRowMajor>(
+        pg, px, pe, g.OC, N, cdiv(npix, KT), splits, "conv_backward_filter");
+  }
   template <int MT, int NT, int KT>
   bool run() {
-    const uint32_t Cp = pad4(g.C), OCp = pad4(g.OC), KK = g.k * g.k, N = KK * Cp;
-    const uint32_t OHW = g.OH * g.OW, npix = g.B * OHW;
-    const GradKRParams pg{gn, OCp, npix, npix * OCp};
+    const uint32_t KK = g.k * g.k, OHW = g.OH * g.OW, npix = g.B * OHW;
+    if (pk) return go<MT, NT, KT, LdPkKR<MT, KT>>(pk_params(xn, g), KK * g.C);
+    const uint32_t Cp = pad4(g.C), N = KK * Cp;
     const XTapParams px{xn, g.H, g.W, Cp, g.k, g.s, g.p, g.OW, OHW, npix, N,
                         g.B * g.H * g.W * Cp, make_fastdiv(OHW), make_fastdiv(g.OW),
                         make_fastdiv(Cp), make_fastdiv(g.k)};
-    if (trans) {
-      const EpiRowMajor::Params pe{part, N, g.OC, g.OC, g.OC * N};
-      return launch<MT, NT, KT, LdXTapKR<MT, KT>, LdGradKR<NT, KT>, EpiRowMajor>(
-          px, pg, pe, N, g.OC, cdiv(npix, KT), splits, "conv_backward_filter");
-    }
-    const EpiRowMajor::Params pe{part, g.OC, N, N, g.OC * N};
-    return launch<MT, NT, KT, LdGradKR<MT, KT>, LdXTapKR<NT, KT>, EpiRowMajor>(
-        pg, px, pe, g.OC, N, cdiv(npix, KT), splits, "conv_backward_filter");
+    return go<MT, NT, KT, LdXTapKR<MT, KT>>(px, N);
   }
 };
 
@@ -1556,22 +1789,26 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
   const uint32_t Cp = pad4(g.C), OCp = pad4(g.OC), KK = g.k * g.k;
   const uint32_t OHW = g.OH * g.OW, npix = g.B * OHW, HW = g.H * g.W;
   if (!operand_fits(size_t(npix) * OCp, "conv_backward") ||
-      !operand_fits(nhwc_floats(g.B, g.C, g.H, g.W), "conv_backward") ||
+      !operand_fits(xcopy_floats(g), "conv_backward") ||
       !operand_fits(size_t(g.C) * KK * OCp, "conv_backward"))
     return false;
-  // Workspace carve-up: G (NHWC), db partials, x (NHWC) if not kept by the
-  // forward, dW split-K partials, dX filters, dX split-K partials.
+  // Workspace carve-up: G (NHWC), db partials, the copy of x if not kept by
+  // the forward, dW split-K partials, dX filters, dX split-K partials.
+  // Fewer than four input channels: x is channel-packed and the dW tap axis
+  // runs over KK * C unpadded taps (Cx = C), otherwise over KK * pad4(C).
+  const bool pk = packed_x(g);
+  const uint32_t Cx = pk ? g.C : Cp;
   const uint32_t npb = cdiv(OHW, 64);
   const size_t nG = al64(size_t(npix) * OCp);
   const size_t nDb = db ? al64(size_t(g.B) * npb * g.OC) : 0;
-  const size_t nX = (dw && !x_nhwc) ? al64(nhwc_floats(g.B, g.C, g.H, g.W)) : 0;
+  const size_t nX = (dw && !x_nhwc) ? al64(xcopy_floats(g)) : 0;
   TileCfg dwc{128, 128, 16, 1}, dxc{128, 128, 16, 1};
   size_t nP = 0, nW = 0, nQ = 0;
   bool dwT = false;
   if (dw) {
     // Orientation with the fuller tile grid; a grid of a few tiles gets more
     // split-K slices so that the whole chip works on it.
-    const uint32_t taps = KK * Cp;
+    const uint32_t taps = KK * Cx;
     dwT = tile_fill(taps, g.OC) > tile_fill(g.OC, taps) * 1.25;
     const uint32_t dM = dwT ? taps : g.OC, dN = dwT ? g.OC : taps;
     const uint32_t ntiles = cdiv(dM, pick_tile_m(dM)) * cdiv(dN, pick_tile(dN));
@@ -1580,10 +1817,11 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
         [&](const TileCfg& t) {
           DwRun r{};
           r.trans = dwT;
+          r.pk = pk;
           return tiles_occ(t, r);
         },
         false, true);
-    nP = al64(size_t(dwc.splits) * g.OC * KK * Cp);
+    nP = al64(size_t(dwc.splits) * 4 * cdiv(size_t(g.OC) * taps, 4));
   }
   if (dx) {
     const bool blk = blocked_k(OCp);
@@ -1611,7 +1849,7 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
   if (dw) {
     const float* xn = x_nhwc;
     if (!xn) {
-      if (!to_nhwc(x, xs, g.B, g.C, g.H, g.W)) return false;
+      if (!(pk ? to_pk(x, xs, g) : to_nhwc(x, xs, g.B, g.C, g.H, g.W))) return false;
       xn = xs;
     }
     bool ok;
@@ -1619,9 +1857,9 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
       const double fl = 2.0 * g.OC * g.C * KK * double(npix);
       ProfScope prof("conv_dw", fl,
                      4.0 * (double(npix) * OCp + double(g.B) * g.H * g.W * Cp + double(g.OC) * KK * Cp));
-      ok = tiles_dispatch(dwc, DwRun{gn, xn, part, g, dwc.splits, dwT});
+      ok = tiles_dispatch(dwc, DwRun{gn, xn, part, g, dwc.splits, dwT, pk});
       if (ok) {
-        ok = dw_final(part, dw, g.OC, g.C, KK, Cp, dwc.splits, dwT);
+        ok = dw_final(part, dw, g.OC, g.C, KK, Cx, dwc.splits, dwT);
       }
     }
     if (!ok) return false;
@@ -1629,7 +1867,7 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
   if (dx) {
     const bool blk = blocked_k(OCp);
     hipLaunchKernelGGL(k_permute_w, dim3(cdiv(size_t(g.C) * KK * OCp, 256)), dim3(256), 0,
-                       stream(), w, wt, g.OC, g.C, KK, OCp, 1, blk ? 1 : 0);
+                       stream(), w, wt, g.OC, g.C, KK, OCp, KK * OCp, 1, blk ? 1 : 0);
     if (!check_launch("permute_w")) return false;
     const double fl = 2.0 * g.OC * g.C * KK * double(npix);
     {

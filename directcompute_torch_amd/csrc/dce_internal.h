@@ -276,13 +276,21 @@ inline uint32_t pad4(uint32_t c) { return (c + 3u) & ~3u; }
 // count padded to pad4(C) (zeros): out[((b*H + h)*W + w)*Cp + c].
 size_t nhwc_floats(uint32_t B, uint32_t C, uint32_t H, uint32_t W);
 bool to_nhwc(const float* x, float* out, uint32_t B, uint32_t C, uint32_t H, uint32_t W);
+// The copy of x that a convolution's GEMMs read: NHWC as above, or, for
+// fewer than four input channels, channel-packed and zero-padded by the
+// convolution's padding ([B][H + 2p][W + 2p][C], unpadded C).  xcopy_floats
+// is its size and xcopy_tag a value that differs between the two layouts
+// (and between paddings of the packed one).
+bool packed_x(const ConvGeom& g);
+size_t xcopy_floats(const ConvGeom& g);
+uint32_t xcopy_tag(const ConvGeom& g);
 // y = act(conv(x, w) + bias) in NCHW.  x_nhwc_keep, when not null, receives
-// the NHWC copy of x (nhwc_floats(B, C, H, W)) for a later backward.
+// the copy of x (xcopy_floats(g) floats) for a later backward.
 bool conv_forward(const float* x, float* x_nhwc_keep, const float* w, const float* bias,
                   float* y, const ConvGeom& g, uint32_t act);
 // dW[OC, C, k, k], db[OC], dX (NCHW) from G = dy masked by y (> 0 kept; y may
 // be null: no mask).  Any of dw, db, dx may be null (not requested).
-// x_nhwc, when not null, is the NHWC copy produced by conv_forward.
+// x_nhwc, when not null, is the copy of x produced by conv_forward.
 bool conv_backward(const float* dy, const float* y, const float* x, const float* x_nhwc,
                    const float* w, float* dw, float* db, float* dx, const ConvGeom& g);
 // C[M,N] = op(A)·op(B); flags bit0: A stored K×M, bit1: B stored N×K.

@@ -51,6 +51,7 @@ CONV_CASES = [
     (2, 16, 12, 12, 96, 1, 1, 0, 1),      # 1x1 expand x6 (dW with taps as rows)
     (2, 3, 10, 11, 40, 1, 1, 0, 1),       # 1x1, C = 3 padded to 4 (dW with taps as rows)
     (2, 3, 64, 64, 16, 3, 1, 1, 1),       # one dW tile: many split-K slices
+    (2, 2, 7, 9, 8, 3, 2, 1, 1),          # C = 2 (channel-packed x), stride 2
     (2, 16, 14, 14, 20, 3, 2, 1, 1),      # stride 2, OC not multiple of 16
     (2, 17, 9, 9, 33, 3, 2, 0, 2),        # tanh act: no derivative applied (reference quirk)
     (1, 8, 7, 7, 8, 3, 3, 1, 0),          # stride 3
@@ -58,14 +59,15 @@ CONV_CASES = [
 ]
 
 
-def _conv_case(eng, B, C, H, W, OC, k, s, p, act, want=(1, 1, 1), seed=0):
+def _conv_case(eng, B, C, H, W, OC, k, s, p, act, want=(1, 1, 1), seed=0, keep=True):
     r = rng(2000 + seed + B + C * 3 + H * 5 + OC * 7 + k + s + p)
     x = r.standard_normal((B, C, H, W)).astype(np.float32)
     w = he(r, (OC, C, k, k), C * k * k)
     b = (0.1 * r.standard_normal(OC)).astype(np.float32)
     hx, hw, hb = upload(eng, x), upload(eng, w), upload(eng, b)
     pim = ctypes.c_void_p()
-    hy = eng.lib.ConvForwardFused(hx, hw, hb, B, C, H, W, OC, k, k, s, p, act, ctypes.byref(pim))
+    hy = eng.lib.ConvForwardFused(hx, hw, hb, B, C, H, W, OC, k, k, s, p, act,
+                                  ctypes.byref(pim) if keep else None)
     assert hy, eng.last_error()
     OH, OW = K.conv_out_hw(H, W, k, s, p)
     y = download(eng, hy, (B, OC, OH, OW))
@@ -104,6 +106,14 @@ def _conv_case(eng, B, C, H, W, OC, k, s, p, act, want=(1, 1, 1), seed=0):
 @pytest.mark.parametrize("case", CONV_CASES, ids=[str(c) for c in CONV_CASES])
 def test_conv_forward_backward(eng, case):
     _conv_case(eng, *case)
+
+
+@pytest.mark.parametrize("case", [(2, 3, 35, 35, 64, 11, 4, 2, 1), (2, 1, 12, 10, 6, 5, 1, 2, 1),
+                                  (2, 16, 9, 9, 8, 3, 1, 1, 1)], ids=str)
+def test_conv_backward_rebuilds_x_copy(eng, case):
+    """Without the forward's handle the backward builds its own copy of x
+    (channel-packed for C < 4, NHWC otherwise)."""
+    _conv_case(eng, *case, seed=5, keep=False)
 
 
 @pytest.mark.parametrize("want", [(0, 1, 1), (1, 0, 0), (0, 0, 1), (1, 1, 0)])
