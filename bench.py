@@ -713,7 +713,7 @@ def main():
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "conv-backward implicit GEMM, all layers: dW k_igemm<LdGradKR,LdXTapKR> + k_dw_final, dX k_igemm<LdDenseRK,LdPixRK> (+ k_splitk_nchw when split)",
+            "kernel": "conv-backward implicit GEMM, all layers: dW k_igemm<LdGradKR,LdXTapKR> (LdPkKR for c1, C = 3) + k_dw_final, dX k_igemm<LdDenseRK,LdPixRK> (+ k_splitk_nchw when split)",
             "achieved": round(achieved, 3),
             "peak": MFMA_FP32_PEAK_TFLOPS,
             "unit": "TFLOP/s",
