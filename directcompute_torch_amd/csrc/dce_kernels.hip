@@ -2075,11 +2075,10 @@ static bool sh_dw_fwd(const Dispatch& d) {
     const uint32_t BW = (g.OW + 1) / 2;
     const FastDiv fLW = make_fastdiv(bb.v4 ? bb.LW / 4 : bb.LW), fNb = make_fastdiv(nb),
                   fBW = make_fastdiv(BW);
-    // One resident round of blocks, each walking bands with a grid stride.
+    // One block per band, in band order (as the dX band kernel).
 #define DCE_DWF_V(K, SS, V)                                                                      \
   {                                                                                             \
-    const uint32_t blocks = std::min<uint32_t>(                                                 \
-        nbands, uint32_t(num_cus()) * blocks_per_cu(k_dw_fwd_band<K, SS, V>, 256));             \
+    const uint32_t blocks = nbands;                                                             \
     hipLaunchKernelGGL((k_dw_fwd_band<K, SS, V>), dim3(blocks), dim3(256), 0, stream(), x.p,     \
                        f.p, bias.p, y.p, g.C, g.H, g.W, g.OH, g.OW, g.p, bb.RB, nb, nbands,      \
                        bb.R, bb.LW, BW, nx, fLW, fNb, fBW);                                      \
@@ -2115,12 +2114,15 @@ static bool sh_dw_bwd_input(const Dispatch& d) {
     const FastDiv fLW = make_fastdiv(bb.v4 ? bb.LW / 4 : bb.LW), fNb = make_fastdiv(nb),
                   fBW = make_fastdiv(BW);
     const uint32_t podd = g.p & 1;
-    // One resident round of blocks (the runtime's occupancy), each walking
-    // bands with a grid stride: no partly filled second round.
+    // One block per band, in band (= memory) order: the blocks that run at
+    // the same time then write neighbouring rows of dx.  Measured against a
+    // resident round of blocks walking the bands with a grid stride (which
+    // overlaps each block's next window load with its compute): 64x144x56x56
+    // s1 40.6 -> 38.1 us, 64x96x112x112 s2 81.4 -> 77.0 us.  On a plain
+    // 1.2 GB fill the same contrast is 6.85 against 4.4-5.0 TB/s.
 #define DCE_DWI_V(K, SS, PO, V)                                                                   \
   {                                                                                              \
-    const uint32_t blocks = std::min<uint32_t>(                                                  \
-        nbands, uint32_t(num_cus()) * blocks_per_cu(k_dw_bwd_input_band<K, SS, PO, V, kDwCW>, 256));   \
+    const uint32_t blocks = nbands;                                                              \
     hipLaunchKernelGGL((k_dw_bwd_input_band<K, SS, PO, V, kDwCW>), dim3(blocks), dim3(256), 0,          \
                        stream(), dy.p, f.p, dx.p, g.C, g.H, g.W, g.OH, g.OW, g.p, bb.RB, nb,     \
                        nbands, bb.R, bb.LW, BW, ndy, fLW, fNb, fBW);                             \
