@@ -1516,22 +1516,53 @@ bool to_nhwc(const float* x, float* out, uint32_t B, uint32_t C, uint32_t H, uin
   return to_nhwc_masked(x, nullptr, out, nullptr, B, C, H * W, nullptr);
 }
 
-// Channel-packed, zero-padded copy (fewer than four channels): one thread per
-// padded pixel, out[((b*Hp + h)*Wp + w)*C + c] = x[b][c][h - p][w - p], zero
-// in the border.
-__global__ void k_to_pk(const float* __restrict__ x, float* __restrict__ out, uint32_t C,
-                        uint32_t H, uint32_t W, uint32_t p, uint32_t Hp, uint32_t Wp,
-                        uint32_t npix, FastDiv dWp, FastDiv dHp) {
+// Channel-packed, zero-padded copy (fewer than four channels): out[((b*Hp +
+// h)*Wp + w)*C + c] = x[b][c][h - p][w - p], zero in the border.  A thread
+// takes 4 consecutive padded pixels of one row: one 16-byte load per channel
+// (4-byte aligned: unaligned access is on) where the 4 source columns lie in
+// the image, else element loads, and C 16-byte stores (the 4*C outputs are
+// contiguous and 16-byte aligned when Wp % 4 == 0; otherwise element stores).
+template <int C>
+__global__ void k_to_pk(const float* __restrict__ x, float* __restrict__ out, uint32_t H,
+                        uint32_t W, uint32_t p, uint32_t Hp, uint32_t Wp, uint32_t WQ, uint32_t nq,
+                        FastDiv dWQ, FastDiv dHp) {
   const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= npix) return;
-  const uint32_t t = fdiv(i, dWp), w = i - t * Wp;
+  if (i >= nq) return;
+  const uint32_t t = fdiv(i, dWQ), wq = i - t * WQ;  // t = b * Hp + h
   const uint32_t b = fdiv(t, dHp), h = t - b * Hp;
-  const uint32_t ih = h - p, iw = w - p;  // wraps when in the border
-  const bool in = ih < H && iw < W;
-  const size_t plane = size_t(H) * W;
-  const size_t src = in ? (size_t(b) * C * H + ih) * W + iw : 0;
-  float* dst = out + size_t(i) * C;
-  for (uint32_t c = 0; c < C; ++c) dst[c] = in ? x[src + c * plane] : 0.f;
+  const uint32_t w0 = 4 * wq, ih = h - p;  // ih wraps when in the border
+  const int iw0 = int(w0) - int(p);
+  const bool rowin = ih < H;
+  const bool fullin = rowin && iw0 >= 0 && iw0 + 4 <= int(W);
+  float o[4 * C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const float* src = x + ((size_t(b) * C + c) * H + (rowin ? ih : 0)) * W;
+    f4 q;
+    if (fullin) {
+      q = ldu<f4>(src + iw0);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int iw = iw0 + e;
+        q[e] = (rowin && iw >= 0 && iw < int(W)) ? src[iw] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e * C + c] = q[e];
+  }
+  float* dst = out + (size_t(t) * Wp + w0) * C;
+  if (Wp % 4 == 0) {
+#pragma unroll
+    for (int k = 0; k < C; ++k) *reinterpret_cast<f4*>(dst + 4 * k) = f4{o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]};
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (w0 + e < Wp) {
+#pragma unroll
+        for (int c = 0; c < C; ++c) dst[e * C + c] = o[e * C + c];
+      }
+  }
 }
 
 bool packed_x(const ConvGeom& g) { return g.C < 4; }
@@ -1545,9 +1576,19 @@ uint32_t xcopy_tag(const ConvGeom& g) { return packed_x(g) ? 0x10000u + g.p : pa
 
 static bool to_pk(const float* x, float* out, const ConvGeom& g) {
   const uint32_t Hp = g.H + 2 * g.p, Wp = g.W + 2 * g.p, npix = g.B * Hp * Wp;
+  const uint32_t WQ = cdiv(Wp, 4), nq = g.B * Hp * WQ;
   ProfScope prof("nhwc", 0, 4.0 * (double(g.B) * g.C * g.H * g.W + double(npix) * g.C));
-  hipLaunchKernelGGL(k_to_pk, dim3(cdiv(npix, 256)), dim3(256), 0, stream(), x, out, g.C, g.H,
-                     g.W, g.p, Hp, Wp, npix, make_fastdiv(Wp), make_fastdiv(Hp));
+  const dim3 grid(cdiv(nq, 256));
+  const FastDiv fWQ = make_fastdiv(WQ), fHp = make_fastdiv(Hp);
+  if (g.C == 1)
+    hipLaunchKernelGGL(k_to_pk<1>, grid, dim3(256), 0, stream(), x, out, g.H, g.W, g.p, Hp, Wp, WQ,
+                       nq, fWQ, fHp);
+  else if (g.C == 2)
+    hipLaunchKernelGGL(k_to_pk<2>, grid, dim3(256), 0, stream(), x, out, g.H, g.W, g.p, Hp, Wp, WQ,
+                       nq, fWQ, fHp);
+  else
+    hipLaunchKernelGGL(k_to_pk<3>, grid, dim3(256), 0, stream(), x, out, g.H, g.W, g.p, Hp, Wp, WQ,
+                       nq, fWQ, fHp);
   return check_launch("to_pk");
 }
 

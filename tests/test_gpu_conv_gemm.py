@@ -52,6 +52,7 @@ CONV_CASES = [
     (2, 3, 10, 11, 40, 1, 1, 0, 1),       # 1x1, C = 3 padded to 4 (dW with taps as rows)
     (2, 3, 64, 64, 16, 3, 1, 1, 1),       # one dW tile: many split-K slices
     (2, 2, 7, 9, 8, 3, 2, 1, 1),          # C = 2 (channel-packed x), stride 2
+    (2, 3, 30, 30, 8, 5, 2, 1, 1),        # C = 3, padded width 32 (16-byte stores of the packed copy)
     (2, 16, 14, 14, 20, 3, 2, 1, 1),      # stride 2, OC not multiple of 16
     (2, 17, 9, 9, 33, 3, 2, 0, 2),        # tanh act: no derivative applied (reference quirk)
     (1, 8, 7, 7, 8, 3, 3, 1, 0),          # stride 3
