@@ -1889,7 +1889,7 @@ __global__ void __launch_bounds__(256)
   __shared__ __attribute__((aligned(16))) float sx[kDwBand];
   __shared__ __attribute__((aligned(16))) float sg[dw_gband(S)];
   __shared__ float red[4][T];
-  const uint32_t c = blockIdx.y;
+  const uint32_t c = blockIdx.x, piece = blockIdx.y, npieces = gridDim.y;
   BRes bx, bg;
   bx.init(x, B * C * H * W);
   bg.init(dy, B * C * OH * OW);
@@ -1898,8 +1898,8 @@ __global__ void __launch_bounds__(256)
   const int lox = DwRegs<V4, kDwRegs>::shift(-int(p));
   // The channel's B * nb (image, band) units, split evenly over the pieces.
   const uint32_t units = B * nb;
-  const uint32_t u0 = uint32_t(uint64_t(units) * blockIdx.x / gridDim.x);
-  const uint32_t total = uint32_t(uint64_t(units) * (blockIdx.x + 1) / gridDim.x) - u0;
+  const uint32_t u0 = uint32_t(uint64_t(units) * piece / npieces);
+  const uint32_t total = uint32_t(uint64_t(units) * (piece + 1) / npieces) - u0;
   auto issue = [&](uint32_t j) {
     const uint32_t u = u0 + j;
     const uint32_t n = fdiv(u, dNb), o0 = (u - n * nb) * RB;
@@ -1968,7 +1968,7 @@ __global__ void __launch_bounds__(256)
   if (threadIdx.x < T) {
     const int q = threadIdx.x;
     const double t = (double(red[0][q]) + double(red[1][q])) + (double(red[2][q]) + double(red[3][q]));
-    part[(size_t(c) * gridDim.x + blockIdx.x) * T + q] = t;
+    part[(size_t(c) * npieces + piece) * T + q] = t;
   }
 }
 
@@ -2169,12 +2169,16 @@ static bool sh_dw_bwd_filter(const Dispatch& d) {
 #undef DCE_DWO
     const uint32_t want =
         std::max<uint32_t>(1, uint32_t(num_cus()) * uint32_t(occ) / std::max<uint32_t>(1, g.C));
-    const uint32_t pieces = std::min<uint32_t>(g.B, want);
+    // Stride 2 takes one image per piece instead (64x96x112x112: 73.8 ->
+    // 70.4 us; stride 1 measured slower that way, 45.7 -> 49.6 us).  The
+    // grid runs channels fastest, so the blocks that run together read the
+    // planes of one image.
+    const uint32_t pieces = g.s == 2 ? g.B : std::min<uint32_t>(g.B, want);
     double* part = reinterpret_cast<double*>(workspace(size_t(g.C) * pieces * (taps + 1) * 2));
     if (!part) return false;
     ProfScope prof("dw_bwd_filter", 2.0 * taps * double(len) * g.C,
                    4.0 * double(len) * g.C + 4.0 * double(g.B) * g.C * g.H * g.W);
-    const dim3 grid(pieces, g.C);
+    const dim3 grid(g.C, pieces);
     const uint32_t nb = cdiv(g.OH, bb.RB);
     const FastDiv fLX = make_fastdiv(bb.v4 ? bb.LW / 4 : bb.LW),
                   fLG = make_fastdiv(bb.v4 ? bb.LW2 / 4 : bb.LW2), fNb = make_fastdiv(nb),
