@@ -618,7 +618,10 @@ __global__ void k_bn_partial(Buf x, Buf dy, Buf mean, Buf var, float eps, uint32
 
 // Same sums over quads when S % 4 == 0 (every quad lies in one plane): the
 // piece is a range of quad indices k (plane n = k / (S/4)), read kBnUnroll
-// quads at a time so that each thread keeps several loads in flight.
+// quads at a time so that each thread keeps several loads in flight.  The
+// grid is (channel, piece) with channels fastest, so the blocks that run
+// together read neighbouring planes of the same images (64x96x112x112
+// backward reduce 104.6 -> 96.6 us against pieces fastest).
 constexpr int kBnUnroll = 4;
 template <int MODE, bool NT>
 __global__ void __launch_bounds__(256)
@@ -627,7 +630,7 @@ __global__ void __launch_bounds__(256)
                   uint32_t C, uint32_t S4, uint32_t len4, uint32_t pieces, FastDiv dS4,
                   double* __restrict__ part) {
   __shared__ double sh[4];
-  const uint32_t c = blockIdx.y, pc = blockIdx.x;
+  const uint32_t c = blockIdx.x, pc = blockIdx.y;
   const uint32_t k0 = uint32_t((uint64_t(len4) * pc) / pieces);
   const uint32_t k1 = uint32_t((uint64_t(len4) * (pc + 1)) / pieces);
   float mu = 0.f, rstd = 0.f;
@@ -740,7 +743,7 @@ static bool bn_reduce(const char* what, int mode, const Dispatch& d, Buf x, Buf 
     const FastDiv dS4 = make_fastdiv(S4);
     const bool nt = stream_nt((mode == 0 ? 4.0 : 8.0) * double(total));
 #define DCE_BNP(M, NT)                                                                         \
-  hipLaunchKernelGGL((k_bn_partial4<M, NT>), grid, dim3(256), 0, stream(), x.p,               \
+  hipLaunchKernelGGL((k_bn_partial4<M, NT>), dim3(C, pc.pieces), dim3(256), 0, stream(), x.p, \
                      M ? dy.p : nullptr, M ? mean.p : nullptr, M ? var.p : nullptr, eps, C, S4, \
                      len4, pc.pieces, dS4, part)
     if (mode == 0 && nt) DCE_BNP(0, true);
