@@ -124,6 +124,9 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.AdamBatch.restype = None
     lib.ClipGradNorm.argtypes = [P(c_void_p), P(c_uint), c_uint, c_float]
     lib.ClipGradNorm.restype = c_float
+    lib.AdamBatchCounted.argtypes = ([P(c_void_p)] * 4 + [P(c_uint), c_uint, c_void_p, c_uint]
+                                     + [ctypes.c_double] * 3 + [c_float] * 3)
+    lib.AdamBatchCounted.restype = None
     lib.SetProfiling.argtypes = [ctypes.c_int]
     lib.SetProfiling.restype = None
     lib.GetProfile.argtypes = [ctypes.c_char_p, P(ctypes.c_uint64), P(ctypes.c_double), P(ctypes.c_double), P(ctypes.c_double)]
@@ -138,6 +141,8 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.ReplayGraph.restype = ctypes.c_bool
     lib.ReleaseGraph.argtypes = [c_void_p]
     lib.ReleaseGraph.restype = None
+    lib.SetStreamingThreshold.argtypes = [ctypes.c_double]
+    lib.SetStreamingThreshold.restype = ctypes.c_double
     lib.ResetProfile.argtypes = []
     lib.ResetProfile.restype = None
     return lib

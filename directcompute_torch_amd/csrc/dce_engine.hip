@@ -40,6 +40,8 @@ static std::vector<Buffer*> g_recycled;  // dead records, reused for new handles
 static uint64_t g_poolHits = 0, g_poolMisses = 0, g_poolBytes = 0;
 static uint64_t g_poolCapBytes = 0;
 
+double g_streamBytes = kStreamBytes;
+
 static float* g_ws = nullptr;
 static size_t g_wsFloats = 0;
 
@@ -516,7 +518,9 @@ void ReleaseBufferBatch(void** handles, uint32_t count) {
 void UpdateBuffer(void* handle, float* data) {
   if (!handle || !data || !g_init) return;
   Buffer* b = as_buffer(handle, "UpdateBuffer");
-  if (b) upload(b->ptr, data, b->count);
+  if (!b) return;
+  b->tag = 0;  // the contents are the caller's now
+  upload(b->ptr, data, b->count);
 }
 
 void ReadBuffer(void* handle, float* dst) {
@@ -534,7 +538,9 @@ void ReadBuffer(void* handle, float* dst) {
 void ClearBuffer(void* handle) {
   if (!handle || !g_init) return;
   Buffer* b = as_buffer(handle, "ClearBuffer");
-  if (b) fill_zero(b->ptr, b->count);
+  if (!b) return;
+  b->tag = 0;
+  fill_zero(b->ptr, b->count);
 }
 
 void FlushGPU(void) {}
@@ -588,6 +594,17 @@ bool CompileShaderEx(const char* name, const wchar_t* path, const char* entry) {
   return false;
 }
 
+// A kernel's outputs lose any producer tag (pooling geometry, conv input
+// copy) before it runs: their contents are then the kernel's, not the
+// producer's that the tag describes.
+static void run_entry(const ShaderEntry* e, const Dispatch& d) {
+  for (uint32_t i = 0; d.uavs && i < d.nU; ++i) {
+    Buffer* b = static_cast<Buffer*>(d.uavs[i]);
+    if (b && b->magic == kMagicLive) b->tag = 0;
+  }
+  e->fn(d);
+}
+
 void RunShader(const char* name, void** srvs, uint32_t srvCount, void** uavs,
                uint32_t uavCount, uint32_t* threads, void* cb, uint32_t cbSize) {
   if (!g_init || !name) return;
@@ -598,7 +615,7 @@ void RunShader(const char* name, void** srvs, uint32_t srvCount, void** uavs,
   }
   Dispatch d{srvs, srvCount, uavs, uavCount, threads, static_cast<const uint8_t*>(cb),
              cb ? cbSize : 0u};
-  e->fn(d);
+  run_entry(e, d);
 }
 
 void RunShaderRaw(const char* name, void** srvs, uint32_t srvCount, void** uavs,
@@ -634,15 +651,15 @@ void RunSequence(SeqCmd* cmds, uint32_t count) {
   for (uint32_t i = 0; i < count; ++i) {
     SeqCmd& c = cmds[i];
     if (!c.shader) continue;
-    const ShaderEntry* e = static_cast<const ShaderEntry*>(c.shader);
-    if (find_shader(e->name) != e) {
+    const ShaderEntry* e = shader_entry(c.shader);
+    if (!e) {
       set_error("RunSequence: command %u has an unresolved shader pointer", i);
       continue;
     }
     Dispatch d{c.srvs, std::min<uint32_t>(c.srvCount, 8), c.uavs,
                std::min<uint32_t>(c.uavCount, 4), c.threads, c.cbData,
                std::min<uint32_t>(c.cbSize, 64)};
-    e->fn(d);
+    run_entry(e, d);
   }
 }
 
@@ -917,6 +934,20 @@ float ClipGradNorm(void** grads, uint32_t* sizes, uint32_t numGrads, float maxNo
   return h[0];
 }
 
+void AdamBatchCounted(void** params, void** grads, void** m, void** v, uint32_t* sizes,
+                      uint32_t numParams, void* stepState, uint32_t t, double lr, double beta1,
+                      double beta2, float eps, float weightDecay, float clip) {
+  if (!g_init || !params || !grads || !m || !v || !sizes || !numParams) return;
+  Buffer* st = as_buffer(stepState, "AdamBatchCounted(stepState)");
+  if (!st) return;
+  if (st->count < 2) {
+    set_error("AdamBatchCounted: the step state buffer needs 2 floats (has %u)", st->count);
+    return;
+  }
+  adam_counted_multi(params, grads, m, v, sizes, numParams, st->ptr, t, lr, beta1, beta2, eps,
+                     weightDecay, clip);
+}
+
 // ----------------------------------------------------------------- profiling
 void SetProfiling(int enabled) {
   if (!enabled) resolve_profile();
@@ -1033,6 +1064,12 @@ void ReleaseGraph(void* graph) {
     for (float* p : g_wsRetired) hipFree(p);
     g_wsRetired.clear();
   }
+}
+
+double SetStreamingThreshold(double bytes) {
+  const double prev = g_streamBytes;
+  g_streamBytes = bytes < 0 ? kStreamBytes : bytes;
+  return prev;
 }
 
 void SetProfileFilter(const char* families) {

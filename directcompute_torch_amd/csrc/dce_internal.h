@@ -129,8 +129,12 @@ __device__ __forceinline__ void stu(void* p, const V& v) {
 // policy wins: the producer's output is still in the MALL when the next
 // kernel reads it.
 // ---------------------------------------------------------------------------
+// The threshold is a run-time value (default kStreamBytes) so that both
+// template instances of every streaming kernel can be checked at small sizes
+// (SetStreamingThreshold).
 constexpr double kStreamBytes = 256.0 * 1024 * 1024;
-inline bool stream_nt(double bytes) { return bytes > kStreamBytes; }
+extern double g_streamBytes;
+inline bool stream_nt(double bytes) { return bytes > g_streamBytes; }
 __device__ __forceinline__ f4 ldnt4(const float* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const f4*>(p));
 }
@@ -334,6 +338,8 @@ struct ShaderEntry {
   ShaderFn fn;
 };
 const ShaderEntry* find_shader(const char* name);
+// The entry at address p, or nullptr when p is not an element of the registry.
+const ShaderEntry* shader_entry(const void* p);
 
 // Multi-tensor optimiser launchers (dce_optim.hip).
 bool sgd_multi(void** params, void** grads, const uint32_t* sizes, uint32_t n,
@@ -346,5 +352,10 @@ bool scale_grads_multi(void** grads, const uint32_t* sizes, uint32_t n,
                        const float* d_norm_scale);
 bool adam_multi(void** params, void** grads, void** m, void** v, const uint32_t* sizes,
                 uint32_t n, float step, float b1, float b2, float eps, float wd, float clip);
+// Adam with the step counter and step size in device memory state[0..1]
+// (t_set > 0: set the counter to t_set; 0: advance it by one).
+bool adam_counted_multi(void** params, void** grads, void** m, void** v,
+                        const uint32_t* sizes, uint32_t n, float* state, uint32_t t_set,
+                        double lr, double b1, double b2, float eps, float wd, float clip);
 
 }  // namespace dce

@@ -1169,12 +1169,23 @@ __global__ void k_maxpool_bwd_blk(const float* __restrict__ dz, const uint32_t* 
   }
 }
 
-// Fallback when the pooling geometry is unknown: zero + scatter-add.
-__global__ void k_maxpool_bwd_scatter(Buf dz, const uint32_t* idx, Buf dx, uint32_t n) {
-  const uint32_t o = gtid();
-  if (o >= n) return;
-  const uint32_t t = idx[o];
-  if (t != 0xFFFFFFFFu && t < dx.n) atomicAdd(dx.p + t, ld(dz, o));
+// Fallback when the pooling geometry is unknown (indices this library did
+// not produce): one thread per (b, c) plane adds the plane's dZ values to
+// dX[idx] in output order, after dX was cleared.  Every input then sums its
+// windows in (oh, ow) order, as the gather kernels do, with no atomics.  An
+// index outside its own plane cannot come from a pooling window; it is
+// dropped, as is the no-argmax marker 0xFFFFFFFF.
+__global__ void k_maxpool_bwd_planes(const float* __restrict__ dz, const uint32_t* __restrict__ idx,
+                                     float* __restrict__ dx, uint32_t planes, uint32_t outPer,
+                                     uint32_t inPer) {
+  const uint32_t p = gtid();
+  if (p >= planes) return;
+  const uint32_t lo = p * inPer, hi = lo + inPer;
+  for (uint32_t j = 0; j < outPer; ++j) {
+    const uint32_t o = p * outPer + j;
+    const uint32_t t = idx[o];
+    if (t >= lo && t < hi) dx[t] += dz[o];
+  }
 }
 
 bool maxpool_backward(const float* dz, const float* idx, float* dx, uint32_t B, uint32_t C,
@@ -1217,9 +1228,16 @@ bool maxpool_backward(const float* dz, const float* idx, float* dx, uint32_t B, 
                          W, k, s, OH, OW, fW, fH);
     return check_launch("maxpool_backward");
   }
+  const uint32_t planes = B * C;
+  if (!planes || xcount % planes != 0) {
+    set_error("MaxPoolBackwardFused: indices carry no pooling geometry and the input size %u "
+              "is not a multiple of batch*channels = %u", xcount, planes);
+    return false;
+  }
   if (!fill_zero(dx, xcount)) return false;
-  hipLaunchKernelGGL(k_maxpool_bwd_scatter, dim3(cdiv(n, 256)), dim3(256), 0, stream(),
-                     Buf{const_cast<float*>(dz), n}, ip, Buf{dx, xcount}, n);
+  if (n == 0) return true;
+  hipLaunchKernelGGL(k_maxpool_bwd_planes, dim3(cdiv(planes, 64)), dim3(64), 0, stream(), dz, ip,
+                     dx, planes, OH * OW, xcount / planes);
   return check_launch("maxpool_backward");
 }
 
@@ -1230,7 +1248,21 @@ static bool sh_maxpool_forward(const Dispatch& d) {
   if (!n) return true;
   hipLaunchKernelGGL(k_maxpool_fwd, dim3(cdiv(n, 256)), dim3(256), 0, stream(), S(d, 0), U(d, 0),
                      U(d, 1), B * C, H, W, k, s, OH, OW);
-  return check_launch("maxpool_forward");
+  if (!check_launch("maxpool_forward")) return false;
+  // The indices record their window geometry, as those of MaxPoolForwardFused
+  // do, so that MaxPoolBackwardFused can run its gather kernels on them.  The
+  // geometry must be the one the kernel's output grid implies.
+  Buf ib = U(d, 1);
+  if (ib.p && uint64_t(ib.n) >= n && k && s && H >= k && W >= k && (H - k) / s + 1 == OH &&
+      (W - k) / s + 1 == OW) {
+    Buffer* I = static_cast<Buffer*>(d.uavs[1]);
+    I->tag = kPoolTag;
+    I->meta[0] = H;
+    I->meta[1] = W;
+    I->meta[2] = k;
+    I->meta[3] = s;
+  }
+  return true;
 }
 // RunShader("maxpool_backward") keeps the reference's store semantics
 // (nn_maxpool_backward.hlsl:21-24): dX[idx] = dZ, the caller clears dX.
@@ -2505,6 +2537,16 @@ const ShaderEntry* find_shader(const char* name) {
   for (const ShaderEntry& e : kShaders)
     if (strcmp(e.name, name) == 0) return &e;
   return nullptr;
+}
+
+// A pointer is a registry entry only if it is the address of one element of
+// the table; nothing behind it is read before this holds.
+const ShaderEntry* shader_entry(const void* p) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p), lo = reinterpret_cast<uintptr_t>(kShaders);
+  const size_t n = sizeof(kShaders) / sizeof(kShaders[0]);
+  if (a < lo || a >= lo + n * sizeof(ShaderEntry) || (a - lo) % sizeof(ShaderEntry) != 0)
+    return nullptr;
+  return &kShaders[(a - lo) / sizeof(ShaderEntry)];
 }
 
 }  // namespace dce

@@ -10,6 +10,7 @@
 #include "dce_internal.h"
 
 #include <algorithm>
+#include <cmath>
 #include <vector>
 
 namespace dce {
@@ -169,6 +170,32 @@ __global__ void __launch_bounds__(256) k_multi_devscale(const Table t, Op op, co
   const int ti = find_tensor(t, blockIdx.x);
   apply_chunk<Op, READ, WRITE, NT>(t, op, ti, (blockIdx.x - t.start[ti]) * kChunk);
 }
+// Adam with the bias-corrected step size read from device memory
+// (state[1], written by k_adam_tick just before), so that a recorded step
+// replays with the step size of its own step count.
+template <bool NT>
+__global__ void __launch_bounds__(256) k_multi_adam_dev(const Table t, AdamOp op,
+                                                          const float* state) {
+  op.step = state[1];
+  const int ti = find_tensor(t, blockIdx.x);
+  apply_chunk<AdamOp, 15, 13, NT>(t, op, ti, (blockIdx.x - t.start[ti]) * kChunk);
+}
+
+// Step counter of Adam / AdamW on the device: state[0] holds t (u32 bits),
+// state[1] the step size lr*sqrt(1 - b2^t)/(1 - b1^t) for that t.  It is
+// evaluated in double from the double hyper-parameters and rounded once to
+// float, as the reference evaluates it in Python and hands the float to the
+// shader (nn_engine.py:2219-2220).  t_set > 0 sets the counter (an eager step
+// whose count the host knows); t_set == 0 advances it by one (a recorded
+// step, whose every replay is the next step).
+__global__ void k_adam_tick(float* state, uint32_t t_set, double lr, double b1, double b2) {
+  if (threadIdx.x != 0) return;
+  const uint32_t t = t_set ? t_set : __float_as_uint(state[0]) + 1u;
+  const double td = double(t);
+  state[0] = __uint_as_float(t);
+  state[1] = float(lr * sqrt(1.0 - pow(b2, td)) / (1.0 - pow(b1, td)));
+}
+
 struct SgdScaledDev : SgdScaledOp {
   static constexpr bool kSkipUnit = false;
 };
@@ -393,6 +420,29 @@ bool adam_multi(void** params, void** grads, void** m, void** v, const uint32_t*
       hipLaunchKernelGGL((k_multi<AdamOp, 15, 13, false>), dim3(table_blocks(t)), dim3(256), 0,
                          stream(), t, AdamOp{step, b1, b2, eps, wd, clip});
     if (!check_launch("AdamBatch")) return false;
+  }
+  return true;
+}
+
+bool adam_counted_multi(void** params, void** grads, void** m, void** v,
+                        const uint32_t* sizes, uint32_t n, float* state, uint32_t t_set,
+                        double lr, double b1, double b2, float eps, float wd, float clip) {
+  std::vector<Table> tabs;
+  if (!build_tables(params, grads, m, v, sizes, n, true, tabs, nullptr)) return false;
+  hipLaunchKernelGGL(k_adam_tick, dim3(1), dim3(64), 0, stream(), state, t_set, lr, b1, b2);
+  if (!check_launch("AdamBatchCounted(tick)")) return false;
+  const double bytes = 28.0 * table_elems(tabs);
+  const bool nt = stream_nt(bytes);
+  ProfScope prof("adam", 0, bytes);
+  const AdamOp op{0.f, float(b1), float(b2), eps, wd, clip};
+  for (const Table& t : tabs) {
+    if (nt)
+      hipLaunchKernelGGL(k_multi_adam_dev<true>, dim3(table_blocks(t)), dim3(256), 0, stream(), t,
+                         op, state);
+    else
+      hipLaunchKernelGGL(k_multi_adam_dev<false>, dim3(table_blocks(t)), dim3(256), 0, stream(),
+                         t, op, state);
+    if (!check_launch("AdamBatchCounted")) return false;
   }
   return true;
 }

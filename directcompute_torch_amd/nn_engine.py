@@ -149,52 +149,68 @@ def _shape_size(shape):
 # --------------------------------------------------------------------------
 # Tensor / Function
 # --------------------------------------------------------------------------
+# Every buffer this module creates goes through _create_buffer, so that
+# discover_buffer_sizes can watch the sizes a training step asks for.
+_size_log = None
+
+
+def _create_buffer(ptr, count):
+    if _size_log is not None:
+        _size_log.add(int(count))
+    return lib.CreateBuffer(ptr, count)
+
+
+def _fptr(arr):
+    return arr.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
 class Tensor:
+    """A device buffer handle with a shape and an autograd context.
+
+    `data` is the host array the tensor was built from, or the array that
+    sync() last filled; device work never updates it by itself."""
     __slots__ = ["data", "shape", "size", "requires_grad", "grad", "gpu_buf", "_ctx", "_cached_topo"]
 
     def __init__(self, data, requires_grad=False, track=True):
-        if isinstance(data, np.ndarray):
-            arr = data if data.dtype == np.float32 else data.astype(np.float32)
-        else:
-            arr = np.array(data, dtype=np.float32)
+        arr = data if isinstance(data, np.ndarray) else np.array(data, dtype=np.float32)
+        if arr.dtype != np.float32:
+            arr = arr.astype(np.float32)
         arr = np.ascontiguousarray(arr)
+        self._init_fields(arr.shape, requires_grad, _create_buffer(_fptr(arr), arr.size), track)
         self.data = arr
-        self.shape = arr.shape
-        self.size = arr.size
+
+    def _init_fields(self, shape, requires_grad, handle, track):
+        self.data = None
+        self.shape = shape
+        self.size = _shape_size(shape)
         self.requires_grad = requires_grad
         self.grad = None
-        self.gpu_buf = lib.CreateBuffer(arr.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), self.size)
+        self.gpu_buf = handle
         self._ctx = None
         if track:
             _all_tensors.append(self)
 
     def __del__(self):
         try:
-            if self.gpu_buf:
-                lib.ReleaseBuffer(self.gpu_buf)
-                self.gpu_buf = None
+            h, self.gpu_buf = self.gpu_buf, None
+            if h:
+                lib.ReleaseBuffer(h)
         except Exception:
             pass
 
     @classmethod
     def from_gpu(cls, handle, shape, requires_grad=False, track=True):
+        """Wrap an existing handle (ownership moves to the tensor)."""
         t = object.__new__(cls)
-        t.data = None
-        t.shape = shape
-        t.size = _shape_size(shape)
-        t.requires_grad = requires_grad
-        t.grad = None
-        t.gpu_buf = handle
-        t._ctx = None
-        if track:
-            _all_tensors.append(t)
+        t._init_fields(shape, requires_grad, handle, track)
         return t
 
     @classmethod
     def empty(cls, shape, requires_grad=False, track=True):
-        t = cls.from_gpu(_check(lib.CreateBuffer(None, _shape_size(shape)), "CreateBuffer"),
-                         tuple(shape), requires_grad=requires_grad, track=track)
-        return t
+        """A tensor over a pooled buffer whose contents are undefined."""
+        shape = tuple(shape)
+        h = _check(_create_buffer(None, _shape_size(shape)), "CreateBuffer")
+        return cls.from_gpu(h, shape, requires_grad=requires_grad, track=track)
 
     @classmethod
     def empty_like(cls, other, requires_grad=None, track=True):
@@ -202,52 +218,61 @@ class Tensor:
         return cls.empty(other.shape, requires_grad=req, track=track)
 
     def sync(self):
-        if self.gpu_buf:
-            if self.data is None or self.data.shape != tuple(self.shape):
-                self.data = np.empty(self.shape, dtype=np.float32)
-            lib.ReadBuffer(self.gpu_buf, self.data.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+        """Blocking read-back into self.data (allocated on first use)."""
+        if not self.gpu_buf:
+            return self.data
+        want = tuple(self.shape)
+        if self.data is None or self.data.shape != want:
+            self.data = np.empty(want, dtype=np.float32)
+        lib.ReadBuffer(self.gpu_buf, _fptr(self.data))
         return self.data
 
     def upload(self, data):
         """Overwrite the device buffer with `data` (no new buffer)."""
-        if data.dtype != np.float32:
-            data = data.astype(np.float32)
-        data = np.ascontiguousarray(data)
-        self.data = data
-        self.shape = data.shape
-        self.size = data.size
-        lib.UpdateBuffer(self.gpu_buf, data.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+        arr = np.ascontiguousarray(data, dtype=np.float32)
+        self.data, self.shape, self.size = arr, arr.shape, arr.size
+        lib.UpdateBuffer(self.gpu_buf, _fptr(arr))
+
+    def _topo_order(self):
+        """Every tensor that takes part in the backward pass, each after all of
+        its inputs.  Depth-first post-order from this tensor in which a node's
+        inputs are taken last to first: the order nn_engine.py:575-603
+        produces, which fixes the order gradients are accumulated in."""
+        order, done = [], set()
+        frames = [[self, None]]           # [node, inputs still to take]
+        while frames:
+            frame = frames[-1]
+            node = frame[0]
+            if frame[1] is None:
+                if node in done:
+                    frames.pop()
+                    continue
+                ins = node._ctx.inputs if node._ctx else ()
+                frame[1] = [t for t in ins if isinstance(t, Tensor) and t.requires_grad]
+            todo = frame[1]
+            while todo and todo[-1] in done:
+                todo.pop()
+            if todo:
+                frames.append([todo.pop(), None])
+            else:
+                done.add(node)
+                order.append(node)
+                frames.pop()
+        return order
 
     def backward(self, grad=None):
-        """Reverse-topological traversal (nn_engine.py:575-603)."""
-        if grad is None:
-            grad = Tensor(np.ones(self.shape, dtype=np.float32), track=False)
-        self.grad = grad
+        """Seed this tensor's gradient (ones by default) and run every
+        Function.backward from the output towards the leaves.  The traversal
+        order is computed once per output tensor and cached."""
+        self.grad = grad if grad is not None else Tensor(np.ones(self.shape, np.float32), track=False)
         try:
-            topo = self._cached_topo
+            order = self._cached_topo
         except AttributeError:
-            topo = []
-            visited = set()
-            stack = [self]
-            while stack:
-                v = stack[-1]
-                if v in visited:
-                    stack.pop()
-                    continue
-                done = True
-                if v._ctx:
-                    for i in v._ctx.inputs:
-                        if isinstance(i, Tensor) and i.requires_grad and i not in visited:
-                            stack.append(i)
-                            done = False
-                if done:
-                    visited.add(v)
-                    stack.pop()
-                    topo.append(v)
-            self._cached_topo = topo
-        for v in reversed(topo):
-            if v._ctx and v.grad is not None:
-                v._ctx.backward(v.grad)
+            order = self._cached_topo = self._topo_order()
+        for node in reversed(order):
+            ctx = node._ctx
+            if ctx and node.grad is not None:
+                ctx.backward(node.grad)
 
     def _accumulate_grad(self, grad):
         """First gradient is aliased; later ones are added in place with
@@ -268,7 +293,7 @@ class Function:
 
 
 def _new(count, what):
-    return _check(lib.CreateBuffer(None, count), what)
+    return _check(_create_buffer(None, count), what)
 
 
 # --------------------------------------------------------------------------
@@ -900,8 +925,25 @@ class BatchNorm2d:
                            self.momentum, self.training)
 
 
+def _param_attrs(obj):
+    """Attributes holding a layer's trainable tensors, in the order
+    Model.parameters lists them.  Normalisation layers are matched by class
+    name, so that a model's own BatchNorm2d / LayerNorm classes count too
+    (nn_engine.py:1959-1971)."""
+    if isinstance(obj, (ConvLayer, DepthwiseConvLayer)):
+        return ("filters", "bias")
+    if isinstance(obj, Linear):
+        return ("w", "b")
+    if type(obj).__name__ in ("BatchNorm2d", "LayerNorm"):
+        return ("gamma", "beta")
+    return ()
+
+
 class Model:
-    """Parameter discovery / train / eval as nn_engine.py:1930-1987."""
+    """Base class of user models: parameter discovery, train / eval mode.
+
+    Layers are found among the model's attributes in dir() order (sorted by
+    name), as in nn_engine.py:1930-1987."""
 
     def __init__(self):
         self._forward_trace = []
@@ -912,106 +954,99 @@ class Model:
     def forward(self, x):
         raise NotImplementedError
 
+    def _members(self):
+        return ((name, getattr(self, name)) for name in dir(self))
+
     def parameters(self):
-        params = []
-        for name in dir(self):
-            attr = getattr(self, name)
-            if isinstance(attr, (ConvLayer, DepthwiseConvLayer)):
-                params.extend([attr.filters, attr.bias])
-            elif isinstance(attr, Linear):
-                params.extend([attr.w, attr.b])
-            elif attr.__class__.__name__ in ("BatchNorm2d", "LayerNorm"):
-                params.extend([attr.gamma, attr.beta])
-        return params
+        return [getattr(layer, a) for _, layer in self._members() for a in _param_attrs(layer)]
 
     def train(self, mode=True):
-        for name in dir(self):
-            attr = getattr(self, name)
-            if hasattr(attr, "training"):
-                attr.training = mode
+        for _, member in self._members():
+            if hasattr(member, "training"):
+                member.training = mode
 
     def eval(self):
         self.train(False)
 
     def _get_layers(self):
-        return [(n, getattr(self, n)) for n in sorted(dir(self))
-                if isinstance(getattr(self, n), (ConvLayer, DepthwiseConvLayer, Linear))]
+        kinds = (ConvLayer, DepthwiseConvLayer, Linear)
+        return [(n, m) for n, m in self._members() if isinstance(m, kinds)]
 
 
 # --------------------------------------------------------------------------
 # Optimisers (nn_engine.py:2172-2242)
 # --------------------------------------------------------------------------
-class SGD:
+# True while ComputeGraph records a step: the optimiser then records work
+# that stays valid on every replay (AdamW advances its device step counter
+# instead of setting it).
+_recording = False
+
+
+class _Optimizer:
+    """Parameters, zero_grad, and the handle tables a multi-tensor launch
+    takes (allocated once; refilled each step with the parameters that have a
+    gradient)."""
+
     def __init__(self, params, lr):
         self.params = params
         self.lr = lr
         n = len(params)
-        self._param_arr = (ctypes.c_void_p * n)()
-        self._grad_arr = (ctypes.c_void_p * n)()
-        self._size_arr = (ctypes.c_uint * n)()
-
-    def zero_grad(self):
-        for p in self.params:
-            if p.grad:
-                p.grad = None
-
-    def step(self, clip=1.0):
-        """w -= lr*clamp(g, -clip, clip) for every parameter with a gradient."""
-        n = 0
-        for p in self.params:
-            if p.grad:
-                self._param_arr[n] = p.gpu_buf
-                self._grad_arr[n] = p.grad.gpu_buf
-                self._size_arr[n] = p.size
-                n += 1
-        if n > 0:
-            lib.SGDBatch(self._param_arr, self._grad_arr, self._size_arr, n, self.lr, clip)
-
-
-class AdamW:
-    """AdamW with the reference's update rule: host-side bias-corrected step
-    size lr*sqrt(1-b2^t)/(1-b1^t), decay lr*wd*w on the old weight, element
-    clip of the gradient; one multi-tensor launch per step."""
-
-    def __init__(self, params, lr=0.001, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01):
-        self.params = params
-        self.lr = lr
-        self.beta1, self.beta2 = betas
-        self.eps = eps
-        self.weight_decay = weight_decay
-        self.t = 0
-        self.m = [Tensor(np.zeros(p.shape), track=False) for p in params]
-        self.v = [Tensor(np.zeros(p.shape), track=False) for p in params]
-        self._m_bufs = [x.gpu_buf for x in self.m]
-        self._v_bufs = [x.gpu_buf for x in self.v]
-        n = len(params)
         self._pa = (ctypes.c_void_p * n)()
         self._ga = (ctypes.c_void_p * n)()
-        self._ma = (ctypes.c_void_p * n)()
-        self._va = (ctypes.c_void_p * n)()
         self._sa = (ctypes.c_uint * n)()
 
     def zero_grad(self):
         for p in self.params:
-            if p.grad:
-                p.grad = None
+            p.grad = None
+
+    def _live(self):
+        """Fill the tables with (param, grad, size) of every parameter that has
+        a gradient, in parameter order; returns their indices."""
+        live = [i for i, p in enumerate(self.params) if p.grad is not None]
+        for slot, i in enumerate(live):
+            p = self.params[i]
+            self._pa[slot], self._ga[slot], self._sa[slot] = p.gpu_buf, p.grad.gpu_buf, p.size
+        return live
+
+
+class SGD(_Optimizer):
+    def step(self, clip=1.0):
+        """w -= lr*clamp(g, -clip, clip) for every parameter with a gradient."""
+        n = len(self._live())
+        if n:
+            lib.SGDBatch(self._pa, self._ga, self._sa, n, self.lr, clip)
+
+
+class AdamW(_Optimizer):
+    """AdamW with the reference's update rule: bias-corrected step size
+    lr*sqrt(1-b2^t)/(1-b1^t), decay lr*wd*w on the old weight, element clip of
+    the gradient; one multi-tensor launch per step.  The step count lives on
+    the device too (AdamBatchCounted), so that a step recorded by ComputeGraph
+    replays as the next step; `t` mirrors it on the host."""
+
+    def __init__(self, params, lr=0.001, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01):
+        super().__init__(params, lr)
+        self.beta1, self.beta2 = betas
+        self.eps = eps
+        self.weight_decay = weight_decay
+        self.t = 0
+        self.m = [Tensor(np.zeros(p.shape, np.float32), track=False) for p in params]
+        self.v = [Tensor(np.zeros(p.shape, np.float32), track=False) for p in params]
+        self._state = Tensor(np.zeros(2, np.float32), track=False)  # [t bits, step size]
+        n = len(params)
+        self._ma = (ctypes.c_void_p * n)()
+        self._va = (ctypes.c_void_p * n)()
 
     def step(self, clip=1.0):
         self.t += 1
-        step_size = self.lr * (1 - self.beta2 ** self.t) ** 0.5 / (1 - self.beta1 ** self.t)
-        n = 0
-        for i, p in enumerate(self.params):
-            if not p.grad:
-                continue
-            self._pa[n] = p.gpu_buf
-            self._ga[n] = p.grad.gpu_buf
-            self._ma[n] = self._m_bufs[i]
-            self._va[n] = self._v_bufs[i]
-            self._sa[n] = p.size
-            n += 1
-        if n:
-            lib.AdamBatch(self._pa, self._ga, self._ma, self._va, self._sa, n, step_size,
-                          self.beta1, self.beta2, self.eps, self.lr * self.weight_decay, clip)
+        live = self._live()
+        for slot, i in enumerate(live):
+            self._ma[slot], self._va[slot] = self.m[i].gpu_buf, self.v[i].gpu_buf
+        if live:
+            lib.AdamBatchCounted(self._pa, self._ga, self._ma, self._va, self._sa, len(live),
+                                 self._state.gpu_buf, 0 if _recording else self.t, self.lr,
+                                 self.beta1, self.beta2, self.eps, self.lr * self.weight_decay,
+                                 clip)
 
 
 class Adam(AdamW):
@@ -1033,39 +1068,42 @@ def gpu_accumulate_loss(loss_tensor, accum_buf):
 
 
 class Metrics:
-    """GPU-resident loss / accuracy accumulators, read back in collect()."""
+    """Loss and accuracy accumulated on the device over an epoch; collect()
+    is the only read-back (nn_engine.py:2336-2385).  The correct count is a
+    u32 held in a float buffer."""
 
     def __init__(self):
-        self._correct_buf = _new(1, "Metrics")
-        self._loss_buf = _new(1, "Metrics")
-        self._f1 = np.empty(1, dtype=np.float32)
-        self._f1_ptr = self._f1.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+        self._bufs = {"loss": _new(1, "Metrics"), "correct": _new(1, "Metrics")}
+        self._host = np.zeros(1, np.float32)
         self._n_batches = 0
         self.reset()
 
     def reset(self):
-        lib.ClearBuffer(self._correct_buf)
-        lib.ClearBuffer(self._loss_buf)
+        for h in self._bufs.values():
+            lib.ClearBuffer(h)
         self._n_batches = 0
 
     def update(self, loss, logits, labels):
-        gpu_accumulate_loss(loss, self._loss_buf)
-        gpu_argmax_correct(logits, labels, self._correct_buf)
+        gpu_accumulate_loss(loss, self._bufs["loss"])
+        gpu_argmax_correct(logits, labels, self._bufs["correct"])
         self._n_batches += 1
 
+    def _read(self, key):
+        lib.ReadBuffer(self._bufs[key], _fptr(self._host))
+        return self._host.copy()
+
     def collect(self, num_samples):
-        lib.ReadBuffer(self._loss_buf, self._f1_ptr)
-        avg_loss = float(self._f1[0]) / self._n_batches if self._n_batches else 0.0
-        lib.ReadBuffer(self._correct_buf, self._f1_ptr)
-        correct = int(np.frombuffer(self._f1.tobytes(), dtype=np.uint32)[0])
-        return avg_loss, (correct / num_samples if num_samples else 0.0)
+        """(mean loss per batch, accuracy over num_samples)."""
+        total = float(self._read("loss")[0])
+        correct = int(self._read("correct").view(np.uint32)[0])
+        mean_loss = total / self._n_batches if self._n_batches else 0.0
+        return mean_loss, (correct / num_samples if num_samples else 0.0)
 
     def __del__(self):
         try:
-            if self._correct_buf:
-                lib.ReleaseBuffer(self._correct_buf)
-            if self._loss_buf:
-                lib.ReleaseBuffer(self._loss_buf)
+            bufs, self._bufs = self._bufs, {}
+            for h in bufs.values():
+                lib.ReleaseBuffer(h)
         except Exception:
             pass
 
@@ -1083,8 +1121,8 @@ end_batch.flush_interval = 10
 
 
 class ComputeGraph:
-    """Record one training step -- forward, softmax-CE loss, backward and the
-    optimiser update -- once, then replay it with new data
+    """Record one training step -- forward, loss, backward, optional global
+    norm clip and the optimiser update -- once, then replay it with new data
     (nn_engine.py:2505-2771).
 
     The reference records the step's RunShader dispatches and replays them with
@@ -1095,118 +1133,133 @@ class ComputeGraph:
     step's buffers until release().
 
     trace() runs the traced batch eagerly (which also sizes the pool and the
-    workspace), then records the same step.  Host scalars are those of the
-    recorded step: the SGD learning rate and clip, and for Adam / AdamW the
-    bias-corrected step size of the traced step.  The model may not read
-    buffers back or upload more than 256 floats inside the step.
+    workspace), then records the same step.  The loss is softmax-CE unless
+    `loss_fn(logits, labels)` is given (e.g. dice_loss); `max_norm` adds the
+    global gradient-norm clip before the update (clip_grad_norm, computed and
+    applied on the device).  Host scalars are those of the recorded step (SGD
+    learning rate and clip); Adam / AdamW keep their step count on the device,
+    so every replay is the next step, and `optimizer.t` follows the replays.
+    The step may not read buffers back or upload more than 256 floats.
     """
 
     def __init__(self):
         self._graph = None
-        self._input_handle = None
-        self._label_handle = None
-        self._loss_handle = None
-        self._logits_handle = None
-        self._loss_size = 0
-        self._logits_shape = None
-        self._input_shape = None
-        self._label_shape = None
+        self._handles = {}         # input, labels, loss, logits
+        self._shapes = {}
+        self._optimizer = None
         self._compiled = False
 
-    def _step(self, forward_fn, optimizer, clip):
+    def _step(self, forward_fn, optimizer, clip, loss_fn, max_norm, params):
         optimizer.zero_grad()
-        lib.AddRefBuffer(self._input_handle)
-        # The traced input's gradient is never readable after the step, so it
-        # is not requested (nn_engine.py:2631 asks for it and discards it).
-        xb = Tensor.from_gpu(self._input_handle, self._input_shape)
-        lib.AddRefBuffer(self._label_handle)
-        yb = Tensor.from_gpu(self._label_handle, self._label_shape)
-        logits = forward_fn(xb)
-        loss = softmax_ce(logits, yb)
+        wrapped = {}
+        for key in ("input", "labels"):
+            lib.AddRefBuffer(self._handles[key])
+            # The traced input's gradient is never readable after the step, so
+            # it is not requested (nn_engine.py:2631 asks for it and drops it).
+            wrapped[key] = Tensor.from_gpu(self._handles[key], self._shapes[key])
+        logits = forward_fn(wrapped["input"])
+        loss = (loss_fn or softmax_ce)(logits, wrapped["labels"])
         loss.backward()
+        if max_norm is not None:
+            clip_grad_norm(params, max_norm)
         optimizer.step(clip=clip)
         return loss, logits
 
-    def trace(self, forward_fn, optimizer, X_batch, Y_batch, params, clip=1.0):
+    def _keep(self, key, tensor):
+        lib.AddRefBuffer(tensor.gpu_buf)
+        self._handles[key] = tensor.gpu_buf
+        self._shapes[key] = tuple(tensor.shape)
+
+    def _upload(self, key, arr):
+        a = np.ascontiguousarray(arr, dtype=np.float32)
+        if a.shape != self._shapes[key]:
+            raise ValueError(f"replay {key} shape {a.shape} differs from the traced {self._shapes[key]}")
+        lib.UpdateBuffer(self._handles[key], _fptr(a))
+
+    def trace(self, forward_fn, optimizer, X_batch, Y_batch, params, clip=1.0, loss_fn=None,
+              max_norm=None):
         """Run one batch eagerly, then record the same step as a graph.
         Returns the eager step's (loss, logits) tensors, whose buffers are
         released on return as in the reference."""
         self.release()
-        X = np.ascontiguousarray(X_batch, dtype=np.float32)
-        Y = np.ascontiguousarray(Y_batch, dtype=np.float32)
-        self._input_shape, self._label_shape = X.shape, Y.shape
-        self._input_handle = _check(
-            lib.CreateBuffer(X.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), X.size), "CreateBuffer")
-        self._label_handle = _check(
-            lib.CreateBuffer(Y.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), Y.size), "CreateBuffer")
-        loss, logits = self._step(forward_fn, optimizer, clip)
-        loss_val = np.empty(loss.size, dtype=np.float32)
-        logits_val = np.empty(logits.shape, dtype=np.float32)
-        lib.ReadBuffer(loss.gpu_buf, loss_val.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
-        lib.ReadBuffer(logits.gpu_buf, logits_val.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+        for key, arr in (("input", X_batch), ("labels", Y_batch)):
+            a = np.ascontiguousarray(arr, dtype=np.float32)
+            self._handles[key] = _check(_create_buffer(_fptr(a), a.size), "CreateBuffer")
+            self._shapes[key] = a.shape
+        step_args = (forward_fn, optimizer, clip, loss_fn, max_norm, params)
+        loss, logits = self._step(*step_args)
+        eager = {"loss": loss.sync().copy(), "logits": logits.sync().copy()}
         release_all_buffers()
+
+        global _recording
+        t_before = getattr(optimizer, "t", None)
         if not lib.BeginCapture():
             raise RuntimeError(f"BeginCapture failed: {last_error()}")
+        _recording = True
         try:
-            loss2, logits2 = self._step(forward_fn, optimizer, clip)
-            self._loss_handle, self._loss_size = loss2.gpu_buf, loss2.size
-            self._logits_handle, self._logits_shape = logits2.gpu_buf, logits2.shape
-            lib.AddRefBuffer(self._loss_handle)
-            lib.AddRefBuffer(self._logits_handle)
+            rec_loss, rec_logits = self._step(*step_args)
+            self._keep("loss", rec_loss)
+            self._keep("logits", rec_logits)
         except BaseException:
+            _recording = False
             graph = lib.EndCapture()
             release_all_buffers()
             if graph:
                 lib.ReleaseGraph(graph)
             self.release()
             raise
+        finally:
+            _recording = False
+            if t_before is not None:
+                optimizer.t = t_before   # the recorded step has not run yet
         graph = lib.EndCapture()
         release_all_buffers()
         if not graph:
             self.release()
             raise RuntimeError(f"ComputeGraph.trace: capture failed: {last_error()}")
         self._graph = graph
+        self._optimizer = optimizer
         self._params_ref = params
         self._compiled = True
-        # read_loss / read_logits before the first replay give the traced step's values
-        lib.UpdateBuffer(self._loss_handle, loss_val.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
-        lib.UpdateBuffer(self._logits_handle, logits_val.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+        # read_loss / read_logits before the first replay give the eager step's values
+        for key in ("loss", "logits"):
+            lib.UpdateBuffer(self._handles[key], _fptr(eager[key]))
         return loss, logits
 
     def replay(self, X_batch, Y_batch):
-        """Upload a new batch into the traced input/label buffers and enqueue
+        """Upload a new batch into the traced input / label buffers and enqueue
         one replay of the step."""
         if not self._compiled:
             raise RuntimeError("Graph not compiled. Call trace() first.")
-        X = np.ascontiguousarray(X_batch, dtype=np.float32)
-        Y = np.ascontiguousarray(Y_batch, dtype=np.float32)
-        if X.shape != self._input_shape or Y.shape != self._label_shape:
-            raise ValueError("replay batch shapes differ from the traced ones")
-        lib.UpdateBuffer(self._input_handle, X.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
-        lib.UpdateBuffer(self._label_handle, Y.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+        self._upload("input", X_batch)
+        self._upload("labels", Y_batch)
         if not lib.ReplayGraph(self._graph):
             raise RuntimeError(f"ReplayGraph failed: {last_error()}")
+        if hasattr(self._optimizer, "t"):
+            self._optimizer.t += 1
 
-    def read_loss(self):
-        out = np.empty(self._loss_size, dtype=np.float32)
-        lib.ReadBuffer(self._loss_handle, out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
-        return float(out[0])
-
-    def read_logits(self):
-        out = np.empty(self._logits_shape, dtype=np.float32)
-        lib.ReadBuffer(self._logits_handle, out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+    def _read(self, key):
+        out = np.empty(self._shapes[key], dtype=np.float32)
+        lib.ReadBuffer(self._handles[key], _fptr(out))
         return out
 
+    def read_loss(self):
+        """The last step's loss (the mean, for a per-sample loss such as Dice)."""
+        v = self._read("loss")
+        return float(v.reshape(-1)[0]) if v.size == 1 else float(v.mean())
+
+    def read_logits(self):
+        return self._read("logits")
+
     def release(self):
-        """Free the graph, the buffers it holds and the input/label buffers."""
+        """Free the graph, the buffers it holds and the input / label buffers."""
         if self._graph:
             lib.ReleaseGraph(self._graph)
             self._graph = None
-        for name in ("_input_handle", "_label_handle", "_loss_handle", "_logits_handle"):
-            h = getattr(self, name)
+        handles, self._handles = self._handles, {}
+        for h in handles.values():
             if h:
                 lib.ReleaseBuffer(h)
-                setattr(self, name, None)
         self._compiled = False
 
     def __del__(self):
@@ -1217,45 +1270,36 @@ class ComputeGraph:
 
 
 def warm_pool(sizes, copies=2):
-    sizes = list(sizes)
-    arr = (ctypes.c_uint * len(sizes))(*sizes)
-    lib.WarmPool(arr, len(sizes), copies)
+    """Pre-allocate `copies` pooled buffers of every element count in `sizes`."""
+    counts = sorted(int(c) for c in sizes)
+    lib.WarmPool((ctypes.c_uint * len(counts))(*counts), len(counts), copies)
 
 
 def discover_buffer_sizes(forward_fn, params, X_batch, Y_batch, optimizer):
-    """Run one batch while recording every CreateBuffer size."""
-    sizes = set()
-    global lib
-    real = lib
-
-    class _Spy:
-        def __getattr__(self, name):
-            return getattr(real, name)
-
-        def CreateBuffer(self, data, count):
-            sizes.add(int(count))
-            return real.CreateBuffer(data, count)
-
-    lib = _Spy()
+    """Element counts of the buffers one softmax-CE training step creates from
+    Python (nn_engine.py:2421-2444): the step runs once, eagerly, with the
+    module's buffer-creation hook recording every count."""
+    global _size_log
+    seen = set()
+    _size_log = seen
     try:
         optimizer.zero_grad()
-        xb = Tensor(X_batch, track=True)
-        yb = Tensor(Y_batch, track=True)
-        logits = forward_fn(xb)
-        loss = softmax_ce(logits, yb)
-        loss.backward()
+        logits = forward_fn(Tensor(X_batch, track=True))
+        softmax_ce(logits, Tensor(Y_batch, track=True)).backward()
         optimizer.step(clip=1.0)
         end_batch()
     finally:
-        lib = real
-    return sizes
+        _size_log = None
+    return seen
 
 
 def auto_warm(forward_fn, params, X_sample, Y_sample, optimizer, copies=2):
-    sizes = discover_buffer_sizes(forward_fn, params, X_sample, Y_sample, optimizer)
-    warm_pool(sizes, copies)
+    """discover_buffer_sizes, then warm_pool with those counts; the pool's
+    hit / miss counters restart afterwards."""
+    found = discover_buffer_sizes(forward_fn, params, X_sample, Y_sample, optimizer)
+    warm_pool(found, copies)
     lib.ResetPoolStats()
-    return sizes
+    return found
 
 
 def get_pool_stats():

@@ -194,6 +194,18 @@ void AdamBatch(void** params, void** grads, void** m, void** v, uint32_t* sizes,
  * maxNorm/(norm+1e-6).  Blocking; returns the norm. */
 float ClipGradNorm(void** grads, uint32_t* sizes, uint32_t numGrads, float maxNorm);
 
+/* AdamBatch with the step counter kept on the device, so that a recorded
+ * step (BeginCapture) replays as the next step, not as a copy of the recorded
+ * one.  stepState is a buffer of at least 2 floats: [0] = t (u32 bits),
+ * [1] = the step size lr*sqrt(1-beta2^t)/(1-beta1^t), evaluated on the device
+ * in double from the double hyper-parameters and rounded once to float, as
+ * AdamW.step evaluates it in Python (nn_engine.py:2217-2238).  t > 0 sets the
+ * counter to t; t == 0 advances it by one (use 0 in a recorded step).
+ * weightDecay is lr*wd, as AdamBatch. */
+void AdamBatchCounted(void** params, void** grads, void** m, void** v, uint32_t* sizes,
+                      uint32_t numParams, void* stepState, uint32_t t, double lr,
+                      double beta1, double beta2, float eps, float weightDecay, float clip);
+
 /* Kernel-family timing with HIP events on the engine stream (for bench.py).
  * SetProfiling(1) starts recording every launch of the named families;
  * GetProfile returns launches, summed milliseconds, summed algorithmic
@@ -206,6 +218,14 @@ void ResetProfile(void);
 /* Restrict recording to a comma-separated list of families (NULL or "": all),
  * so that a timed run carries only the events it reports. */
 void SetProfileFilter(const char* families);
+
+/* Passes that move more than `bytes` bytes use nontemporal (streaming) loads
+ * and stores; smaller ones use the default cache policy.  The default is
+ * 256 MiB, the size of the MI355X Infinity Cache; a negative value restores
+ * it.  Returns the previous threshold.  The choice changes speed only, never
+ * results: it exists for tuning and so that tests can run both kernel forms
+ * at small sizes. */
+double SetStreamingThreshold(double bytes);
 
 /* Record / replay of queued work as a HIP graph: the MI355X form of the
  * reference's ComputeGraph (nn_engine.py:2505-2771), which records RunShader

@@ -39,8 +39,10 @@ class T:
         return self.data.shape
 
     def _acc(self, g):
+        """First gradient is kept, later ones are added with grad_accum
+        (nn_engine.py:605-610)."""
         g = np.asarray(g, dtype=F64).reshape(self.data.shape)
-        self.grad = g.copy() if self.grad is None else self.grad + g
+        self.grad = g.copy() if self.grad is None else K.grad_accum(self.grad, g)
 
     def backward(self):
         topo, seen = [], set()

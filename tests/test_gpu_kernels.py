@@ -36,6 +36,21 @@ def new(eng, n):
     return h
 
 
+@pytest.fixture(params=["cached", "streaming"])
+def policy(request, eng):
+    """Run a test with the default cache policy and again with every pass
+    forced onto the nontemporal (streaming) kernel forms, which by default
+    only passes over 256 MiB take."""
+    if request.param == "cached":
+        yield request.param
+        return
+    prev = eng.lib.SetStreamingThreshold(0.0)
+    try:
+        yield request.param
+    finally:
+        eng.lib.SetStreamingThreshold(prev)
+
+
 # ----------------------------------------------------------------- buffers
 def test_buffer_roundtrip_update_clear(eng):
     for n in (1, 7, 256, 257, 100003, 5_000_000):
@@ -106,7 +121,7 @@ BINARY = [
 
 
 @pytest.mark.parametrize("n", [1, 5, 1024, 1000003])
-def test_activations(eng, n):
+def test_activations(eng, n, policy):
     r = rng(n)
     x = (4 * r.standard_normal(n)).astype(np.float32)
     x[: min(n, 3)] = [0.0, 6.0, -0.0][: min(n, 3)]
@@ -229,10 +244,65 @@ def test_maxpool_raw_shaders(eng):
     release(eng, hx, ho, hi, hdz, hdx)
 
 
+@pytest.mark.parametrize("B,C,H,W,k,s", [(2, 4, 55, 55, 3, 2), (2, 3, 8, 8, 2, 2), (1, 2, 9, 9, 3, 1)])
+def test_maxpool_backward_untagged_indices(eng, B, C, H, W, k, s):
+    """MaxPoolBackwardFused on indices that carry no pooling geometry (here a
+    copy the caller uploaded): the per-plane fallback sums every window in
+    (oh, ow) order, the gather kernels' order, so it matches the tagged path
+    bit for bit and the oracle's routing; no float atomics, so it repeats
+    exactly.  Indices from RunShader("maxpool_forward") carry the geometry."""
+    r = rng(B * C * H * W + 11)
+    x = r.standard_normal((B, C, H, W)).astype(np.float32)
+    x.flat[::13] = 0.25             # ties
+    OH, OW = (H - k) // s + 1, (W - k) // s + 1
+    ref_out, ref_idx = K.maxpool_forward(x, k, s)
+    dz = r.standard_normal((B, C, OH, OW)).astype(np.float32)
+    hx, hdz = upload(eng, x), upload(eng, dz)
+    outs = []
+    for kind in ("fused", "runshader", "uploaded", "uploaded"):
+        if kind == "fused":
+            pidx = ctypes.c_void_p()
+            ho = eng.lib.MaxPoolForwardFused(hx, B, C, H, W, k, s, ctypes.byref(pidx))
+            hi = pidx.value
+        elif kind == "runshader":
+            ho, hi = new(eng, ref_idx.size), new(eng, ref_idx.size)
+            run(eng, "maxpool_forward", [hx], [ho, hi], B, C, H, W, k, s, OH, OW)
+        else:
+            ho, hi = None, upload(eng, ref_idx.view(np.float32))
+        eng.lib.ClearLastError()
+        hdx = eng.lib.MaxPoolBackwardFused(hdz, hi, B, C, OH, OW, x.size)   # consumes hi
+        assert hdx, eng.last_error()
+        outs.append(download(eng, hdx, x.shape))
+        release(eng, ho, hdx)
+    ref_dx = K.maxpool_backward(dz, ref_idx, x.size).reshape(x.shape)
+    for o in outs:
+        assert np.array_equal(o, outs[0])
+    assert rel_err(outs[0], ref_dx) <= 1e-6
+    if k <= s:
+        assert np.array_equal(outs[0], ref_dx.astype(np.float32))
+    # an index outside its own (b, c) plane cannot come from a pooling window
+    bad = ref_idx.copy().reshape(-1)
+    bad[0] = x.size - 1
+    hi = upload(eng, bad.view(np.float32))
+    hdx = eng.lib.MaxPoolBackwardFused(hdz, hi, B, C, OH, OW, x.size)
+    assert hdx, eng.last_error()
+    got = download(eng, hdx, x.shape).reshape(-1)
+    keep = np.ones(bad.size, bool)
+    keep[0] = False
+    exp = K.maxpool_backward(dz.reshape(-1)[keep], bad[keep], x.size)
+    assert rel_err(got, exp) <= 1e-6
+    release(eng, hdx)
+    # no geometry and an input size that is not a whole number of planes
+    hi = upload(eng, ref_idx.view(np.float32))
+    assert not eng.lib.MaxPoolBackwardFused(hdz, hi, B, C, OH, OW, x.size + 1)
+    assert "not a multiple" in eng.last_error()
+    release(eng, hx, hdz)
+
+
 # ---------------------------------------------------------------- batchnorm
 @pytest.mark.parametrize("N,C,H,W", [(2, 3, 5, 5), (8, 16, 32, 32), (4, 96, 28, 28), (64, 6, 12, 12), (1, 1, 1, 7),
                                      (16, 4, 64, 64)])
-def test_batchnorm(eng, N, C, H, W):
+def test_batchnorm(eng, N, C, H, W, policy):
     r = rng(N * C * H * W)
     x = (r.standard_normal((N, C, H, W)) * 2 + 0.5).astype(np.float32)
     gamma = (1 + 0.1 * r.standard_normal(C)).astype(np.float32)
@@ -267,7 +337,7 @@ def test_batchnorm(eng, N, C, H, W):
 
 # --------------------------------------------------- pooling / resampling
 @pytest.mark.parametrize("B,C,H,W", [(2, 3, 7, 7), (8, 64, 8, 8), (1, 1, 1, 1)])
-def test_global_avg_pool(eng, B, C, H, W):
+def test_global_avg_pool(eng, B, C, H, W, policy):
     x = rng(B + C).standard_normal((B, C, H, W)).astype(np.float32)
     g = rng(7).standard_normal((B, C)).astype(np.float32)
     hx, ho, hg, hdx = upload(eng, x), new(eng, B * C), upload(eng, g), new(eng, x.size)
@@ -279,7 +349,7 @@ def test_global_avg_pool(eng, B, C, H, W):
 
 
 @pytest.mark.parametrize("B,C,H,W,sH,sW", [(2, 3, 4, 5, 2, 2), (1, 16, 32, 32, 2, 2), (2, 2, 3, 3, 3, 2)])
-def test_upsample(eng, B, C, H, W, sH, sW):
+def test_upsample(eng, B, C, H, W, sH, sW, policy):
     x = rng(H * W).standard_normal((B, C, H, W)).astype(np.float32)
     OH, OW = H * sH, W * sW
     dy = rng(5).standard_normal((B, C, OH, OW)).astype(np.float32)
@@ -292,7 +362,7 @@ def test_upsample(eng, B, C, H, W, sH, sW):
 
 
 @pytest.mark.parametrize("H,W", [(4, 5), (3, 5)])   # plane sizes 20 (quad path) and 15
-def test_concat_slice(eng, H, W):
+def test_concat_slice(eng, H, W, policy):
     B, S = 2, H * W
     a = rng(1).standard_normal((B, 3, H, W)).astype(np.float32)
     b = rng(2).standard_normal((B, 5, H, W)).astype(np.float32)
@@ -322,7 +392,7 @@ DW_CASES = [
 
 
 @pytest.mark.parametrize("B,C,H,W,k,s,p", DW_CASES)
-def test_depthwise(eng, B, C, H, W, k, s, p):
+def test_depthwise(eng, B, C, H, W, k, s, p, policy):
     r = rng(B * C * H + k + s)
     x = r.standard_normal((B, C, H, W)).astype(np.float32)
     f = r.standard_normal((C, 1, k, k)).astype(np.float32)
@@ -403,7 +473,7 @@ def _arrays(hs):
     return (ctypes.c_void_p * len(hs))(*hs)
 
 
-def test_sgd_batch(eng):
+def test_sgd_batch(eng, policy):
     ws, gs = _param_set(1, SIZES)
     hw, hg = [upload(eng, w) for w in ws], [upload(eng, g) for g in gs]
     pa, ga = _arrays(hw + [None]), _arrays(hg + [hg[0]])     # trailing NULL param is skipped
@@ -415,7 +485,7 @@ def test_sgd_batch(eng):
 
 
 @pytest.mark.parametrize("max_norm", [1.0, 1e6])
-def test_sgd_batch_clipped(eng, max_norm):
+def test_sgd_batch_clipped(eng, max_norm, policy):
     ws, gs = _param_set(2, SIZES)
     hw, hg = [upload(eng, w) for w in ws], [upload(eng, g) for g in gs]
     sa = (ctypes.c_uint * len(SIZES))(*SIZES)
@@ -427,7 +497,7 @@ def test_sgd_batch_clipped(eng, max_norm):
     release(eng, *hw, *hg)
 
 
-def test_clip_grad_norm(eng):
+def test_clip_grad_norm(eng, policy):
     _, gs = _param_set(3, SIZES)
     hg = [upload(eng, g) for g in gs]
     sa = (ctypes.c_uint * len(SIZES))(*SIZES)
@@ -440,7 +510,7 @@ def test_clip_grad_norm(eng):
 
 
 @pytest.mark.parametrize("wd,clip", [(0.01, 1.0), (0.0, 1e30)])
-def test_adam_batch_and_shader(eng, wd, clip):
+def test_adam_batch_and_shader(eng, wd, clip, policy):
     ws, gs = _param_set(4, SIZES)
     r = rng(5)
     ms = [(0.1 * r.standard_normal(n)).astype(np.float32) for n in SIZES]
@@ -468,6 +538,40 @@ def test_adam_batch_and_shader(eng, wd, clip):
     w_r, m_r, v_r = K.adam(ws[5], gs[5], ms[5], vs[5], o_step, o_b1, o_b2, o_eps, o_wd, clip)
     assert rel_err(download(eng, w2, ws[5].shape), w_r) <= 1e-6
     release(eng, *hw, *hg, *hm, *hv, w2, m2, v2)
+
+
+def test_adam_batch_counted(eng, policy):
+    """AdamBatchCounted keeps t and the step size on the device: t > 0 sets
+    the counter, t == 0 advances it.  The step size equals the float32 of the
+    host's float64 formula (nn_engine.py:2219-2220) and the update equals
+    AdamBatch with that step size, bit for bit."""
+    ws, gs = _param_set(6, SIZES)
+    r = rng(7)
+    ms = [(0.1 * r.standard_normal(n)).astype(np.float32) for n in SIZES]
+    vs = [(0.1 * r.random(n)).astype(np.float32) for n in SIZES]
+    lr, b1, b2, eps, wd, clip = 1e-3, 0.9, 0.999, 1e-8, 0.01, 1.0
+    sa = (ctypes.c_uint * len(SIZES))(*SIZES)
+    a = [[upload(eng, x) for x in arrs] for arrs in (ws, gs, ms, vs)]   # counted
+    b = [[upload(eng, x) for x in arrs] for arrs in (ws, gs, ms, vs)]   # host step size
+    state = upload(eng, np.zeros(2, np.float32))
+    for t_arg, t in ((5, 5), (0, 6), (0, 7), (2, 2), (0, 3), (1000, 1000)):
+        eng.lib.AdamBatchCounted(*(_arrays(h) for h in a), sa, len(SIZES), state, t_arg, lr, b1, b2,
+                                 eps, lr * wd, clip)
+        st = download(eng, state, (2,))
+        assert int(st[:1].view(np.uint32)[0]) == t
+        step = K.adam_step_size(lr, b1, b2, t)
+        assert abs(float(st[1]) - float(np.float32(step))) <= 2.0 ** -23 * step, (t, st[1], step)
+        eng.lib.AdamBatch(*(_arrays(h) for h in b), sa, len(SIZES), float(st[1]), b1, b2, eps, lr * wd,
+                          clip)
+        for i in range(len(SIZES)):
+            for j in (0, 2, 3):
+                assert np.array_equal(download(eng, a[j][i], (SIZES[i],)),
+                                      download(eng, b[j][i], (SIZES[i],))), (t, i, j)
+    eng.lib.ClearLastError()
+    short = upload(eng, np.zeros(1, np.float32))
+    eng.lib.AdamBatchCounted(*(_arrays(h) for h in a), sa, len(SIZES), short, 1, lr, b1, b2, eps, 0.0, clip)
+    assert "2 floats" in eng.last_error()
+    release(eng, *[h for arrs in a + b for h in arrs], state, short)
 
 
 def test_norm_clip_shaders(eng):
@@ -552,4 +656,14 @@ def test_run_sequence(eng):
     sa = (ctypes.c_uint * 1)(n)
     eng.lib.RunSequenceWithSGD(ctypes.byref(cmds), 1, _arrays([hw]), _arrays([ho]), sa, 1, 0.1, 1.0)
     assert rel_err(download(eng, hw, (n,)), K.sgd(x, K.relu_grad(g, x), 0.1, 1.0)) <= 1e-6
+    # a shader pointer that is not a registry entry is refused before it is
+    # read: one inside the table but between entries, and host memory
+    before = download(eng, ho, (n,))
+    junk = (ctypes.c_char * 64)()
+    for bogus in (cmds[0].shader + 1, ctypes.addressof(junk)):
+        cmds[0].shader = bogus
+        eng.lib.ClearLastError()
+        eng.lib.RunSequence(ctypes.byref(cmds), 1)
+        assert "unresolved shader pointer" in eng.last_error()
+    assert np.array_equal(download(eng, ho, (n,)), before)
     release(eng, hg, hx, ho, hw)

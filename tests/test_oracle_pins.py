@@ -266,6 +266,54 @@ def test_bias_ops_vs_autograd():
     close(K.bias_grad(A.T.copy(), 6, 9, 1, 6), A.sum(axis=0))
 
 
+def test_add_bias_linear_layer_vs_autograd():
+    """K.add_bias and the engine's AddBias backward (dA = g, db = column sums
+    of g) as the last Linear layer of LeNet / AlexNet uses them: x @ W + b,
+    (in, out) weights, against torch autograd."""
+    r = rng(43)
+    x, W, b = r.standard_normal((5, 7)), r.standard_normal((7, 4)), r.standard_normal(4)
+    g = r.standard_normal((5, 4))
+    xt, Wt, bt = t64(x, True), t64(W, True), t64(b, True)
+    y = xt @ Wt + bt
+    y.backward(t64(g))
+    close(K.add_bias(x @ W, b), y.detach().numpy())
+    xo, Wo, bo = E.T(x, True), E.T(W, True), E.T(b, True)
+    out = E.add_bias(E.matmul(xo, Wo), bo)
+    close(out.data, y.detach().numpy())
+    out._backward(g)
+    # the matmul node received dA = g; run it to reach x and W
+    mm = out._parents[0]
+    mm._backward(mm.grad)
+    close(bo.grad, bt.grad.numpy())
+    close(Wo.grad, Wt.grad.numpy())
+    close(xo.grad, xt.grad.numpy())
+    # a bias row broadcast over a single row and over many rows
+    close(K.add_bias(np.zeros((1, 4)), b), b[None, :])
+    close(K.add_bias(np.ones((300, 4)), b), 1.0 + np.tile(b, (300, 1)))
+
+
+def test_grad_accum_fan_out_vs_autograd():
+    """Gradient accumulation (K.grad_accum, the oracle's only way of adding a
+    second gradient to a tensor) through a graph where one tensor feeds three
+    consumers, one of them twice, against torch autograd."""
+    r = rng(44)
+    x = r.standard_normal((3, 6))
+    w = r.standard_normal((6, 6))
+    xt, wt = t64(x, True), t64(w, True)
+    h = xt @ wt
+    y = F.relu(h) + torch.sigmoid(h) + h * 1.0 + h
+    y.sum().backward()
+    xo, wo = E.T(x, True), E.T(w, True)
+    ho = E.matmul(xo, wo)
+    yo = E.add(E.add(E.add(E.relu(ho), E.sigmoid(ho)), ho), ho)
+    yo.backward()
+    close(xo.grad, xt.grad.numpy())
+    close(wo.grad, wt.grad.numpy())
+    # the kernel itself: acc + g, repeated accumulation, float32 operands
+    a, g = r.standard_normal(9).astype(np.float32), r.standard_normal(9).astype(np.float32)
+    close(K.grad_accum(K.grad_accum(a, g), g), a.astype(np.float64) + 2 * g.astype(np.float64))
+
+
 def test_pool_resample_plumbing_vs_autograd():
     r = rng(42)
     x = r.standard_normal((2, 3, 4, 5))
@@ -352,7 +400,25 @@ def test_sgd_and_norm_clip_vs_torch():
         pt.grad = torch.clamp(t64(g), -1.0, 1.0)
         torch.optim.SGD([pt], lr=0.05).step()
         close(K.sgd(w, g, 0.05, 1.0), pt.detach().numpy())
-        close(K.sgd_clipped(w, g, 0.05, scale), w - 0.05 * g * scale)
+
+
+@pytest.mark.parametrize("max_norm", [1.0, 1e3], ids=["clipped", "unclipped"])
+def test_sgd_clipped_vs_torch(max_norm):
+    """SGDBatchClipped's update (K.grad_norm_scale, then K.sgd_clipped per
+    tensor) equals torch.optim.SGD stepping on gradients scaled in place by
+    clip_grad_norm_ (same coefficient max/(norm + 1e-6))."""
+    r = rng(72)
+    ws = [r.standard_normal(n) for n in (3, 11, 40)]
+    gs = [r.standard_normal(n) * 2 for n in (3, 11, 40)]
+    pts = [t64(w, True) for w in ws]
+    for p, g in zip(pts, gs):
+        p.grad = t64(g)
+    torch.nn.utils.clip_grad_norm_(pts, max_norm)
+    torch.optim.SGD(pts, lr=0.05).step()
+    norm, scale = K.grad_norm_scale(gs, max_norm)
+    assert (scale < 1.0) == (max_norm == 1.0)
+    for w, g, p in zip(ws, gs, pts):
+        close(K.sgd_clipped(w, g, 0.05, scale), p.detach().numpy())
 
 
 def test_adamw_vs_torch_three_steps():
