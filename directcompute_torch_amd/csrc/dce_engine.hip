@@ -483,6 +483,7 @@ bool InitEngine(void) {
     set_error("InitEngine: scratch allocation failed");
     return false;
   }
+  if (!noalloc_setup(g_device)) return false;
   g_init = true;
   g_err[0] = 0;
   return true;
@@ -946,6 +947,15 @@ void AdamBatchCounted(void** params, void** grads, void** m, void** v, uint32_t*
   }
   adam_counted_multi(params, grads, m, v, sizes, numParams, st->ptr, t, lr, beta1, beta2, eps,
                      weightDecay, clip);
+}
+
+float ClipGradNormNoAlloc(void** grads, uint32_t* sizes, uint32_t numGrads, float maxNorm) {
+  if (!g_init) {
+    set_error("ClipGradNormNoAlloc: engine not initialised");
+    return -1.0f;
+  }
+  if (!grads || !sizes || !numGrads) return 0.0f;
+  return clip_grad_norm_noalloc(g_device, grads, sizes, numGrads, maxNorm, g_capturing);
 }
 
 // ----------------------------------------------------------------- profiling

@@ -357,5 +357,11 @@ bool adam_multi(void** params, void** grads, void** m, void** v, const uint32_t*
 bool adam_counted_multi(void** params, void** grads, void** m, void** v,
                         const uint32_t* sizes, uint32_t n, float* state, uint32_t t_set,
                         double lr, double b1, double b2, float eps, float wd, float clip);
+// Static-scratch norm clip (no allocation): noalloc_setup records the scratch
+// array's address on `device` (which must be current); clip_grad_norm_noalloc
+// returns the norm, NaN while capturing, or -1 with the error set.
+bool noalloc_setup(int device);
+float clip_grad_norm_noalloc(int device, void** grads, const uint32_t* sizes, uint32_t n,
+                             float max_norm, bool capturing);
 
 }  // namespace dce

@@ -447,4 +447,137 @@ bool adam_counted_multi(void** params, void** grads, void** m, void** v,
   return true;
 }
 
+// ---------------------------------------------------------------------------
+// Norm clip without allocation.  Callers that may not allocate device memory
+// (code under HIP graph capture, tight serving loops) get the kernels of
+// ClipGradNorm with their scratch -- the per-block partial sums and the
+// [norm, scale] pair -- in this file-scope array instead of the growable
+// workspace.  kNoAllocParts partials cover up to kNoAllocParts * kChunk
+// gradient elements (fewer when tensors end inside a chunk).  Each GPU holds
+// its own copy of the array, at its own address, until the process ends; the
+// host uses only the address hipGetSymbolAddress reports for the current
+// device (the array's name is a host-side stand-in, not a device address).
+// Every call on a GPU shares that GPU's copy: calls overlapping on one GPU
+// would race, which the library's single in-order stream rules out for its
+// own calls.  Every partial is written before it is read, and the pair is
+// written by the final kernel, so nothing needs clearing between calls.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kNoAllocParts = 65536;
+constexpr uint32_t kNoAllocDoubles = kNoAllocParts + 32;  // partials, then the pair
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) double scratch[kNoAllocDoubles];
+static double* g_scratchDev[kMaxDevices];
+
+bool noalloc_setup(int device) {
+  if (device < 0 || device >= kMaxDevices) {
+    set_error("InitEngine: device %d beyond the %d the scratch table holds", device, kMaxDevices);
+    return false;
+  }
+  if (g_scratchDev[device]) return true;
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p) {
+    hipGetLastError();
+    set_error("InitEngine: hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+    return false;
+  }
+  g_scratchDev[device] = static_cast<double*>(p);
+  return true;
+}
+
+float clip_grad_norm_noalloc(int device, void** grads, const uint32_t* sizes, uint32_t n,
+                             float max_norm, bool capturing) {
+  double* part = (device >= 0 && device < kMaxDevices) ? g_scratchDev[device] : nullptr;
+  if (!part) {
+    set_error("ClipGradNormNoAlloc: no scratch address for device %d", device);
+    return -1.0f;
+  }
+  float* ns = reinterpret_cast<float*>(part + kNoAllocParts);
+  // Pass 1: validate every handle and count the partials, before any launch.
+  uint64_t total = 0;
+  for (uint32_t i = 0; i < n; ++i) {
+    if (!grads[i]) continue;
+    Buffer* G = as_buffer(grads[i], "ClipGradNormNoAlloc(grad)");
+    if (!G) return -1.0f;
+    total += cdiv(std::min(sizes[i], G->count), kChunk);
+  }
+  if (total > kNoAllocParts) {
+    set_error("ClipGradNormNoAlloc: %llu partial sums exceed the %u of the static scratch "
+              "(at most %u chunks of %u gradient elements)",
+              (unsigned long long)total, kNoAllocParts, kNoAllocParts, kChunk);
+    return -1.0f;
+  }
+  // Pass 2: the Σg² partials, one table of at most kMaxT tensors per launch.
+  const bool nt = stream_nt(4.0 * double(total) * kChunk);
+  Table t{};
+  uint32_t base = 0, blocks = 0;
+  auto flush_sumsq = [&]() -> bool {
+    if (!t.count) return true;
+    t.start[t.count] = blocks;
+    if (nt)
+      hipLaunchKernelGGL(k_multi_sumsq<true>, dim3(blocks), dim3(256), 0, stream(), t, part, base);
+    else
+      hipLaunchKernelGGL(k_multi_sumsq<false>, dim3(blocks), dim3(256), 0, stream(), t, part, base);
+    base += blocks;
+    t = Table{};
+    blocks = 0;
+    return check_launch("ClipGradNormNoAlloc(sumsq)");
+  };
+  for (uint32_t i = 0; i < n; ++i) {
+    if (!grads[i]) continue;
+    Buffer* G = static_cast<Buffer*>(grads[i]);
+    const uint32_t cnt = std::min(sizes[i], G->count);
+    if (!cnt) continue;
+    if (t.count == kMaxT && !flush_sumsq()) return -1.0f;
+    t.g[t.count] = G->ptr;
+    t.n[t.count] = cnt;
+    t.start[t.count] = blocks;
+    t.count++;
+    blocks += cdiv(cnt, kChunk);
+  }
+  if (!flush_sumsq()) return -1.0f;
+  hipLaunchKernelGGL(k_norm_final, dim3(1), dim3(1024), 0, stream(), part, base, max_norm, ns);
+  if (!check_launch("ClipGradNormNoAlloc(final)")) return -1.0f;
+  // Pass 3: scale in place when the norm exceeds max_norm (read on the device).
+  ScaleDev op;
+  op.scale = 1.f;
+  t = Table{};
+  blocks = 0;
+  auto flush_scale = [&]() -> bool {
+    if (!t.count) return true;
+    t.start[t.count] = blocks;
+    if (nt)
+      hipLaunchKernelGGL((k_multi_devscale<ScaleDev, 2, 2, true>), dim3(blocks), dim3(256), 0,
+                         stream(), t, op, ns);
+    else
+      hipLaunchKernelGGL((k_multi_devscale<ScaleDev, 2, 2, false>), dim3(blocks), dim3(256), 0,
+                         stream(), t, op, ns);
+    t = Table{};
+    blocks = 0;
+    return check_launch("ClipGradNormNoAlloc(scale)");
+  };
+  for (uint32_t i = 0; i < n; ++i) {
+    if (!grads[i]) continue;
+    Buffer* G = static_cast<Buffer*>(grads[i]);
+    const uint32_t cnt = std::min(sizes[i], G->count);
+    if (!cnt) continue;
+    if (t.count == kMaxT && !flush_scale()) return -1.0f;
+    t.g[t.count] = G->ptr;
+    t.n[t.count] = cnt;
+    t.start[t.count] = blocks;
+    t.count++;
+    blocks += cdiv(cnt, kChunk);
+  }
+  if (!flush_scale()) return -1.0f;
+  if (capturing) return std::nanf("");  // the norm exists only when the graph runs
+  float h[2] = {0.f, 0.f};
+  if (hipMemcpyAsync(h, ns, sizeof(h), hipMemcpyDeviceToHost, stream()) != hipSuccess ||
+      hipStreamSynchronize(stream()) != hipSuccess) {
+    hipGetLastError();
+    set_error("ClipGradNormNoAlloc: reading the norm back failed");
+    return -1.0f;
+  }
+  return h[0];
+}
+
 }  // namespace dce

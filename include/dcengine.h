@@ -206,6 +206,20 @@ void AdamBatchCounted(void** params, void** grads, void** m, void** v, uint32_t*
                       uint32_t numParams, void* stepState, uint32_t t, double lr,
                       double beta1, double beta2, float eps, float weightDecay, float clip);
 
+/* ClipGradNorm that allocates nothing.  It has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same kernels, arguments and result as ClipGradNorm, but the partial sums
+ * live in a static device array of 65536 doubles (512 KiB, held by every GPU
+ * the library runs on until the process ends) instead of the growable
+ * workspace: at most 65536 chunks of 4096 gradient elements (268,435,456
+ * elements when every tensor fills its chunks; each tensor rounds up to whole
+ * chunks).  Larger requests are refused: returns -1 and sets the error.
+ * Calls on one GPU share its array, so calls that overlap on one GPU race;
+ * the library's single stream keeps its own calls in order.  Blocking;
+ * returns the norm (NaN while a capture is open). */
+float ClipGradNormNoAlloc(void** grads, uint32_t* sizes, uint32_t numGrads, float maxNorm);
+
 /* Kernel-family timing with HIP events on the engine stream (for bench.py).
  * SetProfiling(1) starts recording every launch of the named families;
  * GetProfile returns launches, summed milliseconds, summed algorithmic
