@@ -9,13 +9,20 @@ clip 1.0) of all 61.1 M parameters, through the drop-in ``nn_engine`` API.
 Inputs are synthetic and already resident in device memory when the timed
 region starts.  Prints ONE JSON line on stdout; diagnostics go to stderr.
 
-Roofline object: the conv-backward implicit-GEMM kernels (dW and dX, all
-layers of one step) timed with HIP events on the engine stream over the timed
-region; achieved = algorithmic FLOPs (2*OC*C*k*k*B*OH*OW per dW and per dX;
-c1 has no dX since the input needs no gradient) / summed kernel time.
+Roofline object: the conv backward of every layer of one step -- each
+ConvBackwardFused call as a whole: the masked NHWC transpose of dy with its
+bias-gradient partials, the bias-gradient sum, the filter re-layout, the dW and
+dX implicit-GEMM kernels and their split-K finishes -- timed with HIP events on
+the engine stream over the timed region; achieved = algorithmic FLOPs
+(2*OC*C*k*k*B*OH*OW per dW and per dX; c1 has no dX since the input needs no
+gradient) / summed call time.  The GEMM kernels alone are reported beside it.
+
+A second timed pass uploads a fresh batch from host memory every step, as the
+reference's training loop does (train_alexnet.py:110); its rate is reported as
+`value_upload_inclusive`, never as `value`.
 
 cpu_baseline: the float64 NumPy oracle running the same train step on a
-64-image sample on the host, timed on this machine.
+256-image sample on the host, timed on this machine.
 """
 from __future__ import annotations
 
@@ -47,7 +54,8 @@ FCS = [("l1", 9216, 4096, True), ("l2", 4096, 4096, True), ("l3", 4096, 1000, Fa
 BATCH = 128
 SEED = 5 * 1000
 # Kernel families timed (HIP events) during the timed steps; no others record.
-BENCH_FAMILIES = ("conv_dw", "conv_dx", "conv_fwd", "gemm", "maxpool_fwd", "maxpool_bwd", "adam")
+BENCH_FAMILIES = ("conv_bwd", "conv_dw", "conv_dx", "conv_fwd", "gemm", "maxpool_fwd", "maxpool_bwd",
+                  "adam")
 
 
 TRAFFIC_PROFILE = os.path.join(REPO, "profiles", "alexnet224_b128_conv_bwd_hbm_traffic.md")
@@ -131,9 +139,8 @@ def build_alexnet(nn, params):
     return AlexNet()
 
 
-def cpu_baseline(sample=256):
-    """Time the float64 oracle on the same train step for `sample` images."""
-    from oracle import models as OM
+def _blas_info():
+    """(threads the host BLAS uses, its name and version)."""
     threads = os.cpu_count() or 1
     blas = "unknown"
     try:
@@ -144,6 +151,64 @@ def cpu_baseline(sample=256):
             blas = f"{info[0].get('internal_api')} {info[0].get('version')}"
     except Exception:
         pass
+    return threads, blas
+
+
+def _time_oracle(fn, images_per_call, budget_s=10.0):
+    """Call fn() until budget_s seconds have passed (at least once); returns
+    (images per second, calls, seconds)."""
+    calls, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        calls += 1
+        dt = time.perf_counter() - t0
+        if dt >= budget_s:
+            return images_per_call * calls / dt, calls, dt
+
+
+def cpu_baseline_config(cid, budget_s=10.0):
+    """The float64 oracle on a bounded sample of configuration `cid`'s step,
+    timed on the host (about budget_s seconds); same seeds as the GPU run."""
+    from oracle import models as OM
+    threads, blas = _blas_info()
+    r = np.random.default_rng
+    if cid == 1:
+        P = OM.he_params(r(1001), OM.LENET_CONVS, OM.LENET_FCS)
+        x = r(1000).standard_normal((64, 1, 28, 28)).astype(np.float32)
+        y = r(1002).integers(0, 10, 64).astype(np.float32)
+        n, what = 64, "LeNet-5 train steps (fwd + bwd + SGD) at batch 64"
+        fn = lambda: OM.lenet_step(P, x, y)
+    elif cid == 2:
+        n = 8
+        w = (r(2001).standard_normal((128, 64, 3, 3)) * np.sqrt(2.0 / 576)).astype(np.float32)
+        x = r(2000).standard_normal((n, 64, 56, 56)).astype(np.float32)
+        dy = r(2002).standard_normal((n, 128, 56, 56)).astype(np.float32)
+        what = f"conv backward (mask, dW, db, dX) of {n} of the 128 images"
+        fn = lambda: OM.conv_backward_step(x, w, dy)
+    elif cid == 3:
+        n = 2
+        P = OM.mobilenet_stack_params(r(3001))
+        x = r(3000).standard_normal((n, 16, 112, 112)).astype(np.float32)
+        y = r(3002).integers(0, 10, n).astype(np.float32)
+        what = f"MobileNetV2-stack train steps (fwd + bwd + SGD) on {n} of the 64 images"
+        fn = lambda: OM.mobilenet_stack_step(P, x, y)
+    else:
+        n = 1
+        P = OM.unet_params(r(4001))
+        x = r(4000).random((n, 3, 256, 256)).astype(np.float32)
+        m = (r(4002).random((n, 1, 32, 32)) < 0.3).astype(np.float32)
+        t = m.repeat(8, axis=2).repeat(8, axis=3)
+        what = f"UNet-base16 train steps (fwd + Dice + bwd + clip + Adam) on {n} of the 8 images"
+        fn = lambda: OM.unet_step(P, x, t)
+    rate, calls, dt = _time_oracle(fn, n, budget_s)
+    return {"value": round(rate, 3), "unit": "img/s", "cores": threads, "kind": "port",
+            "sample": f"{calls} x {what}, float64 NumPy oracle, {blas}, {dt:.1f} s"}
+
+
+def cpu_baseline(sample=256):
+    """Time the float64 oracle on the same train step for `sample` images."""
+    from oracle import models as OM
+    threads, blas = _blas_info()
     rng = np.random.default_rng(SEED + 1)
     params = he_params(rng)
     x = np.random.default_rng(SEED).standard_normal((sample, 3, 224, 224)).astype(np.float32)
@@ -351,7 +416,7 @@ def memory_suite(reps=10):
 
 def _prof_all(lib):
     """Every kernel family's (launches, ms, flops, bytes) recorded so far."""
-    fams = ("conv_fwd", "conv_dw", "conv_dx", "gemm", "maxpool_fwd", "maxpool_bwd", "bn_stats",
+    fams = ("conv_bwd", "conv_fwd", "conv_dw", "conv_dx", "gemm", "maxpool_fwd", "maxpool_bwd", "bn_stats",
             "bn_bwd_reduce", "dw_bwd_input", "dw_bwd_filter", "gap_bwd", "upsample_bwd",
             "dice_loss_grad", "bias_grad", "sgd", "adam", "grad_norm", "clip_scale",
             "relu_grad", "relu6_grad", "sigmoid_grad", "grad_accum", "batchnorm_backward_dx",
@@ -365,7 +430,7 @@ def _prof_all(lib):
     return out
 
 
-def configs_suite(steps=10, warmup=3, ids=None):
+def configs_suite(steps=10, warmup=3, ids=None, cpu=True):
     """The other measured configurations of the backward path, each a full
     training step through the nn_engine API (synthetic inputs, seeds
     1000*config + {0: x, 1: weights, 2: labels}):
@@ -392,7 +457,7 @@ def configs_suite(steps=10, warmup=3, ids=None):
     def ones(n, rg=True):
         return T(np.ones(n), rg)
 
-    def run_config(cid, name, batch, step, extra=None):
+    def run_config(cid, name, batch, step, extra=None, mode="eager"):
         for _ in range(warmup):
             step()
         lib.SyncGPU()
@@ -408,11 +473,12 @@ def configs_suite(steps=10, warmup=3, ids=None):
         lib.GetPoolStats(ctypes.byref(h1), ctypes.byref(m1))
         pool = {"hits_per_step": (h1.value - h0.value) / steps, "misses_per_step": (m1.value - m0.value) / steps}
         lib.ResetProfile()
-        lib.SetProfiling(1)
-        for _ in range(steps):
-            step()
-        lib.SyncGPU()
-        lib.SetProfiling(0)
+        if mode == "eager":   # a graph replay records no per-family events
+            lib.SetProfiling(1)
+            for _ in range(steps):
+                step()
+            lib.SyncGPU()
+            lib.SetProfiling(0)
         fams = {}
         for f, (n, ms, fl, by) in _prof_all(lib).items():
             rec = {"launches_per_step": round(n / steps, 2), "ms_per_step": round(ms / steps, 4)}
@@ -423,22 +489,27 @@ def configs_suite(steps=10, warmup=3, ids=None):
                 gb = by / (ms * 1e-3) / 1e9
                 rec.update({"GB/s": round(gb, 1), "frac_hbm": round(gb / HBM_PEAK_GBS, 4)})
             fams[f] = rec
-        dw, dx = fams.get("conv_dw"), fams.get("conv_dx")
         bwd = None
-        if dw:
-            fl = sum(v[2] for k, v in _prof_all(lib).items() if k in ("conv_dw", "conv_dx"))
-            ms = sum(v[1] for k, v in _prof_all(lib).items() if k in ("conv_dw", "conv_dx"))
+        allf = _prof_all(lib)
+        if "conv_bwd" in allf:
+            _, ms, fl, _ = allf["conv_bwd"]
+            ms_g = sum(v[1] for k, v in allf.items() if k in ("conv_dw", "conv_dx"))
             tf = fl / (ms * 1e-3) / 1e12
             bwd = {"gflop_per_step": round(fl / steps / 1e9, 2), "ms_per_step": round(ms / steps, 4),
-                   "TFLOP/s": round(tf, 2), "frac_mfma": round(tf / MFMA_FP32_PEAK_TFLOPS, 4)}
-        rec = {"suite": "configs", "config": cid, "workload": name, "batch": batch,
+                   "TFLOP/s": round(tf, 2), "frac_mfma": round(tf / MFMA_FP32_PEAK_TFLOPS, 4),
+                   "gemm_kernels_ms_per_step": round(ms_g / steps, 4),
+                   "gemm_kernels_frac_mfma": round(fl / (ms_g * 1e-3) / 1e12 / MFMA_FP32_PEAK_TFLOPS, 4)}
+        rec = {"suite": "configs", "config": cid, "mode": mode, "workload": name, "batch": batch,
                "ms_per_step": round(dt * 1e3, 4), "img_s": round(batch / dt, 1),
                "host_issue_ms_per_step": round(th * 1e3, 4),
                "conv_bwd": bwd, "pool": pool, "families": fams}
         if extra:
             rec.update(extra)
+        if cpu and mode == "eager":
+            nn.end_batch()
+            rec["cpu_baseline"] = cpu_baseline_config(cid)
         print(json.dumps(rec), flush=True)
-        log(f"[configs] {cid} {name}: {dt * 1e3:.3f} ms/step (host issue {th * 1e3:.3f}), {batch / dt:.0f} img/s"
+        log(f"[configs] {cid} {mode} {name}: {dt * 1e3:.3f} ms/step (host issue {th * 1e3:.3f}), {batch / dt:.0f} img/s"
             + (f"; conv-bwd {bwd['TFLOP/s']} TFLOP/s ({bwd['frac_mfma'] * 100:.1f}%)" if bwd else "")
             + f"; pool misses/step {pool['misses_per_step']:.1f} of {pool['hits_per_step'] + pool['misses_per_step']:.1f}")
         nn.end_batch()
@@ -463,6 +534,18 @@ def configs_suite(steps=10, warmup=3, ids=None):
             opt.step(clip=1.0)
             nn.end_batch()
         run_config(1, "LeNet-5 b64 train step (SGD lr 0.01, clip 1.0)", 64, lenet_step)
+
+        def lenet_fwd(xb):
+            h = nn.maxpool2d(nn.conv2d(xb, P[0], P[1], 1, 0, 1), 2, 2)
+            h = nn.flatten(nn.maxpool2d(nn.conv2d(h, P[2], P[3], 1, 0, 1), 2, 2))
+            h = nn.bias_relu(nn.matmul(h, P[4]), P[5])
+            h = nn.bias_relu(nn.matmul(h, P[6]), P[7])
+            return nn.add_bias(nn.matmul(h, P[8]), P[9])
+        graph = nn.ComputeGraph()
+        graph.trace(lenet_fwd, opt, x.sync(), y.sync(), P, clip=1.0)
+        run_config(1, "LeNet-5 b64 train step (SGD lr 0.01, clip 1.0), replayed with ComputeGraph",
+                   64, graph.replay, mode="graph")
+        graph.release()
 
     # 2 single conv backward
     def config2():
@@ -553,9 +636,8 @@ def configs_suite(steps=10, warmup=3, ids=None):
             w, bb, g, be, rm, rv = U[name]
             return nn.relu(nn.batchnorm2d(nn.conv2d(h, w, bb, 1, 1, 0), g, be, rm, rv))
 
-        def unet_step():
-            opt4.zero_grad()
-            h = x4
+        def unet_fwd(xb):
+            h = xb
             skips = []
             for i in range(4):
                 h = cbr(cbr(h, f"e{i}a"), f"e{i}b")
@@ -565,13 +647,21 @@ def configs_suite(steps=10, warmup=3, ids=None):
             for i in reversed(range(4)):
                 h = nn.concat([nn.upsample2d(h, 2, 2), skips[i]])
                 h = cbr(cbr(h, f"d{i}a"), f"d{i}b")
-            loss = nn.dice_loss(nn.sigmoid(nn.conv2d(h, head[0], head[1], 1, 0, 0)), t4)
+            return nn.sigmoid(nn.conv2d(h, head[0], head[1], 1, 0, 0))
+
+        def unet_step():
+            opt4.zero_grad()
+            loss = nn.dice_loss(unet_fwd(x4), t4)
             loss.backward()
             nn.clip_grad_norm(Pu, 1.0)
             opt4.step(clip=1e30)
             nn.end_batch()
-        run_config(4, "UNet-base16 b8 @256^2 (4 levels, conv3x3-BN-ReLU x2, Dice on sigmoid; "
-                      "norm clip 1.0 + Adam lr 1e-3)", 8, unet_step)
+        name4 = "UNet-base16 b8 @256^2 (4 levels, conv3x3-BN-ReLU x2, Dice on sigmoid; norm clip 1.0 + Adam lr 1e-3)"
+        run_config(4, name4, 8, unet_step)
+        graph = nn.ComputeGraph()
+        graph.trace(unet_fwd, opt4, x4.sync(), t4.sync(), Pu, clip=1e30, loss_fn=nn.dice_loss, max_norm=1.0)
+        run_config(4, name4 + ", replayed with ComputeGraph", 8, graph.replay, mode="graph")
+        graph.release()
 
     for cid, fn in ((1, config1), (2, config2), (3, config3), (4, config4)):
         if not ids or cid in ids:
@@ -621,7 +711,8 @@ def main():
         return
     if args.suite == "configs":
         ids = {int(v) for v in args.configs.split(",")} if args.configs else None
-        configs_suite(steps=min(args.steps, 10), warmup=args.warmup, ids=ids)
+        configs_suite(steps=min(args.steps, 10), warmup=args.warmup, ids=ids,
+                      cpu=not args.no_cpu_baseline)
         return
 
     from directcompute_torch_amd import nn_engine as nn
@@ -679,15 +770,40 @@ def main():
             log(f"[bench] {f:12s} launches/step {n / args.steps:5.1f}  ms/step {ms / args.steps:8.3f}  {extra}")
     n_dw, ms_dw, fl_dw, _ = fams["conv_dw"]
     n_dx, ms_dx, fl_dx, _ = fams["conv_dx"]
-    ms_bwd = ms_dw + ms_dx
-    fl_bwd = fl_dw + fl_dx
+    n_bwd, ms_bwd, fl_bwd, _ = fams["conv_bwd"]
+    ms_gemm = ms_dw + ms_dx
     expect = conv_bwd_flops(BATCH) * args.steps
-    if abs(fl_bwd - expect) > 1e-6 * expect:
-        log(f"[bench] WARNING conv-bwd FLOP count {fl_bwd:.4e} != expected {expect:.4e}")
+    for what, fl in (("conv-bwd calls", fl_bwd), ("conv-bwd GEMMs", fl_dw + fl_dx)):
+        if abs(fl - expect) > 1e-6 * expect:
+            log(f"[bench] WARNING {what} FLOP count {fl:.4e} != expected {expect:.4e}")
     achieved = fl_bwd / (ms_bwd * 1e-3) / 1e12 if ms_bwd > 0 else 0.0
+    achieved_gemm = fl_bwd / (ms_gemm * 1e-3) / 1e12 if ms_gemm > 0 else 0.0
     log(f"[bench] {img_s:.1f} img/s, {dt * 1e3:.2f} ms/step; conv-bwd {achieved:.2f} TFLOP/s "
-        f"({achieved / MFMA_FP32_PEAK_TFLOPS * 100:.1f}% of fp32 MFMA peak), "
-        f"{ms_bwd / args.steps:.3f} ms/step in conv-bwd kernels")
+        f"({achieved / MFMA_FP32_PEAK_TFLOPS * 100:.1f}% of fp32 MFMA peak) over "
+        f"{ms_bwd / args.steps:.3f} ms/step of ConvBackwardFused calls; their GEMM kernels alone "
+        f"{achieved_gemm:.2f} TFLOP/s over {ms_gemm / args.steps:.3f} ms/step")
+
+    # The same step with a fresh batch uploaded from (pageable) host memory
+    # every step, as the reference's loop does.
+    host_x = np.random.default_rng(SEED).standard_normal((BATCH, 3, 224, 224)).astype(np.float32)
+
+    def step_upload():
+        opt.zero_grad()
+        xb = nn.Tensor(host_x, track=True)
+        loss = nn.softmax_ce(model(xb), y)
+        loss.backward()
+        opt.step(clip=1.0)
+        nn.end_batch()
+
+    step_upload()
+    lib.SyncGPU()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step_upload()
+    lib.SyncGPU()
+    dt_up = (time.perf_counter() - t0) / args.steps
+    log(f"[bench] with a {host_x.nbytes / 2**20:.0f} MiB host batch uploaded every step: "
+        f"{BATCH / dt_up:.1f} img/s, {dt_up * 1e3:.2f} ms/step")
 
     traffic, alg_bytes = measured_traffic()
     if traffic:
@@ -703,6 +819,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
+        "value_upload_inclusive": round(BATCH / dt_up, 2),
+        "ms_per_step_upload_inclusive": round(dt_up * 1e3, 4),
         "dtype": "fp32",
         "data": "synthetic",
         "config": {
@@ -713,18 +831,24 @@ def main():
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "conv-backward implicit GEMM, all layers: dW k_igemm<LdGradKR,LdXTapKR> (LdPkKR for c1, C = 3) + k_dw_final, dX k_igemm<LdDenseRK,LdPixRK> (+ k_splitk_nchw when split)",
+            "kernel": "conv backward of all layers, each ConvBackwardFused call whole: G pass "
+                      "k_to_nhwc (ReLU mask + NHWC transpose + bias partials), k_rowsum, k_permute_w, "
+                      "dW k_igemm<LdGradKR,LdXTapKR> (LdPkKR for c1, C = 3) + k_dw_final, "
+                      "dX k_igemm<LdDenseRK,LdPixRK> (+ k_splitk_nchw when split)",
             "achieved": round(achieved, 3),
             "peak": MFMA_FP32_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / MFMA_FP32_PEAK_TFLOPS, 4),
+            "gemm_kernels_achieved": round(achieved_gemm, 3),
+            "gemm_kernels_frac": round(achieved_gemm / MFMA_FP32_PEAK_TFLOPS, 4),
             "traffic": traffic,
             "traffic_unit": "HBM bytes per conv-backward GEMM launch incl. its split-K finish "
                             "(rocprofv3 FETCH_SIZE/WRITE_SIZE scaled by a copy kernel; "
                             "profiles/alexnet224_b128_conv_bwd_hbm_traffic.md)" if traffic else None,
             "algorithmic_bytes_per_launch": alg_bytes,
-            "launches_per_step": (n_dw + n_dx) / args.steps,
-            "kernel_ms_per_step": round(ms_bwd / args.steps, 4),
+            "calls_per_step": n_bwd / args.steps,
+            "gemm_launches_per_step": (n_dw + n_dx) / args.steps,
+            "ms_per_step": round(ms_bwd / args.steps, 4),
         },
     }
     if not args.no_cpu_baseline:

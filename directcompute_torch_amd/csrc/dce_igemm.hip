@@ -1840,6 +1840,11 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
   const bool pk = packed_x(g);
   const uint32_t Cx = pk ? g.C : Cp;
   const uint32_t npb = cdiv(OHW, 64);
+  // The whole call as one family: the masked transpose of dy, the bias-grad
+  // sum, any rebuilt copy of x, the filter re-layout and the split-K finishes
+  // count with the GEMMs' FLOPs.
+  const double callFlops = 2.0 * g.OC * g.C * KK * double(npix) * ((dw ? 1 : 0) + (dx ? 1 : 0));
+  ProfScope profAll("conv_bwd", callFlops, 0.0);
   const size_t nG = al64(size_t(npix) * OCp);
   const size_t nDb = db ? al64(size_t(g.B) * npb * g.OC) : 0;
   const size_t nX = (dw && !x_nhwc) ? al64(xcopy_floats(g)) : 0;

@@ -130,6 +130,15 @@ def release_all_buffers():
             t._ctx.inputs = ()
             t._ctx = None
         t.grad = None
+        # A cached traversal order contains the tensor itself: dropping it
+        # breaks that cycle, so the tensors it lists (untracked views such as
+        # Flatten's, which hold a reference on their buffer) are freed now
+        # rather than by a later cyclic garbage collection, and their buffers
+        # are back in the pool before the next step asks for them.
+        try:
+            del t._cached_topo
+        except AttributeError:
+            pass
         if t.gpu_buf:
             handles.append(t.gpu_buf)
             t.gpu_buf = None
@@ -1226,13 +1235,17 @@ class ComputeGraph:
             lib.UpdateBuffer(self._handles[key], _fptr(eager[key]))
         return loss, logits
 
-    def replay(self, X_batch, Y_batch):
+    def replay(self, X_batch=None, Y_batch=None):
         """Upload a new batch into the traced input / label buffers and enqueue
-        one replay of the step."""
+        one replay of the step.  A batch given as None is not uploaded: the
+        step then runs on what the buffer holds (the last batch, or data a
+        caller wrote into input_tensor() / label_tensor() on the device)."""
         if not self._compiled:
             raise RuntimeError("Graph not compiled. Call trace() first.")
-        self._upload("input", X_batch)
-        self._upload("labels", Y_batch)
+        if X_batch is not None:
+            self._upload("input", X_batch)
+        if Y_batch is not None:
+            self._upload("labels", Y_batch)
         if not lib.ReplayGraph(self._graph):
             raise RuntimeError(f"ReplayGraph failed: {last_error()}")
         if hasattr(self._optimizer, "t"):
@@ -1250,6 +1263,18 @@ class ComputeGraph:
 
     def read_logits(self):
         return self._read("logits")
+
+    def _view(self, key):
+        lib.AddRefBuffer(self._handles[key])
+        return Tensor.from_gpu(self._handles[key], self._shapes[key], track=False)
+
+    def input_tensor(self):
+        """The traced input buffer as a tensor (a new reference), so that a
+        batch already on the device can be copied in without a host trip."""
+        return self._view("input")
+
+    def label_tensor(self):
+        return self._view("labels")
 
     def release(self):
         """Free the graph, the buffers it holds and the input / label buffers."""

@@ -508,3 +508,80 @@ def test_engine64_mobilenet_block_vs_autograd():
     close(xo.grad, xt.grad.numpy(), 1e-9)
     for k in ("e", "g1", "b1", "d", "g2", "b2", "p", "g3", "b3"):
         close(O[k].grad, T[k].grad.numpy(), 1e-9)
+
+
+# ------------------------------------------------------- benchmark steps
+def _bn_train(h, g, b):
+    return F.batch_norm(h, None, None, g, b, training=True, eps=1e-5)
+
+
+def test_mobilenet_stack_step_vs_autograd():
+    """oracle.models.mobilenet_stack_step (the CPU baseline of the MobileNetV2
+    stack) against the same network in torch autograd, then SGD."""
+    from oracle import models as OM
+    r = rng(90)
+    P = OM.mobilenet_stack_params(r)
+    for k in P:                                   # non-trivial BN affine terms
+        if k.endswith(".g"):
+            P[k] = (1 + 0.2 * r.standard_normal(P[k].shape)).astype(np.float32)
+        elif k.endswith(".be") or k.endswith(".b"):
+            P[k] = (0.1 * r.standard_normal(P[k].shape)).astype(np.float32)
+    x = r.standard_normal((2, 16, 12, 12)).astype(np.float32)
+    lab = r.integers(0, 10, 2).astype(np.float32)
+    T = {k: t64(v, True) for k, v in P.items()}
+    h = t64(x)
+    for i, (ci, co, s) in enumerate(OM.MBV2_BLOCKS):
+        t = F.hardtanh(_bn_train(F.conv2d(h, T[f"b{i}.exp.w"], T[f"b{i}.exp.b"]), T[f"b{i}.bn1.g"],
+                                 T[f"b{i}.bn1.be"]), 0, 6)
+        t = F.conv2d(t, T[f"b{i}.dw.w"], T[f"b{i}.dw.b"], stride=s, padding=1, groups=ci * 6)
+        t = F.hardtanh(_bn_train(t, T[f"b{i}.bn2.g"], T[f"b{i}.bn2.be"]), 0, 6)
+        t = _bn_train(F.conv2d(t, T[f"b{i}.proj.w"], T[f"b{i}.proj.b"]), T[f"b{i}.bn3.g"], T[f"b{i}.bn3.be"])
+        h = t + h if (s == 1 and ci == co) else t
+    z = h.mean(dim=(2, 3)) @ T["fc.w"] + T["fc.b"]
+    loss_t = F.cross_entropy(z, torch.tensor(lab.astype(np.int64)))
+    loss_t.backward()
+    loss, g, new = OM.mobilenet_stack_step(P, x, lab, lr=0.01)
+    assert abs(loss - float(loss_t.detach())) < 1e-9
+    for k in P:
+        close(g[k], T[k].grad.numpy(), 1e-8)
+        close(new[k], P[k].astype(np.float64) - 0.01 * T[k].grad.numpy(), 1e-9)
+
+
+def test_unet_step_vs_autograd():
+    """oracle.models.unet_step (the CPU baseline of the UNet configuration) at
+    two levels against torch autograd: Dice on the sigmoid output, global-norm
+    clip (torch clip_grad_norm_), first Adam step (torch Adam with
+    eps_t = eps / sqrt(1 - b2))."""
+    from oracle import models as OM
+    r = rng(91)
+    P = OM.unet_params(r, base=4, levels=2)
+    x = r.random((2, 3, 8, 8)).astype(np.float32)
+    tg = (r.random((2, 1, 8, 8)) < 0.3).astype(np.float32)
+    T = {k: t64(v, True) for k, v in P.items()}
+
+    def cbr(h, n):
+        return F.relu(_bn_train(F.conv2d(h, T[n + ".w"], T[n + ".b"], padding=1), T[n + ".g"], T[n + ".be"]))
+    h, skips = t64(x), []
+    for i in range(2):
+        h = cbr(cbr(h, f"e{i}a"), f"e{i}b")
+        skips.append(h)
+        h = F.max_pool2d(h, 2)
+    h = cbr(cbr(h, "ba"), "bb")
+    for i in reversed(range(2)):
+        h = torch.cat([F.interpolate(h, scale_factor=2, mode="nearest"), skips[i]], dim=1)
+        h = cbr(cbr(h, f"d{i}a"), f"d{i}b")
+    p = torch.sigmoid(F.conv2d(h, T["head.w"], T["head.b"]))
+    tt = t64(tg)
+    inter = (p * tt).sum([1, 2, 3])
+    dl = 1 - 2 * inter / (p.sum([1, 2, 3]) + tt.sum([1, 2, 3]) + 1e-6)
+    dl.mean().backward()
+    loss, g, new = OM.unet_step(P, x, tg, levels=2, lr=1e-3, max_norm=0.05)
+    assert abs(loss - float(dl.mean())) < 1e-12
+    for k in P:
+        close(g[k], T[k].grad.numpy(), 1e-8)
+    params = [T[k] for k in sorted(P)]
+    torch.nn.utils.clip_grad_norm_(params, 0.05)
+    opt = torch.optim.Adam(params, lr=1e-3, eps=1e-8 / np.sqrt(1 - 0.999))
+    opt.step()
+    for k in P:
+        close(new[k], T[k].detach().numpy(), 1e-9)
