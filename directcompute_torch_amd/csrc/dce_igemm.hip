@@ -622,6 +622,149 @@ struct LdPkKR : LoaderBase<Stage<R, KT, true, false>> {
 };
 
 // ---------------------------------------------------------------------------
+// Stride-phase copy for convolutions over C < 4 channels with stride S <= 4
+// (k_to_ps): xs[((b*Hp + r)*C + c)*S + ph][col] = x[b][c][r - p][col*S + ph
+// - p] (zero outside the image), rows of Ncol floats (Ncol % 4 == 0), Hp =
+// H + 2p.  The output pixels form a padded grid (b, oh, ow) with ow < OWp =
+// pad4(OW); the extra columns are computed and dropped (their G is zero).
+// Tap t = (c*k + kh)*k + kw of output pixel (b, oh, ow) reads
+//   xs[pixel part (b*Hp + oh*S)*RS + ow] + [tap part (kh*C + c)*S*Ncol +
+//   (kw % S)*Ncol + kw / S],  RS = C*S*Ncol,
+// so four consecutive output pixels of one tap are four consecutive floats:
+// a quad never straddles anything (taps or pixels), unlike the channel-packed
+// layout whose tap quads straddle kernel rows.  Quads start at 4-byte
+// alignment (kw / S); the GPU runs with unaligned access enabled.
+// ---------------------------------------------------------------------------
+struct PsParams {
+  const float* src;
+  uint32_t RS, Hp, S, Ncol, C, k, KK, kdim;  // kdim = C*KK taps
+  uint32_t OWp, OHWp, npix, n;               // npix = B*OHWp padded pixels; n: floats
+  FastDiv dOHWp, dOWp, dKK, dK, dS;
+};
+
+__device__ __forceinline__ uint32_t ps_pixel(const PsParams& P, uint32_t n) {
+  const uint32_t b = fdiv(n, P.dOHWp), rem = n - b * P.OHWp;
+  const uint32_t oh = fdiv(rem, P.dOWp), ow = rem - oh * P.OWp;
+  return (b * P.Hp + oh * P.S) * P.RS + ow;
+}
+__device__ __forceinline__ uint32_t ps_tap(const PsParams& P, uint32_t t) {
+  const uint32_t c = fdiv(t, P.dKK), r = t - c * P.KK;
+  const uint32_t kh = fdiv(r, P.dK), kw = r - kh * P.k;
+  const uint32_t cq = fdiv(kw, P.dS), ph = kw - cq * P.S;
+  return ((kh * P.C + c) * P.S + ph) * P.Ncol + cq;
+}
+
+// Forward B operand (KROW): rows = padded output pixels, k = taps.  A
+// thread's quads share one row quad (4 pixels, fixed for the K loop).
+template <int R, int KT>
+struct LdPsKR : LoaderBase<Stage<R, KT, true, false>> {
+  using St = Stage<R, KT, true, false>;
+  static constexpr bool KROW = true;
+  using LoaderBase<St>::Q;
+  using Params = PsParams;
+  BRes b;
+  PsParams P;
+  uint32_t kk0, pbase;
+  __device__ __forceinline__ void init(const Params& p, uint32_t row0, int tid) {
+    this->base_init(tid);
+    P = p;
+    b.init(p.src, p.n);
+    kk0 = St::qk(tid, 0);
+    const uint32_t n0 = row0 + St::qrow_data(tid, 0);
+    pbase = (this->act && n0 < p.npix) ? ps_pixel(p, n0) : kOob;
+  }
+  __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+      const uint32_t t = kt * KT + kk0 + St::DK * i;
+      r[i] = b.ld4(pbase != kOob && t < P.kdim ? pbase + ps_tap(P, t) : kOob);
+    }
+  }
+};
+
+// dW operand (ROWK): rows = taps (fixed per thread), k = padded pixels.
+template <int R, int KT>
+struct LdPsRK : LoaderBase<Stage<R, KT, false>> {
+  using St = Stage<R, KT, false>;
+  static constexpr bool KROW = false;
+  using LoaderBase<St>::Q;
+  using Params = PsParams;
+  BRes b;
+  PsParams P;
+  uint32_t kq;
+  uint32_t toff[Q];
+  __device__ __forceinline__ void init(const Params& p, uint32_t row0, int tid) {
+    this->base_init(tid);
+    P = p;
+    b.init(p.src, p.n);
+    kq = St::qk(tid, 0);
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+      const uint32_t t = row0 + St::qrow(tid, i);
+      toff[i] = (this->act && t < p.kdim) ? ps_tap(p, t) : kOob;
+    }
+  }
+  __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
+    const uint32_t k0 = kt * KT + kq;
+    const uint32_t pb = k0 < P.npix ? ps_pixel(P, k0) : kOob;
+#pragma unroll
+    for (int i = 0; i < Q; ++i) r[i] = b.ld4(pb != kOob && toff[i] != kOob ? pb + toff[i] : kOob);
+  }
+};
+
+// dW operand (ROWK, direct to LDS): rows = output channels, k = padded
+// pixels of the masked gradient G_pad[b][oc][oh][OWp] (k_mask_pad).  OHWp is
+// a multiple of 4, so a pixel quad is 16-byte aligned and inside one image.
+struct GPadParams {
+  const float* g;
+  uint32_t OC, OHWp, npix, n;
+  FastDiv dOHWp;
+};
+template <int R, int KT>
+struct LdGPadRK : LoaderBase<Stage<R, KT, false>> {
+  using St = Stage<R, KT, false>;
+  static constexpr bool KROW = false;
+  using LoaderBase<St>::Q;
+  using Params = GPadParams;
+  BRes b;
+  GPadParams P;
+  uint32_t kq;
+  uint32_t ocoff[Q];
+  __device__ __forceinline__ void init(const Params& p, uint32_t row0, int tid) {
+    this->base_init(tid);
+    P = p;
+    b.init(p.g, p.n);
+    kq = St::qk(tid, 0);
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+      const uint32_t oc = row0 + St::qrow(tid, i);
+      ocoff[i] = (this->act && oc < p.OC) ? oc * p.OHWp : kOob;
+    }
+  }
+  __device__ __forceinline__ void offsets(uint32_t kt, uint32_t (&o)[Q]) const {
+    const uint32_t k0 = kt * KT + kq;
+    const uint32_t bb = fdiv(k0, P.dOHWp);
+    const uint32_t base = k0 < P.npix ? bb * P.OC * P.OHWp + (k0 - bb * P.OHWp) : kOob;
+#pragma unroll
+    for (int i = 0; i < Q; ++i) o[i] = base != kOob && ocoff[i] != kOob ? base + ocoff[i] : kOob;
+  }
+  __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
+    uint32_t o[Q];
+    offsets(kt, o);
+#pragma unroll
+    for (int i = 0; i < Q; ++i) r[i] = b.ld4(o[i]);
+  }
+  static constexpr bool LDSD = true;
+  __device__ __forceinline__ void issue_lds(uint32_t kt, float* S) const {
+    if (St::PART && !this->act) return;  // whole waves (NQ is a multiple of 64)
+    uint32_t o[Q];
+    offsets(kt, o);
+#pragma unroll
+    for (int i = 0; i < Q; ++i) b.ld4_lds(o[i], S + this->wbase + i * St::DLDS);
+  }
+};
+
+// ---------------------------------------------------------------------------
 // Epilogues.  Lane l of wave (wm, wn) holds, for MFMA block (i, j) and
 // register v, C[m0 + wm*16FM + 16i + 4(l/16) + v][n0 + wn*16FN + 16j + l%16].
 // ---------------------------------------------------------------------------
@@ -683,6 +826,47 @@ struct EpiNCHW {
             else if (p.act == 2)
               z = tanhf(z);
             p.out[base + m * p.HW] = z;
+          }
+        }
+      }
+    }
+  }
+};
+
+// NCHW output over a padded pixel grid (n = b*OHWp + oh*OWp + ow, ow < OWp):
+// columns with ow >= OW are dropped; otherwise as EpiNCHW.
+struct EpiNCHWPad {
+  struct Params {
+    float* out;
+    const float* bias;
+    uint32_t M, OHW, OW, OWp, OHWp, N, act;
+    FastDiv dOHWp, dOWp;
+  };
+  template <int MT, int NT, int FM, int FN>
+  __device__ static __forceinline__ void store(const Params& p, const f4 (&acc)[FM][FN],
+                                               uint32_t m0, uint32_t n0, uint32_t, int wm,
+                                               int wn, int lane) {
+    const int r = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const uint32_t n = n0 + wn * (FN * 16) + j * 16 + r;
+      const uint32_t b = fdiv(n, p.dOHWp), rem = n - b * p.OHWp;
+      const uint32_t oh = fdiv(rem, p.dOWp), ow = rem - oh * p.OWp;
+      if (n >= p.N || ow >= p.OW) continue;
+      const uint32_t base = b * p.M * p.OHW + oh * p.OW + ow;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const uint32_t m = m0 + wm * (FM * 16) + i * 16 + 4 * g + v;
+          if (m < p.M) {
+            float z = acc[i][j][v];
+            if (p.bias) z += p.bias[m];
+            if (p.act == 1)
+              z = fmaxf(z, 0.f);
+            else if (p.act == 2)
+              z = tanhf(z);
+            p.out[base + m * p.OHW] = z;
           }
         }
       }
@@ -1565,14 +1749,201 @@ __global__ void k_to_pk(const float* __restrict__ x, float* __restrict__ out, ui
   }
 }
 
-bool packed_x(const ConvGeom& g) { return g.C < 4; }
+// Stride-phase copy (see PsParams): thread (b, r, c, column quad cq) reads
+// the 4*S consecutive source elements of padded row r from column 4*cq*S - p
+// (16-byte loads at 4-byte alignment where they lie in the image, element
+// loads at its edges) and stores one 16-byte quad per phase.
+template <int S>
+__global__ void __launch_bounds__(256)
+    k_to_ps(const float* __restrict__ x, float* __restrict__ out, uint32_t C, uint32_t H,
+            uint32_t W, uint32_t p, uint32_t Hp, uint32_t Ncol, uint32_t nq, FastDiv dNQ,
+            FastDiv dC, FastDiv dHp) {
+  const uint32_t i = xcd_block_id() * 256 + threadIdx.x;  // neighbouring rows share an L2
+  if (i >= nq) return;
+  const uint32_t NQ = dNQ.d;
+  const uint32_t t = fdiv(i, dNQ), cq = i - t * NQ;     // t = (b*Hp + r)*C + c
+  const uint32_t u = fdiv(t, dC), c = t - u * C;        // u = b*Hp + r
+  const uint32_t b = fdiv(u, dHp), r = u - b * Hp;
+  const uint32_t ih = r - p;                            // wraps in the border
+  const int iw0 = int(4 * cq * S) - int(p);
+  const bool rowin = ih < H;
+  const float* src = x + ((size_t(b) * C + c) * H + (rowin ? ih : 0)) * W;
+  float v[4 * S];
+  if (rowin && iw0 >= 0 && iw0 + 4 * S <= int(W)) {
+#pragma unroll
+    for (int q = 0; q < S; ++q) {
+      const f4 a = ldu<f4>(src + iw0 + 4 * q);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[4 * q + e] = a[e];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4 * S; ++j) {
+      const int iw = iw0 + j;
+      v[j] = (rowin && iw >= 0 && iw < int(W)) ? src[iw] : 0.f;
+    }
+  }
+  float* dst = out + size_t(t) * S * Ncol + 4 * cq;
+#pragma unroll
+  for (int ph = 0; ph < S; ++ph)
+    *reinterpret_cast<f4*>(dst + ph * Ncol) = f4{v[ph], v[S + ph], v[2 * S + ph], v[3 * S + ph]};
+}
+
+// Masked gradient on the padded pixel grid for the stride-phase dW GEMM:
+// G_pad[b][oc][oh][ow] = dy masked by y (y <= 0 -> 0; a NaN y keeps it) for
+// ow < OW, 0 for OW <= ow < OWp.  Block = one chunk of up to kMaskChunk
+// padded elements of one (b, oc) plane, four 16-byte quads per thread (all
+// loaded before any is stored); dbPart[oc][b*nchunk + chunk] = the block's
+// sum of the masked values (thread, wave, then wave order).
+constexpr uint32_t kMaskChunk = 4096;
+__global__ void __launch_bounds__(256)
+    k_mask_pad(const float* __restrict__ dy, const float* __restrict__ y, float* __restrict__ g,
+               float* __restrict__ dbPart, uint32_t OC, uint32_t OH, uint32_t OW, uint32_t OWp,
+               uint32_t nchunk, uint32_t nB, FastDiv dChunk, FastDiv dOWp) {
+  __shared__ float sh[4];
+  // XCD-contiguous numbering: neighbouring chunks share the cache lines of
+  // rows of odd length, and then share an L2.
+  const uint32_t id = xcd_block_id();
+  const uint32_t plane = fdiv(id, dChunk), chunk = id - plane * nchunk;
+  const uint32_t OHWp = OH * OWp;
+  const float* dyp = dy + size_t(plane) * OH * OW;
+  const float* yp = y ? y + size_t(plane) * OH * OW : nullptr;
+  // Every quad is one 16-byte load (4-byte aligned; unaligned access is on),
+  // issued back to back with no branch between them: a quad that would run
+  // past its row (or a thread past the plane) loads the 4 elements ending at
+  // the row's last one (at the plane's start) and shifts them into place,
+  // zero-filling.  Rows of fewer than 4 elements take element loads.
+  f4 v[4], m[4];
+  uint32_t e[4];
+  if (OW >= 4) {
+    uint32_t shift[4], src[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      e[j] = chunk * kMaskChunk + 4 * (threadIdx.x + 256 * j);
+      const uint32_t ej = e[j] < OHWp ? e[j] : 0u;
+      const uint32_t oh = fdiv(ej, dOWp), ow = ej - oh * OWp;
+      shift[j] = ow + 4 <= OW ? 0u : ow + 4 - OW;  // 1..3 for a row's last quad
+      src[j] = oh * OW + ow - shift[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[j] = ldu<f4>(dyp + src[j]);
+      m[j] = yp ? ldu<f4>(yp + src[j]) : f4{1.f, 1.f, 1.f, 1.f};
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t d = shift[j];
+      const f4 a = v[j], b = m[j];
+      v[j] = f4{d == 0 ? a[0] : d == 1 ? a[1] : d == 2 ? a[2] : a[3],
+                d == 0 ? a[1] : d == 1 ? a[2] : d == 2 ? a[3] : 0.f,
+                d == 0 ? a[2] : d == 1 ? a[3] : 0.f, d == 0 ? a[3] : 0.f};
+      m[j] = f4{d == 0 ? b[0] : d == 1 ? b[1] : d == 2 ? b[2] : b[3],
+                d == 0 ? b[1] : d == 1 ? b[2] : d == 2 ? b[3] : 1.f,
+                d == 0 ? b[2] : d == 1 ? b[3] : 1.f, d == 0 ? b[3] : 1.f};
+      if (e[j] >= OHWp) v[j] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      e[j] = chunk * kMaskChunk + 4 * (threadIdx.x + 256 * j);
+      v[j] = m[j] = f4{0.f, 0.f, 0.f, 0.f};
+      if (e[j] >= OHWp) continue;
+      const uint32_t oh = fdiv(e[j], dOWp), ow = e[j] - oh * OWp;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        v[j][q] = ow + q < OW ? dyp[oh * OW + ow + q] : 0.f;
+        m[j][q] = (yp && ow + q < OW) ? yp[oh * OW + ow + q] : 1.f;
+      }
+    }
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[j][q] = m[j][q] <= 0.f ? 0.f : v[j][q];
+    if (e[j] < OHWp) *reinterpret_cast<f4*>(g + size_t(plane) * OHWp + e[j]) = v[j];
+    sum += (v[j][0] + v[j][1]) + (v[j][2] + v[j][3]);
+  }
+  if (dbPart == nullptr) return;
+  sum = wave_reduce(sum);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = sum;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t b = plane / OC, oc = plane - b * OC;
+    dbPart[size_t(oc) * nB * nchunk + size_t(b) * nchunk + chunk] = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+  }
+}
+
+// Layout of the conv input copy: channel-innermost (C >= 4), stride-phase
+// (C < 4, stride <= 4) or channel-packed (C < 4, larger strides).
+bool ps_x(const ConvGeom& g) { return g.C < 4 && g.s <= 4; }
+bool packed_x(const ConvGeom& g) { return g.C < 4 && g.s > 4; }
+
+struct PsGeom {
+  uint32_t Hp, OWp, OHWp, Ncol, RS;
+  size_t floats;
+};
+static PsGeom ps_geom(const ConvGeom& g) {
+  PsGeom q;
+  q.Hp = g.H + 2 * g.p;
+  q.OWp = pad4(g.OW);
+  q.OHWp = g.OH * q.OWp;
+  // Columns: the padded image, and every quad a padded output row's taps
+  // read (up to OWp - 1 + (k - 1) / S).
+  const uint32_t cols = std::max(cdiv(g.W + 2 * g.p, g.s), q.OWp + (g.k - 1) / g.s);
+  q.Ncol = pad4(cols);
+  q.RS = g.C * g.s * q.Ncol;
+  q.floats = size_t(g.B) * q.Hp * q.RS;
+  return q;
+}
 
 size_t xcopy_floats(const ConvGeom& g) {
+  if (ps_x(g)) return ps_geom(g).floats;
   if (!packed_x(g)) return nhwc_floats(g.B, g.C, g.H, g.W);
   return size_t(g.B) * (g.H + 2 * g.p) * (g.W + 2 * g.p) * g.C;
 }
 
-uint32_t xcopy_tag(const ConvGeom& g) { return packed_x(g) ? 0x10000u + g.p : pad4(g.C); }
+uint32_t xcopy_tag(const ConvGeom& g) {
+  if (ps_x(g)) return 0x20000u + g.p + (g.s << 8) + (g.k << 12);
+  return packed_x(g) ? 0x10000u + g.p : pad4(g.C);
+}
+
+static bool to_ps(const float* x, float* out, const ConvGeom& g) {
+  const PsGeom q = ps_geom(g);
+  const uint32_t NQ = q.Ncol / 4, nq = g.B * q.Hp * g.C * NQ;
+  ProfScope prof("nhwc", 0, 4.0 * (double(g.B) * g.C * g.H * g.W + double(q.floats)));
+  const dim3 grid(cdiv(nq, 256));
+  const FastDiv fNQ = make_fastdiv(NQ), fC = make_fastdiv(g.C), fHp = make_fastdiv(q.Hp);
+#define DCE_PS(S_)                                                                            \
+  if (g.s == S_)                                                                              \
+    hipLaunchKernelGGL(k_to_ps<S_>, grid, dim3(256), 0, stream(), x, out, g.C, g.H, g.W, g.p, \
+                       q.Hp, q.Ncol, nq, fNQ, fC, fHp);
+  DCE_PS(1) DCE_PS(2) DCE_PS(3) DCE_PS(4)
+#undef DCE_PS
+  return check_launch("to_ps");
+}
+
+static PsParams ps_params(const float* src, const ConvGeom& g) {
+  const PsGeom q = ps_geom(g);
+  const uint32_t KK = g.k * g.k;
+  return PsParams{src, q.RS, q.Hp, g.s, q.Ncol, g.C, g.k, KK, g.C * KK, q.OWp, q.OHWp,
+                  g.B * q.OHWp, uint32_t(q.floats), make_fastdiv(q.OHWp), make_fastdiv(q.OWp),
+                  make_fastdiv(KK), make_fastdiv(g.k), make_fastdiv(g.s)};
+}
+
+// G_pad (and, with dbPart, the bias-gradient partials: OC rows of
+// B * nchunk); returns nchunk.
+static uint32_t mask_pad(const float* dy, const float* y, float* gp, float* dbPart,
+                         const ConvGeom& g, bool* ok) {
+  const PsGeom q = ps_geom(g);
+  const uint32_t nchunk = cdiv(q.OHWp, kMaskChunk), planes = g.B * g.OC;
+  ProfScope prof("conv_grad_nhwc", 0, 4.0 * (2.0 * g.B * g.OC * g.OH * g.OW + double(planes) * q.OHWp));
+  hipLaunchKernelGGL(k_mask_pad, dim3(planes * nchunk), dim3(256), 0, stream(), dy, y, gp, dbPart,
+                     g.OC, g.OH, g.OW, q.OWp, nchunk, g.B, make_fastdiv(nchunk),
+                     make_fastdiv(q.OWp));
+  *ok = check_launch("mask_pad");
+  return nchunk;
+}
 
 static bool to_pk(const float* x, float* out, const ConvGeom& g) {
   const uint32_t Hp = g.H + 2 * g.p, Wp = g.W + 2 * g.p, npix = g.B * Hp * Wp;
@@ -1695,8 +2066,59 @@ struct FwdPkRun {
   }
 };
 
+// Forward over the stride-phase copy (C < 4, stride <= 4): K runs over the
+// taps (c, kh, kw), the filters' own order (rows padded to pad4(C*KK)); the
+// columns are the padded pixel grid, written through EpiNCHWPad (no split).
+struct FwdPsRun {
+  const float* wp;
+  const float* xs;
+  const float* bias;
+  float* y;
+  ConvGeom g;
+  uint32_t act;
+  template <int MT, int NT, int KT>
+  int occ(bool) const {
+    return occupancy(k_igemm<MT, NT, KT, LdDenseRK<MT, KT>, LdPsKR<NT, KT>, EpiNCHWPad>);
+  }
+  template <int MT, int NT, int KT>
+  bool run() {
+    const uint32_t kdim = pad4(g.C * g.k * g.k);
+    using LA = LdDenseRK<MT, KT>;
+    using LB = LdPsKR<NT, KT>;
+    const typename LA::Params pa{wp, kdim, g.OC, kdim, g.OC * kdim};
+    const PsParams pb = ps_params(xs, g);
+    const EpiNCHWPad::Params pe{y, bias, g.OC, g.OH * g.OW, g.OW, pb.OWp, pb.OHWp, pb.npix, act,
+                                pb.dOHWp, pb.dOWp};
+    return launch<MT, NT, KT, LA, LB, EpiNCHWPad>(pa, pb, pe, g.OC, pb.npix, cdiv(kdim, KT), 1,
+                                                  "conv_forward");
+  }
+};
+
+static bool conv_forward_ps(const float* x, float* keep, const float* w, const float* bias,
+                            float* y, const ConvGeom& g, uint32_t act) {
+  const PsGeom q = ps_geom(g);
+  const uint32_t taps = g.C * g.k * g.k, kdim = pad4(taps), N = g.B * q.OHWp;
+  if (!operand_fits(q.floats, "conv_forward") || !operand_fits(size_t(g.OC) * kdim, "conv_forward"))
+    return false;
+  TileCfg cfg = choose("DCE_TUNE_FWD", g.OC, N, kdim, 1, true,
+                       [&](const TileCfg& t) { return tiles_occ16(t, FwdPsRun{}); }, true);
+  cfg.splits = 1;  // the padded-grid epilogue writes the output directly
+  const size_t nw = al64(size_t(g.OC) * kdim);
+  float* ws = workspace(nw + (keep ? 0 : al64(q.floats)));
+  if (!ws) return false;
+  float* xs = keep ? keep : ws + nw;
+  if (!to_ps(x, xs, g)) return false;
+  hipLaunchKernelGGL(k_pad_cols, dim3(cdiv(nw, 256)), dim3(256), 0, stream(), w, ws, g.OC, taps,
+                     kdim);
+  if (!check_launch("pad_w")) return false;
+  ProfScope prof("conv_fwd", 2.0 * g.OC * taps * double(g.B) * g.OH * g.OW,
+                 4.0 * (double(g.B) * g.C * g.H * g.W + double(g.B) * g.OC * g.OH * g.OW));
+  return tiles_dispatch16(cfg, FwdPsRun{ws, xs, bias, y, g, act});
+}
+
 bool conv_forward(const float* x, float* x_nhwc_keep, const float* w, const float* bias,
                   float* y, const ConvGeom& g, uint32_t act) {
+  if (ps_x(g)) return conv_forward_ps(x, x_nhwc_keep, w, bias, y, g, act);
   const bool pk = packed_x(g);
   const uint32_t Cp = pad4(g.C), KK = g.k * g.k, kdim = pk ? pad4(KK * g.C) : KK * Cp;
   const bool blk = !pk && blocked_k(Cp), s1 = g.s == 1;
@@ -1740,15 +2162,19 @@ bool conv_forward(const float* x, float* x_nhwc_keep, const float* w, const floa
 // `trans` swaps the operands (taps as output rows) for layers with fewer taps
 // x channels than output channels, so the narrow tiles cover the short axis.
 struct DwRun {
-  const float* gn;
+  const float* gn;  // G: NHWC, or G_pad for the stride-phase layout
   const float* xn;
   float* part;
   ConvGeom g;
   uint32_t splits;
   bool trans;
   bool pk;  // xn is the channel-packed copy: taps (kh, kw, c) with C unpadded
+  bool ps;  // xn is the stride-phase copy, gn G_pad: taps (c, kh, kw), padded pixels
   template <int MT, int NT, int KT>
   int occ(bool) const {
+    if (ps)
+      return trans ? occupancy(k_igemm<MT, NT, KT, LdPsRK<MT, KT>, LdGPadRK<NT, KT>, EpiRowMajor>)
+                   : occupancy(k_igemm<MT, NT, KT, LdGPadRK<MT, KT>, LdPsRK<NT, KT>, EpiRowMajor>);
     if (pk)
       return trans ? occupancy(k_igemm<MT, NT, KT, LdPkKR<MT, KT>, LdGradKR<NT, KT>, EpiRowMajor>)
                    : occupancy(k_igemm<MT, NT, KT, LdGradKR<MT, KT>, LdPkKR<NT, KT>, EpiRowMajor>);
@@ -1772,8 +2198,23 @@ struct DwRun {
         pg, px, pe, g.OC, N, cdiv(npix, KT), splits, "conv_backward_filter");
   }
   template <int MT, int NT, int KT>
+  bool run_ps() {
+    const PsParams px = ps_params(xn, g);
+    const GPadParams pg{gn, g.OC, px.OHWp, px.npix, g.B * g.OC * px.OHWp, px.dOHWp};
+    const uint32_t N = px.kdim, zs = 4 * cdiv(size_t(g.OC) * N, 4), kt = cdiv(px.npix, KT);
+    if (trans) {
+      const EpiRowMajor::Params pe{part, N, g.OC, g.OC, zs};
+      return launch<MT, NT, KT, LdPsRK<MT, KT>, LdGPadRK<NT, KT>, EpiRowMajor>(
+          px, pg, pe, N, g.OC, kt, splits, "conv_backward_filter");
+    }
+    const EpiRowMajor::Params pe{part, g.OC, N, N, zs};
+    return launch<MT, NT, KT, LdGPadRK<MT, KT>, LdPsRK<NT, KT>, EpiRowMajor>(
+        pg, px, pe, g.OC, N, kt, splits, "conv_backward_filter");
+  }
+  template <int MT, int NT, int KT>
   bool run() {
     const uint32_t KK = g.k * g.k, OHW = g.OH * g.OW, npix = g.B * OHW;
+    if (ps) return run_ps<MT, NT, KT>();
     if (pk) return go<MT, NT, KT, LdPkKR<MT, KT>>(pk_params(xn, g), KK * g.C);
     const uint32_t Cp = pad4(g.C), N = KK * Cp;
     const XTapParams px{xn, g.H, g.W, Cp, g.k, g.s, g.p, g.OW, OHW, npix, N,
@@ -1833,21 +2274,32 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
       !operand_fits(xcopy_floats(g), "conv_backward") ||
       !operand_fits(size_t(g.C) * KK * OCp, "conv_backward"))
     return false;
-  // Workspace carve-up: G (NHWC), db partials, the copy of x if not kept by
-  // the forward, dW split-K partials, dX filters, dX split-K partials.
-  // Fewer than four input channels: x is channel-packed and the dW tap axis
-  // runs over KK * C unpadded taps (Cx = C), otherwise over KK * pad4(C).
-  const bool pk = packed_x(g);
-  const uint32_t Cx = pk ? g.C : Cp;
+  // Workspace carve-up: G (NHWC) and / or G_pad, db partials, the copy of x
+  // if not kept by the forward, dW split-K partials, dX filters, dX split-K
+  // partials.  Fewer than four input channels: x is stride-phase split (or,
+  // for strides above 4, channel-packed) and the dW tap axis runs over KK * C
+  // unpadded taps (Cx = C), otherwise over KK * pad4(C).
+  const bool pk = packed_x(g), ps = ps_x(g);
+  const uint32_t Cx = (pk || ps) ? g.C : Cp;
   const uint32_t npb = cdiv(OHW, 64);
   // The whole call as one family: the masked transpose of dy, the bias-grad
   // sum, any rebuilt copy of x, the filter re-layout and the split-K finishes
   // count with the GEMMs' FLOPs.
   const double callFlops = 2.0 * g.OC * g.C * KK * double(npix) * ((dw ? 1 : 0) + (dx ? 1 : 0));
   ProfScope profAll("conv_bwd", callFlops, 0.0);
-  const size_t nG = al64(size_t(npix) * OCp);
-  const size_t nDb = db ? al64(size_t(g.B) * npb * g.OC) : 0;
+  // The stride-phase dW reads the masked gradient on the padded pixel grid
+  // (G_pad, which also yields the bias-gradient partials); dX reads the NHWC
+  // G of the transpose pass.  Other layouts use the NHWC G for both.
+  const PsGeom q = ps ? ps_geom(g) : PsGeom{};
+  const bool useGpad = ps && (dw || (db && !dx)), useGnhwc = !ps || dx;
+  const uint32_t nchunk = ps ? cdiv(q.OHWp, kMaskChunk) : 0;
+  const uint32_t dbRows = useGpad ? g.B * nchunk : g.B * npb;
+  const uint32_t dwK = ps ? g.B * q.OHWp : npix;  // dW GEMM K extent (pixels)
+  const size_t nG = useGnhwc ? al64(size_t(npix) * OCp) : 0;
+  const size_t nGp = useGpad ? al64(size_t(g.B) * g.OC * q.OHWp) : 0;
+  const size_t nDb = db ? al64(size_t(dbRows) * g.OC) : 0;
   const size_t nX = (dw && !x_nhwc) ? al64(xcopy_floats(g)) : 0;
+  if (ps && !operand_fits(nGp, "conv_backward")) return false;
   TileCfg dwc{128, 128, 16, 1}, dxc{128, 128, 16, 1};
   size_t nP = 0, nW = 0, nQ = 0;
   bool dwT = false;
@@ -1859,11 +2311,12 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
     const uint32_t dM = dwT ? taps : g.OC, dN = dwT ? g.OC : taps;
     const uint32_t ntiles = cdiv(dM, pick_tile_m(dM)) * cdiv(dN, pick_tile(dN));
     dwc = choose(
-        "DCE_TUNE_DW", dM, dN, npix, ntiles <= 4 ? 1024 : 256, false,
+        "DCE_TUNE_DW", dM, dN, dwK, ntiles <= 4 ? 1024 : 256, false,
         [&](const TileCfg& t) {
           DwRun r{};
           r.trans = dwT;
           r.pk = pk;
+          r.ps = ps;
           return tiles_occ(t, r);
         },
         false, true);
@@ -1877,25 +2330,36 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
     nW = al64(size_t(g.C) * KK * OCp);
     nQ = dxc.splits > 1 ? size_t(dxc.splits) * g.C * g.B * HW : 0;
   }
-  float* ws = workspace(nG + nDb + nX + nP + nW + nQ);
+  float* ws = workspace(nG + nGp + nDb + nX + nP + nW + nQ);
   if (!ws) return false;
   float* gn = ws;
-  float* dbPart = db ? gn + nG : nullptr;
-  float* xs = ws + nG + nDb;
+  float* gp = gn + nG;
+  float* dbPart = db ? gp + nGp : nullptr;
+  float* xs = gp + nGp + nDb;
   float* part = xs + nX;
   float* wt = part + nP;
   float* qpart = wt + nW;
 
+  if (useGpad) {
+    bool ok = false;
+    mask_pad(dy, y, gp, dbPart, g, &ok);
+    if (!ok) return false;
+  }
   uint32_t npbGot = npb;
-  if (!to_nhwc_masked(dy, y, gn, dbPart, g.B, g.OC, OHW, &npbGot)) return false;
+  if (useGnhwc &&
+      !to_nhwc_masked(dy, y, gn, useGpad ? nullptr : dbPart, g.B, g.OC, OHW, &npbGot))
+    return false;
   if (db) {
-    hipLaunchKernelGGL(k_rowsum, dim3(g.OC), dim3(256), 0, stream(), dbPart, db, g.B * npbGot);
+    hipLaunchKernelGGL(k_rowsum, dim3(g.OC), dim3(256), 0, stream(), dbPart, db,
+                       useGpad ? dbRows : g.B * npbGot);
     if (!check_launch("bias_grad")) return false;
   }
   if (dw) {
     const float* xn = x_nhwc;
     if (!xn) {
-      if (!(pk ? to_pk(x, xs, g) : to_nhwc(x, xs, g.B, g.C, g.H, g.W))) return false;
+      const bool built = ps ? to_ps(x, xs, g)
+                            : (pk ? to_pk(x, xs, g) : to_nhwc(x, xs, g.B, g.C, g.H, g.W));
+      if (!built) return false;
       xn = xs;
     }
     bool ok;
@@ -1903,9 +2367,12 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
       const double fl = 2.0 * g.OC * g.C * KK * double(npix);
       ProfScope prof("conv_dw", fl,
                      4.0 * (double(npix) * OCp + double(g.B) * g.H * g.W * Cp + double(g.OC) * KK * Cp));
-      ok = tiles_dispatch(dwc, DwRun{gn, xn, part, g, dwc.splits, dwT, pk});
+      ok = tiles_dispatch(dwc, DwRun{ps ? gp : gn, xn, part, g, dwc.splits, dwT, pk, ps});
       if (ok) {
-        ok = dw_final(part, dw, g.OC, g.C, KK, Cx, dwc.splits, dwT);
+        // The stride-phase taps are already in the filters' (c, kh, kw)
+        // order: the finish is a plain split sum (one channel of C*KK taps).
+        ok = ps ? dw_final(part, dw, g.OC, 1, KK * g.C, 1, dwc.splits, dwT)
+                : dw_final(part, dw, g.OC, g.C, KK, Cx, dwc.splits, dwT);
       }
     }
     if (!ok) return false;

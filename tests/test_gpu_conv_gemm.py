@@ -57,6 +57,14 @@ CONV_CASES = [
     (2, 17, 9, 9, 33, 3, 2, 0, 2),        # tanh act: no derivative applied (reference quirk)
     (1, 8, 7, 7, 8, 3, 3, 1, 0),          # stride 3
     (2, 192, 6, 6, 256, 3, 1, 1, 1),      # deep channels
+    # C < 4 and stride <= 4: the stride-phase copy (padded pixel grid)
+    (2, 1, 19, 21, 6, 3, 3, 1, 1),        # C = 1, stride 3, OW 7 -> 8 padded columns
+    (2, 2, 17, 29, 12, 4, 4, 0, 0),       # even k, stride 4, no activation
+    (2, 3, 9, 9, 5, 1, 2, 0, 1),          # 1x1, stride 2
+    (2, 3, 224, 224, 64, 11, 4, 2, 1),    # AlexNet c1 at full resolution
+    # C < 4 and stride > 4: the channel-packed copy
+    (2, 3, 23, 23, 8, 7, 5, 2, 1),
+    (1, 1, 20, 22, 4, 6, 6, 0, 1),
 ]
 
 
@@ -110,10 +118,11 @@ def test_conv_forward_backward(eng, case):
 
 
 @pytest.mark.parametrize("case", [(2, 3, 35, 35, 64, 11, 4, 2, 1), (2, 1, 12, 10, 6, 5, 1, 2, 1),
-                                  (2, 16, 9, 9, 8, 3, 1, 1, 1)], ids=str)
+                                  (2, 2, 20, 20, 4, 6, 5, 1, 1), (2, 16, 9, 9, 8, 3, 1, 1, 1)],
+                         ids=str)
 def test_conv_backward_rebuilds_x_copy(eng, case):
     """Without the forward's handle the backward builds its own copy of x
-    (channel-packed for C < 4, NHWC otherwise)."""
+    (stride-phase or channel-packed for C < 4, NHWC otherwise)."""
     _conv_case(eng, *case, seed=5, keep=False)
 
 
@@ -211,6 +220,72 @@ def test_single_conv_full_size_sampled(eng):
     assert rel_err(np.array(got_s), np.array(ref_s)) <= TOL
 
 
+def _dw_ref_taps(G, x, k, s, p, oc_sel):
+    """dW[oc, c, kh, kw] for the selected output channels: one float64
+    contraction over the whole batch per tap."""
+    B, C, H, W = x.shape
+    OH, OW = G.shape[2], G.shape[3]
+    xp = np.zeros((B, C, H + 2 * p, W + 2 * p), np.float32)
+    xp[:, :, p:p + H, p:p + W] = x
+    Gf = G[:, oc_sel].transpose(1, 0, 2, 3).reshape(len(oc_sel), -1)
+    out = np.empty((len(oc_sel), C, k, k))
+    for kh in range(k):
+        for kw in range(k):
+            xs = xp[:, :, kh:kh + s * (OH - 1) + 1:s, kw:kw + s * (OW - 1) + 1:s]
+            out[:, :, kh, kw] = Gf @ xs.transpose(1, 0, 2, 3).reshape(C, -1).astype(np.float64).T
+    return out
+
+
+@pytest.mark.parametrize("layer", ["c1", "c2"])
+def test_alexnet_b128_conv_backward_full_size(eng, layer):
+    """The AlexNet-224 batch-128 c1 (x[128,3,224,224], W[64,3,11,11], s4 p2:
+    the stride-phase dW) and c2 (x[128,64,27,27], W[192,64,5,5], s1 p2)
+    backward at the timed size, ReLU mask from the device's forward: db and
+    dW of every (c1) or 24 sampled (c2) output channels against float64
+    contractions over the full batch, and for c2 32 sampled dX pixels."""
+    B, C, H, OC, k, s, p = (128, 3, 224, 64, 11, 4, 2) if layer == "c1" else (128, 64, 27, 192, 5, 1, 2)
+    print(f"alexnet b128 {layer} backward", flush=True)
+    r = rng(5 * 1000 + k)
+    x = r.standard_normal((B, C, H, H)).astype(np.float32)
+    w = he(r, (OC, C, k, k), C * k * k)
+    b = np.zeros(OC, np.float32)
+    hx, hw, hb = upload(eng, x), upload(eng, w), upload(eng, b)
+    pim = ctypes.c_void_p()
+    hy = eng.lib.ConvForwardFused(hx, hw, hb, B, C, H, H, OC, k, k, s, p, 1, ctypes.byref(pim))
+    assert hy, eng.last_error()
+    OH, OW = K.conv_out_hw(H, H, k, s, p)
+    y = download(eng, hy, (B, OC, OH, OW))
+    dy = r.standard_normal(y.shape).astype(np.float32)
+    hdy = upload(eng, dy)
+    want_x = 0 if layer == "c1" else 1
+    pdf, pdb, pdx = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+    eng.lib.ConvBackwardFused(hdy, hy, hx, hw, pim.value, B, C, H, H, OC, k, k, s, p, 1, want_x, 1, 1,
+                              ctypes.byref(pdf), ctypes.byref(pdb), ctypes.byref(pdx))
+    assert pdf.value and pdb.value, eng.last_error()
+    dW = download(eng, pdf.value, w.shape)
+    db = download(eng, pdb.value, (OC,))
+    dX = download(eng, pdx.value, x.shape) if want_x else None
+    release(eng, hx, hw, hb, hy, hdy, pdf.value, pdb.value, pdx.value)
+    G = np.where(y <= 0, 0.0, dy.astype(np.float64))
+    assert rel_err(db, G.sum(axis=(0, 2, 3))) <= TOL
+    oc_sel = np.arange(OC) if layer == "c1" else np.sort(r.choice(OC, 24, replace=False))
+    assert rel_err(dW[oc_sel], _dw_ref_taps(G, x, k, s, p, oc_sel)) <= TOL
+    if want_x:
+        Gp = np.zeros((B, OC, OH + 2 * p, OW + 2 * p))
+        Gp[:, :, p:p + OH, p:p + OW] = G
+        w64 = w.astype(np.float64)
+        ref_s, got_s = [], []
+        for _ in range(32):
+            bb, ih, iw = int(r.integers(B)), int(r.integers(H)), int(r.integers(H))
+            acc = np.zeros(C)
+            for kh in range(k):
+                for kw in range(k):   # stride 1: oh = ih + p - kh
+                    acc += w64[:, :, kh, kw].T @ Gp[bb, :, ih + 2 * p - kh, iw + 2 * p - kw]
+            ref_s.append(acc)
+            got_s.append(dX[bb, :, ih, iw])
+        assert rel_err(np.array(got_s), np.array(ref_s)) <= TOL
+
+
 TILE_CFGS = [f"{mt},{nt},{kt},{sp}" for mt in (64, 128) for nt in (64, 128) for kt in (16, 32)
              for sp in (1, 3)]
 
@@ -224,6 +299,7 @@ def test_forced_tile_configs(eng, monkeypatch, cfg):
         monkeypatch.setenv(var, cfg)
     _conv_case(eng, 2, 16, 14, 14, 20, 3, 2, 1, 1)   # stride 2, OC not a multiple of 16
     _conv_case(eng, 2, 48, 10, 10, 16, 3, 1, 1, 1)   # stride 1
+    _conv_case(eng, 2, 3, 23, 21, 72, 5, 2, 1, 1)    # C = 3: stride-phase dW (75 taps, OC 72)
     for flags in range(4):
         test_matmul_alloc(eng, 127, 129, 130, flags)
         test_matmul_alloc(eng, 5, 7, 3, flags)
