@@ -230,7 +230,8 @@ def memory_suite(reps=10):
     """Backward memory-bound kernels at the shapes of the benchmark networks,
     each driven through the same dispatch the API's backward makes.  One JSON
     line per kernel: algorithmic bytes per launch (each required tensor read
-    or written once), mean HIP-event time, GB/s and fraction of 8 TB/s."""
+    or written once), the time per launch of `reps` back-to-back launches
+    (one HIP-event pair around them), GB/s and fraction of 8 TB/s."""
     from directcompute_torch_amd import nn_engine as nn
     lib = nn.lib
     rng = np.random.default_rng(SEED + 7)
@@ -257,17 +258,28 @@ def memory_suite(reps=10):
 
     out = []
 
-    def run(kernel, family, shape, nbytes, fn):
+    def run(kernel, family, shape, nbytes, fn, per_launch=False):
+        # One event pair around `reps` back-to-back launches (an event pair per
+        # launch would add its own few microseconds of idle GPU to each), or,
+        # with per_launch, the family's own event pair inside each call (for
+        # calls that launch more than the kernel measured).
         fn()
         lib.SyncGPU()
         lib.ResetProfile()
-        lib.SetProfiling(1)
+        if per_launch:
+            lib.SetProfiling(1)
+        else:
+            lib.BeginProfileRegion(family.encode(), 0.0, float(nbytes) * reps)
         for _ in range(reps):
             fn()
+        if per_launch:
+            lib.SyncGPU()
+            lib.SetProfiling(0)
+        else:
+            lib.EndProfileRegion()
         lib.SyncGPU()
-        lib.SetProfiling(0)
         n, ms = prof(family)
-        us = ms / max(n, 1) * 1e3
+        us = ms / (max(n, 1) if per_launch else reps) * 1e3
         gbps = nbytes / (us * 1e-6) / 1e9 if us > 0 else 0.0
         rec = {"suite": "memory", "kernel": kernel, "family": family, "shape": list(shape),
                "bytes_per_launch": int(nbytes), "us": round(us, 2), "GB/s": round(gbps, 1),
@@ -327,21 +339,23 @@ def memory_suite(reps=10):
         run(f"depthwise_conv_backward_filter_s{s}", "dw_bwd_filter", (B, C, H, W), 4 * (nx + ny),
             lambda: nn._dispatch(b"depthwise_conv_backward_filter", (dys, xs), (dfs, dbs), C, 1, 1, **cb))
 
-    # Max-pool backward: UNet 2x2 s2 and AlexNet c1 3x3 s2 (indices from the fused forward,
-    # which the backward consumes, so each launch is preceded by a forward)
+    # Max-pool backward: UNet 2x2 s2 and AlexNet c1 3x3 s2.  The indices of one
+    # fused forward serve every launch: each backward consumes one reference,
+    # so the handle carries one per launch.
     for (shape, k, st) in (((8, 16, 256, 256), 2, 2), ((128, 64, 55, 55), 3, 2)):
         B, C, H, W = shape
         OH, OW = (H - k) // st + 1, (W - k) // st + 1
         xin, dz = buf(shape), buf((B, C, OH, OW))
         nx, no = B * C * H * W, B * C * OH * OW
+        pidx = ctypes.c_void_p()
+        held.append(lib.MaxPoolForwardFused(xin, B, C, H, W, k, st, ctypes.byref(pidx)))
+        for _ in range(reps + 1):
+            lib.AddRefBuffer(pidx.value)
 
-        def mp(xin=xin, dz=dz, B=B, C=C, H=H, W=W, OH=OH, OW=OW, nx=nx, k=k, st=st):
-            pidx = ctypes.c_void_p()
-            y = lib.MaxPoolForwardFused(xin, B, C, H, W, k, st, ctypes.byref(pidx))
-            d = lib.MaxPoolBackwardFused(dz, pidx.value, B, C, OH, OW, nx)
-            lib.ReleaseBuffer(y)
-            lib.ReleaseBuffer(d)
+        def mp(idx=pidx.value, dz=dz, B=B, C=C, OH=OH, OW=OW, nx=nx):
+            lib.ReleaseBuffer(lib.MaxPoolBackwardFused(dz, idx, B, C, OH, OW, nx))
         run(f"maxpool_backward_{k}x{k}s{st}", "maxpool_bwd", shape, 8 * no + 4 * nx, mp)
+        lib.ReleaseBuffer(pidx.value)
 
     # UNet decoder: nearest upsample x2 backward, concat backward (slice)
     B, C, H, W = 8, 32, 128, 128
@@ -386,7 +400,7 @@ def memory_suite(reps=10):
                                   0, 0, 1, ctypes.byref(pdf), ctypes.byref(pdb), ctypes.byref(pdx))
             lib.ReleaseBuffer(pdb.value)
         run(f"conv_grad_reshape_relu_{name}", "conv_grad_nhwc", (BATCH, cout, o, o),
-            4 * BATCH * o * o * (2 * cout + cpad), gpass)
+            4 * BATCH * o * o * (2 * cout + cpad), gpass, per_launch=True)
 
     # Optimisers over AlexNet's 61.1 M parameters (16 tensors)
     shapes = [(c[2], c[1], c[3], c[3]) for c in CONVS] + [(c[2],) for c in CONVS] + \
@@ -405,7 +419,7 @@ def memory_suite(reps=10):
     run("AdamBatch", "adam", (tot,), 28 * tot,
         lambda: lib.AdamBatch(pa, ga, ma, va, sa, P, 1e-9, 0.9, 0.999, 1e-8, 0.0, 1.0))
     run("ClipGradNorm: sum of squares", "grad_norm", (tot,), 4 * tot,
-        lambda: lib.ClipGradNorm(ga, sa, P, 1e30))
+        lambda: lib.ClipGradNorm(ga, sa, P, 1e30), per_launch=True)
 
     for h in held:
         lib.ReleaseBuffer(h)

@@ -143,6 +143,10 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.ReplayGraph.restype = ctypes.c_bool
     lib.ReleaseGraph.argtypes = [c_void_p]
     lib.ReleaseGraph.restype = None
+    lib.BeginProfileRegion.argtypes = [ctypes.c_char_p, ctypes.c_double, ctypes.c_double]
+    lib.BeginProfileRegion.restype = ctypes.c_bool
+    lib.EndProfileRegion.argtypes = []
+    lib.EndProfileRegion.restype = ctypes.c_bool
     lib.SetStreamingThreshold.argtypes = [ctypes.c_double]
     lib.SetStreamingThreshold.restype = ctypes.c_double
     lib.ResetProfile.argtypes = []

@@ -19,6 +19,7 @@
 #include <cstring>
 #include <map>
 #include <mutex>
+#include <set>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -1074,6 +1075,40 @@ void ReleaseGraph(void* graph) {
     for (float* p : g_wsRetired) hipFree(p);
     g_wsRetired.clear();
   }
+}
+
+// One event pair around everything queued between the two calls, recorded as
+// one launch of `family` (the name is kept for the process's lifetime).
+static hipEvent_t g_regionEv = nullptr;
+static const char* g_regionFam = nullptr;
+static double g_regionFlops = 0, g_regionBytes = 0;
+
+bool BeginProfileRegion(const char* family, double flops, double bytes) {
+  static std::set<std::string> names;
+  if (!ensure_init() || !family || g_capturing || g_regionEv) {
+    set_error("BeginProfileRegion: not initialised, no family, capturing, or a region is open");
+    return false;
+  }
+  g_regionFam = names.insert(family).first->c_str();
+  g_regionFlops = flops;
+  g_regionBytes = bytes;
+  g_regionEv = take_event();
+  if (!g_regionEv) return false;
+  hipEventRecord(g_regionEv, g_stream);
+  return true;
+}
+
+bool EndProfileRegion(void) {
+  if (!g_regionEv) {
+    set_error("EndProfileRegion: no region is open");
+    return false;
+  }
+  hipEvent_t e1 = take_event();
+  if (!e1) return false;
+  hipEventRecord(e1, g_stream);
+  g_profPending.push_back({g_regionFam, g_regionEv, e1, g_regionFlops, g_regionBytes});
+  g_regionEv = nullptr;
+  return true;
 }
 
 double SetStreamingThreshold(double bytes) {

@@ -119,6 +119,8 @@ struct LoaderBase {
   // the unpadded [row][k] stages qualify: there a wave's 64 quads of one load
   // are 64 consecutive 16-byte LDS slots in lane order (lds_off(t) = 4 t).
   static constexpr bool LDSD = false;
+  // As the B operand: accumulate C transposed (MFMA B fragment first).
+  static constexpr bool kTransAcc = false;
   int lds0, wbase;
   bool act;
   __device__ __forceinline__ void base_init(int tid) {
@@ -264,6 +266,7 @@ struct LdPixRK : LoaderBase<Stage<R, KT, false>> {
   // channel block are wave-uniform, so a quad's source offset is a per-quad
   // constant qbase plus a uniform tap term -- no per-tile multiplies.
   static constexpr bool FAST = BLK && (FWD || S1);
+  static constexpr bool kTransAcc = true;  // pixel columns: quad stores (measured faster)
   BRes b;
   uint32_t srcH, srcW, Cp, k, s, kdim, kq;
   FastDiv dInner, dK;
@@ -660,6 +663,7 @@ template <int R, int KT>
 struct LdPsKR : LoaderBase<Stage<R, KT, true, false>> {
   using St = Stage<R, KT, true, false>;
   static constexpr bool KROW = true;
+  static constexpr bool kTransAcc = true;  // pixel columns: quad stores (measured faster)
   using LoaderBase<St>::Q;
   using Params = PsParams;
   BRes b;
@@ -765,29 +769,65 @@ struct LdGPadRK : LoaderBase<Stage<R, KT, false>> {
 };
 
 // ---------------------------------------------------------------------------
-// Epilogues.  Lane l of wave (wm, wn) holds, for MFMA block (i, j) and
-// register v, C[m0 + wm*16FM + 16i + 4(l/16) + v][n0 + wn*16FN + 16j + l%16].
+// Epilogues.  The accumulator layout depends on the MFMA operand order, a
+// per-kernel choice (TACC, a trait of the B loader: whichever measured faster
+// for that kernel's instruction schedule).  Lane l of wave (wm, wn) holds,
+// for block (i, j) and register v, with r = l % 16, g = l / 16:
+//   TACC false:  C[m0 + wm*16FM + 16i + 4g + v][n0 + wn*16FN + 16j + r]
+//                (four consecutive rows of one column: four scalar stores);
+//   TACC true:   C[m0 + wm*16FM + 16i + r][n0 + wn*16FN + 16j + 4g + v]
+//                (B fragment first: four consecutive columns of one row,
+//                 16 contiguous bytes of a row-major C: one quad store).
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ float epi_act(float z, uint32_t act) {
+  if (act == 1) return fmaxf(z, 0.f);
+  if (act == 2) return tanhf(z);
+  return z;
+}
+
 struct EpiRowMajor {
   struct Params {
     float* c;
     uint32_t M, N, ldc, splitStride;
   };
-  template <int MT, int NT, int FM, int FN>
+  template <int MT, int NT, int FM, int FN, bool TACC>
   __device__ static __forceinline__ void store(const Params& p, const f4 (&acc)[FM][FN],
                                                uint32_t m0, uint32_t n0, uint32_t z, int wm,
                                                int wn, int lane) {
     float* c = p.c + size_t(z) * p.splitStride;
     const int r = lane & 15, g = lane >> 4;
+    if constexpr (!TACC) {
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const uint32_t n = n0 + wn * (FN * 16) + j * 16 + r;
+      for (int j = 0; j < FN; ++j) {
+        const uint32_t n = n0 + wn * (FN * 16) + j * 16 + r;
 #pragma unroll
-      for (int i = 0; i < FM; ++i) {
+        for (int i = 0; i < FM; ++i) {
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const uint32_t m = m0 + wm * (FM * 16) + i * 16 + 4 * g + v;
-          if (m < p.M && n < p.N) c[m * p.ldc + n] = acc[i][j][v];
+          for (int v = 0; v < 4; ++v) {
+            const uint32_t m = m0 + wm * (FM * 16) + i * 16 + 4 * g + v;
+            if (m < p.M && n < p.N) c[m * p.ldc + n] = acc[i][j][v];
+          }
+        }
+      }
+      return;
+    }
+    // Quad stores need 16-byte aligned rows (uniform over the launch).
+    const bool vec =
+        ((p.ldc | p.splitStride) & 3) == 0 && (reinterpret_cast<uintptr_t>(p.c) & 15) == 0;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const uint32_t m = m0 + wm * (FM * 16) + i * 16 + r;
+      if (m >= p.M) continue;
+      float* row = c + size_t(m) * p.ldc;
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const uint32_t n = n0 + wn * (FN * 16) + j * 16 + 4 * g;
+        if (vec && n + 3 < p.N) {
+          *reinterpret_cast<f4*>(row + n) = acc[i][j];
+        } else {
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            if (n + v < p.N) row[n + v] = acc[i][j][v];
         }
       }
     }
@@ -795,7 +835,10 @@ struct EpiRowMajor {
 };
 
 // NCHW output: out[b][m][pix] for n = b*HW + pix; optional bias + activation
-// (0 identity, 1 ReLU, 2 tanh), as nn_conv_reshape.hlsl:23-26.
+// (0 identity, 1 ReLU, 2 tanh), as nn_conv_reshape.hlsl:23-26.  With TACC a
+// lane's four columns are four consecutive pixels of one plane unless they
+// cross an image boundary; the quad is stored at 4-byte alignment (planes of
+// odd size; unaligned access is on).
 struct EpiNCHW {
   struct Params {
     float* out;
@@ -803,29 +846,56 @@ struct EpiNCHW {
     uint32_t M, HW, N, act;
     FastDiv dHW;
   };
-  template <int MT, int NT, int FM, int FN>
+  template <int MT, int NT, int FM, int FN, bool TACC>
   __device__ static __forceinline__ void store(const Params& p, const f4 (&acc)[FM][FN],
                                                uint32_t m0, uint32_t n0, uint32_t, int wm,
                                                int wn, int lane) {
     const int r = lane & 15, g = lane >> 4;
+    if constexpr (!TACC) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const uint32_t n = n0 + wn * (FN * 16) + j * 16 + r;
+        const uint32_t b = fdiv(n, p.dHW);
+        const uint32_t base = b * p.M * p.HW + (n - b * p.HW);
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const uint32_t m = m0 + wm * (FM * 16) + i * 16 + 4 * g + v;
+            if (m < p.M && n < p.N)
+              p.out[base + m * p.HW] = epi_act(acc[i][j][v] + (p.bias ? p.bias[m] : 0.f), p.act);
+          }
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-      const uint32_t n = n0 + wn * (FN * 16) + j * 16 + r;
+      const uint32_t n = n0 + wn * (FN * 16) + j * 16 + 4 * g;
+      if (n >= p.N) continue;
       const uint32_t b = fdiv(n, p.dHW);
-      const uint32_t base = b * p.M * p.HW + (n - b * p.HW);
+      const uint32_t pix = n - b * p.HW;
+      const bool quad = pix + 3 < p.HW && n + 3 < p.N;
+      const size_t base = size_t(b) * p.M * p.HW + pix;
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
+        const uint32_t m = m0 + wm * (FM * 16) + i * 16 + r;
+        if (m >= p.M) continue;
+        const float bias = p.bias ? p.bias[m] : 0.f;
+        f4 z;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const uint32_t m = m0 + wm * (FM * 16) + i * 16 + 4 * g + v;
-          if (m < p.M && n < p.N) {
-            float z = acc[i][j][v];
-            if (p.bias) z += p.bias[m];
-            if (p.act == 1)
-              z = fmaxf(z, 0.f);
-            else if (p.act == 2)
-              z = tanhf(z);
-            p.out[base + m * p.HW] = z;
+        for (int v = 0; v < 4; ++v) z[v] = epi_act(acc[i][j][v] + bias, p.act);
+        if (quad) {
+          stu(p.out + base + size_t(m) * p.HW, z);
+        } else {
+          uint32_t bb = b, pp = pix;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            if (n + v < p.N) p.out[(size_t(bb) * p.M + m) * p.HW + pp] = z[v];
+            if (++pp == p.HW) {
+              pp = 0;
+              ++bb;
+            }
           }
         }
       }
@@ -833,8 +903,9 @@ struct EpiNCHW {
   }
 };
 
-// NCHW output over a padded pixel grid (n = b*OHWp + oh*OWp + ow, ow < OWp):
-// columns with ow >= OW are dropped; otherwise as EpiNCHW.
+// NCHW output over a padded pixel grid (n = b*OHWp + oh*OWp + ow, ow < OWp,
+// OWp % 4 == 0, so a TACC lane's four columns share one padded row): columns
+// with ow >= OW are dropped; otherwise as EpiNCHW.
 struct EpiNCHWPad {
   struct Params {
     float* out;
@@ -842,31 +913,42 @@ struct EpiNCHWPad {
     uint32_t M, OHW, OW, OWp, OHWp, N, act;
     FastDiv dOHWp, dOWp;
   };
-  template <int MT, int NT, int FM, int FN>
+  template <int MT, int NT, int FM, int FN, bool TACC>
   __device__ static __forceinline__ void store(const Params& p, const f4 (&acc)[FM][FN],
                                                uint32_t m0, uint32_t n0, uint32_t, int wm,
                                                int wn, int lane) {
     const int r = lane & 15, g = lane >> 4;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-      const uint32_t n = n0 + wn * (FN * 16) + j * 16 + r;
+      const uint32_t n = n0 + wn * (FN * 16) + j * 16 + (TACC ? 4 * g : r);
       const uint32_t b = fdiv(n, p.dOHWp), rem = n - b * p.OHWp;
       const uint32_t oh = fdiv(rem, p.dOWp), ow = rem - oh * p.OWp;
       if (n >= p.N || ow >= p.OW) continue;
-      const uint32_t base = b * p.M * p.OHW + oh * p.OW + ow;
+      const size_t base = size_t(b) * p.M * p.OHW + oh * p.OW + ow;
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
+        if constexpr (!TACC) {
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const uint32_t m = m0 + wm * (FM * 16) + i * 16 + 4 * g + v;
-          if (m < p.M) {
-            float z = acc[i][j][v];
-            if (p.bias) z += p.bias[m];
-            if (p.act == 1)
-              z = fmaxf(z, 0.f);
-            else if (p.act == 2)
-              z = tanhf(z);
-            p.out[base + m * p.OHW] = z;
+          for (int v = 0; v < 4; ++v) {
+            const uint32_t m = m0 + wm * (FM * 16) + i * 16 + 4 * g + v;
+            if (m < p.M)
+              p.out[base + size_t(m) * p.OHW] =
+                  epi_act(acc[i][j][v] + (p.bias ? p.bias[m] : 0.f), p.act);
+          }
+        } else {
+          const uint32_t m = m0 + wm * (FM * 16) + i * 16 + r;
+          if (m >= p.M) continue;
+          const float bias = p.bias ? p.bias[m] : 0.f;
+          f4 z;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) z[v] = epi_act(acc[i][j][v] + bias, p.act);
+          float* dst = p.out + base + size_t(m) * p.OHW;
+          if (ow + 3 < p.OW) {
+            stu(dst, z);
+          } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              if (ow + v < p.OW) dst[v] = z[v];
           }
         }
       }
@@ -942,6 +1024,7 @@ __global__ void __launch_bounds__(kThreads)
     for (int j = 0; j < FN; ++j) acc[i][j] = zero4();
 
   constexpr bool DA = LA::LDSD, DB = LB::LDSD;
+  constexpr bool TACC = LB::kTransAcc;
   const int r = lane & 15, g = lane >> 4;
   // MFMAs of the K tile in LDS stage `cur`.
   auto compute = [&](int cur) {
@@ -959,7 +1042,9 @@ __global__ void __launch_bounds__(kThreads)
         for (int i = 0; i < FM; ++i)
 #pragma unroll
           for (int j = 0; j < FN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][s], bf[j][s], acc[i][j], 0, 0, 0);
+            // TACC: B first, the block accumulates C transposed (see the epilogues).
+            acc[i][j] = TACC ? __builtin_amdgcn_mfma_f32_16x16x4f32(bf[j][s], af[i][s], acc[i][j], 0, 0, 0)
+                             : __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][s], bf[j][s], acc[i][j], 0, 0, 0);
     };
     if constexpr (WKS) {
       slice(16 * wave);
@@ -1013,7 +1098,7 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] += red[(w * FM * FN + i * FN + j) * 64 + lane];
   }
-  EPI::template store<MT, NT, FM, FN>(pe, acc, m0, n0, z, wm, wn, lane);
+  EPI::template store<MT, NT, FM, FN, TACC>(pe, acc, m0, n0, z, wm, wn, lane);
 }
 
 // ---------------------------------------------------------------------------

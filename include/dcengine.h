@@ -233,6 +233,14 @@ void ResetProfile(void);
  * so that a timed run carries only the events it reports. */
 void SetProfileFilter(const char* families);
 
+/* One HIP-event pair around all work queued between the two calls, recorded
+ * as one launch of `family` with the given algorithmic FLOPs and bytes
+ * (GetProfile reads it back), independent of SetProfiling.  For timing a
+ * run of back-to-back launches without an event pair per launch.  One region
+ * at a time; refused while capturing. */
+bool BeginProfileRegion(const char* family, double flops, double bytes);
+bool EndProfileRegion(void);
+
 /* Passes that move more than `bytes` bytes use nontemporal (streaming) loads
  * and stores; smaller ones use the default cache policy.  The default is
  * 256 MiB, the size of the MI355X Infinity Cache; a negative value restores
