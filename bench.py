@@ -64,21 +64,21 @@ TRAFFIC_PROFILE = os.path.join(REPO, "profiles", "alexnet224_b128_conv_bwd_hbm_t
 
 
 def measured_traffic():
-    """HBM bytes per conv-backward GEMM launch (its split-K finish included)
-    from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE measurement, and the
-    algorithmic bytes per launch; (None, None) when the summary is absent."""
+    """HBM bytes per ConvBackwardFused call (every kernel of the call) from
+    the committed rocprofv3 FETCH_SIZE / WRITE_SIZE measurement, and the
+    algorithmic bytes per call; (None, None) when the summary is absent."""
     try:
         text = open(TRAFFIC_PROFILE).read()
     except OSError:
         return None, None
     vals = {}
-    for key in ("conv_bwd_hbm_bytes_per_step", "conv_bwd_gemm_launches_per_step",
+    for key in ("conv_bwd_hbm_bytes_per_step", "conv_bwd_calls_per_step",
                 "conv_bwd_algorithmic_bytes_per_step"):
         m = re.search(key + r": (\d+)", text)
         if not m:
             return None, None
         vals[key] = int(m.group(1))
-    n = vals["conv_bwd_gemm_launches_per_step"]
+    n = vals["conv_bwd_calls_per_step"]
     return vals["conv_bwd_hbm_bytes_per_step"] / n, vals["conv_bwd_algorithmic_bytes_per_step"] / n
 
 
@@ -857,8 +857,9 @@ def main():
         "roofline": {
             "bound": "mfma",
             "kernel": "conv backward of all layers, each ConvBackwardFused call whole: G pass "
-                      "k_to_nhwc (ReLU mask + NHWC transpose + bias partials), k_rowsum, k_permute_w, "
-                      "dW k_igemm<LdGradKR,LdXTapKR> (LdPkKR for c1, C = 3) + k_dw_final, "
+                      "k_to_nhwc (ReLU mask + NHWC transpose + bias partials; k_mask_pad for c1), "
+                      "k_rowsum, k_permute_w, dW k_igemm<LdGradKR,LdXTapKR> (c1, C = 3: "
+                      "k_igemm<LdGPadRK,LdPsRK> on the stride-phase copy) + k_dw_final, "
                       "dX k_igemm<LdDenseRK,LdPixRK> (+ k_splitk_nchw when split)",
             "achieved": round(achieved, 3),
             "peak": MFMA_FP32_PEAK_TFLOPS,
@@ -867,10 +868,10 @@ def main():
             "gemm_kernels_achieved": round(achieved_gemm, 3),
             "gemm_kernels_frac": round(achieved_gemm / MFMA_FP32_PEAK_TFLOPS, 4),
             "traffic": traffic,
-            "traffic_unit": "HBM bytes per conv-backward GEMM launch incl. its split-K finish "
+            "traffic_unit": "HBM bytes per ConvBackwardFused call, all its kernels "
                             "(rocprofv3 FETCH_SIZE/WRITE_SIZE scaled by a copy kernel; "
                             "profiles/alexnet224_b128_conv_bwd_hbm_traffic.md)" if traffic else None,
-            "algorithmic_bytes_per_launch": alg_bytes,
+            "algorithmic_bytes_per_call": alg_bytes,
             "calls_per_step": n_bwd / args.steps,
             "gemm_launches_per_step": (n_dw + n_dx) / args.steps,
             "ms_per_step": round(ms_bwd / args.steps, 4),
