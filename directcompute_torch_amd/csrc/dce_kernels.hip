@@ -1905,13 +1905,14 @@ __global__ void __launch_bounds__(256)
 // is the limit there, and more LDS per block cost occupancy: 73 -> 77 us).
 __host__ __device__ constexpr uint32_t dw_gband(uint32_t S) { return S == 1 ? kDwBand : kDwBand / 2; }
 
-// dW / db partials.  Block (y, c) walks the bands (image n, output rows
-// [o0, o0 + RB), RB even) of channel c for n = y, y + gridDim.x, ...:
+// dW / db partials.  Block (c, piece) walks a contiguous range of channel c's
+// B * nb units (unit u = band u mod nb of image u / nb: output rows
+// [o0, o0 + RB), RB even); the ranges split the units evenly over the pieces:
 //   LDS x cell (i, j) = x[o0*S - p + i][j - p]      (LXR x LXW, zero outside)
 //   LDS g cell (i, j) = dy[o0 + i][j]               (LGR x LGW, zero outside)
 // A thread takes 2 x 2 blocks of dy and the (S + K) x (S + K) x window under
 // them.  The K*K + 1 running sums are reduced once per block (waves by
-// shuffle, then the 4 wave sums in order) and stored as part[c][y][t] (double).
+// shuffle, then the 4 wave sums in order) and stored as part[c][piece][t] (double).
 template <int K, int S, bool V4>
 __global__ void __launch_bounds__(256)
     k_dw_bwd_filter_band(const float* __restrict__ dy, const float* __restrict__ x,

@@ -413,6 +413,70 @@ def test_depthwise(eng, B, C, H, W, k, s, p, policy):
     release(eng, hx, hf, hb, hdy, hy, hdx, hdf, hdb)
 
 
+# ------------------------------------- MobileNetV2 b64 @112^2 at full size
+@pytest.mark.parametrize("B,C,H,W,s", [(64, 96, 112, 112, 2), (64, 144, 56, 56, 1), (64, 192, 28, 28, 1)])
+def test_mobilenet_b64_block_full_size_sampled(eng, B, C, H, W, s):
+    """The expanded tensors of the MobileNetV2 stack's blocks at the timed
+    size (b64 @112^2): BN statistics and forward, ReLU6, depthwise 3x3
+    forward and backward, ReLU6 gradient and BN backward over the whole
+    tensor, with the piece counts, band plans and streaming forms this size
+    selects (passes over 256 MiB).  Channels are independent in all of them,
+    so each sampled channel is checked against the float64 oracle over the
+    full batch exactly.  Every stage takes the device's previous output as
+    its input, as the training step does."""
+    r = rng(C * H)
+    x = (r.standard_normal((B, C, H, W)) * 2 + 0.5).astype(np.float32)
+    gamma = (1 + 0.1 * r.standard_normal(C)).astype(np.float32)
+    beta = (0.1 * r.standard_normal(C)).astype(np.float32)
+    f = (r.standard_normal((C, 1, 3, 3)) / 3).astype(np.float32)
+    fb = (0.1 * r.standard_normal(C)).astype(np.float32)
+    OH, OW = (H - 1) // s + 1, (W - 1) // s + 1
+    dz = r.standard_normal((B, C, OH, OW)).astype(np.float32)
+    cs = [0, C // 2 + 1, C - 1]
+    n, eps, mom = x.size, 1e-5, 0.1
+    shp = (B, C, H, W)
+    hx, hg, hb, hf, hfb, hdz = (upload(eng, a) for a in (x, gamma, beta, f, fb, dz))
+    hrm, hrv = upload(eng, np.zeros(C, np.float32)), upload(eng, np.ones(C, np.float32))
+    hmu, hvar, hy, ha = new(eng, C), new(eng, C), new(eng, n), new(eng, n)
+    hz, hda, hdf, hdfb = new(eng, dz.size), new(eng, n), new(eng, f.size), new(eng, C)
+    hdy, hdg, hdbe, hdx = new(eng, n), new(eng, C), new(eng, C), new(eng, n)
+    xs = x[:, cs]
+
+    run(eng, "batchnorm_mean_var", [hx], [hmu, hvar, hrm, hrv], B, C, H * W, 1, fbits(mom))
+    mu, var = download(eng, hmu, (C,)), download(eng, hvar, (C,))
+    mu_r, var_r, _, _ = K.batchnorm_mean_var(xs, np.zeros(3), np.ones(3), mom, True)
+    assert rel_err(mu[cs], mu_r) <= 1e-5 and rel_err(var[cs], var_r) <= 1e-5
+    run(eng, "batchnorm_forward", [hx, hmu, hvar, hg, hb], [hy], B, C, H * W, fbits(eps))
+    y = download(eng, hy, shp)[:, cs]
+    assert rel_err(y, K.batchnorm_forward(xs, mu[cs], var[cs], gamma[cs], beta[cs], eps)) <= 1e-5
+    run(eng, "relu6", [hy], [ha], n)
+    a = download(eng, ha, shp)[:, cs]
+    assert rel_err(a, K.relu6(y)) <= 1e-6
+    cb = (B, C, H, W, 3, 3, s, 1, OH)
+    run(eng, "depthwise_conv_forward", [ha, hf, hfb], [hz], *cb)
+    z = download(eng, hz, dz.shape)[:, cs]
+    assert rel_err(z, K.depthwise_forward(a, f[cs], fb[cs], s, 1)) <= 1e-5
+    run(eng, "depthwise_conv_backward_input", [hdz, hf], [hda], *cb)
+    da = download(eng, hda, shp)[:, cs]
+    assert rel_err(da, K.depthwise_backward_input(dz[:, cs], f[cs], a.shape, s, 1)) <= TOL
+    run(eng, "depthwise_conv_backward_filter", [hdz, ha], [hdf, hdfb], *cb)
+    df_r, dfb_r = K.depthwise_backward_filter(dz[:, cs], a, 3, 3, s, 1)
+    assert rel_err(download(eng, hdf, f.shape)[cs], df_r) <= TOL
+    assert rel_err(download(eng, hdfb, (C,))[cs], dfb_r) <= TOL
+    run(eng, "relu6_grad", [hda, hy], [hdy], n)
+    dy = download(eng, hdy, shp)[:, cs]
+    assert rel_err(dy, K.relu6_grad(da, y)) <= 1e-6
+    run(eng, "batchnorm_backward_reduce", [hx, hdy, hmu, hvar], [hdg, hdbe], B, C, H * W, fbits(eps))
+    dg, dbe = download(eng, hdg, (C,)), download(eng, hdbe, (C,))
+    dg_r, dbe_r = K.batchnorm_backward_reduce(xs, dy, mu[cs], var[cs], eps)
+    assert rel_err(dg[cs], dg_r) <= TOL and rel_err(dbe[cs], dbe_r) <= TOL
+    run(eng, "batchnorm_backward_dx", [hx, hdy, hmu, hvar, hg, hdg, hdbe], [hdx], B, C, H * W, fbits(eps))
+    dx_r = K.batchnorm_backward_dx(xs, dy, mu[cs], var[cs], gamma[cs], dg[cs], dbe[cs], eps)
+    assert rel_err(download(eng, hdx, shp)[:, cs], dx_r) <= TOL
+    release(eng, hx, hg, hb, hf, hfb, hdz, hrm, hrv, hmu, hvar, hy, ha, hz, hda, hdf, hdfb, hdy, hdg,
+            hdbe, hdx)
+
+
 # ------------------------------------------------------------ loss / metrics
 @pytest.mark.parametrize("B,Kc", [(1, 2), (64, 10), (128, 1000), (300, 7)])
 def test_softmax_ce(eng, B, Kc):

@@ -93,11 +93,12 @@ def test_lenet_gradient_accumulation(eng):
     _compare_grads(g, total)
 
 
-def test_alexnet_step_adamw(eng):
-    """AlexNet-224 (Linear 9216-4096-4096-1000) full step at batch 2 with
-    AdamW lr 1e-4, wd 0.01, element clip 1.0 -- every layer shape of the
-    benchmark except the batch size."""
-    B = 2
+@pytest.mark.parametrize("B", [2, 128], ids=["b2", "b128"])
+def test_alexnet_step_adamw(eng, B):
+    """AlexNet-224 (Linear 9216-4096-4096-1000) full step with AdamW lr 1e-4,
+    wd 0.01, element clip 1.0: at batch 2, and at batch 128 -- the timed
+    training step itself, with its split-K choices, stride-phase c1 copy and
+    tile plans."""
     x = rng(5000).standard_normal((B, 3, 224, 224)).astype(np.float32)
     y = rng(5002).integers(0, 1000, B).astype(np.float32)
     P = WL.alexnet_params(rng(5001))
@@ -126,11 +127,11 @@ def test_alexnet_step_adamw(eng):
         assert rel_err(new[k], w_r) <= 1e-6, k
 
 
-def test_unet_step_clip_adam(eng):
+@pytest.mark.parametrize("B,S", [(2, 64), (8, 256)], ids=["b2_64", "b8_256"])
+def test_unet_step_clip_adam(eng, B, S):
     """UNet-base16 (4 levels, conv3x3-BN-ReLU x2, maxpool, upsample, concat,
-    1x1 head, sigmoid, Dice) at batch 2, 64x64; global-norm clip 1.0 then
-    Adam lr 1e-3."""
-    B, S = 2, 64
+    1x1 head, sigmoid, Dice); global-norm clip 1.0 then Adam lr 1e-3.  At
+    batch 2 64x64, and at the timed size, batch 8 256x256."""
     x = rng(4000).random((B, 3, S, S)).astype(np.float32)
     blobs = (rng(4002).random((B, 1, S // 8, S // 8)) < 0.3).astype(np.float32)
     t = np.repeat(np.repeat(blobs, 8, axis=2), 8, axis=3)
@@ -160,12 +161,13 @@ def test_unet_step_clip_adam(eng):
         assert rel_err(new[k], w_r) <= 1e-6, k
 
 
-def test_mobilenet_ir_stack_step(eng):
+@pytest.mark.parametrize("B,S", [(2, 32), (64, 112)], ids=["b2_32", "b64_112"])
+def test_mobilenet_ir_stack_step(eng, B, S):
     """MobileNetV2 inverted-residual stack (16->24 s2, 24->24, 24->32 s2,
-    32->32 x2; BN train mode, ReLU6, depthwise 3x3, residual adds) at batch 2,
-    32x32, then GAP + Linear + softmax-CE, SGD."""
-    B = 2
-    x = rng(3000).standard_normal((B, 16, 32, 32)).astype(np.float32)
+    32->32 x2; BN train mode, ReLU6, depthwise 3x3, residual adds), then GAP +
+    Linear + softmax-CE, SGD.  At batch 2 32x32, and at the timed size, batch
+    64 112x112 (the float64 oracle needs about 13 GB of host memory)."""
+    x = rng(3000).standard_normal((B, 16, S, S)).astype(np.float32)
     y = rng(3002).integers(0, 10, B).astype(np.float32)
     P = WL.mobilenet_params(rng(3001))
     be, loss, pins = _run_device(eng, WL.mobilenet, P, x, lambda b, z: b.softmax_ce(z, y))
