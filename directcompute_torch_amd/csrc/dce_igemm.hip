@@ -1105,6 +1105,59 @@ __global__ void __launch_bounds__(kThreads)
 // Side kernels: NHWC transpose (+ ReLU mask + bias-gradient partials),
 // filter re-layouts, split-K sums.
 // ---------------------------------------------------------------------------
+// Filters in the K order of the pixel loaders (flat or blocked), zero for
+// padding channels; `inner` is the padded channel count the K axis runs over
+// (Cp for the forward, OCp for dX):
+// mode 0 (forward A): out[oc][kk] = w[oc][c][khw]   with c  = channel of kk
+// mode 1 (dX A):      out[c][kk]  = w[oc][c][khw]   with oc = channel of kk
+// where kk = khw*inner + ch (flat) or (cb*KK + khw)*kCB + ci, ch = cb*kCB + ci
+// (blocked).  Rows are ld >= KK*inner floats apart, zero past KK*inner; size
+// rows * ld, rows = OC (mode 0) or C (mode 1).  The packed forward (C < 4
+// channels) uses the flat order with inner = C and ld = pad4(KK*C).
+struct WPerm {
+  const float* w;  // null: nothing to re-lay
+  float* out;
+  uint32_t OC, C, KK, inner, ld;
+  int mode, blocked;
+  uint32_t blocks() const { return w ? cdiv(size_t(mode == 0 ? OC : C) * ld, 256) : 0; }
+};
+
+__device__ __forceinline__ void permute_w_elem(const WPerm& pw, uint32_t i) {
+  const float* __restrict__ w = pw.w;
+  float* __restrict__ out = pw.out;
+  const uint32_t OC = pw.OC, C = pw.C, KK = pw.KK, inner = pw.inner, ld = pw.ld;
+  const int mode = pw.mode, blocked = pw.blocked;
+  const uint32_t kdim = KK * inner;
+  const uint32_t rows = mode == 0 ? OC : C;
+  if (i >= rows * ld) return;
+  const uint32_t r = i / ld, kk = i - r * ld;
+  if (kk >= kdim) {  // row pitch padding
+    out[i] = 0.f;
+    return;
+  }
+  uint32_t khw, ch;
+  if (blocked) {
+    const uint32_t blk = kk / kCB, ci = kk - blk * kCB;
+    const uint32_t cb = blk / KK;
+    khw = blk - cb * KK;
+    ch = cb * kCB + ci;
+  } else {
+    khw = kk / inner;
+    ch = kk - khw * inner;
+  }
+  if (mode == 0)
+    out[i] = ch < C ? w[(r * C + ch) * KK + khw] : 0.f;
+  else
+    out[i] = ch < OC ? w[(ch * C + r) * KK + khw] : 0.f;
+}
+
+__global__ void k_permute_w(WPerm pw) { permute_w_elem(pw, blockIdx.x * blockDim.x + threadIdx.x); }
+
+static bool permute_w(const WPerm& pw) {
+  hipLaunchKernelGGL(k_permute_w, dim3(pw.blocks()), dim3(256), 0, stream(), pw);
+  return check_launch("permute_w");
+}
+
 // out[((b*HW) + p)*Cp + c] = (c < C) ? in[(b*C + c)*HW + p] masked : 0.
 // Block: CB channels x PB = 2048 / CB pixels through LDS (CB = 16 for tensors
 // of at most 16 channels, 32 otherwise, so few-channel tensors do not leave
@@ -1115,11 +1168,17 @@ __global__ void __launch_bounds__(kThreads)
 // rows of odd length leave the load quads only 4-byte aligned; the GPU runs
 // with unaligned access enabled.  A quad that would cross the end of its row
 // is read dword by dword.
+// Workgroups past the first nMain re-lay filters instead (pw: the forward's
+// filter permutation, which then costs no launch of its own).
 template <int CB>
 __global__ void __launch_bounds__(256)
     k_to_nhwc(const float* __restrict__ in, const float* __restrict__ y, float* __restrict__ out,
               float* __restrict__ dbPart, uint32_t C, uint32_t HW, uint32_t Cp, uint32_t npb,
-              uint32_t ncb, uint32_t nB) {
+              uint32_t ncb, uint32_t nB, uint32_t nMain, WPerm pw) {
+  if (blockIdx.x >= nMain) {
+    permute_w_elem(pw, (blockIdx.x - nMain) * 256 + threadIdx.x);
+    return;
+  }
   constexpr int PB = 2048 / CB, PQ = PB / 4;  // pixels per block, pixel quads per row
   constexpr int CR = 256 / PQ;                // channel rows per load pass
   constexpr int PR = 256 / (CB / 4);          // pixels per store pass
@@ -1128,7 +1187,7 @@ __global__ void __launch_bounds__(256)
   // 1-D grid over (pixel block, channel block, image), pixel block fastest,
   // in XCD-contiguous order: a plane row's neighbouring blocks share its
   // partial cache lines.
-  const uint32_t id = xcd_block_id();
+  const uint32_t id = xcd_block_id(nMain);
   const uint32_t pb = id % npb, rest = id / npb;
   const uint32_t c0 = (rest % ncb) * CB, p0 = pb * PB, b = rest / ncb;
   const int tid = threadIdx.x;
@@ -1202,11 +1261,12 @@ __global__ void k_to_nhwc_small(const float* __restrict__ in, float* __restrict_
 }
 
 // out[c] = sum of the `rows` partials of channel c (stored contiguously,
-// part[c*rows + r]): 256 strided per-thread sums, then a fixed tree.
-__global__ void __launch_bounds__(256)
-    k_rowsum(const float* __restrict__ part, float* __restrict__ out, uint32_t rows) {
+// part[c*rows + r]): 256 strided per-thread sums, then a fixed tree.  One
+// 256-thread block per channel.
+__device__ __forceinline__ void rowsum_block(const float* __restrict__ part,
+                                             float* __restrict__ out, uint32_t rows,
+                                             uint32_t c) {
   __shared__ float sh[4];
-  const uint32_t c = blockIdx.x;
   const float* p = part + size_t(c) * rows;
   float s = 0.f;
 #pragma unroll 8
@@ -1217,42 +1277,11 @@ __global__ void __launch_bounds__(256)
   if (threadIdx.x == 0) out[c] = (sh[0] + sh[1]) + (sh[2] + sh[3]);
 }
 
-// Filters in the K order of the pixel loaders (flat or blocked), zero for
-// padding channels; `inner` is the padded channel count the K axis runs over
-// (Cp for the forward, OCp for dX):
-// mode 0 (forward A): out[oc][kk] = w[oc][c][khw]   with c  = channel of kk
-// mode 1 (dX A):      out[c][kk]  = w[oc][c][khw]   with oc = channel of kk
-// where kk = khw*inner + ch (flat) or (cb*KK + khw)*kCB + ci, ch = cb*kCB + ci
-// (blocked).  Rows are ld >= KK*inner floats apart, zero past KK*inner; size
-// rows * ld, rows = OC (mode 0) or C (mode 1).  The packed forward (C < 4
-// channels) uses the flat order with inner = C and ld = pad4(KK*C).
-__global__ void k_permute_w(const float* __restrict__ w, float* __restrict__ out, uint32_t OC,
-                            uint32_t C, uint32_t KK, uint32_t inner, uint32_t ld, int mode,
-                            int blocked) {
-  const uint32_t kdim = KK * inner;
-  const uint32_t rows = mode == 0 ? OC : C;
-  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= rows * ld) return;
-  const uint32_t r = i / ld, kk = i - r * ld;
-  if (kk >= kdim) {  // row pitch padding
-    out[i] = 0.f;
-    return;
-  }
-  uint32_t khw, ch;
-  if (blocked) {
-    const uint32_t blk = kk / kCB, ci = kk - blk * kCB;
-    const uint32_t cb = blk / KK;
-    khw = blk - cb * KK;
-    ch = cb * kCB + ci;
-  } else {
-    khw = kk / inner;
-    ch = kk - khw * inner;
-  }
-  if (mode == 0)
-    out[i] = ch < C ? w[(r * C + ch) * KK + khw] : 0.f;
-  else
-    out[i] = ch < OC ? w[(ch * C + r) * KK + khw] : 0.f;
+__global__ void __launch_bounds__(256)
+    k_rowsum(const float* __restrict__ part, float* __restrict__ out, uint32_t rows) {
+  rowsum_block(part, out, rows, blockIdx.x);
 }
+
 
 // Deterministic split-K sum: out[i] = sum_z part[z*n + i] in z order.
 __global__ void k_splitk_sum(const float* __restrict__ part, float* __restrict__ out, uint32_t n,
@@ -1295,10 +1324,32 @@ __global__ void __launch_bounds__(256)
 // stride of the tap axis (pad4(C), or C for the packed layout), and each
 // split's partials start 4 * ceil(OC*KK*Cp / 4) floats apart.  Padding
 // channels (c >= C) and the tail past OC*KK*Cp are dropped.
+//
+// The same launch carries the conv backward's other small passes as extra
+// blocks after the nMain finishing blocks, so that they cost no launch of
+// their own: side.nRow blocks sum the bias-gradient partials (rowsum_block)
+// and the rest re-lay the filters for the dX GEMM (permute_w_elem, mode 1).
+// The jobs touch disjoint buffers.
+struct BwdSide {
+  const float* dbPart;  // bias-gradient partials [OC][dbRows]
+  float* db;
+  uint32_t dbRows, nRow;  // nRow = OC, or 0 for no bias gradient
+  WPerm perm;             // the dX filters (perm.w null: none)
+};
+
 template <int SL>
 __global__ void __launch_bounds__(256)
     k_dw_final(const f4* __restrict__ part, float* __restrict__ dw, uint32_t OC, uint32_t C,
-               uint32_t KK, uint32_t Cp, uint32_t splits, uint32_t trans) {
+               uint32_t KK, uint32_t Cp, uint32_t splits, uint32_t trans, uint32_t nMain,
+               BwdSide side) {
+  if (blockIdx.x >= nMain) {
+    const uint32_t j = blockIdx.x - nMain;
+    if (j < side.nRow)
+      rowsum_block(side.dbPart, side.db, side.dbRows, j);
+    else
+      permute_w_elem(side.perm, (j - side.nRow) * 256 + threadIdx.x);
+    return;
+  }
   constexpr uint32_t QB = 256 / SL;
   __shared__ f4 sh[SL][QB];
   const uint32_t N = KK * Cp, total = OC * N, nq = (total + 3) / 4;
@@ -1353,19 +1404,21 @@ static uint32_t dw_final_slices(uint32_t nq, uint32_t splits) {
 }
 
 static bool dw_final(const float* part, float* dw, uint32_t OC, uint32_t C, uint32_t KK,
-                     uint32_t Cp, uint32_t splits, bool trans) {
+                     uint32_t Cp, uint32_t splits, bool trans, BwdSide side = BwdSide{}) {
   const uint32_t nq = cdiv(size_t(OC) * KK * Cp, 4), sl = dw_final_slices(nq, splits);
   const f4* p4 = reinterpret_cast<const f4*>(part);
   const uint32_t tr = trans ? 1u : 0u;
+  const uint32_t nMain = cdiv(nq, 256u / sl);
+  const dim3 grid(nMain + side.nRow + side.perm.blocks());
   if (sl == 1)
-    hipLaunchKernelGGL(k_dw_final<1>, dim3(cdiv(nq, 256u)), dim3(256), 0, stream(), p4, dw, OC, C,
-                       KK, Cp, splits, tr);
+    hipLaunchKernelGGL(k_dw_final<1>, grid, dim3(256), 0, stream(), p4, dw, OC, C, KK, Cp, splits,
+                       tr, nMain, side);
   else if (sl == 4)
-    hipLaunchKernelGGL(k_dw_final<4>, dim3(cdiv(nq, 64u)), dim3(256), 0, stream(), p4, dw, OC, C,
-                       KK, Cp, splits, tr);
+    hipLaunchKernelGGL(k_dw_final<4>, grid, dim3(256), 0, stream(), p4, dw, OC, C, KK, Cp, splits,
+                       tr, nMain, side);
   else
-    hipLaunchKernelGGL(k_dw_final<16>, dim3(cdiv(nq, 16u)), dim3(256), 0, stream(), p4, dw, OC,
-                       C, KK, Cp, splits, tr);
+    hipLaunchKernelGGL(k_dw_final<16>, grid, dim3(256), 0, stream(), p4, dw, OC, C, KK, Cp,
+                       splits, tr, nMain, side);
   return check_launch("dw_final");
 }
 
@@ -1650,6 +1703,17 @@ static bool split_nchw(const float* part, const float* bias, float* out, uint32_
   return check_launch("splitk_nchw");
 }
 
+// Deterministic split-K sum of row-major partials into c (n elements).
+static bool split_sum(const float* part, float* c, uint32_t n, uint32_t splits) {
+  if (n % 4 == 0 && aligned16(part) && aligned16(c))
+    hipLaunchKernelGGL(k_splitk_sum4, dim3(cdiv(n / 4, 256u)), dim3(256), 0, stream(),
+                       reinterpret_cast<const f4*>(part), reinterpret_cast<f4*>(c), n / 4, splits);
+  else
+    hipLaunchKernelGGL(k_splitk_sum, dim3(cdiv(n, 256u)), dim3(256), 0, stream(), part, c, n,
+                       splits);
+  return check_launch("splitk_sum");
+}
+
 // ----------------------------------------------------------------- GEMM
 template <bool AT, bool BT>
 struct GemmRun {
@@ -1657,6 +1721,7 @@ struct GemmRun {
   float* c;
   uint32_t M, K, N, splits;
   uint32_t lda, ldb, kdA, kdB;  // row strides and K extents as stored (padded)
+  float* part;                  // split-K partials (splits > 1)
   // A[m][k]: stored M x K (ROWK) or K x M (KROW); B[n][k]: stored N x K (ROWK) or K x N (KROW).
   template <int MT, int KT>
   using LAt = typename std::conditional<AT, LdDenseKR<MT, KT>, LdDenseRK<MT, KT>>::type;
@@ -1672,9 +1737,14 @@ struct GemmRun {
     using LB = LBt<NT, KT>;
     const typename LA::Params pa{a, lda, AT ? lda : M, kdA, (AT ? K : M) * lda};
     const typename LB::Params pb{b, ldb, BT ? N : ldb, kdB, (BT ? N : K) * ldb};
+    const uint32_t kt = cdiv(std::max(kdA, kdB), KT);
     const EpiRowMajor::Params pe{c, M, N, N, M * N};
-    return launch<MT, NT, KT, LA, LB, EpiRowMajor>(pa, pb, pe, M, N, cdiv(std::max(kdA, kdB), KT),
-                                                  splits, "gemm");
+    if (splits > 1) {
+      const EpiRowMajor::Params pr{part, M, N, N, M * N};
+      return launch<MT, NT, KT, LA, LB, EpiRowMajor>(pa, pb, pr, M, N, kt, splits, "gemm") &&
+             split_sum(part, c, M * N, splits);
+    }
+    return launch<MT, NT, KT, LA, LB, EpiRowMajor>(pa, pb, pe, M, N, kt, 1, "gemm");
   }
 };
 
@@ -1733,7 +1803,7 @@ bool gemm(const float* a, const float* b, float* c, uint32_t M, uint32_t K, uint
     if (!check_launch("gemm_pad")) return false;
     bp = ws + nA;
   }
-  float* out = cfg.splits > 1 ? ws + nA + nB : c;
+  float* part = cfg.splits > 1 ? ws + nA + nB : nullptr;
   const uint32_t lda = pad4(aCols), ldb = pad4(bCols);
   // K extents: a ROWK operand's k axis is its padded row (zeros past K); a
   // KROW operand's k axis is its row count K.
@@ -1743,24 +1813,13 @@ bool gemm(const float* a, const float* b, float* c, uint32_t M, uint32_t K, uint
     ProfScope prof("gemm", 2.0 * M * N * double(K),
                    4.0 * (double(M) * K + double(K) * N + double(M) * N));
     if (!aT && !bT)
-      ok = tiles_dispatch(cfg, GemmRun<false, false>{ap, bp, out, M, K, N, cfg.splits, lda, ldb, kdA, kdB});
+      ok = tiles_dispatch(cfg, GemmRun<false, false>{ap, bp, c, M, K, N, cfg.splits, lda, ldb, kdA, kdB, part});
     else if (!aT && bT)
-      ok = tiles_dispatch(cfg, GemmRun<false, true>{ap, bp, out, M, K, N, cfg.splits, lda, ldb, kdA, kdB});
+      ok = tiles_dispatch(cfg, GemmRun<false, true>{ap, bp, c, M, K, N, cfg.splits, lda, ldb, kdA, kdB, part});
     else if (aT && !bT)
-      ok = tiles_dispatch(cfg, GemmRun<true, false>{ap, bp, out, M, K, N, cfg.splits, lda, ldb, kdA, kdB});
+      ok = tiles_dispatch(cfg, GemmRun<true, false>{ap, bp, c, M, K, N, cfg.splits, lda, ldb, kdA, kdB, part});
     else
-      ok = tiles_dispatch(cfg, GemmRun<true, true>{ap, bp, out, M, K, N, cfg.splits, lda, ldb, kdA, kdB});
-    if (ok && cfg.splits > 1) {
-      const uint32_t n = M * N;
-      if (n % 4 == 0 && aligned16(out) && aligned16(c))
-        hipLaunchKernelGGL(k_splitk_sum4, dim3(cdiv(n / 4, 256u)), dim3(256), 0, stream(),
-                           reinterpret_cast<const f4*>(out), reinterpret_cast<f4*>(c), n / 4,
-                           cfg.splits);
-      else
-        hipLaunchKernelGGL(k_splitk_sum, dim3(cdiv(n, 256u)), dim3(256), 0, stream(), out, c, n,
-                           cfg.splits);
-      ok = check_launch("splitk_sum");
-    }
+      ok = tiles_dispatch(cfg, GemmRun<true, true>{ap, bp, c, M, K, N, cfg.splits, lda, ldb, kdA, kdB, part});
   }
   return ok;
 }
@@ -1771,7 +1830,8 @@ size_t nhwc_floats(uint32_t B, uint32_t C, uint32_t H, uint32_t W) {
 }
 
 static bool to_nhwc_masked(const float* in, const float* y, float* out, float* dbPart,
-                           uint32_t B, uint32_t C, uint32_t HW, uint32_t* npbOut) {
+                           uint32_t B, uint32_t C, uint32_t HW, uint32_t* npbOut,
+                           const WPerm& pw = WPerm{}) {
   const uint32_t Cp = pad4(C);
   // Family "conv_grad_nhwc": the masked dy -> G pass of the conv backward
   // (reads dy and y, writes G); "nhwc": a plain copy of an activation.
@@ -1781,19 +1841,19 @@ static bool to_nhwc_masked(const float* in, const float* y, float* out, float* d
     const uint32_t npix = B * HW;
     hipLaunchKernelGGL(k_to_nhwc_small, dim3(cdiv(npix, 256)), dim3(256), 0, stream(), in, out, C,
                        HW, Cp, npix, make_fastdiv(HW));
-    return check_launch("to_nhwc");
+    return check_launch("to_nhwc") && (!pw.w || permute_w(pw));
   }
   if (Cp <= 16) {
-    const uint32_t npb = cdiv(HW, 128);
+    const uint32_t npb = cdiv(HW, 128), nMain = npb * B;
     if (npbOut) *npbOut = npb;
-    hipLaunchKernelGGL(k_to_nhwc<16>, dim3(npb * B), dim3(256), 0, stream(), in, y, out, dbPart,
-                       C, HW, Cp, npb, 1u, B);
+    hipLaunchKernelGGL(k_to_nhwc<16>, dim3(nMain + pw.blocks()), dim3(256), 0, stream(), in, y,
+                       out, dbPart, C, HW, Cp, npb, 1u, B, nMain, pw);
   } else {
     const uint32_t npb = cdiv(HW, 64);
     if (npbOut) *npbOut = npb;
-    const uint32_t ncb = cdiv(Cp, 32);
-    hipLaunchKernelGGL(k_to_nhwc<32>, dim3(npb * ncb * B), dim3(256), 0, stream(), in, y, out,
-                       dbPart, C, HW, Cp, npb, ncb, B);
+    const uint32_t ncb = cdiv(Cp, 32), nMain = npb * ncb * B;
+    hipLaunchKernelGGL(k_to_nhwc<32>, dim3(nMain + pw.blocks()), dim3(256), 0, stream(), in, y,
+                       out, dbPart, C, HW, Cp, npb, ncb, B, nMain, pw);
   }
   return check_launch("to_nhwc");
 }
@@ -2122,12 +2182,13 @@ struct FwdRun {
                                  g.B * g.H * g.W * Cp, make_fastdiv(OHW), make_fastdiv(g.OW),
                                  make_fastdiv(BLK ? KK : Cp), make_fastdiv(g.k)};
     const uint32_t kt = cdiv(kdim, KT);
-    if (splits > 1) {
-      const EpiRowMajor::Params pe{part, g.OC, N, N, g.OC * N};
-      return launch<MT, NT, KT, LA, LB, EpiRowMajor>(pa, pb, pe, g.OC, N, kt, splits,
-                                                    "conv_forward");
-    }
     const EpiNCHW::Params pe{y, bias, g.OC, OHW, N, act, make_fastdiv(OHW)};
+    if (splits > 1) {
+      const EpiRowMajor::Params pr{part, g.OC, N, N, g.OC * N};
+      return launch<MT, NT, KT, LA, LB, EpiRowMajor>(pa, pb, pr, g.OC, N, kt, splits,
+                                                    "conv_forward") &&
+             split_nchw(part, bias, y, g.OC, N, OHW, splits, act);
+    }
     return launch<MT, NT, KT, LA, LB, EpiNCHW>(pa, pb, pe, g.OC, N, kt, 1, "conv_forward");
   }
 };
@@ -2158,12 +2219,13 @@ struct FwdPkRun {
     const typename LA::Params pa{wp, kdim, g.OC, kdim, g.OC * kdim};
     const PkParams pb = pk_params(xp, g);
     const uint32_t kt = cdiv(kdim, KT);
-    if (splits > 1) {
-      const EpiRowMajor::Params pe{part, g.OC, N, N, g.OC * N};
-      return launch<MT, NT, KT, LA, LB, EpiRowMajor>(pa, pb, pe, g.OC, N, kt, splits,
-                                                    "conv_forward");
-    }
     const EpiNCHW::Params pe{y, bias, g.OC, OHW, N, act, make_fastdiv(OHW)};
+    if (splits > 1) {
+      const EpiRowMajor::Params pr{part, g.OC, N, N, g.OC * N};
+      return launch<MT, NT, KT, LA, LB, EpiRowMajor>(pa, pb, pr, g.OC, N, kt, splits,
+                                                    "conv_forward") &&
+             split_nchw(part, bias, y, g.OC, N, OHW, splits, act);
+    }
     return launch<MT, NT, KT, LA, LB, EpiNCHW>(pa, pb, pe, g.OC, N, kt, 1, "conv_forward");
   }
 };
@@ -2242,10 +2304,11 @@ bool conv_forward(const float* x, float* x_nhwc_keep, const float* w, const floa
   float* wp = ws;
   float* xn = x_nhwc_keep ? x_nhwc_keep : ws + nw;
   float* part = ws + nw + nxs;
-  if (!(pk ? to_pk(x, xn, g) : to_nhwc(x, xn, g.B, g.C, g.H, g.W))) return false;
-  hipLaunchKernelGGL(k_permute_w, dim3(cdiv(size_t(g.OC) * kdim, 256)), dim3(256), 0, stream(), w,
-                     wp, g.OC, g.C, KK, pk ? g.C : Cp, kdim, 0, blk ? 1 : 0);
-  if (!check_launch("permute_w")) return false;
+  // The filter re-layout rides in the NHWC copy's launch.
+  const WPerm fwdPerm{w, wp, g.OC, g.C, KK, pk ? g.C : Cp, kdim, 0, blk ? 1 : 0};
+  if (pk ? !(to_pk(x, xn, g) && permute_w(fwdPerm))
+         : !to_nhwc_masked(x, nullptr, xn, nullptr, g.B, g.C, g.H * g.W, nullptr, fwdPerm))
+    return false;
   const double fl = 2.0 * g.OC * g.C * KK * double(g.B) * g.OH * g.OW;
   {
     ProfScope prof("conv_fwd", fl,
@@ -2254,7 +2317,6 @@ bool conv_forward(const float* x, float* x_nhwc_keep, const float* w, const floa
         pk ? tiles_dispatch16(cfg, FwdPkRun{wp, xn, bias, y, part, g, act, cfg.splits})
            : conv_variant<FwdRun>(s1, blk, cfg, wp, xn, bias, y, part, g, act, cfg.splits);
     if (!ok) return false;
-    if (cfg.splits > 1) return split_nchw(part, bias, y, g.OC, N, g.OH * g.OW, cfg.splits, act);
   }
   return true;
 }
@@ -2358,12 +2420,13 @@ struct DxRun {
                                  g.B * g.OH * g.OW * OCp, make_fastdiv(HW), make_fastdiv(g.W),
                                  make_fastdiv(BLK ? KK : OCp), make_fastdiv(g.k)};
     const uint32_t kt = cdiv(kdim, KT);
-    if (splits > 1) {
-      const EpiRowMajor::Params pe{part, g.C, N, N, g.C * N};
-      return launch<MT, NT, KT, LA, LB, EpiRowMajor>(pa, pb, pe, g.C, N, kt, splits,
-                                                    "conv_backward_input");
-    }
     const EpiNCHW::Params pe{dx, nullptr, g.C, HW, N, 0, make_fastdiv(HW)};
+    if (splits > 1) {
+      const EpiRowMajor::Params pr{part, g.C, N, N, g.C * N};
+      return launch<MT, NT, KT, LA, LB, EpiRowMajor>(pa, pb, pr, g.C, N, kt, splits,
+                                                    "conv_backward_input") &&
+             split_nchw(part, nullptr, dx, g.C, N, HW, splits, 0);
+    }
     return launch<MT, NT, KT, LA, LB, EpiNCHW>(pa, pb, pe, g.C, N, kt, 1, "conv_backward_input");
   }
 };
@@ -2451,9 +2514,12 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
   if (useGnhwc &&
       !to_nhwc_masked(dy, y, gn, useGpad ? nullptr : dbPart, g.B, g.OC, OHW, &npbGot))
     return false;
-  if (db) {
-    hipLaunchKernelGGL(k_rowsum, dim3(g.OC), dim3(256), 0, stream(), dbPart, db,
-                       useGpad ? dbRows : g.B * npbGot);
+  // With dW, the bias-gradient sum and the dX filter re-layout ride in the
+  // dW finishing launch (BwdSide); otherwise they run on their own.
+  const uint32_t dbRowsGot = useGpad ? dbRows : g.B * npbGot;
+  const WPerm dxPerm{w, wt, g.OC, g.C, KK, OCp, KK * OCp, 1, dx && blocked_k(OCp) ? 1 : 0};
+  if (db && !dw) {
+    hipLaunchKernelGGL(k_rowsum, dim3(g.OC), dim3(256), 0, stream(), dbPart, db, dbRowsGot);
     if (!check_launch("bias_grad")) return false;
   }
   if (dw) {
@@ -2471,25 +2537,30 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
                      4.0 * (double(npix) * OCp + double(g.B) * g.H * g.W * Cp + double(g.OC) * KK * Cp));
       ok = tiles_dispatch(dwc, DwRun{ps ? gp : gn, xn, part, g, dwc.splits, dwT, pk, ps});
       if (ok) {
+        BwdSide side{};
+        if (db) {
+          side.dbPart = dbPart;
+          side.db = db;
+          side.dbRows = dbRowsGot;
+          side.nRow = g.OC;
+        }
+        if (dx) side.perm = dxPerm;
         // The stride-phase taps are already in the filters' (c, kh, kw)
         // order: the finish is a plain split sum (one channel of C*KK taps).
-        ok = ps ? dw_final(part, dw, g.OC, 1, KK * g.C, 1, dwc.splits, dwT)
-                : dw_final(part, dw, g.OC, g.C, KK, Cx, dwc.splits, dwT);
+        ok = ps ? dw_final(part, dw, g.OC, 1, KK * g.C, 1, dwc.splits, dwT, side)
+                : dw_final(part, dw, g.OC, g.C, KK, Cx, dwc.splits, dwT, side);
       }
     }
     if (!ok) return false;
   }
   if (dx) {
-    const bool blk = blocked_k(OCp);
-    hipLaunchKernelGGL(k_permute_w, dim3(cdiv(size_t(g.C) * KK * OCp, 256)), dim3(256), 0,
-                       stream(), w, wt, g.OC, g.C, KK, OCp, KK * OCp, 1, blk ? 1 : 0);
-    if (!check_launch("permute_w")) return false;
+    const bool blk = dxPerm.blocked != 0;
+    if (!dw && !permute_w(dxPerm)) return false;
     const double fl = 2.0 * g.OC * g.C * KK * double(npix);
     {
       ProfScope prof("conv_dx", fl, 4.0 * (double(npix) * OCp + double(g.B) * g.C * g.H * g.W));
       if (!conv_variant<DxRun>(g.s == 1, blk, dxc, wt, gn, dx, qpart, g, dxc.splits))
         return false;
-      if (dxc.splits > 1) return split_nchw(qpart, nullptr, dx, g.C, g.B * HW, HW, dxc.splits, 0);
     }
   }
   return true;

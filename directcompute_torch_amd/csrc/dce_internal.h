@@ -165,11 +165,14 @@ __device__ __forceinline__ void st4s(float* p, f4 v) {
 // logical blocks that share cache lines (rows of odd length, halos) then hit
 // the same L2 instead of fetching the line once per XCD.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t xcd_block_id() {
-  const uint32_t nwg = gridDim.x, L = blockIdx.x;
+// The form with a count renumbers the first nwg workgroups of a grid whose
+// remaining workgroups do other work.
+__device__ __forceinline__ uint32_t xcd_block_id(uint32_t nwg) {
+  const uint32_t L = blockIdx.x;
   const uint32_t q = nwg >> 3, r = nwg & 7, x = L & 7;
   return x * q + min(x, r) + (L >> 3);
 }
+__device__ __forceinline__ uint32_t xcd_block_id() { return xcd_block_id(gridDim.x); }
 
 // Workgroups of `threads` threads of one kernel that a CU holds at once (from
 // the runtime, cached per kernel address: kernels of one signature share the
