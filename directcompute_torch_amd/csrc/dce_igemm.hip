@@ -1325,16 +1325,13 @@ __global__ void __launch_bounds__(256)
 // split's partials start 4 * ceil(OC*KK*Cp / 4) floats apart.  Padding
 // channels (c >= C) and the tail past OC*KK*Cp are dropped.
 //
-// The same launch carries the conv backward's other small passes as extra
-// blocks after the nMain finishing blocks, so that they cost no launch of
-// their own: side.nRow blocks sum the bias-gradient partials (rowsum_block)
-// and the rest re-lay the filters for the dX GEMM (permute_w_elem, mode 1).
-// The jobs touch disjoint buffers.
+// The same launch carries the conv backward's bias-gradient sum as side.nRow
+// extra blocks after the nMain finishing blocks (rowsum_block), so that it
+// costs no launch of its own; the two jobs touch disjoint buffers.
 struct BwdSide {
   const float* dbPart;  // bias-gradient partials [OC][dbRows]
   float* db;
   uint32_t dbRows, nRow;  // nRow = OC, or 0 for no bias gradient
-  WPerm perm;             // the dX filters (perm.w null: none)
 };
 
 template <int SL>
@@ -1343,11 +1340,7 @@ __global__ void __launch_bounds__(256)
                uint32_t KK, uint32_t Cp, uint32_t splits, uint32_t trans, uint32_t nMain,
                BwdSide side) {
   if (blockIdx.x >= nMain) {
-    const uint32_t j = blockIdx.x - nMain;
-    if (j < side.nRow)
-      rowsum_block(side.dbPart, side.db, side.dbRows, j);
-    else
-      permute_w_elem(side.perm, (j - side.nRow) * 256 + threadIdx.x);
+    rowsum_block(side.dbPart, side.db, side.dbRows, blockIdx.x - nMain);
     return;
   }
   constexpr uint32_t QB = 256 / SL;
@@ -1409,7 +1402,7 @@ static bool dw_final(const float* part, float* dw, uint32_t OC, uint32_t C, uint
   const f4* p4 = reinterpret_cast<const f4*>(part);
   const uint32_t tr = trans ? 1u : 0u;
   const uint32_t nMain = cdiv(nq, 256u / sl);
-  const dim3 grid(nMain + side.nRow + side.perm.blocks());
+  const dim3 grid(nMain + side.nRow);
   if (sl == 1)
     hipLaunchKernelGGL(k_dw_final<1>, grid, dim3(256), 0, stream(), p4, dw, OC, C, KK, Cp, splits,
                        tr, nMain, side);
@@ -2510,19 +2503,25 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
     mask_pad(dy, y, gp, dbPart, g, &ok);
     if (!ok) return false;
   }
-  uint32_t npbGot = npb;
-  if (useGnhwc &&
-      !to_nhwc_masked(dy, y, gn, useGpad ? nullptr : dbPart, g.B, g.OC, OHW, &npbGot))
-    return false;
-  // With dW, the bias-gradient sum and the dX filter re-layout ride in the
-  // dW finishing launch (BwdSide); otherwise they run on their own.
-  const uint32_t dbRowsGot = useGpad ? dbRows : g.B * npbGot;
+  // The dX filter re-layout rides in the G pass launch (dX always has the
+  // NHWC G), the bias-gradient sum in the dW finishing launch.
   const WPerm dxPerm{w, wt, g.OC, g.C, KK, OCp, KK * OCp, 1, dx && blocked_k(OCp) ? 1 : 0};
+  uint32_t npbGot = npb;
+  if (useGnhwc && !to_nhwc_masked(dy, y, gn, useGpad ? nullptr : dbPart, g.B, g.OC, OHW, &npbGot,
+                                  dx ? dxPerm : WPerm{}))
+    return false;
+  const uint32_t dbRowsGot = useGpad ? dbRows : g.B * npbGot;
   if (db && !dw) {
     hipLaunchKernelGGL(k_rowsum, dim3(g.OC), dim3(256), 0, stream(), dbPart, db, dbRowsGot);
     if (!check_launch("bias_grad")) return false;
   }
-  if (dw) {
+  auto dx_chain = [&]() {
+    ProfScope prof("conv_dx", 2.0 * g.OC * g.C * KK * double(npix),
+                   4.0 * (double(npix) * OCp + double(g.B) * g.C * g.H * g.W));
+    return conv_variant<DxRun>(g.s == 1, dxPerm.blocked != 0, dxc, wt, gn, dx, qpart, g,
+                               dxc.splits);
+  };
+  auto dw_gemm = [&]() {
     const float* xn = x_nhwc;
     if (!xn) {
       const bool built = ps ? to_ps(x, xs, g)
@@ -2530,39 +2529,25 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
       if (!built) return false;
       xn = xs;
     }
-    bool ok;
-    {
-      const double fl = 2.0 * g.OC * g.C * KK * double(npix);
-      ProfScope prof("conv_dw", fl,
-                     4.0 * (double(npix) * OCp + double(g.B) * g.H * g.W * Cp + double(g.OC) * KK * Cp));
-      ok = tiles_dispatch(dwc, DwRun{ps ? gp : gn, xn, part, g, dwc.splits, dwT, pk, ps});
-      if (ok) {
-        BwdSide side{};
-        if (db) {
-          side.dbPart = dbPart;
-          side.db = db;
-          side.dbRows = dbRowsGot;
-          side.nRow = g.OC;
-        }
-        if (dx) side.perm = dxPerm;
-        // The stride-phase taps are already in the filters' (c, kh, kw)
-        // order: the finish is a plain split sum (one channel of C*KK taps).
-        ok = ps ? dw_final(part, dw, g.OC, 1, KK * g.C, 1, dwc.splits, dwT, side)
-                : dw_final(part, dw, g.OC, g.C, KK, Cx, dwc.splits, dwT, side);
-      }
+    ProfScope prof("conv_dw", 2.0 * g.OC * g.C * KK * double(npix),
+                   4.0 * (double(npix) * OCp + double(g.B) * g.H * g.W * Cp + double(g.OC) * KK * Cp));
+    return tiles_dispatch(dwc, DwRun{ps ? gp : gn, xn, part, g, dwc.splits, dwT, pk, ps});
+  };
+  auto dw_finish = [&]() {
+    BwdSide side{};
+    if (db) {
+      side.dbPart = dbPart;
+      side.db = db;
+      side.dbRows = dbRowsGot;
+      side.nRow = g.OC;
     }
-    if (!ok) return false;
-  }
-  if (dx) {
-    const bool blk = dxPerm.blocked != 0;
-    if (!dw && !permute_w(dxPerm)) return false;
-    const double fl = 2.0 * g.OC * g.C * KK * double(npix);
-    {
-      ProfScope prof("conv_dx", fl, 4.0 * (double(npix) * OCp + double(g.B) * g.C * g.H * g.W));
-      if (!conv_variant<DxRun>(g.s == 1, blk, dxc, wt, gn, dx, qpart, g, dxc.splits))
-        return false;
-    }
-  }
+    // The stride-phase taps are already in the filters' (c, kh, kw) order:
+    // the finish is a plain split sum (one channel of C*KK taps).
+    return ps ? dw_final(part, dw, g.OC, 1, KK * g.C, 1, dwc.splits, dwT, side)
+              : dw_final(part, dw, g.OC, g.C, KK, Cx, dwc.splits, dwT, side);
+  };
+  if (dw && !(dw_gemm() && dw_finish())) return false;
+  if (dx && !dx_chain()) return false;
   return true;
 }
 
