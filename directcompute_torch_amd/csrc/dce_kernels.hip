@@ -567,13 +567,16 @@ struct BnPieces {
   uint32_t pieces;
   uint32_t len;  // elements per channel = N*S
 };
-// Pieces per channel: about four rounds of resident blocks (8 per CU) over
+// Pieces per channel: about eight rounds of resident blocks (8 per CU) over
 // all channels, so that the last, partly filled round is a small share of
-// the pass; each piece at least 2048 elements long, at most 512 pieces.
+// the pass; each piece at least 2048 elements long, at most 512 pieces.  At
+// 64x96x112x112 (MI355X): backward reduce 92.9 / 88.7 / 87.3 us and
+// statistics 55.2 / 54.3 / 69.3 us at 4 / 8 / 16 rounds (beyond 8 the
+// statistics' pieces fall under one 1024-quad batch per block).
 static BnPieces bn_pieces(uint32_t N, uint32_t C, uint32_t S) {
   BnPieces p;
   p.len = N * S;
-  const uint32_t want = cdiv(uint32_t(num_cus()) * 32, std::max<uint32_t>(1, C));
+  const uint32_t want = cdiv(uint32_t(num_cus()) * 64, std::max<uint32_t>(1, C));
   p.pieces = std::max<uint32_t>(1, std::min<uint32_t>({want, cdiv(p.len, 2048), 512u}));
   return p;
 }
@@ -617,13 +620,14 @@ __global__ void k_bn_partial(Buf x, Buf dy, Buf mean, Buf var, float eps, uint32
 }
 
 // Same sums over quads when S % 4 == 0 (every quad lies in one plane): the
-// piece is a range of quad indices k (plane n = k / (S/4)), read kBnUnroll
-// quads at a time so that each thread keeps several loads in flight.  The
+// piece is a range of quad indices k (plane n = k / (S/4)), read U =
+// kBnUnroll quads at a time so that each thread keeps several loads in
+// flight (8 measured no faster for the statistics).  The
 // grid is (channel, piece) with channels fastest, so the blocks that run
 // together read neighbouring planes of the same images (64x96x112x112
 // backward reduce 104.6 -> 96.6 us against pieces fastest).
 constexpr int kBnUnroll = 4;
-template <int MODE, bool NT>
+template <int MODE, bool NT, int U>
 __global__ void __launch_bounds__(256)
     k_bn_partial4(const float* __restrict__ x, const float* __restrict__ dy,
                   const float* __restrict__ mean, const float* __restrict__ var, float eps,
@@ -639,11 +643,12 @@ __global__ void __launch_bounds__(256)
     rstd = 1.0f / sqrtf(var[c] + eps);
   }
   double a0 = 0.0, a1 = 0.0;
-  for (uint32_t kb = k0 + threadIdx.x; kb < k1; kb += 256 * kBnUnroll) {
-    f4 xv[kBnUnroll], gv[kBnUnroll];
-    bool ok[kBnUnroll];
+  // Batches of U quads per thread; the next batch's loads are issued
+  // before the current batch is added, so the adds overlap the memory
+  // traffic.  Lanes past the piece load quad k0 (in range) and skip it.
+  auto load = [&](uint32_t kb, f4 (&xv)[U], f4 (&gv)[U], bool (&ok)[U]) {
 #pragma unroll
-    for (int u = 0; u < kBnUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       const uint32_t k = kb + u * 256;
       ok[u] = k < k1;
       const uint32_t kk = ok[u] ? k : k0;
@@ -652,8 +657,10 @@ __global__ void __launch_bounds__(256)
       xv[u] = ld4s<NT>(x + q * 4);
       if (MODE == 1) gv[u] = ld4s<NT>(dy + q * 4);
     }
+  };
+  auto add = [&](const f4 (&xv)[U], const f4 (&gv)[U], const bool (&ok)[U]) {
 #pragma unroll
-    for (int u = 0; u < kBnUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       if (!ok[u]) continue;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -667,6 +674,26 @@ __global__ void __launch_bounds__(256)
         }
       }
     }
+  };
+  f4 xv[U], gv[U];
+  bool ok[U];
+  uint32_t kb = k0 + threadIdx.x;
+  if (kb < k1) load(kb, xv, gv, ok);
+  while (kb < k1) {
+    const uint32_t kn = kb + 256 * U;
+    f4 xn[U], gn[U];
+    bool okn[U];
+    const bool more = kn < k1;
+    if (more) load(kn, xn, gn, okn);
+    add(xv, gv, ok);
+    if (!more) break;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      xv[u] = xn[u];
+      gv[u] = gn[u];
+      ok[u] = okn[u];
+    }
+    kb = kn;
   }
   const double s0 = block_sum256(a0, sh);
   const double s1 = block_sum256(a1, sh);
@@ -743,7 +770,8 @@ static bool bn_reduce(const char* what, int mode, const Dispatch& d, Buf x, Buf 
     const FastDiv dS4 = make_fastdiv(S4);
     const bool nt = stream_nt((mode == 0 ? 4.0 : 8.0) * double(total));
 #define DCE_BNP(M, NT)                                                                         \
-  hipLaunchKernelGGL((k_bn_partial4<M, NT>), dim3(C, pc.pieces), dim3(256), 0, stream(), x.p, \
+  hipLaunchKernelGGL((k_bn_partial4<M, NT, kBnUnroll>), dim3(C, pc.pieces), dim3(256), 0,       \
+                     stream(), x.p,                                                            \
                      M ? dy.p : nullptr, M ? mean.p : nullptr, M ? var.p : nullptr, eps, C, S4, \
                      len4, pc.pieces, dS4, part)
     if (mode == 0 && nt) DCE_BNP(0, true);
@@ -1169,6 +1197,38 @@ __global__ void k_maxpool_bwd_blk(const float* __restrict__ dz, const uint32_t* 
   }
 }
 
+// 2 x 2 windows with stride 2 on planes of twice the output size (W a
+// multiple of 4): a thread takes two neighbouring windows (ow = 2q, 2q + 1)
+// with one 8-byte load of their indices and one of their values, and writes
+// the 2 x 4 inputs they cover as two 16-byte stores.  Each input lies in
+// exactly one window; it receives 0 + that window's value when the window's
+// argmax is this input, else 0 (the sum of the block kernel, same bits).
+__global__ void __launch_bounds__(256)
+    k_maxpool_bwd_22q(const float* __restrict__ dz, const uint32_t* __restrict__ idx,
+                      float* __restrict__ dx, uint32_t items, uint32_t OW2, FastDiv dOW2) {
+  typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+  const uint32_t item = blockIdx.x * 256 + threadIdx.x;
+  if (item >= items) return;
+  const uint32_t t = fdiv(item, dOW2), q = item - t * OW2;  // t = plane * OH + oh
+  const uint32_t o = t * (2 * OW2) + 2 * q;
+  const u2 iv = *reinterpret_cast<const u2*>(idx + o);
+  const f2 dv = *reinterpret_cast<const f2*>(dz + o);
+  const uint32_t W = 4 * OW2;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    // Input row 2*oh + r of the plane: (plane * H + 2 * oh + r) * W = (2t + r) * W.
+    const uint32_t i0 = (2 * t + r) * W + 4 * q;
+    f4 out;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float acc = 0.f;
+      if ((c < 2 ? iv[0] : iv[1]) == i0 + c) acc += c < 2 ? dv[0] : dv[1];
+      out[c] = acc;
+    }
+    *reinterpret_cast<f4*>(dx + i0) = out;
+  }
+}
+
 // Fallback when the pooling geometry is unknown (indices this library did
 // not produce): one thread per (b, c) plane adds the plane's dZ values to
 // dX[idx] in output order, after dX was cleared.  Every input then sums its
@@ -1200,7 +1260,15 @@ bool maxpool_backward(const float* dz, const float* idx, float* dx, uint32_t B, 
       const uint32_t BH = cdiv(H, 2), BW = cdiv(W, 2), items = B * C * BH * BW;
       const dim3 grid(cdiv(items, 256));
       const FastDiv fBW = make_fastdiv(BW), fBH = make_fastdiv(BH);
-      if (k == 2)
+      const bool quad = k == 2 && H == 2 * OH && W == 2 * OW && OW % 2 == 0 &&
+                        (reinterpret_cast<uintptr_t>(dx) & 15) == 0 &&
+                        (reinterpret_cast<uintptr_t>(dz) & 7) == 0 &&
+                        (reinterpret_cast<uintptr_t>(ip) & 7) == 0;
+      if (quad) {
+        const uint32_t OW2 = OW / 2, n2 = B * C * OH * OW2;
+        hipLaunchKernelGGL(k_maxpool_bwd_22q, dim3(cdiv(n2, 256)), dim3(256), 0, stream(), dz, ip,
+                           dx, n2, OW2, make_fastdiv(OW2));
+      } else if (k == 2)
         hipLaunchKernelGGL((k_maxpool_bwd_blk<2, 2, false>), grid, dim3(256), 0, stream(), dz,
                            ip, dx, items, H, W, OH, OW, BH, BW, fBW, fBH);
       else if (OW >= 2)
@@ -1703,7 +1771,7 @@ struct DwS2 {
 // vector store when they lie in the row (unaligned for rows whose length is
 // not a multiple of CW: unaligned access is on).  Taps are summed in
 // (fh, fw) order for every output, as the generic kernel.
-template <int K, int S, int PODD, bool V4, int CW>
+template <int K, int S, int PODD, bool V4, int CW, bool NT>
 __global__ void __launch_bounds__(256)
     k_dw_bwd_input_band(const float* __restrict__ dy, const float* __restrict__ f,
                         float* __restrict__ dx, uint32_t C, uint32_t H, uint32_t W, uint32_t OH,
@@ -1795,7 +1863,13 @@ __global__ void __launch_bounds__(256)
           const uint32_t col = CW * q;
           float* row = dxp + size_t(ih) * W + col;
           if (col + CW - 1 < W) {
-            if constexpr (CW == 4)
+            if constexpr (CW == 4 && NT) {
+              // Rows of a multiple of 4 floats keep the quads 16-byte aligned.
+              if ((W & 3) == 0)
+                stnt4(row, f4{o[0], o[1], o[2], o[3]});
+              else
+                stu(row, f4{o[0], o[1], o[2], o[3]});
+            } else if constexpr (CW == 4)
               stu(row, f4{o[0], o[1], o[2], o[3]});
             else
               stu(row, f2{o[0], o[1]});
@@ -2156,12 +2230,19 @@ static bool sh_dw_bwd_input(const Dispatch& d) {
     // overlaps each block's next window load with its compute): 64x144x56x56
     // s1 40.6 -> 38.1 us, 64x96x112x112 s2 81.4 -> 77.0 us.  On a plain
     // 1.2 GB fill the same contrast is 6.85 against 4.4-5.0 TB/s.
+    // Passes over more than the MALL store dx with the nontemporal policy.
+    const bool nt = stream_nt(4.0 * (double(total) + ndy)) &&
+                    (reinterpret_cast<uintptr_t>(dx.p) & 15) == 0;
+#define DCE_DWI_NT(K, SS, PO, V, NT)                                                             \
+  hipLaunchKernelGGL((k_dw_bwd_input_band<K, SS, PO, V, kDwCW, NT>), dim3(nbands), dim3(256), 0, \
+                     stream(), dy.p, f.p, dx.p, g.C, g.H, g.W, g.OH, g.OW, g.p, bb.RB, nb,       \
+                     nbands, bb.R, bb.LW, BW, ndy, fLW, fNb, fBW);
 #define DCE_DWI_V(K, SS, PO, V)                                                                   \
   {                                                                                              \
-    const uint32_t blocks = nbands;                                                              \
-    hipLaunchKernelGGL((k_dw_bwd_input_band<K, SS, PO, V, kDwCW>), dim3(blocks), dim3(256), 0,          \
-                       stream(), dy.p, f.p, dx.p, g.C, g.H, g.W, g.OH, g.OW, g.p, bb.RB, nb,     \
-                       nbands, bb.R, bb.LW, BW, ndy, fLW, fNb, fBW);                             \
+    if (nt)                                                                                      \
+      DCE_DWI_NT(K, SS, PO, V, true)                                                             \
+    else                                                                                         \
+      DCE_DWI_NT(K, SS, PO, V, false)                                                            \
   }
 #define DCE_DWI(K, SS, PO)                                                                        \
   if (g.kH == K && g.s == SS && (SS == 1 || podd == PO)) {                                       \
@@ -2174,6 +2255,7 @@ static bool sh_dw_bwd_input(const Dispatch& d) {
     DCE_DWI(5, 1, 0) DCE_DWI(5, 2, 0) DCE_DWI(5, 2, 1)
 #undef DCE_DWI
 #undef DCE_DWI_V
+#undef DCE_DWI_NT
     return check_launch("depthwise_conv_backward_input");
   }
   hipLaunchKernelGGL(k_dw_bwd_input, dim3(cdiv(total, 256)), dim3(256), 0, stream(), dy, f, dx, g,

@@ -195,7 +195,9 @@ POOL_CASES = [(2, 3, 8, 8, 2, 2), (2, 4, 55, 55, 3, 2), (1, 2, 27, 27, 3, 2), (3
               (1, 2, 256, 200, 2, 2), (1, 2, 121, 301, 3, 2), (1, 1, 9, 8199, 3, 2),
               # 3x3 s2 around the paired-window path's limits: one window column
               # (scalar path), two columns, and an even width
-              (2, 3, 5, 4, 3, 2), (2, 3, 6, 5, 3, 2), (2, 3, 10, 56, 3, 2)]
+              (2, 3, 5, 4, 3, 2), (2, 3, 6, 5, 3, 2), (2, 3, 10, 56, 3, 2),
+              # 2x2 s2: the two-window quad path (even output width) and an odd one
+              (2, 16, 64, 64, 2, 2), (1, 2, 12, 10, 2, 2)]
 
 
 @pytest.mark.parametrize("B,C,H,W,k,s", POOL_CASES)
