@@ -81,14 +81,26 @@ struct Stage {
   static constexpr int DROW = KROW ? 0 : kThreads / KQ;
   static constexpr int DK = KROW ? kThreads / RQ : 0;
   static constexpr int DLDS = KROW ? DK * LD : DROW * LD;
+  // ROWK quad swizzle: logical k-quad q of row `row` sits at physical quad
+  // q ^ fr(row).  A fragment read takes quad q of 16 consecutive rows; rows
+  // are KT floats, so 64 / KT consecutive rows fill the 64 banks once and the
+  // unswizzled quads of rows 64 / KT apart share banks (4-way conflicts at
+  // KT = 16, 16-way at KT = 64).  fr spreads the 16 rows over all 64 banks.
+  // Thread t still owns the 16-byte slot t of its row group (the direct
+  // loads' lane order); it loads the logical quad that belongs there.
+  static_assert(KROW || (KT <= 64 && 64 % KT == 0), "ROWK swizzle period");
+  static_assert(KROW || Q == 1 || DROW % 16 == 0, "fr is periodic in 16 rows");
+  __device__ static __forceinline__ int fr(int row) { return (row / (64 / KT)) % KQ; }
   __device__ static __forceinline__ int qrow(int t, int i) {
     return KROW ? 4 * (t % RQ) : t / KQ + DROW * i;
   }
+  // Logical k offset of the data in thread t's quad i (DROW is a multiple of
+  // fr's 16-row period, so it is the same for every i).
   __device__ static __forceinline__ int qk(int t, int i) {
-    return KROW ? t / RQ + DK * i : 4 * (t % KQ);
+    return KROW ? t / RQ + DK * i : 4 * ((t % KQ) ^ fr(t / KQ));
   }
   __device__ static __forceinline__ int lds_off(int t) {
-    return KROW ? qk(t, 0) * LD + qrow(t, 0) : qrow(t, 0) * LD + qk(t, 0);
+    return KROW ? qk(t, 0) * LD + qrow(t, 0) : qrow(t, 0) * LD + 4 * (t % KQ);
   }
   // SWZ: logical row quad rq of k row k sits at physical quad rq ^ fk(k).
   __device__ static __forceinline__ int fk(int k) { return 4 * ((k >> 2) & 3); }
@@ -100,7 +112,7 @@ struct Stage {
   }
   // MFMA operand of 16 rows starting at rb, k slice kb: components s = 0..3.
   __device__ static __forceinline__ f4 frag(const float* S, int rb, int r, int g, int kb) {
-    if (!KROW) return *reinterpret_cast<const f4*>(S + (rb + r) * LD + kb + 4 * g);
+    if (!KROW) return *reinterpret_cast<const f4*>(S + (rb + r) * LD + 4 * ((kb / 4 + g) ^ fr(rb + r)));
     f4 v;
     const int row = rb + r;
 #pragma unroll
