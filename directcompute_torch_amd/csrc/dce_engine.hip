@@ -58,6 +58,7 @@ static std::vector<float*> g_wsRetired;
 static int g_liveGraphs = 0;
 static bool refuse_in_capture(const char* what);
 static float* g_misc = nullptr;  // 1024 floats of device scratch for scalars
+static float* g_ones = nullptr;  // 4 floats of 1.0
 
 // Pinned staging ring for host->device uploads.
 constexpr int kSlots = 4;
@@ -75,6 +76,7 @@ void set_error(const char* fmt, ...) {
 }
 
 hipStream_t stream() { return g_stream; }
+const float* ones4() { return g_ones; }
 int num_cus() { return g_cus; }
 
 bool ensure_init() {
@@ -480,7 +482,11 @@ bool InitEngine(void) {
   snprintf(g_info.description, sizeof(g_info.description), "%s (%s)",
            prop.name[0] ? prop.name : "AMD Instinct GPU", prop.gcnArchName);
   g_poolCapBytes = uint64_t(prop.totalGlobalMem) / 2;
-  if (hipMalloc((void**)&g_misc, 1024 * 4) != hipSuccess) {
+  const float ones[4] = {1.f, 1.f, 1.f, 1.f};
+  if (hipMalloc((void**)&g_misc, 1024 * 4) != hipSuccess ||
+      hipMalloc((void**)&g_ones, sizeof(ones)) != hipSuccess ||
+      hipMemcpy(g_ones, ones, sizeof(ones), hipMemcpyHostToDevice) != hipSuccess) {
+    hipGetLastError();
     set_error("InitEngine: scratch allocation failed");
     return false;
   }

@@ -244,6 +244,131 @@ struct LdDenseKR : LoaderBase<Stage<R, KT, true>> {
 };
 
 // ---------------------------------------------------------------------------
+// NCHW operands of the pointwise (1 x 1, stride 1, no padding) convolutions,
+// read in place: a pixel n = b*HW + pix of channel ch is src[(b*Ch + ch)*HW
+// + pix].  HW % 4 == 0, so four consecutive pixels (a quad) lie in one image.
+// ---------------------------------------------------------------------------
+// KROW: rows = pixels n, k = channel (zero for k >= Ch or n >= N).
+struct NchwKRParams {
+  const float* src;
+  uint32_t Ch, HW, N, n;
+  FastDiv dHW;
+};
+template <int R, int KT>
+struct LdNchwKR : LoaderBase<Stage<R, KT, true>> {
+  using St = Stage<R, KT, true>;
+  static constexpr bool KROW = true;
+  static constexpr bool kTransAcc = true;  // pixel columns: quad stores
+  using LoaderBase<St>::Q;
+  using Params = NchwKRParams;
+  BRes b;
+  uint32_t Ch, HW, kk0;
+  uint32_t base[Q];  // quad i's offset at channel 0, or kOob past the pixels
+  __device__ __forceinline__ void init(const Params& P, uint32_t row0, int tid) {
+    this->base_init(tid);
+    b.init(P.src, P.n);
+    Ch = P.Ch;
+    HW = P.HW;
+    kk0 = St::qk(tid, 0);
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+      const uint32_t n = row0 + St::qrow_data(tid, i);
+      const uint32_t bb = fdiv(n, P.dHW);
+      base[i] = (this->act && n < P.N) ? bb * P.Ch * P.HW + (n - bb * P.HW) : kOob;
+    }
+  }
+  __device__ __forceinline__ void offsets(uint32_t kt, uint32_t (&o)[Q]) const {
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+      const uint32_t ch = kt * KT + kk0 + St::DK * i;
+      o[i] = (base[i] != kOob && ch < Ch) ? base[i] + ch * HW : kOob;
+    }
+  }
+  __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
+    uint32_t o[Q];
+    offsets(kt, o);
+#pragma unroll
+    for (int i = 0; i < Q; ++i) r[i] = b.ld4(o[i]);
+  }
+  static constexpr bool LDSD = St::SWZ;
+  __device__ __forceinline__ void issue_lds(uint32_t kt, float* S) const {
+    uint32_t o[Q];
+    offsets(kt, o);
+#pragma unroll
+    for (int i = 0; i < Q; ++i) b.ld4_lds(o[i], S + this->wbase + i * St::DLDS);
+  }
+};
+
+// ROWK: rows = channels, k = pixel n over the batch (the pointwise dW
+// operands).  Row `onesRow` (when below R rows of the grid) reads 1 for
+// every k < K, from a 4-float buffer of ones: the dW GEMM then yields the
+// bias gradient, sum over k of the other operand, as its extra column.
+struct NchwRKParams {
+  const float* src;
+  const float* ones;
+  uint32_t Ch, HW, K, n, onesRow;
+  FastDiv dHW;
+};
+template <int R, int KT>
+struct LdNchwRK : LoaderBase<Stage<R, KT, false>> {
+  using St = Stage<R, KT, false>;
+  static constexpr bool KROW = false;
+  using LoaderBase<St>::Q;
+  using Params = NchwRKParams;
+  BRes b, bo;
+  uint32_t Ch, HW, K, kq;
+  FastDiv dHW;
+  uint32_t rowoff[Q];  // quad i's channel offset ch * HW, or kOob past the channels
+  bool one[Q];
+  __device__ __forceinline__ void init(const Params& P, uint32_t row0, int tid) {
+    this->base_init(tid);
+    b.init(P.src, P.n);
+    bo.init(P.ones, 4);
+    Ch = P.Ch;
+    HW = P.HW;
+    K = P.K;
+    dHW = P.dHW;
+    kq = St::qk(tid, 0);
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+      const uint32_t r = row0 + St::qrow(tid, i);
+      one[i] = this->act && r == P.onesRow;
+      rowoff[i] = (this->act && r < P.Ch) ? r * P.HW : kOob;
+    }
+  }
+  // The thread's quads share their k (ROWK): one image / pixel split per tile.
+  __device__ __forceinline__ void offsets(uint32_t kt, uint32_t (&o)[Q]) const {
+    const uint32_t k0 = kt * KT + kq;
+    const uint32_t bb = fdiv(k0, dHW);
+    const uint32_t img = bb * Ch * HW + (k0 - bb * HW);
+#pragma unroll
+    for (int i = 0; i < Q; ++i) o[i] = (rowoff[i] != kOob && k0 < K) ? img + rowoff[i] : kOob;
+  }
+  __device__ __forceinline__ void load(uint32_t kt, f4 (&r)[Q]) const {
+    uint32_t o[Q];
+    offsets(kt, o);
+    const bool kin = kt * KT + kq < K;
+#pragma unroll
+    for (int i = 0; i < Q; ++i) r[i] = one[i] ? bo.ld4(kin ? 0u : kOob) : b.ld4(o[i]);
+  }
+  static constexpr bool LDSD = true;
+  __device__ __forceinline__ void issue_lds(uint32_t kt, float* S) const {
+    if (St::PART && !this->act) return;  // whole waves (NQ is a multiple of 64)
+    uint32_t o[Q];
+    offsets(kt, o);
+    const bool kin = kt * KT + kq < K;
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+      float* dst = S + this->wbase + i * St::DLDS;
+      if (one[i])
+        bo.ld4_lds(kin ? 0u : kOob, dst);
+      else
+        b.ld4_lds(o[i], dst);
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
 // Pixel-row gather over an NHWC source (ROWK): rows = pixels of a grid
 // (b, a, c); k runs over the taps (kh, kw) and the Cp source channels (Cp the
 // padded channel count, Cp % 4 == 0) in one of two orders:
@@ -1346,11 +1471,13 @@ struct BwdSide {
   uint32_t dbRows, nRow;  // nRow = OC, or 0 for no bias gradient
 };
 
+// dbCol (not null, KK == 1, !trans): the tap axis' column C holds the bias
+// gradient (a GEMM operand row of ones), written to dbCol[oc].
 template <int SL>
 __global__ void __launch_bounds__(256)
     k_dw_final(const f4* __restrict__ part, float* __restrict__ dw, uint32_t OC, uint32_t C,
                uint32_t KK, uint32_t Cp, uint32_t splits, uint32_t trans, uint32_t nMain,
-               BwdSide side) {
+               BwdSide side, float* __restrict__ dbCol) {
   if (blockIdx.x >= nMain) {
     rowsum_block(side.dbPart, side.db, side.dbRows, blockIdx.x - nMain);
     return;
@@ -1396,7 +1523,10 @@ __global__ void __launch_bounds__(256)
       n = i - oc * N;
     }
     const uint32_t khw = n / Cp, c = n - khw * Cp;
-    if (c < C) dw[(size_t(oc) * C + c) * KK + khw] = s[j];
+    if (c < C)
+      dw[(size_t(oc) * C + c) * KK + khw] = s[j];
+    else if (dbCol && c == C)
+      dbCol[oc] = s[j];
   }
 }
 
@@ -1409,7 +1539,8 @@ static uint32_t dw_final_slices(uint32_t nq, uint32_t splits) {
 }
 
 static bool dw_final(const float* part, float* dw, uint32_t OC, uint32_t C, uint32_t KK,
-                     uint32_t Cp, uint32_t splits, bool trans, BwdSide side = BwdSide{}) {
+                     uint32_t Cp, uint32_t splits, bool trans, BwdSide side = BwdSide{},
+                     float* dbCol = nullptr) {
   const uint32_t nq = cdiv(size_t(OC) * KK * Cp, 4), sl = dw_final_slices(nq, splits);
   const f4* p4 = reinterpret_cast<const f4*>(part);
   const uint32_t tr = trans ? 1u : 0u;
@@ -1417,13 +1548,13 @@ static bool dw_final(const float* part, float* dw, uint32_t OC, uint32_t C, uint
   const dim3 grid(nMain + side.nRow);
   if (sl == 1)
     hipLaunchKernelGGL(k_dw_final<1>, grid, dim3(256), 0, stream(), p4, dw, OC, C, KK, Cp, splits,
-                       tr, nMain, side);
+                       tr, nMain, side, dbCol);
   else if (sl == 4)
     hipLaunchKernelGGL(k_dw_final<4>, grid, dim3(256), 0, stream(), p4, dw, OC, C, KK, Cp, splits,
-                       tr, nMain, side);
+                       tr, nMain, side, dbCol);
   else
     hipLaunchKernelGGL(k_dw_final<16>, grid, dim3(256), 0, stream(), p4, dw, OC, C, KK, Cp,
-                       splits, tr, nMain, side);
+                       splits, tr, nMain, side, dbCol);
   return check_launch("dw_final");
 }
 
@@ -2058,6 +2189,12 @@ __global__ void __launch_bounds__(256)
 // Layout of the conv input copy: channel-innermost (C >= 4), stride-phase
 // (C < 4, stride <= 4) or channel-packed (C < 4, larger strides).
 bool ps_x(const ConvGeom& g) { return g.C < 4 && g.s <= 4; }
+// Pointwise convolutions (1 x 1, stride 1, no padding, planes of a multiple
+// of 4 pixels, at least 4 channels) read x, dy and write y, dx in NCHW: the
+// GEMMs take the planes as they are, with no channel-innermost copy.
+bool pw_x(const ConvGeom& g) {
+  return g.k == 1 && g.s == 1 && g.p == 0 && (g.H * g.W) % 4 == 0 && g.C >= 4;
+}
 bool packed_x(const ConvGeom& g) { return g.C < 4 && g.s > 4; }
 
 struct PsGeom {
@@ -2079,12 +2216,21 @@ static PsGeom ps_geom(const ConvGeom& g) {
 }
 
 size_t xcopy_floats(const ConvGeom& g) {
+  if (pw_x(g)) return 4;  // no copy: a placeholder handle
   if (ps_x(g)) return ps_geom(g).floats;
   if (!packed_x(g)) return nhwc_floats(g.B, g.C, g.H, g.W);
   return size_t(g.B) * (g.H + 2 * g.p) * (g.W + 2 * g.p) * g.C;
 }
 
+// Floats of the copy of x the general conv path builds (a pointwise layer
+// that takes that path, for its ReLU mask, needs the NHWC copy its forward
+// did not keep).
+static size_t xbuild_floats(const ConvGeom& g) {
+  return pw_x(g) ? nhwc_floats(g.B, g.C, g.H, g.W) : xcopy_floats(g);
+}
+
 uint32_t xcopy_tag(const ConvGeom& g) {
+  if (pw_x(g)) return 0x40000u;
   if (ps_x(g)) return 0x20000u + g.p + (g.s << 8) + (g.k << 12);
   return packed_x(g) ? 0x10000u + g.p : pad4(g.C);
 }
@@ -2299,8 +2445,62 @@ static bool conv_forward_ps(const float* x, float* keep, const float* w, const f
   return tiles_dispatch16(cfg, FwdPsRun{ws, xs, bias, y, g, act});
 }
 
+// Pointwise forward: y[oc][n] = sum_c w[oc][c] x[c][n] over the pixels n =
+// b*HW + pix of NCHW x, filters padded to pad4(C) per row.
+struct FwdPwRun {
+  const float* wp;
+  const float* x;
+  const float* bias;
+  float* y;
+  float* part;
+  ConvGeom g;
+  uint32_t act, splits;
+  template <int MT, int NT, int KT>
+  int occ(bool split) const {
+    using LA = LdDenseRK<MT, KT>;
+    using LB = LdNchwKR<NT, KT>;
+    return split ? occupancy(k_igemm<MT, NT, KT, LA, LB, EpiRowMajor>)
+                 : occupancy(k_igemm<MT, NT, KT, LA, LB, EpiNCHW>);
+  }
+  template <int MT, int NT, int KT>
+  bool run() {
+    const uint32_t Cp = pad4(g.C), HW = g.H * g.W, N = g.B * HW;
+    using LA = LdDenseRK<MT, KT>;
+    using LB = LdNchwKR<NT, KT>;
+    const typename LA::Params pa{wp, Cp, g.OC, Cp, g.OC * Cp};
+    const NchwKRParams pb{x, g.C, HW, N, g.B * g.C * HW, make_fastdiv(HW)};
+    const uint32_t kt = cdiv(Cp, KT);
+    const EpiNCHW::Params pe{y, bias, g.OC, HW, N, act, make_fastdiv(HW)};
+    if (splits > 1) {
+      const EpiRowMajor::Params pr{part, g.OC, N, N, g.OC * N};
+      return launch<MT, NT, KT, LA, LB, EpiRowMajor>(pa, pb, pr, g.OC, N, kt, splits,
+                                                    "conv_forward") &&
+             split_nchw(part, bias, y, g.OC, N, HW, splits, act);
+    }
+    return launch<MT, NT, KT, LA, LB, EpiNCHW>(pa, pb, pe, g.OC, N, kt, 1, "conv_forward");
+  }
+};
+
+static bool conv_forward_pw(const float* x, const float* w, const float* bias, float* y,
+                            const ConvGeom& g, uint32_t act) {
+  const uint32_t Cp = pad4(g.C), N = g.B * g.H * g.W;
+  if (!operand_fits(size_t(g.B) * g.C * g.H * g.W, "conv_forward")) return false;
+  const TileCfg cfg = choose(
+      "DCE_TUNE_FWD", g.OC, N, Cp, 8, true,
+      [&](const TileCfg& t) { return tiles_occ16(t, FwdPwRun{}); }, true);
+  const size_t nw = al64(size_t(g.OC) * Cp);
+  const size_t nP = cfg.splits > 1 ? size_t(cfg.splits) * g.OC * N : 0;
+  float* ws = workspace(nw + nP);
+  if (!ws) return false;
+  if (!permute_w(WPerm{w, ws, g.OC, g.C, 1, Cp, Cp, 0, 0})) return false;
+  ProfScope prof("conv_fwd", 2.0 * g.OC * g.C * double(N),
+                 4.0 * (double(g.B) * g.C * g.H * g.W + double(g.B) * g.OC * g.OH * g.OW));
+  return tiles_dispatch16(cfg, FwdPwRun{ws, x, bias, y, ws + nw, g, act, cfg.splits});
+}
+
 bool conv_forward(const float* x, float* x_nhwc_keep, const float* w, const float* bias,
                   float* y, const ConvGeom& g, uint32_t act) {
+  if (pw_x(g)) return conv_forward_pw(x, w, bias, y, g, act);
   if (ps_x(g)) return conv_forward_ps(x, x_nhwc_keep, w, bias, y, g, act);
   const bool pk = packed_x(g);
   const uint32_t Cp = pad4(g.C), KK = g.k * g.k, kdim = pk ? pad4(KK * g.C) : KK * Cp;
@@ -2450,12 +2650,123 @@ struct DxRun {
   }
 };
 
+// Pointwise dX: dx[c][n] = sum_oc w[oc][c] dy[oc][n] (NCHW dy and dx; the
+// filters re-laid [c][pad4(OC)]).
+struct DxPwRun {
+  const float* wt;
+  const float* dy;
+  float* dx;
+  float* part;
+  ConvGeom g;
+  uint32_t splits;
+  template <int MT, int NT, int KT>
+  int occ(bool split) const {
+    using LA = LdDenseRK<MT, KT>;
+    using LB = LdNchwKR<NT, KT>;
+    return split ? occupancy(k_igemm<MT, NT, KT, LA, LB, EpiRowMajor>)
+                 : occupancy(k_igemm<MT, NT, KT, LA, LB, EpiNCHW>);
+  }
+  template <int MT, int NT, int KT>
+  bool run() {
+    const uint32_t OCp = pad4(g.OC), HW = g.H * g.W, N = g.B * HW;
+    using LA = LdDenseRK<MT, KT>;
+    using LB = LdNchwKR<NT, KT>;
+    const typename LA::Params pa{wt, OCp, g.C, OCp, g.C * OCp};
+    const NchwKRParams pb{dy, g.OC, HW, N, g.B * g.OC * HW, make_fastdiv(HW)};
+    const uint32_t kt = cdiv(OCp, KT);
+    const EpiNCHW::Params pe{dx, nullptr, g.C, HW, N, 0, make_fastdiv(HW)};
+    if (splits > 1) {
+      const EpiRowMajor::Params pr{part, g.C, N, N, g.C * N};
+      return launch<MT, NT, KT, LA, LB, EpiRowMajor>(pa, pb, pr, g.C, N, kt, splits,
+                                                    "conv_backward_input") &&
+             split_nchw(part, nullptr, dx, g.C, N, HW, splits, 0);
+    }
+    return launch<MT, NT, KT, LA, LB, EpiNCHW>(pa, pb, pe, g.C, N, kt, 1, "conv_backward_input");
+  }
+};
+
+// Pointwise dW: dw[oc][c] = sum_n dy[oc][n] x[c][n]; with db, x gets a row of
+// ones (column C of the product is the bias gradient, written by the finish).
+struct DwPwRun {
+  const float* dy;
+  const float* x;
+  float* part;
+  ConvGeom g;
+  uint32_t N, splits;  // N = C, or C + 1 with the ones row
+  template <int MT, int NT, int KT>
+  int occ(bool) const {
+    return occupancy(k_igemm<MT, NT, KT, LdNchwRK<MT, KT>, LdNchwRK<NT, KT>, EpiRowMajor>);
+  }
+  template <int MT, int NT, int KT>
+  bool run() {
+    const uint32_t HW = g.H * g.W, K = g.B * HW;
+    const NchwRKParams pa{dy, ones4(), g.OC, HW, K, g.B * g.OC * HW, 0xFFFFFFFFu, make_fastdiv(HW)};
+    const NchwRKParams pb{x, ones4(), g.C, HW, K, g.B * g.C * HW, N > g.C ? g.C : 0xFFFFFFFFu,
+                          make_fastdiv(HW)};
+    const EpiRowMajor::Params pe{part, g.OC, N, N, 4 * cdiv(size_t(g.OC) * N, 4)};
+    return launch<MT, NT, KT, LdNchwRK<MT, KT>, LdNchwRK<NT, KT>, EpiRowMajor>(
+        pa, pb, pe, g.OC, N, cdiv(K, KT), splits, "conv_backward_filter");
+  }
+};
+
+static bool conv_backward_pw(const float* dy, const float* x, const float* w, float* dw,
+                             float* db, float* dx, const ConvGeom& g) {
+  const uint32_t OCp = pad4(g.OC), HW = g.H * g.W, N = g.B * HW;
+  const double fl = 2.0 * g.OC * g.C * double(N);
+  ProfScope profAll("conv_bwd", fl * ((dw ? 1 : 0) + (dx ? 1 : 0)), 0.0);
+  const uint32_t Ndw = g.C + (db ? 1u : 0u);
+  TileCfg dwc{128, 128, 16, 1}, dxc{128, 128, 16, 1};
+  size_t nP = 0, nW = 0, nQ = 0;
+  if (dw) {
+    const uint32_t ntiles = cdiv(g.OC, pick_tile_m(g.OC)) * cdiv(Ndw, pick_tile(Ndw));
+    dwc = choose(
+        "DCE_TUNE_DW", g.OC, Ndw, N, ntiles <= 4 ? 1024 : 256, false,
+        [&](const TileCfg& t) { return tiles_occ(t, DwPwRun{}); }, false, true);
+    nP = al64(size_t(dwc.splits) * 4 * cdiv(size_t(g.OC) * Ndw, 4));
+  }
+  if (dx) {
+    dxc = choose(
+        "DCE_TUNE_DX", g.C, N, OCp, 8, true,
+        [&](const TileCfg& t) { return tiles_occ16(t, DxPwRun{}); }, true);
+    nW = al64(size_t(g.C) * OCp);
+    nQ = dxc.splits > 1 ? size_t(dxc.splits) * g.C * N : 0;
+  }
+  float* ws = workspace(nP + nW + nQ);
+  if (!ws) return false;
+  float* part = ws;
+  float* wt = ws + nP;
+  float* qpart = wt + nW;
+  if (dw) {
+    ProfScope prof("conv_dw", fl, 4.0 * (double(N) * g.OC + double(N) * g.C));
+    if (!tiles_dispatch(dwc, DwPwRun{dy, x, part, g, Ndw, dwc.splits}) ||
+        !dw_final(part, dw, g.OC, g.C, 1, Ndw, dwc.splits, false, BwdSide{}, db))
+      return false;
+  }
+  if (dx) {
+    if (!permute_w(WPerm{w, wt, g.OC, g.C, 1, OCp, OCp, 1, 0})) return false;
+    ProfScope prof("conv_dx", fl, 4.0 * (double(N) * g.OC + double(N) * g.C));
+    if (!tiles_dispatch16(dxc, DxPwRun{wt, dy, dx, qpart, g, dxc.splits})) return false;
+  }
+  return true;
+}
+
 bool conv_backward(const float* dy, const float* y, const float* x, const float* x_nhwc,
                    const float* w, float* dw, float* db, float* dx, const ConvGeom& g) {
+  // Pointwise layers with no ReLU mask (and dW requested whenever db is: the
+  // bias gradient is the dW product's ones column) read NCHW in place.
+  if (pw_x(g)) {
+    if (!y && (dw || !db)) {
+      if (!operand_fits(size_t(g.B) * g.C * g.H * g.W, "conv_backward") ||
+          !operand_fits(size_t(g.B) * g.OC * g.H * g.W, "conv_backward"))
+        return false;
+      return conv_backward_pw(dy, x, w, dw, db, dx, g);
+    }
+    x_nhwc = nullptr;  // the forward kept no copy: the general path builds its own
+  }
   const uint32_t Cp = pad4(g.C), OCp = pad4(g.OC), KK = g.k * g.k;
   const uint32_t OHW = g.OH * g.OW, npix = g.B * OHW, HW = g.H * g.W;
   if (!operand_fits(size_t(npix) * OCp, "conv_backward") ||
-      !operand_fits(xcopy_floats(g), "conv_backward") ||
+      !operand_fits(xbuild_floats(g), "conv_backward") ||
       !operand_fits(size_t(g.C) * KK * OCp, "conv_backward"))
     return false;
   // Workspace carve-up: G (NHWC) and / or G_pad, db partials, the copy of x
@@ -2482,7 +2793,7 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
   const size_t nG = useGnhwc ? al64(size_t(npix) * OCp) : 0;
   const size_t nGp = useGpad ? al64(size_t(g.B) * g.OC * q.OHWp) : 0;
   const size_t nDb = db ? al64(size_t(dbRows) * g.OC) : 0;
-  const size_t nX = (dw && !x_nhwc) ? al64(xcopy_floats(g)) : 0;
+  const size_t nX = (dw && !x_nhwc) ? al64(xbuild_floats(g)) : 0;
   if (ps && !operand_fits(nGp, "conv_backward")) return false;
   TileCfg dwc{128, 128, 16, 1}, dxc{128, 128, 16, 1};
   size_t nP = 0, nW = 0, nQ = 0;

@@ -49,6 +49,9 @@ bool check_launch(const char* what);
 // the single in-order stream.  Grows on demand (the old block is freed only
 // after the stream drains).  Returns nullptr (error set) on failure.
 float* workspace(size_t floats);
+// Four floats of 1.0 in device memory (set at InitEngine), for loaders that
+// feed a row of ones to a GEMM.
+const float* ones4();
 
 // Handle validation: returns the Buffer or nullptr (error set) for NULL,
 // released or foreign handles.

@@ -65,6 +65,12 @@ CONV_CASES = [
     # C < 4 and stride > 4: the channel-packed copy
     (2, 3, 23, 23, 8, 7, 5, 2, 1),
     (1, 1, 20, 22, 4, 6, 6, 0, 1),
+    # pointwise (1x1, planes of a multiple of 4 pixels, C >= 4): NCHW GEMMs in place
+    (2, 96, 14, 14, 24, 1, 1, 0, 0),      # MobileNetV2 project
+    (4, 5, 8, 8, 7, 1, 1, 0, 0),          # ragged channel counts (padded K)
+    (2, 144, 28, 28, 32, 1, 1, 0, 2),     # tanh: no derivative, so no mask
+    (8, 16, 56, 56, 96, 1, 1, 0, 0),      # expand at a MobileNet plane size (split-K dW)
+    (2, 40, 6, 6, 130, 1, 1, 0, 0),       # db column at a tile edge (N = 41), OC past 128
 ]
 
 
@@ -129,6 +135,16 @@ def test_conv_backward_rebuilds_x_copy(eng, case):
 @pytest.mark.parametrize("want", [(0, 1, 1), (1, 0, 0), (0, 0, 1), (1, 1, 0)])
 def test_conv_backward_subsets(eng, want):
     _conv_case(eng, 2, 16, 10, 10, 32, 3, 1, 1, 1, want=want, seed=11)
+
+
+@pytest.mark.parametrize("want", [(0, 1, 1), (1, 0, 0), (0, 0, 1), (1, 1, 0), (0, 1, 0)])
+@pytest.mark.parametrize("act", [0, 1])
+def test_pointwise_conv_backward_subsets(eng, want, act):
+    """Pointwise layers: every gradient subset, without (NCHW GEMMs in place;
+    db alone goes through the general path) and with the ReLU mask (the
+    general path, building the NHWC copy the forward did not keep)."""
+    _conv_case(eng, 2, 32, 12, 12, 48, 1, 1, 0, act, want=want, seed=13)
+    _conv_case(eng, 2, 32, 12, 12, 48, 1, 1, 0, act, want=want, seed=14, keep=False)
 
 
 def test_conv_backward_relu_mask_nan_keeps_grad(eng):
