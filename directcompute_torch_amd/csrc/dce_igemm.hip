@@ -2488,14 +2488,17 @@ static bool conv_forward_pw(const float* x, const float* w, const float* bias, f
   const TileCfg cfg = choose(
       "DCE_TUNE_FWD", g.OC, N, Cp, 8, true,
       [&](const TileCfg& t) { return tiles_occ16(t, FwdPwRun{}); }, true);
-  const size_t nw = al64(size_t(g.OC) * Cp);
+  // Filters [OC][C] are already the A operand when C % 4 == 0 (16-byte rows).
+  const bool wDirect = g.C % 4 == 0 && aligned16(w);
+  const size_t nw = wDirect ? 0 : al64(size_t(g.OC) * Cp);
   const size_t nP = cfg.splits > 1 ? size_t(cfg.splits) * g.OC * N : 0;
-  float* ws = workspace(nw + nP);
-  if (!ws) return false;
-  if (!permute_w(WPerm{w, ws, g.OC, g.C, 1, Cp, Cp, 0, 0})) return false;
+  float* ws = (nw + nP) ? workspace(nw + nP) : nullptr;
+  if ((nw + nP) && !ws) return false;
+  if (!wDirect && !permute_w(WPerm{w, ws, g.OC, g.C, 1, Cp, Cp, 0, 0})) return false;
   ProfScope prof("conv_fwd", 2.0 * g.OC * g.C * double(N),
                  4.0 * (double(g.B) * g.C * g.H * g.W + double(g.B) * g.OC * g.OH * g.OW));
-  return tiles_dispatch16(cfg, FwdPwRun{ws, x, bias, y, ws + nw, g, act, cfg.splits});
+  return tiles_dispatch16(
+      cfg, FwdPwRun{wDirect ? w : ws, x, bias, y, ws ? ws + nw : nullptr, g, act, cfg.splits});
 }
 
 bool conv_forward(const float* x, float* x_nhwc_keep, const float* w, const float* bias,
@@ -2652,6 +2655,9 @@ struct DxRun {
 
 // Pointwise dX: dx[c][n] = sum_oc w[oc][c] dy[oc][n] (NCHW dy and dx; the
 // filters re-laid [c][pad4(OC)]).
+// WK: the A operand is the filters themselves, [OC][C] read as [k = oc][row
+// = c] (C % 4 == 0); otherwise their re-layout [C][pad4(OC)].
+template <bool WK>
 struct DxPwRun {
   const float* wt;
   const float* dy;
@@ -2659,9 +2665,11 @@ struct DxPwRun {
   float* part;
   ConvGeom g;
   uint32_t splits;
+  template <int MT, int KT>
+  using LAt = typename std::conditional<WK, LdDenseKR<MT, KT>, LdDenseRK<MT, KT>>::type;
   template <int MT, int NT, int KT>
   int occ(bool split) const {
-    using LA = LdDenseRK<MT, KT>;
+    using LA = LAt<MT, KT>;
     using LB = LdNchwKR<NT, KT>;
     return split ? occupancy(k_igemm<MT, NT, KT, LA, LB, EpiRowMajor>)
                  : occupancy(k_igemm<MT, NT, KT, LA, LB, EpiNCHW>);
@@ -2669,9 +2677,10 @@ struct DxPwRun {
   template <int MT, int NT, int KT>
   bool run() {
     const uint32_t OCp = pad4(g.OC), HW = g.H * g.W, N = g.B * HW;
-    using LA = LdDenseRK<MT, KT>;
+    using LA = LAt<MT, KT>;
     using LB = LdNchwKR<NT, KT>;
-    const typename LA::Params pa{wt, OCp, g.C, OCp, g.C * OCp};
+    const typename LA::Params pa = WK ? typename LA::Params{wt, g.C, g.C, g.OC, g.OC * g.C}
+                                      : typename LA::Params{wt, OCp, g.C, OCp, g.C * OCp};
     const NchwKRParams pb{dy, g.OC, HW, N, g.B * g.OC * HW, make_fastdiv(HW)};
     const uint32_t kt = cdiv(OCp, KT);
     const EpiNCHW::Params pe{dx, nullptr, g.C, HW, N, 0, make_fastdiv(HW)};
@@ -2724,18 +2733,22 @@ static bool conv_backward_pw(const float* dy, const float* x, const float* w, fl
         [&](const TileCfg& t) { return tiles_occ(t, DwPwRun{}); }, false, true);
     nP = al64(size_t(dwc.splits) * 4 * cdiv(size_t(g.OC) * Ndw, 4));
   }
+  const bool wk = g.C % 4 == 0 && aligned16(w);  // dX reads the filters in place
   if (dx) {
     dxc = choose(
         "DCE_TUNE_DX", g.C, N, OCp, 8, true,
-        [&](const TileCfg& t) { return tiles_occ16(t, DxPwRun{}); }, true);
-    nW = al64(size_t(g.C) * OCp);
+        [&](const TileCfg& t) {
+          return wk ? tiles_occ16(t, DxPwRun<true>{}) : tiles_occ16(t, DxPwRun<false>{});
+        },
+        true);
+    nW = wk ? 0 : al64(size_t(g.C) * OCp);
     nQ = dxc.splits > 1 ? size_t(dxc.splits) * g.C * N : 0;
   }
-  float* ws = workspace(nP + nW + nQ);
-  if (!ws) return false;
+  float* ws = (nP + nW + nQ) ? workspace(nP + nW + nQ) : nullptr;
+  if ((nP + nW + nQ) && !ws) return false;
   float* part = ws;
-  float* wt = ws + nP;
-  float* qpart = wt + nW;
+  float* wt = ws ? ws + nP : nullptr;
+  float* qpart = wt ? wt + nW : nullptr;
   if (dw) {
     ProfScope prof("conv_dw", fl, 4.0 * (double(N) * g.OC + double(N) * g.C));
     if (!tiles_dispatch(dwc, DwPwRun{dy, x, part, g, Ndw, dwc.splits}) ||
@@ -2743,9 +2756,11 @@ static bool conv_backward_pw(const float* dy, const float* x, const float* w, fl
       return false;
   }
   if (dx) {
-    if (!permute_w(WPerm{w, wt, g.OC, g.C, 1, OCp, OCp, 1, 0})) return false;
+    if (!wk && !permute_w(WPerm{w, wt, g.OC, g.C, 1, OCp, OCp, 1, 0})) return false;
     ProfScope prof("conv_dx", fl, 4.0 * (double(N) * g.OC + double(N) * g.C));
-    if (!tiles_dispatch16(dxc, DxPwRun{wt, dy, dx, qpart, g, dxc.splits})) return false;
+    const bool ok = wk ? tiles_dispatch16(dxc, DxPwRun<true>{w, dy, dx, qpart, g, dxc.splits})
+                       : tiles_dispatch16(dxc, DxPwRun<false>{wt, dy, dx, qpart, g, dxc.splits});
+    if (!ok) return false;
   }
   return true;
 }
