@@ -1491,6 +1491,14 @@ __global__ void __launch_bounds__(256)
   if (q < nq) {
     const size_t zs = nq;
     uint32_t z = w;
+    // Eight loads in flight, added in z order.
+    for (; z + 7 * SL < splits; z += 8 * SL) {
+      f4 t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) t[u] = part[(z + u * SL) * zs + q];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) s += t[u];
+    }
     for (; z + 3 * SL < splits; z += 4 * SL) {
       const f4 a = part[z * zs + q], b = part[(z + SL) * zs + q];
       const f4 c = part[(z + 2 * SL) * zs + q], d = part[(z + 3 * SL) * zs + q];
@@ -1609,7 +1617,17 @@ __global__ void __launch_bounds__(256)
       v = fmaxf(v, 0.f);
     else if (act == 2)
       v = tanhf(v);
-    out[(size_t(b) * M + m) * HW + pix] = v;
+    s[j] = v;
+  }
+  if (pix + 3 < HW) {
+    // The quad lies in one plane: one 16-byte store (4-byte aligned for planes
+    // of odd size; unaligned access is on).
+    stu(out + (size_t(b) * M + m) * HW + pix, s);
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    out[(size_t(b) * M + m) * HW + pix] = s[j];
     if (++pix == HW) {
       pix = 0;
       ++b;
