@@ -446,7 +446,7 @@ def _prof_all(lib):
     return out
 
 
-def configs_suite(steps=10, warmup=3, ids=None, cpu=True):
+def configs_suite(steps=10, warmup=3, ids=None, cpu=True, graphs=True):
     """The other measured configurations of the backward path, each a full
     training step through the nn_engine API (synthetic inputs, seeds
     1000*config + {0: x, 1: weights, 2: labels}):
@@ -557,11 +557,12 @@ def configs_suite(steps=10, warmup=3, ids=None, cpu=True):
             h = nn.bias_relu(nn.matmul(h, P[4]), P[5])
             h = nn.bias_relu(nn.matmul(h, P[6]), P[7])
             return nn.add_bias(nn.matmul(h, P[8]), P[9])
-        graph = nn.ComputeGraph()
-        graph.trace(lenet_fwd, opt, x.sync(), y.sync(), P, clip=1.0)
-        run_config(1, "LeNet-5 b64 train step (SGD lr 0.01, clip 1.0), replayed with ComputeGraph",
-                   64, graph.replay, mode="graph")
-        graph.release()
+        if graphs:
+            graph = nn.ComputeGraph()
+            graph.trace(lenet_fwd, opt, x.sync(), y.sync(), P, clip=1.0)
+            run_config(1, "LeNet-5 b64 train step (SGD lr 0.01, clip 1.0), replayed with ComputeGraph",
+                       64, graph.replay, mode="graph")
+            graph.release()
 
     # 2 single conv backward
     def config2():
@@ -674,10 +675,12 @@ def configs_suite(steps=10, warmup=3, ids=None, cpu=True):
             nn.end_batch()
         name4 = "UNet-base16 b8 @256^2 (4 levels, conv3x3-BN-ReLU x2, Dice on sigmoid; norm clip 1.0 + Adam lr 1e-3)"
         run_config(4, name4, 8, unet_step)
-        graph = nn.ComputeGraph()
-        graph.trace(unet_fwd, opt4, x4.sync(), t4.sync(), Pu, clip=1e30, loss_fn=nn.dice_loss, max_norm=1.0)
-        run_config(4, name4 + ", replayed with ComputeGraph", 8, graph.replay, mode="graph")
-        graph.release()
+        if graphs:
+            graph = nn.ComputeGraph()
+            graph.trace(unet_fwd, opt4, x4.sync(), t4.sync(), Pu, clip=1e30, loss_fn=nn.dice_loss,
+                        max_norm=1.0)
+            run_config(4, name4 + ", replayed with ComputeGraph", 8, graph.replay, mode="graph")
+            graph.release()
 
     for cid, fn in ((1, config1), (2, config2), (3, config3), (4, config4)):
         if not ids or cid in ids:
@@ -712,6 +715,9 @@ def main():
                          "configs: LeNet, single conv, MobileNetV2 stack, UNet steps, one line each")
     ap.add_argument("--configs", default="",
                     help="with --suite configs: comma-separated configuration numbers (default all)")
+    ap.add_argument("--eager-only", action="store_true",
+                    help="with --suite configs: skip the ComputeGraph replays (rocprofv3's kernel "
+                         "tracing of graph capture crashed the process on this image)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of 256 MiB three times (the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -728,7 +734,7 @@ def main():
     if args.suite == "configs":
         ids = {int(v) for v in args.configs.split(",")} if args.configs else None
         configs_suite(steps=min(args.steps, 10), warmup=args.warmup, ids=ids,
-                      cpu=not args.no_cpu_baseline)
+                      cpu=not args.no_cpu_baseline, graphs=not args.eager_only)
         return
 
     from directcompute_torch_amd import nn_engine as nn
