@@ -863,10 +863,11 @@ def main():
         "roofline": {
             "bound": "mfma",
             "kernel": "conv backward of all layers, each ConvBackwardFused call whole: G pass "
-                      "k_to_nhwc (ReLU mask + NHWC transpose + bias partials; k_mask_pad for c1), "
-                      "k_rowsum, k_permute_w, dW k_igemm<LdGradKR,LdXTapKR> (c1, C = 3: "
-                      "k_igemm<LdGPadRK,LdPsRK> on the stride-phase copy) + k_dw_final, "
-                      "dX k_igemm<LdDenseRK,LdPixRK> (+ k_splitk_nchw when split)",
+                      "k_to_nhwc (ReLU mask + NHWC transpose + bias partials, with the dX filter "
+                      "re-layout as extra blocks; k_mask_pad for c1), dW k_igemm<LdGradKR,LdXTapKR> "
+                      "(c1, C = 3: k_igemm<LdGPadRK,LdPsRK> on the stride-phase copy) + k_dw_final "
+                      "(with the bias-gradient sum as extra blocks), dX k_igemm<LdDenseRK,LdPixRK> "
+                      "(+ k_splitk_nchw4 when split)",
             "achieved": round(achieved, 3),
             "peak": MFMA_FP32_PEAK_TFLOPS,
             "unit": "TFLOP/s",
