@@ -152,8 +152,12 @@ static hipEvent_t take_event() {
     g_eventFree.pop_back();
     return e;
   }
+  // Timing only: no system-scope fence when the event is recorded (the
+  // fence writes back and invalidates the caches, which cost every profiled
+  // launch a cold L2 and a few microseconds of idle GPU).  The profile is
+  // read after a stream synchronisation.
   hipEvent_t e = nullptr;
-  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  if (hipEventCreateWithFlags(&e, hipEventDisableSystemFence) != hipSuccess) return nullptr;
   return e;
 }
 
