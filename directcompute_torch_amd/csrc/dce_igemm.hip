@@ -18,7 +18,9 @@
 // Both feed the MFMA with the same k order: in MFMA s of a 16-wide k slice,
 // lane l (r = l % 16, g = l / 16) supplies A[r][4g + s] and B[4g + s][r], so
 // the four MFMAs together cover k 0..15 (the matrix unit sums over g).  KROW
-// rows carry a +4 pad; ROWK rows are unpadded (see Stage).
+// rows carry a +4 pad; ROWK rows are unpadded (see Stage).  A wave with 2 or
+// 4 fragments of a KROW operand interleaves them row by row, so that one
+// ds_read_b64 / b128 per k serves all of them (Stage::frags_rif).
 //
 // Convolutions work on channel-innermost ("NHWC", channels padded to a
 // multiple of 4) copies of their activations so that a quad is four
@@ -109,6 +111,33 @@ struct Stage {
   __device__ static __forceinline__ int qrow_data(int t, int i) {
     if (!SWZ) return qrow(t, i);
     return 4 * ((t % RQ) ^ fk(qk(t, i)));
+  }
+  static constexpr bool kRow = KROW;
+  // KROW, F = 2 or 4 fragments read together ("row-interleaved"): fragment i
+  // takes rows rb + F*rho + i (rho = 0..15), so lane (r, g) finds the F
+  // fragments' values at k = kb + 4g + s in F consecutive floats of one k row
+  // (inside one row quad, so the SWZ swizzle moves them together): one
+  // ds_read_b64 / b128 per s instead of F ds_read_b32.  The epilogues map the
+  // accumulator rows back (frow).
+  template <int F>
+  __device__ static __forceinline__ void frags_rif(const float* S, int rb, int r, int g, int kb,
+                                                   f4 (&out)[F]) {
+    static_assert(KROW && (F == 2 || F == 4), "row-interleaved fragments: KROW, F in {2, 4}");
+    const int row = rb + F * r;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int k = kb + 4 * g + s;
+      const float* p = S + k * LD + (SWZ ? 4 * ((row >> 2) ^ fk(k)) + (row & 3) : row);
+      if constexpr (F == 4) {
+        const f4 v = *reinterpret_cast<const f4*>(p);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) out[i][s] = v[i];
+      } else {
+        const f2 v = *reinterpret_cast<const f2*>(p);
+        out[0][s] = v[0];
+        out[1][s] = v[1];
+      }
+    }
   }
   // MFMA operand of 16 rows starting at rb, k slice kb: components s = 0..3.
   __device__ static __forceinline__ f4 frag(const float* S, int rb, int r, int g, int kb) {
@@ -915,7 +944,16 @@ struct LdGPadRK : LoaderBase<Stage<R, KT, false>> {
 //   TACC true:   C[m0 + wm*16FM + 16i + r][n0 + wn*16FN + 16j + 4g + v]
 //                (B fragment first: four consecutive columns of one row,
 //                 16 contiguous bytes of a row-major C: one quad store).
+// With row-interleaved fragments (RA for the A operand, RB for B; see
+// Stage::frags_rif) the wave-local row 16i + rho of fragment i becomes
+// F*rho + i (frow).  RB is only used without TACC: lane (r, g) then holds FN
+// consecutive columns FN*r .. FN*r + FN - 1 of each of its rows (j = 0 ..
+// FN - 1), which EpiRowMajor stores as one FN-float vector.
 // ---------------------------------------------------------------------------
+template <bool RIF, int F>
+__device__ __forceinline__ uint32_t frow(int i, int rho) {
+  return RIF ? uint32_t(F * rho + i) : uint32_t(16 * i + rho);
+}
 __device__ __forceinline__ float epi_act(float z, uint32_t act) {
   if (act == 1) return fmaxf(z, 0.f);
   if (act == 2) return tanhf(z);
@@ -927,12 +965,40 @@ struct EpiRowMajor {
     float* c;
     uint32_t M, N, ldc, splitStride;
   };
-  template <int MT, int NT, int FM, int FN, bool TACC>
+  template <int MT, int NT, int FM, int FN, bool TACC, bool RA, bool RB>
   __device__ static __forceinline__ void store(const Params& p, const f4 (&acc)[FM][FN],
                                                uint32_t m0, uint32_t n0, uint32_t z, int wm,
                                                int wn, int lane) {
     float* c = p.c + size_t(z) * p.splitStride;
     const int r = lane & 15, g = lane >> 4;
+    if constexpr (!TACC && RB) {
+      // FN consecutive columns per row: one FN-float store (rows aligned to
+      // FN floats, uniform over the launch).
+      const bool vec = ((p.ldc | p.splitStride) & (FN - 1)) == 0 &&
+                       (reinterpret_cast<uintptr_t>(p.c) & (4 * FN - 1)) == 0;
+      const uint32_t n = n0 + wn * (FN * 16) + FN * r;
+      if (n >= p.N) return;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const uint32_t m = m0 + wm * (FM * 16) + frow<RA, FM>(i, 4 * g + v);
+          if (m >= p.M) continue;
+          float* dst = c + size_t(m) * p.ldc + n;
+          if (vec && n + FN - 1 < p.N) {
+            if constexpr (FN == 4)
+              *reinterpret_cast<f4*>(dst) = f4{acc[i][0][v], acc[i][1][v], acc[i][2][v], acc[i][3][v]};
+            else
+              *reinterpret_cast<f2*>(dst) = f2{acc[i][0][v], acc[i][1][v]};
+          } else {
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+              if (n + j < p.N) dst[j] = acc[i][j][v];
+          }
+        }
+      }
+      return;
+    }
     if constexpr (!TACC) {
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
@@ -941,7 +1007,7 @@ struct EpiRowMajor {
         for (int i = 0; i < FM; ++i) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            const uint32_t m = m0 + wm * (FM * 16) + i * 16 + 4 * g + v;
+            const uint32_t m = m0 + wm * (FM * 16) + frow<RA, FM>(i, 4 * g + v);
             if (m < p.M && n < p.N) c[m * p.ldc + n] = acc[i][j][v];
           }
         }
@@ -953,7 +1019,7 @@ struct EpiRowMajor {
         ((p.ldc | p.splitStride) & 3) == 0 && (reinterpret_cast<uintptr_t>(p.c) & 15) == 0;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
-      const uint32_t m = m0 + wm * (FM * 16) + i * 16 + r;
+      const uint32_t m = m0 + wm * (FM * 16) + frow<RA, FM>(i, r);
       if (m >= p.M) continue;
       float* row = c + size_t(m) * p.ldc;
 #pragma unroll
@@ -983,7 +1049,7 @@ struct EpiNCHW {
     uint32_t M, HW, N, act;
     FastDiv dHW;
   };
-  template <int MT, int NT, int FM, int FN, bool TACC>
+  template <int MT, int NT, int FM, int FN, bool TACC, bool RA, bool RB>
   __device__ static __forceinline__ void store(const Params& p, const f4 (&acc)[FM][FN],
                                                uint32_t m0, uint32_t n0, uint32_t, int wm,
                                                int wn, int lane) {
@@ -991,14 +1057,14 @@ struct EpiNCHW {
     if constexpr (!TACC) {
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
-        const uint32_t n = n0 + wn * (FN * 16) + j * 16 + r;
+        const uint32_t n = n0 + wn * (FN * 16) + frow<RB, FN>(j, r);
         const uint32_t b = fdiv(n, p.dHW);
         const uint32_t base = b * p.M * p.HW + (n - b * p.HW);
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            const uint32_t m = m0 + wm * (FM * 16) + i * 16 + 4 * g + v;
+            const uint32_t m = m0 + wm * (FM * 16) + frow<RA, FM>(i, 4 * g + v);
             if (m < p.M && n < p.N)
               p.out[base + m * p.HW] = epi_act(acc[i][j][v] + (p.bias ? p.bias[m] : 0.f), p.act);
           }
@@ -1016,7 +1082,7 @@ struct EpiNCHW {
       const size_t base = size_t(b) * p.M * p.HW + pix;
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
-        const uint32_t m = m0 + wm * (FM * 16) + i * 16 + r;
+        const uint32_t m = m0 + wm * (FM * 16) + frow<RA, FM>(i, r);
         if (m >= p.M) continue;
         const float bias = p.bias ? p.bias[m] : 0.f;
         f4 z;
@@ -1050,14 +1116,15 @@ struct EpiNCHWPad {
     uint32_t M, OHW, OW, OWp, OHWp, N, act;
     FastDiv dOHWp, dOWp;
   };
-  template <int MT, int NT, int FM, int FN, bool TACC>
+  template <int MT, int NT, int FM, int FN, bool TACC, bool RA, bool RB>
   __device__ static __forceinline__ void store(const Params& p, const f4 (&acc)[FM][FN],
                                                uint32_t m0, uint32_t n0, uint32_t, int wm,
                                                int wn, int lane) {
+    static_assert(!(TACC && RB), "row-interleaved B fragments are not used with TACC");
     const int r = lane & 15, g = lane >> 4;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-      const uint32_t n = n0 + wn * (FN * 16) + j * 16 + (TACC ? 4 * g : r);
+      const uint32_t n = n0 + wn * (FN * 16) + (TACC ? j * 16 + 4 * g : frow<RB, FN>(j, r));
       const uint32_t b = fdiv(n, p.dOHWp), rem = n - b * p.OHWp;
       const uint32_t oh = fdiv(rem, p.dOWp), ow = rem - oh * p.OWp;
       if (n >= p.N || ow >= p.OW) continue;
@@ -1067,13 +1134,13 @@ struct EpiNCHWPad {
         if constexpr (!TACC) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            const uint32_t m = m0 + wm * (FM * 16) + i * 16 + 4 * g + v;
+            const uint32_t m = m0 + wm * (FM * 16) + frow<RA, FM>(i, 4 * g + v);
             if (m < p.M)
               p.out[base + size_t(m) * p.OHW] =
                   epi_act(acc[i][j][v] + (p.bias ? p.bias[m] : 0.f), p.act);
           }
         } else {
-          const uint32_t m = m0 + wm * (FM * 16) + i * 16 + r;
+          const uint32_t m = m0 + wm * (FM * 16) + frow<RA, FM>(i, r);
           if (m >= p.M) continue;
           const float bias = p.bias ? p.bias[m] : 0.f;
           f4 z;
@@ -1162,6 +1229,10 @@ __global__ void __launch_bounds__(kThreads)
 
   constexpr bool DA = LA::LDSD, DB = LB::LDSD;
   constexpr bool TACC = LB::kTransAcc;
+  // Row-interleaved fragments for [k][row] operands read 2 or 4 fragments at
+  // a time (B only without TACC, whose quad stores need 16-row fragments).
+  constexpr bool RA = SA::kRow && (FM == 2 || FM == 4);
+  constexpr bool RB = SB::kRow && !TACC && (FN == 2 || FN == 4);
   const int r = lane & 15, g = lane >> 4;
   // MFMAs of the K tile in LDS stage `cur`.
   auto compute = [&](int cur) {
@@ -1169,10 +1240,18 @@ __global__ void __launch_bounds__(kThreads)
     const float* Bc = Bs + cur * SB::SIZE;
     auto slice = [&](int ks) {
       f4 af[FM], bf[FN];
+      if constexpr (RA) {
+        SA::template frags_rif<FM>(Ac, wm * WM, r, g, ks, af);
+      } else {
 #pragma unroll
-      for (int i = 0; i < FM; ++i) af[i] = SA::frag(Ac, wm * WM + i * 16, r, g, ks);
+        for (int i = 0; i < FM; ++i) af[i] = SA::frag(Ac, wm * WM + i * 16, r, g, ks);
+      }
+      if constexpr (RB) {
+        SB::template frags_rif<FN>(Bc, wn * WN, r, g, ks, bf);
+      } else {
 #pragma unroll
-      for (int j = 0; j < FN; ++j) bf[j] = SB::frag(Bc, wn * WN + j * 16, r, g, ks);
+        for (int j = 0; j < FN; ++j) bf[j] = SB::frag(Bc, wn * WN + j * 16, r, g, ks);
+      }
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -1235,7 +1314,7 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] += red[(w * FM * FN + i * FN + j) * 64 + lane];
   }
-  EPI::template store<MT, NT, FM, FN, TACC>(pe, acc, m0, n0, z, wm, wn, lane);
+  EPI::template store<MT, NT, FM, FN, TACC, RA, RB>(pe, acc, m0, n0, z, wm, wn, lane);
 }
 
 // ---------------------------------------------------------------------------
