@@ -315,7 +315,8 @@ def memory_suite(reps=10):
     x, dy = buf(mb), buf(mb)
     mean, var, gamma = buf((C,), "zero"), buf((C,), "unit"), buf((C,), "unit")
     dg, db, dx = buf((C,), "zero"), buf((C,), "zero"), buf(mb, "zero")
-    nn._dispatch(b"batchnorm_mean_var", (x,), (mean, var, buf((C,), "zero"), buf((C,), "unit")),
+    rmean, rvar = buf((C,), "zero"), buf((C,), "unit")   # running statistics
+    nn._dispatch(b"batchnorm_mean_var", (x,), (mean, var, rmean, rvar),
                  C, 1, 1, u1=B, u2=C, u3=S, u4=1, u5=f2u(0.1), cbSize=20)
     cb = dict(u1=B, u2=C, u3=S, u4=f2u(1e-5))
     run("batchnorm_backward_reduce", "bn_bwd_reduce", mb, 8 * n,
@@ -323,8 +324,10 @@ def memory_suite(reps=10):
     run("batchnorm_backward_dx", "bn_bwd_dx", mb, 12 * n,
         lambda: nn._dispatch(b"batchnorm_backward_dx", (x, dy, mean, var, gamma, dg, db), (dx,),
                              (n + 255) // 256, 1, 1, **cb))
+    # The running statistics are made once: a buffer created inside the timed
+    # launches would time its allocation and host upload too.
     run("batchnorm_mean_var", "bn_stats", mb, 4 * n,
-        lambda: nn._dispatch(b"batchnorm_mean_var", (x,), (mean, var, buf((C,), "zero"), buf((C,), "unit")),
+        lambda: nn._dispatch(b"batchnorm_mean_var", (x,), (mean, var, rmean, rvar),
                              C, 1, 1, u1=B, u2=C, u3=S, u4=1, u5=f2u(0.1), cbSize=20))
 
     # Depthwise 3x3 backward: stride 1 (hidden 144 at 56^2) and stride 2 (96 at 112^2 -> 56^2)
