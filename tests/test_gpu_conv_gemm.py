@@ -147,6 +147,51 @@ def test_pointwise_conv_backward_subsets(eng, want, act):
     _conv_case(eng, 2, 32, 12, 12, 48, 1, 1, 0, act, want=want, seed=14, keep=False)
 
 
+PS_CASES = [
+    (2, 3, 35, 35, 64, 11, 4, 2, 1),      # AlexNet c1 geometry (OW 8, no pad columns)
+    (2, 3, 23, 21, 72, 5, 2, 1, 1),       # OW 10 -> 12 padded columns
+    (2, 2, 7, 7, 6, 3, 2, 0, 1),          # OW 3: rows of fewer than 4 elements
+    (2, 1, 12, 12, 40, 3, 1, 1, 1),       # 9 taps, 40 channels: taps as the dW rows
+    (1, 3, 6, 5, 8, 5, 1, 2, 0),          # no activation (no mask)
+]
+
+
+@pytest.mark.parametrize("case", PS_CASES)
+@pytest.mark.parametrize("want", [(0, 1, 1), (0, 1, 0), (0, 0, 1), (1, 1, 1), (1, 0, 1), (1, 1, 0)])
+def test_stride_phase_backward_subsets(eng, case, want):
+    """Fewer than 4 input channels (stride-phase copy): every gradient subset,
+    with the masked gradient on the padded pixel grid (dW, db) and the NHWC
+    gradient (dX; db when dW is not wanted)."""
+    _conv_case(eng, *case, want=want, seed=17)
+
+
+def test_stride_phase_relu_mask_nan_keeps_grad(eng):
+    """The masked gradient on the padded pixel grid (stride-phase dW and db):
+    y <= 0 zeroes it, a NaN y keeps it (nn_conv_grad_reshape_relu.hlsl:36), in
+    the last quad of an output row as in the others."""
+    B, C, H, W, OC, k, s, p = 2, 3, 23, 21, 8, 5, 2, 1
+    OH, OW = K.conv_out_hw(H, W, k, s, p)
+    r = rng(78)
+    x = r.standard_normal((B, C, H, W)).astype(np.float32)
+    w = he(r, (OC, C, k, k), C * k * k)
+    y = r.standard_normal((B, OC, OH, OW)).astype(np.float32)
+    y[0, 0, 0, 0] = np.nan
+    y[1, 2, 3, OW - 1] = np.nan
+    y[0, 1, 1, OW - 2] = 0.0
+    dy = r.standard_normal(y.shape).astype(np.float32)
+    hs = [upload(eng, a) for a in (x, w, y, dy)]
+    pdf, pdb, pdx = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+    eng.lib.ConvBackwardFused(hs[3], hs[2], hs[0], hs[1], None, B, C, H, W, OC, k, k, s, p, 1, 0, 1, 1,
+                              ctypes.byref(pdf), ctypes.byref(pdb), ctypes.byref(pdx))
+    assert pdf.value and pdb.value and not pdx.value, eng.last_error()
+    dW_ref, db_ref, _ = K.conv_backward(dy, y, x, w, s, p, 1, need_x=0)
+    got = (download(eng, pdf.value, w.shape), download(eng, pdb.value, (OC,)))
+    release(eng, *hs, pdf.value, pdb.value)
+    for g, ref in zip(got, (dW_ref, db_ref)):
+        assert np.isfinite(g).all() == np.isfinite(ref).all()
+        assert rel_err(g, ref) <= TOL
+
+
 def test_conv_backward_relu_mask_nan_keeps_grad(eng):
     """y <= 0 zeroes the gradient; NaN in y keeps it (nn_conv_grad_reshape_relu.hlsl:36)."""
     B, C, H, W, OC, k = 1, 16, 6, 6, 16, 3
