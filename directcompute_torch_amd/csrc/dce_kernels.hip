@@ -1983,10 +1983,17 @@ __host__ __device__ constexpr uint32_t dw_gband(uint32_t S) { return S == 1 ? kD
 // B * nb units (unit u = band u mod nb of image u / nb: output rows
 // [o0, o0 + RB), RB even); the ranges split the units evenly over the pieces:
 //   LDS x cell (i, j) = x[o0*S - p + i][j - p]      (LXR x LXW, zero outside)
-//   LDS g cell (i, j) = dy[o0 + i][j]               (LGR x LGW, zero outside)
-// A thread takes 2 x 2 blocks of dy and the (S + K) x (S + K) x window under
-// them.  The K*K + 1 running sums are reduced once per block (waves by
-// shuffle, then the 4 wave sums in order) and stored as part[c][piece][t] (double).
+//   LDS g cell (i, j) = dy[o0 + i][j]               (LGR x LGW, zero outside; S = 2)
+// A thread takes 2 x 2 blocks of dy (items e = tid + 256 i of the band's
+// (LGR / 2) x (LGW / 2) blocks) and the (S + K) x (S + K) x window under them.
+// Stride 1: each dy value is used by one thread only, so the thread loads its
+// blocks (at most NI) straight into registers -- the next unit's while the
+// current one is multiplied, zero outside the plane -- and only the x window,
+// which neighbouring blocks share, goes through LDS (64x144x56x56: 44.3 ->
+// 41.9 us).  Stride 2 stages the dy window in LDS too (the register form
+// measured 68 -> 75 us at 64x96x112x112).  The K*K + 1 running sums are
+// reduced once per block (waves by shuffle, then the 4 wave sums in order)
+// and stored as part[c][piece][t] (double).
 template <int K, int S, bool V4>
 __global__ void __launch_bounds__(256)
     k_dw_bwd_filter_band(const float* __restrict__ dy, const float* __restrict__ x,
@@ -1996,33 +2003,68 @@ __global__ void __launch_bounds__(256)
                          FastDiv dLXW, FastDiv dLGW, FastDiv dNb, FastDiv dBW) {
   constexpr int T = K * K + 1;
   constexpr int XW = S + K;  // x window edge under a 2 x 2 dy block
+  constexpr bool GREG = S == 1;                       // dy blocks in registers
+  constexpr int NI = GREG ? int(dw_gband(S) / 1024) : 1;  // LGR * LGW <= dw_gband(S)
   __shared__ __attribute__((aligned(16))) float sx[kDwBand];
-  __shared__ __attribute__((aligned(16))) float sg[dw_gband(S)];
+  __shared__ __attribute__((aligned(16))) float sg[GREG ? 4 : dw_gband(S)];
   __shared__ float red[4][T];
   const uint32_t c = blockIdx.x, piece = blockIdx.y, npieces = gridDim.y;
   BRes bx, bg;
   bx.init(x, B * C * H * W);
   bg.init(dy, B * C * OH * OW);
   DwRegs<V4, kDwRegs> xv;
-  DwRegs<V4, dw_gband(S) / 256> gv;
+  DwRegs<V4, GREG ? 4 : dw_gband(S) / 256> gv;  // S = 2: the next unit's dy window
   const int lox = DwRegs<V4, kDwRegs>::shift(-int(p));
   // The channel's B * nb (image, band) units, split evenly over the pieces.
   const uint32_t units = B * nb;
   const uint32_t u0 = uint32_t(uint64_t(units) * piece / npieces);
   const uint32_t total = uint32_t(uint64_t(units) * (piece + 1) / npieces) - u0;
+  const uint32_t items = (LGR / 2) * (LGW / 2);
+  // Stride 1: this thread's 2 x 2 blocks, band rows 2a, columns 2b (fixed for
+  // every unit), and the next unit's dy values of them.
+  uint32_t ia[NI], ib[NI];
+#pragma unroll
+  for (int it = 0; it < NI; ++it) {
+    const uint32_t e = threadIdx.x + 256u * it;
+    ia[it] = fdiv(e, dBW);
+    ib[it] = e - ia[it] * (LGW / 2);
+  }
+  float gq[NI][4];
   auto issue = [&](uint32_t j) {
     const uint32_t u = u0 + j;
     const uint32_t n = fdiv(u, dNb), o0 = (u - n * nb) * RB;
     const uint32_t plane = n * C + c;
     xv.load(bx, plane * H * W, H, W, DwWin{int(o0 * S) - int(p), -int(p), LXR, LXW}, dLXW);
-    gv.load(bg, plane * OH * OW, OH, OW, DwWin{int(o0), 0, LGR, LGW}, dLGW);
+    if constexpr (!GREG) {
+      gv.load(bg, plane * OH * OW, OH, OW, DwWin{int(o0), 0, LGR, LGW}, dLGW);
+    } else {
+      const uint32_t gb = plane * OH * OW;
+#pragma unroll
+      for (int it = 0; it < NI; ++it) {
+        const bool in = threadIdx.x + 256u * it < items;
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const uint32_t row = o0 + 2 * ia[it] + r, col = 2 * ib[it];
+          if (V4) {
+            // Rows of a multiple of 4 floats: the pair is one 8-byte load.
+            const f2 v = bg.ld2(in && row < OH && col < OW ? gb + row * OW + col : kOob);
+            gq[it][2 * r] = v[0];
+            gq[it][2 * r + 1] = v[1];
+          } else {
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc)
+              gq[it][2 * r + cc] =
+                  bg.ld1(in && row < OH && col + cc < OW ? gb + row * OW + col + cc : kOob);
+          }
+        }
+      }
+    }
   };
   // Stride 2: LDS rows are stored phase-split, x by column mod 4 and dy by
   // column mod 2.  A thread's x columns 4*b2 + jj + lox then sit at b2 +
   // xo[jj] and its dy columns 2*b2 + cc at b2 + cc * LGW / 2, so consecutive
   // lanes (consecutive b2) read consecutive words instead of every 4th bank
-  // (s2 dW 77 -> 74 us at MobileNetV2's 112x112; for stride 1 the split's
-  // dword stores cost more than the 2-way conflicts they remove).
+  // (s2 dW 77 -> 74 us at MobileNetV2's 112x112).
   constexpr int PX = S == 2 ? 4 : 1, PG = S == 2 ? 2 : 1;
   int xo[XW];
 #pragma unroll
@@ -2030,6 +2072,24 @@ __global__ void __launch_bounds__(256)
   float acc[T];
 #pragma unroll
   for (int q = 0; q < T; ++q) acc[q] = 0.f;
+  // One 2 x 2 dy block g with the x window under block (a, b2).
+  auto block = [&](uint32_t a, uint32_t b2, const float (&g)[2][2]) {
+    float xw[XW][XW];
+#pragma unroll
+    for (int i = 0; i < XW; ++i)
+#pragma unroll
+      for (int jj = 0; jj < XW; ++jj) xw[i][jj] = sx[(2 * a * S + i) * LXW + (2 * S / PX) * b2 + xo[jj]];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc) {
+        acc[K * K] += g[r][cc];
+#pragma unroll
+        for (int fh = 0; fh < K; ++fh)
+#pragma unroll
+          for (int fw = 0; fw < K; ++fw) acc[fh * K + fw] += g[r][cc] * xw[r * S + fh][cc * S + fw];
+      }
+  };
   if (total) issue(0);
   for (uint32_t jb = 0; jb < total; ++jb) {
     __syncthreads();  // the previous band's LDS reads are done
@@ -2038,34 +2098,32 @@ __global__ void __launch_bounds__(256)
       gv.template store_ph<PG>(sg, LGR, LGW, dLGW);
     } else {
       xv.store(sx, LXR, LXW);
-      gv.store(sg, LGR, LGW);
     }
+    float gc[NI][4];
+#pragma unroll
+    for (int it = 0; it < NI; ++it)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) gc[it][v] = gq[it][v];
     __syncthreads();
     if (jb + 1 < total) issue(jb + 1);
-    const uint32_t items = (LGR / 2) * (LGW / 2);
-    for (uint32_t e = threadIdx.x; e < items; e += 256) {
-      const uint32_t a = fdiv(e, dBW), b2 = e - a * (LGW / 2);
-      float g[2][2];
+    if constexpr (GREG) {
 #pragma unroll
-      for (int r = 0; r < 2; ++r)
+      for (int it = 0; it < NI; ++it) {
+        if (threadIdx.x + 256u * it >= items) break;
+        const float g[2][2] = {{gc[it][0], gc[it][1]}, {gc[it][2], gc[it][3]}};
+        block(ia[it], ib[it], g);
+      }
+    } else {
+      for (uint32_t e = threadIdx.x; e < items; e += 256) {
+        const uint32_t a = fdiv(e, dBW), b2 = e - a * (LGW / 2);
+        float g[2][2];
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc)
-          g[r][cc] = sg[(2 * a + r) * LGW + (cc % PG) * (LGW / PG) + (2 / PG) * b2 + cc / PG];
-      float xw[XW][XW];
+        for (int r = 0; r < 2; ++r)
 #pragma unroll
-      for (int i = 0; i < XW; ++i)
-#pragma unroll
-        for (int jj = 0; jj < XW; ++jj) xw[i][jj] = sx[(2 * a * S + i) * LXW + (2 * S / PX) * b2 + xo[jj]];
-#pragma unroll
-      for (int r = 0; r < 2; ++r)
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-          acc[K * K] += g[r][cc];
-#pragma unroll
-          for (int fh = 0; fh < K; ++fh)
-#pragma unroll
-            for (int fw = 0; fw < K; ++fw) acc[fh * K + fw] += g[r][cc] * xw[r * S + fh][cc * S + fw];
-        }
+          for (int cc = 0; cc < 2; ++cc)
+            g[r][cc] = sg[(2 * a + r) * LGW + (cc % PG) * (LGW / PG) + (2 / PG) * b2 + cc / PG];
+        block(a, b2, g);
+      }
     }
   }
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
