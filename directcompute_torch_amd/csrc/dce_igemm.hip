@@ -2799,6 +2799,7 @@ struct DwPwRun {
   float* part;
   ConvGeom g;
   uint32_t N, splits;  // N = C, or C + 1 with the ones row
+  bool trans;          // input channels as the product's rows (partials [z][c][oc])
   template <int MT, int NT, int KT>
   int occ(bool) const {
     return occupancy(k_igemm<MT, NT, KT, LdNchwRK<MT, KT>, LdNchwRK<NT, KT>, EpiRowMajor>);
@@ -2809,7 +2810,13 @@ struct DwPwRun {
     const NchwRKParams pa{dy, ones4(), g.OC, HW, K, g.B * g.OC * HW, 0xFFFFFFFFu, make_fastdiv(HW)};
     const NchwRKParams pb{x, ones4(), g.C, HW, K, g.B * g.C * HW, N > g.C ? g.C : 0xFFFFFFFFu,
                           make_fastdiv(HW)};
-    const EpiRowMajor::Params pe{part, g.OC, N, N, 4 * cdiv(size_t(g.OC) * N, 4)};
+    const uint32_t zs = 4 * cdiv(size_t(g.OC) * N, 4);
+    if (trans) {
+      const EpiRowMajor::Params pe{part, N, g.OC, g.OC, zs};
+      return launch<MT, NT, KT, LdNchwRK<MT, KT>, LdNchwRK<NT, KT>, EpiRowMajor>(
+          pb, pa, pe, N, g.OC, cdiv(K, KT), splits, "conv_backward_filter");
+    }
+    const EpiRowMajor::Params pe{part, g.OC, N, N, zs};
     return launch<MT, NT, KT, LdNchwRK<MT, KT>, LdNchwRK<NT, KT>, EpiRowMajor>(
         pa, pb, pe, g.OC, N, cdiv(K, KT), splits, "conv_backward_filter");
   }
@@ -2823,10 +2830,15 @@ static bool conv_backward_pw(const float* dy, const float* x, const float* w, fl
   const uint32_t Ndw = g.C + (db ? 1u : 0u);
   TileCfg dwc{128, 128, 16, 1}, dxc{128, 128, 16, 1};
   size_t nP = 0, nW = 0, nQ = 0;
+  // dW orientation with the fuller tile grid: expand layers (many more
+  // output than input channels) put the few input channels on the narrow
+  // rows.
+  const bool dwT = tile_fill(Ndw, g.OC) > tile_fill(g.OC, Ndw) * 1.25;
   if (dw) {
-    const uint32_t ntiles = cdiv(g.OC, pick_tile_m(g.OC)) * cdiv(Ndw, pick_tile(Ndw));
+    const uint32_t dM = dwT ? Ndw : g.OC, dN = dwT ? g.OC : Ndw;
+    const uint32_t ntiles = cdiv(dM, pick_tile_m(dM)) * cdiv(dN, pick_tile(dN));
     dwc = choose(
-        "DCE_TUNE_DW", g.OC, Ndw, N, ntiles <= 4 ? 1024 : 256, false,
+        "DCE_TUNE_DW", dM, dN, N, ntiles <= 4 ? 1024 : 256, false,
         [&](const TileCfg& t) { return tiles_occ(t, DwPwRun{}); }, false, true);
     nP = al64(size_t(dwc.splits) * 4 * cdiv(size_t(g.OC) * Ndw, 4));
   }
@@ -2848,8 +2860,8 @@ static bool conv_backward_pw(const float* dy, const float* x, const float* w, fl
   float* qpart = wt ? wt + nW : nullptr;
   if (dw) {
     ProfScope prof("conv_dw", fl, 4.0 * (double(N) * g.OC + double(N) * g.C));
-    if (!tiles_dispatch(dwc, DwPwRun{dy, x, part, g, Ndw, dwc.splits}) ||
-        !dw_final(part, dw, g.OC, g.C, 1, Ndw, dwc.splits, false, BwdSide{}, db))
+    if (!tiles_dispatch(dwc, DwPwRun{dy, x, part, g, Ndw, dwc.splits, dwT}) ||
+        !dw_final(part, dw, g.OC, g.C, 1, Ndw, dwc.splits, dwT, BwdSide{}, db))
       return false;
   }
   if (dx) {

@@ -71,6 +71,7 @@ CONV_CASES = [
     (2, 144, 28, 28, 32, 1, 1, 0, 2),     # tanh: no derivative, so no mask
     (8, 16, 56, 56, 96, 1, 1, 0, 0),      # expand at a MobileNet plane size (split-K dW)
     (2, 40, 6, 6, 130, 1, 1, 0, 0),       # db column at a tile edge (N = 41), OC past 128
+    (3, 5, 8, 12, 40, 1, 1, 0, 0),        # expand: input channels (+ db row) as the dW rows
 ]
 
 
@@ -139,12 +140,14 @@ def test_conv_backward_subsets(eng, want):
 
 @pytest.mark.parametrize("want", [(0, 1, 1), (1, 0, 0), (0, 0, 1), (1, 1, 0), (0, 1, 0)])
 @pytest.mark.parametrize("act", [0, 1])
-def test_pointwise_conv_backward_subsets(eng, want, act):
+@pytest.mark.parametrize("C,OC", [(32, 48), (8, 72)], ids=["c32_48", "expand_8_72"])
+def test_pointwise_conv_backward_subsets(eng, want, act, C, OC):
     """Pointwise layers: every gradient subset, without (NCHW GEMMs in place;
     db alone goes through the general path) and with the ReLU mask (the
-    general path, building the NHWC copy the forward did not keep)."""
-    _conv_case(eng, 2, 32, 12, 12, 48, 1, 1, 0, act, want=want, seed=13)
-    _conv_case(eng, 2, 32, 12, 12, 48, 1, 1, 0, act, want=want, seed=14, keep=False)
+    general path, building the NHWC copy the forward did not keep); 8 -> 72
+    channels puts the input channels on the dW product's rows."""
+    _conv_case(eng, 2, C, 12, 12, OC, 1, 1, 0, act, want=want, seed=13)
+    _conv_case(eng, 2, C, 12, 12, OC, 1, 1, 0, act, want=want, seed=14, keep=False)
 
 
 PS_CASES = [
