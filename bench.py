@@ -226,12 +226,13 @@ def cpu_baseline(sample=256):
 HBM_PEAK_BYTES_PER_S = HBM_PEAK_GBS * 1e9
 
 
-def memory_suite(reps=10):
+def memory_suite(reps=10, trials=5):
     """Backward memory-bound kernels at the shapes of the benchmark networks,
     each driven through the same dispatch the API's backward makes.  One JSON
     line per kernel: algorithmic bytes per launch (each required tensor read
     or written once), the time per launch of `reps` back-to-back launches
-    (one HIP-event pair around them), GB/s and fraction of 8 TB/s."""
+    (one HIP-event pair around them; the median of `trials` such runs), GB/s
+    and fraction of 8 TB/s."""
     from directcompute_torch_amd import nn_engine as nn
     lib = nn.lib
     rng = np.random.default_rng(SEED + 7)
@@ -262,24 +263,29 @@ def memory_suite(reps=10):
         # One event pair around `reps` back-to-back launches (an event pair per
         # launch would add its own few microseconds of idle GPU to each), or,
         # with per_launch, the family's own event pair inside each call (for
-        # calls that launch more than the kernel measured).
+        # calls that launch more than the kernel measured).  The median of
+        # `trials` such measurements is reported (single runs vary by a few
+        # percent from run to run).
         fn()
         lib.SyncGPU()
-        lib.ResetProfile()
-        if per_launch:
-            lib.SetProfiling(1)
-        else:
-            lib.BeginProfileRegion(family.encode(), 0.0, float(nbytes) * reps)
-        for _ in range(reps):
-            fn()
-        if per_launch:
+        per = []
+        for _ in range(trials):
+            lib.ResetProfile()
+            if per_launch:
+                lib.SetProfiling(1)
+            else:
+                lib.BeginProfileRegion(family.encode(), 0.0, float(nbytes) * reps)
+            for _ in range(reps):
+                fn()
+            if per_launch:
+                lib.SyncGPU()
+                lib.SetProfiling(0)
+            else:
+                lib.EndProfileRegion()
             lib.SyncGPU()
-            lib.SetProfiling(0)
-        else:
-            lib.EndProfileRegion()
-        lib.SyncGPU()
-        n, ms = prof(family)
-        us = ms / (max(n, 1) if per_launch else reps) * 1e3
+            n, ms = prof(family)
+            per.append(ms / (max(n, 1) if per_launch else reps) * 1e3)
+        us = float(np.median(per))
         gbps = nbytes / (us * 1e-6) / 1e9 if us > 0 else 0.0
         rec = {"suite": "memory", "kernel": kernel, "family": family, "shape": list(shape),
                "bytes_per_launch": int(nbytes), "us": round(us, 2), "GB/s": round(gbps, 1),
@@ -352,7 +358,7 @@ def memory_suite(reps=10):
         nx, no = B * C * H * W, B * C * OH * OW
         pidx = ctypes.c_void_p()
         held.append(lib.MaxPoolForwardFused(xin, B, C, H, W, k, st, ctypes.byref(pidx)))
-        for _ in range(reps + 1):
+        for _ in range(trials * reps + 1):
             lib.AddRefBuffer(pidx.value)
 
         def mp(idx=pidx.value, dz=dz, B=B, C=C, OH=OH, OW=OW, nx=nx):

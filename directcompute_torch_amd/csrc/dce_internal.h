@@ -94,11 +94,18 @@ struct BRes {
   __device__ __forceinline__ f4 ld4(uint32_t off) const {
     return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, off * 4u, 0, 0));
   }
+  // Nontemporal form (the NT cache-policy bit), for passes larger than the MALL.
+  __device__ __forceinline__ f4 ld4nt(uint32_t off) const {
+    return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, off * 4u, 0, 2));
+  }
   __device__ __forceinline__ float ld1(uint32_t off) const {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off * 4u, 0, 0));
   }
   __device__ __forceinline__ f2 ld2(uint32_t off) const {
     return __builtin_bit_cast(f2, __builtin_amdgcn_raw_buffer_load_b64(r, off * 4u, 0, 0));
+  }
+  __device__ __forceinline__ f2 ld2nt(uint32_t off) const {
+    return __builtin_bit_cast(f2, __builtin_amdgcn_raw_buffer_load_b64(r, off * 4u, 0, 2));
   }
   // 16 bytes per lane straight into LDS: the wave's lanes fill 64 consecutive
   // 16-byte slots from `lds` (wave-uniform) in lane order; an offset past

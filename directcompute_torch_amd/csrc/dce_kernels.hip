@@ -1678,7 +1678,7 @@ __device__ __forceinline__ void dw_win_store(float* lds, const float (&v)[N], ui
 // column, and its width w.LW (the stored width) is a multiple of 4.  Each
 // quad then lies wholly inside or wholly outside the plane and is one 16-byte
 // buffer load (a quarter of the loads and index divisions of the dword form).
-template <int N>
+template <int N, bool NT = false>
 __device__ __forceinline__ void dw_win_load4(const BRes& b, uint32_t base, uint32_t rows,
                                              uint32_t cols, const DwWin& w, FastDiv dQW,
                                              f4 (&v)[N]) {
@@ -1690,7 +1690,8 @@ __device__ __forceinline__ void dw_win_load4(const BRes& b, uint32_t base, uint3
     const uint32_t i = fdiv(q, dQW), jq = q - i * qw;
     const int r = w.rb + int(i), c = cs + 4 * int(jq);
     const bool ok = q < w.R * qw && r >= 0 && r < int(rows) && c >= 0 && c < int(cols);
-    v[u] = b.ld4(ok ? base + uint32_t(r) * cols + uint32_t(c) : kOob);
+    const uint32_t off = ok ? base + uint32_t(r) * cols + uint32_t(c) : kOob;
+    v[u] = NT ? b.ld4nt(off) : b.ld4(off);
   }
 }
 template <int N>
@@ -1704,10 +1705,12 @@ template <bool V4, int N>
 struct DwRegs {
   float v[V4 ? 1 : N];
   f4 q[V4 ? N / 4 : 1];
+  // NT: nontemporal quad loads (the dword form has no such variant).
+  template <bool NT = false>
   __device__ __forceinline__ void load(const BRes& b, uint32_t base, uint32_t rows, uint32_t cols,
                                        const DwWin& w, FastDiv d) {
     if constexpr (V4)
-      dw_win_load4(b, base, rows, cols, w, d, q);
+      dw_win_load4<N / 4, NT>(b, base, rows, cols, w, d, q);
     else
       dw_win_load(b, base, rows, cols, w, d, v);
   }
@@ -1991,10 +1994,11 @@ __host__ __device__ constexpr uint32_t dw_gband(uint32_t S) { return S == 1 ? kD
 // current one is multiplied, zero outside the plane -- and only the x window,
 // which neighbouring blocks share, goes through LDS (64x144x56x56: 44.3 ->
 // 41.9 us).  Stride 2 stages the dy window in LDS too (the register form
-// measured 68 -> 75 us at 64x96x112x112).  The K*K + 1 running sums are
-// reduced once per block (waves by shuffle, then the 4 wave sums in order)
-// and stored as part[c][piece][t] (double).
-template <int K, int S, bool V4>
+// measured 68 -> 75 us at 64x96x112x112).  NT: nontemporal loads, for
+// passes larger than the MALL (stride 2 at 64x96x112x112: 68 -> 63 us).  The
+// K*K + 1 running sums are reduced once per block (waves by shuffle, then
+// the 4 wave sums in order) and stored as part[c][piece][t] (double).
+template <int K, int S, bool V4, bool NT>
 __global__ void __launch_bounds__(256)
     k_dw_bwd_filter_band(const float* __restrict__ dy, const float* __restrict__ x,
                          double* __restrict__ part, uint32_t B, uint32_t C, uint32_t H,
@@ -2034,9 +2038,10 @@ __global__ void __launch_bounds__(256)
     const uint32_t u = u0 + j;
     const uint32_t n = fdiv(u, dNb), o0 = (u - n * nb) * RB;
     const uint32_t plane = n * C + c;
-    xv.load(bx, plane * H * W, H, W, DwWin{int(o0 * S) - int(p), -int(p), LXR, LXW}, dLXW);
+    xv.template load<NT>(bx, plane * H * W, H, W, DwWin{int(o0 * S) - int(p), -int(p), LXR, LXW},
+                         dLXW);
     if constexpr (!GREG) {
-      gv.load(bg, plane * OH * OW, OH, OW, DwWin{int(o0), 0, LGR, LGW}, dLGW);
+      gv.template load<NT>(bg, plane * OH * OW, OH, OW, DwWin{int(o0), 0, LGR, LGW}, dLGW);
     } else {
       const uint32_t gb = plane * OH * OW;
 #pragma unroll
@@ -2047,7 +2052,8 @@ __global__ void __launch_bounds__(256)
           const uint32_t row = o0 + 2 * ia[it] + r, col = 2 * ib[it];
           if (V4) {
             // Rows of a multiple of 4 floats: the pair is one 8-byte load.
-            const f2 v = bg.ld2(in && row < OH && col < OW ? gb + row * OW + col : kOob);
+            const uint32_t off = in && row < OH && col < OW ? gb + row * OW + col : kOob;
+            const f2 v = NT ? bg.ld2nt(off) : bg.ld2(off);
             gq[it][2 * r] = v[0];
             gq[it][2 * r + 1] = v[1];
           } else {
@@ -2339,8 +2345,8 @@ static bool sh_dw_bwd_filter(const Dispatch& d) {
     int occ = 1;
 #define DCE_DWO(K, SS)                                                                      \
   if (g.kH == K && g.s == SS)                                                              \
-    occ = bb.v4 ? blocks_per_cu(k_dw_bwd_filter_band<K, SS, true>, 256)                    \
-                : blocks_per_cu(k_dw_bwd_filter_band<K, SS, false>, 256);
+    occ = bb.v4 ? blocks_per_cu(k_dw_bwd_filter_band<K, SS, true, false>, 256)             \
+                : blocks_per_cu(k_dw_bwd_filter_band<K, SS, false, false>, 256);
     DCE_DWO(3, 1) DCE_DWO(3, 2) DCE_DWO(5, 1) DCE_DWO(5, 2)
 #undef DCE_DWO
     const uint32_t want =
@@ -2352,17 +2358,25 @@ static bool sh_dw_bwd_filter(const Dispatch& d) {
     const uint32_t pieces = g.s == 2 ? g.B : std::min<uint32_t>(g.B, want);
     double* part = reinterpret_cast<double*>(workspace(size_t(g.C) * pieces * (taps + 1) * 2));
     if (!part) return false;
-    ProfScope prof("dw_bwd_filter", 2.0 * taps * double(len) * g.C,
-                   4.0 * double(len) * g.C + 4.0 * double(g.B) * g.C * g.H * g.W);
+    const double bytes = 4.0 * double(len) * g.C + 4.0 * double(g.B) * g.C * g.H * g.W;
+    ProfScope prof("dw_bwd_filter", 2.0 * taps * double(len) * g.C, bytes);
+    const bool nt = stream_nt(bytes);
     const dim3 grid(g.C, pieces);
     const uint32_t nb = cdiv(g.OH, bb.RB);
     const FastDiv fLX = make_fastdiv(bb.v4 ? bb.LW / 4 : bb.LW),
                   fLG = make_fastdiv(bb.v4 ? bb.LW2 / 4 : bb.LW2), fNb = make_fastdiv(nb),
                   fBW = make_fastdiv(bb.LW2 / 2);
-#define DCE_DWF_V(K, SS, V)                                                                      \
-  hipLaunchKernelGGL((k_dw_bwd_filter_band<K, SS, V>), grid, dim3(256), 0, stream(), dy.p, x.p,   \
+#define DCE_DWF_N(K, SS, V, N)                                                                   \
+  hipLaunchKernelGGL((k_dw_bwd_filter_band<K, SS, V, N>), grid, dim3(256), 0, stream(), dy.p, x.p,\
                      part, g.B, g.C, g.H, g.W, g.OH, g.OW, g.p, bb.RB, nb, bb.R, bb.LW, bb.R2,    \
                      bb.LW2, fLX, fLG, fNb, fBW);
+#define DCE_DWF_V(K, SS, V)                                                                      \
+  {                                                                                              \
+    if (nt && V)                                                                                 \
+      DCE_DWF_N(K, SS, V, true)                                                                  \
+    else                                                                                         \
+      DCE_DWF_N(K, SS, V, false)                                                                 \
+  }
 #define DCE_DWF(K, SS)                                                                          \
   if (g.kH == K && g.s == SS) {                                                                \
     if (bb.v4)                                                                                 \
@@ -2373,6 +2387,7 @@ static bool sh_dw_bwd_filter(const Dispatch& d) {
     DCE_DWF(3, 1) DCE_DWF(3, 2) DCE_DWF(5, 1) DCE_DWF(5, 2)
 #undef DCE_DWF
 #undef DCE_DWF_V
+#undef DCE_DWF_N
     hipLaunchKernelGGL(k_dw_bwd_filter_final, dim3(cdiv(g.C * (taps + 1), 4)), dim3(256), 0,
                        stream(), part, pieces, g.C, taps, U(d, 0), U(d, 1));
     return check_launch("depthwise_conv_backward_filter");
