@@ -124,6 +124,34 @@ def test_conv_forward_backward(eng, case):
     _conv_case(eng, *case)
 
 
+def _random_conv_cases(n, seed):
+    """Seeded random geometries (each layout: stride-phase, channel-packed,
+    pointwise, NHWC at every stride / pad / kernel size up to 7, ragged
+    channel counts, tiny and odd planes)."""
+    r = rng(seed)
+    out = []
+    while len(out) < n:
+        k = int(r.integers(1, 8))
+        s = int(r.integers(1, 6))
+        p = int(r.integers(0, k))
+        H, W = int(r.integers(k, 24)), int(r.integers(k, 24))
+        if (H + 2 * p - k) // s + 1 < 1 or (W + 2 * p - k) // s + 1 < 1:
+            continue
+        out.append((int(r.integers(1, 4)), int(r.integers(1, 41)), H, W, int(r.integers(1, 70)),
+                    k, s, p, int(r.integers(0, 3))))
+    return out
+
+
+RANDOM_CONV_CASES = _random_conv_cases(40, 31337)
+
+
+@pytest.mark.parametrize("case", RANDOM_CONV_CASES, ids=[str(c) for c in RANDOM_CONV_CASES])
+def test_conv_random_geometries(eng, case):
+    """Forward, dW, db and dX against the float64 oracle on seeded random
+    geometries (with and without the forward's channel-innermost copy)."""
+    _conv_case(eng, *case, seed=23, keep=bool(case[0] % 2))
+
+
 @pytest.mark.parametrize("case", [(2, 3, 35, 35, 64, 11, 4, 2, 1), (2, 1, 12, 10, 6, 5, 1, 2, 1),
                                   (2, 2, 20, 20, 4, 6, 5, 1, 1), (2, 16, 9, 9, 8, 3, 1, 1, 1)],
                          ids=str)
