@@ -37,6 +37,22 @@ def test_matmul_alloc(eng, M, Kd, N, flags):
     assert rel_err(c, ref) <= TOL
 
 
+def _random_gemm_cases(n, seed):
+    r = rng(seed)
+    return [(int(r.integers(1, 300)), int(r.integers(1, 700)), int(r.integers(1, 300)), int(r.integers(0, 4)))
+            for _ in range(n)]
+
+
+RANDOM_GEMM_CASES = _random_gemm_cases(24, 4242)
+
+
+@pytest.mark.parametrize("M,Kd,N,flags", RANDOM_GEMM_CASES)
+def test_matmul_alloc_random_shapes(eng, M, Kd, N, flags):
+    """MatMulAlloc on seeded random shapes and transpose flags (ragged tiles,
+    padded operand copies, split-K and the small-GEMM tiles)."""
+    test_matmul_alloc(eng, M, Kd, N, flags)
+
+
 CONV_CASES = [
     # B, C, H, W, OC, k, s, p, act
     (2, 3, 9, 8, 4, 3, 1, 1, 1),
