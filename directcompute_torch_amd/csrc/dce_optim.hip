@@ -239,18 +239,23 @@ __global__ void __launch_bounds__(256) k_multi_sumsq(const Table t, double* part
 
 // norm = sqrt(Σ partials); scale = norm > max ? max/(norm + 1e-6) : 1
 // (nn_grad_norm_final.hlsl:31-34).
-// One block of 1024 threads; thread t adds partials t, t + 1024, ... (four
-// loads in flight), then a fixed shuffle / LDS tree.
+// One block of 1024 threads; thread t adds partials t, t + 1024, ... in
+// rounds of 16 loads issued together (one memory round trip per 16384
+// partials: AlexNet's 61 M parameters make about 15,000), then a fixed
+// shuffle / LDS tree.
 __global__ void __launch_bounds__(1024)
     k_norm_final(const double* part, uint32_t total, float maxNorm, float* ns) {
   __shared__ double sh[16];
   double s = 0;
-  for (uint32_t i = threadIdx.x; i < total; i += 4096) {
-    double v[4];
+  for (uint32_t i0 = 0; i0 < total; i0 += 16 * 1024) {
+    double v[16];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) v[u] = i + u * 1024 < total ? part[i + u * 1024] : 0.0;
+    for (int u = 0; u < 16; ++u) {
+      const uint32_t i = i0 + threadIdx.x + u * 1024;
+      v[u] = i < total ? part[i] : 0.0;
+    }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) s += v[u];
+    for (int u = 0; u < 16; ++u) s += v[u];
   }
   s = wave_reduce(s);
   if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = s;
