@@ -7,20 +7,25 @@
 // Workgroup: 256 threads = 4 wave64 owning an MT x NT output tile: for MT in
 // {64, 128} the waves sit 2x2, each with an (MT/2) x (NT/2) block of 16x16
 // accumulators; for the narrow tiles MT in {16, 32} (few output channels)
-// they sit 1x4, each with an MT x (NT/4) block.  K advances in tiles of KT (16 or 32) through a double
-// buffered LDS stage with one barrier per tile; the next tile's global loads
-// are in flight while the current one is multiplied.
+// they sit 1x4, each with an MT x (NT/4) block, or (KT = 64) each wave takes
+// the whole tile over its own 16-deep slice of every K tile.  K advances in
+// tiles of KT (16, 32 or 64) through a double buffered LDS stage with one
+// barrier per tile; the next tile's global loads are in flight while the
+// current one is multiplied.
 //
 // Every global load is a (predicated) 16-byte load of four consecutive
-// elements ("quad").  An operand is staged in LDS in one of two layouts:
+// elements ("quad"), into registers or straight into LDS.  An operand is
+// staged in LDS in one of two layouts:
 //   ROWK  [row][k], quads along k  (row stride KT)       -> ds_read_b128
-//   KROW  [k][row], quads along rows (k stride R + 4)    -> 4 x ds_read_b32
+//   KROW  [k][row], quads along rows                     -> 4 x ds_read_b32
 // Both feed the MFMA with the same k order: in MFMA s of a 16-wide k slice,
 // lane l (r = l % 16, g = l / 16) supplies A[r][4g + s] and B[4g + s][r], so
-// the four MFMAs together cover k 0..15 (the matrix unit sums over g).  KROW
-// rows carry a +4 pad; ROWK rows are unpadded (see Stage).  A wave with 2 or
-// 4 fragments of a KROW operand interleaves them row by row, so that one
-// ds_read_b64 / b128 per k serves all of them (Stage::frags_rif).
+// the four MFMAs together cover k 0..15 (the matrix unit sums over g).  ROWK
+// rows are unpadded with their quads XOR-swizzled by row; KROW rows at least
+// 64 wide are unpadded and swizzled by k where the loader allows it, the
+// others padded by 4 floats (see Stage).  A wave with 2 or 4 fragments of a KROW operand
+// interleaves them row by row, so that one ds_read_b64 / b128 per k serves
+// all of them (Stage::frags_rif).
 //
 // Convolutions work on channel-innermost ("NHWC", channels padded to a
 // multiple of 4) copies of their activations so that a quad is four
@@ -31,9 +36,13 @@
 // where G = dy masked by the ReLU output (y <= 0 -> 0), produced once per
 // backward by a transpose pass that also reduces the bias gradient.  No
 // im2col / col2im buffer exists; the NHWC copy of x is what ConvForwardFused
-// hands back as its "im2col" handle.
-// Split-K (blockIdx.z) writes partial tiles that a second pass sums in a
-// fixed order; nothing uses atomics, so results are deterministic.
+// hands back as its "im2col" handle.  Two layer kinds take other operands:
+// pointwise (1x1, stride 1) layers multiply the NCHW planes in place, and
+// layers with fewer than 4 input channels read a stride-phase copy of x
+// (stride-phase section below).
+// Split-K writes partial tiles (split z is the slowest index of the tile
+// numbering) that a second pass sums in a fixed order; nothing uses atomics,
+// so results are deterministic.
 #include "dce_internal.h"
 
 #include <algorithm>
