@@ -226,16 +226,13 @@ def cpu_baseline(sample=256):
 HBM_PEAK_BYTES_PER_S = HBM_PEAK_GBS * 1e9
 
 
-def memory_suite(reps=10, trials=5, pause_s=0.05):
+def memory_suite(reps=10, trials=5):
     """Backward memory-bound kernels at the shapes of the benchmark networks,
     each driven through the same dispatch the API's backward makes.  One JSON
     line per kernel: algorithmic bytes per launch (each required tensor read
     or written once), the time per launch of `reps` back-to-back launches
-    (one HIP-event pair around them; the median of `trials` such runs, each
-    after `pause_s` of idle GPU), GB/s and fraction of 8 TB/s; and the same
-    figures for `trials` runs straight after one another (`us_sustained`:
-    50 launches back to back, where a kernel that draws much power can trip
-    the GPU's clock control)."""
+    (one HIP-event pair around them; the median of `trials` such runs), GB/s
+    and fraction of 8 TB/s."""
     from directcompute_torch_amd import nn_engine as nn
     lib = nn.lib
     rng = np.random.default_rng(SEED + 7)
@@ -269,10 +266,10 @@ def memory_suite(reps=10, trials=5, pause_s=0.05):
         # calls that launch more than the kernel measured).  The median of
         # `trials` such measurements is reported (single runs vary by a few
         # percent from run to run).
-        # Each timed run starts after a pause (a kernel meets the GPU once per
-        # layer inside a training step); the sustained runs follow one
-        # another directly.
-        def one():
+        fn()
+        lib.SyncGPU()
+        per = []
+        for _ in range(trials):
             lib.ResetProfile()
             if per_launch:
                 lib.SetProfiling(1)
@@ -287,24 +284,12 @@ def memory_suite(reps=10, trials=5, pause_s=0.05):
                 lib.EndProfileRegion()
             lib.SyncGPU()
             n, ms = prof(family)
-            return ms / (max(n, 1) if per_launch else reps) * 1e3
-
-        fn()
-        lib.SyncGPU()
-        per = []
-        for _ in range(trials):
-            time.sleep(pause_s)
-            per.append(one())
-        time.sleep(pause_s)
-        sus = [one() for _ in range(trials)]
-        us, us_s = float(np.median(per)), float(np.median(sus))
+            per.append(ms / (max(n, 1) if per_launch else reps) * 1e3)
+        us = float(np.median(per))
         gbps = nbytes / (us * 1e-6) / 1e9 if us > 0 else 0.0
-        gbps_s = nbytes / (us_s * 1e-6) / 1e9 if us_s > 0 else 0.0
         rec = {"suite": "memory", "kernel": kernel, "family": family, "shape": list(shape),
                "bytes_per_launch": int(nbytes), "us": round(us, 2), "GB/s": round(gbps, 1),
-               "frac_hbm": round(gbps * 1e9 / HBM_PEAK_BYTES_PER_S, 4),
-               "us_sustained": round(us_s, 2),
-               "frac_hbm_sustained": round(gbps_s * 1e9 / HBM_PEAK_BYTES_PER_S, 4)}
+               "frac_hbm": round(gbps * 1e9 / HBM_PEAK_BYTES_PER_S, 4)}
         out.append(rec)
         print(json.dumps(rec), flush=True)
 
@@ -373,7 +358,7 @@ def memory_suite(reps=10, trials=5, pause_s=0.05):
         nx, no = B * C * H * W, B * C * OH * OW
         pidx = ctypes.c_void_p()
         held.append(lib.MaxPoolForwardFused(xin, B, C, H, W, k, st, ctypes.byref(pidx)))
-        for _ in range(2 * trials * reps + 1):
+        for _ in range(trials * reps + 1):
             lib.AddRefBuffer(pidx.value)
 
         def mp(idx=pidx.value, dz=dz, B=B, C=C, OH=OH, OW=OW, nx=nx):
@@ -447,16 +432,11 @@ def memory_suite(reps=10, trials=5, pause_s=0.05):
 
     for h in held:
         lib.ReleaseBuffer(h)
-    big = [r for r in out if r["bytes_per_launch"] >= 64 << 20]
-    fr = [r["frac_hbm"] for r in big]
-    frs = [r["frac_hbm_sustained"] for r in big]
+    fr = [r["frac_hbm"] for r in out if r["bytes_per_launch"] >= 64 << 20]
     print(json.dumps({"suite": "memory", "summary": {
         "kernels": len(out), "kernels_over_64MiB": len(fr),
         "median_frac_hbm_over_64MiB": round(float(np.median(fr)), 4) if fr else None,
-        "min_frac_hbm_over_64MiB": round(float(min(fr)), 4) if fr else None,
-        "median_frac_hbm_sustained_over_64MiB": round(float(np.median(frs)), 4) if frs else None,
-        "min_frac_hbm_sustained_over_64MiB": round(float(min(frs)), 4) if frs else None}}),
-          flush=True)
+        "min_frac_hbm_over_64MiB": round(float(min(fr)), 4) if fr else None}}), flush=True)
 
 
 def _prof_all(lib):
