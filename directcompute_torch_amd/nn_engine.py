@@ -305,6 +305,23 @@ def _new(count, what):
     return _check(_create_buffer(None, count), what)
 
 
+# Flagged GEMM into a caller's buffer.  The reference chooses its shader by
+# output size; here every flagged-GEMM name reaches the same MFMA GEMM (the
+# launch shape comes from the constants), so the choice only keeps the shader
+# names of a recorded dispatch the same.
+_MM_SMALL_TILE, _MM_LARGE_TILE, _MM_LARGE_MIN = 16, 64, 64
+
+
+def _run_mm(a_buf, b_buf, out_buf, M, K, N, flags=0):
+    """out = op(A)·op(B) into an existing buffer of M×N floats (flags bit0: A
+    stored K×M, bit1: B stored N×K), the helper the reference's matmul
+    benchmarks and verification scripts call (nn_engine.py:887-893)."""
+    large = M >= _MM_LARGE_MIN and N >= _MM_LARGE_MIN
+    t = _MM_LARGE_TILE if large else _MM_SMALL_TILE
+    _dispatch(b"matmul_dgpu" if large else b"matmul_universal", (a_buf, b_buf), (out_buf,),
+              (N + t - 1) // t, (M + t - 1) // t, 1, u1=M, u2=K, u3=N, u4=flags)
+
+
 # --------------------------------------------------------------------------
 # Ops
 # --------------------------------------------------------------------------

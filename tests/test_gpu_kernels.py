@@ -703,6 +703,21 @@ def test_im2col_col2im_reshapes(eng):
     release(eng, hx, hcol, hdx, hmm, hb, hy, hdz, hyy, hG)
 
 
+@pytest.mark.parametrize("M,Kd,N", [(5, 9, 7), (130, 67, 129), (64, 300, 64)])
+def test_run_mm(eng, M, Kd, N):
+    """nn_engine._run_mm (nn_engine.py:887-893): the flagged GEMM into a
+    caller's buffer, through the small- and large-output shader names, for
+    every transpose flag, against the float64 oracle."""
+    r = rng(M * 7 + Kd)
+    a = r.standard_normal(M * Kd).astype(np.float32)
+    b = r.standard_normal(Kd * N).astype(np.float32)
+    ha, hb, hc = upload(eng, a), upload(eng, b), new(eng, M * N)
+    for flags in range(4):
+        eng._run_mm(ha, hb, hc, M, Kd, N, flags)
+        assert rel_err(download(eng, hc, (M, N)), K.matmul(a, b, M, Kd, N, flags)) <= TOL
+    release(eng, ha, hb, hc)
+
+
 def test_run_sequence(eng):
     """RunSequence replays SeqCmd records (engine.cpp:952-966) built with ResolveShader."""
     from directcompute_torch_amd._lib import SeqCmd
