@@ -1361,3 +1361,79 @@ def drain_pool():
 def sync_gpu():
     """Block until all queued GPU work is done."""
     lib.SyncGPU()
+
+
+# --------------------------------------------------------------------------
+# Profiler
+# --------------------------------------------------------------------------
+class KernelProfiler:
+    """The reference's `profiler` object (nn_engine.py:183-306) with the same
+    calls -- install / uninstall / enable / disable / reset / report -- but
+    measured on the device: the engine brackets each kernel family's launches
+    with HIP events on its stream, so `report` shows GPU time per family (the
+    reference times the host-side ctypes calls, which on an asynchronous
+    stream measure submission).  Nothing is wrapped, so install() and
+    uninstall() have nothing to do.  The memory lines report the buffer
+    pool: bytes held for reuse and its hit / miss counts."""
+
+    # Families the engine records: the fused paths and every RunShader
+    # kernel that runs under its own name.
+    FAMILIES = ("conv_fwd", "conv_bwd", "conv_dw", "conv_dx", "gemm", "nhwc", "conv_grad_nhwc",
+                "maxpool_fwd", "maxpool_bwd", "bn_stats", "bn_fwd", "bn_bwd_reduce", "bn_bwd_dx",
+                "dw_bwd_input", "dw_bwd_filter", "gap_bwd", "upsample_bwd", "bias_grad",
+                "dice_loss_grad", "sgd", "sgd_clipped", "adam", "grad_norm", "clip_scale",
+                "relu", "relu_grad", "relu6", "relu6_grad", "leaky_relu", "leaky_relu_grad",
+                "sigmoid", "sigmoid_grad", "add", "scale_add", "grad_accum")
+
+    def __init__(self):
+        self.enabled = False
+
+    def install(self):
+        pass
+
+    def uninstall(self):
+        pass
+
+    def enable(self):
+        self.enabled = True
+        lib.SetProfiling(1)
+        self.reset()
+
+    def disable(self):
+        self.enabled = False
+        lib.SetProfiling(0)
+
+    def reset(self):
+        lib.ResetProfile()
+        lib.ResetPoolStats()
+
+    def stats(self):
+        """{family: (launches, total ms)} recorded since the last reset."""
+        lib.SyncGPU()
+        out = {}
+        n, ms = ctypes.c_uint64(), ctypes.c_double()
+        fl, by = ctypes.c_double(), ctypes.c_double()
+        for f in self.FAMILIES:
+            if lib.GetProfile(f.encode(), ctypes.byref(n), ctypes.byref(ms), ctypes.byref(fl),
+                              ctypes.byref(by)) and n.value:
+                out[f] = (int(n.value), float(ms.value))
+        return out
+
+    def report(self, epoch_label=""):
+        if not self.enabled:
+            return
+        st = self.stats()
+        total = sum(ms for _, ms in st.values())
+        calls = sum(c for c, _ in st.values())
+        bar = "=" * 80
+        print(f"\n{bar}\n  GPU kernel time {epoch_label}\n{bar}")
+        print(f"  {'Family':<28} {'Calls':>6} {'Total ms':>10} {'Avg ms':>10} {'% Time':>8}")
+        for f, (c, ms) in sorted(st.items(), key=lambda kv: -kv[1][1]):
+            print(f"  {f:<28} {c:>6} {ms:>10.3f} {ms / c:>10.4f} {100.0 * ms / total if total else 0.0:>7.1f}%")
+        print(f"  {'TOTAL':<28} {calls:>6} {total:>10.3f}")
+        hits, misses = get_pool_stats()
+        print(f"\n  Pool held:  {get_pool_memory() / 1024 / 1024:>8.2f} MB  "
+              f"(requests: {hits} reused, {misses} allocated)\n{bar}\n")
+
+
+profiler = KernelProfiler()

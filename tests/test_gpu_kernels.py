@@ -718,6 +718,31 @@ def test_run_mm(eng, M, Kd, N):
     release(eng, ha, hb, hc)
 
 
+def test_profiler_device_time(eng, capsys):
+    """nn_engine.profiler keeps the reference's profiler calls
+    (nn_engine.py:183-306: install, enable, report, reset, disable,
+    uninstall) and reports each kernel family's launches and GPU time."""
+    n = 4096
+    r = rng(77)
+    hg, hx, ho = upload(eng, r.standard_normal(n).astype(np.float32)), \
+        upload(eng, r.standard_normal(n).astype(np.float32)), new(eng, n)
+    p = eng.profiler
+    p.install()
+    p.enable()
+    for _ in range(3):
+        run(eng, "relu_grad", [hg, hx], [ho], n)
+    st = p.stats()
+    assert st["relu_grad"][0] == 3 and st["relu_grad"][1] > 0
+    p.report("test")
+    out = capsys.readouterr().out
+    assert "relu_grad" in out and "TOTAL" in out
+    p.reset()
+    assert "relu_grad" not in p.stats()
+    p.disable()
+    p.uninstall()
+    release(eng, hg, hx, ho)
+
+
 def test_run_sequence(eng):
     """RunSequence replays SeqCmd records (engine.cpp:952-966) built with ResolveShader."""
     from directcompute_torch_amd._lib import SeqCmd
