@@ -720,7 +720,9 @@ static bool conv_geom(const char* what, uint32_t B, uint32_t C, uint32_t H, uint
   g->OH = (H + 2 * p - kH) / s + 1;
   g->OW = (W + 2 * p - kW) / s + 1;
   uint64_t xs = uint64_t(B) * C * H * W, ys = uint64_t(B) * OC * g->OH * g->OW;
-  if (xs >= (1ull << 31) || ys >= (1ull << 31)) {
+  // The filters too: the callers' 32-bit buffer-size checks rely on it.
+  uint64_t ws = uint64_t(OC) * C * kH * kW;
+  if (xs >= (1ull << 31) || ys >= (1ull << 31) || ws >= (1ull << 31)) {
     set_error("%s: tensor too large for 31-bit indexing", what);
     return false;
   }
@@ -882,8 +884,11 @@ void* MaxPoolBackwardFused(void* gradOut, void* indices, uint32_t batch, uint32_
   Buffer* DZ = as_buffer(gradOut, "MaxPoolBackwardFused(grad)");
   Buffer* I = DZ ? as_buffer(indices, "MaxPoolBackwardFused(indices)") : nullptr;
   void* dx = nullptr;
-  uint32_t n = batch * inC * outH * outW;
-  if (I && (DZ->count < n || I->count < n)) {
+  const uint64_t n64 = uint64_t(batch) * inC * outH * outW;
+  const uint32_t n = uint32_t(n64);
+  if (I && n64 >= (1ull << 31)) {
+    set_error("MaxPoolBackwardFused: tensor too large for 31-bit indexing");
+  } else if (I && (DZ->count < n || I->count < n)) {
     set_error("MaxPoolBackwardFused: buffer smaller than geometry");
   } else if (I) {
     dx = create_buffer(nullptr, xSize);

@@ -2230,7 +2230,7 @@ static DwBand dw_band_filter(const DwGeom& g) {
 
 static bool dw_ok(const DwGeom& g, const char* what) {
   if (!g.B || !g.C || !g.H || !g.W || !g.kH || !g.kW || !g.s || !g.OH || !g.OW) return false;
-  if (uint64_t(g.B) * g.C * std::max(g.H * g.W, g.OH * g.OW) >= (1ull << 31)) {
+  if (uint64_t(g.B) * g.C * std::max(uint64_t(g.H) * g.W, uint64_t(g.OH) * g.OW) >= (1ull << 31)) {
     set_error("%s: tensor too large", what);
     return false;
   }

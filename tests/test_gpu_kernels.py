@@ -98,6 +98,41 @@ def test_gpu_info(eng):
     assert b"gfx950" in info.description
 
 
+def test_fused_calls_reject_bad_geometry(eng):
+    """The fused entry points return NULL, and leave the reason in
+    GetLastErrorString, for buffers smaller than their geometry, invalid
+    geometry, and sizes past 31-bit indexing (the filters' included), so no
+    kernel runs over memory the buffers do not hold."""
+    lib = eng.lib
+    small = new(eng, 16)
+    w, b = new(eng, 8 * 4 * 3 * 3), new(eng, 8)
+
+    def rejected(h, what):
+        assert not h
+        err = eng.last_error()
+        assert what in err, err
+        lib.ClearLastError()
+
+    rejected(lib.ConvForwardFused(small, w, b, 2, 4, 8, 8, 8, 3, 3, 1, 1, 0, None), "smaller")
+    rejected(lib.ConvForwardFused(small, w, b, 1, 4, 2, 2, 8, 5, 5, 1, 0, 0, None), "invalid geometry")
+    # 65536 x 65536 1x1 filters on a 1x1 image: activations fit, the filters do not.
+    rejected(lib.ConvForwardFused(small, small, small, 1, 65536, 1, 1, 65536, 1, 1, 1, 0, 0, None),
+             "too large")
+    pdf, pdb, pdx = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+    lib.ConvBackwardFused(small, None, small, w, None, 2, 4, 8, 8, 8, 3, 3, 1, 1, 0, 1, 1, 1,
+                          ctypes.byref(pdf), ctypes.byref(pdb), ctypes.byref(pdx))
+    assert not (pdf.value or pdb.value or pdx.value)
+    rejected(None, "smaller")
+    rejected(lib.MatMulAlloc(small, small, 64, 64, 64, 0), "smaller")
+    pidx = ctypes.c_void_p()
+    rejected(lib.MaxPoolForwardFused(small, 2, 4, 8, 8, 2, 2, ctypes.byref(pidx)), "does not match")
+    assert not pidx.value
+    # MaxPoolBackwardFused consumes its index handle, error or not.
+    rejected(lib.MaxPoolBackwardFused(small, new(eng, 16), 65536, 65536, 1, 1, 16), "too large")
+    rejected(lib.MaxPoolBackwardFused(small, new(eng, 16), 2, 4, 4, 4, 64), "smaller")
+    release(eng, small, w, b)
+
+
 def test_unknown_shader_is_noop_with_error(eng):
     h = upload(eng, np.ones(4, np.float32))
     eng.lib.ClearLastError()
