@@ -450,6 +450,59 @@ def test_depthwise(eng, B, C, H, W, k, s, p, policy):
     release(eng, hx, hf, hb, hdy, hy, hdx, hdf, hdb)
 
 
+def _random_dw_cases(n, seed):
+    """Seeded depthwise geometries: K in {3, 5}, stride 1 or 2, every padding
+    below K, odd and even plane sizes from K to 69, 1-39 channels."""
+    r = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        k, s = int(r.choice([3, 5])), int(r.choice([1, 2]))
+        p = int(r.integers(0, k))
+        H, W = int(r.integers(k, 70)), int(r.integers(k, 70))
+        out.append((int(r.integers(1, 4)), int(r.integers(1, 40)), H, W, k, s, p))
+    return out
+
+
+DW_RANDOM = _random_dw_cases(24, 2718)
+
+
+@pytest.mark.parametrize("case", DW_RANDOM, ids=["x".join(map(str, c)) for c in DW_RANDOM])
+def test_depthwise_random_geometries(eng, case):
+    """Depthwise forward, dX, dW and db on seeded random geometries (band and
+    generic kernels, quad and dword windows) against the float64 oracle."""
+    test_depthwise(eng, *case, policy="cached")
+
+
+def _random_pool_cases(n, seed):
+    r = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        k, s = int(r.choice([2, 3])), int(r.choice([1, 2, 3]))
+        out.append((int(r.integers(1, 4)), int(r.integers(1, 20)), int(r.integers(k, 60)),
+                    int(r.integers(k, 60)), k, s))
+    return out
+
+
+POOL_RANDOM = _random_pool_cases(16, 1618)
+
+
+@pytest.mark.parametrize("case", POOL_RANDOM, ids=["x".join(map(str, c)) for c in POOL_RANDOM])
+def test_maxpool_random_geometries(eng, case):
+    """Fused max-pool forward (values, indices) and backward routing on seeded
+    random geometries, overlapping and gapped windows included."""
+    test_maxpool_fused(eng, *case)
+
+
+BN_RANDOM = [tuple(int(v) for v in np.random.default_rng(1414 + i).integers([1, 1, 1, 1], [9, 48, 40, 40]))
+             for i in range(12)]
+
+
+@pytest.mark.parametrize("case", BN_RANDOM, ids=["x".join(map(str, c)) for c in BN_RANDOM])
+def test_batchnorm_random_shapes(eng, case):
+    """BatchNorm statistics, forward and backward on seeded random shapes."""
+    test_batchnorm(eng, *case, policy="cached")
+
+
 # ------------------------------------- MobileNetV2 b64 @112^2 at full size
 @pytest.mark.parametrize("B,C,H,W,s", [(64, 96, 112, 112, 2), (64, 144, 56, 56, 1), (64, 192, 28, 28, 1)])
 def test_mobilenet_b64_block_full_size_sampled(eng, B, C, H, W, s):
