@@ -694,6 +694,53 @@ def test_adam_batch_and_shader(eng, wd, clip, policy):
     release(eng, *hw, *hg, *hm, *hv, w2, m2, v2)
 
 
+def _ragged_sizes(seed, count):
+    """Seeded tensor sizes for the multi-tensor kernels: 1 to 20000
+    elements, with exact multiples of the 4096-element chunk mixed in;
+    more tensors than one launch table holds (48) when count > 48."""
+    r = np.random.default_rng(seed)
+    sizes = [int(v) for v in r.integers(1, 20000, count)]
+    for i in range(0, count, 7):
+        sizes[i] = 4096 * int(r.integers(1, 4))
+    return sizes
+
+
+@pytest.mark.parametrize("seed,count", [(11, 5), (12, 47), (13, 49), (14, 101)])
+def test_optimisers_ragged_tensor_lists(eng, seed, count):
+    """SGDBatch, AdamBatch and ClipGradNorm over seeded ragged tensor lists,
+    across launch-table boundaries, against the float64 oracle."""
+    sizes = _ragged_sizes(seed, count)
+    sa = (ctypes.c_uint * count)(*sizes)
+    ws, gs = _param_set(seed, sizes)
+    hw, hg = [upload(eng, w) for w in ws], [upload(eng, g) for g in gs]
+    eng.lib.SGDBatch(_arrays(hw), _arrays(hg), sa, count, 0.05, 1.0)
+    for h, w, g in zip(hw, ws, gs):
+        assert rel_err(download(eng, h, w.shape), K.sgd(w, g, 0.05, 1.0)) <= 1e-6
+    release(eng, *hw)
+    r = rng(seed + 100)
+    ws = [r.standard_normal(n).astype(np.float32) for n in sizes]
+    ms = [(0.1 * r.standard_normal(n)).astype(np.float32) for n in sizes]
+    vs = [(0.1 * r.random(n)).astype(np.float32) for n in sizes]
+    lr, b1, b2, eps, wd, clip, t = 1e-3, 0.9, 0.999, 1e-8, 0.01, 1.0, 2
+    step = K.adam_step_size(lr, b1, b2, t)
+    f32 = lambda v: float(np.float32(v))
+    hw, hm, hv = ([upload(eng, a) for a in arrs] for arrs in (ws, ms, vs))
+    eng.lib.AdamBatch(_arrays(hw), _arrays(hg), _arrays(hm), _arrays(hv), sa, count, step, b1, b2,
+                      eps, lr * wd, clip)
+    for i in range(count):
+        w_r, m_r, v_r = K.adam(ws[i], gs[i], ms[i], vs[i], f32(step), f32(b1), f32(b2), f32(eps),
+                               f32(lr * wd), clip)
+        assert rel_err(download(eng, hw[i], ws[i].shape), w_r) <= 1e-6
+        assert rel_err(download(eng, hm[i], ms[i].shape), m_r) <= 1e-6
+        assert rel_err(download(eng, hv[i], vs[i].shape), v_r) <= 1e-6
+    norm = eng.lib.ClipGradNorm(_arrays(hg), sa, count, 1.0)
+    n_ref, scale = K.grad_norm_scale(gs, 1.0)
+    assert abs(norm - n_ref) <= 1e-5 * n_ref
+    for h, g in zip(hg, gs):
+        assert rel_err(download(eng, h, g.shape), g.astype(np.float64) * scale) <= 1e-6
+    release(eng, *hw, *hg, *hm, *hv)
+
+
 def test_adam_batch_counted(eng, policy):
     """AdamBatchCounted keeps t and the step size on the device: t > 0 sets
     the counter, t == 0 advances it.  The step size equals the float32 of the
