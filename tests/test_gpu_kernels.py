@@ -155,7 +155,8 @@ BINARY = [
 ]
 
 
-@pytest.mark.parametrize("n", [1, 5, 1024, 1000003])
+@pytest.mark.parametrize("n", [1, 5, 1024, 1000003] +
+                         [int(v) for v in np.random.default_rng(919).integers(2, 300000, 4)])
 def test_activations(eng, n, policy):
     r = rng(n)
     x = (4 * r.standard_normal(n)).astype(np.float32)
@@ -373,7 +374,9 @@ def test_batchnorm(eng, N, C, H, W, policy):
 
 
 # --------------------------------------------------- pooling / resampling
-@pytest.mark.parametrize("B,C,H,W", [(2, 3, 7, 7), (8, 64, 8, 8), (1, 1, 1, 1)])
+@pytest.mark.parametrize("B,C,H,W", [(2, 3, 7, 7), (8, 64, 8, 8), (1, 1, 1, 1)] +
+                         [tuple(int(v) for v in np.random.default_rng(717 + i).integers([1, 1, 1, 1], [9, 70, 40, 40]))
+                          for i in range(6)])
 def test_global_avg_pool(eng, B, C, H, W, policy):
     x = rng(B + C).standard_normal((B, C, H, W)).astype(np.float32)
     g = rng(7).standard_normal((B, C)).astype(np.float32)
@@ -385,7 +388,10 @@ def test_global_avg_pool(eng, B, C, H, W, policy):
     release(eng, hx, ho, hg, hdx)
 
 
-@pytest.mark.parametrize("B,C,H,W,sH,sW", [(2, 3, 4, 5, 2, 2), (1, 16, 32, 32, 2, 2), (2, 2, 3, 3, 3, 2)])
+@pytest.mark.parametrize("B,C,H,W,sH,sW", [(2, 3, 4, 5, 2, 2), (1, 16, 32, 32, 2, 2), (2, 2, 3, 3, 3, 2)] +
+                         [tuple(int(v) for v in np.random.default_rng(818 + i).integers([1, 1, 1, 1, 1, 1],
+                                                                                        [5, 20, 40, 40, 4, 4]))
+                          for i in range(6)])
 def test_upsample(eng, B, C, H, W, sH, sW, policy):
     x = rng(H * W).standard_normal((B, C, H, W)).astype(np.float32)
     OH, OW = H * sH, W * sW
@@ -568,7 +574,11 @@ def test_mobilenet_b64_block_full_size_sampled(eng, B, C, H, W, s):
 
 
 # ------------------------------------------------------------ loss / metrics
-@pytest.mark.parametrize("B,Kc", [(1, 2), (64, 10), (128, 1000), (300, 7)])
+SOFTMAX_RANDOM = [tuple(int(v) for v in np.random.default_rng(515 + i).integers([1, 2], [260, 3000]))
+                  for i in range(8)]   # seeded: class counts past the 1024-class register rows too
+
+
+@pytest.mark.parametrize("B,Kc", [(1, 2), (64, 10), (128, 1000), (300, 7)] + SOFTMAX_RANDOM)
 def test_softmax_ce(eng, B, Kc):
     r = rng(B * Kc)
     z = (3 * r.standard_normal((B, Kc))).astype(np.float32)
@@ -596,7 +606,9 @@ def test_softmax_ce(eng, B, Kc):
     release(eng, hz, hl, hp, hloss, hg, hc, hz2, acc)
 
 
-@pytest.mark.parametrize("B,C,H,W", [(2, 1, 16, 16), (8, 1, 64, 64), (3, 2, 5, 7), (8, 1, 256, 256)])
+@pytest.mark.parametrize("B,C,H,W", [(2, 1, 16, 16), (8, 1, 64, 64), (3, 2, 5, 7), (8, 1, 256, 256)] +
+                         [tuple(int(v) for v in np.random.default_rng(616 + i).integers([1, 1, 1, 1], [9, 3, 90, 90]))
+                          for i in range(6)])
 def test_dice(eng, B, C, H, W):
     r = rng(B * H)
     p = r.random((B, C, H, W)).astype(np.float32)
