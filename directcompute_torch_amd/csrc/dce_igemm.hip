@@ -1519,23 +1519,40 @@ __global__ void k_splitk_sum(const float* __restrict__ part, float* __restrict__
 }
 
 // Quad form of k_splitk_sum for n % 4 == 0 (same summation order).
-__global__ void __launch_bounds__(256)
-    k_splitk_sum4(const f4* __restrict__ part, f4* __restrict__ out, uint32_t nq,
-                  uint32_t splits) {
-  const uint32_t q = blockIdx.x * 256 + threadIdx.x;
-  if (q >= nq) return;
+// Sum of the split partials p[0], p[zs], p[2 zs], ... in split order; the
+// loads of each group of up to four are issued before its adds (the finishes
+// run at 2 - 3 splits, which a one-at-a-time loop would serialise).
+__device__ __forceinline__ f4 sum_splits4(const f4* __restrict__ p, size_t zs, uint32_t splits) {
   f4 s = {0.f, 0.f, 0.f, 0.f};
   uint32_t z = 0;
   for (; z + 3 < splits; z += 4) {
-    const f4 a = part[size_t(z) * nq + q], b = part[size_t(z + 1) * nq + q];
-    const f4 c = part[size_t(z + 2) * nq + q], d = part[size_t(z + 3) * nq + q];
+    const f4 a = p[z * zs], b = p[(z + 1) * zs], c = p[(z + 2) * zs], d = p[(z + 3) * zs];
     s += a;
     s += b;
     s += c;
     s += d;
   }
-  for (; z < splits; ++z) s += part[size_t(z) * nq + q];
-  out[q] = s;
+  const uint32_t rem = splits - z;  // uniform across the grid
+  if (rem == 3) {
+    const f4 a = p[z * zs], b = p[(z + 1) * zs], c = p[(z + 2) * zs];
+    s += a;
+    s += b;
+    s += c;
+  } else if (rem == 2) {
+    const f4 a = p[z * zs], b = p[(z + 1) * zs];
+    s += a;
+    s += b;
+  } else if (rem == 1) {
+    s += p[z * zs];
+  }
+  return s;
+}
+__global__ void __launch_bounds__(256)
+    k_splitk_sum4(const f4* __restrict__ part, f4* __restrict__ out, uint32_t nq,
+                  uint32_t splits) {
+  const uint32_t q = blockIdx.x * 256 + threadIdx.x;
+  if (q >= nq) return;
+  out[q] = sum_splits4(part + q, nq, splits);
 }
 
 // dW finalize: dw[oc][c][khw] = sum_z part[z][oc][khw*Cp + c], or with
@@ -1683,18 +1700,7 @@ __global__ void __launch_bounds__(256)
   const uint32_t q = blockIdx.x * 256 + threadIdx.x;
   const uint32_t nq = M * (N / 4);
   if (q >= nq) return;
-  const size_t zs = nq;
-  f4 s = {0.f, 0.f, 0.f, 0.f};
-  uint32_t z = 0;
-  for (; z + 3 < splits; z += 4) {
-    const f4 a = part[z * zs + q], b = part[(z + 1) * zs + q];
-    const f4 c = part[(z + 2) * zs + q], d = part[(z + 3) * zs + q];
-    s += a;
-    s += b;
-    s += c;
-    s += d;
-  }
-  for (; z < splits; ++z) s += part[z * zs + q];
+  f4 s = sum_splits4(part + q, nq, splits);
   const uint32_t m = (4 * q) / N, n0 = 4 * q - m * N;
   uint32_t b = n0 / HW, pix = n0 - b * HW;
 #pragma unroll
