@@ -168,6 +168,38 @@ def test_conv_random_geometries(eng, case):
     _conv_case(eng, *case, seed=23, keep=bool(case[0] % 2))
 
 
+def _random_special_cases(n, seed, pointwise):
+    """Seeded geometries of the two special layouts: inputs of 1-3 channels
+    (stride-phase copy for strides up to 4, channel-packed above) with
+    kernels up to 11, or pointwise 1x1 stride-1 layers on NCHW planes."""
+    r = rng(seed)
+    out = []
+    while len(out) < n:
+        if pointwise:
+            k, s, p, C = 1, 1, 0, int(r.integers(1, 65))
+            H, W = int(r.integers(1, 31)), int(r.integers(1, 31))
+        else:
+            k, s = int(r.integers(1, 12)), int(r.integers(1, 6))
+            p, C = int(r.integers(0, k)), int(r.integers(1, 4))
+            H, W = int(r.integers(k, 40)), int(r.integers(k, 40))
+        if (H + 2 * p - k) // s + 1 < 1 or (W + 2 * p - k) // s + 1 < 1:
+            continue
+        out.append((int(r.integers(1, 4)), C, H, W, int(r.integers(1, 97)), k, s, p,
+                    int(r.integers(0, 3))))
+    return out
+
+
+SPECIAL_CASES = _random_special_cases(16, 4242, False) + _random_special_cases(16, 2424, True)
+
+
+@pytest.mark.parametrize("case", SPECIAL_CASES, ids=[str(c) for c in SPECIAL_CASES])
+def test_conv_random_special_layouts(eng, case):
+    """The stride-phase / channel-packed (C < 4) and pointwise layouts on
+    seeded random geometries: forward, dW, db and dX against the float64
+    oracle."""
+    _conv_case(eng, *case, seed=29, keep=bool(case[1] % 2))
+
+
 @pytest.mark.parametrize("case", [(2, 3, 35, 35, 64, 11, 4, 2, 1), (2, 1, 12, 10, 6, 5, 1, 2, 1),
                                   (2, 2, 20, 20, 4, 6, 5, 1, 1), (2, 16, 9, 9, 8, 3, 1, 1, 1)],
                          ids=str)
