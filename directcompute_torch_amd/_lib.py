@@ -126,7 +126,7 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.ClipGradNorm.restype = c_float
     lib.ClipGradNormNoAlloc.argtypes = [P(c_void_p), P(c_uint), c_uint, c_float]
     lib.ClipGradNormNoAlloc.restype = c_float
-    lib.AdamBatchCounted.argtypes = ([P(c_void_p)] * 4 + [P(c_uint), c_uint, c_void_p, c_uint]
+    lib.AdamBatchCounted.argtypes = ([P(c_void_p)] * 4 + [P(c_uint), c_uint, c_void_p, c_uint, c_float]
                                      + [ctypes.c_double] * 3 + [c_float] * 3)
     lib.AdamBatchCounted.restype = None
     lib.SetProfiling.argtypes = [ctypes.c_int]

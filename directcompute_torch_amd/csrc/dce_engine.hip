@@ -952,8 +952,8 @@ float ClipGradNorm(void** grads, uint32_t* sizes, uint32_t numGrads, float maxNo
 }
 
 void AdamBatchCounted(void** params, void** grads, void** m, void** v, uint32_t* sizes,
-                      uint32_t numParams, void* stepState, uint32_t t, double lr, double beta1,
-                      double beta2, float eps, float weightDecay, float clip) {
+                      uint32_t numParams, void* stepState, uint32_t t, float stepSize, double lr,
+                      double beta1, double beta2, float eps, float weightDecay, float clip) {
   if (!g_init || !params || !grads || !m || !v || !sizes || !numParams) return;
   Buffer* st = as_buffer(stepState, "AdamBatchCounted(stepState)");
   if (!st) return;
@@ -961,8 +961,8 @@ void AdamBatchCounted(void** params, void** grads, void** m, void** v, uint32_t*
     set_error("AdamBatchCounted: the step state buffer needs 2 floats (has %u)", st->count);
     return;
   }
-  adam_counted_multi(params, grads, m, v, sizes, numParams, st->ptr, t, lr, beta1, beta2, eps,
-                     weightDecay, clip);
+  adam_counted_multi(params, grads, m, v, sizes, numParams, st->ptr, t, stepSize, lr, beta1,
+                     beta2, eps, weightDecay, clip);
 }
 
 float ClipGradNormNoAlloc(void** grads, uint32_t* sizes, uint32_t numGrads, float maxNorm) {

@@ -369,10 +369,12 @@ bool scale_grads_multi(void** grads, const uint32_t* sizes, uint32_t n,
 bool adam_multi(void** params, void** grads, void** m, void** v, const uint32_t* sizes,
                 uint32_t n, float step, float b1, float b2, float eps, float wd, float clip);
 // Adam with the step counter and step size in device memory state[0..1]
-// (t_set > 0: set the counter to t_set; 0: advance it by one).
+// (t_set > 0: set the counter to t_set and the step size to step_host; 0:
+// advance the counter by one and evaluate the step size on the device).
 bool adam_counted_multi(void** params, void** grads, void** m, void** v,
                         const uint32_t* sizes, uint32_t n, float* state, uint32_t t_set,
-                        double lr, double b1, double b2, float eps, float wd, float clip);
+                        float step_host, double lr, double b1, double b2, float eps, float wd,
+                        float clip);
 // Static-scratch norm clip (no allocation): noalloc_setup records the scratch
 // array's address on `device` (which must be current); clip_grad_norm_noalloc
 // returns the norm, NaN while capturing, or -1 with the error set.

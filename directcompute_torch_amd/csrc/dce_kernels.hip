@@ -1230,7 +1230,8 @@ __global__ void __launch_bounds__(256)
 }
 
 // Fallback when the pooling geometry is unknown (indices this library did
-// not produce): one thread per (b, c) plane adds the plane's dZ values to
+// not produce), for planes too large for k_maxpool_bwd_plane_lds below: one
+// thread per (b, c) plane adds the plane's dZ values to
 // dX[idx] in output order, after dX was cleared.  Every input then sums its
 // windows in (oh, ow) order, as the gather kernels do, with no atomics.  An
 // index outside its own plane cannot come from a pooling window; it is
@@ -1246,6 +1247,59 @@ __global__ void k_maxpool_bwd_planes(const float* __restrict__ dz, const uint32_
     const uint32_t t = idx[o];
     if (t >= lo && t < hi) dx[t] += dz[o];
   }
+}
+
+// The same per-plane sum with one workgroup per plane and the plane's
+// inputs accumulated in LDS (planes of at most kPlaneLds inputs).  The plane's
+// outputs are taken 256 at a time, in output order; in each round the first
+// lane of a target sums the round's contributions to that target in lane
+// order onto the running value, so every input still adds its windows one by
+// one in output order (((0 + a) + b) + c: the per-thread kernel's rounding),
+// and each input is written once, with no clearing pass.  kPlaneLds keeps the
+// dynamic LDS plus the two 1 KiB round arrays under 64 KiB.
+constexpr uint32_t kPlaneLds = 14336;
+__global__ void __launch_bounds__(256) k_maxpool_bwd_plane_lds(const float* __restrict__ dz,
+                                                               const uint32_t* __restrict__ idx,
+                                                               float* __restrict__ dx,
+                                                               uint32_t outPer, uint32_t inPer) {
+  extern __shared__ float acc[];
+  __shared__ uint32_t tg[256];
+  __shared__ float dv[256];
+  const uint32_t tid = threadIdx.x;
+  const uint64_t lo = uint64_t(blockIdx.x) * inPer;
+  const uint64_t o0 = uint64_t(blockIdx.x) * outPer;
+  for (uint32_t i = tid; i < inPer; i += 256) acc[i] = 0.f;
+  for (uint32_t base = 0; base < outPer; base += 256) {
+    const uint32_t j = base + tid;
+    uint32_t t = 0xFFFFFFFFu;
+    float v = 0.f;
+    if (j < outPer) {
+      const uint32_t g = idx[o0 + j];
+      if (g >= lo && uint64_t(g) < lo + inPer) {
+        t = uint32_t(g - lo);
+        v = dz[o0 + j];
+      }
+    }
+    tg[tid] = t;
+    dv[tid] = v;
+    __syncthreads();   // also orders the clear (first round) and the previous round's adds
+    if (t != 0xFFFFFFFFu) {
+      bool first = true;
+      for (uint32_t l = 0; l < tid; ++l)
+        if (tg[l] == t) {
+          first = false;
+          break;
+        }
+      if (first) {
+        float a = acc[t];
+        for (uint32_t l = tid; l < 256; ++l)
+          if (tg[l] == t) a += dv[l];
+        acc[t] = a;
+      }
+    }
+    __syncthreads();
+  }
+  for (uint32_t i = tid; i < inPer; i += 256) dx[lo + i] = acc[i];
 }
 
 bool maxpool_backward(const float* dz, const float* idx, float* dx, uint32_t B, uint32_t C,
@@ -1302,10 +1356,16 @@ bool maxpool_backward(const float* dz, const float* idx, float* dx, uint32_t B, 
               "is not a multiple of batch*channels = %u", xcount, planes);
     return false;
   }
+  const uint32_t inPer = xcount / planes;
+  if (n == 0) return fill_zero(dx, xcount);
+  if (inPer <= kPlaneLds) {
+    hipLaunchKernelGGL(k_maxpool_bwd_plane_lds, dim3(planes), dim3(256), inPer * sizeof(float),
+                       stream(), dz, ip, dx, OH * OW, inPer);
+    return check_launch("maxpool_backward");
+  }
   if (!fill_zero(dx, xcount)) return false;
-  if (n == 0) return true;
   hipLaunchKernelGGL(k_maxpool_bwd_planes, dim3(cdiv(planes, 64)), dim3(64), 0, stream(), dz, ip,
-                     dx, planes, OH * OW, xcount / planes);
+                     dx, planes, OH * OW, inPer);
   return check_launch("maxpool_backward");
 }
 
@@ -2518,6 +2578,151 @@ __global__ void k_gemm_checked(Buf A, Buf B, Buf C, uint32_t M, uint32_t K, uint
   }
   st(C, i, s);
 }
+// ===========================================================================
+// Direct valid convolutions (stride 1, no padding, square kernel ks):
+// conv_forward_tiled, conv_backprop_filters_tiled, conv_backprop_input_fused.
+// All three share the constants {batch, inC, inH, inW, outC, ks, outH, outW,
+// act}.  When outH = inH - ks + 1, outW = inW - ks + 1 and every buffer holds
+// its geometry they run on the implicit-GEMM core (conv_forward /
+// conv_backward); otherwise on the checked kernels below, which follow the
+// shaders' flat index arithmetic (32-bit, wrapping) with the D3D11 rule of
+// reads past a buffer returning 0 and writes past it dropped.
+// ===========================================================================
+struct TiledGeom {
+  uint32_t B, C, H, W, OC, k, OH, OW;
+};
+static TiledGeom tiled_geom(const Dispatch& d) {
+  return TiledGeom{CU(d, 0), CU(d, 1), CU(d, 2), CU(d, 3), CU(d, 4), CU(d, 5), CU(d, 6), CU(d, 7)};
+}
+static bool tiled_valid(const TiledGeom& g) {
+  return g.k && g.H >= g.k && g.W >= g.k && g.OH == g.H - g.k + 1 && g.OW == g.W - g.k + 1 &&
+         g.B && g.C && g.OC;
+}
+static ConvGeom tiled_conv(const TiledGeom& g) {
+  return ConvGeom{g.B, g.C, g.H, g.W, g.OC, g.k, 1, 0, g.OH, g.OW};
+}
+__device__ __forceinline__ float tiled_act(float z, uint32_t act) {
+  if (act == 1) return fmaxf(0.f, z);
+  if (act == 2) return tanhf(z);
+  return z;
+}
+// nn_conv_forward_tiled.hlsl:22-71: out[b, oc, pix] = act(Σ_k F[oc, k]·X(k, b, pix) + bias[oc]).
+__global__ void k_conv_tiled_fwd_checked(Buf x, Buf f, Buf bias, Buf out, TiledGeom g,
+                                         uint32_t act) {
+  const uint32_t N = g.B * g.OH * g.OW, K = g.C * g.k * g.k;
+  const uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= uint64_t(N) * g.OC) return;
+  const uint32_t row = uint32_t(i / N), col = uint32_t(i - uint64_t(row) * N);
+  const uint32_t b = col / (g.OH * g.OW), pix = col % (g.OH * g.OW), oh = pix / g.OW,
+                 ow = pix % g.OW;
+  float acc = 0.f;
+  for (uint32_t t = 0; t < K; ++t) {
+    const uint32_t ic = t / (g.k * g.k), kk = t % (g.k * g.k), kh = kk / g.k, kw = kk % g.k;
+    acc += ld(f, row * K + t) *
+           ld(x, b * (g.C * g.H * g.W) + ic * (g.H * g.W) + (oh + kh) * g.W + (ow + kw));
+  }
+  st(out, b * (g.OC * g.OH * g.OW) + row * (g.OH * g.OW) + pix, tiled_act(acc + ld(bias, row), act));
+}
+// nn_conv_backprop_filters_tiled.hlsl:21-74: dF[oc, t] = Σ_{b, pix} dZ[b, oc, pix]·X(t, b, pix).
+__global__ void k_conv_tiled_dw_checked(Buf dz, Buf x, Buf df, TiledGeom g) {
+  const uint32_t N = g.B * g.OH * g.OW, tr = g.C * g.k * g.k;
+  const uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= uint64_t(tr) * g.OC) return;
+  const uint32_t row = uint32_t(i / tr), col = uint32_t(i - uint64_t(row) * tr);
+  const uint32_t ic = col / (g.k * g.k), kk = col % (g.k * g.k), kh = kk / g.k, kw = kk % g.k;
+  float acc = 0.f;
+  for (uint32_t t = 0; t < N; ++t) {
+    const uint32_t b = t / (g.OH * g.OW), pix = t % (g.OH * g.OW), oh = pix / g.OW,
+                   ow = pix % g.OW;
+    acc += ld(dz, b * (g.OC * g.OH * g.OW) + row * (g.OH * g.OW) + pix) *
+           ld(x, b * (g.C * g.H * g.W) + ic * (g.H * g.W) + (oh + kh) * g.W + (ow + kw));
+  }
+  st(df, row * tr + col, acc);
+}
+// The derivative factor of nn_conv_backprop_input_fused.hlsl:45-49, from the
+// previous layer's activation output a: ReLU 1 or 0, tanh 1 - a², else 1.
+struct OpPrevActGrad {
+  uint32_t act;
+  __device__ float operator()(float g, float a) const {
+    float dA = 1.0f;
+    if (act == 1) dA = a > 0.f ? 1.0f : 0.0f;
+    else if (act == 2) dA = 1.0f - a * a;
+    return g * dA;
+  }
+};
+// nn_conv_backprop_input_fused.hlsl:19-50, one thread per input element.
+__global__ void k_conv_tiled_dx_checked(Buf dz, Buf f, Buf aprev, Buf dx, TiledGeom g,
+                                        uint32_t act) {
+  const uint32_t total = g.B * g.C * g.H * g.W;
+  const uint32_t i = gtid();
+  if (i >= total) return;
+  const uint32_t iw = i % g.W, ih = (i / g.W) % g.H, ic = (i / (g.W * g.H)) % g.C,
+                 b = i / (g.C * g.H * g.W);
+  float acc = 0.f;
+  for (uint32_t oc = 0; oc < g.OC; ++oc)
+    for (uint32_t kh = 0; kh < g.k; ++kh) {
+      const int oh = int(ih) - int(kh);
+      if (oh < 0 || oh >= int(g.OH)) continue;
+      for (uint32_t kw = 0; kw < g.k; ++kw) {
+        const int ow = int(iw) - int(kw);
+        if (ow < 0 || ow >= int(g.OW)) continue;
+        acc += ld(dz, b * (g.OC * g.OH * g.OW) + oc * (g.OH * g.OW) + uint32_t(oh) * g.OW +
+                          uint32_t(ow)) *
+               ld(f, oc * (g.C * g.k * g.k) + ic * (g.k * g.k) + kh * g.k + kw);
+      }
+    }
+  st(dx, i, OpPrevActGrad{act}(acc, ld(aprev, i)));
+}
+
+static bool sh_conv_forward_tiled(const Dispatch& d) {
+  const TiledGeom g = tiled_geom(d);
+  const uint32_t act = CU(d, 8);
+  const uint64_t n = uint64_t(g.B) * g.OH * g.OW * g.OC;
+  if (!n) return true;
+  Buf x = S(d, 0), f = S(d, 1), bias = S(d, 2), y = U(d, 0);
+  if (tiled_valid(g) && covers(x, uint64_t(g.B) * g.C * g.H * g.W) &&
+      covers(f, uint64_t(g.OC) * g.C * g.k * g.k) && covers(bias, g.OC) && covers(y, n))
+    return conv_forward(x.p, nullptr, f.p, bias.p, y.p, tiled_conv(g), act <= 2 ? act : 0);
+  hipLaunchKernelGGL(k_conv_tiled_fwd_checked, dim3(uint32_t(cdiv(n, 256))), dim3(256), 0,
+                     stream(), x, f, bias, y, g, act);
+  return check_launch("conv_forward_tiled");
+}
+// t0 = dZ, t1 = A_prev; u0 = dF, u1 = dB (bound by the reference's dispatch
+// but never written by its shader, so it is left untouched here too).
+static bool sh_conv_backprop_filters_tiled(const Dispatch& d) {
+  const TiledGeom g = tiled_geom(d);
+  const uint64_t n = uint64_t(g.OC) * g.C * g.k * g.k;
+  if (!n) return true;
+  Buf dz = S(d, 0), x = S(d, 1), df = U(d, 0);
+  if (tiled_valid(g) && covers(dz, uint64_t(g.B) * g.OC * g.OH * g.OW) &&
+      covers(x, uint64_t(g.B) * g.C * g.H * g.W) && covers(df, n))
+    return conv_backward(dz.p, nullptr, x.p, nullptr, nullptr, df.p, nullptr, nullptr,
+                         tiled_conv(g));
+  hipLaunchKernelGGL(k_conv_tiled_dw_checked, dim3(uint32_t(cdiv(n, 256))), dim3(256), 0,
+                     stream(), dz, x, df, g);
+  return check_launch("conv_backprop_filters_tiled");
+}
+// t0 = dZ, t1 = filters, t2 = A_prev (the previous layer's activation
+// output); u0 = dInput.  The derivative of the previous activation (act
+// word: 1 ReLU, 2 tanh) multiplies the transposed convolution.
+static bool sh_conv_backprop_input_fused(const Dispatch& d) {
+  const TiledGeom g = tiled_geom(d);
+  const uint32_t act = CU(d, 8);
+  const uint64_t n = uint64_t(g.B) * g.C * g.H * g.W;
+  if (!n || n >= (1ull << 32)) return n == 0;
+  Buf dz = S(d, 0), f = S(d, 1), a = S(d, 2), dx = U(d, 0);
+  if (tiled_valid(g) && covers(dz, uint64_t(g.B) * g.OC * g.OH * g.OW) &&
+      covers(f, uint64_t(g.OC) * g.C * g.k * g.k) && covers(a, n) && covers(dx, n)) {
+    if (!conv_backward(dz.p, nullptr, a.p, nullptr, f.p, nullptr, nullptr, dx.p, tiled_conv(g)))
+      return false;
+    if (act != 1 && act != 2) return true;
+    return run_ew("conv_prev_act_grad", OpPrevActGrad{act}, dx, dx, a, uint32_t(n), false);
+  }
+  hipLaunchKernelGGL(k_conv_tiled_dx_checked, dim3(uint32_t(cdiv(n, 256))), dim3(256), 0,
+                     stream(), dz, f, a, dx, g, act);
+  return check_launch("conv_backprop_input_fused");
+}
+
 static bool sh_matmul(const Dispatch& d) {
   uint32_t M = CU(d, 0), K = CU(d, 1), N = CU(d, 2), flags = CU(d, 3) & 3u;
   uint64_t mn = uint64_t(M) * N;
@@ -2679,6 +2884,9 @@ static const ShaderEntry kShaders[] = {
     {"depthwise_conv_backward_filter", sh_dw_bwd_filter},
     {"im2col", sh_im2col},
     {"col2im", sh_col2im},
+    {"conv_forward_tiled", sh_conv_forward_tiled},
+    {"conv_backprop_filters_tiled", sh_conv_backprop_filters_tiled},
+    {"conv_backprop_input_fused", sh_conv_backprop_input_fused},
     {"conv_reshape", sh_conv_reshape},
     {"conv_grad_reshape", sh_conv_grad_reshape<false>},
     {"conv_grad_reshape_relu", sh_conv_grad_reshape<true>},

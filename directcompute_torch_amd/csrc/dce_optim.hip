@@ -182,18 +182,20 @@ __global__ void __launch_bounds__(256) k_multi_adam_dev(const Table t, AdamOp op
 }
 
 // Step counter of Adam / AdamW on the device: state[0] holds t (u32 bits),
-// state[1] the step size lr*sqrt(1 - b2^t)/(1 - b1^t) for that t.  It is
-// evaluated in double from the double hyper-parameters and rounded once to
-// float, as the reference evaluates it in Python and hands the float to the
-// shader (nn_engine.py:2219-2220).  t_set > 0 sets the counter (an eager step
-// whose count the host knows); t_set == 0 advances it by one (a recorded
-// step, whose every replay is the next step).
-__global__ void k_adam_tick(float* state, uint32_t t_set, double lr, double b1, double b2) {
+// state[1] the step size lr*sqrt(1 - b2^t)/(1 - b1^t) for that t.  t_set > 0
+// sets the counter (an eager step whose count the host knows) and stores the
+// host's step size, evaluated as the reference evaluates it in Python and
+// hands the float to the shader (nn_engine.py:2219-2220).  t_set == 0
+// advances the counter by one (a recorded step, whose every replay is the
+// next step) and evaluates the same expression here, in double from the
+// double hyper-parameters, rounded once to float.
+__global__ void k_adam_tick(float* state, uint32_t t_set, float step_host, double lr, double b1,
+                            double b2) {
   if (threadIdx.x != 0) return;
   const uint32_t t = t_set ? t_set : __float_as_uint(state[0]) + 1u;
   const double td = double(t);
   state[0] = __uint_as_float(t);
-  state[1] = float(lr * sqrt(1.0 - pow(b2, td)) / (1.0 - pow(b1, td)));
+  state[1] = t_set ? step_host : float(lr * sqrt(1.0 - pow(b2, td)) / (1.0 - pow(b1, td)));
 }
 
 struct SgdScaledDev : SgdScaledOp {
@@ -431,10 +433,12 @@ bool adam_multi(void** params, void** grads, void** m, void** v, const uint32_t*
 
 bool adam_counted_multi(void** params, void** grads, void** m, void** v,
                         const uint32_t* sizes, uint32_t n, float* state, uint32_t t_set,
-                        double lr, double b1, double b2, float eps, float wd, float clip) {
+                        float step_host, double lr, double b1, double b2, float eps, float wd,
+                        float clip) {
   std::vector<Table> tabs;
   if (!build_tables(params, grads, m, v, sizes, n, true, tabs, nullptr)) return false;
-  hipLaunchKernelGGL(k_adam_tick, dim3(1), dim3(64), 0, stream(), state, t_set, lr, b1, b2);
+  hipLaunchKernelGGL(k_adam_tick, dim3(1), dim3(64), 0, stream(), state, t_set, step_host, lr,
+                     b1, b2);
   if (!check_launch("AdamBatchCounted(tick)")) return false;
   const double bytes = 28.0 * table_elems(tabs);
   const bool nt = stream_nt(bytes);

@@ -48,7 +48,8 @@ _SHARED_MB = _gpu_info.sharedMemory // (1024 * 1024)
 # required for names that are never dispatched.
 shaders = [
     "matmul_universal", "matmul_coarsened", "matmul_heavy", "add_bias", "relu", "relu_grad",
-    "softmax", "softmax_ce_grad", "bias_grad", "sgd", "loss", "maxpool_forward",
+    "softmax", "softmax_ce_grad", "bias_grad", "sgd", "loss",
+    "conv_forward_tiled", "conv_backprop_filters_tiled", "conv_backprop_input_fused", "maxpool_forward",
     "maxpool_backward", "grad_accum", "im2col", "conv_reshape", "conv_grad_reshape", "col2im",
     "argmax_correct", "accumulate_scalar", "bias_relu", "conv_grad_reshape_relu",
     "batchnorm_mean_var", "batchnorm_forward", "batchnorm_backward_reduce",
@@ -374,7 +375,10 @@ class MatMul(Function):
 
 class Conv2D(Function):
     """ConvForwardFused / ConvBackwardFused (nn_engine.py:954-1016).  The
-    implicit-GEMM library keeps no im2col buffer, so `im2col_handle` is None."""
+    implicit-GEMM library keeps no im2col matrix: `im2col_handle` holds the
+    forward's channel-innermost copy of x (the stride-phase or channel-packed
+    copy for fewer than 4 input channels, a 4-float placeholder for pointwise
+    layers), which ConvBackwardFused consumes and releases."""
 
     def __del__(self):
         h = getattr(self, "im2col_handle", None)
@@ -1065,14 +1069,17 @@ class AdamW(_Optimizer):
 
     def step(self, clip=1.0):
         self.t += 1
+        # bias-corrected step size, evaluated as nn_engine.py:2220 does; a
+        # recorded step (t argument 0) has the device evaluate it per replay
+        step_size = self.lr * (1 - self.beta2 ** self.t) ** 0.5 / (1 - self.beta1 ** self.t)
         live = self._live()
         for slot, i in enumerate(live):
             self._ma[slot], self._va[slot] = self.m[i].gpu_buf, self.v[i].gpu_buf
         if live:
             lib.AdamBatchCounted(self._pa, self._ga, self._ma, self._va, self._sa, len(live),
-                                 self._state.gpu_buf, 0 if _recording else self.t, self.lr,
-                                 self.beta1, self.beta2, self.eps, self.lr * self.weight_decay,
-                                 clip)
+                                 self._state.gpu_buf, 0 if _recording else self.t, step_size,
+                                 self.lr, self.beta1, self.beta2, self.eps,
+                                 self.lr * self.weight_decay, clip)
 
 
 class Adam(AdamW):
@@ -1419,18 +1426,37 @@ class KernelProfiler:
                 out[f] = (int(n.value), float(ms.value))
         return out
 
+    # Families that enclose others: conv_bwd brackets each whole
+    # ConvBackwardFused call, whose conv_dw, conv_dx and conv_grad_nhwc
+    # launches are recorded under their own names as well.
+    AGGREGATES = ("conv_bwd",)
+
+    @classmethod
+    def table(cls, st):
+        """Rows (family, calls, ms, % of time) of the leaf families, the
+        aggregate rows (family, calls, ms) and the leaf total (calls, ms).
+        Aggregates are left out of the total, so the percentages add up to
+        100 and no time is counted twice."""
+        leaf = {f: v for f, v in st.items() if f not in cls.AGGREGATES}
+        total = sum(ms for _, ms in leaf.values())
+        calls = sum(c for c, _ in leaf.values())
+        rows = [(f, c, ms, 100.0 * ms / total if total else 0.0)
+                for f, (c, ms) in sorted(leaf.items(), key=lambda kv: -kv[1][1])]
+        aggs = [(f, *st[f]) for f in cls.AGGREGATES if f in st]
+        return rows, aggs, (calls, total)
+
     def report(self, epoch_label=""):
         if not self.enabled:
             return
-        st = self.stats()
-        total = sum(ms for _, ms in st.values())
-        calls = sum(c for c, _ in st.values())
+        rows, aggs, (calls, total) = self.table(self.stats())
         bar = "=" * 80
         print(f"\n{bar}\n  GPU kernel time {epoch_label}\n{bar}")
         print(f"  {'Family':<28} {'Calls':>6} {'Total ms':>10} {'Avg ms':>10} {'% Time':>8}")
-        for f, (c, ms) in sorted(st.items(), key=lambda kv: -kv[1][1]):
-            print(f"  {f:<28} {c:>6} {ms:>10.3f} {ms / c:>10.4f} {100.0 * ms / total if total else 0.0:>7.1f}%")
+        for f, c, ms, pct in rows:
+            print(f"  {f:<28} {c:>6} {ms:>10.3f} {ms / c:>10.4f} {pct:>7.1f}%")
         print(f"  {'TOTAL':<28} {calls:>6} {total:>10.3f}")
+        for f, c, ms in aggs:
+            print(f"  {f + ' (whole calls, in TOTAL)':<28} {c:>6} {ms:>10.3f} {ms / c:>10.4f}")
         hits, misses = get_pool_stats()
         print(f"\n  Pool held:  {get_pool_memory() / 1024 / 1024:>8.2f} MB  "
               f"(requests: {hits} reused, {misses} allocated)\n{bar}\n")

@@ -197,14 +197,17 @@ float ClipGradNorm(void** grads, uint32_t* sizes, uint32_t numGrads, float maxNo
 /* AdamBatch with the step counter kept on the device, so that a recorded
  * step (BeginCapture) replays as the next step, not as a copy of the recorded
  * one.  stepState is a buffer of at least 2 floats: [0] = t (u32 bits),
- * [1] = the step size lr*sqrt(1-beta2^t)/(1-beta1^t), evaluated on the device
- * in double from the double hyper-parameters and rounded once to float, as
- * AdamW.step evaluates it in Python (nn_engine.py:2217-2238).  t > 0 sets the
- * counter to t; t == 0 advances it by one (use 0 in a recorded step).
- * weightDecay is lr*wd, as AdamBatch. */
+ * [1] = the step size lr*sqrt(1-beta2^t)/(1-beta1^t) of that step.  t > 0
+ * sets the counter to t and the step size to stepSize, which the caller
+ * evaluates as AdamW.step does in Python (nn_engine.py:2217-2238).  t == 0
+ * advances the counter by one and evaluates the step size on the device, in
+ * double from the double hyper-parameters, rounded once to float (use 0 in a
+ * recorded step; stepSize is then ignored).  weightDecay is lr*wd, as
+ * AdamBatch. */
 void AdamBatchCounted(void** params, void** grads, void** m, void** v, uint32_t* sizes,
-                      uint32_t numParams, void* stepState, uint32_t t, double lr,
-                      double beta1, double beta2, float eps, float weightDecay, float clip);
+                      uint32_t numParams, void* stepState, uint32_t t, float stepSize,
+                      double lr, double beta1, double beta2, float eps, float weightDecay,
+                      float clip);
 
 /* ClipGradNorm that allocates nothing.  It has no counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under

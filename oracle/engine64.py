@@ -24,7 +24,7 @@ F64 = np.float64
 class T:
     """A float64 tensor node.  ``data`` is float64; ``grad`` accumulates."""
 
-    __slots__ = ("data", "grad", "requires_grad", "_parents", "_backward", "name")
+    __slots__ = ("data", "grad", "requires_grad", "_parents", "_backward", "name", "pre", "own_idx")
 
     def __init__(self, data, requires_grad=False, name=None):
         self.data = np.asarray(data, dtype=F64)
@@ -33,6 +33,8 @@ class T:
         self._parents = ()
         self._backward = None
         self.name = name
+        self.pre = None       # pre-activation, when a decision pattern was given
+        self.own_idx = None   # the oracle's own argmax scan (maxpool2d)
 
     @property
     def shape(self):
@@ -76,7 +78,10 @@ def _node(data, parents, backward):
 def conv2d(x, w, b, stride=1, padding=0, act=0, mask=None):
     """``mask`` (bool, output shape; act == 1 only) pins the ReLU decision
     (y > 0) to a given pattern, e.g. the device's own, so that a value
-    within round-off of 0 cannot route the gradient differently."""
+    within round-off of 0 cannot route the gradient differently.  The node
+    then keeps the pre-activation as ``pre``, so that a caller can check the
+    given decisions against the oracle's own (z > 0)."""
+    z = None
     if act == 1 and mask is not None:
         z = K.conv_forward(x.data, w.data, b.data, stride, padding, 0)
         y = np.where(mask, z, 0.0)
@@ -97,13 +102,17 @@ def conv2d(x, w, b, stride=1, padding=0, act=0, mask=None):
             b._acc(db)
         if x.requires_grad:
             x._acc(dX)
-    return _node(y, (x, w, b), bw)
+    node = _node(y, (x, w, b), bw)
+    node.pre = z
+    return node
 
 
 def maxpool2d(x, pool_size=2, stride=2, indices=None):
     """``indices`` may be supplied (uint32, from the device) so that routing
-    follows exactly the same argmax as the run under test."""
+    follows exactly the same argmax as the run under test; the node keeps the
+    oracle's own scan as ``own_idx``."""
     out, idx = K.maxpool_forward(x.data, pool_size, stride)
+    own_idx = idx
     if indices is not None:
         idx = np.asarray(indices, dtype=np.uint32).reshape(idx.shape)
         flat = x.data.reshape(-1)
@@ -113,6 +122,7 @@ def maxpool2d(x, pool_size=2, stride=2, indices=None):
         x._acc(K.maxpool_backward(g, idx, x.data.size))
     node = _node(out, (x,), bw)
     node.name = idx
+    node.own_idx = own_idx
     return node
 
 
@@ -148,9 +158,12 @@ def add_bias(A, b):
 
 
 def bias_relu(A, b, mask=None):
+    """``mask`` pins the decision A + b > 0; the node keeps A + b as ``pre``."""
     out = K.bias_relu(A.data, b.data)
+    pre = None
     if mask is not None:
-        out = np.where(mask, K.add_bias(A.data, b.data), 0.0)
+        pre = K.add_bias(A.data, b.data)
+        out = np.where(mask, pre, 0.0)
 
     def bw(g):
         eff = K.relu_grad(g, out) if mask is None else np.where(mask, g, 0.0)
@@ -158,7 +171,9 @@ def bias_relu(A, b, mask=None):
             A._acc(eff)
         if b.requires_grad:
             b._acc(eff.sum(axis=0))
-    return _node(out, (A, b), bw)
+    node = _node(out, (A, b), bw)
+    node.pre = pre
+    return node
 
 
 def relu(x, mask=None):

@@ -134,6 +134,115 @@ def conv_backward(dy, y, x, Wt, s, p, act, need_x=True, need_w=True, need_b=True
     return dW, db, dX
 
 
+# The three direct valid convolutions the reference compiles (nn_engine.py:148):
+# stride 1, no padding, square kernel ks, constants {batch, inC, inH, inW, outC,
+# ks, outH, outW, act}.  They work on flat buffers, with the shaders' own 32-bit
+# index arithmetic (wrapping) and the D3D11 rule that a read past a buffer
+# returns 0 and a write past it is dropped, so any geometry is defined; with
+# outH = inH - ks + 1 and outW = inW - ks + 1 they are ordinary valid
+# convolutions.  Each returns the updated output buffer.
+
+def _u32(a):
+    return np.asarray(a, dtype=np.int64) & 0xFFFFFFFF
+
+
+def _rd(buf, idx):
+    """buf[idx] with reads past the buffer returning 0."""
+    buf = _f64(buf).reshape(-1)
+    idx = _u32(idx)
+    ok = idx < buf.size
+    return np.where(ok, buf[np.where(ok, idx, 0)], 0.0)
+
+
+def _wr(out, idx, vals):
+    """out[idx] = vals, dropping writes past the buffer."""
+    out = _f64(out).reshape(-1).copy()
+    idx = _u32(idx)
+    vals = np.broadcast_to(_f64(vals), idx.shape).reshape(-1)
+    idx = idx.reshape(-1)
+    ok = idx < out.size
+    out[idx[ok]] = vals[ok]
+    return out
+
+
+def conv_forward_tiled(x, F, bias, out, batch, inC, inH, inW, outC, ks, outH, outW, act):
+    """nn_conv_forward_tiled.hlsl:22-71.  M = outC rows of filters (row-major,
+    K = inC*ks*ks), N = batch*outH*outW columns; the input patch of column
+    (b, oh, ow) at k = (ic, kh, kw) is input[b*inC*inH*inW + ic*inH*inW +
+    (oh+kh)*inW + ow+kw]; z = acc + bias[row]; act 1 = max(0, z), 2 = tanh,
+    else z; written at output[b*outC*outH*outW + row*outH*outW + pixel]."""
+    M, N, K, P = outC, batch * outH * outW, inC * ks * ks, outH * outW
+    col = np.arange(N, dtype=np.int64)
+    b, pix = col // P, col % P
+    oh, ow = pix // outW, pix % outW
+    t = np.arange(K, dtype=np.int64)
+    ic, kk = t // (ks * ks), t % (ks * ks)
+    kh, kw = kk // ks, kk % ks
+    xi = (b[None, :] * (inC * inH * inW) + ic[:, None] * (inH * inW)
+          + (oh[None, :] + kh[:, None]) * inW + (ow[None, :] + kw[:, None]))
+    patches = _rd(x, xi)                                         # K x N
+    rows = np.arange(M, dtype=np.int64)
+    Fm = _rd(F, rows[:, None] * K + t[None, :])                  # M x K
+    z = Fm @ patches + _rd(bias, rows)[:, None]
+    if act == 1:
+        z = np.maximum(0.0, z)
+    elif act == 2:
+        z = np.tanh(z)
+    oi = b[None, :] * (outC * P) + rows[:, None] * P + pix[None, :]
+    return _wr(out, oi, z)
+
+
+def conv_backprop_filters_tiled(dZ, x, dF, batch, inC, inH, inW, outC, ks, outH, outW):
+    """nn_conv_backprop_filters_tiled.hlsl:21-74.  dF[row*tr + col] (tr =
+    inC*ks*ks, col = (ic, kh, kw)) = Σ over k in batch*outH*outW of
+    dZ[b*outC*outH*outW + row*outH*outW + p] * input[b*inC*inH*inW +
+    ic*inH*inW + (oh+kh)*inW + ow+kw].  No activation mask; the dB buffer
+    the dispatch binds is never written."""
+    M, N, tr, P = outC, batch * outH * outW, inC * ks * ks, outH * outW
+    k = np.arange(N, dtype=np.int64)
+    b, p = k // P, k % P
+    oh, ow = p // outW, p % outW
+    rows = np.arange(M, dtype=np.int64)
+    dz = _rd(dZ, b[None, :] * (outC * P) + rows[:, None] * P + p[None, :])     # M x N
+    c = np.arange(tr, dtype=np.int64)
+    ic, kk = c // (ks * ks), c % (ks * ks)
+    kh, kw = kk // ks, kk % ks
+    xi = (b[:, None] * (inC * inH * inW) + ic[None, :] * (inH * inW)
+          + (oh[:, None] + kh[None, :]) * inW + (ow[:, None] + kw[None, :]))
+    return _wr(dF, rows[:, None] * tr + c[None, :], dz @ _rd(x, xi))
+
+
+def conv_backprop_input_fused(dZ, F, a_prev, dx, batch, inC, inH, inW, outC, ks, outH, outW,
+                              prev_act):
+    """nn_conv_backprop_input_fused.hlsl:19-50.  For each input element gid <
+    batch*inC*inH*inW: acc = Σ_{oc, kh, kw} dZ[b, oc, ih-kh, iw-kw] *
+    filters[oc, ic, kh, kw] over the in-range (oh, ow); dA from a =
+    A_prev[gid]: prevActType 1 -> (a > 0 ? 1 : 0), 2 -> 1 - a², else 1;
+    dInput[gid] = acc * dA."""
+    total = batch * inC * inH * inW
+    g = np.arange(total, dtype=np.int64)
+    iw, ih = g % inW, (g // inW) % inH
+    ic, b = (g // (inW * inH)) % inC, g // (inC * inH * inW)
+    acc = np.zeros(total)
+    for oc in range(outC):
+        for kh in range(ks):
+            oh = ih - kh
+            for kw in range(ks):
+                ow = iw - kw
+                ok = (oh >= 0) & (oh < outH) & (ow >= 0) & (ow < outW)
+                zi = b * (outC * outH * outW) + oc * (outH * outW) + np.where(ok, oh * outW + ow, 0)
+                fv = _rd(F, np.full(1, oc * (inC * ks * ks) + kh * ks + kw) + ic * (ks * ks))
+                acc += np.where(ok, _rd(dZ, zi) * fv, 0.0)
+    a = _rd(a_prev, g)
+    if prev_act == 1:
+        dA = np.where(a > 0.0, 1.0, 0.0)
+    elif prev_act == 2:
+        dA = 1.0 - a * a
+    else:
+        dA = np.ones_like(a)
+    return _wr(dx, g, acc * dA)
+
+
 def matmul(A, Bm, M, K, N, flags):
     """Flagged GEMM shared by matmul_{heavy,dgpu,universal,reduce}: bit0 means A
     is stored K×M (A[k*M+m]), bit1 means B is stored N×K (B[n*K+k]); C is M×N

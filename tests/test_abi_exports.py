@@ -65,6 +65,8 @@ def test_calls_without_init_fail_cleanly():
     assert lib.GetPoolMemory() == 0
     assert lib.CompileShader(b"conv_reshape", None)
     assert lib.CompileShader(b"batchnorm_backward_dx", None)
+    for name in (b"conv_forward_tiled", b"conv_backprop_filters_tiled", b"conv_backprop_input_fused"):
+        assert lib.CompileShader(name, None), name          # nn_engine.py:148
     assert not lib.CompileShader(b"gelu", None)       # no kernel source in the reference
     assert not lib.CompileShaderEx(b"custom", None, b"CSMain")
     assert lib.ResolveShader(b"relu_grad")

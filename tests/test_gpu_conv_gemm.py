@@ -8,6 +8,7 @@ import numpy as np
 import pytest
 
 from oracle import kernels as K
+from tests import workloads as WL
 from tests.helpers import TOL, download, he, rel_err, release, rng, upload
 
 pytestmark = pytest.mark.gpu
@@ -321,6 +322,8 @@ def test_single_conv_full_size_sampled(eng):
     hy = eng.lib.ConvForwardFused(hx, hw, hb, B, C, H, W, OC, k, k, 1, 1, 1, None)
     assert hy, eng.last_error()
     y = download(eng, hy, (B, OC, H, W))
+    oc_fwd = np.sort(rng(2 * 1000 + 1).choice(OC, 8, replace=False))
+    _audit_forward(y, _fwd_ref_sampled(x, w, b, 1, 1, oc_fwd), oc_fwd, "single conv")
     dy = r.standard_normal(y.shape).astype(np.float32)
     hdy = upload(eng, dy)
     pdf, pdb, pdx = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
@@ -360,6 +363,32 @@ def test_single_conv_full_size_sampled(eng):
     assert rel_err(np.array(got_s), np.array(ref_s)) <= TOL
 
 
+def _fwd_ref_sampled(x, w, b, s, p, oc_sel):
+    """Pre-activations z[b, oc, oh, ow] of the selected output channels over
+    the whole batch, in float64: one contraction over the channels per tap."""
+    B, C, H, W = x.shape
+    k = w.shape[2]
+    OH, OW = (H + 2 * p - k) // s + 1, (W + 2 * p - k) // s + 1
+    xp = np.zeros((B, C, H + 2 * p, W + 2 * p), np.float32)
+    xp[:, :, p:p + H, p:p + W] = x
+    ws = w[oc_sel].astype(np.float64)
+    z = np.zeros((B, len(oc_sel), OH, OW)) + b[oc_sel].astype(np.float64).reshape(1, -1, 1, 1)
+    for kh in range(k):
+        for kw in range(k):
+            xs = xp[:, :, kh:kh + s * (OH - 1) + 1:s, kw:kw + s * (OW - 1) + 1:s].astype(np.float64)
+            z += np.einsum("oc,bchw->bohw", ws[:, :, kh, kw], xs, optimize=True)
+    return z
+
+
+def _audit_forward(y, z_sel, oc_sel, what):
+    """The device's ReLU forward on the sampled channels against the float64
+    pre-activations: the decisions the backward adopts (y > 0) may disagree
+    with z > 0 only at near-ties, and the positive outputs match z."""
+    a = WL.DecisionAudit()
+    a.relu("pos", z_sel, y[:, oc_sel], dev_is_output=True)
+    print(f"  {what} forward, {len(oc_sel)} sampled channels: {a.check(1e-5, 1e-5)}", flush=True)
+
+
 def _dw_ref_taps(G, x, k, s, p, oc_sel):
     """dW[oc, c, kh, kw] for the selected output channels: one float64
     contraction over the whole batch per tap."""
@@ -395,6 +424,8 @@ def test_alexnet_b128_conv_backward_full_size(eng, layer):
     assert hy, eng.last_error()
     OH, OW = K.conv_out_hw(H, H, k, s, p)
     y = download(eng, hy, (B, OC, OH, OW))
+    oc_fwd = np.sort(rng(5 * 1000 + k + 1).choice(OC, 16, replace=False))
+    _audit_forward(y, _fwd_ref_sampled(x, w, b, s, p, oc_fwd), oc_fwd, f"alexnet b128 {layer}")
     dy = r.standard_normal(y.shape).astype(np.float32)
     hdy = upload(eng, dy)
     want_x = 0 if layer == "c1" else 1
@@ -490,3 +521,96 @@ def test_linear_tile_order(eng, monkeypatch):
     monkeypatch.setenv("DCE_XCD", "0")
     _conv_case(eng, 2, 64, 13, 13, 192, 5, 1, 2, 1)
     test_matmul_alloc(eng, 200, 300, 100, 0)
+
+
+# ------------------------------------------- direct valid convolutions
+def _run_shader(eng, name, srvs, uavs, cb):
+    import struct
+    sa = (ctypes.c_void_p * len(srvs))(*srvs)
+    ua = (ctypes.c_void_p * len(uavs))(*uavs)
+    th = (ctypes.c_uint * 3)(1, 1, 1)
+    words = [struct.unpack("I", struct.pack("I", v))[0] for v in cb]
+    cba = (ctypes.c_uint * len(words))(*words)
+    eng.lib.ClearLastError()
+    eng.lib.RunShader(name.encode(), sa, len(srvs), ua, len(uavs), th,
+                      ctypes.cast(cba, ctypes.c_void_p), 4 * len(words))
+    assert eng.last_error() == "", eng.last_error()
+
+
+TILED_GPU = [(4, 16, 20, 20, 24, 3), (2, 3, 30, 26, 8, 5), (3, 20, 16, 16, 12, 1), (2, 7, 13, 11, 5, 4),
+             (16, 32, 28, 28, 64, 3)]
+
+
+@pytest.mark.parametrize("B,C,H,W,OC,k", TILED_GPU)
+def test_tiled_conv_shaders(eng, B, C, H, W, OC, k):
+    """conv_forward_tiled, conv_backprop_filters_tiled and
+    conv_backprop_input_fused (nn_engine.py:148; valid convolution, stride 1,
+    no padding) through RunShader with the reference's constant layout, on
+    the implicit-GEMM core (generic, stride-phase C < 4 and pointwise k = 1
+    layouts), against the float64 oracle: act 0 / ReLU / tanh forward, the
+    filter gradient (its dB slot left untouched, as the shader never writes
+    it) and the input gradient times the previous ReLU / tanh derivative."""
+    print(f"tiled conv shaders B{B} C{C} {H}x{W} OC{OC} k{k}", flush=True)
+    r = rng(B * 1000 + C * 37 + k)
+    OH, OW = H - k + 1, W - k + 1
+    geo = (B, C, H, W, OC, k, OH, OW)
+    x = r.standard_normal((B, C, H, W)).astype(np.float32)
+    w = he(r, (OC, C, k, k), C * k * k)
+    b = (0.1 * r.standard_normal(OC)).astype(np.float32)
+    dz = r.standard_normal((B, OC, OH, OW)).astype(np.float32)
+    hx, hw, hb, hdz = upload(eng, x), upload(eng, w), upload(eng, b), upload(eng, dz)
+    hy = eng.lib.CreateBuffer(None, B * OC * OH * OW)
+    for act in (0, 1, 2):
+        _run_shader(eng, "conv_forward_tiled", [hx, hw, hb], [hy], [*geo, act])
+        ref = K.conv_forward_tiled(x, w, b, np.zeros(B * OC * OH * OW), *geo, act)
+        assert rel_err(download(eng, hy, (B * OC * OH * OW,)), ref) <= TOL, act
+    hdf = eng.lib.CreateBuffer(None, OC * C * k * k)
+    sentinel = np.full(OC, 7.0, np.float32)
+    hdb = upload(eng, sentinel)
+    _run_shader(eng, "conv_backprop_filters_tiled", [hdz, hx], [hdf, hdb], list(geo))
+    ref = K.conv_backprop_filters_tiled(dz, x, np.zeros(OC * C * k * k), *geo)
+    assert rel_err(download(eng, hdf, (OC * C * k * k,)), ref) <= TOL
+    assert np.array_equal(download(eng, hdb, (OC,)), sentinel)
+    u = r.standard_normal(x.shape).astype(np.float32)
+    hdx = eng.lib.CreateBuffer(None, x.size)
+    for act, a in ((0, u), (1, np.maximum(u, 0)), (2, np.tanh(u).astype(np.float32))):
+        ha = upload(eng, a)
+        _run_shader(eng, "conv_backprop_input_fused", [hdz, hw, ha], [hdx], [*geo, act])
+        ref = K.conv_backprop_input_fused(dz, w, a, np.zeros(x.size), *geo, act)
+        assert rel_err(download(eng, hdx, (x.size,)), ref) <= TOL, act
+        release(eng, ha)
+    release(eng, hx, hw, hb, hdz, hy, hdf, hdb, hdx)
+
+
+def test_tiled_conv_shaders_flat_geometry(eng):
+    """Geometry that is not a valid convolution and buffers shorter than the
+    geometry take the checked kernels, which follow the shaders' flat index
+    arithmetic with reads past a buffer returning 0 and writes dropped."""
+    r = rng(4242)
+    geo = (2, 2, 5, 4, 3, 2, 5, 3)
+    B, C, H, W, OC, ks, OH, OW = geo
+    x = r.standard_normal(B * C * H * W - 5).astype(np.float32)
+    f = r.standard_normal(OC * C * ks * ks).astype(np.float32)
+    bias = r.standard_normal(OC - 1).astype(np.float32)
+    out0 = r.standard_normal(B * OC * OH * OW - 4).astype(np.float32)
+    hx, hf, hb = upload(eng, x), upload(eng, f), upload(eng, bias)
+    for act in (0, 1, 2):
+        ho = upload(eng, out0)
+        _run_shader(eng, "conv_forward_tiled", [hx, hf, hb], [ho], [*geo, act])
+        assert rel_err(download(eng, ho, out0.shape), K.conv_forward_tiled(x, f, bias, out0, *geo, act)) <= 1e-5
+        release(eng, ho)
+    dz = r.standard_normal(B * OC * OH * OW - 3).astype(np.float32)
+    dF0 = r.standard_normal(OC * C * ks * ks - 2).astype(np.float32)
+    hdz, hdf = upload(eng, dz), upload(eng, dF0)
+    _run_shader(eng, "conv_backprop_filters_tiled", [hdz, hx], [hdf], list(geo))
+    assert rel_err(download(eng, hdf, dF0.shape), K.conv_backprop_filters_tiled(dz, x, dF0, *geo)) <= 1e-5
+    ap = r.standard_normal(B * C * H * W - 7).astype(np.float32)
+    dx0 = r.standard_normal(B * C * H * W - 1).astype(np.float32)
+    ha = upload(eng, ap)
+    for act in (0, 1, 2):
+        hdx = upload(eng, dx0)
+        _run_shader(eng, "conv_backprop_input_fused", [hdz, hf, ha], [hdx], [*geo, act])
+        ref = K.conv_backprop_input_fused(dz, f, ap, dx0, *geo, act)
+        assert rel_err(download(eng, hdx, dx0.shape), ref) <= 1e-5
+        release(eng, hdx)
+    release(eng, hx, hf, hb, hdz, hdf, ha)

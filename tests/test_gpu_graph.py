@@ -67,7 +67,7 @@ def _eager_step(eng, be, net, opt, x, y, clip, loss_kind, max_norm, pins=False):
     loss = fn(out, eng.Tensor(y, track=True))
     extra = {}
     if pins:
-        extra["pins"] = dict(pool_indices=be.pool_indices(), masks=be.masks())
+        extra["pins"] = dict(pool_indices=be.pool_indices(), decisions=be.decisions())
     loss.backward()
     if pins:
         extra["grads"] = be.grads()
@@ -89,10 +89,11 @@ def _check_against_oracle(net, loss_kind, opt_kind, opt, P_before, mv_before, x,
     max-pool and ReLU decisions), and the update the optimiser rule gives from
     the device's gradients -- with the step count of this step for Adam."""
     from oracle import kernels as K
-    from tests.test_gpu_models import _compare_grads
+    from tests.test_gpu_models import _audit, _compare_grads
     ob = WL.Oracle(P_before, **extra["pins"])
     out = net(ob, x)
     oloss = ob.softmax_ce(out, y) if loss_kind == "ce" else ob.dice(out, y)
+    _audit(ob, fwd_tol=1e-5 if loss_kind == "ce" else 4e-5)   # UNet: deep conv + BN chain
     oloss.backward()
     og = ob.grads()
     ref_loss = float(np.mean(oloss.data))

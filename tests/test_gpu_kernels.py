@@ -282,6 +282,35 @@ def test_maxpool_raw_shaders(eng):
     release(eng, hx, ho, hi, hdz, hdx)
 
 
+@pytest.mark.parametrize("planes,outPer,inPer", [(6, 729, 3025), (3, 700, 40), (2, 300, 20000)],
+                         ids=["lds_pool1", "lds_dense_dups", "per_thread_large_plane"])
+def test_maxpool_backward_arbitrary_indices(eng, planes, outPer, inPer):
+    """MaxPoolBackwardFused on caller indices that no pooling window could
+    make: many outputs per input (duplicates inside one 256-output round of
+    the LDS kernel), indices in another plane and the 0xFFFFFFFF marker.  Each
+    input must add its plane's contributions one by one in output order, so
+    the result equals a float32 np.add.at in that order bit for bit (planes
+    up to 14336 inputs take the LDS kernel, larger ones the per-thread one)."""
+    r = rng(planes * outPer + inPer)
+    dz = r.standard_normal(planes * outPer).astype(np.float32)
+    local = r.integers(0, min(inPer, 97), planes * outPer)          # heavy duplication
+    idx = (np.repeat(np.arange(planes), outPer) * inPer + local).astype(np.uint32)
+    idx[::17] = 0xFFFFFFFF                                           # no argmax
+    idx[5::23] = (idx[5::23] + inPer) % (planes * inPer)             # another plane: dropped
+    ref = np.zeros(planes * inPer, np.float32)
+    keep = (idx != 0xFFFFFFFF) & (idx // inPer == np.repeat(np.arange(planes), outPer))
+    np.add.at(ref, idx[keep].astype(np.int64), dz[keep])
+    hdz = upload(eng, dz)
+    for _ in range(2):
+        hi = upload(eng, idx.view(np.float32))
+        eng.lib.ClearLastError()
+        hdx = eng.lib.MaxPoolBackwardFused(hdz, hi, planes, 1, outPer, 1, planes * inPer)
+        assert hdx, eng.last_error()
+        assert np.array_equal(download(eng, hdx, ref.shape), ref)
+        release(eng, hdx)
+    release(eng, hdz)
+
+
 @pytest.mark.parametrize("B,C,H,W,k,s", [(2, 4, 55, 55, 3, 2), (2, 3, 8, 8, 2, 2), (1, 2, 9, 9, 3, 1)])
 def test_maxpool_backward_untagged_indices(eng, B, C, H, W, k, s):
     """MaxPoolBackwardFused on indices that carry no pooling geometry (here a
@@ -755,9 +784,11 @@ def test_optimisers_ragged_tensor_lists(eng, seed, count):
 
 def test_adam_batch_counted(eng, policy):
     """AdamBatchCounted keeps t and the step size on the device: t > 0 sets
-    the counter, t == 0 advances it.  The step size equals the float32 of the
-    host's float64 formula (nn_engine.py:2219-2220) and the update equals
-    AdamBatch with that step size, bit for bit."""
+    the counter and stores the host's step size unchanged (an eager step is
+    bit for bit the reference's nn_engine.py:2219-2220 float), t == 0 advances
+    the counter and evaluates the step size on the device (within one float
+    ulp of the host formula; the stepSize argument is ignored).  The update
+    equals AdamBatch with the stored step size, bit for bit."""
     ws, gs = _param_set(6, SIZES)
     r = rng(7)
     ms = [(0.1 * r.standard_normal(n)).astype(np.float32) for n in SIZES]
@@ -768,12 +799,16 @@ def test_adam_batch_counted(eng, policy):
     b = [[upload(eng, x) for x in arrs] for arrs in (ws, gs, ms, vs)]   # host step size
     state = upload(eng, np.zeros(2, np.float32))
     for t_arg, t in ((5, 5), (0, 6), (0, 7), (2, 2), (0, 3), (1000, 1000)):
-        eng.lib.AdamBatchCounted(*(_arrays(h) for h in a), sa, len(SIZES), state, t_arg, lr, b1, b2,
-                                 eps, lr * wd, clip)
+        step = K.adam_step_size(lr, b1, b2, t)
+        host = float(np.float32(step)) if t_arg else 123.0      # ignored when t_arg == 0
+        eng.lib.AdamBatchCounted(*(_arrays(h) for h in a), sa, len(SIZES), state, t_arg, host, lr,
+                                 b1, b2, eps, lr * wd, clip)
         st = download(eng, state, (2,))
         assert int(st[:1].view(np.uint32)[0]) == t
-        step = K.adam_step_size(lr, b1, b2, t)
-        assert abs(float(st[1]) - float(np.float32(step))) <= 2.0 ** -23 * step, (t, st[1], step)
+        if t_arg:
+            assert st[1] == np.float32(step), (t, st[1], step)
+        else:
+            assert abs(float(st[1]) - float(np.float32(step))) <= 2.0 ** -23 * step, (t, st[1], step)
         eng.lib.AdamBatch(*(_arrays(h) for h in b), sa, len(SIZES), float(st[1]), b1, b2, eps, lr * wd,
                           clip)
         for i in range(len(SIZES)):
@@ -782,7 +817,8 @@ def test_adam_batch_counted(eng, policy):
                                       download(eng, b[j][i], (SIZES[i],))), (t, i, j)
     eng.lib.ClearLastError()
     short = upload(eng, np.zeros(1, np.float32))
-    eng.lib.AdamBatchCounted(*(_arrays(h) for h in a), sa, len(SIZES), short, 1, lr, b1, b2, eps, 0.0, clip)
+    eng.lib.AdamBatchCounted(*(_arrays(h) for h in a), sa, len(SIZES), short, 1, 1e-3, lr, b1, b2, eps,
+                             0.0, clip)
     assert "2 floats" in eng.last_error()
     release(eng, *[h for arrs in a + b for h in arrs], state, short)
 
@@ -885,6 +921,20 @@ def test_profiler_device_time(eng, capsys):
     assert "relu_grad" in out and "TOTAL" in out
     p.reset()
     assert "relu_grad" not in p.stats()
+    # a whole ConvBackwardFused call is recorded as conv_bwd and its kernels
+    # under their own families: the report's percentages still add up to 100
+    x = eng.Tensor(r.standard_normal((2, 8, 12, 12)).astype(np.float32), requires_grad=True, track=False)
+    w = eng.Tensor((r.standard_normal((16, 8, 3, 3)) * 0.2).astype(np.float32), requires_grad=True,
+                   track=False)
+    b = eng.Tensor(np.zeros(16, np.float32), requires_grad=True, track=False)
+    eng.conv2d(x, w, b, 1, 1, 1).backward()          # seed = ones (nn_engine.py:575-603)
+    st = p.stats()
+    assert "conv_bwd" in st and "conv_dw" in st
+    rows, aggs, (_, total) = p.table(st)
+    assert [a[0] for a in aggs] == ["conv_bwd"] and "conv_bwd" not in [q[0] for q in rows]
+    assert abs(sum(q[3] for q in rows) - 100.0) < 1e-6
+    assert total < sum(ms for _, ms in st.values())
+    eng.end_batch()
     p.disable()
     p.uninstall()
     release(eng, hg, hx, ho)

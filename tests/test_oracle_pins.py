@@ -34,6 +34,123 @@ CONV = [(2, 3, 9, 8, 4, 3, 1, 1), (1, 2, 11, 11, 3, 5, 2, 2), (2, 4, 7, 7, 5, 3,
         (2, 5, 6, 6, 3, 1, 1, 0)]
 
 
+# --------------------------------------------- direct valid convolutions
+TILED = [(2, 3, 9, 8, 4, 3), (1, 5, 7, 7, 6, 1), (3, 2, 12, 10, 5, 5), (2, 4, 6, 6, 3, 6)]
+
+
+@pytest.mark.parametrize("B,C,H,W,OC,k", TILED)
+def test_tiled_convs_valid_geometry_vs_torch(B, C, H, W, OC, k):
+    """K.conv_forward_tiled / conv_backprop_filters_tiled /
+    conv_backprop_input_fused on valid geometry (stride 1, no padding)
+    against torch's conv2d, conv2d_weight and autograd through the previous
+    layer's ReLU / tanh (dA = 1 - a² is tanh's derivative at its output)."""
+    r = rng(B * 100 + C * 10 + k)
+    OH, OW = H - k + 1, W - k + 1
+    x, w, b = r.standard_normal((B, C, H, W)), r.standard_normal((OC, C, k, k)), r.standard_normal(OC)
+    dz = r.standard_normal((B, OC, OH, OW))
+    geo = (B, C, H, W, OC, k, OH, OW)
+    z = F.conv2d(t64(x), t64(w), t64(b))
+    for act, ref in ((0, z), (1, F.relu(z)), (2, torch.tanh(z)), (7, z)):
+        out = K.conv_forward_tiled(x, w, b, np.zeros(B * OC * OH * OW), *geo, act)
+        close(out.reshape(z.shape), ref.numpy())
+    dF = K.conv_backprop_filters_tiled(dz, x, np.zeros(OC * C * k * k), *geo)
+    close(dF.reshape(w.shape), torch.nn.grad.conv2d_weight(t64(x), w.shape, t64(dz)).numpy())
+    u = r.standard_normal(x.shape)
+    for act, fn in ((0, lambda v: v), (1, F.relu), (2, torch.tanh)):
+        ut = t64(u, True)
+        a = fn(ut)
+        F.conv2d(a, t64(w)).backward(t64(dz))
+        dx = K.conv_backprop_input_fused(dz, w, a.detach().numpy(), np.zeros(x.size), *geo, act)
+        close(dx.reshape(x.shape), ut.grad.numpy())
+
+
+def _tiled_brute(kind, bufs, geo, act=0):
+    """Scalar loops written from the three HLSL texts, with the D3D11 rule
+    for out-of-range reads (0) and writes (dropped); 32-bit index math."""
+    B, C, H, W, OC, ks, OH, OW = geo
+    M32 = 0xFFFFFFFF
+
+    def rd(a, i):
+        i &= M32
+        return float(a[i]) if i < len(a) else 0.0
+
+    out = list(bufs[-1])
+
+    def wr(i, v):
+        i &= M32
+        if i < len(out):
+            out[i] = v
+    if kind == "fwd":
+        x, f, bias = bufs[:3]
+        K_ = C * ks * ks
+        for row in range(OC):
+            for col in range(B * OH * OW):
+                b, pix = col // (OH * OW), col % (OH * OW)
+                oh, ow = pix // OW, pix % OW
+                acc = 0.0
+                for t in range(K_):
+                    ic, kk = t // (ks * ks), t % (ks * ks)
+                    acc += rd(f, row * K_ + t) * rd(x, b * (C * H * W) + ic * (H * W) + (oh + kk // ks) * W
+                                                   + ow + kk % ks)
+                zz = acc + rd(bias, row)
+                a = max(0.0, zz) if act == 1 else (np.tanh(zz) if act == 2 else zz)
+                wr(b * (OC * OH * OW) + row * (OH * OW) + pix, a)
+    elif kind == "dw":
+        dz, x = bufs[:2]
+        tr = C * ks * ks
+        for row in range(OC):
+            for col in range(tr):
+                ic, kk = col // (ks * ks), col % (ks * ks)
+                acc = 0.0
+                for k_idx in range(B * OH * OW):
+                    b, p = k_idx // (OH * OW), k_idx % (OH * OW)
+                    acc += rd(dz, b * (OC * OH * OW) + row * (OH * OW) + p) * \
+                        rd(x, b * (C * H * W) + ic * (H * W) + (p // OW + kk // ks) * W + p % OW + kk % ks)
+                wr(row * tr + col, acc)
+    else:
+        dz, f, ap = bufs[:3]
+        for g in range(B * C * H * W):
+            iw, ih, ic, b = g % W, (g // W) % H, (g // (W * H)) % C, g // (C * H * W)
+            acc = 0.0
+            for oc in range(OC):
+                for kh in range(ks):
+                    oh = ih - kh
+                    if 0 <= oh < OH:
+                        for kw in range(ks):
+                            ow = iw - kw
+                            if 0 <= ow < OW:
+                                acc += rd(dz, b * (OC * OH * OW) + oc * (OH * OW) + oh * OW + ow) * \
+                                    rd(f, oc * (C * ks * ks) + ic * (ks * ks) + kh * ks + kw)
+            a = rd(ap, g)
+            dA = (1.0 if a > 0 else 0.0) if act == 1 else (1.0 - a * a if act == 2 else 1.0)
+            wr(g, acc * dA)
+    return np.array(out)
+
+
+def test_tiled_convs_flat_semantics_brute_force():
+    """Geometry that is not a valid convolution (an output taller than the
+    input allows, so patch rows run into the next row / plane) and buffers
+    shorter than the geometry: the oracle follows the shaders' flat index
+    arithmetic and the D3D11 out-of-range rules exactly."""
+    r = rng(55)
+    geo = (2, 2, 5, 4, 3, 2, 5, 3)          # valid would be OH = 4
+    B, C, H, W, OC, ks, OH, OW = geo
+    x = r.standard_normal(B * C * H * W - 5)  # short input: the last reads return 0
+    f = r.standard_normal(OC * C * ks * ks)
+    bias = r.standard_normal(OC - 1)         # short bias
+    out0 = r.standard_normal(B * OC * OH * OW - 4)   # short output: writes dropped
+    for act in (0, 1, 2):
+        close(K.conv_forward_tiled(x, f, bias, out0, *geo, act), _tiled_brute("fwd", [x, f, bias, out0], geo, act))
+    dz = r.standard_normal(B * OC * OH * OW - 3)
+    dF0 = r.standard_normal(OC * C * ks * ks - 2)
+    close(K.conv_backprop_filters_tiled(dz, x, dF0, *geo), _tiled_brute("dw", [dz, x, dF0], geo))
+    ap = r.standard_normal(B * C * H * W - 7)
+    dx0 = r.standard_normal(B * C * H * W - 1)
+    for act in (0, 1, 2):
+        close(K.conv_backprop_input_fused(dz, f, ap, dx0, *geo, act),
+              _tiled_brute("dx", [dz, f, ap, dx0], geo, act))
+
+
 # ------------------------------------------------------------------ conv
 @pytest.mark.parametrize("B,C,H,W,OC,k,s,p", CONV)
 def test_conv_forward_vs_torch(B, C, H, W, OC, k, s, p):
@@ -264,6 +381,18 @@ def test_bias_ops_vs_autograd():
     # bias_grad in both layouts it is dispatched with
     close(K.bias_grad(A, 6, 9, 9, 1), A.sum(axis=0))
     close(K.bias_grad(A.T.copy(), 6, 9, 1, 6), A.sum(axis=0))
+
+
+def test_scale_add_vs_torch_add():
+    """K.scale_add (nn_scale_add.hlsl:9) against torch.add(α·a, b, alpha=β), plus
+    the identities that a dropped or swapped coefficient breaks."""
+    r = rng(43)
+    a, b = r.standard_normal(37), r.standard_normal(37)
+    for alpha, beta in ((1.5, -0.5), (0.0, 2.0), (-3.0, 0.0), (0.25, 0.75)):
+        close(K.scale_add(a, b, alpha, beta), torch.add(t64(a) * alpha, t64(b), alpha=beta).numpy())
+    close(K.scale_add(a, b, 1.0, 0.0), a)
+    close(K.scale_add(a, b, 0.0, 1.0), b)
+    close(K.scale_add(a, a, 2.0, -2.0), np.zeros_like(a))
 
 
 def test_add_bias_linear_layer_vs_autograd():

@@ -106,3 +106,56 @@ def test_noalloc_clip_refuses_beyond_scratch(eng):
         assert norm == pytest.approx(np.sqrt(float(MAX_PARTS * CHUNK)), rel=1e-6)
     finally:
         release(eng, h)
+
+
+def test_noalloc_clip_under_capture_and_no_pool_use(eng):
+    """The property the entry point exists for: it allocates nothing.  An
+    eager call leaves the buffer pool's counters and held bytes unchanged,
+    and a call recorded between BeginCapture and EndCapture (where the engine
+    refuses allocations and read-backs, so an allocating call would fail the
+    capture) returns NaN, records a graph, and every replay of that graph
+    clips like an eager ClipGradNorm on the same gradients, bit for bit."""
+    print("no-alloc clip, pool counters and graph capture", flush=True)
+    lib = eng.lib
+    r = rng(7102)
+    grads = [(3 * r.standard_normal(n)).astype(np.float32) for n in (4097, 300, 70_001)]
+    sizes = [g.size for g in grads]
+    hs = [upload(eng, g) for g in grads]
+    ref = [upload(eng, g) for g in grads]
+    try:
+        ga, sa = _arrays(hs, sizes)
+        rga, _ = _arrays(ref, sizes)
+        # eager: no pool request, nothing newly held
+        lib.SyncGPU()
+        lib.ResetPoolStats()
+        held = lib.GetPoolMemory()
+        eng.lib.ClearLastError()
+        n_eager = lib.ClipGradNormNoAlloc(ga, sa, len(hs), 1.0)
+        assert eng.last_error() == "" and n_eager > 1.0
+        assert eng.get_pool_stats() == (0, 0) and lib.GetPoolMemory() == held
+        # recorded
+        for h, g in zip(hs, grads):
+            lib.UpdateBuffer(h, g.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+        assert lib.BeginCapture()
+        assert np.isnan(lib.ClipGradNormNoAlloc(ga, sa, len(hs), 1.0))
+        graph = lib.EndCapture()
+        assert graph, eng.last_error()
+        try:
+            for rep in range(3):
+                # eager work between replays: restore the inputs, clip the
+                # reference copies with the allocating entry point
+                for h, rh, g in zip(hs, ref, grads):
+                    lib.UpdateBuffer(h, g.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+                    lib.UpdateBuffer(rh, g.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+                n_ref = lib.ClipGradNorm(rga, sa, len(ref), 1.0)
+                assert n_ref == n_eager
+                assert lib.ReplayGraph(graph), eng.last_error()
+                lib.SyncGPU()
+                for h, rh, g in zip(hs, ref, grads):
+                    a, b = download(eng, h, g.shape), download(eng, rh, g.shape)
+                    assert np.array_equal(a, b), rep
+                    assert not np.array_equal(a, g)            # the replay clipped
+        finally:
+            lib.ReleaseGraph(graph)
+    finally:
+        release(eng, *hs, *ref)

@@ -39,6 +39,85 @@ def dw_p(rng, P, name, c, k):
     P[name + ".b"] = (0.01 * rng.standard_normal(c)).astype(np.float32)
 
 
+# ------------------------------------------------------------------ decisions
+class DecisionAudit:
+    """Checks the discrete decisions the oracle adopts from the device run.
+
+    The oracle routes gradients through the device's ReLU / ReLU6 masks and
+    max-pool argmax indices, so that an activation within float32 round-off
+    of 0, 6 or a tie cannot send a gradient down another path than the one
+    under test.  Adoption alone would also hide a wrong forward (a positive
+    output zeroed by the device would be zeroed by the oracle too), so every
+    adopted decision is compared with the oracle's own:
+
+    * ReLU (conv + ReLU, bias + ReLU, relu on its input): own = z > 0, where
+      z is the oracle's float64 pre-activation; a disagreement must be a
+      near-tie, |z| <= tie_tol * max|z| of that tensor;
+    * ReLU6: own = 0 < z < 6; near-tie: min(|z|, |z - 6|) <= tie_tol * max|z|;
+    * max-pool: own = the oracle's first-max scan; near-tie: the input values
+      at the two indices differ by <= tie_tol * max|x|.
+
+    It also compares the device's forward values with the oracle's: the
+    device's ReLU-type outputs where both sides call them positive, and the
+    device's relu / relu6 inputs everywhere, relative to max|z| (fwd_tol)."""
+
+    def __init__(self):
+        self.sites = []   # (kind, elements, disagreements, worst tie margin, forward error)
+
+    @staticmethod
+    def _rel(a, scale):
+        return float(a) / scale if scale > 0 else float(a)
+
+    def relu(self, kind, z, dev, dev_is_output):
+        """kind "pos" or "six"; z: oracle pre-activation; dev: the device's
+        values (the ReLU output when dev_is_output, else its input)."""
+        z = np.asarray(z, np.float64)
+        dev = np.asarray(dev, np.float64).reshape(z.shape)
+        scale = float(np.max(np.abs(z))) if z.size else 0.0
+        if kind == "six":
+            mine, theirs = (z > 0) & (z < 6), (dev > 0) & (dev < 6)
+            margin = np.minimum(np.abs(z), np.abs(z - 6.0))
+        else:
+            mine, theirs = z > 0, dev > 0
+            margin = np.abs(z)
+        flips = mine != theirs
+        worst = self._rel(margin[flips].max(), scale) if flips.any() else 0.0
+        both = (mine & theirs) if dev_is_output else np.ones(z.shape, bool)
+        ferr = self._rel(np.abs(dev[both] - z[both]).max(), scale) if both.any() else 0.0
+        self.sites.append((kind, z.size, int(flips.sum()), worst, ferr))
+
+    def pool(self, x, own_idx, dev_idx):
+        x = np.asarray(x, np.float64).reshape(-1)
+        own = np.asarray(own_idx, np.uint32).reshape(-1)
+        dev = np.asarray(dev_idx, np.uint32).reshape(-1)
+        flips = own != dev
+        worst = 0.0
+        if flips.any():
+            scale = float(np.max(np.abs(x)))
+            n = x.size
+            a, b = own[flips].astype(np.int64), dev[flips].astype(np.int64)
+            if (a >= n).any() or (b >= n).any():      # one side found no maximum
+                worst = float("inf")
+            else:
+                worst = self._rel(np.abs(x[a] - x[b]).max(), scale)
+        self.sites.append(("pool", own.size, int(flips.sum()), worst, 0.0))
+
+    def check(self, tie_tol=1e-5, fwd_tol=1e-5):
+        """Assert every disagreement is a near-tie and every forward value is
+        close; returns a one-line summary (the counts) for the test log."""
+        assert self.sites, "no decision was audited"
+        flips = sum(s[2] for s in self.sites)
+        n = sum(s[1] for s in self.sites)
+        worst_tie = max(s[3] for s in self.sites)
+        worst_fwd = max(s[4] for s in self.sites)
+        msg = (f"{len(self.sites)} decision sites, {n} decisions, {flips} disagreements "
+               f"(worst tie margin {worst_tie:.2e}), forward max rel err {worst_fwd:.2e}")
+        for i, (kind, _, nf, tie, fe) in enumerate(self.sites):
+            assert tie <= tie_tol, f"site {i} ({kind}): {nf} disagreements, margin {tie:.3e}; {msg}"
+            assert fe <= fwd_tol, f"site {i} ({kind}): forward error {fe:.3e}; {msg}"
+        return msg
+
+
 # ------------------------------------------------------------------ backends
 class Device:
     """Ops through the drop-in nn_engine module."""
@@ -127,15 +206,12 @@ class Device:
             out.append(idx)
         return out
 
-    def masks(self):
-        """The device's ReLU-type decisions of the last forward (bool arrays,
-        in op order): y > 0 for conv+ReLU and bias+ReLU outputs, x > 0 for
-        relu inputs, 0 < x < 6 for relu6 inputs."""
-        out = []
-        for t, kind in self.mask_nodes:
-            v = t.sync().copy()
-            out.append((v > 0) & (v < 6) if kind == "six" else v > 0)
-        return out
+    def decisions(self):
+        """The device's values at every ReLU-type decision of the last forward,
+        in op order, as (kind, float32 array): the outputs of conv + ReLU and
+        bias + ReLU, the inputs of relu ("pos") and relu6 ("six").  The
+        decision is v > 0 (0 < v < 6 for "six")."""
+        return [(kind, t.sync().copy()) for t, kind in self.mask_nodes]
 
     def grads(self):
         return {k: v.grad.sync().copy() for k, v in self.P.items() if v.grad is not None}
@@ -145,36 +221,56 @@ class Device:
 
 
 class Oracle:
-    """The same ops on the float64 oracle.  `pool_indices` (from the device
-    run) pins maxpool routing to the argmax the device chose."""
+    """The same ops on the float64 oracle.  `pool_indices` and `decisions`
+    (from the device run: Device.pool_indices(), Device.decisions()) pin the
+    max-pool routing and the ReLU / ReLU6 masks to the device's choices, and
+    `audit` (a DecisionAudit) records each adopted decision against the
+    oracle's own; call audit.check() after the forward."""
 
-    def __init__(self, params, pool_indices=None, masks=None):
+    def __init__(self, params, pool_indices=None, decisions=None):
         from oracle import engine64 as E
         self.E = E
         self.P = {k: E.T(v, requires_grad=True) for k, v in params.items()}
         self.pool_indices = list(pool_indices) if pool_indices is not None else None
-        self.masks = list(masks) if masks is not None else None
+        self.decisions = list(decisions) if decisions is not None else None
+        self.audit = DecisionAudit()
         self.rs = {}
 
-    def _mask(self):
-        return self.masks.pop(0) if self.masks else None
+    def _decision(self, expect):
+        if not self.decisions:
+            return None, None
+        kind, v = self.decisions.pop(0)
+        assert kind == expect, (kind, expect)
+        return v, ((v > 0) & (v < 6) if kind == "six" else v > 0)
 
     def input(self, a):
         return self.E.T(a)
 
     def conv(self, x, name, s=1, p=0, act=0):
-        return self.E.conv2d(x, self.P[name + ".w"], self.P[name + ".b"], s, p, act,
-                             mask=self._mask() if act == 1 else None)
+        dev, mask = self._decision("pos") if act == 1 else (None, None)
+        y = self.E.conv2d(x, self.P[name + ".w"], self.P[name + ".b"], s, p, act, mask=mask)
+        if mask is not None:
+            self.audit.relu("pos", y.pre, dev, dev_is_output=True)
+        return y
 
     def maxpool(self, x, k, s):
         idx = self.pool_indices.pop(0) if self.pool_indices else None
-        return self.E.maxpool2d(x, k, s, indices=idx)
+        y = self.E.maxpool2d(x, k, s, indices=idx)
+        if idx is not None:
+            self.audit.pool(x.data, y.own_idx, idx)
+        return y
 
     def relu(self, x):
-        return self.E.relu(x, mask=self._mask())
+        dev, mask = self._decision("pos")
+        if mask is not None:
+            self.audit.relu("pos", x.data, dev, dev_is_output=False)
+        return self.E.relu(x, mask=mask)
 
     def relu6(self, x):
-        return self.E.relu6(x, mask=self._mask())
+        dev, mask = self._decision("six")
+        if mask is not None:
+            self.audit.relu("six", x.data, dev, dev_is_output=False)
+        return self.E.relu6(x, mask=mask)
 
     def sigmoid(self, x):
         return self.E.sigmoid(x)
@@ -185,7 +281,11 @@ class Oracle:
     def linear(self, x, name, relu):
         m = self.E.matmul(x, self.P[name + ".w"])
         if relu:
-            return self.E.bias_relu(m, self.P[name + ".b"], mask=self._mask())
+            dev, mask = self._decision("pos")
+            y = self.E.bias_relu(m, self.P[name + ".b"], mask=mask)
+            if mask is not None:
+                self.audit.relu("pos", y.pre, dev, dev_is_output=True)
+            return y
         return self.E.add_bias(m, self.P[name + ".b"])
 
     def bn(self, x, name):
