@@ -1194,7 +1194,9 @@ __device__ __forceinline__ void tile_coords(const TileGrid& tg, uint32_t& mt, ui
 // lane, and four workgroups per CU (the LDS limit) need the rest of the
 // register file to fit in 64 more.
 template <int MT, int NT>
-constexpr int igemm_min_waves() { return MT * NT == 128 * 128 ? 4 : 1; }
+constexpr int igemm_min_waves() {
+  return MT * NT == 128 * 128 ? 4 : (MT * NT == 256 * 128 ? 2 : 1);
+}
 
 template <int MT, int NT, int KT, class LA, class LB, class EPI>
 __global__ void __launch_bounds__(kThreads)
@@ -1243,40 +1245,36 @@ __global__ void __launch_bounds__(kThreads)
   constexpr bool RA = SA::kRow && (FM == 2 || FM == 4);
   constexpr bool RB = SB::kRow && !TACC && (FN == 2 || FN == 4);
   const int r = lane & 15, g = lane >> 4;
-  // MFMAs of the K tile in LDS stage `cur`.
-  auto compute = [&](int cur) {
+  // Fragments of one 16-deep k slice of LDS stage `cur`, and its MFMAs.
+  struct Frags {
+    f4 a[FM], b[FN];
+  };
+  auto read_slice = [&](int cur, int ks, Frags& f) {
     const float* Ac = As + cur * SA::SIZE;
     const float* Bc = Bs + cur * SB::SIZE;
-    auto slice = [&](int ks) {
-      f4 af[FM], bf[FN];
-      if constexpr (RA) {
-        SA::template frags_rif<FM>(Ac, wm * WM, r, g, ks, af);
-      } else {
-#pragma unroll
-        for (int i = 0; i < FM; ++i) af[i] = SA::frag(Ac, wm * WM + i * 16, r, g, ks);
-      }
-      if constexpr (RB) {
-        SB::template frags_rif<FN>(Bc, wn * WN, r, g, ks, bf);
-      } else {
-#pragma unroll
-        for (int j = 0; j < FN; ++j) bf[j] = SB::frag(Bc, wn * WN + j * 16, r, g, ks);
-      }
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-          for (int j = 0; j < FN; ++j)
-            // TACC: B first, the block accumulates C transposed (see the epilogues).
-            acc[i][j] = TACC ? __builtin_amdgcn_mfma_f32_16x16x4f32(bf[j][s], af[i][s], acc[i][j], 0, 0, 0)
-                             : __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][s], bf[j][s], acc[i][j], 0, 0, 0);
-    };
-    if constexpr (WKS) {
-      slice(16 * wave);
+    if constexpr (RA) {
+      SA::template frags_rif<FM>(Ac, wm * WM, r, g, ks, f.a);
     } else {
 #pragma unroll
-      for (int ks = 0; ks < KT; ks += 16) slice(ks);
+      for (int i = 0; i < FM; ++i) f.a[i] = SA::frag(Ac, wm * WM + i * 16, r, g, ks);
     }
+    if constexpr (RB) {
+      SB::template frags_rif<FN>(Bc, wn * WN, r, g, ks, f.b);
+    } else {
+#pragma unroll
+      for (int j = 0; j < FN; ++j) f.b[j] = SB::frag(Bc, wn * WN + j * 16, r, g, ks);
+    }
+  };
+  auto mfma_slice = [&](const Frags& f) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          // TACC: B first, the block accumulates C transposed (see the epilogues).
+          acc[i][j] = TACC ? __builtin_amdgcn_mfma_f32_16x16x4f32(f.b[j][s], f.a[i][s], acc[i][j], 0, 0, 0)
+                           : __builtin_amdgcn_mfma_f32_16x16x4f32(f.a[i][s], f.b[j][s], acc[i][j], 0, 0, 0);
   };
   if (kb < ke) {
     if constexpr (DA) la.issue_lds(kb, As); else la.load(kb, ra);
@@ -1290,13 +1288,31 @@ __global__ void __launch_bounds__(kThreads)
   for (uint32_t kt = kb; kt < ke; ++kt) {
     const int cur = int(kt - kb) & 1;
     const bool more = kt + 1 < ke;
+    // The first slice's fragments are read before the next tile's loads are
+    // issued: a direct load into LDS that is still in flight would otherwise
+    // make the compiler wait for it before any LDS read.
+    Frags f0;
+    read_slice(cur, WKS ? 16 * wave : 0, f0);
     // Next tile: register staging, or straight into the other LDS stage (its
     // readers finished before the previous barrier).
     if (more) {
       if constexpr (DA) la.issue_lds(kt + 1, As + (cur ^ 1) * SA::SIZE); else la.load(kt + 1, ra);
       if constexpr (DB) lb.issue_lds(kt + 1, Bs + (cur ^ 1) * SB::SIZE); else lb.load(kt + 1, rb);
     }
-    compute(cur);
+    mfma_slice(f0);
+    if constexpr (!WKS) {
+#pragma unroll
+      for (int ks = 16; ks < KT; ks += 16) {
+        Frags f;
+        read_slice(cur, ks, f);
+        mfma_slice(f);
+      }
+    }
+    // Every MFMA of the tile is issued before the wait for the next tile's
+    // loads and the barrier (the scheduler would otherwise hoist them above
+    // part of the MFMAs, and a wave would stall on the loads with MFMA work
+    // still unissued).
+    __builtin_amdgcn_sched_barrier(0);
     if (more) {
       if constexpr (!DA) la.store(As + (cur ^ 1) * SA::SIZE, ra);
       if constexpr (!DB) lb.store(Bs + (cur ^ 1) * SB::SIZE, rb);
@@ -1866,6 +1882,12 @@ static TileCfg choose(const char* var, uint32_t M, uint32_t N, uint32_t kdim, ui
     }
   }
   c.splits = bestS;
+  // A 128 x 256 tile (two workgroups per CU) beats 128 x 128 (four) on the
+  // pixel-row GEMMs whose rows fill whole 128-row tiles and that need split K
+  // to fill the chip: AlexNet b128 c4 / c5 forward and c5 dX 3-5 % faster at
+  // the same split count.  Unsplit ones (c3 forward, the 56x56 single conv)
+  // run as fast or slower on it.
+  if (kt16_only && c.MT == 128 && c.NT == 128 && M % 128 == 0 && c.splits >= 2) c.NT = 256;
   if (const char* e = getenv("DCE_TUNE_LOG")) {
     if (*e && *e != '0')
       fprintf(stderr, "[dcengine] %s M=%u N=%u K=%u -> %dx%dx%d splits %u (occupancy %d)\n", var, M,
@@ -1893,6 +1915,7 @@ static bool tiles_dispatch(const TileCfg& c, F&& f) {
 #define DCE_T(a, b, k) \
   if (c.MT == a && c.NT == b && c.KT == k) return f.template run<a, b, k>();
   DCE_T(128, 128, 32) DCE_T(128, 64, 32) DCE_T(64, 128, 32) DCE_T(64, 64, 32)
+  DCE_T(256, 128, 16) DCE_T(128, 256, 16)
   DCE_T(128, 128, 16) DCE_T(128, 64, 16) DCE_T(64, 128, 16) DCE_T(64, 64, 16)
   DCE_T(32, 128, 16) DCE_T(32, 64, 16) DCE_T(16, 128, 16) DCE_T(16, 64, 16)
   DCE_T(32, 128, 64) DCE_T(32, 64, 64) DCE_T(16, 128, 64) DCE_T(16, 64, 64)
@@ -1907,6 +1930,7 @@ template <class F>
 static bool tiles_dispatch16(const TileCfg& c, F&& f) {
 #define DCE_T(a, b) \
   if (c.MT == a && c.NT == b && c.KT == 16) return f.template run<a, b, 16>();
+  DCE_T(256, 128) DCE_T(128, 256)
   DCE_T(128, 128) DCE_T(128, 64) DCE_T(64, 128) DCE_T(64, 64)
   DCE_T(32, 256) DCE_T(32, 128) DCE_T(16, 256) DCE_T(16, 128)
 #undef DCE_T
@@ -1917,6 +1941,7 @@ template <class F>
 static int tiles_occ16(const TileCfg& c, const F& f) {
 #define DCE_T(a, b) \
   if (c.MT == a && c.NT == b && c.KT == 16) return f.template occ<a, b, 16>(c.splits > 1);
+  DCE_T(256, 128) DCE_T(128, 256)
   DCE_T(128, 128) DCE_T(128, 64) DCE_T(64, 128) DCE_T(64, 64)
   DCE_T(32, 256) DCE_T(32, 128) DCE_T(16, 256) DCE_T(16, 128)
 #undef DCE_T
@@ -1929,6 +1954,7 @@ static int tiles_occ(const TileCfg& c, const F& f) {
 #define DCE_T(a, b, k) \
   if (c.MT == a && c.NT == b && c.KT == k) return f.template occ<a, b, k>(c.splits > 1);
   DCE_T(128, 128, 32) DCE_T(128, 64, 32) DCE_T(64, 128, 32) DCE_T(64, 64, 32)
+  DCE_T(256, 128, 16) DCE_T(128, 256, 16)
   DCE_T(128, 128, 16) DCE_T(128, 64, 16) DCE_T(64, 128, 16) DCE_T(64, 64, 16)
   DCE_T(32, 128, 16) DCE_T(32, 64, 16) DCE_T(16, 128, 16) DCE_T(16, 64, 16)
   DCE_T(32, 128, 64) DCE_T(32, 64, 64) DCE_T(16, 128, 64) DCE_T(16, 64, 64)

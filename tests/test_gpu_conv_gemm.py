@@ -458,7 +458,7 @@ def test_alexnet_b128_conv_backward_full_size(eng, layer):
 
 
 TILE_CFGS = [f"{mt},{nt},{kt},{sp}" for mt in (64, 128) for nt in (64, 128) for kt in (16, 32)
-             for sp in (1, 3)]
+             for sp in (1, 3)] + [f"{mt},{nt},16,{sp}" for mt, nt in ((256, 128), (128, 256)) for sp in (1, 3)]
 
 
 @pytest.mark.parametrize("cfg", TILE_CFGS)
