@@ -232,7 +232,11 @@ def memory_suite(reps=10, trials=5):
     line per kernel: algorithmic bytes per launch (each required tensor read
     or written once), the time per launch of `reps` back-to-back launches
     (one HIP-event pair around them; the median of `trials` such runs), GB/s
-    and fraction of 8 TB/s."""
+    and fraction of 8 TB/s; and the same for a single launch with cold caches
+    (`us_cold`, `frac_hbm_cold`): before each timed launch a 1 GiB read pass
+    (the norm's sum of squares over a 1 GiB tensor) evicts the operands from
+    the 256 MiB MALL and the L2s, so the launch reads HBM, as a kernel inside
+    a training step whose working set exceeds the MALL does."""
     from directcompute_torch_amd import nn_engine as nn
     lib = nn.lib
     rng = np.random.default_rng(SEED + 7)
@@ -258,6 +262,15 @@ def memory_suite(reps=10, trials=5):
         return n.value, ms.value
 
     out = []
+    flush_n = 1 << 28                           # 1 GiB of floats, read by the cold-cache flush
+    flush_h = lib.CreateBuffer(None, flush_n)
+    held.append(flush_h)
+    lib.ClearBuffer(flush_h)
+    flush_g = (ctypes.c_void_p * 1)(flush_h)
+    flush_s = (ctypes.c_uint * 1)(flush_n)
+
+    def flush():
+        lib.ClipGradNorm(flush_g, flush_s, 1, 1e30)   # reads 1 GiB; a zero norm scales nothing
 
     def run(kernel, family, shape, nbytes, fn, per_launch=False):
         # One event pair around `reps` back-to-back launches (an event pair per
@@ -287,9 +300,31 @@ def memory_suite(reps=10, trials=5):
             per.append(ms / (max(n, 1) if per_launch else reps) * 1e3)
         us = float(np.median(per))
         gbps = nbytes / (us * 1e-6) / 1e9 if us > 0 else 0.0
+        cold = []
+        for _ in range(trials):
+            flush()
+            lib.SyncGPU()
+            lib.ResetProfile()
+            if per_launch:
+                lib.SetProfiling(1)
+            else:
+                lib.BeginProfileRegion(family.encode(), 0.0, float(nbytes))
+            fn()
+            if per_launch:
+                lib.SyncGPU()
+                lib.SetProfiling(0)
+            else:
+                lib.EndProfileRegion()
+            lib.SyncGPU()
+            n, ms = prof(family)
+            cold.append(ms / max(n, 1) * 1e3 if per_launch else ms * 1e3)
+        us_c = float(np.median(cold))
+        gbps_c = nbytes / (us_c * 1e-6) / 1e9 if us_c > 0 else 0.0
         rec = {"suite": "memory", "kernel": kernel, "family": family, "shape": list(shape),
                "bytes_per_launch": int(nbytes), "us": round(us, 2), "GB/s": round(gbps, 1),
-               "frac_hbm": round(gbps * 1e9 / HBM_PEAK_BYTES_PER_S, 4)}
+               "frac_hbm": round(gbps * 1e9 / HBM_PEAK_BYTES_PER_S, 4),
+               "us_cold": round(us_c, 2), "GB/s_cold": round(gbps_c, 1),
+               "frac_hbm_cold": round(gbps_c * 1e9 / HBM_PEAK_BYTES_PER_S, 4)}
         out.append(rec)
         print(json.dumps(rec), flush=True)
 
@@ -358,7 +393,7 @@ def memory_suite(reps=10, trials=5):
         nx, no = B * C * H * W, B * C * OH * OW
         pidx = ctypes.c_void_p()
         held.append(lib.MaxPoolForwardFused(xin, B, C, H, W, k, st, ctypes.byref(pidx)))
-        for _ in range(trials * reps + 1):
+        for _ in range(trials * (reps + 1) + 1):   # warm runs, cold runs and the first call
             lib.AddRefBuffer(pidx.value)
 
         def mp(idx=pidx.value, dz=dz, B=B, C=C, OH=OH, OW=OW, nx=nx):
@@ -433,10 +468,13 @@ def memory_suite(reps=10, trials=5):
     for h in held:
         lib.ReleaseBuffer(h)
     fr = [r["frac_hbm"] for r in out if r["bytes_per_launch"] >= 64 << 20]
+    fc = [r["frac_hbm_cold"] for r in out if r["bytes_per_launch"] >= 64 << 20]
     print(json.dumps({"suite": "memory", "summary": {
         "kernels": len(out), "kernels_over_64MiB": len(fr),
         "median_frac_hbm_over_64MiB": round(float(np.median(fr)), 4) if fr else None,
-        "min_frac_hbm_over_64MiB": round(float(min(fr)), 4) if fr else None}}), flush=True)
+        "min_frac_hbm_over_64MiB": round(float(min(fr)), 4) if fr else None,
+        "median_frac_hbm_cold_over_64MiB": round(float(np.median(fc)), 4) if fc else None,
+        "min_frac_hbm_cold_over_64MiB": round(float(min(fc)), 4) if fc else None}}), flush=True)
 
 
 def _prof_all(lib):

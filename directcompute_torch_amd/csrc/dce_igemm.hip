@@ -1883,17 +1883,36 @@ static TileCfg choose(const char* var, uint32_t M, uint32_t N, uint32_t kdim, ui
   }
   c.splits = bestS;
   // A 128 x 256 tile (two workgroups per CU) beats 128 x 128 (four) on the
-  // pixel-row GEMMs whose rows fill whole 128-row tiles and that need split K
-  // to fill the chip: AlexNet b128 c4 / c5 forward and c5 dX 3-5 % faster at
-  // the same split count.  Unsplit ones (c3 forward, the 56x56 single conv)
-  // run as fast or slower on it.
-  if (kt16_only && c.MT == 128 && c.NT == 128 && M % 128 == 0 && c.splits >= 2) c.NT = 256;
+  // pixel-row GEMMs whose rows fill whole 128-row tiles, that need split K to
+  // fill the chip and whose 128 x 256 grid still gives every CU about two
+  // workgroups: AlexNet b128 c4 / c5 forward and c5 dX (510 workgroups) 3-5 %
+  // faster at the same split count.  Unsplit ones (c3 forward, the 56x56
+  // single conv) run as fast or slower on it, and small grids (UNet's 32x32
+  // and 16x16 levels: 64-384 workgroups) lose up to half their speed.
+  if (kt16_only && c.MT == 128 && c.NT == 128 && M % 128 == 0 && c.splits >= 2 &&
+      uint64_t(cdiv(M, 128)) * cdiv(N, 256) * c.splits * 8 >= uint64_t(num_cus()) * 15)
+    c.NT = 256;
   if (const char* e = getenv("DCE_TUNE_LOG")) {
     if (*e && *e != '0')
       fprintf(stderr, "[dcengine] %s M=%u N=%u K=%u -> %dx%dx%d splits %u (occupancy %d)\n", var, M,
               N, kdim, c.MT, c.NT, c.KT, c.splits, occ(c));
   }
   return c;
+}
+
+// Pixel-row GEMMs (forward, dX) of convolutions with few channels on small
+// images: at most 128 output rows, dot products of at most 1152 (128
+// channels x 3 x 3) and at most 131072 pixels (UNet-base16 b8 below the
+// 256^2 level).  The cost model prices their K tiles at its 2 us latency
+// floor and splits them 4-7 ways or runs them on 128-row tiles (M = 96);
+// measured, unsplit 32-row tiles over more workgroups are 10-20 % faster
+// (UNet levels 1-3: 36-41 -> 31-36 us per layer, M = 96 dX 92 -> 73 us).
+// An override through DCE_TUNE_* keeps its tile.
+static void narrow_short_k(TileCfg& c, const char* var, uint32_t M, uint32_t N, uint32_t kdim) {
+  if (const char* e = getenv(var))
+    if (*e) return;
+  if (M > 128 || kdim > 1152 || N > 131072) return;
+  c = TileCfg{M <= 16 ? 16 : 32, 128, 16, 1};
 }
 
 template <int MT, int NT, int KT, class LA, class LB, class EPI>
@@ -2650,12 +2669,13 @@ bool conv_forward(const float* x, float* x_nhwc_keep, const float* w, const floa
   const uint32_t N = g.B * g.OH * g.OW;
   if (!operand_fits(nx, "conv_forward") || !operand_fits(size_t(g.OC) * kdim, "conv_forward"))
     return false;
-  const TileCfg cfg = choose(
+  TileCfg cfg = choose(
       "DCE_TUNE_FWD", g.OC, N, kdim, 8, true,
       [&](const TileCfg& t) {
         return pk ? tiles_occ16(t, FwdPkRun{}) : conv_variant_occ<FwdRun>(s1, blk, t);
       },
       true);
+  if (!pk) narrow_short_k(cfg, "DCE_TUNE_FWD", g.OC, N, kdim);
   const size_t nw = al64(size_t(g.OC) * kdim);
   const size_t nxs = x_nhwc_keep ? 0 : al64(nx);
   const size_t nP = cfg.splits > 1 ? size_t(cfg.splits) * g.OC * N : 0;
@@ -2987,6 +3007,7 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
     dxc = choose(
         "DCE_TUNE_DX", g.C, g.B * HW, KK * OCp, 8, true,
         [&](const TileCfg& t) { return conv_variant_occ<DxRun>(g.s == 1, blk, t); }, true);
+    narrow_short_k(dxc, "DCE_TUNE_DX", g.C, g.B * HW, KK * OCp);
     nW = al64(size_t(g.C) * KK * OCp);
     nQ = dxc.splits > 1 ? size_t(dxc.splits) * g.C * g.B * HW : 0;
   }
