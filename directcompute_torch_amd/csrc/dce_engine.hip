@@ -213,6 +213,32 @@ static void resolve_profile() {
 // instead of freeing the excess (a stream drain each) and allocating again.
 static size_t max_pool_for_size(uint32_t) { return 4096; }
 
+// Producer tags (Buffer::tag).  A new tag gets a fresh generation; dropping
+// one releases the buffer it owns.
+static uint64_t g_gen = 0;
+static void set_tag(Buffer* b, uint32_t tag) {
+  b->tag = tag;
+  b->gen = ++g_gen;
+}
+// park: the owned buffer goes back to the pool even past the pool's byte
+// cap, so that the call frees nothing (the no-allocation entry point).
+static void park_buffer(Buffer* b);
+static void drop_tag(Buffer* b, bool park = false) {
+  b->tag = 0;
+  b->src = b->aux = nullptr;
+  if (Buffer* s = b->side) {
+    b->side = nullptr;
+    if (park) park_buffer(s); else release_buffer(s);
+  }
+}
+// Buffers an entry point writes in place lose their tags.
+static void drop_tags(void** hs, uint32_t n, bool park = false) {
+  for (uint32_t i = 0; hs && i < n; ++i) {
+    Buffer* b = static_cast<Buffer*>(hs[i]);
+    if (b && b->magic == kMagicLive) drop_tag(b, park);
+  }
+}
+
 static void free_record(Buffer* b) {
   // The stream may still reference the memory: drain it first.
   hipStreamSynchronize(g_stream);
@@ -334,6 +360,8 @@ static Buffer* alloc_record(uint32_t count) {
   b->refCount = 1;
   b->magic = kMagicLive;
   b->tag = 0;
+  b->gen = 0;
+  b->src = b->aux = b->side = nullptr;
   return b;
 }
 
@@ -372,16 +400,29 @@ void* create_buffer(const float* data, uint32_t count) {
 }
 
 static void release_internal(Buffer* b) {
+  drop_tag(b);
   auto& pool = g_pool[b->count];
   uint64_t bytes = uint64_t(b->count) * 4;
   if (pool.size() < max_pool_for_size(b->count) && g_poolBytes + bytes <= g_poolCapBytes) {
     b->magic = kMagicPooled;
-    b->tag = 0;
     pool.push_back(b);
     g_poolBytes += bytes;
   } else {
     free_record(b);
   }
+}
+
+static void park_buffer(Buffer* b) {
+  if (--b->refCount > 0) return;
+  if (g_capturing) {
+    b->refCount = 1;
+    g_captureHeld.push_back(b);
+    return;
+  }
+  drop_tag(b, true);
+  b->magic = kMagicPooled;
+  g_pool[b->count].push_back(b);
+  g_poolBytes += uint64_t(b->count) * 4;
 }
 
 void release_buffer(void* h) {
@@ -531,7 +572,7 @@ void UpdateBuffer(void* handle, float* data) {
   if (!handle || !data || !g_init) return;
   Buffer* b = as_buffer(handle, "UpdateBuffer");
   if (!b) return;
-  b->tag = 0;  // the contents are the caller's now
+  drop_tag(b);  // the contents are the caller's now
   upload(b->ptr, data, b->count);
 }
 
@@ -551,7 +592,7 @@ void ClearBuffer(void* handle) {
   if (!handle || !g_init) return;
   Buffer* b = as_buffer(handle, "ClearBuffer");
   if (!b) return;
-  b->tag = 0;
+  drop_tag(b);
   fill_zero(b->ptr, b->count);
 }
 
@@ -612,7 +653,7 @@ bool CompileShaderEx(const char* name, const wchar_t* path, const char* entry) {
 static void run_entry(const ShaderEntry* e, const Dispatch& d) {
   for (uint32_t i = 0; d.uavs && i < d.nU; ++i) {
     Buffer* b = static_cast<Buffer*>(d.uavs[i]);
-    if (b && b->magic == kMagicLive) b->tag = 0;
+    if (b && b->magic == kMagicLive) drop_tag(b);
   }
   e->fn(d);
 }
@@ -774,6 +815,16 @@ void* ConvForwardFused(void* x, void* filters, void* bias, uint32_t batch, uint3
     K->meta[4] = xcopy_tag(g);
     *pIm2col = keep;
   }
+  if (actType == 1 && conv_g_layout(g) == kGLayoutPad) {
+    // A max-pool over this output can then make its backward's masked G.
+    Buffer* Y = static_cast<Buffer*>(out);
+    set_tag(Y, kReluOutTag);
+    Y->meta[0] = conv_g_layout(g);
+    Y->meta[1] = batch;
+    Y->meta[2] = outC;
+    Y->meta[3] = g.OH;
+    Y->meta[4] = g.OW;
+  }
   return out;
 }
 
@@ -801,6 +852,20 @@ void ConvBackwardFused(void* gradOut, void* fwdOut, void* x, void* filters, void
       set_error("ConvBackwardFused: buffer smaller than geometry");
     } else {
       const float* yp = Y ? Y->ptr : nullptr;
+      // dy from MaxPoolBackwardFused over this very output (unchanged since):
+      // its masked G is already made.
+      PreG pre{};
+      const PreG* pp = nullptr;
+      if (Y && DY->tag == kGradGTag && DY->side && DY->src == Y &&
+          tag_alive(Y, kReluOutTag, DY->srcGen) && DY->meta[0] == conv_g_layout(g) &&
+          DY->meta[1] == batch && DY->meta[2] == outC && DY->meta[3] == g.OH &&
+          DY->meta[4] == g.OW) {
+        pre.layout = DY->meta[0];
+        pre.g = DY->side->ptr;
+        pre.db = pre.g + g_side_floats(pre.layout, batch, outC, g.OH, g.OW);
+        pre.dbRows = DY->aux32;
+        pp = &pre;
+      }
       const float* xn = nullptr;
       if (im2col) {
         Buffer* Kb = static_cast<Buffer*>(im2col);
@@ -818,7 +883,7 @@ void ConvBackwardFused(void* gradOut, void* fwdOut, void* x, void* filters, void
         good = conv_backward(DY->ptr, yp, X->ptr, xn, Wt->ptr,
                              dW ? static_cast<Buffer*>(dW)->ptr : nullptr,
                              dB ? static_cast<Buffer*>(dB)->ptr : nullptr,
-                             dX ? static_cast<Buffer*>(dX)->ptr : nullptr, g);
+                             dX ? static_cast<Buffer*>(dX)->ptr : nullptr, g, pp);
       if (good) {
         if (pDFilters) *pDFilters = dW;
         if (pDBias) *pDBias = dB;
@@ -866,11 +931,22 @@ void* MaxPoolForwardFused(void* x, uint32_t batch, uint32_t inC, uint32_t inH, u
     release_buffer(idx);
     return nullptr;
   }
-  I->tag = kPoolTag;
+  set_tag(I, kPoolTag);
   I->meta[0] = inH;
   I->meta[1] = inW;
   I->meta[2] = poolSize;
   I->meta[3] = stride;
+  // Links for the masked backward: the pooled values, and the input when it
+  // is a ReLU conv output of this geometry.
+  Buffer* P = static_cast<Buffer*>(out);
+  set_tag(P, kPoolOutTag);
+  I->aux = P;
+  I->auxGen = P->gen;
+  if (X->tag == kReluOutTag && X->meta[1] == batch && X->meta[2] == inC && X->meta[3] == inH &&
+      X->meta[4] == inW) {
+    I->src = X;
+    I->srcGen = X->gen;
+  }
   if (pIndices)
     *pIndices = idx;
   else
@@ -899,8 +975,40 @@ void* MaxPoolBackwardFused(void* gradOut, void* indices, uint32_t batch, uint32_
           (m[0] - m[2]) / m[3] + 1 == outH && (m[1] - m[2]) / m[3] + 1 == outW) {
         H = m[0]; W = m[1]; k = m[2]; s = m[3];
       }
-      if (!maxpool_backward(DZ->ptr, I->ptr, static_cast<Buffer*>(dx)->ptr, batch, inC, outH,
-                            outW, xSize, H, W, k, s)) {
+      // Over a ReLU conv output (unchanged since the forward, as are the
+      // pooled values): also the conv backward's masked G, owned by dx.
+      Buffer* DX = static_cast<Buffer*>(dx);
+      Buffer* X = H ? I->src : nullptr;
+      const uint32_t lay = X ? X->meta[0] : 0;
+      Buffer* side = nullptr;
+      if (X && tag_alive(X, kReluOutTag, I->srcGen) && tag_alive(I->aux, kPoolOutTag, I->auxGen) &&
+          I->aux->count >= n && maxpool_backward_g_ok(inC, H, W, outH, outW, k, s, lay)) {
+        const size_t nG = g_side_floats(lay, batch, inC, H, W);
+        const uint32_t rows = maxpool_backward_g_rows(batch, H, W, lay);
+        const size_t total = nG + size_t(rows) * inC;
+        if (total < 0xFFFFFFFFull) side = static_cast<Buffer*>(create_buffer(nullptr, uint32_t(total)));
+        if (side) {
+          if (maxpool_backward_g(DZ->ptr, I->ptr, I->aux->ptr, DX->ptr, side->ptr, side->ptr + nG,
+                                 batch, inC, outH, outW, H, W, k, lay, (W + 3u) & ~3u)) {
+            set_tag(DX, kGradGTag);
+            DX->side = side;
+            DX->src = X;
+            DX->srcGen = X->gen;
+            DX->meta[0] = lay;
+            DX->meta[1] = batch;
+            DX->meta[2] = inC;
+            DX->meta[3] = H;
+            DX->meta[4] = W;
+            DX->aux32 = rows;
+          } else {
+            release_buffer(side);
+            release_buffer(dx);
+            dx = nullptr;
+          }
+        }
+      }
+      if (dx && !side &&
+          !maxpool_backward(DZ->ptr, I->ptr, DX->ptr, batch, inC, outH, outW, xSize, H, W, k, s)) {
         release_buffer(dx);
         dx = nullptr;
       }
@@ -915,12 +1023,14 @@ void* MaxPoolBackwardFused(void* gradOut, void* indices, uint32_t batch, uint32_
 void SGDBatch(void** params, void** grads, uint32_t* sizes, uint32_t numParams, float lr,
               float clip) {
   if (!g_init || !params || !grads || !sizes || !numParams) return;
+  drop_tags(params, numParams);
   sgd_multi(params, grads, sizes, numParams, lr, clip);
 }
 
 float SGDBatchClipped(void** params, void** grads, uint32_t* sizes, uint32_t numParams,
                       float lr, float maxNorm) {
   if (!g_init || !params || !grads || !sizes || !numParams) return 0.0f;
+  drop_tags(params, numParams);
   float* d_ns = g_misc;  // [norm, scale]
   if (!grad_norm_multi(grads, sizes, numParams, maxNorm, d_ns)) return 0.0f;
   if (!sgd_scaled_multi(params, grads, sizes, numParams, lr, d_ns)) return 0.0f;
@@ -935,12 +1045,16 @@ void AdamBatch(void** params, void** grads, void** m, void** v, uint32_t* sizes,
                uint32_t numParams, float stepSize, float beta1, float beta2, float eps,
                float weightDecay, float clip) {
   if (!g_init || !params || !grads || !m || !v || !sizes || !numParams) return;
+  drop_tags(params, numParams);
+  drop_tags(m, numParams);
+  drop_tags(v, numParams);
   adam_multi(params, grads, m, v, sizes, numParams, stepSize, beta1, beta2, eps, weightDecay,
              clip);
 }
 
 float ClipGradNorm(void** grads, uint32_t* sizes, uint32_t numGrads, float maxNorm) {
   if (!g_init || !grads || !sizes || !numGrads) return 0.0f;
+  drop_tags(grads, numGrads);
   float* ns = g_misc;  // [norm, scale]
   if (!grad_norm_multi(grads, sizes, numGrads, maxNorm, ns)) return 0.0f;
   if (!scale_grads_multi(grads, sizes, numGrads, ns)) return 0.0f;
@@ -955,6 +1069,9 @@ void AdamBatchCounted(void** params, void** grads, void** m, void** v, uint32_t*
                       uint32_t numParams, void* stepState, uint32_t t, float stepSize, double lr,
                       double beta1, double beta2, float eps, float weightDecay, float clip) {
   if (!g_init || !params || !grads || !m || !v || !sizes || !numParams) return;
+  drop_tags(params, numParams);
+  drop_tags(m, numParams);
+  drop_tags(v, numParams);
   Buffer* st = as_buffer(stepState, "AdamBatchCounted(stepState)");
   if (!st) return;
   if (st->count < 2) {
@@ -971,6 +1088,7 @@ float ClipGradNormNoAlloc(void** grads, uint32_t* sizes, uint32_t numGrads, floa
     return -1.0f;
   }
   if (!grads || !sizes || !numGrads) return 0.0f;
+  drop_tags(grads, numGrads, true);
   return clip_grad_norm_noalloc(g_device, grads, sizes, numGrads, maxNorm, g_capturing);
 }
 

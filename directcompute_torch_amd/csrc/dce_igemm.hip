@@ -2935,8 +2935,12 @@ static bool conv_backward_pw(const float* dy, const float* x, const float* w, fl
   return true;
 }
 
+uint32_t conv_g_layout(const ConvGeom& g) { return ps_x(g) ? kGLayoutPad : kGLayoutNhwc; }
+uint32_t conv_g_pad_width(const ConvGeom& g) { return ps_geom(g).OWp; }
+
 bool conv_backward(const float* dy, const float* y, const float* x, const float* x_nhwc,
-                   const float* w, float* dw, float* db, float* dx, const ConvGeom& g) {
+                   const float* w, float* dw, float* db, float* dx, const ConvGeom& g,
+                   const PreG* pre) {
   // Pointwise layers with no ReLU mask (and dW requested whenever db is: the
   // bias gradient is the dW product's ones column) read NCHW in place.
   if (pw_x(g)) {
@@ -2972,12 +2976,15 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
   // G of the transpose pass.  Other layouts use the NHWC G for both.
   const PsGeom q = ps ? ps_geom(g) : PsGeom{};
   const bool useGpad = ps && (dw || (db && !dx)), useGnhwc = !ps || dx;
+  // A G_pad made by dy's producer (with its bias-gradient partials) replaces
+  // the masking pass that makes it.
+  const bool preG = pre && pre->layout == kGLayoutPad && useGpad;
   const uint32_t nchunk = ps ? cdiv(q.OHWp, kMaskChunk) : 0;
   const uint32_t dbRows = useGpad ? g.B * nchunk : g.B * npb;
   const uint32_t dwK = ps ? g.B * q.OHWp : npix;  // dW GEMM K extent (pixels)
   const size_t nG = useGnhwc ? al64(size_t(npix) * OCp) : 0;
-  const size_t nGp = useGpad ? al64(size_t(g.B) * g.OC * q.OHWp) : 0;
-  const size_t nDb = db ? al64(size_t(dbRows) * g.OC) : 0;
+  const size_t nGp = (useGpad && !preG) ? al64(size_t(g.B) * g.OC * q.OHWp) : 0;
+  const size_t nDb = (db && !preG) ? al64(size_t(dbRows) * g.OC) : 0;
   const size_t nX = (dw && !x_nhwc) ? al64(xbuild_floats(g)) : 0;
   if (ps && !operand_fits(nGp, "conv_backward")) return false;
   TileCfg dwc{128, 128, 16, 1}, dxc{128, 128, 16, 1};
@@ -3020,8 +3027,12 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
   float* part = xs + nX;
   float* wt = part + nP;
   float* qpart = wt + nW;
+  if (preG) {
+    gp = const_cast<float*>(pre->g);
+    if (db) dbPart = const_cast<float*>(pre->db);
+  }
 
-  if (useGpad) {
+  if (useGpad && !preG) {
     bool ok = false;
     mask_pad(dy, y, gp, dbPart, g, &ok);
     if (!ok) return false;
@@ -3033,7 +3044,7 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
   if (useGnhwc && !to_nhwc_masked(dy, y, gn, useGpad ? nullptr : dbPart, g.B, g.OC, OHW, &npbGot,
                                   dx ? dxPerm : WPerm{}))
     return false;
-  const uint32_t dbRowsGot = useGpad ? dbRows : g.B * npbGot;
+  const uint32_t dbRowsGot = preG ? pre->dbRows : (useGpad ? dbRows : g.B * npbGot);
   if (db && !dw) {
     hipLaunchKernelGGL(k_rowsum, dim3(g.OC), dim3(256), 0, stream(), dbPart, db, dbRowsGot);
     if (!check_launch("bias_grad")) return false;

@@ -25,11 +25,52 @@ struct Buffer {
   //            backward can run as a deterministic gather;
   //  kNhwcTag: channel-innermost copy of a conv input kept by
   //            ConvForwardFused as its "im2col" handle, meta = {B, C, H, W, Cp}.
+  //  kReluOutTag: output of a ReLU ConvForwardFused whose backward reads its
+  //            masked gradient on the padded pixel grid (fewer than 4 input
+  //            channels), meta = {kGLayoutPad, B, OC, OH, OW};
+  //  kPoolOutTag: output of MaxPoolForwardFused (its values are the
+  //            windows' maxima, which the masked max-pool backward reads);
+  //  kGradGTag: gradient written by MaxPoolBackwardFused for a ReLU conv
+  //            output (src): `side` holds that conv's masked gradient G in
+  //            the layout its backward reads, followed by bias-gradient
+  //            partials, meta = {layout, B, OC, OH, OW}, aux32 = partial rows.
+  // A tag is dropped (drop_tag) whenever the buffer is written by anything
+  // but its producer, and when the buffer goes back to the pool.
   uint32_t tag;
   uint32_t meta[5];
+  // Tag identity: a fresh value of a global counter each time a tag is set,
+  // so that a link to another buffer (src, aux) stays valid only while that
+  // buffer still carries the tag it had when the link was made (records are
+  // recycled, never deleted).
+  uint64_t gen;
+  Buffer* src;      // kPoolTag: the pooled input (ReLU conv output); kGradGTag: that conv output
+  uint64_t srcGen;
+  Buffer* aux;      // kPoolTag: the pooled output
+  uint64_t auxGen;
+  Buffer* side;     // kGradGTag: owned buffer [G | bias-gradient partials]
+  uint32_t aux32;
 };
 constexpr uint32_t kPoolTag = 0x9001u;
 constexpr uint32_t kNhwcTag = 0x9002u;
+constexpr uint32_t kReluOutTag = 0x9003u;
+constexpr uint32_t kPoolOutTag = 0x9004u;
+constexpr uint32_t kGradGTag = 0x9005u;
+// Layouts of a conv backward's masked gradient G.
+constexpr uint32_t kGLayoutPad = 1;   // [B*OC][OH][pad4(OW)], zero past OW (stride-phase dW)
+constexpr uint32_t kGLayoutNhwc = 2;  // [B*OH*OW][pad4(OC)] (the transpose pass)
+
+// Floats of G in `layout` for a conv output [B][C][H][W], rounded up to 64
+// (the bias-gradient partials follow it in a kGradGTag side buffer).
+inline size_t g_side_floats(uint32_t layout, uint32_t B, uint32_t C, uint32_t H, uint32_t W) {
+  (void)layout;  // kGLayoutPad
+  const size_t n = size_t(B) * C * H * ((W + 3u) & ~3u);
+  return (n + 63) & ~size_t(63);
+}
+
+// Does buffer `b` still carry tag `tag` of generation `gen`?
+inline bool tag_alive(const Buffer* b, uint32_t tag, uint64_t gen) {
+  return b && b->magic == kMagicLive && b->tag == tag && b->gen == gen;
+}
 
 // A bounds-carrying view used by the RunShader-compatible kernels: reads past
 // `n` return 0 and writes past `n` are dropped, like D3D11 structured buffers.
@@ -308,11 +349,26 @@ uint32_t xcopy_tag(const ConvGeom& g);
 // the copy of x (xcopy_floats(g) floats) for a later backward.
 bool conv_forward(const float* x, float* x_nhwc_keep, const float* w, const float* bias,
                   float* y, const ConvGeom& g, uint32_t act);
+// The layout of G that conv_backward reads for this geometry (kGLayoutPad or
+// kGLayoutNhwc), and the padded row width of kGLayoutPad.
+uint32_t conv_g_layout(const ConvGeom& g);
+uint32_t conv_g_pad_width(const ConvGeom& g);
+// A masked gradient G made by the producer of dy (the max-pool backward):
+// g in `layout` (kGLayoutPad), db = bias-gradient partials [OC][dbRows].
+struct PreG {
+  uint32_t layout;
+  const float* g;
+  const float* db;
+  uint32_t dbRows;
+};
 // dW[OC, C, k, k], db[OC], dX (NCHW) from G = dy masked by y (> 0 kept; y may
 // be null: no mask).  Any of dw, db, dx may be null (not requested).
-// x_nhwc, when not null, is the copy of x produced by conv_forward.
+// x_nhwc, when not null, is the copy of x produced by conv_forward.  pre, when
+// not null, is G (of dy masked by y) already made: the pass that would make
+// it from dy and y is skipped.
 bool conv_backward(const float* dy, const float* y, const float* x, const float* x_nhwc,
-                   const float* w, float* dw, float* db, float* dx, const ConvGeom& g);
+                   const float* w, float* dw, float* db, float* dx, const ConvGeom& g,
+                   const PreG* pre = nullptr);
 // C[M,N] = op(A)·op(B); flags bit0: A stored K×M, bit1: B stored N×K.
 bool gemm(const float* a, const float* b, float* c, uint32_t M, uint32_t K,
           uint32_t N, uint32_t flags);
@@ -337,6 +393,19 @@ bool maxpool_forward(const float* x, float* out, float* idx, uint32_t B, uint32_
 bool maxpool_backward(const float* dz, const float* idx, float* dx, uint32_t B,
                       uint32_t C, uint32_t OH, uint32_t OW, uint32_t xcount,
                       uint32_t H, uint32_t W, uint32_t k, uint32_t s);
+// Max-pool backward over a ReLU conv output (stride 2, windows of 2 or 3):
+// dx as maxpool_backward, and the conv backward's masked gradient G of dx
+// (masked where the window maximum `pooled` is <= 0, which is the conv
+// output at the window's argmax) on the padded pixel grid (layout
+// kGLayoutPad, rows of gw = pad4(W) floats), with bias-gradient partials
+// db[C][rows]; maxpool_backward_g_rows gives rows.  maxpool_backward_g_ok
+// tells whether a geometry and layout are supported.
+bool maxpool_backward_g_ok(uint32_t C, uint32_t H, uint32_t W, uint32_t OH, uint32_t OW,
+                           uint32_t k, uint32_t s, uint32_t layout);
+uint32_t maxpool_backward_g_rows(uint32_t B, uint32_t H, uint32_t W, uint32_t layout);
+bool maxpool_backward_g(const float* dz, const float* idx, const float* pooled, float* dx,
+                        float* g, float* db, uint32_t B, uint32_t C, uint32_t OH, uint32_t OW,
+                        uint32_t H, uint32_t W, uint32_t k, uint32_t layout, uint32_t gw);
 
 // Shader registry (dce_kernels.hip).
 struct Dispatch {

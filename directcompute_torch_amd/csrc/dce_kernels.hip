@@ -1112,88 +1112,179 @@ __global__ void k_maxpool_bwd_gather_n(const float* __restrict__ dz,
   dx[i] = acc;
 }
 
-// Block form: a thread owns an S x S block of inputs (rows aS.., cols bS..),
-// which the windows o in [a - (K-1)/S, a] x [b - (K-1)/S, b] cover; it loads
-// each of those NW x NW (index, value) pairs once.  A window whose recorded
-// argmax is input i necessarily contains i, so every input of the block adds
-// the values of the matching windows, in (oh, ow) order as above.
+// The windows covering the S x S input block (a, b) of one plane: a thread
+// owns the block and loads the NW x NW windows o in [a - (K-1)/S, a] x
+// [b - (K-1)/S, b] once, as (argmax index, value) pairs; with MASK also each
+// window's maximum.  A window whose recorded argmax is input i necessarily
+// contains i, so every input of the block adds the values of the matching
+// windows, in (oh, ow) order (sum).
 // PAIR (NW == 2, OW >= 2): the two window columns b-1, b of a window row are
-// one 8-byte load at column ps = clamp(b-1, 0, OW-2), and a block row's S = 2
-// outputs one 8-byte store whenever both lie in the row.  These addresses are
+// one 8-byte load at column ps = clamp(b-1, 0, OW-2).  These addresses are
 // only 4-byte aligned when rows have odd length; the GPU runs with unaligned
 // access enabled, and halving the memory instructions takes the AlexNet
 // 55x55 backward from 35 to 25 us (warm) and 51 to 38 us (cold caches).
+// MASK (a max-pool over a ReLU conv output): the maximum of a window is the
+// conv output at its argmax, so the conv backward's mask (output <= 0 ->
+// gradient 0) is known per window: sum<true> adds only the windows whose
+// maximum is not <= 0.  Every window routed to input i has the same maximum
+// (that input's value), so sum<true>(i) is either sum<false>(i), bit for bit,
+// or 0.
+template <int K, int S, bool PAIR, bool MASK>
+struct PoolWin {
+  static constexpr int NW = (K - 1) / S + 1;
+  static_assert(!PAIR || (NW == 2 && S == 2), "pair loads cover two window columns");
+  uint32_t id[NW][NW];
+  float v[NW][NW];
+  bool keep[NW][NW];
+
+  __device__ __forceinline__ void load(const float* __restrict__ dz,
+                                       const uint32_t* __restrict__ idx,
+                                       const float* __restrict__ pooled, uint32_t plane,
+                                       uint32_t a, uint32_t b, uint32_t OH, uint32_t OW) {
+    if constexpr (PAIR) {
+      typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+      const uint32_t ps = min(max(int(b) - 1, 0), int(OW) - 2);
+      const bool lok = b >= 1, rok = b < OW;
+      const bool li = b == OW, ri = b != 0;  // element of the pair holding column b-1 / b
+#pragma unroll
+      for (int wa = 0; wa < NW; ++wa) {
+        const int oh = int(a) - (NW - 1) + wa;
+        const bool hok = oh >= 0 && oh < int(OH);
+        const uint32_t o = (plane * OH + uint32_t(hok ? oh : 0)) * OW + ps;
+        const u2 iv = ldu<u2>(idx + o);
+        const f2 dv = ldu<f2>(dz + o);
+        id[wa][0] = (hok && lok) ? (li ? iv[1] : iv[0]) : 0xFFFFFFFFu;
+        id[wa][1] = (hok && rok) ? (ri ? iv[1] : iv[0]) : 0xFFFFFFFFu;
+        v[wa][0] = li ? dv[1] : dv[0];
+        v[wa][1] = ri ? dv[1] : dv[0];
+        if constexpr (MASK) {
+          const f2 pv = ldu<f2>(pooled + o);
+          keep[wa][0] = !((li ? pv[1] : pv[0]) <= 0.f);
+          keep[wa][1] = !((ri ? pv[1] : pv[0]) <= 0.f);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int wa = 0; wa < NW; ++wa) {
+        const int oh = int(a) - (NW - 1) + wa;
+#pragma unroll
+        for (int wb = 0; wb < NW; ++wb) {
+          const int ow = int(b) - (NW - 1) + wb;
+          const bool ok = oh >= 0 && oh < int(OH) && ow >= 0 && ow < int(OW);
+          const uint32_t o = (plane * OH + uint32_t(ok ? oh : 0)) * OW + uint32_t(ok ? ow : 0);
+          const uint32_t iv = idx[o];
+          v[wa][wb] = dz[o];
+          id[wa][wb] = ok ? iv : 0xFFFFFFFFu;
+          if constexpr (MASK) keep[wa][wb] = !(pooled[o] <= 0.f);
+        }
+      }
+    }
+  }
+
+  template <bool KEEP>
+  __device__ __forceinline__ float sum(uint32_t i) const {
+    float acc = 0.f;
+#pragma unroll
+    for (int wa = 0; wa < NW; ++wa)
+#pragma unroll
+      for (int wb = 0; wb < NW; ++wb)
+        if (id[wa][wb] == i && (!KEEP || keep[wa][wb])) acc += v[wa][wb];
+    return acc;
+  }
+};
+
+// Stores input row ih's S = 2 gradients of block column b: one 8-byte store
+// when the pair lies in the row (aligned for rows of even length; PAIR also
+// takes odd ones).
+template <bool PAIR>
+__device__ __forceinline__ void store_pair_row(float* __restrict__ row, uint32_t b, uint32_t W,
+                                               float o0, float o1) {
+  if (2 * b + 1 < W && (PAIR || (W & 1) == 0)) {
+    stu(row, f2{o0, o1});
+  } else {
+    row[0] = o0;
+    if (2 * b + 1 < W) row[1] = o1;
+  }
+}
+
+// Block form: a thread owns an S x S block of inputs (PoolWin) and writes
+// its gradients, an output pair of a row as one 8-byte store whenever both
+// lie in the row.
 template <int K, int S, bool PAIR>
 __global__ void k_maxpool_bwd_blk(const float* __restrict__ dz, const uint32_t* __restrict__ idx,
                                   float* __restrict__ dx, uint32_t items, uint32_t H, uint32_t W,
                                   uint32_t OH, uint32_t OW, uint32_t BH, uint32_t BW,
                                   FastDiv dBW, FastDiv dBH) {
-  constexpr int NW = (K - 1) / S + 1;
-  static_assert(!PAIR || (NW == 2 && S == 2), "pair loads cover two window columns");
   const uint32_t item = blockIdx.x * 256 + threadIdx.x;
   if (item >= items) return;
   const uint32_t t = fdiv(item, dBW), b = item - t * BW;
   const uint32_t plane = fdiv(t, dBH), a = t - plane * BH;
-  uint32_t id[NW][NW];
-  float v[NW][NW];
-  if constexpr (PAIR) {
-    typedef uint32_t u2 __attribute__((ext_vector_type(2)));
-    const uint32_t ps = min(max(int(b) - 1, 0), int(OW) - 2);
-    const bool lok = b >= 1, rok = b < OW;
-    const bool li = b == OW, ri = b != 0;  // element of the pair holding column b-1 / b
-#pragma unroll
-    for (int wa = 0; wa < NW; ++wa) {
-      const int oh = int(a) - (NW - 1) + wa;
-      const bool hok = oh >= 0 && oh < int(OH);
-      const uint32_t o = (plane * OH + uint32_t(hok ? oh : 0)) * OW + ps;
-      const u2 iv = ldu<u2>(idx + o);
-      const f2 dv = ldu<f2>(dz + o);
-      id[wa][0] = (hok && lok) ? (li ? iv[1] : iv[0]) : 0xFFFFFFFFu;
-      id[wa][1] = (hok && rok) ? (ri ? iv[1] : iv[0]) : 0xFFFFFFFFu;
-      v[wa][0] = li ? dv[1] : dv[0];
-      v[wa][1] = ri ? dv[1] : dv[0];
-    }
-  } else {
-#pragma unroll
-    for (int wa = 0; wa < NW; ++wa) {
-      const int oh = int(a) - (NW - 1) + wa;
-#pragma unroll
-      for (int wb = 0; wb < NW; ++wb) {
-        const int ow = int(b) - (NW - 1) + wb;
-        const bool ok = oh >= 0 && oh < int(OH) && ow >= 0 && ow < int(OW);
-        const uint32_t o = (plane * OH + uint32_t(ok ? oh : 0)) * OW + uint32_t(ok ? ow : 0);
-        const uint32_t iv = idx[o];
-        v[wa][wb] = dz[o];
-        id[wa][wb] = ok ? iv : 0xFFFFFFFFu;
-      }
-    }
-  }
+  PoolWin<K, S, PAIR, false> pw;
+  pw.load(dz, idx, nullptr, plane, a, b, OH, OW);
 #pragma unroll
   for (int r = 0; r < S; ++r) {
     const uint32_t ih = a * S + r;
     if (ih >= H) continue;
+    const uint32_t i0 = (plane * H + ih) * W + b * S;
     float o[S];
 #pragma unroll
-    for (int c = 0; c < S; ++c) {
-      const uint32_t i = (plane * H + ih) * W + b * S + c;
-      float acc = 0.f;
-#pragma unroll
-      for (int wa = 0; wa < NW; ++wa)
-#pragma unroll
-        for (int wb = 0; wb < NW; ++wb)
-          if (id[wa][wb] == i) acc += v[wa][wb];
-      o[c] = acc;
-    }
-    // The S = 2 pair goes out as one 8-byte store when it lies in the row
-    // (aligned for rows of even length; PAIR also takes odd ones).
-    float* row = dx + (plane * H + ih) * W + b * S;
-    if (S == 2 && b * S + 1 < W && (PAIR || (W & 1) == 0)) {
-      stu(row, f2{o[0], o[S - 1]});
+    for (int c = 0; c < S; ++c) o[c] = pw.template sum<false>(i0 + c);
+    float* row = dx + i0;
+    if constexpr (S == 2) {
+      store_pair_row<PAIR>(row, b, W, o[0], o[1]);
     } else {
 #pragma unroll
       for (int c = 0; c < S; ++c)
         if (b * S + c < W) row[c] = o[c];
     }
+  }
+}
+
+// Max-pool backward over a ReLU conv output whose backward reads its masked
+// gradient on the padded pixel grid (kGLayoutPad, the stride-phase dW): dx
+// as k_maxpool_bwd_blk (S = 2), and G_pad[plane][ih][iw] for iw < gw
+// (= pad4(W); zero for iw >= W) with the bias-gradient partials.  One wave
+// per (plane, chunk of 64 blocks): a wave's blocks lie in one plane, so the
+// wave's G sum is one partial, db[c][b*nch + chunk].
+template <int K, bool PAIR>
+__global__ void __launch_bounds__(256)
+    k_maxpool_bwd_gpad(const float* __restrict__ dz, const uint32_t* __restrict__ idx,
+                       const float* __restrict__ pooled, float* __restrict__ dx,
+                       float* __restrict__ gp, float* __restrict__ db, uint32_t C, uint32_t H,
+                       uint32_t W, uint32_t OH, uint32_t OW, uint32_t gw, uint32_t BW,
+                       uint32_t nblk, uint32_t nch, uint32_t nB, uint32_t waves, FastDiv dBW,
+                       FastDiv dNch) {
+  const uint32_t wv = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wv >= waves) return;  // whole waves
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t plane = fdiv(wv, dNch), chunk = wv - plane * nch;
+  const uint32_t item = chunk * 64 + lane;
+  const bool live = item < nblk;
+  const uint32_t it = live ? item : 0u;
+  const uint32_t a = fdiv(it, dBW), b = it - a * BW;
+  PoolWin<K, 2, PAIR, true> pw;
+  pw.load(dz, idx, pooled, plane, a, b, OH, OW);
+  float sum = 0.f;
+  if (live) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const uint32_t ih = 2 * a + r;
+      if (ih >= H) continue;
+      const uint32_t i0 = (plane * H + ih) * W + 2 * b;
+      const float o0 = pw.template sum<false>(i0), o1 = pw.template sum<false>(i0 + 1);
+      const float m0 = pw.template sum<true>(i0);
+      const float m1 = 2 * b + 1 < W ? pw.template sum<true>(i0 + 1) : 0.f;
+      store_pair_row<PAIR>(dx + i0, b, W, o0, o1);
+      float* grow = gp + (size_t(plane) * H + ih) * gw + 2 * b;  // 8-byte aligned: gw % 4 == 0
+      *reinterpret_cast<f2*>(grow) = f2{m0, m1};
+      if (b == BW - 1 && gw > 2 * BW) *reinterpret_cast<f2*>(grow + 2) = f2{0.f, 0.f};
+      sum += m0 + m1;
+    }
+  }
+  sum = wave_reduce(sum);
+  if (lane == 0) {
+    const uint32_t bi = plane / C, c = plane - bi * C;
+    db[size_t(c) * nB * nch + size_t(bi) * nch + chunk] = sum;
   }
 }
 
@@ -1367,6 +1458,47 @@ bool maxpool_backward(const float* dz, const float* idx, float* dx, uint32_t B, 
   hipLaunchKernelGGL(k_maxpool_bwd_planes, dim3(cdiv(planes, 64)), dim3(64), 0, stream(), dz, ip,
                      dx, planes, OH * OW, inPer);
   return check_launch("maxpool_backward");
+}
+
+// Only the padded-grid layout: G in NCHW order, written by the same plane-
+// ordered waves as dx.  An NHWC form (32 channels x 8 blocks per workgroup,
+// G through an LDS transpose) measured slower than the plain backward plus
+// the conv's own masking pass (AlexNet pool2 76 us against 21 + 22 us): a
+// wave's loads and dx stores then span 8 planes, 16-24 cache lines per
+// instruction instead of 2-4.
+bool maxpool_backward_g_ok(uint32_t C, uint32_t H, uint32_t W, uint32_t OH, uint32_t OW,
+                           uint32_t k, uint32_t s, uint32_t layout) {
+  return s == 2 && (k == 2 || k == 3) && C && H && W && OH && OW && layout == kGLayoutPad;
+}
+
+uint32_t maxpool_backward_g_rows(uint32_t B, uint32_t H, uint32_t W, uint32_t layout) {
+  (void)layout;
+  return B * cdiv(cdiv(H, 2) * cdiv(W, 2), 64);
+}
+
+bool maxpool_backward_g(const float* dz, const float* idx, const float* pooled, float* dx,
+                        float* g, float* db, uint32_t B, uint32_t C, uint32_t OH, uint32_t OW,
+                        uint32_t H, uint32_t W, uint32_t k, uint32_t layout, uint32_t gw) {
+  const uint32_t n = B * C * OH * OW, xcount = B * C * H * W;
+  ProfScope prof("maxpool_bwd", 0, 12.0 * n + 4.0 * xcount + 4.0 * double(B) * C * H * gw);
+  const uint32_t* ip = reinterpret_cast<const uint32_t*>(idx);
+  const uint32_t BW = cdiv(W, 2), nblk = cdiv(H, 2) * BW;
+  const FastDiv fBW = make_fastdiv(BW);
+  if (layout != kGLayoutPad) {
+    set_error("maxpool_backward_g: unsupported G layout %u", layout);
+    return false;
+  }
+  const uint32_t nch = cdiv(nblk, 64), waves = B * C * nch;
+  const dim3 grid(cdiv(waves, 4));
+  const FastDiv fN = make_fastdiv(nch);
+#define DCE_GPAD(K, P)                                                                          \
+  hipLaunchKernelGGL((k_maxpool_bwd_gpad<K, P>), grid, dim3(256), 0, stream(), dz, ip, pooled, \
+                     dx, g, db, C, H, W, OH, OW, gw, BW, nblk, nch, B, waves, fBW, fN)
+  if (k == 2) DCE_GPAD(2, false);
+  else if (k == 3 && OW >= 2) DCE_GPAD(3, true);
+  else DCE_GPAD(3, false);
+#undef DCE_GPAD
+  return check_launch("maxpool_backward_g");
 }
 
 static bool sh_maxpool_forward(const Dispatch& d) {
