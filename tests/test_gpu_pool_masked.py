@@ -175,3 +175,30 @@ def test_pool_g_shortcut_dropped_on_writes(eng, case, write):
     finally:
         eng.lib.SetProfiling(0)
         eng.lib.ResetProfile()
+
+
+def _random_cases(n, seed):
+    """Seeded random ReLU convolutions over 1-3 input channels (strides 1-4:
+    the padded-grid layout) followed by a 2x2 or 3x3 stride-2 max-pool: odd
+    and even plane widths, pad-column counts 0-3, one-window-column planes."""
+    r = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        k, s = int(r.integers(1, 8)), int(r.integers(1, 5))
+        p = int(r.integers(0, k))
+        H, W = int(r.integers(k, 40)), int(r.integers(k, 40))
+        OH, OW = (H + 2 * p - k) // s + 1, (W + 2 * p - k) // s + 1
+        pk = int(r.choice([2, 3]))
+        if OH < pk or OW < pk:
+            continue
+        out.append((int(r.integers(1, 4)), int(r.integers(1, 4)), H, W, int(r.integers(1, 40)),
+                    k, s, p, pk))
+    return out
+
+
+RANDOM = _random_cases(16, 2718)
+
+
+@pytest.mark.parametrize("case", RANDOM, ids=[str(c) for c in RANDOM])
+def test_pool_backward_makes_conv_g_random(eng, case):
+    test_pool_backward_makes_conv_g(eng, case, want_x=False)
