@@ -421,6 +421,9 @@ struct LdNchwRK : LoaderBase<Stage<R, KT, false>> {
 //   FWD: source = x, rows = output pixels, tap reads x[b, a*s + kh - p, c*s + kw - p].
 //   !FWD (dX): source = G, rows = input pixels, tap reads G[b, oh, ow] with
 //        oh*s == a + p - kh exactly (S1: s == 1, no divisibility test).
+//        A strided dX runs as s*s sub-pixel phases, each an S1 gather over
+//        its own grid of input pixels with nh x nw taps (k = nw) and the
+//        column origin shifted by pwd (phase_dx below).
 // ---------------------------------------------------------------------------
 constexpr int kCB = 16;
 
@@ -436,6 +439,7 @@ struct LdPixRK : LoaderBase<Stage<R, KT, false>> {
     uint32_t srcH, srcW, Cp, k, s, p;
     uint32_t gridW, gridHW, N, kdim, n;
     FastDiv dGridHW, dGridW, dInner, dK;  // dInner: KK (blocked) or Cp (flat)
+    int pwd;  // dX: the column origin is c + p + pwd (0 but for the sub-pixel phases)
   };
   // FAST (blocked order, forward or stride-1 dX): the K tile's tap and
   // channel block are wave-uniform, so a quad's source offset is a per-quad
@@ -472,7 +476,7 @@ struct LdPixRK : LoaderBase<Stage<R, KT, false>> {
         c0[i] = int(c * P.s) - int(P.p);
       } else {
         r0[i] = int(a + P.p);
-        c0[i] = int(c + P.p);
+        c0[i] = int(c + P.p) + P.pwd;
       }
       // A row past the grid gets an origin no tap can bring into the image.
       if (n >= P.N) r0[i] = FWD ? -(1 << 20) : (1 << 20);
@@ -1169,6 +1173,41 @@ struct EpiNCHWPad {
   }
 };
 
+// One sub-pixel phase of a strided dX: columns n = b*GHW + a*GW + c of the
+// phase's pixel grid go to out[b][m][ph + s*a][pw + s*c] (NCHW, H x W
+// planes).  Consecutive columns land s floats apart, so every value is its
+// own store.
+struct EpiNCHWPhase {
+  struct Params {
+    float* out;
+    uint32_t M, H, W, GW, GHW, N, s, ph, pw;
+    FastDiv dGHW, dGW;
+  };
+  __device__ static __forceinline__ size_t at(const Params& p, uint32_t n, uint32_t m) {
+    const uint32_t b = fdiv(n, p.dGHW), rem = n - b * p.GHW;
+    const uint32_t a = fdiv(rem, p.dGW), c = rem - a * p.GW;
+    return (size_t(b) * p.M + m) * p.H * p.W + size_t(p.ph + p.s * a) * p.W + p.pw + p.s * c;
+  }
+  template <int MT, int NT, int FM, int FN, bool TACC, bool RA, bool RB>
+  __device__ static __forceinline__ void store(const Params& p, const f4 (&acc)[FM][FN],
+                                               uint32_t m0, uint32_t n0, uint32_t, int wm,
+                                               int wn, int lane) {
+    static_assert(!(TACC && RB), "row-interleaved B fragments are not used with TACC");
+    const int r = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          // TACC: row 16i + r, column 16j + 4g + v; else row 16i + 4g + v, column 16j + r
+          const uint32_t m = m0 + wm * (FM * 16) + (TACC ? frow<RA, FM>(i, r) : frow<RA, FM>(i, 4 * g + v));
+          const uint32_t n = n0 + wn * (FN * 16) + (TACC ? j * 16 + 4 * g + v : frow<RB, FN>(j, r));
+          if (m < p.M && n < p.N) p.out[at(p, n, m)] = acc[i][j][v];
+        }
+  }
+};
+
 // ---------------------------------------------------------------------------
 // The kernel.
 // ---------------------------------------------------------------------------
@@ -1355,11 +1394,15 @@ __global__ void __launch_bounds__(kThreads)
 // (blocked).  Rows are ld >= KK*inner floats apart, zero past KK*inner; size
 // rows * ld, rows = OC (mode 0) or C (mode 1).  The packed forward (C < 4
 // channels) uses the flat order with inner = C and ld = pad4(KK*C).
+// With vw != 0 the K order runs over the taps of one sub-pixel phase of a
+// strided dX: virtual tap v = jh * vw + jw is the filter tap (rh + s*jh,
+// rw + s*jw) of a kk x kk filter, and KK counts the phase's taps.
 struct WPerm {
   const float* w;  // null: nothing to re-lay
   float* out;
   uint32_t OC, C, KK, inner, ld;
   int mode, blocked;
+  uint32_t vw, kk, s, rh, rw;
   uint32_t blocks() const { return w ? cdiv(size_t(mode == 0 ? OC : C) * ld, 256) : 0; }
 };
 
@@ -1386,10 +1429,16 @@ __device__ __forceinline__ void permute_w_elem(const WPerm& pw, uint32_t i) {
     khw = kk / inner;
     ch = kk - khw * inner;
   }
+  uint32_t wk = khw, wKK = KK;
+  if (pw.vw) {
+    const uint32_t jh = khw / pw.vw, jw = khw - jh * pw.vw;
+    wk = (pw.rh + pw.s * jh) * pw.kk + pw.rw + pw.s * jw;
+    wKK = pw.kk * pw.kk;
+  }
   if (mode == 0)
-    out[i] = ch < C ? w[(r * C + ch) * KK + khw] : 0.f;
+    out[i] = ch < C ? w[(r * C + ch) * wKK + wk] : 0.f;
   else
-    out[i] = ch < OC ? w[(ch * C + r) * KK + khw] : 0.f;
+    out[i] = ch < OC ? w[(ch * C + r) * wKK + wk] : 0.f;
 }
 
 __global__ void k_permute_w(WPerm pw) { permute_w_elem(pw, blockIdx.x * blockDim.x + threadIdx.x); }
@@ -2811,6 +2860,97 @@ struct DxRun {
   }
 };
 
+// One sub-pixel phase of a strided dX (s > 1).  The input pixels (b, ph +
+// s*a, pw + s*c) receive only the taps kh = rh + s*jh (jh < nh), kw = rw +
+// s*jw (jw < nw) with rh = (ph + p) mod s, whose output pixels are (a + qh -
+// jh, c + qw - jw), qh = (ph + p - rh) / s: a stride-1 gather over the
+// phase's own GH x GW grid with an nh x nw kernel.
+struct PhaseGeom {
+  uint32_t ph, pw, rh, rw, nh, nw, qh, qw, GH, GW;
+};
+
+template <bool BLK>
+struct DxPhaseRun {
+  const float* wt;
+  const float* gn;
+  float* dx;
+  ConvGeom g;
+  PhaseGeom q;
+  template <int MT, int NT, int KT>
+  int occ(bool) const {
+    return occupancy(
+        k_igemm<MT, NT, KT, LdDenseRK<MT, KT>, LdPixRK<NT, KT, false, true, BLK>, EpiNCHWPhase>);
+  }
+  template <int MT, int NT, int KT>
+  bool run() {
+    const uint32_t OCp = pad4(g.OC), KK = q.nh * q.nw, kdim = KK * OCp;
+    const uint32_t GHW = q.GH * q.GW, N = g.B * GHW;
+    using LA = LdDenseRK<MT, KT>;
+    using LB = LdPixRK<NT, KT, false, true, BLK>;
+    const typename LA::Params pa{wt, kdim, g.C, kdim, g.C * kdim};
+    const typename LB::Params pb{gn, g.OH, g.OW, OCp, q.nw, 1, q.qh, q.GW, GHW, N, kdim,
+                                 g.B * g.OH * g.OW * OCp, make_fastdiv(GHW), make_fastdiv(q.GW),
+                                 make_fastdiv(BLK ? KK : OCp), make_fastdiv(q.nw),
+                                 int(q.qw) - int(q.qh)};
+    const EpiNCHWPhase::Params pe{dx, g.C, g.H, g.W, q.GW, GHW, N, g.s, q.ph, q.pw,
+                                  make_fastdiv(GHW), make_fastdiv(q.GW)};
+    return launch<MT, NT, KT, LA, LB, EpiNCHWPhase>(pa, pb, pe, g.C, N, cdiv(kdim, KT), 1,
+                                                    "conv_backward_input");
+  }
+};
+
+// dX of a strided convolution as its s*s sub-pixel phases: every input pixel
+// multiplies only the taps that reach it, where the strided gather walks all
+// k*k taps for every pixel and finds all but about 1/s^2 of them out of
+// step.  Each phase gets its own filter re-layout (into wt, C * k*k * OCp
+// floats) and GEMM, unsplit; phases that no tap reaches (k < s) are zero.
+static bool phase_dx(const float* w, float* wt, const float* gn, float* dx, const ConvGeom& g) {
+  const uint32_t s = g.s, OCp = pad4(g.OC);
+  const bool blk = blocked_k(OCp);
+  auto geom = [&](uint32_t ph, uint32_t pw) {
+    PhaseGeom q{};
+    q.ph = ph;
+    q.pw = pw;
+    q.GH = ph < g.H ? cdiv(g.H - ph, s) : 0;
+    q.GW = pw < g.W ? cdiv(g.W - pw, s) : 0;
+    q.rh = (ph + g.p) % s;
+    q.rw = (pw + g.p) % s;
+    q.nh = q.rh < g.k ? cdiv(g.k - q.rh, s) : 0;
+    q.nw = q.rw < g.k ? cdiv(g.k - q.rw, s) : 0;
+    q.qh = (ph + g.p - q.rh) / s;
+    q.qw = (pw + g.p - q.rw) / s;
+    return q;
+  };
+  bool empty = false;
+  for (uint32_t ph = 0; ph < s; ++ph)
+    for (uint32_t pw = 0; pw < s; ++pw) {
+      const PhaseGeom q = geom(ph, pw);
+      empty |= q.GH * q.GW > 0 && q.nh * q.nw == 0;
+    }
+  if (empty && !fill_zero(dx, size_t(g.B) * g.C * g.H * g.W)) return false;
+  for (uint32_t ph = 0; ph < s; ++ph)
+    for (uint32_t pw = 0; pw < s; ++pw) {
+      const PhaseGeom q = geom(ph, pw);
+      if (q.GH * q.GW == 0 || q.nh * q.nw == 0) continue;
+      const uint32_t KK = q.nh * q.nw, kdim = KK * OCp, N = g.B * q.GH * q.GW;
+      if (!permute_w(WPerm{w, wt, g.OC, g.C, KK, OCp, kdim, 1, blk ? 1 : 0, q.nw, g.k, s, q.rh,
+                           q.rw}))
+        return false;
+      TileCfg c = choose(
+          "DCE_TUNE_DX", g.C, N, kdim, 1, true,
+          [&](const TileCfg& t) {
+            return blk ? tiles_occ16(t, DxPhaseRun<true>{}) : tiles_occ16(t, DxPhaseRun<false>{});
+          },
+          true);
+      narrow_short_k(c, "DCE_TUNE_DX", g.C, N, kdim);
+      c.splits = 1;
+      const bool ok = blk ? tiles_dispatch16(c, DxPhaseRun<true>{wt, gn, dx, g, q})
+                          : tiles_dispatch16(c, DxPhaseRun<false>{wt, gn, dx, g, q});
+      if (!ok) return false;
+    }
+  return true;
+}
+
 // Pointwise dX: dx[c][n] = sum_oc w[oc][c] dy[oc][n] (NCHW dy and dx; the
 // filters re-laid [c][pad4(OC)]).
 // WK: the A operand is the filters themselves, [OC][C] read as [k = oc][row
@@ -3009,15 +3149,22 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
         false, true);
     nP = al64(size_t(dwc.splits) * 4 * cdiv(size_t(g.OC) * taps, 4));
   }
-  if (dx) {
+  // A dX at stride 3 or more runs as sub-pixel phases (phase_dx), each with
+  // its own filter re-layout and no split: the strided gather would walk
+  // s^2 times the taps that reach a pixel (AlexNet c1's dX at b128: 18.0 ->
+  // 1.24 ms).  At stride 2 the gather's 4x is about what the phases' extra
+  // launches and smaller, unsplit grids cost (ResNet-like layers of 0.4-7
+  // GFLOP measured from 40 % faster to 65 % slower), so it stays.
+  const bool phased = dx && g.s >= 3;
+  if (dx && !phased) {
     const bool blk = blocked_k(OCp);
     dxc = choose(
         "DCE_TUNE_DX", g.C, g.B * HW, KK * OCp, 8, true,
         [&](const TileCfg& t) { return conv_variant_occ<DxRun>(g.s == 1, blk, t); }, true);
     narrow_short_k(dxc, "DCE_TUNE_DX", g.C, g.B * HW, KK * OCp);
-    nW = al64(size_t(g.C) * KK * OCp);
     nQ = dxc.splits > 1 ? size_t(dxc.splits) * g.C * g.B * HW : 0;
   }
+  if (dx) nW = al64(size_t(g.C) * KK * OCp);
   float* ws = workspace(nG + nGp + nDb + nX + nP + nW + nQ);
   if (!ws) return false;
   float* gn = ws;
@@ -3042,7 +3189,7 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
   const WPerm dxPerm{w, wt, g.OC, g.C, KK, OCp, KK * OCp, 1, dx && blocked_k(OCp) ? 1 : 0};
   uint32_t npbGot = npb;
   if (useGnhwc && !to_nhwc_masked(dy, y, gn, useGpad ? nullptr : dbPart, g.B, g.OC, OHW, &npbGot,
-                                  dx ? dxPerm : WPerm{}))
+                                  dx && !phased ? dxPerm : WPerm{}))
     return false;
   const uint32_t dbRowsGot = preG ? pre->dbRows : (useGpad ? dbRows : g.B * npbGot);
   if (db && !dw) {
@@ -3052,6 +3199,7 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
   auto dx_chain = [&]() {
     ProfScope prof("conv_dx", 2.0 * g.OC * g.C * KK * double(npix),
                    4.0 * (double(npix) * OCp + double(g.B) * g.C * g.H * g.W));
+    if (phased) return phase_dx(w, wt, gn, dx, g);
     return conv_variant<DxRun>(g.s == 1, dxPerm.blocked != 0, dxc, wt, gn, dx, qpart, g,
                                dxc.splits);
   };

@@ -201,6 +201,25 @@ def test_conv_random_special_layouts(eng, case):
     _conv_case(eng, *case, seed=29, keep=bool(case[1] % 2))
 
 
+PHASE_CASES = [
+    # stride >= 3: dX as s*s sub-pixel phases, each a GEMM over its own taps
+    (2, 24, 20, 19, 32, 2, 3, 0, 1),      # k < s: phases without taps (zero planes)
+    (1, 64, 30, 30, 48, 5, 3, 2, 1),      # 2 or 1 taps per phase row, odd phase planes
+    (2, 16, 33, 31, 20, 7, 4, 3, 0),      # no activation, ragged plane widths
+    (1, 40, 17, 17, 64, 4, 4, 0, 1),      # k == s: one tap per phase
+    (2, 8, 26, 23, 16, 1, 3, 0, 1),       # 1x1 stride 3: one live phase
+    (1, 32, 45, 45, 96, 11, 4, 2, 1),     # AlexNet c1 shape over 32 channels
+]
+
+
+@pytest.mark.parametrize("case", PHASE_CASES, ids=[str(c) for c in PHASE_CASES])
+def test_conv_dx_stride_phases(eng, case):
+    """Strided dX by sub-pixel phases against the float64 oracle (with and
+    without the forward's channel-innermost copy)."""
+    _conv_case(eng, *case, seed=37, keep=True)
+    _conv_case(eng, *case, want=(1, 0, 0), seed=38, keep=False)
+
+
 @pytest.mark.parametrize("case", [(2, 3, 35, 35, 64, 11, 4, 2, 1), (2, 1, 12, 10, 6, 5, 1, 2, 1),
                                   (2, 2, 20, 20, 4, 6, 5, 1, 1), (2, 16, 9, 9, 8, 3, 1, 1, 1)],
                          ids=str)
