@@ -800,11 +800,40 @@ void* ConvForwardFused(void* x, void* filters, void* bias, uint32_t batch, uint3
     }
   }
   Buffer* K = static_cast<Buffer*>(keep);
+  // With no activation a batch norm usually follows: the GEMM leaves the
+  // statistics of y in a side buffer, which batchnorm_mean_var on y reads
+  // instead of making its own pass over y.
+  struct StatsCtx {
+    Buffer* side;
+    uint32_t C;
+  } sctx{nullptr, outC};
+  ConvStatsReq sreq{[](void* ctx, uint32_t pieces) -> double* {
+                      StatsCtx* c = static_cast<StatsCtx*>(ctx);
+                      const uint64_t n = uint64_t(c->C) * pieces * 4;  // two doubles per piece
+                      if (n >= 0xFFFFFFFFull) return nullptr;
+                      c->side = static_cast<Buffer*>(create_buffer(nullptr, uint32_t(n)));
+                      return c->side ? reinterpret_cast<double*>(c->side->ptr) : nullptr;
+                    },
+                    &sctx, 0};
   if (!conv_forward(X->ptr, K ? K->ptr : nullptr, Wt->ptr, Bi->ptr,
-                    static_cast<Buffer*>(out)->ptr, g, actType)) {
+                    static_cast<Buffer*>(out)->ptr, g, actType, actType == 0 ? &sreq : nullptr)) {
     release_buffer(out);
     release_buffer(keep);
+    release_buffer(sctx.side);
     return nullptr;
+  }
+  if (sctx.side) {
+    Buffer* Y = static_cast<Buffer*>(out);
+    if (sreq.pieces) {
+      set_tag(Y, kBnStatsTag);
+      Y->meta[0] = batch;
+      Y->meta[1] = outC;
+      Y->meta[2] = g.OH * g.OW;
+      Y->aux32 = sreq.pieces;
+      Y->side = sctx.side;
+    } else {
+      release_buffer(sctx.side);
+    }
   }
   if (K) {
     K->tag = kNhwcTag;

@@ -1208,6 +1208,100 @@ struct EpiNCHWPhase {
   }
 };
 
+// EpiNCHW that also leaves the batch-norm statistics of the values it stores:
+// for each output row m (a channel) the sums of z and z*z over the tile's
+// columns below N, as doubles at stats[(m * pieces + nt) * 2 + {0, 1}] with
+// nt the tile's column index: one piece per column tile, the layout of the
+// BN statistics' partial sums.  The transposed-accumulation form only (the
+// pixel and pointwise GEMMs): a lane's row is fixed per fragment, so it
+// stores each quad as EpiNCHW does and adds its (at most 16) values of the
+// row in float; the lanes' float pairs go to LDS (the A stages, free after
+// the main loop's last barrier) and after one barrier a thread per row adds
+// them in double in a fixed order (the same bits on every run).  The row's
+// bias is loaded once for both uses.
+struct EpiNCHWStats {
+  static constexpr bool kStats = true;
+  struct Params {
+    EpiNCHW::Params o;
+    double* stats;
+    uint32_t pieces;
+  };
+  // All WGN waves of the workgroup call this.  lds: WGN * 4 * MT float2.
+  template <int MT, int NT, int FM, int FN, bool TACC, bool RA, bool RB, int WGN>
+  __device__ static __forceinline__ void store_stats(const Params& p, const f4 (&acc)[FM][FN],
+                                                     uint32_t m0, uint32_t n0, int wm, int wn,
+                                                     int lane, float* lds) {
+    static_assert(TACC && WGN > 1, "pixel-column GEMMs with several waves per row block");
+    const EpiNCHW::Params& o = p.o;
+    const int r = lane & 15, g = lane >> 4;
+    float2* red = reinterpret_cast<float2*>(lds);
+    uint32_t m[FM];
+    float bv[FM], f0[FM], f1[FM];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      m[i] = m0 + wm * (FM * 16) + frow<RA, FM>(i, r);
+      bv[i] = o.bias && m[i] < o.M ? o.bias[m[i]] : 0.f;
+      f0[i] = f1[i] = 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const uint32_t n = n0 + wn * (FN * 16) + j * 16 + 4 * g;
+      const uint32_t b = fdiv(n, o.dHW);
+      const uint32_t pix = n - b * o.HW;
+      const bool quad = pix + 3 < o.HW && n + 3 < o.N;
+      const size_t base = size_t(b) * o.M * o.HW + pix;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        f4 z;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          z[v] = epi_act(acc[i][j][v] + bv[i], o.act);
+          const float zz = m[i] < o.M && n + v < o.N ? z[v] : 0.f;
+          f0[i] += zz;
+          f1[i] = fmaf(zz, zz, f1[i]);
+        }
+        if (m[i] >= o.M || n >= o.N) continue;
+        if (quad) {
+          stu(o.out + base + size_t(m[i]) * o.HW, z);
+        } else {
+          uint32_t bb = b, pp = pix;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            if (n + v < o.N) o.out[(size_t(bb) * o.M + m[i]) * o.HW + pp] = z[v];
+            if (++pp == o.HW) {
+              pp = 0;
+              ++bb;
+            }
+          }
+        }
+      }
+    }
+    // Lane (r, g) of wave (wm, wn) holds row wm*WM + frow(i, r): slot
+    // (wn * 4 + g) of that row.
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      red[(wn * 4 + g) * MT + wm * (FM * 16) + frow<RA, FM>(i, r)] = float2{f0[i], f1[i]};
+    __syncthreads();
+    const int t = threadIdx.x;
+    if (t < MT && m0 + t < o.M) {
+      double s0 = 0, s1 = 0;
+#pragma unroll
+      for (int w = 0; w < WGN * 4; ++w) {
+        const float2 e = red[w * MT + t];
+        s0 += double(e.x);
+        s1 += double(e.y);
+      }
+      double* d = p.stats + (size_t(m0 + t) * p.pieces + n0 / NT) * 2;
+      d[0] = s0;
+      d[1] = s1;
+    }
+  }
+};
+template <class E, class = void>
+struct EpiStats : std::false_type {};
+template <class E>
+struct EpiStats<E, std::void_t<decltype(E::kStats)>> : std::true_type {};
+
 // ---------------------------------------------------------------------------
 // The kernel.
 // ---------------------------------------------------------------------------
@@ -1378,7 +1472,12 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] += red[(w * FM * FN + i * FN + j) * 64 + lane];
   }
-  EPI::template store<MT, NT, FM, FN, TACC, RA, RB>(pe, acc, m0, n0, z, wm, wn, lane);
+  if constexpr (EpiStats<EPI>::value) {
+    static_assert(WGN * 4 * MT * 8 <= int(sizeof(As)), "the statistics' lane sums fit the A stages");
+    EPI::template store_stats<MT, NT, FM, FN, TACC, RA, RB, WGN>(pe, acc, m0, n0, wm, wn, lane, As);
+  } else {
+    EPI::template store<MT, NT, FM, FN, TACC, RA, RB>(pe, acc, m0, n0, z, wm, wn, lane);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1794,6 +1893,73 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// k_splitk_nchw that also leaves the batch-norm statistics of what it
+// stores (as EpiNCHWStats): block (piece, m) finishes columns
+// [piece * kStatsSpan, (piece + 1) * kStatsSpan) of row m, with the same sum
+// order as k_splitk_nchw / k_splitk_nchw4 (the same bits of y), and writes
+// the double sums of z and z*z over them to stats[(m * pieces + piece) * 2].
+// Q4 (N % 4 == 0, 16-byte aligned partials): thread t takes the quad of
+// columns 4t .. 4t + 3 of the block's span, as k_splitk_nchw4 does.
+constexpr uint32_t kStatsSpan = 1024;
+template <bool Q4>
+__global__ void __launch_bounds__(256)
+    k_splitk_nchw_stats(const float* __restrict__ part, const float* __restrict__ bias,
+                        float* __restrict__ out, uint32_t M, uint32_t N, uint32_t HW,
+                        uint32_t splits, uint32_t act, double* __restrict__ stats,
+                        uint32_t pieces, FastDiv dHW) {
+  __shared__ double sh[4];
+  const uint32_t m = blockIdx.y, piece = blockIdx.x;
+  const float bv = bias ? bias[m] : 0.f;
+  double a0 = 0.0, a1 = 0.0;
+  if constexpr (Q4) {
+    const uint32_t n0 = piece * kStatsSpan + 4 * threadIdx.x;
+    if (n0 < N) {
+      const size_t nq = size_t(M) * (N / 4);
+      f4 z = sum_splits4(reinterpret_cast<const f4*>(part) + (size_t(m) * N + n0) / 4, nq, splits);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        z[e] = epi_act(z[e] + bv, act);
+        a0 += double(z[e]);
+        a1 += double(z[e]) * double(z[e]);
+      }
+      uint32_t b = fdiv(n0, dHW), pix = n0 - b * HW;
+      if (pix + 3 < HW) {
+        stu(out + (size_t(b) * M + m) * HW + pix, z);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          out[(size_t(b) * M + m) * HW + pix] = z[e];
+          if (++pix == HW) {
+            pix = 0;
+            ++b;
+          }
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (uint32_t u = 0; u < kStatsSpan / 256; ++u) {
+      const uint32_t n = piece * kStatsSpan + u * 256 + threadIdx.x;
+      if (n >= N) break;
+      const size_t i = size_t(m) * N + n;
+      float z = 0.f;
+      for (uint32_t k = 0; k < splits; ++k) z += part[size_t(k) * M * N + i];
+      z = epi_act(z + bv, act);
+      const uint32_t b = fdiv(n, dHW), pix = n - b * HW;
+      out[(size_t(b) * M + m) * HW + pix] = z;
+      a0 += double(z);
+      a1 += double(z) * double(z);
+    }
+  }
+  const double s0 = block_sum256(a0, sh);
+  const double s1 = block_sum256(a1, sh);
+  if (threadIdx.x == 0) {
+    double* d = stats + (size_t(m) * pieces + piece) * 2;
+    d[0] = s0;
+    d[1] = s1;
+  }
+}
+
 // Zero-padded copy of a row-major [rows][cols] matrix to row stride ldp.
 __global__ void k_pad_cols(const float* __restrict__ in, float* __restrict__ out, uint32_t rows,
                            uint32_t cols, uint32_t ldp) {
@@ -2033,6 +2199,17 @@ static int tiles_occ(const TileCfg& c, const F& f) {
 static inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 static inline size_t al64(size_t n) { return (n + 63) & ~size_t(63); }
 
+static bool split_nchw_stats(const float* part, const float* bias, float* out, uint32_t M,
+                             uint32_t N, uint32_t HW, uint32_t splits, uint32_t act,
+                             double* stats, uint32_t pieces) {
+  if (N % 4 == 0 && aligned16(part))
+    hipLaunchKernelGGL(k_splitk_nchw_stats<true>, dim3(pieces, M), dim3(256), 0, stream(), part,
+                       bias, out, M, N, HW, splits, act, stats, pieces, make_fastdiv(HW));
+  else
+    hipLaunchKernelGGL(k_splitk_nchw_stats<false>, dim3(pieces, M), dim3(256), 0, stream(), part,
+                       bias, out, M, N, HW, splits, act, stats, pieces, make_fastdiv(HW));
+  return check_launch("splitk_nchw");
+}
 static bool split_nchw(const float* part, const float* bias, float* out, uint32_t M, uint32_t N,
                        uint32_t HW, uint32_t splits, uint32_t act) {
   if (N % 4 == 0 && aligned16(part))
@@ -2535,6 +2712,8 @@ struct FwdRun {
   float* part;
   ConvGeom g;
   uint32_t act, splits;
+  double* stats;  // stride 1: BN statistics of y (pieces as stats_buffer sets them)
+  uint32_t pieces;
   template <int MT, int NT, int KT>
   int occ(bool split) const {
     using LA = LdDenseRK<MT, KT>;
@@ -2558,7 +2737,15 @@ struct FwdRun {
       const EpiRowMajor::Params pr{part, g.OC, N, N, g.OC * N};
       return launch<MT, NT, KT, LA, LB, EpiRowMajor>(pa, pb, pr, g.OC, N, kt, splits,
                                                     "conv_forward") &&
-             split_nchw(part, bias, y, g.OC, N, OHW, splits, act);
+             (stats ? split_nchw_stats(part, bias, y, g.OC, N, OHW, splits, act, stats, pieces)
+                    : split_nchw(part, bias, y, g.OC, N, OHW, splits, act));
+    }
+    if constexpr (S1) {
+      if (stats) {
+        const EpiNCHWStats::Params ps{pe, stats, pieces};
+        return launch<MT, NT, KT, LA, LB, EpiNCHWStats>(pa, pb, ps, g.OC, N, kt, 1,
+                                                        "conv_forward");
+      }
     }
     return launch<MT, NT, KT, LA, LB, EpiNCHW>(pa, pb, pe, g.OC, N, kt, 1, "conv_forward");
   }
@@ -2661,6 +2848,8 @@ struct FwdPwRun {
   float* part;
   ConvGeom g;
   uint32_t act, splits;
+  double* stats;  // BN statistics of y (pieces as stats_buffer sets them)
+  uint32_t pieces;
   template <int MT, int NT, int KT>
   int occ(bool split) const {
     using LA = LdDenseRK<MT, KT>;
@@ -2681,14 +2870,31 @@ struct FwdPwRun {
       const EpiRowMajor::Params pr{part, g.OC, N, N, g.OC * N};
       return launch<MT, NT, KT, LA, LB, EpiRowMajor>(pa, pb, pr, g.OC, N, kt, splits,
                                                     "conv_forward") &&
-             split_nchw(part, bias, y, g.OC, N, HW, splits, act);
+             (stats ? split_nchw_stats(part, bias, y, g.OC, N, HW, splits, act, stats, pieces)
+                    : split_nchw(part, bias, y, g.OC, N, HW, splits, act));
+    }
+    if (stats) {
+      const EpiNCHWStats::Params ps{pe, stats, pieces};
+      return launch<MT, NT, KT, LA, LB, EpiNCHWStats>(pa, pb, ps, g.OC, N, kt, 1, "conv_forward");
     }
     return launch<MT, NT, KT, LA, LB, EpiNCHW>(pa, pb, pe, g.OC, N, kt, 1, "conv_forward");
   }
 };
 
+// The buffer for the BN statistics of a conv forward's output when its GEMM
+// leaves them (pixel GEMMs at stride 1 and pointwise GEMMs, no activation):
+// one piece per column tile, or per kStatsSpan columns of the split-K finish.
+static double* stats_buffer(ConvStatsReq* st, const TileCfg& cfg, uint32_t N, uint32_t act,
+                            bool able) {
+  if (!st || act != 0 || !able) return nullptr;
+  const uint32_t pieces = cfg.splits > 1 ? cdiv(N, kStatsSpan) : cdiv(N, cfg.NT);
+  double* d = st->get(st->ctx, pieces);
+  if (d) st->pieces = pieces;
+  return d;
+}
+
 static bool conv_forward_pw(const float* x, const float* w, const float* bias, float* y,
-                            const ConvGeom& g, uint32_t act) {
+                            const ConvGeom& g, uint32_t act, ConvStatsReq* st) {
   const uint32_t Cp = pad4(g.C), N = g.B * g.H * g.W;
   if (!operand_fits(size_t(g.B) * g.C * g.H * g.W, "conv_forward")) return false;
   const TileCfg cfg = choose(
@@ -2703,13 +2909,15 @@ static bool conv_forward_pw(const float* x, const float* w, const float* bias, f
   if (!wDirect && !permute_w(WPerm{w, ws, g.OC, g.C, 1, Cp, Cp, 0, 0})) return false;
   ProfScope prof("conv_fwd", 2.0 * g.OC * g.C * double(N),
                  4.0 * (double(g.B) * g.C * g.H * g.W + double(g.B) * g.OC * g.OH * g.OW));
-  return tiles_dispatch16(
-      cfg, FwdPwRun{wDirect ? w : ws, x, bias, y, ws ? ws + nw : nullptr, g, act, cfg.splits});
+  double* stats = stats_buffer(st, cfg, N, act, true);
+  return tiles_dispatch16(cfg, FwdPwRun{wDirect ? w : ws, x, bias, y, ws ? ws + nw : nullptr, g,
+                                        act, cfg.splits, stats, st ? st->pieces : 0});
 }
 
 bool conv_forward(const float* x, float* x_nhwc_keep, const float* w, const float* bias,
-                  float* y, const ConvGeom& g, uint32_t act) {
-  if (pw_x(g)) return conv_forward_pw(x, w, bias, y, g, act);
+                  float* y, const ConvGeom& g, uint32_t act, ConvStatsReq* st) {
+  if (st) st->pieces = 0;
+  if (pw_x(g)) return conv_forward_pw(x, w, bias, y, g, act, st);
   if (ps_x(g)) return conv_forward_ps(x, x_nhwc_keep, w, bias, y, g, act);
   const bool pk = packed_x(g);
   const uint32_t Cp = pad4(g.C), KK = g.k * g.k, kdim = pk ? pad4(KK * g.C) : KK * Cp;
@@ -2742,9 +2950,11 @@ bool conv_forward(const float* x, float* x_nhwc_keep, const float* w, const floa
   {
     ProfScope prof("conv_fwd", fl,
                    4.0 * (double(g.B) * g.C * g.H * g.W + double(g.B) * g.OC * g.OH * g.OW));
+    double* stats = stats_buffer(st, cfg, N, act, !pk && s1);
     const bool ok =
         pk ? tiles_dispatch16(cfg, FwdPkRun{wp, xn, bias, y, part, g, act, cfg.splits})
-           : conv_variant<FwdRun>(s1, blk, cfg, wp, xn, bias, y, part, g, act, cfg.splits);
+           : conv_variant<FwdRun>(s1, blk, cfg, wp, xn, bias, y, part, g, act, cfg.splits,
+                                  stats, st ? st->pieces : 0u);
     if (!ok) return false;
   }
   return true;

@@ -33,7 +33,11 @@ struct Buffer {
   //  kGradGTag: gradient written by MaxPoolBackwardFused for a ReLU conv
   //            output (src): `side` holds that conv's masked gradient G in
   //            the layout its backward reads, followed by bias-gradient
-  //            partials, meta = {layout, B, OC, OH, OW}, aux32 = partial rows.
+  //            partials, meta = {layout, B, OC, OH, OW}, aux32 = partial rows;
+  //  kBnStatsTag: output of a ConvForwardFused with no activation whose GEMM
+  //            left the batch-norm statistics of its values: `side` holds
+  //            the per-channel double sums of y and y*y as [C][pieces][2],
+  //            meta = {B, C, H*W}, aux32 = pieces.
   // A tag is dropped (drop_tag) whenever the buffer is written by anything
   // but its producer, and when the buffer goes back to the pool.
   uint32_t tag;
@@ -47,7 +51,7 @@ struct Buffer {
   uint64_t srcGen;
   Buffer* aux;      // kPoolTag: the pooled output
   uint64_t auxGen;
-  Buffer* side;     // kGradGTag: owned buffer [G | bias-gradient partials]
+  Buffer* side;     // kGradGTag: owned buffer [G | bias-gradient partials]; kBnStatsTag: the sums
   uint32_t aux32;
 };
 constexpr uint32_t kPoolTag = 0x9001u;
@@ -55,6 +59,7 @@ constexpr uint32_t kNhwcTag = 0x9002u;
 constexpr uint32_t kReluOutTag = 0x9003u;
 constexpr uint32_t kPoolOutTag = 0x9004u;
 constexpr uint32_t kGradGTag = 0x9005u;
+constexpr uint32_t kBnStatsTag = 0x9006u;
 // Layouts of a conv backward's masked gradient G.
 constexpr uint32_t kGLayoutPad = 1;   // [B*OC][OH][pad4(OW)], zero past OW (stride-phase dW)
 constexpr uint32_t kGLayoutNhwc = 2;  // [B*OH*OW][pad4(OC)] (the transpose pass)
@@ -321,6 +326,19 @@ __device__ __forceinline__ T wave_reduce(T v, Op op = Op()) {
   return op(xl::readlane(v, 0), xl::readlane(v, 32));
 }
 
+// Block-wide sum (256 threads) in double, in a fixed order; result valid in
+// thread 0.  sh: 4 doubles of shared memory.
+__device__ __forceinline__ double block_sum256(double v, double* sh) {
+  v = wave_reduce(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) sh[w] = v;
+  __syncthreads();
+  double s = 0;
+  if (threadIdx.x == 0) s = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+  return s;
+}
+
 // ---------------------------------------------------------------------------
 // Convolution geometry (NCHW, square kernels, zero padding, floor mode).
 // ---------------------------------------------------------------------------
@@ -345,10 +363,20 @@ bool to_nhwc(const float* x, float* out, uint32_t B, uint32_t C, uint32_t H, uin
 bool packed_x(const ConvGeom& g);
 size_t xcopy_floats(const ConvGeom& g);
 uint32_t xcopy_tag(const ConvGeom& g);
+// Batch-norm statistics of a conv forward's output, asked for by the caller:
+// when the forward's GEMM can leave them (no activation, stride 1, no split,
+// x of at least 4 channels or a pointwise layer) it calls get(ctx, pieces)
+// for a buffer of OC * pieces * 2 doubles, writes the per-channel sums of y
+// and y*y there ([oc][piece][2]) and sets `pieces`; otherwise pieces is 0.
+struct ConvStatsReq {
+  double* (*get)(void* ctx, uint32_t pieces);
+  void* ctx;
+  uint32_t pieces;
+};
 // y = act(conv(x, w) + bias) in NCHW.  x_nhwc_keep, when not null, receives
 // the copy of x (xcopy_floats(g) floats) for a later backward.
 bool conv_forward(const float* x, float* x_nhwc_keep, const float* w, const float* bias,
-                  float* y, const ConvGeom& g, uint32_t act);
+                  float* y, const ConvGeom& g, uint32_t act, ConvStatsReq* st = nullptr);
 // The layout of G that conv_backward reads for this geometry (kGLayoutPad or
 // kGLayoutNhwc), and the padded row width of kGLayoutPad.
 uint32_t conv_g_layout(const ConvGeom& g);

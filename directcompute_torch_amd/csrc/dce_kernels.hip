@@ -27,17 +27,6 @@ __device__ __forceinline__ void st(const Buf& b, uint32_t i, float v) {
 }
 __device__ __forceinline__ uint32_t gtid() { return blockIdx.x * blockDim.x + threadIdx.x; }
 
-// Block-wide sum (256 threads) in double; result valid in thread 0.
-__device__ __forceinline__ double block_sum256(double v, double* sh) {
-  v = wave_reduce(v);
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  __syncthreads();
-  if (lane == 0) sh[w] = v;
-  __syncthreads();
-  double s = 0;
-  if (threadIdx.x == 0) s = (sh[0] + sh[1]) + (sh[2] + sh[3]);
-  return s;
-}
 
 // ===========================================================================
 // Generic elementwise kernels: out[i] = F(in0[i], in1[i]).
@@ -723,12 +712,9 @@ __device__ __forceinline__ bool bn_piece_sums(const double* part, uint32_t piece
 // batchnorm_mean_var finalize: the formulas of nn_batchnorm_mean_var.hlsl:46-59
 // (one-pass var = max(0, E[x^2] - E[x]^2), unbiased running var
 // var*m/max(1, m-1), momentum update), evaluated in double.
-__global__ void __launch_bounds__(256)
-    k_bn_stats_final(const double* part, uint32_t pieces, uint32_t C, uint32_t m, Buf mean,
-                     Buf var, Buf rmean, Buf rvar, uint32_t training, float momentum) {
-  uint32_t c;
-  double s0, s1;
-  if (!bn_piece_sums(part, pieces, C, c, s0, s1)) return;
+__device__ __forceinline__ void bn_stats_store(uint32_t c, double s0, double s1, uint32_t m,
+                                               Buf mean, Buf var, Buf rmean, Buf rvar,
+                                               uint32_t training, float momentum) {
   const double mu = s0 / m;
   const double v = fmax(0.0, s1 / m - mu * mu);
   st(mean, c, float(mu));
@@ -739,6 +725,33 @@ __global__ void __launch_bounds__(256)
     st(rmean, c, float((1.0 - mo) * ld(rmean, c) + mo * mu));
     st(rvar, c, float((1.0 - mo) * ld(rvar, c) + mo * unb));
   }
+}
+__global__ void __launch_bounds__(256)
+    k_bn_stats_final(const double* part, uint32_t pieces, uint32_t C, uint32_t m, Buf mean,
+                     Buf var, Buf rmean, Buf rvar, uint32_t training, float momentum) {
+  uint32_t c;
+  double s0, s1;
+  if (!bn_piece_sums(part, pieces, C, c, s0, s1)) return;
+  bn_stats_store(c, s0, s1, m, mean, var, rmean, rvar, training, momentum);
+}
+// The same finish over the thousands of pieces a conv forward's GEMM leaves
+// (one per column tile): a workgroup per channel, thread t adding pieces t,
+// t + 256, ..., then the block tree, in a fixed order.
+__global__ void __launch_bounds__(256)
+    k_bn_stats_final_wide(const double* part, uint32_t pieces, uint32_t m, Buf mean, Buf var,
+                          Buf rmean, Buf rvar, uint32_t training, float momentum) {
+  __shared__ double sh[4];
+  const uint32_t c = blockIdx.x;
+  const double2* pc = reinterpret_cast<const double2*>(part) + size_t(c) * pieces;
+  double a0 = 0.0, a1 = 0.0;
+  for (uint32_t p = threadIdx.x; p < pieces; p += 256) {
+    const double2 e = pc[p];
+    a0 += e.x;
+    a1 += e.y;
+  }
+  const double s0 = block_sum256(a0, sh);
+  const double s1 = block_sum256(a1, sh);
+  if (threadIdx.x == 0) bn_stats_store(c, s0, s1, m, mean, var, rmean, rvar, training, momentum);
 }
 __global__ void __launch_bounds__(256)
     k_bn_grad_final(const double* part, uint32_t pieces, uint32_t C, Buf dgamma, Buf dbeta) {
@@ -808,6 +821,16 @@ static bool sh_bn_mean_var(const Dispatch& d) {
   uint32_t N = CU(d, 0), C = CU(d, 1), Sz = CU(d, 2), training = CU(d, 3);
   float momentum = CF(d, 4);
   if (!N || !C || !Sz) return true;
+  // x straight from a conv forward that left its statistics: finish those.
+  const Buffer* X = d.nS ? static_cast<const Buffer*>(d.srvs[0]) : nullptr;
+  if (X && X->magic == kMagicLive && X->tag == kBnStatsTag && X->side && X->meta[0] == N &&
+      X->meta[1] == C && X->meta[2] == Sz) {
+    ProfScope prof("bn_stats_side", 0, 16.0 * double(C) * X->aux32);
+    hipLaunchKernelGGL(k_bn_stats_final_wide, dim3(C), dim3(256), 0, stream(),
+                       reinterpret_cast<const double*>(X->side->ptr), X->aux32, N * Sz, U(d, 0),
+                       U(d, 1), U(d, 2), U(d, 3), training, momentum);
+    return check_launch("batchnorm_mean_var");
+  }
   double* part;
   BnPieces pc;
   ProfScope prof("bn_stats", 0, 4.0 * double(N) * C * Sz);

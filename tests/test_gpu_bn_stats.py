@@ -1,0 +1,189 @@
+"""GPU parity of the batch-norm statistics left by a conv forward's GEMM
+(batchnorm_mean_var, nn_batchnorm_mean_var.hlsl:19-61, on the output of a
+ConvForwardFused with no activation, engine.cpp:690-738):
+
+* ConvForwardFused with actType 0 at stride 1 over 4 or more channels (pixel
+  or pointwise GEMM; the split-K finish when K is split) writes y as before
+  and keeps the per-channel sums of y and y*y;
+  batchnorm_mean_var on y then only finishes them (family bn_stats_side,
+  no pass over y), and mean, var and the running statistics agree with the
+  same call on an untagged copy of y within 1e-6 (double sums in another
+  order) and with the float64 oracle within 1e-5;
+* layouts that do not leave statistics (C < 4, stride 2, ReLU) and
+  any write to y in between (UpdateBuffer, a shader writing y) fall back to
+  the statistics pass, and the results follow the written values."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import kernels as K
+from tests.helpers import TOL, download, he, rel_err, release, rng, upload
+from tests.test_gpu_kernels import fbits, new, run
+
+pytestmark = pytest.mark.gpu
+
+# (B, C, H, W, OC, k, s, p, act, side): side = the GEMM leaves the statistics
+CASES = [
+    (2, 16, 32, 32, 16, 3, 1, 1, 0, True),     # UNet level 0 shape (small)
+    (2, 32, 17, 15, 32, 3, 1, 1, 0, True),     # ragged planes: a partial last column tile
+    (3, 24, 9, 11, 72, 1, 1, 0, 0, True),      # pointwise expand (MobileNetV2)
+    (1, 256, 8, 8, 256, 3, 1, 1, 0, True),     # deep channels, few pixels: split K (the finish leaves them)
+    (2, 96, 14, 14, 24, 1, 1, 0, 0, True),     # pointwise project
+    (1, 48, 20, 20, 20, 3, 1, 1, 0, True),     # OC not a multiple of the tile rows
+    (2, 8, 12, 12, 136, 3, 1, 1, 0, True),     # OC past 128: two row blocks
+    (1, 16, 5, 7, 12, 5, 1, 2, 0, True),       # 5x5, tiny planes (one column tile)
+    (2, 3, 20, 20, 16, 3, 1, 1, 0, False),     # C < 4: stride-phase layout, no statistics
+    (2, 16, 20, 20, 16, 3, 2, 1, 0, False),    # stride 2
+    (2, 16, 20, 20, 16, 3, 1, 1, 1, False),    # ReLU
+]
+
+
+def _count(eng, fam):
+    n, ms, fl, by = ctypes.c_uint64(), ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+    ok = eng.lib.GetProfile(fam.encode(), ctypes.byref(n), ctypes.byref(ms), ctypes.byref(fl),
+                            ctypes.byref(by))
+    return int(n.value) if ok else 0
+
+
+def _forward(eng, case, seed):
+    B, C, H, W, OC, k, s, p, act, _ = case
+    r = rng(seed)
+    x = r.standard_normal((B, C, H, W)).astype(np.float32)
+    w = he(r, (OC, C, k, k), C * k * k)
+    # a per-channel offset, so that the one-pass variance is exercised
+    b = (0.5 + r.standard_normal(OC)).astype(np.float32)
+    hx, hw, hb = upload(eng, x), upload(eng, w), upload(eng, b)
+    hy = eng.lib.ConvForwardFused(hx, hw, hb, B, C, H, W, OC, k, k, s, p, act, None)
+    assert hy, eng.last_error()
+    OH, OW = K.conv_out_hw(H, W, k, s, p)
+    y = download(eng, hy, (B, OC, OH, OW))
+    assert rel_err(y, K.conv_forward(x, w, b, s, p, act)) <= TOL
+    release(eng, hx, hw, hb)
+    return hy, y, r
+
+
+def _mean_var(eng, hy, shape, rm, rv, mom=0.1):
+    """batchnorm_mean_var on hy; returns (mean, var, running mean, running
+    var) and the launches of the two statistics families."""
+    B, C, H, W = shape
+    hmu, hvar, hrm, hrv = new(eng, C), new(eng, C), upload(eng, rm), upload(eng, rv)
+    eng.lib.ResetProfile()
+    run(eng, "batchnorm_mean_var", [hy], [hmu, hvar, hrm, hrv], B, C, H * W, 1, fbits(mom))
+    out = [download(eng, h, (C,)) for h in (hmu, hvar, hrm, hrv)]
+    fams = (_count(eng, "bn_stats_side"), _count(eng, "bn_stats"))
+    release(eng, hmu, hvar, hrm, hrv)
+    return out, fams
+
+
+def _copy(eng, h, n):
+    """An untagged copy of buffer h (0 + h, bit for bit)."""
+    c = new(eng, n)
+    eng.lib.ClearBuffer(c)
+    run(eng, "grad_accum", [h], [c], n)
+    return c
+
+
+def _check_oracle(got, y, rm, rv, what, mom=0.1):
+    ref = K.batchnorm_mean_var(y, rm, rv, mom, True)
+    for name, g, rf in zip(("mean", "var", "running mean", "running var"), got, ref):
+        assert rel_err(g, rf) <= 1e-5, f"{what} {name}: {rel_err(g, rf):.3e}"
+
+
+@pytest.mark.parametrize("case", CASES, ids=[str(c) for c in CASES])
+def test_conv_forward_leaves_bn_statistics(eng, case):
+    side = case[-1]
+    eng.lib.SetProfiling(1)
+    try:
+        hy, y, r = _forward(eng, case, 5100 + sum(case[:-1]))
+        C = y.shape[1]
+        rm = r.standard_normal(C).astype(np.float32)
+        rv = (1.0 + r.random(C)).astype(np.float32)
+        got, fams = _mean_var(eng, hy, y.shape, rm, rv)
+        assert fams == ((1, 0) if side else (0, 1)), fams
+        # the tag survives a read: a second call finishes the same sums
+        again, fams2 = _mean_var(eng, hy, y.shape, rm, rv)
+        assert fams2 == fams
+        for a, b in zip(got, again):
+            assert np.array_equal(a, b)
+        hc = _copy(eng, hy, y.size)
+        plain, pf = _mean_var(eng, hc, y.shape, rm, rv)
+        assert pf == (0, 1)
+        for name, a, b in zip(("mean", "var", "rm", "rv"), got, plain):
+            assert rel_err(a, b) <= 1e-6, f"{name} vs the statistics pass: {rel_err(a, b):.3e}"
+        _check_oracle(got, y, rm, rv, "side" if side else "pass")
+        release(eng, hy, hc)
+    finally:
+        eng.lib.SetProfiling(0)
+        eng.lib.ResetProfile()
+
+
+@pytest.mark.parametrize("write", ["update", "shader"])
+def test_bn_statistics_dropped_on_writes(eng, write):
+    """A write to y between the conv forward and batchnorm_mean_var turns the
+    GEMM's statistics off; the statistics follow the written values."""
+    case = CASES[0]
+    eng.lib.SetProfiling(1)
+    try:
+        hy, y, r = _forward(eng, case, 5200)
+        if write == "update":
+            y = (2.0 * y + 1.0).astype(np.float32)
+            eng.lib.UpdateBuffer(hy, np.ascontiguousarray(y).ctypes.data_as(
+                ctypes.POINTER(ctypes.c_float)))
+        else:
+            extra = r.standard_normal(y.shape).astype(np.float32)
+            he_ = upload(eng, extra)
+            run(eng, "grad_accum", [he_], [hy], y.size)
+            y = download(eng, hy, y.shape)
+            release(eng, he_)
+        C = y.shape[1]
+        rm, rv = np.zeros(C, np.float32), np.ones(C, np.float32)
+        got, fams = _mean_var(eng, hy, y.shape, rm, rv)
+        assert fams == (0, 1), fams
+        _check_oracle(got, y, rm, rv, write)
+        release(eng, hy)
+    finally:
+        eng.lib.SetProfiling(0)
+        eng.lib.ResetProfile()
+
+
+def test_bn_statistics_other_geometry(eng):
+    """batchnorm_mean_var over y with another (N, C, S) view than the conv's
+    output takes the statistics pass."""
+    case = CASES[0]
+    eng.lib.SetProfiling(1)
+    try:
+        hy, y, r = _forward(eng, case, 5300)
+        B, C, H, W = y.shape
+        view = (B * 2, C // 2, H, W)
+        yv = y.reshape(view)
+        rm, rv = np.zeros(view[1], np.float32), np.ones(view[1], np.float32)
+        got, fams = _mean_var(eng, hy, view, rm, rv)
+        assert fams == (0, 1), fams
+        _check_oracle(got, yv, rm, rv, "view")
+        release(eng, hy)
+    finally:
+        eng.lib.SetProfiling(0)
+        eng.lib.ResetProfile()
+
+
+def _random_cases(n, seed):
+    """Seeded stride-1, no-activation convolutions of 4-64 input channels
+    (pixel GEMMs over the NHWC copy, or pointwise), 1-160 output channels."""
+    r = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        k = int(r.choice([1, 3, 5]))
+        p = 0 if k == 1 else int(r.integers(0, k // 2 + 1))
+        H, W = int(r.integers(k, 40)), int(r.integers(k, 40))
+        out.append((int(r.integers(1, 4)), int(r.integers(4, 65)), H, W, int(r.integers(1, 161)),
+                    k, 1, p, 0, True))
+    return out
+
+
+RANDOM = _random_cases(12, 9001)
+
+
+@pytest.mark.parametrize("case", RANDOM, ids=[str(c) for c in RANDOM])
+def test_conv_forward_leaves_bn_statistics_random(eng, case):
+    test_conv_forward_leaves_bn_statistics(eng, case)
