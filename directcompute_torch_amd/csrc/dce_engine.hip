@@ -231,6 +231,21 @@ static void drop_tag(Buffer* b, bool park = false) {
     if (park) park_buffer(s); else release_buffer(s);
   }
 }
+void tag_bn_stats(void* y, void* side, uint32_t B, uint32_t C, uint32_t S, uint32_t pieces) {
+  Buffer* Y = static_cast<Buffer*>(y);
+  if (!Y || Y->magic != kMagicLive) {
+    release_buffer(side);
+    return;
+  }
+  drop_tag(Y);
+  set_tag(Y, kBnStatsTag);
+  Y->meta[0] = B;
+  Y->meta[1] = C;
+  Y->meta[2] = S;
+  Y->aux32 = pieces;
+  Y->side = static_cast<Buffer*>(side);
+}
+
 // Buffers an entry point writes in place lose their tags.
 static void drop_tags(void** hs, uint32_t n, bool park = false) {
   for (uint32_t i = 0; hs && i < n; ++i) {
@@ -823,17 +838,10 @@ void* ConvForwardFused(void* x, void* filters, void* bias, uint32_t batch, uint3
     return nullptr;
   }
   if (sctx.side) {
-    Buffer* Y = static_cast<Buffer*>(out);
-    if (sreq.pieces) {
-      set_tag(Y, kBnStatsTag);
-      Y->meta[0] = batch;
-      Y->meta[1] = outC;
-      Y->meta[2] = g.OH * g.OW;
-      Y->aux32 = sreq.pieces;
-      Y->side = sctx.side;
-    } else {
+    if (sreq.pieces)
+      tag_bn_stats(out, sctx.side, batch, outC, g.OH * g.OW, sreq.pieces);
+    else
       release_buffer(sctx.side);
-    }
   }
   if (K) {
     K->tag = kNhwcTag;

@@ -104,6 +104,9 @@ const float* ones4();
 Buffer* as_buffer(void* h, const char* what);
 void* create_buffer(const float* host, uint32_t count);
 void release_buffer(void* h);
+// Tag buffer y (B x C x S floats) kBnStatsTag: `side` (owned by y from now
+// on) holds the per-channel double sums of y and y*y, [C][pieces][2].
+void tag_bn_stats(void* y, void* side, uint32_t B, uint32_t C, uint32_t S, uint32_t pieces);
 
 // ---------------------------------------------------------------------------
 // Fast unsigned division by a run-time constant (numerators < 2^31).

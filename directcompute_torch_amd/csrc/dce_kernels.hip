@@ -2108,15 +2108,20 @@ __global__ void __launch_bounds__(256)
 // (2a*S, 2b*S).  Taps are summed in (fh, fw) order and the bias added last,
 // as in the generic kernel.  An output pair inside its row is one 8-byte
 // store (4-byte aligned for rows of odd length: unaligned access is on).
-template <int K, int S, bool V4>
+// STATS: the band also leaves the batch-norm statistics of what it stores,
+// the double sums of y and y*y (threads add their values in float, then
+// the block tree in double) at stats[(c * B * nb + n * nb + band) * 2]:
+// one piece per band of each image, [C][B * nb][2].
+template <int K, int S, bool V4, bool STATS>
 __global__ void __launch_bounds__(256)
     k_dw_fwd_band(const float* __restrict__ x, const float* __restrict__ f,
                   const float* __restrict__ bias, float* __restrict__ y, uint32_t C, uint32_t H,
                   uint32_t W, uint32_t OH, uint32_t OW, uint32_t p, uint32_t RB, uint32_t nb,
                   uint32_t nbands, uint32_t LR, uint32_t LW, uint32_t BW, uint32_t nx,
-                  FastDiv dLW, FastDiv dNb, FastDiv dBW) {
+                  FastDiv dLW, FastDiv dNb, FastDiv dBW, double* __restrict__ stats) {
   constexpr int XW = S + K;
   __shared__ __attribute__((aligned(16))) float sd[kDwBand];
+  __shared__ double ssum[4];
   BRes bx;
   bx.init(x, nx);
   DwRegs<V4, kDwRegs> v;
@@ -2158,6 +2163,7 @@ __global__ void __launch_bounds__(256)
     const uint32_t o1 = min(o0 + RB, OH);
     float* yp = y + size_t(plane) * OH * OW;
     const uint32_t items = ((o1 - o0 + 1) / 2) * BW;
+    float f0 = 0.f, f1 = 0.f;
     for (uint32_t e = threadIdx.x; e < items; e += 256) {
       const uint32_t a = fdiv(e, dBW), b2 = e - a * BW;
       float win_[XW][XW];
@@ -2182,10 +2188,28 @@ __global__ void __launch_bounds__(256)
           float* row = yp + size_t(oh) * OW + 2 * b2;
           if (2 * b2 + 1 < OW) {
             stu(row, f2{o[0], o[1]});
+            if constexpr (STATS) {
+              f0 += o[0] + o[1];
+              f1 = fmaf(o[1], o[1], fmaf(o[0], o[0], f1));
+            }
           } else {
             row[0] = o[0];
+            if constexpr (STATS) {
+              f0 += o[0];
+              f1 = fmaf(o[0], o[0], f1);
+            }
           }
         }
+      }
+    }
+    if constexpr (STATS) {
+      const double s0 = block_sum256(double(f0), ssum);
+      const double s1 = block_sum256(double(f1), ssum);
+      if (threadIdx.x == 0) {
+        const uint32_t n = plane / C, pieces = (nbands / C);
+        double* d = stats + (size_t(c) * pieces + n * nb + (band - plane * nb)) * 2;
+        d[0] = s0;
+        d[1] = s1;
       }
     }
   }
@@ -2464,13 +2488,26 @@ static bool sh_dw_fwd(const Dispatch& d) {
     const uint32_t BW = (g.OW + 1) / 2;
     const FastDiv fLW = make_fastdiv(bb.v4 ? bb.LW / 4 : bb.LW), fNb = make_fastdiv(nb),
                   fBW = make_fastdiv(BW);
+    // The batch-norm statistics of y ride along (a BN usually follows): a
+    // side buffer of C * B * nb double pairs, owned by y once the launch is
+    // made.
+    const uint32_t pieces = g.B * nb;
+    Buffer* side = nullptr;
+    if (d.nU && uint64_t(g.C) * pieces * 4 < 0xFFFFFFFFull)
+      side = static_cast<Buffer*>(create_buffer(nullptr, g.C * pieces * 4));
+    double* stats = side ? reinterpret_cast<double*>(side->ptr) : nullptr;
     // One block per band, in band order (as the dX band kernel).
 #define DCE_DWF_V(K, SS, V)                                                                      \
   {                                                                                             \
     const uint32_t blocks = nbands;                                                             \
-    hipLaunchKernelGGL((k_dw_fwd_band<K, SS, V>), dim3(blocks), dim3(256), 0, stream(), x.p,     \
-                       f.p, bias.p, y.p, g.C, g.H, g.W, g.OH, g.OW, g.p, bb.RB, nb, nbands,      \
-                       bb.R, bb.LW, BW, nx, fLW, fNb, fBW);                                      \
+    if (stats)                                                                                  \
+      hipLaunchKernelGGL((k_dw_fwd_band<K, SS, V, true>), dim3(blocks), dim3(256), 0, stream(),  \
+                         x.p, f.p, bias.p, y.p, g.C, g.H, g.W, g.OH, g.OW, g.p, bb.RB, nb,       \
+                         nbands, bb.R, bb.LW, BW, nx, fLW, fNb, fBW, stats);                     \
+    else                                                                                        \
+      hipLaunchKernelGGL((k_dw_fwd_band<K, SS, V, false>), dim3(blocks), dim3(256), 0, stream(), \
+                         x.p, f.p, bias.p, y.p, g.C, g.H, g.W, g.OH, g.OW, g.p, bb.RB, nb,       \
+                         nbands, bb.R, bb.LW, BW, nx, fLW, fNb, fBW, nullptr);                   \
   }
 #define DCE_DWF(K, SS)                                                                           \
   if (g.kH == K && g.s == SS) {                                                                 \
@@ -2482,7 +2519,12 @@ static bool sh_dw_fwd(const Dispatch& d) {
     DCE_DWF(3, 1) DCE_DWF(3, 2) DCE_DWF(5, 1) DCE_DWF(5, 2)
 #undef DCE_DWF
 #undef DCE_DWF_V
-    return check_launch("depthwise_conv_forward");
+    if (!check_launch("depthwise_conv_forward")) {
+      release_buffer(side);
+      return false;
+    }
+    if (side) tag_bn_stats(d.uavs[0], side, g.B, g.C, g.OH * g.OW, pieces);
+    return true;
   }
   hipLaunchKernelGGL(k_dw_fwd, dim3(cdiv(total, 256)), dim3(256), 0, stream(), S(d, 0), S(d, 1),
                      S(d, 2), U(d, 0), g, total);

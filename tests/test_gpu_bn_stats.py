@@ -9,6 +9,8 @@ ConvForwardFused with no activation, engine.cpp:690-738):
   no pass over y), and mean, var and the running statistics agree with the
   same call on an untagged copy of y within 1e-6 (double sums in another
   order) and with the float64 oracle within 1e-5;
+* depthwise_conv_forward (nn_depthwise_conv_forward.hlsl:24-50) through its
+  band kernels (3x3 / 5x5, stride 1 / 2) leaves them too;
 * layouts that do not leave statistics (C < 4, stride 2, ReLU) and
   any write to y in between (UpdateBuffer, a shader writing y) fall back to
   the statistics pass, and the results follow the written values."""
@@ -187,3 +189,51 @@ RANDOM = _random_cases(12, 9001)
 @pytest.mark.parametrize("case", RANDOM, ids=[str(c) for c in RANDOM])
 def test_conv_forward_leaves_bn_statistics_random(eng, case):
     test_conv_forward_leaves_bn_statistics(eng, case)
+
+
+# (B, C, H, W, k, s, p): depthwise convolutions on the band kernels
+DW_CASES = [
+    (2, 24, 28, 28, 3, 1, 1),     # MobileNetV2 dw 3x3 s1
+    (2, 16, 29, 31, 3, 2, 1),     # stride 2, odd planes
+    (1, 8, 17, 12, 5, 1, 2),      # 5x5
+    (3, 5, 9, 9, 5, 2, 2),        # 5x5 stride 2, ragged channels
+    (2, 4, 57, 6, 3, 1, 0),       # tall narrow planes, no padding
+]
+
+
+@pytest.mark.parametrize("case", DW_CASES, ids=[str(c) for c in DW_CASES])
+def test_depthwise_forward_leaves_bn_statistics(eng, case):
+    B, C, H, W, k, s, p = case
+    r = rng(5400 + sum(case))
+    x = r.standard_normal((B, C, H, W)).astype(np.float32)
+    f = (r.standard_normal((C, 1, k, k)) / k).astype(np.float32)
+    fb = (0.5 + r.standard_normal(C)).astype(np.float32)
+    OH, OW = (H + 2 * p - k) // s + 1, (W + 2 * p - k) // s + 1
+    hx, hf, hfb, hy = upload(eng, x), upload(eng, f), upload(eng, fb), new(eng, B * C * OH * OW)
+    eng.lib.SetProfiling(1)
+    try:
+        run(eng, "depthwise_conv_forward", [hx, hf, hfb], [hy], B, C, H, W, k, k, s, p, OH)
+        y = download(eng, hy, (B, C, OH, OW))
+        assert rel_err(y, K.depthwise_forward(x, f, fb, s, p)) <= 1e-5
+        rm = r.standard_normal(C).astype(np.float32)
+        rv = (1.0 + r.random(C)).astype(np.float32)
+        got, fams = _mean_var(eng, hy, y.shape, rm, rv)
+        assert fams == (1, 0), fams
+        hc = _copy(eng, hy, y.size)
+        plain, pf = _mean_var(eng, hc, y.shape, rm, rv)
+        assert pf == (0, 1)
+        for name, a, b in zip(("mean", "var", "rm", "rv"), got, plain):
+            assert rel_err(a, b) <= 1e-6, f"{name} vs the statistics pass: {rel_err(a, b):.3e}"
+        _check_oracle(got, y, rm, rv, "depthwise")
+        # a second forward into the same output replaces the statistics
+        x2 = (2.0 * x - 1.0).astype(np.float32)
+        eng.lib.UpdateBuffer(hx, x2.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+        run(eng, "depthwise_conv_forward", [hx, hf, hfb], [hy], B, C, H, W, k, k, s, p, OH)
+        y2 = download(eng, hy, (B, C, OH, OW))
+        got2, fams2 = _mean_var(eng, hy, y.shape, rm, rv)
+        assert fams2 == (1, 0)
+        _check_oracle(got2, y2, rm, rv, "depthwise again")
+        release(eng, hx, hf, hfb, hy, hc)
+    finally:
+        eng.lib.SetProfiling(0)
+        eng.lib.ResetProfile()
