@@ -231,7 +231,8 @@ static void drop_tag(Buffer* b, bool park = false) {
     if (park) park_buffer(s); else release_buffer(s);
   }
 }
-void tag_bn_stats(void* y, void* side, uint32_t B, uint32_t C, uint32_t S, uint32_t pieces) {
+void tag_bn_stats(void* y, void* side, uint32_t B, uint32_t C, uint32_t S, uint32_t pieces,
+                  uint32_t H, uint32_t W) {
   Buffer* Y = static_cast<Buffer*>(y);
   if (!Y || Y->magic != kMagicLive) {
     release_buffer(side);
@@ -242,8 +243,27 @@ void tag_bn_stats(void* y, void* side, uint32_t B, uint32_t C, uint32_t S, uint3
   Y->meta[0] = B;
   Y->meta[1] = C;
   Y->meta[2] = S;
+  Y->meta[3] = H;
+  Y->meta[4] = W;
   Y->aux32 = pieces;
   Y->side = static_cast<Buffer*>(side);
+}
+void tag_grad_g_nhwc(void* dx, void* side, uint32_t B, uint32_t C, uint32_t H, uint32_t W,
+                     uint32_t rows) {
+  Buffer* D = static_cast<Buffer*>(dx);
+  if (!D || D->magic != kMagicLive) {
+    release_buffer(side);
+    return;
+  }
+  drop_tag(D);
+  set_tag(D, kGradGTag);
+  D->meta[0] = kGLayoutNhwc;
+  D->meta[1] = B;
+  D->meta[2] = C;
+  D->meta[3] = H;
+  D->meta[4] = W;
+  D->aux32 = rows;
+  D->side = static_cast<Buffer*>(side);
 }
 
 // Buffers an entry point writes in place lose their tags.
@@ -838,8 +858,11 @@ void* ConvForwardFused(void* x, void* filters, void* bias, uint32_t batch, uint3
     return nullptr;
   }
   if (sctx.side) {
-    if (sreq.pieces)
-      tag_bn_stats(out, sctx.side, batch, outC, g.OH * g.OW, sreq.pieces);
+    if (sreq.pieces) {
+      const bool gn = conv_g_nhwc_pass(g);
+      tag_bn_stats(out, sctx.side, batch, outC, g.OH * g.OW, sreq.pieces, gn ? g.OH : 0,
+                   gn ? g.OW : 0);
+    }
     else
       release_buffer(sctx.side);
   }
@@ -893,10 +916,14 @@ void ConvBackwardFused(void* gradOut, void* fwdOut, void* x, void* filters, void
       // its masked G is already made.
       PreG pre{};
       const PreG* pp = nullptr;
-      if (Y && DY->tag == kGradGTag && DY->side && DY->src == Y &&
-          tag_alive(Y, kReluOutTag, DY->srcGen) && DY->meta[0] == conv_g_layout(g) &&
-          DY->meta[1] == batch && DY->meta[2] == outC && DY->meta[3] == g.OH &&
-          DY->meta[4] == g.OW) {
+      const bool gMatch = DY->tag == kGradGTag && DY->side && DY->meta[1] == batch &&
+                          DY->meta[2] == outC && DY->meta[3] == g.OH && DY->meta[4] == g.OW;
+      // A ReLU conv's masked G (the max-pool backward over its output), or
+      // the plain NHWC G of dy (the batch-norm backward that made dy) for a
+      // conv with no ReLU mask.
+      if ((Y && gMatch && DY->src == Y && tag_alive(Y, kReluOutTag, DY->srcGen) &&
+           DY->meta[0] == conv_g_layout(g)) ||
+          (!Y && actType != 1 && gMatch && DY->meta[0] == kGLayoutNhwc && conv_g_nhwc_pass(g))) {
         pre.layout = DY->meta[0];
         pre.g = DY->side->ptr;
         pre.db = pre.g + g_side_floats(pre.layout, batch, outC, g.OH, g.OW);

@@ -1559,11 +1559,24 @@ static bool permute_w(const WPerm& pw) {
 // is read dword by dword.
 // Workgroups past the first nMain re-lay filters instead (pw: the forward's
 // filter permutation, which then costs no launch of its own).
-template <int CB>
+// BNDX: `in` is the dy of a batch norm and `y` its input x; the values
+// transposed are that batch norm's dx (bn_dx_elem), which the kernel also
+// stores in NCHW to bn.dx: batchnorm_backward_dx and the transpose pass of
+// the conv below it in one pass.
+struct BnDxArgs {
+  const float* mean;
+  const float* var;
+  const float* gamma;
+  const float* dg;
+  const float* db;
+  float* dx;
+  float eps, m;
+};
+template <int CB, bool BNDX = false>
 __global__ void __launch_bounds__(256)
     k_to_nhwc(const float* __restrict__ in, const float* __restrict__ y, float* __restrict__ out,
               float* __restrict__ dbPart, uint32_t C, uint32_t HW, uint32_t Cp, uint32_t npb,
-              uint32_t ncb, uint32_t nB, uint32_t nMain, WPerm pw) {
+              uint32_t ncb, uint32_t nB, uint32_t nMain, WPerm pw, BnDxArgs bn = BnDxArgs{}) {
   if (blockIdx.x >= nMain) {
     permute_w_elem(pw, (blockIdx.x - nMain) * 256 + threadIdx.x);
     return;
@@ -1605,12 +1618,40 @@ __global__ void __launch_bounds__(256)
       }
     }
   }
+  if constexpr (BNDX) {
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t c = c0 + tid / PQ + CR * j, p = p0 + 4 * pq;
+      if (c >= C) {
+        v[j] = zero4();
+        continue;
+      }
+      const float mu = bn.mean[c], rstd = 1.0f / sqrtf(bn.var[c] + bn.eps);
+      const float g = bn.gamma[c], dg = bn.dg[c], db = bn.db[c];
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      // ReLU mask: y <= 0 zeroes the gradient (a NaN y keeps it).
-      t[tid / PQ + CR * j][4 * pq + e] = m[j][e] <= 0.f ? 0.f : v[j][e];
+      for (int e = 0; e < 4; ++e)
+        v[j][e] = p + e < HW ? bn_dx_elem(m[j][e], v[j][e], mu, rstd, g, dg, db, bn.m) : 0.f;
+      float* dst = bn.dx + (size_t(b) * C + c) * HW + p;
+      if (p + 3 < HW) {
+        stu(dst, v[j]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (p + e < HW) dst[e] = v[j][e];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t[tid / PQ + CR * j][4 * pq + e] = v[j][e];
+  } else {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        // ReLU mask: y <= 0 zeroes the gradient (a NaN y keeps it).
+        t[tid / PQ + CR * j][4 * pq + e] = m[j][e] <= 0.f ? 0.f : v[j][e];
+  }
   __syncthreads();
   if (dbPart != nullptr && tid < 8 * CB) {
     // 8 lanes per channel, PB / 8 pixels each, then a fixed butterfly.
@@ -1746,9 +1787,15 @@ template <int SL>
 __global__ void __launch_bounds__(256)
     k_dw_final(const f4* __restrict__ part, float* __restrict__ dw, uint32_t OC, uint32_t C,
                uint32_t KK, uint32_t Cp, uint32_t splits, uint32_t trans, uint32_t nMain,
-               BwdSide side, float* __restrict__ dbCol) {
+               BwdSide side, float* __restrict__ dbCol, WPerm pw) {
   if (blockIdx.x >= nMain) {
-    rowsum_block(side.dbPart, side.db, side.dbRows, blockIdx.x - nMain);
+    // Extra blocks: the bias-gradient sum (one per channel), then a filter
+    // re-layout riding in this launch.
+    const uint32_t e = blockIdx.x - nMain;
+    if (e < side.nRow)
+      rowsum_block(side.dbPart, side.db, side.dbRows, e);
+    else
+      permute_w_elem(pw, (e - side.nRow) * 256 + threadIdx.x);
     return;
   }
   constexpr uint32_t QB = 256 / SL;
@@ -1817,21 +1864,21 @@ static uint32_t dw_final_slices(uint32_t nq, uint32_t splits) {
 
 static bool dw_final(const float* part, float* dw, uint32_t OC, uint32_t C, uint32_t KK,
                      uint32_t Cp, uint32_t splits, bool trans, BwdSide side = BwdSide{},
-                     float* dbCol = nullptr) {
+                     float* dbCol = nullptr, const WPerm& pw = WPerm{}) {
   const uint32_t nq = cdiv(size_t(OC) * KK * Cp, 4), sl = dw_final_slices(nq, splits);
   const f4* p4 = reinterpret_cast<const f4*>(part);
   const uint32_t tr = trans ? 1u : 0u;
   const uint32_t nMain = cdiv(nq, 256u / sl);
-  const dim3 grid(nMain + side.nRow);
+  const dim3 grid(nMain + side.nRow + pw.blocks());
   if (sl == 1)
     hipLaunchKernelGGL(k_dw_final<1>, grid, dim3(256), 0, stream(), p4, dw, OC, C, KK, Cp, splits,
-                       tr, nMain, side, dbCol);
+                       tr, nMain, side, dbCol, pw);
   else if (sl == 4)
     hipLaunchKernelGGL(k_dw_final<4>, grid, dim3(256), 0, stream(), p4, dw, OC, C, KK, Cp, splits,
-                       tr, nMain, side, dbCol);
+                       tr, nMain, side, dbCol, pw);
   else
     hipLaunchKernelGGL(k_dw_final<16>, grid, dim3(256), 0, stream(), p4, dw, OC, C, KK, Cp,
-                       splits, tr, nMain, side, dbCol);
+                       splits, tr, nMain, side, dbCol, pw);
   return check_launch("dw_final");
 }
 
@@ -2362,6 +2409,12 @@ size_t nhwc_floats(uint32_t B, uint32_t C, uint32_t H, uint32_t W) {
   return size_t(B) * H * W * pad4(C);
 }
 
+// Bias-gradient partial rows per channel of the transpose pass (the pixel
+// blocks of every plane): 128-pixel blocks for up to 16 channels, else 64.
+static uint32_t to_nhwc_rows(uint32_t B, uint32_t Cp, uint32_t HW) {
+  return B * (Cp <= 16 ? cdiv(HW, 128) : cdiv(HW, 64));
+}
+
 static bool to_nhwc_masked(const float* in, const float* y, float* out, float* dbPart,
                            uint32_t B, uint32_t C, uint32_t HW, uint32_t* npbOut,
                            const WPerm& pw = WPerm{}) {
@@ -2389,6 +2442,28 @@ static bool to_nhwc_masked(const float* in, const float* y, float* out, float* d
                        out, dbPart, C, HW, Cp, npb, ncb, B, nMain, pw);
   }
   return check_launch("to_nhwc");
+}
+
+uint32_t bn_dx_g_rows(uint32_t B, uint32_t C, uint32_t HW) { return to_nhwc_rows(B, pad4(C), HW); }
+
+bool bn_dx_g(const float* x, const float* dy, const float* mean, const float* var,
+             const float* gamma, const float* dg, const float* db, float eps, float* dx,
+             float* g, float* dbPart, uint32_t B, uint32_t C, uint32_t HW) {
+  const uint32_t Cp = pad4(C);
+  if (uint64_t(B) * C * HW >= kOob || uint64_t(B) * HW * Cp >= kOob) return false;
+  ProfScope prof("bn_bwd_dx", 0, 4.0 * double(B) * HW * (3.0 * C + Cp));
+  const BnDxArgs bn{mean, var, gamma, dg, db, dx, eps, float(uint64_t(B) * HW)};
+  // The same blocks (and bias partials) as the conv backward's transpose pass.
+  if (Cp <= 16) {
+    const uint32_t npb = cdiv(HW, 128), nMain = npb * B;
+    hipLaunchKernelGGL((k_to_nhwc<16, true>), dim3(nMain), dim3(256), 0, stream(), dy, x, g,
+                       dbPart, C, HW, Cp, npb, 1u, B, nMain, WPerm{}, bn);
+  } else {
+    const uint32_t npb = cdiv(HW, 64), ncb = cdiv(Cp, 32), nMain = npb * ncb * B;
+    hipLaunchKernelGGL((k_to_nhwc<32, true>), dim3(nMain), dim3(256), 0, stream(), dy, x, g,
+                       dbPart, C, HW, Cp, npb, ncb, B, nMain, WPerm{}, bn);
+  }
+  return check_launch("batchnorm_backward_dx");
 }
 
 bool to_nhwc(const float* x, float* out, uint32_t B, uint32_t C, uint32_t H, uint32_t W) {
@@ -3286,6 +3361,7 @@ static bool conv_backward_pw(const float* dy, const float* x, const float* w, fl
 }
 
 uint32_t conv_g_layout(const ConvGeom& g) { return ps_x(g) ? kGLayoutPad : kGLayoutNhwc; }
+bool conv_g_nhwc_pass(const ConvGeom& g) { return !ps_x(g) && !pw_x(g); }
 uint32_t conv_g_pad_width(const ConvGeom& g) { return ps_geom(g).OWp; }
 
 bool conv_backward(const float* dy, const float* y, const float* x, const float* x_nhwc,
@@ -3329,12 +3405,15 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
   // A G_pad made by dy's producer (with its bias-gradient partials) replaces
   // the masking pass that makes it.
   const bool preG = pre && pre->layout == kGLayoutPad && useGpad;
+  // An NHWC G made by dy's producer (the batch-norm backward; no ReLU mask)
+  // replaces the transpose pass.
+  const bool preGn = pre && pre->layout == kGLayoutNhwc && !ps && !y;
   const uint32_t nchunk = ps ? cdiv(q.OHWp, kMaskChunk) : 0;
   const uint32_t dbRows = useGpad ? g.B * nchunk : g.B * npb;
   const uint32_t dwK = ps ? g.B * q.OHWp : npix;  // dW GEMM K extent (pixels)
-  const size_t nG = useGnhwc ? al64(size_t(npix) * OCp) : 0;
+  const size_t nG = (useGnhwc && !preGn) ? al64(size_t(npix) * OCp) : 0;
   const size_t nGp = (useGpad && !preG) ? al64(size_t(g.B) * g.OC * q.OHWp) : 0;
-  const size_t nDb = (db && !preG) ? al64(size_t(dbRows) * g.OC) : 0;
+  const size_t nDb = (db && !preG && !preGn) ? al64(size_t(dbRows) * g.OC) : 0;
   const size_t nX = (dw && !x_nhwc) ? al64(xbuild_floats(g)) : 0;
   if (ps && !operand_fits(nGp, "conv_backward")) return false;
   TileCfg dwc{128, 128, 16, 1}, dxc{128, 128, 16, 1};
@@ -3388,6 +3467,10 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
     gp = const_cast<float*>(pre->g);
     if (db) dbPart = const_cast<float*>(pre->db);
   }
+  if (preGn) {
+    gn = const_cast<float*>(pre->g);
+    if (db) dbPart = const_cast<float*>(pre->db);
+  }
 
   if (useGpad && !preG) {
     bool ok = false;
@@ -3398,10 +3481,16 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
   // NHWC G), the bias-gradient sum in the dW finishing launch.
   const WPerm dxPerm{w, wt, g.OC, g.C, KK, OCp, KK * OCp, 1, dx && blocked_k(OCp) ? 1 : 0};
   uint32_t npbGot = npb;
-  if (useGnhwc && !to_nhwc_masked(dy, y, gn, useGpad ? nullptr : dbPart, g.B, g.OC, OHW, &npbGot,
-                                  dx && !phased ? dxPerm : WPerm{}))
+  if (useGnhwc && !preGn &&
+      !to_nhwc_masked(dy, y, gn, useGpad ? nullptr : dbPart, g.B, g.OC, OHW, &npbGot,
+                      dx && !phased ? dxPerm : WPerm{}))
     return false;
-  const uint32_t dbRowsGot = preG ? pre->dbRows : (useGpad ? dbRows : g.B * npbGot);
+  // With the producer's G the dX filter re-layout rides in the dW finish
+  // (which runs before dX), or runs by itself when no dW is asked for.
+  const bool permInFinish = preGn && dx && !phased && dw;
+  if (preGn && dx && !phased && !dw && !permute_w(dxPerm)) return false;
+  const uint32_t dbRowsGot =
+      (preG || preGn) ? pre->dbRows : (useGpad ? dbRows : g.B * npbGot);
   if (db && !dw) {
     hipLaunchKernelGGL(k_rowsum, dim3(g.OC), dim3(256), 0, stream(), dbPart, db, dbRowsGot);
     if (!check_launch("bias_grad")) return false;
@@ -3436,7 +3525,8 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
     // The stride-phase taps are already in the filters' (c, kh, kw) order:
     // the finish is a plain split sum (one channel of C*KK taps).
     return ps ? dw_final(part, dw, g.OC, 1, KK * g.C, 1, dwc.splits, dwT, side)
-              : dw_final(part, dw, g.OC, g.C, KK, Cx, dwc.splits, dwT, side);
+              : dw_final(part, dw, g.OC, g.C, KK, Cx, dwc.splits, dwT, side, nullptr,
+                         permInFinish ? dxPerm : WPerm{});
   };
   if (dw && !(dw_gemm() && dw_finish())) return false;
   if (dx && !dx_chain()) return false;

@@ -37,7 +37,11 @@ struct Buffer {
   //  kBnStatsTag: output of a ConvForwardFused with no activation whose GEMM
   //            left the batch-norm statistics of its values: `side` holds
   //            the per-channel double sums of y and y*y as [C][pieces][2],
-  //            meta = {B, C, H*W}, aux32 = pieces.
+  //            meta = {B, C, H*W, H, W}, aux32 = pieces; meta[3..4] are 0
+  //            unless the conv's backward reads its gradient as an NHWC G
+  //            (then batchnorm_backward_dx over y makes that G);
+  //  kGradGTag also marks the dx of batchnorm_backward_dx over such a y:
+  //            side = [NHWC G | bias-gradient partials], src = null.
   // A tag is dropped (drop_tag) whenever the buffer is written by anything
   // but its producer, and when the buffer goes back to the pool.
   uint32_t tag;
@@ -67,9 +71,18 @@ constexpr uint32_t kGLayoutNhwc = 2;  // [B*OH*OW][pad4(OC)] (the transpose pass
 // Floats of G in `layout` for a conv output [B][C][H][W], rounded up to 64
 // (the bias-gradient partials follow it in a kGradGTag side buffer).
 inline size_t g_side_floats(uint32_t layout, uint32_t B, uint32_t C, uint32_t H, uint32_t W) {
-  (void)layout;  // kGLayoutPad
-  const size_t n = size_t(B) * C * H * ((W + 3u) & ~3u);
+  const size_t n = layout == kGLayoutNhwc ? size_t(B) * H * W * ((C + 3u) & ~3u)
+                                          : size_t(B) * C * H * ((W + 3u) & ~3u);
   return (n + 63) & ~size_t(63);
+}
+
+// batchnorm_backward_dx of one element (nn_batchnorm_backward_dx.hlsl:26-38),
+// shared by every kernel that computes it so that they agree bit for bit:
+// rstd = 1 / sqrt(var + eps), m = N * S.
+__device__ __forceinline__ float bn_dx_elem(float x, float dy, float mu, float rstd, float g,
+                                            float dg, float db, float m) {
+  const float xh = (x - mu) * rstd;
+  return (g * rstd) * (dy - (db + xh * dg) / m);
 }
 
 // Does buffer `b` still carry tag `tag` of generation `gen`?
@@ -105,8 +118,14 @@ Buffer* as_buffer(void* h, const char* what);
 void* create_buffer(const float* host, uint32_t count);
 void release_buffer(void* h);
 // Tag buffer y (B x C x S floats) kBnStatsTag: `side` (owned by y from now
-// on) holds the per-channel double sums of y and y*y, [C][pieces][2].
-void tag_bn_stats(void* y, void* side, uint32_t B, uint32_t C, uint32_t S, uint32_t pieces);
+// on) holds the per-channel double sums of y and y*y, [C][pieces][2].  H, W:
+// the plane of a conv output whose backward reads an NHWC G (else 0, 0).
+void tag_bn_stats(void* y, void* side, uint32_t B, uint32_t C, uint32_t S, uint32_t pieces,
+                  uint32_t H = 0, uint32_t W = 0);
+// Tag dx kGradGTag with an NHWC G side buffer (owned by dx from now on) for
+// the conv whose output has B x C channels of H x W; rows = db partial rows.
+void tag_grad_g_nhwc(void* dx, void* side, uint32_t B, uint32_t C, uint32_t H, uint32_t W,
+                     uint32_t rows);
 
 // ---------------------------------------------------------------------------
 // Fast unsigned division by a run-time constant (numerators < 2^31).
@@ -383,11 +402,23 @@ bool conv_forward(const float* x, float* x_nhwc_keep, const float* w, const floa
 // The layout of G that conv_backward reads for this geometry (kGLayoutPad or
 // kGLayoutNhwc), and the padded row width of kGLayoutPad.
 uint32_t conv_g_layout(const ConvGeom& g);
+// Does the backward of this conv without a ReLU mask make an NHWC G (the
+// transpose pass)?  Not for pointwise or fewer-than-4-channel layers.
+bool conv_g_nhwc_pass(const ConvGeom& g);
+// batchnorm_backward_dx (x, dy, the statistics and gamma, dgamma, dbeta of C
+// channels over B planes of HW) writing dx and, with it, the NHWC G of dx
+// (dx transposed to [B*HW][pad4(C)]) and the bias-gradient partials that a
+// conv backward's transpose pass would make: g_side_floats(kGLayoutNhwc, ...)
+// floats of G, then C x rows partials.  rows = bn_dx_g_rows(B, C, HW).
+uint32_t bn_dx_g_rows(uint32_t B, uint32_t C, uint32_t HW);
+bool bn_dx_g(const float* x, const float* dy, const float* mean, const float* var,
+             const float* gamma, const float* dg, const float* db, float eps, float* dx,
+             float* g, float* dbPart, uint32_t B, uint32_t C, uint32_t HW);
 uint32_t conv_g_pad_width(const ConvGeom& g);
 // A masked gradient G made by the producer of dy (the max-pool backward):
 // g in `layout` (kGLayoutPad), db = bias-gradient partials [OC][dbRows].
 struct PreG {
-  uint32_t layout;
+  uint32_t layout;  // kGLayoutPad (a ReLU conv's masked G) or kGLayoutNhwc (no mask)
   const float* g;
   const float* db;
   uint32_t dbRows;

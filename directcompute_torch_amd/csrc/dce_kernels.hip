@@ -888,7 +888,7 @@ __global__ void k_bn_elem(Buf x, Buf dy, Buf mean, Buf var, Buf gamma, Buf beta_
   } else {
     const float g = ld(gamma, c), dg = ld(beta_or_dg, c), db = ld(dbeta, c);
     const float dyv = CHECK ? ld(dy, i) : dy.p[i];
-    const float v = (g * rstd) * (dyv - (db + xh * dg) / m);
+    const float v = bn_dx_elem(xv, dyv, mu, rstd, g, dg, db, m);
     if (CHECK) st(out, i, v); else out.p[i] = v;
   }
 }
@@ -917,10 +917,7 @@ __global__ void __launch_bounds__(256)
     const float g = gamma[c], dg = beta_or_dg[c], db = dbeta[c];
     const f4 gv = ld4s<NT>(dy + size_t(i) * 4);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float xh = (xv[e] - mu) * rstd;
-      r[e] = (g * rstd) * (gv[e] - (db + xh * dg) / m);
-    }
+    for (int e = 0; e < 4; ++e) r[e] = bn_dx_elem(xv[e], gv[e], mu, rstd, g, dg, db, m);
   }
   st4s<NT>(out + size_t(i) * 4, r);
 }
@@ -972,7 +969,39 @@ static bool bn_elem(const char* what, const Dispatch& d) {
   return check_launch(what);
 }
 static bool sh_bn_forward(const Dispatch& d) { return bn_elem<0>("batchnorm_forward", d); }
-static bool sh_bn_backward_dx(const Dispatch& d) { return bn_elem<1>("batchnorm_backward_dx", d); }
+// Over the output of a conv whose backward reads an NHWC G (the forward's
+// tag says so), dx comes with that G and its bias-gradient partials (owned
+// by dx, kGradGTag), and the conv backward then runs no transpose pass.
+static bool sh_bn_backward_dx(const Dispatch& d) {
+  const uint32_t N = CU(d, 0), C = CU(d, 1), Sz = CU(d, 2);
+  const float eps = CF(d, 3);
+  const Buffer* X = d.nS >= 7 ? static_cast<const Buffer*>(d.srvs[0]) : nullptr;
+  if (N && C && Sz && d.nU && X && X->magic == kMagicLive && X->tag == kBnStatsTag &&
+      X->meta[0] == N && X->meta[1] == C && X->meta[2] == Sz && X->meta[3] &&
+      uint64_t(X->meta[3]) * X->meta[4] == Sz) {
+    const uint64_t total = uint64_t(N) * C * Sz;
+    const Buf x = S(d, 0), dy = S(d, 1), mean = S(d, 2), var = S(d, 3), gamma = S(d, 4),
+              dg = S(d, 5), db = S(d, 6), out = U(d, 0);
+    const size_t nG = g_side_floats(kGLayoutNhwc, N, C, X->meta[3], X->meta[4]);
+    const uint32_t rows = bn_dx_g_rows(N, C, Sz);
+    const uint64_t side_n = nG + uint64_t(rows) * C;
+    if (covers(x, total) && covers(dy, total) && covers(out, total) && covers(mean, C) &&
+        covers(var, C) && covers(gamma, C) && covers(dg, C) && covers(db, C) &&
+        side_n < 0xFFFFFFFFull) {
+      Buffer* side = static_cast<Buffer*>(create_buffer(nullptr, uint32_t(side_n)));
+      if (side) {
+        if (!bn_dx_g(x.p, dy.p, mean.p, var.p, gamma.p, dg.p, db.p, eps, out.p, side->ptr,
+                     side->ptr + nG, N, C, Sz)) {
+          release_buffer(side);
+          return false;
+        }
+        tag_grad_g_nhwc(d.uavs[0], side, N, C, X->meta[3], X->meta[4], rows);
+        return true;
+      }
+    }
+  }
+  return bn_elem<1>("batchnorm_backward_dx", d);
+}
 
 // ===========================================================================
 // Max pooling
@@ -2533,7 +2562,7 @@ static bool sh_dw_fwd(const Dispatch& d) {
       release_buffer(side);
       return false;
     }
-    if (side) tag_bn_stats(d.uavs[0], side, g.B, g.C, g.OH * g.OW, pieces);
+    if (side) tag_bn_stats(d.uavs[0], side, g.B, g.C, g.OH * g.OW, pieces);  // no conv G
     return true;
   }
   hipLaunchKernelGGL(k_dw_fwd, dim3(cdiv(total, 256)), dim3(256), 0, stream(), S(d, 0), S(d, 1),

@@ -1,4 +1,5 @@
-"""GPU parity of the batch-norm statistics left by a conv forward's GEMM
+"""GPU parity of the batch-norm statistics left by a conv forward's GEMM, and
+of the conv's NHWC G made by the batch-norm backward
 (batchnorm_mean_var, nn_batchnorm_mean_var.hlsl:19-61, on the output of a
 ConvForwardFused with no activation, engine.cpp:690-738):
 
@@ -13,7 +14,12 @@ ConvForwardFused with no activation, engine.cpp:690-738):
   band kernels (3x3 / 5x5, stride 1 / 2) leaves them too;
 * layouts that do not leave statistics (C < 4, stride 2, ReLU) and
   any write to y in between (UpdateBuffer, a shader writing y) fall back to
-  the statistics pass, and the results follow the written values."""
+  the statistics pass, and the results follow the written values;
+* batchnorm_backward_dx over such a conv's output (when the conv's backward
+  has a transpose pass: not pointwise) also writes the conv's NHWC G and
+  bias-gradient partials; the BN dx and the conv's dW, db, dX are bit for
+  bit those of the unfused chain, the conv backward runs no transpose pass,
+  and a gradient accumulated into dx in between turns it off."""
 import ctypes
 
 import numpy as np
@@ -234,6 +240,125 @@ def test_depthwise_forward_leaves_bn_statistics(eng, case):
         assert fams2 == (1, 0)
         _check_oracle(got2, y2, rm, rv, "depthwise again")
         release(eng, hx, hf, hfb, hy, hc)
+    finally:
+        eng.lib.SetProfiling(0)
+        eng.lib.ResetProfile()
+
+
+# (B, C, H, W, OC, k, s, p): conv (no activation) -> batch norm; the BN
+# backward makes the conv's NHWC G when the conv's backward has a transpose pass
+BNG_CASES = [
+    (2, 16, 24, 24, 16, 3, 1, 1),     # UNet level 0 shape (16 channels: 128-pixel blocks)
+    (2, 32, 13, 17, 48, 3, 1, 1),     # 48 channels: 64-pixel blocks, ragged planes
+    (1, 8, 9, 9, 6, 5, 1, 2),         # OC not a multiple of 4 (padded G rows)
+    (2, 24, 10, 10, 40, 3, 2, 1),     # stride 2 (the forward leaves no statistics: plain BN dx)
+    (2, 24, 8, 8, 36, 1, 1, 0),       # pointwise: no transpose pass, plain BN dx
+]
+
+
+def _bn_chain(eng, case, seed, write_dx=False):
+    """conv -> BN forward -> BN backward -> ConvBackwardFused; returns what the
+    fused chain and the same calls on untagged copies give, and the launch
+    counts of the conv backward's transpose passes."""
+    B, C, H, W, OC, k, s, p = case
+    r = rng(seed)
+    x = r.standard_normal((B, C, H, W)).astype(np.float32)
+    w = he(r, (OC, C, k, k), C * k * k)
+    b = (0.5 + r.standard_normal(OC)).astype(np.float32)
+    hx, hw, hb = upload(eng, x), upload(eng, w), upload(eng, b)
+    pim = ctypes.c_void_p()
+    hy = eng.lib.ConvForwardFused(hx, hw, hb, B, C, H, W, OC, k, k, s, p, 0, ctypes.byref(pim))
+    assert hy, eng.last_error()
+    OH, OW = K.conv_out_hw(H, W, k, s, p)
+    y = download(eng, hy, (B, OC, OH, OW))
+    S_ = OH * OW
+    gamma = (1.0 + 0.2 * r.standard_normal(OC)).astype(np.float32)
+    hg = upload(eng, gamma)
+    hmu, hvar = new(eng, OC), new(eng, OC)
+    hrm, hrv = upload(eng, np.zeros(OC, np.float32)), upload(eng, np.ones(OC, np.float32))
+    run(eng, "batchnorm_mean_var", [hy], [hmu, hvar, hrm, hrv], B, OC, S_, 1, fbits(0.1))
+    dz = r.standard_normal(y.shape).astype(np.float32)
+    hdz = upload(eng, dz)
+    eps = 1e-5
+    hdg, hdb = new(eng, OC), new(eng, OC)
+    run(eng, "batchnorm_backward_reduce", [hy, hdz, hmu, hvar], [hdg, hdb], B, OC, S_, fbits(eps))
+    out = {}
+    yc = _copy(eng, hy, y.size)
+    for name, hin in (("fused", hy), ("plain", yc)):
+        hdx = new(eng, y.size)
+        run(eng, "batchnorm_backward_dx", [hin, hdz, hmu, hvar, hg, hdg, hdb], [hdx], B, OC, S_,
+            fbits(eps))
+        if write_dx and name == "fused":
+            extra = r.standard_normal(y.shape).astype(np.float32)
+            he_ = upload(eng, extra)
+            run(eng, "grad_accum", [he_], [hdx], y.size)
+            release(eng, he_)
+        dx_bn = download(eng, hdx, y.shape)
+        # the conv backward on this dx; a ConvBackwardFused consumes the
+        # forward's copy of x, so the plain call gets a second forward's
+        pim_b = pim
+        if name == "plain":
+            pim_b = ctypes.c_void_p()
+            hy2 = eng.lib.ConvForwardFused(hx, hw, hb, B, C, H, W, OC, k, k, s, p, 0,
+                                           ctypes.byref(pim_b))
+            assert hy2, eng.last_error()
+            release(eng, hy2)
+        pdf, pdb, pdx = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+        eng.lib.ResetProfile()
+        eng.lib.ConvBackwardFused(hdx, None, hx, hw, pim_b.value, B, C, H, W, OC, k, k, s, p, 0, 1,
+                                  1, 1, ctypes.byref(pdf), ctypes.byref(pdb), ctypes.byref(pdx))
+        assert pdf.value and pdb.value and pdx.value, eng.last_error()
+        out[name] = dict(dx_bn=dx_bn, dW=download(eng, pdf.value, w.shape),
+                         db=download(eng, pdb.value, (OC,)), dX=download(eng, pdx.value, x.shape),
+                         passes=_count(eng, "nhwc") + _count(eng, "conv_grad_nhwc"))
+        release(eng, hdx, pdf.value, pdb.value, pdx.value)
+    release(eng, hx, hw, hb, hy, yc, hg, hmu, hvar, hrm, hrv, hdz, hdg, hdb)
+    return out, dict(x=x, w=w, y=y, s=s, p=p)
+
+
+def _check_conv_oracle(f, d, s, p):
+    """dW, dX against the float64 oracle within TOL; db, a sum over every
+    pixel of a batch norm's dx (zero up to round-off, as that dx sums to
+    zero per channel), within 1e-5 of the channel's sum of |dx|."""
+    dW_r, db_r, dX_r = K.conv_backward(f["dx_bn"], d["y"], d["x"], d["w"], s, p, 0)
+    for name, ref in (("dW", dW_r), ("dX", dX_r)):
+        assert rel_err(f[name], ref) <= TOL, f"{name}: {rel_err(f[name], ref):.3e}"
+    scale = np.abs(f["dx_bn"].astype(np.float64)).sum(axis=(0, 2, 3))
+    assert np.all(np.abs(f["db"] - db_r) <= 1e-5 * scale), "db"
+
+
+@pytest.mark.parametrize("case", BNG_CASES, ids=[str(c) for c in BNG_CASES])
+def test_bn_backward_makes_conv_g(eng, case):
+    B, C, H, W, OC, k, s, p = case
+    fused_g = s == 1 and k > 1
+    eng.lib.SetProfiling(1)
+    try:
+        out, d = _bn_chain(eng, case, 5500 + sum(case))
+        f, q = out["fused"], out["plain"]
+        assert np.array_equal(f["dx_bn"], q["dx_bn"]), "BN dx differs from the plain kernel"
+        for name in ("dW", "dX", "db"):
+            assert np.array_equal(f[name], q[name]), f"{name} differs from the unfused chain"
+        if fused_g:
+            assert f["passes"] == 0 and q["passes"] > 0, (f["passes"], q["passes"])
+        else:
+            assert f["passes"] == q["passes"]
+        _check_conv_oracle(f, d, s, p)
+    finally:
+        eng.lib.SetProfiling(0)
+        eng.lib.ResetProfile()
+
+
+def test_bn_backward_g_dropped_on_write(eng):
+    """A gradient accumulated into the BN's dx before the conv backward turns
+    the G off; the conv backward follows the accumulated values."""
+    case = BNG_CASES[0]
+    B, C, H, W, OC, k, s, p = case
+    eng.lib.SetProfiling(1)
+    try:
+        out, d = _bn_chain(eng, case, 5600, write_dx=True)
+        f = out["fused"]
+        assert f["passes"] > 0
+        _check_conv_oracle(f, d, s, p)
     finally:
         eng.lib.SetProfiling(0)
         eng.lib.ResetProfile()
