@@ -248,6 +248,45 @@ void tag_bn_stats(void* y, void* side, uint32_t B, uint32_t C, uint32_t S, uint3
   Y->aux32 = pieces;
   Y->side = static_cast<Buffer*>(side);
 }
+// The activation that followed each batch norm (keyed by its gamma buffer
+// record) the last time one ran on its output.
+static std::unordered_map<const void*, uint32_t> g_bnAct;
+uint32_t bn_act_guess(const void* gamma) {
+  auto it = gamma ? g_bnAct.find(gamma) : g_bnAct.end();
+  return it == g_bnAct.end() ? 0u : it->second;
+}
+void tag_bn_out(void* z, void* gamma, void* side, uint32_t act) {
+  Buffer* Z = static_cast<Buffer*>(z);
+  if (!Z || Z->magic != kMagicLive) {
+    release_buffer(side);
+    return;
+  }
+  drop_tag(Z);
+  set_tag(Z, kBnOutTag);
+  Z->aux = static_cast<Buffer*>(gamma);
+  Z->aux32 = side ? act : 0u;
+  Z->side = static_cast<Buffer*>(side);
+}
+bool bn_act_adopt(void* z, void* a, uint32_t act, uint32_t n) {
+  Buffer* Z = static_cast<Buffer*>(z);
+  Buffer* A = static_cast<Buffer*>(a);
+  if (!Z || Z->magic != kMagicLive || Z->tag != kBnOutTag) return false;
+  if (Z->aux) g_bnAct[Z->aux] = act;
+  Buffer* S = Z->side;
+  if (!S || Z->aux32 != act || !A || A == Z || A->magic != kMagicLive || A->count != S->count ||
+      n != S->count)
+    return false;
+  // A's contents become act(z): take S's storage, give S A's (same size) and
+  // return S to the pool.  Handles are opaque, so no caller holds the old
+  // address; work already queued on A's old storage runs before any reuse
+  // (one stream).
+  std::swap(A->ptr, S->ptr);
+  Z->side = nullptr;
+  Z->aux32 = 0;
+  release_buffer(S);
+  return true;
+}
+
 void tag_grad_g_nhwc(void* dx, void* side, uint32_t B, uint32_t C, uint32_t H, uint32_t W,
                      uint32_t rows) {
   Buffer* D = static_cast<Buffer*>(dx);

@@ -41,7 +41,11 @@ struct Buffer {
   //            unless the conv's backward reads its gradient as an NHWC G
   //            (then batchnorm_backward_dx over y makes that G);
   //  kGradGTag also marks the dx of batchnorm_backward_dx over such a y:
-  //            side = [NHWC G | bias-gradient partials], src = null.
+  //            side = [NHWC G | bias-gradient partials], src = null;
+  //  kBnOutTag: output z of batchnorm_forward; aux = that call's gamma
+  //            buffer (a key only: the layer), and when the forward also
+  //            stored act(z) for the activation that followed this layer
+  //            last time, side = that buffer, aux32 = 1 (relu) or 2 (relu6).
   // A tag is dropped (drop_tag) whenever the buffer is written by anything
   // but its producer, and when the buffer goes back to the pool.
   uint32_t tag;
@@ -64,6 +68,7 @@ constexpr uint32_t kReluOutTag = 0x9003u;
 constexpr uint32_t kPoolOutTag = 0x9004u;
 constexpr uint32_t kGradGTag = 0x9005u;
 constexpr uint32_t kBnStatsTag = 0x9006u;
+constexpr uint32_t kBnOutTag = 0x9007u;
 // Layouts of a conv backward's masked gradient G.
 constexpr uint32_t kGLayoutPad = 1;   // [B*OC][OH][pad4(OW)], zero past OW (stride-phase dW)
 constexpr uint32_t kGLayoutNhwc = 2;  // [B*OH*OW][pad4(OC)] (the transpose pass)
@@ -122,6 +127,17 @@ void release_buffer(void* h);
 // the plane of a conv output whose backward reads an NHWC G (else 0, 0).
 void tag_bn_stats(void* y, void* side, uint32_t B, uint32_t C, uint32_t S, uint32_t pieces,
                   uint32_t H = 0, uint32_t W = 0);
+// The activation (1 relu, 2 relu6, 0 none seen) that last followed the batch
+// norm whose gamma buffer is `gamma`.
+uint32_t bn_act_guess(const void* gamma);
+// Tag z (a batchnorm_forward output) kBnOutTag; side (may be null) holds
+// act(z), owned by z from now on.
+void tag_bn_out(void* z, void* gamma, void* side, uint32_t act);
+// relu (act 1) / relu6 (act 2) of n elements from z into a: when z carries
+// that activation already stored for all n elements of a, a takes that
+// storage over (a's own goes back to the pool) and true is returned; the
+// activation is remembered for z's layer either way.
+bool bn_act_adopt(void* z, void* a, uint32_t act, uint32_t n);
 // Tag dx kGradGTag with an NHWC G side buffer (owned by dx from now on) for
 // the conv whose output has B x C channels of H x W; rows = db partial rows.
 void tag_grad_g_nhwc(void* dx, void* side, uint32_t B, uint32_t C, uint32_t H, uint32_t W,

@@ -159,14 +159,18 @@ static inline bool covers(const Buf& b, uint64_t n) { return b.p && uint64_t(b.n
 // ===========================================================================
 // Elementwise shaders
 // ===========================================================================
+// relu / relu6 over a batch norm's output whose forward already stored the
+// activation (same functor, same elements) adopt that buffer as the output.
 static bool sh_relu(const Dispatch& d) {  // nn_relu.hlsl: no constants, bounded by the output
   Buf o = U(d, 0);
+  if (d.nS && d.nU && bn_act_adopt(d.srvs[0], d.uavs[0], 1, o.n)) return true;
   return run_ew("relu", OpRelu{}, o, S(d, 0), Buf{nullptr, 0}, o.n, true);
 }
 static bool sh_relu_grad(const Dispatch& d) {
   return run_ew("relu_grad", OpReluGrad{}, U(d, 0), S(d, 0), S(d, 1), CU(d, 0), false);
 }
 static bool sh_relu6(const Dispatch& d) {
+  if (d.nS && d.nU && bn_act_adopt(d.srvs[0], d.uavs[0], 2, CU(d, 0))) return true;
   return run_ew("relu6", OpRelu6{}, U(d, 0), S(d, 0), Buf{nullptr, 0}, CU(d, 0), true);
 }
 static bool sh_relu6_grad(const Dispatch& d) {
@@ -893,14 +897,17 @@ __global__ void k_bn_elem(Buf x, Buf dy, Buf mean, Buf var, Buf gamma, Buf beta_
   }
 }
 // Quad form (S % 4 == 0, every buffer covering its size): the four elements
-// of a quad share a channel, whose parameters are computed once.
-template <int MODE, bool NT>
+// of a quad share a channel, whose parameters are computed once.  ACT (the
+// forward only): also store ACT(y) to act_out (1: relu, 2: relu6, with the
+// relu / relu6 shaders' own functors), for the activation that follows.
+template <int MODE, bool NT, int ACT = 0>
 __global__ void __launch_bounds__(256)
     k_bn_elem4(const float* __restrict__ x, const float* __restrict__ dy,
                const float* __restrict__ mean, const float* __restrict__ var,
                const float* __restrict__ gamma, const float* __restrict__ beta_or_dg,
                const float* __restrict__ dbeta, float* __restrict__ out, float eps, uint32_t C,
-               uint32_t total4, FastDiv dS4, FastDiv dC, float m) {
+               uint32_t total4, FastDiv dS4, FastDiv dC, float m,
+               float* __restrict__ act_out = nullptr) {
   const uint32_t i = blockIdx.x * 256 + threadIdx.x;
   if (i >= total4) return;
   const uint32_t q = fdiv(i, dS4);
@@ -920,6 +927,12 @@ __global__ void __launch_bounds__(256)
     for (int e = 0; e < 4; ++e) r[e] = bn_dx_elem(xv[e], gv[e], mu, rstd, g, dg, db, m);
   }
   st4s<NT>(out + size_t(i) * 4, r);
+  if constexpr (ACT != 0) {
+    f4 a;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) a[e] = ACT == 1 ? OpRelu{}(r[e], 0.f) : OpRelu6{}(r[e], 0.f);
+    st4s<NT>(act_out + size_t(i) * 4, a);
+  }
 }
 
 template <int MODE>
@@ -947,6 +960,32 @@ static bool bn_elem(const char* what, const Dispatch& d) {
       covers(mean, C) && covers(var, C) && covers(gamma, C) && covers(b2, C) &&
       (MODE == 0 || covers(db, C))) {
     const uint32_t total4 = uint32_t(total / 4);
+    if constexpr (MODE == 0) {
+      // The activation that followed this batch norm (same gamma) last time
+      // is stored as well, into a buffer that the activation's call adopts
+      // as its output (bn_act_adopt) instead of running.
+      const uint32_t act = d.nS >= 4 && d.nU ? bn_act_guess(d.srvs[3]) : 0;
+      Buffer* side = act ? static_cast<Buffer*>(create_buffer(nullptr, uint32_t(total))) : nullptr;
+      if (side) {
+        const bool nt = stream_nt(12.0 * double(total));
+#define DCE_BNA(A, NTV)                                                                         \
+  hipLaunchKernelGGL((k_bn_elem4<0, NTV, A>), dim3(cdiv(total4, 256)), dim3(256), 0, stream(),  \
+                     x.p, dy.p, mean.p, var.p, gamma.p, b2.p, db.p, out.p, eps, C, total4,      \
+                     make_fastdiv(Sz / 4), make_fastdiv(C), float(uint64_t(N) * Sz), side->ptr)
+        if (act == 1 && nt) DCE_BNA(1, true);
+        else if (act == 1) DCE_BNA(1, false);
+        else if (nt) DCE_BNA(2, true);
+        else DCE_BNA(2, false);
+#undef DCE_BNA
+        if (!check_launch(what)) {
+          release_buffer(side);
+          return false;
+        }
+        tag_bn_out(d.uavs[0], d.srvs[3], side, act);
+        return true;
+      }
+      tag_bn_out(d.uavs[0], d.nS >= 4 ? d.srvs[3] : nullptr, nullptr, 0);
+    }
     if (stream_nt((MODE == 1 ? 12.0 : 8.0) * double(total)))
       hipLaunchKernelGGL((k_bn_elem4<MODE, true>), dim3(cdiv(total4, 256)), dim3(256), 0,
                          stream(), x.p, dy.p, mean.p, var.p, gamma.p, b2.p, db.p, out.p, eps, C,

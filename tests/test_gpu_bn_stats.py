@@ -362,3 +362,89 @@ def test_bn_backward_g_dropped_on_write(eng):
     finally:
         eng.lib.SetProfiling(0)
         eng.lib.ResetProfile()
+
+
+def _bn_forward(eng, hx, shape, hg, hb, eps=1e-5):
+    B, C, H, W = shape
+    hmu, hvar = new(eng, C), new(eng, C)
+    hrm, hrv = upload(eng, np.zeros(C, np.float32)), upload(eng, np.ones(C, np.float32))
+    run(eng, "batchnorm_mean_var", [hx], [hmu, hvar, hrm, hrv], B, C, H * W, 1, fbits(0.1))
+    hz = new(eng, B * C * H * W)
+    run(eng, "batchnorm_forward", [hx, hmu, hvar, hg, hb], [hz], B, C, H * W, fbits(eps))
+    release(eng, hmu, hvar, hrm, hrv)
+    return hz
+
+
+@pytest.mark.parametrize("act", ["relu", "relu6"])
+def test_bn_forward_stores_next_activation(eng, act):
+    """batchnorm_forward also stores the activation that followed the same
+    layer (gamma buffer) last time; that relu / relu6 call then adopts it
+    (no launch) with the bits its own kernel gives.  A write to z in
+    between, another activation or another element count runs the kernel."""
+    B, C, H, W = 2, 12, 10, 8
+    r = rng(5700 + len(act))
+    n = B * C * H * W
+    x = (2.0 * r.standard_normal((B, C, H, W))).astype(np.float32)
+    gamma = (1.0 + r.standard_normal(C)).astype(np.float32)
+    beta = (3.0 * r.standard_normal(C)).astype(np.float32)
+    hx, hg, hb = upload(eng, x), upload(eng, gamma), upload(eng, beta)
+    ref_fn = K.relu if act == "relu" else K.relu6
+    cb = () if act == "relu" else (n,)
+    eng.lib.SetProfiling(1)
+    try:
+        outs = []
+        for rnd in range(3):
+            hz = _bn_forward(eng, hx, x.shape, hg, hb)
+            z = download(eng, hz, x.shape)
+            ha = new(eng, n)
+            eng.lib.ResetProfile()
+            run(eng, act, [hz], [ha], *cb)
+            launches = _count(eng, act)
+            a = download(eng, ha, x.shape)
+            assert np.array_equal(a, ref_fn(z).astype(np.float32)), rnd
+            outs.append((a, launches))
+            release(eng, hz, ha)
+        assert outs[0][1] == 1 and outs[1][1] == 0 and outs[2][1] == 0, [o[1] for o in outs]
+        assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][0], outs[2][0])
+        # a write to z in between: the kernel runs on the written values
+        hz = _bn_forward(eng, hx, x.shape, hg, hb)
+        z2 = (download(eng, hz, x.shape) - 1.0).astype(np.float32)
+        eng.lib.UpdateBuffer(hz, z2.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+        ha = new(eng, n)
+        eng.lib.ResetProfile()
+        run(eng, act, [hz], [ha], *cb)
+        assert _count(eng, act) == 1
+        assert np.array_equal(download(eng, ha, x.shape), ref_fn(z2).astype(np.float32))
+        release(eng, hz, ha)
+        # the other activation on this layer's output: its own kernel
+        other = "relu6" if act == "relu" else "relu"
+        hz = _bn_forward(eng, hx, x.shape, hg, hb)
+        z = download(eng, hz, x.shape)
+        ha = new(eng, n)
+        eng.lib.ResetProfile()
+        run(eng, other, [hz], [ha], *(() if other == "relu" else (n,)))
+        assert _count(eng, other) == 1
+        ofn = K.relu if other == "relu" else K.relu6
+        assert np.array_equal(download(eng, ha, x.shape), ofn(z).astype(np.float32))
+        release(eng, hz, ha)
+        # `act` again (the kernel: the layer stored the other one), then an
+        # output of other elements than the stored one: the kernel
+        hz = _bn_forward(eng, hx, x.shape, hg, hb)
+        ha = new(eng, n)
+        eng.lib.ResetProfile()
+        run(eng, act, [hz], [ha], *cb)
+        assert _count(eng, act) == 1
+        release(eng, hz, ha)
+        hz = _bn_forward(eng, hx, x.shape, hg, hb)
+        z = download(eng, hz, x.shape).reshape(-1)
+        ha = new(eng, n - 8 if act == "relu" else n)
+        eng.lib.ResetProfile()
+        run(eng, act, [hz], [ha], *(() if act == "relu" else (n - 8,)))
+        assert _count(eng, act) == 1
+        a = download(eng, ha, (n - 8 if act == "relu" else n,))
+        assert np.array_equal(a[:n - 8], ref_fn(z)[:n - 8].astype(np.float32))
+        release(eng, hz, ha)
+    finally:
+        eng.lib.SetProfiling(0)
+        eng.lib.ResetProfile()
+        release(eng, hx, hg, hb)
