@@ -226,6 +226,7 @@ static void park_buffer(Buffer* b);
 static void drop_tag(Buffer* b, bool park = false) {
   b->tag = 0;
   b->src = b->aux = nullptr;
+  b->key = nullptr;
   if (Buffer* s = b->side) {
     b->side = nullptr;
     if (park) park_buffer(s); else release_buffer(s);
@@ -255,7 +256,8 @@ uint32_t bn_act_guess(const void* gamma) {
   auto it = gamma ? g_bnAct.find(gamma) : g_bnAct.end();
   return it == g_bnAct.end() ? 0u : it->second;
 }
-void tag_bn_out(void* z, void* gamma, void* side, uint32_t act) {
+void tag_bn_out(void* z, void* x, void* mean, void* gamma, void* side, uint32_t act,
+                uint32_t N, uint32_t C, uint32_t S, float eps) {
   Buffer* Z = static_cast<Buffer*>(z);
   if (!Z || Z->magic != kMagicLive) {
     release_buffer(side);
@@ -263,15 +265,103 @@ void tag_bn_out(void* z, void* gamma, void* side, uint32_t act) {
   }
   drop_tag(Z);
   set_tag(Z, kBnOutTag);
-  Z->aux = static_cast<Buffer*>(gamma);
+  Z->key = gamma;
   Z->aux32 = side ? act : 0u;
   Z->side = static_cast<Buffer*>(side);
+  Z->meta[0] = N;
+  Z->meta[1] = C;
+  Z->meta[2] = S;
+  memcpy(&Z->aux32b, &eps, 4);
+  // x and the statistics, linked while they carry the tags they have now
+  // (the backward's fused reduce uses them only then).
+  Buffer* X = static_cast<Buffer*>(x);
+  Buffer* M = static_cast<Buffer*>(mean);
+  if (X && X->magic == kMagicLive && X->tag == kBnStatsTag && M && M->magic == kMagicLive &&
+      M->tag == kBnMomentTag) {
+    Z->src = X;
+    Z->srcGen = X->gen;
+    Z->aux = M;
+    Z->auxGen = M->gen;
+  }
+}
+void tag_bn_moments(void* mean, void* var) {
+  Buffer* M = static_cast<Buffer*>(mean);
+  Buffer* V = static_cast<Buffer*>(var);
+  if (!M || !V || M == V || M->magic != kMagicLive || V->magic != kMagicLive) return;
+  drop_tag(V);
+  set_tag(V, kBnMomentTag);
+  drop_tag(M);
+  set_tag(M, kBnMomentTag);
+  M->src = V;
+  M->srcGen = V->gen;
+}
+// z's batch norm operands, each still carrying the tag it had when linked.
+static bool bn_links_alive(const Buffer* Z, Buffer** x, Buffer** mean, Buffer** var) {
+  if (!Z || Z->magic != kMagicLive || Z->tag != kBnOutTag || !Z->src || !Z->aux) return false;
+  Buffer* X = Z->src;
+  Buffer* M = Z->aux;
+  if (!tag_alive(X, kBnStatsTag, Z->srcGen) || !tag_alive(M, kBnMomentTag, Z->auxGen) ||
+      !tag_alive(M->src, kBnMomentTag, M->srcGen))
+    return false;
+  *x = X;
+  *mean = M;
+  *var = M->src;
+  return true;
+}
+bool bn_link_of(void* z, BnLink* out) {
+  const Buffer* Z = static_cast<const Buffer*>(z);
+  Buffer *X, *M, *V;
+  if (!bn_links_alive(Z, &X, &M, &V)) return false;
+  const uint64_t n = uint64_t(Z->meta[0]) * Z->meta[1] * Z->meta[2];
+  if (X->count < n || Z->count < n || M->count < Z->meta[1] || V->count < Z->meta[1]) return false;
+  out->x = X->ptr;
+  out->mean = M->ptr;
+  out->var = V->ptr;
+  out->N = Z->meta[0];
+  out->C = Z->meta[1];
+  out->S = Z->meta[2];
+  memcpy(&out->eps, &Z->aux32b, 4);
+  return true;
+}
+void tag_bn_grad_part(void* dz, void* z, void* side, uint32_t pieces) {
+  Buffer* D = static_cast<Buffer*>(dz);
+  const Buffer* Z = static_cast<const Buffer*>(z);
+  Buffer *X, *M, *V;
+  if (!D || D->magic != kMagicLive || !bn_links_alive(Z, &X, &M, &V)) {
+    release_buffer(side);
+    return;
+  }
+  drop_tag(D);
+  set_tag(D, kBnGradPartTag);
+  D->side = static_cast<Buffer*>(side);
+  D->src = X;
+  D->srcGen = X->gen;
+  D->aux = M;
+  D->auxGen = M->gen;
+  for (int i = 0; i < 3; ++i) D->meta[i] = Z->meta[i];
+  D->aux32 = pieces;
+  D->aux32b = Z->aux32b;
+}
+const double* bn_grad_part_of(void* dy, void* x, void* mean, void* var, uint32_t N, uint32_t C,
+                              uint32_t S, float eps, uint32_t* pieces) {
+  const Buffer* D = static_cast<const Buffer*>(dy);
+  if (!D || D->magic != kMagicLive || D->tag != kBnGradPartTag || !D->side) return nullptr;
+  uint32_t eb;
+  memcpy(&eb, &eps, 4);
+  Buffer* M = D->aux;
+  if (D->src != x || M != mean || !tag_alive(D->src, kBnStatsTag, D->srcGen) ||
+      !tag_alive(M, kBnMomentTag, D->auxGen) || M->src != var ||
+      !tag_alive(M->src, kBnMomentTag, M->srcGen) || D->meta[0] != N || D->meta[1] != C ||
+      D->meta[2] != S || D->aux32b != eb)
+    return nullptr;
+  *pieces = D->aux32;
+  return reinterpret_cast<const double*>(D->side->ptr);
 }
 bool bn_act_adopt(void* z, void* a, uint32_t act, uint32_t n) {
   Buffer* Z = static_cast<Buffer*>(z);
   Buffer* A = static_cast<Buffer*>(a);
   if (!Z || Z->magic != kMagicLive || Z->tag != kBnOutTag) return false;
-  if (Z->aux) g_bnAct[Z->aux] = act;
+  if (Z->key) g_bnAct[Z->key] = act;
   Buffer* S = Z->side;
   if (!S || Z->aux32 != act || !A || A == Z || A->magic != kMagicLive || A->count != S->count ||
       n != S->count)
@@ -436,6 +526,7 @@ static Buffer* alloc_record(uint32_t count) {
   b->tag = 0;
   b->gen = 0;
   b->src = b->aux = b->side = nullptr;
+  b->key = nullptr;
   return b;
 }
 

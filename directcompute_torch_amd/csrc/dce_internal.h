@@ -42,10 +42,19 @@ struct Buffer {
   //            (then batchnorm_backward_dx over y makes that G);
   //  kGradGTag also marks the dx of batchnorm_backward_dx over such a y:
   //            side = [NHWC G | bias-gradient partials], src = null;
-  //  kBnOutTag: output z of batchnorm_forward; aux = that call's gamma
-  //            buffer (a key only: the layer), and when the forward also
-  //            stored act(z) for the activation that followed this layer
-  //            last time, side = that buffer, aux32 = 1 (relu) or 2 (relu6).
+  //  kBnOutTag: output z of batchnorm_forward; key = that call's gamma
+  //            buffer (a key only: the layer), meta = {N, C, S}, aux32b =
+  //            the bits of eps; src = x (when it carries kBnStatsTag) and
+  //            aux = the batch mean (kBnMomentTag) it normalised with; when
+  //            the forward also stored act(z) for the activation that
+  //            followed this layer last time, side = that buffer, aux32 = 1
+  //            (relu) or 2 (relu6);
+  //  kBnMomentTag: batch mean and variance of batchnorm_mean_var; the
+  //            mean's src = the variance;
+  //  kBnGradPartTag: dz of relu_grad / relu6_grad over such a z: side holds
+  //            the partial sums of batchnorm_backward_reduce over (x, dz)
+  //            ([C][pieces][2] doubles), src = x, aux = mean, meta = {N, C,
+  //            S}, aux32 = pieces, aux32b = the bits of eps.
   // A tag is dropped (drop_tag) whenever the buffer is written by anything
   // but its producer, and when the buffer goes back to the pool.
   uint32_t tag;
@@ -61,6 +70,8 @@ struct Buffer {
   uint64_t auxGen;
   Buffer* side;     // kGradGTag: owned buffer [G | bias-gradient partials]; kBnStatsTag: the sums
   uint32_t aux32;
+  uint32_t aux32b;
+  const void* key;  // kBnOutTag: the layer's gamma buffer
 };
 constexpr uint32_t kPoolTag = 0x9001u;
 constexpr uint32_t kNhwcTag = 0x9002u;
@@ -69,6 +80,8 @@ constexpr uint32_t kPoolOutTag = 0x9004u;
 constexpr uint32_t kGradGTag = 0x9005u;
 constexpr uint32_t kBnStatsTag = 0x9006u;
 constexpr uint32_t kBnOutTag = 0x9007u;
+constexpr uint32_t kBnMomentTag = 0x9008u;
+constexpr uint32_t kBnGradPartTag = 0x9009u;
 // Layouts of a conv backward's masked gradient G.
 constexpr uint32_t kGLayoutPad = 1;   // [B*OC][OH][pad4(OW)], zero past OW (stride-phase dW)
 constexpr uint32_t kGLayoutNhwc = 2;  // [B*OH*OW][pad4(OC)] (the transpose pass)
@@ -130,9 +143,30 @@ void tag_bn_stats(void* y, void* side, uint32_t B, uint32_t C, uint32_t S, uint3
 // The activation (1 relu, 2 relu6, 0 none seen) that last followed the batch
 // norm whose gamma buffer is `gamma`.
 uint32_t bn_act_guess(const void* gamma);
-// Tag z (a batchnorm_forward output) kBnOutTag; side (may be null) holds
-// act(z), owned by z from now on.
-void tag_bn_out(void* z, void* gamma, void* side, uint32_t act);
+// Tag z (a batchnorm_forward output over x with batch statistics mean /
+// var) kBnOutTag; side (may be null) holds act(z), owned by z from now on.
+void tag_bn_out(void* z, void* x, void* mean, void* gamma, void* side, uint32_t act,
+                uint32_t N, uint32_t C, uint32_t S, float eps);
+// Tag the batch statistics of batchnorm_mean_var kBnMomentTag.
+void tag_bn_moments(void* mean, void* var);
+// For relu_grad / relu6_grad over z: when z is a batchnorm_forward output
+// whose x and statistics are unchanged since, the device pointers of x, mean
+// and var, the shape and eps, and true.
+struct BnLink {
+  const float* x;
+  const float* mean;
+  const float* var;
+  uint32_t N, C, S;
+  float eps;
+};
+bool bn_link_of(void* z, BnLink* out);
+// Tag dz kBnGradPartTag with the partial sums in `side` (owned by dz from
+// now on), made over z's batch norm (bn_link_of).
+void tag_bn_grad_part(void* dz, void* z, void* side, uint32_t pieces);
+// batchnorm_backward_reduce(x, dy, mean, var, eps) over N, C, S: the partial
+// sums dy carries for exactly these operands, or null.
+const double* bn_grad_part_of(void* dy, void* x, void* mean, void* var, uint32_t N, uint32_t C,
+                              uint32_t S, float eps, uint32_t* pieces);
 // relu (act 1) / relu6 (act 2) of n elements from z into a: when z carries
 // that activation already stored for all n elements of a, a takes that
 // storage over (a's own goes back to the pool) and true is returned; the

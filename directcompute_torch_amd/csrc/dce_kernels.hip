@@ -166,15 +166,9 @@ static bool sh_relu(const Dispatch& d) {  // nn_relu.hlsl: no constants, bounded
   if (d.nS && d.nU && bn_act_adopt(d.srvs[0], d.uavs[0], 1, o.n)) return true;
   return run_ew("relu", OpRelu{}, o, S(d, 0), Buf{nullptr, 0}, o.n, true);
 }
-static bool sh_relu_grad(const Dispatch& d) {
-  return run_ew("relu_grad", OpReluGrad{}, U(d, 0), S(d, 0), S(d, 1), CU(d, 0), false);
-}
 static bool sh_relu6(const Dispatch& d) {
   if (d.nS && d.nU && bn_act_adopt(d.srvs[0], d.uavs[0], 2, CU(d, 0))) return true;
   return run_ew("relu6", OpRelu6{}, U(d, 0), S(d, 0), Buf{nullptr, 0}, CU(d, 0), true);
-}
-static bool sh_relu6_grad(const Dispatch& d) {
-  return run_ew("relu6_grad", OpRelu6Grad{}, U(d, 0), S(d, 0), S(d, 1), CU(d, 0), false);
 }
 static bool sh_sigmoid(const Dispatch& d) {
   return run_ew("sigmoid", OpSigmoid{}, U(d, 0), S(d, 0), Buf{nullptr, 0}, CU(d, 0), true);
@@ -619,19 +613,24 @@ __global__ void k_bn_partial(Buf x, Buf dy, Buf mean, Buf var, float eps, uint32
 // grid is (channel, piece) with channels fastest, so the blocks that run
 // together read neighbouring planes of the same images (64x96x112x112
 // backward reduce 104.6 -> 96.6 us against pieces fastest).
+// MODE 2 / 3: dy is not read but made, dy = relu_grad(g, z) / relu6_grad(g,
+// z) with the activation shaders' own functors, and stored to dyOut: the
+// activation's backward and this reduce in one pass, the same sums in the
+// same order as MODE 1 over the stored dy.
 constexpr int kBnUnroll = 4;
 template <int MODE, bool NT, int U>
 __global__ void __launch_bounds__(256)
     k_bn_partial4(const float* __restrict__ x, const float* __restrict__ dy,
                   const float* __restrict__ mean, const float* __restrict__ var, float eps,
                   uint32_t C, uint32_t S4, uint32_t len4, uint32_t pieces, FastDiv dS4,
-                  double* __restrict__ part) {
+                  double* __restrict__ part, const float* __restrict__ zin = nullptr,
+                  float* __restrict__ dyOut = nullptr) {
   __shared__ double sh[4];
   const uint32_t c = blockIdx.x, pc = blockIdx.y;
   const uint32_t k0 = uint32_t((uint64_t(len4) * pc) / pieces);
   const uint32_t k1 = uint32_t((uint64_t(len4) * (pc + 1)) / pieces);
   float mu = 0.f, rstd = 0.f;
-  if (MODE == 1) {
+  if (MODE >= 1) {
     mu = mean[c];
     rstd = 1.0f / sqrtf(var[c] + eps);
   }
@@ -639,7 +638,10 @@ __global__ void __launch_bounds__(256)
   // Batches of U quads per thread; the next batch's loads are issued
   // before the current batch is added, so the adds overlap the memory
   // traffic.  Lanes past the piece load quad k0 (in range) and skip it.
-  auto load = [&](uint32_t kb, f4 (&xv)[U], f4 (&gv)[U], bool (&ok)[U]) {
+  // MODE >= 2: gv holds the incoming gradient and zv the activation input
+  // until add() turns them into dy.
+  auto load = [&](uint32_t kb, f4 (&xv)[U], f4 (&gv)[U], f4 (&zv)[U], bool (&ok)[U],
+                  size_t (&qo)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const uint32_t k = kb + u * 256;
@@ -647,14 +649,23 @@ __global__ void __launch_bounds__(256)
       const uint32_t kk = ok[u] ? k : k0;
       const uint32_t n = fdiv(kk, dS4);
       const size_t q = (size_t(n) * C + c) * S4 + (kk - n * S4);
+      qo[u] = q;
       xv[u] = ld4s<NT>(x + q * 4);
-      if (MODE == 1) gv[u] = ld4s<NT>(dy + q * 4);
+      if (MODE >= 1) gv[u] = ld4s<NT>(dy + q * 4);
+      if (MODE >= 2) zv[u] = ld4s<NT>(zin + q * 4);
     }
   };
-  auto add = [&](const f4 (&xv)[U], const f4 (&gv)[U], const bool (&ok)[U]) {
+  auto add = [&](const f4 (&xv)[U], f4 (&gv)[U], const f4 (&zv)[U], const bool (&ok)[U],
+                 const size_t (&qo)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (!ok[u]) continue;
+      if constexpr (MODE >= 2) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          gv[u][e] = MODE == 2 ? OpReluGrad{}(gv[u][e], zv[u][e]) : OpRelu6Grad{}(gv[u][e], zv[u][e]);
+        st4s<NT>(dyOut + qo[u] * 4, gv[u]);
+      }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         if (MODE == 0) {
@@ -668,23 +679,27 @@ __global__ void __launch_bounds__(256)
       }
     }
   };
-  f4 xv[U], gv[U];
+  f4 xv[U], gv[U], zv[U];
   bool ok[U];
+  size_t qo[U];
   uint32_t kb = k0 + threadIdx.x;
-  if (kb < k1) load(kb, xv, gv, ok);
+  if (kb < k1) load(kb, xv, gv, zv, ok, qo);
   while (kb < k1) {
     const uint32_t kn = kb + 256 * U;
-    f4 xn[U], gn[U];
+    f4 xn[U], gn[U], zn[U];
     bool okn[U];
+    size_t qn[U];
     const bool more = kn < k1;
-    if (more) load(kn, xn, gn, okn);
-    add(xv, gv, ok);
+    if (more) load(kn, xn, gn, zn, okn, qn);
+    add(xv, gv, zv, ok, qo);
     if (!more) break;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       xv[u] = xn[u];
       gv[u] = gn[u];
+      zv[u] = zn[u];
       ok[u] = okn[u];
+      qo[u] = qn[u];
     }
     kb = kn;
   }
@@ -831,6 +846,55 @@ static bool bn_reduce(const char* what, int mode, const Dispatch& d, Buf x, Buf 
   return check_launch(what);
 }
 
+// relu_grad / relu6_grad over the output z of a batch norm whose operands
+// are unchanged since its forward: dz comes with the partial sums of that
+// batch norm's backward reduce over (x, dz), so that the reduce only adds
+// them up (bn_backward_reduce_fused).
+template <int MODE>
+static bool act_grad_bn(const char* what, const Dispatch& d) {
+  if (d.nS < 2 || !d.nU) return false;
+  BnLink L;
+  if (!bn_link_of(d.srvs[1], &L)) return false;
+  const uint64_t total = uint64_t(L.N) * L.C * L.S;
+  const Buf g = S(d, 0), z = S(d, 1), out = U(d, 0);
+  const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (CU(d, 0) != total || L.S % 4 || !covers(g, total) || !covers(z, total) ||
+      !covers(out, total) || !al16(g.p) || !al16(z.p) || !al16(out.p) || !al16(L.x) ||
+      total >= (1ull << 31))
+    return false;
+  const BnPieces pc = bn_pieces(L.N, L.C, L.S);
+  const uint64_t side_n = uint64_t(L.C) * pc.pieces * 4;
+  Buffer* side = side_n < 0xFFFFFFFFull
+                     ? static_cast<Buffer*>(create_buffer(nullptr, uint32_t(side_n)))
+                     : nullptr;
+  if (!side) return false;
+  ProfScope prof(what, 0, 16.0 * double(total));
+  const uint32_t S4 = L.S / 4, len4 = L.N * S4;
+  double* part = reinterpret_cast<double*>(side->ptr);
+  if (stream_nt(16.0 * double(total)))
+    hipLaunchKernelGGL((k_bn_partial4<MODE, true, kBnUnroll>), dim3(L.C, pc.pieces), dim3(256), 0,
+                       stream(), L.x, g.p, L.mean, L.var, L.eps, L.C, S4, len4, pc.pieces,
+                       make_fastdiv(S4), part, z.p, out.p);
+  else
+    hipLaunchKernelGGL((k_bn_partial4<MODE, false, kBnUnroll>), dim3(L.C, pc.pieces), dim3(256),
+                       0, stream(), L.x, g.p, L.mean, L.var, L.eps, L.C, S4, len4, pc.pieces,
+                       make_fastdiv(S4), part, z.p, out.p);
+  if (!check_launch(what)) {
+    release_buffer(side);
+    return false;
+  }
+  tag_bn_grad_part(d.uavs[0], d.srvs[1], side, pc.pieces);
+  return true;
+}
+static bool sh_relu_grad(const Dispatch& d) {
+  if (act_grad_bn<2>("relu_grad", d)) return true;
+  return run_ew("relu_grad", OpReluGrad{}, U(d, 0), S(d, 0), S(d, 1), CU(d, 0), false);
+}
+static bool sh_relu6_grad(const Dispatch& d) {
+  if (act_grad_bn<3>("relu6_grad", d)) return true;
+  return run_ew("relu6_grad", OpRelu6Grad{}, U(d, 0), S(d, 0), S(d, 1), CU(d, 0), false);
+}
+
 static bool sh_bn_mean_var(const Dispatch& d) {
   uint32_t N = CU(d, 0), C = CU(d, 1), Sz = CU(d, 2), training = CU(d, 3);
   float momentum = CF(d, 4);
@@ -843,24 +907,40 @@ static bool sh_bn_mean_var(const Dispatch& d) {
     hipLaunchKernelGGL(k_bn_stats_final_wide, dim3(C), dim3(256), 0, stream(),
                        reinterpret_cast<const double*>(X->side->ptr), X->aux32, N * Sz, U(d, 0),
                        U(d, 1), U(d, 2), U(d, 3), training, momentum);
-    return check_launch("batchnorm_mean_var");
+    if (!check_launch("batchnorm_mean_var")) return false;
+  } else {
+    double* part;
+    BnPieces pc;
+    ProfScope prof("bn_stats", 0, 4.0 * double(N) * C * Sz);
+    if (!bn_reduce("batchnorm_mean_var", 0, d, S(d, 0), Buf{nullptr, 0}, Buf{nullptr, 0},
+                   Buf{nullptr, 0}, 0.f, N, C, Sz, &part, &pc))
+      return false;
+    hipLaunchKernelGGL(k_bn_stats_final, dim3(cdiv(C, 4)), dim3(256), 0, stream(), part,
+                       pc.pieces, C, N * Sz, U(d, 0), U(d, 1), U(d, 2), U(d, 3), training,
+                       momentum);
+    if (!check_launch("batchnorm_mean_var")) return false;
   }
-  double* part;
-  BnPieces pc;
-  ProfScope prof("bn_stats", 0, 4.0 * double(N) * C * Sz);
-  if (!bn_reduce("batchnorm_mean_var", 0, d, S(d, 0), Buf{nullptr, 0}, Buf{nullptr, 0},
-                 Buf{nullptr, 0}, 0.f, N, C, Sz, &part, &pc))
-    return false;
-  hipLaunchKernelGGL(k_bn_stats_final, dim3(cdiv(C, 4)), dim3(256), 0, stream(), part,
-                     pc.pieces, C, N * Sz, U(d, 0), U(d, 1), U(d, 2), U(d, 3), training,
-                     momentum);
-  return check_launch("batchnorm_mean_var");
+  // The statistics, tagged so that the backward can tell they are unchanged.
+  if (d.nU >= 2) tag_bn_moments(d.uavs[0], d.uavs[1]);
+  return true;
 }
 
 static bool sh_bn_backward_reduce(const Dispatch& d) {
   uint32_t N = CU(d, 0), C = CU(d, 1), Sz = CU(d, 2);
   float eps = CF(d, 3);
   if (!N || !C || !Sz) return true;
+  // dy made by relu_grad / relu6_grad over this batch norm's output, with
+  // the partial sums for exactly these operands: add them up.
+  if (d.nS >= 4 && d.nU >= 2) {
+    uint32_t pieces = 0;
+    if (const double* gp = bn_grad_part_of(d.srvs[1], d.srvs[0], d.srvs[2], d.srvs[3], N, C, Sz,
+                                           eps, &pieces)) {
+      ProfScope prof("bn_bwd_reduce_side", 0, 16.0 * double(C) * pieces);
+      hipLaunchKernelGGL(k_bn_grad_final, dim3(cdiv(C, 4)), dim3(256), 0, stream(), gp, pieces, C,
+                         U(d, 0), U(d, 1));
+      return check_launch("batchnorm_backward_reduce");
+    }
+  }
   double* part;
   BnPieces pc;
   ProfScope prof("bn_bwd_reduce", 0, 8.0 * double(N) * C * Sz);
@@ -981,10 +1061,11 @@ static bool bn_elem(const char* what, const Dispatch& d) {
           release_buffer(side);
           return false;
         }
-        tag_bn_out(d.uavs[0], d.srvs[3], side, act);
+        tag_bn_out(d.uavs[0], d.srvs[0], d.srvs[1], d.srvs[3], side, act, N, C, Sz, eps);
         return true;
       }
-      tag_bn_out(d.uavs[0], d.nS >= 4 ? d.srvs[3] : nullptr, nullptr, 0);
+      if (d.nS >= 4 && d.nU)
+        tag_bn_out(d.uavs[0], d.srvs[0], d.srvs[1], d.srvs[3], nullptr, 0, N, C, Sz, eps);
     }
     if (stream_nt((MODE == 1 ? 12.0 : 8.0) * double(total)))
       hipLaunchKernelGGL((k_bn_elem4<MODE, true>), dim3(cdiv(total4, 256)), dim3(256), 0,

@@ -448,3 +448,116 @@ def test_bn_forward_stores_next_activation(eng, act):
         eng.lib.SetProfiling(0)
         eng.lib.ResetProfile()
         release(eng, hx, hg, hb)
+
+
+def _bn_act_setup(eng, seed, act):
+    """conv (no activation) -> batchnorm_mean_var -> batchnorm_forward -> act;
+    returns the handles the backward needs."""
+    B, C, H, W, OC, k, s, p = 2, 16, 12, 12, 24, 3, 1, 1
+    r = rng(seed)
+    x = r.standard_normal((B, C, H, W)).astype(np.float32)
+    w = he(r, (OC, C, k, k), C * k * k)
+    b = (0.5 + r.standard_normal(OC)).astype(np.float32)
+    hx, hw, hb = upload(eng, x), upload(eng, w), upload(eng, b)
+    hy = eng.lib.ConvForwardFused(hx, hw, hb, B, C, H, W, OC, k, k, s, p, 0, None)
+    assert hy, eng.last_error()
+    shape = (B, OC, H, W)
+    n = B * OC * H * W
+    gamma = (1.0 + 0.3 * r.standard_normal(OC)).astype(np.float32)
+    beta = r.standard_normal(OC).astype(np.float32)
+    hg, hbe = upload(eng, gamma), upload(eng, beta)
+    hmu, hvar = new(eng, OC), new(eng, OC)
+    hrm, hrv = upload(eng, np.zeros(OC, np.float32)), upload(eng, np.ones(OC, np.float32))
+    run(eng, "batchnorm_mean_var", [hy], [hmu, hvar, hrm, hrv], B, OC, H * W, 1, fbits(0.1))
+    hz = new(eng, n)
+    run(eng, "batchnorm_forward", [hy, hmu, hvar, hg, hbe], [hz], B, OC, H * W, fbits(1e-5))
+    ha = new(eng, n)
+    run(eng, act, [hz], [ha], *(() if act == "relu" else (n,)))
+    da = r.standard_normal(shape).astype(np.float32)
+    hda = upload(eng, da)
+    release(eng, hx, hw, hb, hrm, hrv, hbe)
+    return dict(hy=hy, hz=hz, ha=ha, hda=hda, hg=hg, hmu=hmu, hvar=hvar, shape=shape, n=n, r=r)
+
+
+def _act_grad_reduce(eng, h, act, z_handle, eps=1e-5, write=None):
+    """act's backward into a new dz, then batchnorm_backward_reduce over
+    (y, dz); returns dz, dgamma, dbeta and the reduce families' launches."""
+    B, OC, H, W = h["shape"]
+    n = h["n"]
+    hdz = new(eng, n)
+    run(eng, act + "_grad", [h["hda"], z_handle], [hdz], n)
+    if write == "dz":
+        he_ = upload(eng, h["r"].standard_normal(h["shape"]).astype(np.float32))
+        run(eng, "grad_accum", [he_], [hdz], n)
+        release(eng, he_)
+    hdg, hdb = new(eng, OC), new(eng, OC)
+    eng.lib.ResetProfile()
+    run(eng, "batchnorm_backward_reduce", [h["hy"], hdz, h["hmu"], h["hvar"]], [hdg, hdb], B, OC,
+        H * W, fbits(eps))
+    fams = (_count(eng, "bn_bwd_reduce_side"), _count(eng, "bn_bwd_reduce"))
+    out = (download(eng, hdz, h["shape"]), download(eng, hdg, (OC,)), download(eng, hdb, (OC,)))
+    release(eng, hdz, hdg, hdb)
+    return out, fams
+
+
+@pytest.mark.parametrize("act", ["relu", "relu6"])
+def test_act_grad_makes_bn_reduce_sums(eng, act):
+    """relu_grad / relu6_grad over a batch norm's output also leaves the sums
+    of that batch norm's backward reduce over (y, dz): dz, dgamma and dbeta
+    are bit for bit those of the unfused calls, and the reduce reads no
+    tensor; a write to y, the statistics or dz in between, or another eps,
+    runs the reduce pass."""
+    eng.lib.SetProfiling(1)
+    try:
+        h = _bn_act_setup(eng, 5800 + len(act), act)
+        zc = _copy(eng, h["hz"], h["n"])  # untagged: the unfused calls
+        (dz, dg, db), fams = _act_grad_reduce(eng, h, act, h["hz"])
+        assert fams == (1, 0), fams
+        (dz_p, dg_p, db_p), fams_p = _act_grad_reduce(eng, h, act, zc)
+        assert fams_p == (0, 1), fams_p
+        assert np.array_equal(dz, dz_p) and np.array_equal(dg, dg_p) and np.array_equal(db, db_p)
+        # against the oracle
+        y = download(eng, h["hy"], h["shape"])
+        mu, var = download(eng, h["hmu"], (h["shape"][1],)), download(eng, h["hvar"], (h["shape"][1],))
+        dg_r, db_r = K.batchnorm_backward_reduce(y, dz, mu, var, 1e-5)
+        assert rel_err(dg, dg_r) <= TOL and rel_err(db, db_r) <= TOL
+        # another eps: the pass
+        _, fams_e = _act_grad_reduce(eng, h, act, h["hz"], eps=1e-3)
+        assert fams_e == (0, 1), fams_e
+        # a gradient accumulated into dz in between: the pass, on the new dz
+        (dz_w, dg_w, db_w), fams_w = _act_grad_reduce(eng, h, act, h["hz"], write="dz")
+        assert fams_w == (0, 1), fams_w
+        dg_r, db_r = K.batchnorm_backward_reduce(y, dz_w, mu, var, 1e-5)
+        assert rel_err(dg_w, dg_r) <= TOL and rel_err(db_w, db_r) <= TOL
+        # a write to the batch statistics: no sums (the reduce reads the new ones)
+        var2 = (var * 2.0 + 0.5).astype(np.float32)
+        eng.lib.UpdateBuffer(h["hvar"], var2.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+        (dz_v, dg_v, db_v), fams_v = _act_grad_reduce(eng, h, act, h["hz"])
+        assert fams_v == (0, 1), fams_v
+        dg_r, db_r = K.batchnorm_backward_reduce(y, dz_v, mu, var2, 1e-5)
+        assert rel_err(dg_v, dg_r) <= TOL and rel_err(db_v, db_r) <= TOL
+        release(eng, zc, h["hy"], h["hz"], h["ha"], h["hda"], h["hg"], h["hmu"], h["hvar"])
+    finally:
+        eng.lib.SetProfiling(0)
+        eng.lib.ResetProfile()
+
+
+def test_act_grad_bn_sums_dropped_on_x_write(eng):
+    """A write to the batch norm's input y after its forward: the activation's
+    backward leaves no sums and the reduce follows the written y."""
+    eng.lib.SetProfiling(1)
+    try:
+        h = _bn_act_setup(eng, 5900, "relu")
+        y = download(eng, h["hy"], h["shape"])
+        y2 = (y + 0.25).astype(np.float32)
+        eng.lib.UpdateBuffer(h["hy"], y2.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+        (dz, dg, db), fams = _act_grad_reduce(eng, h, "relu", h["hz"])
+        assert fams == (0, 1), fams
+        mu = download(eng, h["hmu"], (h["shape"][1],))
+        var = download(eng, h["hvar"], (h["shape"][1],))
+        dg_r, db_r = K.batchnorm_backward_reduce(y2, dz, mu, var, 1e-5)
+        assert rel_err(dg, dg_r) <= TOL and rel_err(db, db_r) <= TOL
+        release(eng, h["hy"], h["hz"], h["ha"], h["hda"], h["hg"], h["hmu"], h["hvar"])
+    finally:
+        eng.lib.SetProfiling(0)
+        eng.lib.ResetProfile()
