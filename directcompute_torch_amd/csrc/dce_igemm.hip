@@ -71,10 +71,9 @@ struct Stage {
   // read takes one float of 16 consecutive rows at 4 k's 4 apart, which the
   // swizzle spreads over all 64 banks (unswizzled, k rows R floats apart
   // would share banks).  Other KROW rows keep a +4 pad.  Unpadded stages take
-  // direct global-to-LDS loads.  The conv dW taps loader (LdXTapKR) stays
-  // padded: with direct loads its per-quad tap rows cost more than the
-  // staging they save.  The dW G operand (LdGradKR, a dense [pixel][OCp]
-  // matrix) takes them: AlexNet's conv backward 112.3 -> 113.0 TFLOP/s.
+  // direct global-to-LDS loads, the conv dW operands included (the G rows
+  // and the per-quad tap rows of x: AlexNet's conv backward 112.3 -> 113.0
+  // -> 113.7 TFLOP/s as each went direct).
   static constexpr bool SWZ = KROW && SWZOK && R >= 64;
   static constexpr int LD = KROW ? (SWZ ? R : R + 4) : KT;
   static constexpr int SIZE = KROW ? KT * LD : R * LD;
@@ -616,8 +615,8 @@ struct XTapParams {
   FastDiv dOHW, dOW, dCp, dK;
 };
 template <int R, int KT>
-struct LdXTapKR : LoaderBase<Stage<R, KT, true, false>> {
-  using St = Stage<R, KT, true, false>;
+struct LdXTapKR : LoaderBase<Stage<R, KT, true>> {
+  using St = Stage<R, KT, true>;
   static constexpr bool KROW = true;
   using LoaderBase<St>::Q;
   using Params = XTapParams;
