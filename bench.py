@@ -482,7 +482,8 @@ def _prof_all(lib):
     fams = ("conv_bwd", "conv_fwd", "conv_dw", "conv_dx", "gemm", "maxpool_fwd", "maxpool_bwd", "bn_stats",
             "bn_stats_side", "bn_fwd", "bn_bwd_reduce", "bn_bwd_reduce_side", "bn_bwd_dx",
             "dw_bwd_input", "dw_bwd_filter",
-            "gap_bwd", "upsample_bwd", "dice_loss_grad", "bias_grad", "sgd", "adam", "grad_norm",
+            "gap_bwd", "upsample", "upsample_bwd", "dice_loss_grad", "bias_grad", "sgd", "adam",
+            "grad_norm",
             "clip_scale", "relu", "relu6", "relu_grad", "relu6_grad", "sigmoid_grad", "grad_accum",
             "slice", "conv_grad_nhwc", "nhwc")
     out = {}

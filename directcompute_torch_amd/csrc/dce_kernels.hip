@@ -1796,11 +1796,42 @@ __global__ void k_upsample_bwd(Buf DY, Buf DX, uint32_t total, uint32_t H, uint3
   }
   st(DX, i, s);
 }
+// Nearest x2 with even W and exact output size: a thread reads an input
+// pair (8 bytes) and writes the 2 x 4 outputs it covers as two 16-byte
+// stores (output rows 2h and 2h + 1 of plane bc start at 2*row*OW, row =
+// bc*H + h).
+template <bool NT>
+__global__ void k_upsample2(const float* __restrict__ x, float* __restrict__ y, uint32_t pairs,
+                            uint32_t W2, FastDiv dW2) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= pairs) return;
+  const uint32_t row = fdiv(i, dW2), j = i - row * W2;
+  const f2 v = reinterpret_cast<const f2*>(x)[i];
+  const f4 q = {v[0], v[0], v[1], v[1]};
+  float* o = y + size_t(2 * row) * (4 * W2) + 4 * j;
+  st4s<NT>(o, q);
+  st4s<NT>(o + 4 * W2, q);
+}
 static bool sh_upsample(const Dispatch& d) {
   uint32_t B = CU(d, 0), C = CU(d, 1), H = CU(d, 2), W = CU(d, 3), OH = CU(d, 4), OW = CU(d, 5),
            sH = CU(d, 6), sW = CU(d, 7);
   uint64_t total = uint64_t(B) * C * OH * OW;
   if (!total || !sH || !sW) return true;
+  ProfScope prof("upsample", 0, 5.0 * double(total));
+  const Buf x = S(d, 0), y = U(d, 0);
+  const uint64_t nin = uint64_t(B) * C * H * W;
+  if (sH == 2 && sW == 2 && OH == 2 * H && OW == 2 * W && W % 2 == 0 && covers(x, nin) &&
+      covers(y, total) && (reinterpret_cast<uintptr_t>(x.p) & 7) == 0 &&
+      (reinterpret_cast<uintptr_t>(y.p) & 15) == 0 && total < (1ull << 32)) {
+    const uint32_t pairs = uint32_t(nin / 2), W2 = W / 2;
+    if (stream_nt(5.0 * double(total)))
+      hipLaunchKernelGGL(k_upsample2<true>, dim3(cdiv(pairs, 256)), dim3(256), 0, stream(), x.p,
+                         y.p, pairs, W2, make_fastdiv(W2));
+    else
+      hipLaunchKernelGGL(k_upsample2<false>, dim3(cdiv(pairs, 256)), dim3(256), 0, stream(), x.p,
+                         y.p, pairs, W2, make_fastdiv(W2));
+    return check_launch("upsample");
+  }
   hipLaunchKernelGGL(k_upsample, dim3(cdiv(total, 256)), dim3(256), 0, stream(), S(d, 0),
                      U(d, 0), uint32_t(total), C, H, W, OH, OW, sH, sW);
   return check_launch("upsample");

@@ -1388,7 +1388,7 @@ class KernelProfiler:
     FAMILIES = ("conv_fwd", "conv_bwd", "conv_dw", "conv_dx", "gemm", "nhwc", "conv_grad_nhwc",
                 "maxpool_fwd", "maxpool_bwd", "bn_stats", "bn_stats_side", "bn_fwd", "bn_bwd_reduce",
                 "bn_bwd_reduce_side", "bn_bwd_dx",
-                "dw_bwd_input", "dw_bwd_filter", "gap_bwd", "upsample_bwd", "bias_grad",
+                "dw_bwd_input", "dw_bwd_filter", "gap_bwd", "upsample", "upsample_bwd", "bias_grad",
                 "dice_loss_grad", "sgd", "sgd_clipped", "adam", "grad_norm", "clip_scale",
                 "relu", "relu_grad", "relu6", "relu6_grad", "leaky_relu", "leaky_relu_grad",
                 "sigmoid", "sigmoid_grad", "add", "scale_add", "grad_accum")

@@ -417,7 +417,8 @@ def test_global_avg_pool(eng, B, C, H, W, policy):
     release(eng, hx, ho, hg, hdx)
 
 
-@pytest.mark.parametrize("B,C,H,W,sH,sW", [(2, 3, 4, 5, 2, 2), (1, 16, 32, 32, 2, 2), (2, 2, 3, 3, 3, 2)] +
+@pytest.mark.parametrize("B,C,H,W,sH,sW", [(2, 3, 4, 5, 2, 2), (1, 16, 32, 32, 2, 2), (2, 2, 3, 3, 3, 2),
+                                           (2, 4, 6, 2, 2, 2), (1, 8, 1, 4, 2, 2), (3, 5, 7, 10, 2, 2)] +
                          [tuple(int(v) for v in np.random.default_rng(818 + i).integers([1, 1, 1, 1, 1, 1],
                                                                                         [5, 20, 40, 40, 4, 4]))
                           for i in range(6)])
