@@ -1034,17 +1034,19 @@ static bool bn_elem(const char* what, const Dispatch& d) {
   Buf db = MODE == 1 ? S(d, 6) : Buf{nullptr, 0};
   Buf out = U(d, 0);
   const bool fast = covers(x, total) && covers(out, total) && (MODE == 0 || covers(dy, total));
-  ProfScope prof(MODE == 0 ? "bn_fwd" : "bn_bwd_dx", 0, (MODE == 0 ? 8.0 : 12.0) * double(total));
   const auto al16 = [](const Buf& b) { return (reinterpret_cast<uintptr_t>(b.p) & 15) == 0; };
-  if (fast && Sz % 4 == 0 && al16(x) && al16(out) && (MODE == 0 || al16(dy)) &&
-      covers(mean, C) && covers(var, C) && covers(gamma, C) && covers(b2, C) &&
-      (MODE == 0 || covers(db, C))) {
+  const bool quad = fast && Sz % 4 == 0 && al16(x) && al16(out) && (MODE == 0 || al16(dy)) &&
+                    covers(mean, C) && covers(var, C) && covers(gamma, C) && covers(b2, C) &&
+                    (MODE == 0 || covers(db, C));
+  // The activation that followed this batch norm (same gamma) last time is
+  // stored as well (quad form of the forward), into a buffer that the
+  // activation's call adopts as its output (bn_act_adopt) instead of running.
+  const uint32_t act = MODE == 0 && quad && d.nS >= 4 && d.nU ? bn_act_guess(d.srvs[3]) : 0;
+  ProfScope prof(MODE == 0 ? "bn_fwd" : "bn_bwd_dx", 0,
+                 (MODE == 0 && !act ? 8.0 : 12.0) * double(total));
+  if (quad) {
     const uint32_t total4 = uint32_t(total / 4);
     if constexpr (MODE == 0) {
-      // The activation that followed this batch norm (same gamma) last time
-      // is stored as well, into a buffer that the activation's call adopts
-      // as its output (bn_act_adopt) instead of running.
-      const uint32_t act = d.nS >= 4 && d.nU ? bn_act_guess(d.srvs[3]) : 0;
       Buffer* side = act ? static_cast<Buffer*>(create_buffer(nullptr, uint32_t(total))) : nullptr;
       if (side) {
         const bool nt = stream_nt(12.0 * double(total));
