@@ -2120,13 +2120,16 @@ static double est_us(uint32_t M, uint32_t N, uint32_t kdim, const TileCfg& c, in
 template <class OccFn>
 static TileCfg choose(const char* var, uint32_t M, uint32_t N, uint32_t kdim, uint32_t max_splits,
                       bool dense_out, OccFn&& occ, bool kt16_only = false,
-                      bool narrow_ksplit = false) {
+                      bool narrow_ksplit = false, bool narrow32 = false) {
   TileCfg c{pick_tile_m(M), pick_tile(N), 16, 1};
   if (kt16_only && c.MT < 64) c.NT = 128;  // the pixel GEMMs' narrow tiles are 128 or 256 wide
   if (narrow_ksplit && c.MT < 64) {
     // Narrow tiles with the waves splitting K: 64 columns (a wave then holds
-    // the whole tile's accumulators; 128 would cost registers and occupancy).
-    c.NT = 64;
+    // the whole tile's accumulators; 128 would cost registers and occupancy),
+    // or 32 (narrow32) when 64 pads the columns by 8 % more: the 144 and 288
+    // taps x channels of 3x3 convs over 16 and 32 channels.
+    const uint64_t w64 = uint64_t(cdiv(N, 64)) * 64, w32 = uint64_t(cdiv(N, 32)) * 32;
+    c.NT = (narrow32 && w64 * 100 > w32 * 108) ? 32 : 64;
     c.KT = 64;
   }
   const uint32_t ktiles = cdiv(kdim, uint32_t(c.KT));
@@ -2194,8 +2197,9 @@ static bool launch(const typename LA::Params& pa, const typename LB::Params& pb,
 
 // Dispatch a functor over the (MT, NT) tile shapes: 64/128 square-ish tiles at
 // two KT depths and the narrow MT = 16/32 tiles at KT = 16 (1 x 4 wave grid)
-// or KT = 64 (waves split the K tile).
-template <class F>
+// or KT = 64 (waves split the K tile).  NARROW32: also 32 columns at KT = 64
+// (the conv dW of few output channels over 16 or 32 input channels).
+template <bool NARROW32 = false, class F>
 static bool tiles_dispatch(const TileCfg& c, F&& f) {
 #define DCE_T(a, b, k) \
   if (c.MT == a && c.NT == b && c.KT == k) return f.template run<a, b, k>();
@@ -2204,6 +2208,9 @@ static bool tiles_dispatch(const TileCfg& c, F&& f) {
   DCE_T(128, 128, 16) DCE_T(128, 64, 16) DCE_T(64, 128, 16) DCE_T(64, 64, 16)
   DCE_T(32, 128, 16) DCE_T(32, 64, 16) DCE_T(16, 128, 16) DCE_T(16, 64, 16)
   DCE_T(32, 128, 64) DCE_T(32, 64, 64) DCE_T(16, 128, 64) DCE_T(16, 64, 64)
+  if constexpr (NARROW32) {
+    DCE_T(32, 32, 64) DCE_T(16, 32, 64)
+  }
 #undef DCE_T
   set_error("igemm: unsupported tile %dx%dx%d", c.MT, c.NT, c.KT);
   return false;
@@ -2234,7 +2241,7 @@ static int tiles_occ16(const TileCfg& c, const F& f) {
 }
 
 // Occupancy of the kernel a functor would launch for cfg.
-template <class F>
+template <bool NARROW32 = false, class F>
 static int tiles_occ(const TileCfg& c, const F& f) {
 #define DCE_T(a, b, k) \
   if (c.MT == a && c.NT == b && c.KT == k) return f.template occ<a, b, k>(c.splits > 1);
@@ -2243,6 +2250,9 @@ static int tiles_occ(const TileCfg& c, const F& f) {
   DCE_T(128, 128, 16) DCE_T(128, 64, 16) DCE_T(64, 128, 16) DCE_T(64, 64, 16)
   DCE_T(32, 128, 16) DCE_T(32, 64, 16) DCE_T(16, 128, 16) DCE_T(16, 64, 16)
   DCE_T(32, 128, 64) DCE_T(32, 64, 64) DCE_T(16, 128, 64) DCE_T(16, 64, 64)
+  if constexpr (NARROW32) {
+    DCE_T(32, 32, 64) DCE_T(16, 32, 64)
+  }
 #undef DCE_T
   return 1;
 }
@@ -3437,9 +3447,9 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
           r.trans = dwT;
           r.pk = pk;
           r.ps = ps;
-          return tiles_occ(t, r);
+          return tiles_occ<true>(t, r);
         },
-        false, true);
+        false, true, !ps && !pk);
     nP = al64(size_t(dwc.splits) * 4 * cdiv(size_t(g.OC) * taps, 4));
   }
   // A dX at stride 3 or more runs as sub-pixel phases (phase_dx), each with
@@ -3516,7 +3526,7 @@ bool conv_backward(const float* dy, const float* y, const float* x, const float*
     }
     ProfScope prof("conv_dw", 2.0 * g.OC * g.C * KK * double(npix),
                    4.0 * (double(npix) * OCp + double(g.B) * g.H * g.W * Cp + double(g.OC) * KK * Cp));
-    return tiles_dispatch(dwc, DwRun{ps ? gp : gn, xn, part, g, dwc.splits, dwT, pk, ps});
+    return tiles_dispatch<true>(dwc, DwRun{ps ? gp : gn, xn, part, g, dwc.splits, dwT, pk, ps});
   };
   auto dw_finish = [&]() {
     BwdSide side{};

@@ -74,6 +74,10 @@ CONV_CASES = [
     (2, 17, 9, 9, 33, 3, 2, 0, 2),        # tanh act: no derivative applied (reference quirk)
     (1, 8, 7, 7, 8, 3, 3, 1, 0),          # stride 3
     (2, 192, 6, 6, 256, 3, 1, 1, 1),      # deep channels
+    # narrow dW tiles 32 columns wide (144 / 288 / 72 taps x channels)
+    (2, 16, 24, 24, 16, 3, 1, 1, 1),
+    (2, 32, 20, 20, 16, 3, 1, 1, 0),
+    (2, 8, 18, 18, 12, 3, 1, 1, 1),       # 72 columns: the last 32-wide tile partly past N
     # C < 4 and stride <= 4: the stride-phase copy (padded pixel grid)
     (2, 1, 19, 21, 6, 3, 3, 1, 1),        # C = 1, stride 3, OW 7 -> 8 padded columns
     (2, 2, 17, 29, 12, 4, 4, 0, 0),       # even k, stride 4, no activation
