@@ -2982,13 +2982,30 @@ static double* stats_buffer(ConvStatsReq* st, const TileCfg& cfg, uint32_t N, ui
   return d;
 }
 
+// Pointwise products with dot products of at most 32 (expand forward,
+// project dX): streaming-bound, one K tile or two per output tile.  For up to
+// 160 output rows, unsplit 32-row tiles (rows filled exactly or nearly, more
+// workgroups in flight) measured faster than the 64- and 128-row choices
+// (MobileNetV2 b64: 96 x 200704 x 24 dX 37.6 -> 26.7 us, 144 x 200704 x 24
+// forward and dX 46.2 -> 42.6 and 43.6 -> 39.9 us, 96 x 802816 x 16 forward
+// 110.3 -> 107.4 us); at 192 rows (x 50176 x 32) they were no faster (dX)
+// or 5 % slower (forward), so the rule stops at 160.  An override through
+// DCE_TUNE_* keeps its tile.
+static void narrow_pw(TileCfg& c, const char* var, uint32_t M, uint32_t kdim) {
+  if (const char* e = getenv(var))
+    if (*e) return;
+  if (M <= 32 || M > 160 || kdim > 32) return;
+  c = TileCfg{32, 128, 16, 1};
+}
+
 static bool conv_forward_pw(const float* x, const float* w, const float* bias, float* y,
                             const ConvGeom& g, uint32_t act, ConvStatsReq* st) {
   const uint32_t Cp = pad4(g.C), N = g.B * g.H * g.W;
   if (!operand_fits(size_t(g.B) * g.C * g.H * g.W, "conv_forward")) return false;
-  const TileCfg cfg = choose(
+  TileCfg cfg = choose(
       "DCE_TUNE_FWD", g.OC, N, Cp, 8, true,
       [&](const TileCfg& t) { return tiles_occ16(t, FwdPwRun{}); }, true);
+  narrow_pw(cfg, "DCE_TUNE_FWD", g.OC, Cp);
   // Filters [OC][C] are already the A operand when C % 4 == 0 (16-byte rows).
   const bool wDirect = g.C % 4 == 0 && aligned16(w);
   const size_t nw = wDirect ? 0 : al64(size_t(g.OC) * Cp);
@@ -3350,6 +3367,7 @@ static bool conv_backward_pw(const float* dy, const float* x, const float* w, fl
           return wk ? tiles_occ16(t, DxPwRun<true>{}) : tiles_occ16(t, DxPwRun<false>{});
         },
         true);
+    narrow_pw(dxc, "DCE_TUNE_DX", g.C, OCp);
     nW = wk ? 0 : al64(size_t(g.C) * OCp);
     nQ = dxc.splits > 1 ? size_t(dxc.splits) * g.C * N : 0;
   }
