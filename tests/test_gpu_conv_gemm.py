@@ -205,6 +205,37 @@ def test_conv_random_special_layouts(eng, case):
     _conv_case(eng, *case, seed=29, keep=bool(case[1] % 2))
 
 
+def _random_tile_rule_cases(n, seed):
+    """Seeded geometries for the padding-aware tile choices: pointwise layers
+    with 16-32 input (or output) channels and 33-160 on the other side (the
+    short-K products on unsplit 32-row tiles), and 3x3 layers over 8-32
+    channels with at most 32 output channels (the dW on 32-column narrow
+    tiles when 64 columns would pad its taps x channels)."""
+    r = rng(seed)
+    out = []
+    for i in range(n):
+        B = int(r.integers(1, 4))
+        H, W = 4 * int(r.integers(2, 9)), int(r.integers(4, 17))
+        if i % 2 == 0:
+            few, many = int(r.choice([16, 24, 32])), int(r.integers(33, 161))
+            C, OC = (few, many) if r.integers(0, 2) else (many, few)
+            out.append((B, C, H, W, OC, 1, 1, 0, int(r.integers(0, 2))))
+        else:
+            C, OC = int(r.choice([8, 16, 24, 32])), int(r.integers(1, 33))
+            out.append((B, C, H, W, OC, 3, 1, 1, int(r.integers(0, 2))))
+    return out
+
+
+TILE_RULE_CASES = _random_tile_rule_cases(12, 777)
+
+
+@pytest.mark.parametrize("case", TILE_RULE_CASES, ids=[str(c) for c in TILE_RULE_CASES])
+def test_conv_tile_rule_geometries(eng, case):
+    """Forward, dW, db and dX against the float64 oracle where the tile
+    choice depends on the padding of the rows and columns."""
+    _conv_case(eng, *case, seed=31, keep=True)
+
+
 PHASE_CASES = [
     # stride >= 3: dX as s*s sub-pixel phases, each a GEMM over its own taps
     (2, 24, 20, 19, 32, 2, 3, 0, 1),      # k < s: phases without taps (zero planes)
